@@ -1,0 +1,422 @@
+"""Benchmark of the one-Qwen-layer hot path on one MI355X.
+
+Default workload (the BASELINE metric's configuration, configs[1]): a full
+Qwen2.5-0.5B-shaped layer decoding one token at context 1024.  One step =
+one layer decode of one token.  Inputs are synthetic (seeded N(0,0.02)
+weights -> Q4_0, N(0,1) activations and fp16 KV) and resident in HBM before
+the timed region.  The step cycles through enough distinct copies of the
+layer (weights + KV cache) to exceed the 256 MB Infinity Cache, so the
+reported GB/s is HBM traffic, not cache hits.
+
+The JSON line also carries the other BASELINE configurations (QKV GEMV,
+0.5B and 7B prefill, 7B batched decode), the roofline of the dominant kernel
+(timed with HIP events on its own stream) and the CPU baseline (the oracle's
+C restatement of the reference's portable path, one host core).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "simple-inference_amd"))
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, GB/s
+INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA, TOP/s
+MALL_BYTES = 256 << 20      # Infinity Cache
+METRIC = "decode layer µs + HBM GB/s; prefill tokens/s + int8 MFMA % (one GPU)"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# synthetic inputs
+# ---------------------------------------------------------------------------
+def make_layer_tensors(si_amd, shape, seed):
+    rng = np.random.default_rng(seed)
+    H, QD = shape.hidden, shape.qheads * shape.hdim
+    KVD, F = shape.kvheads * shape.hdim, shape.ffn
+    q4 = lambda n, k: si_amd.quantize_q4_0(rng.normal(0, 0.02, (n, k)).astype(np.float32))
+    return dict(wq=q4(QD, H), wk=q4(KVD, H), wv=q4(KVD, H), wo=q4(H, QD),
+                norm=rng.normal(1, 0.1, H).astype(np.float32),
+                bq=rng.normal(0, 0.02, QD).astype(np.float32),
+                bk=rng.normal(0, 0.02, KVD).astype(np.float32),
+                bv=rng.normal(0, 0.02, KVD).astype(np.float32),
+                post_norm=rng.normal(1, 0.1, H).astype(np.float32),
+                wgate=q4(F, H), wup=q4(F, H), wdown=q4(H, F))
+
+
+def weight_bytes(shape):
+    H, QD, KVD, F = shape.hidden, shape.qheads * shape.hdim, shape.kvheads * shape.hdim, shape.ffn
+    q4 = lambda n, k: n * k // 32 * 18
+    return q4(QD + 2 * KVD, H) + q4(H, QD) + q4(2 * F, H) + q4(H, F)
+
+
+def small_bytes(shape):
+    """norm gains and QKV bias read once per token."""
+    QD, KVD = shape.qheads * shape.hdim, shape.kvheads * shape.hdim
+    return 4 * (2 * shape.hidden + QD + 2 * KVD)
+
+
+def gemm_int_ops(shape, m):
+    H, QD, KVD, F = shape.hidden, shape.qheads * shape.hdim, shape.kvheads * shape.hdim, shape.ffn
+    return 2 * m * ((QD + 2 * KVD) * H + H * QD + 2 * F * H + H * F)
+
+
+class Timer:
+    """HIP events on a given torch stream."""
+
+    def __init__(self, torch, stream):
+        self.torch, self.stream = torch, stream
+        self.a = torch.cuda.Event(enable_timing=True)
+        self.b = torch.cuda.Event(enable_timing=True)
+
+    def start(self):
+        self.a.record(self.stream)
+
+    def stop_ms(self):
+        self.b.record(self.stream)
+        self.b.synchronize()
+        return self.a.elapsed_time(self.b)
+
+
+# ---------------------------------------------------------------------------
+# configurations
+# ---------------------------------------------------------------------------
+def bench_decode_layer(torch, si_amd, stream, steps, warmup, ctx=1024):
+    """BASELINE config 2 (default workload)."""
+    s = si_amd.make_shape(**si_amd.SHAPES["0.5b"])
+    tens = make_layer_tensors(si_amd, s, 1)
+    kvd = s.kvheads * s.hdim
+    per_copy = weight_bytes(s) + 2 * ctx * kvd * 2 + small_bytes(s)
+    copies = int(np.ceil(1.25 * MALL_BYTES / per_copy))
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    layers, caches = [], []
+    for _ in range(copies):
+        layers.append(si_amd.Layer(s, tens, 1, ctx))
+        kc = torch.randn(ctx * kvd, generator=gen, device="cuda").half()
+        vc = torch.randn(ctx * kvd, generator=gen, device="cuda").half()
+        caches.append((kc, vc))
+    x = torch.randn(s.hidden, generator=gen, device="cuda")
+    out = torch.empty(s.hidden, device="cuda")
+    sh = si_amd.stream_handle(stream)
+    L = si_amd.lib()
+
+    def step(i):
+        lay = layers[i % copies]
+        kc, vc = caches[i % copies]
+        rc = L.si_layer_decode(lay.h, si_amd.ptr(x), si_amd.ptr(kc), si_amd.ptr(vc), ctx,
+                               si_amd.ptr(out), si_amd.SI_LAYER_FULL, sh)
+        if rc:
+            raise si_amd.SiError(rc, L.si_last_error().decode())
+
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            step(i)
+        torch.cuda.synchronize()
+        t = Timer(torch, stream)
+        t.start()
+        for i in range(steps):
+            step(i)
+        ms = t.stop_ms() / steps
+        torch.cuda.synchronize()
+        # per-phase breakdown (events between stages), averaged
+        layers[0].set_timing(True)
+        acc = {}
+        for i in range(20):
+            step(i * copies)  # copy 0 (timing enabled)
+            for k, v in layers[0].phase_ms().items():
+                acc[k] = acc.get(k, 0.0) + v / 20
+        layers[0].set_timing(False)
+    alg = per_copy
+    res = dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, alg_bytes=alg, copies=copies,
+               phases_us={k: round(v * 1e3, 2) for k, v in acc.items()})
+    return res, (layers, caches, s, x)
+
+
+def bench_dominant_gemv(torch, si_amd, stream, ctxobj, launches=400):
+    """Roofline of the decode step's dominant kernel: the fused gate|up
+    mat-vec (k_gemv_q4q8, 4.9 MB of the layer's 8.9 MB), launched alone on the
+    bench stream, cycling through the layer copies (cold weights)."""
+    layers, caches, s, x = ctxobj
+    L = si_amd.lib()
+    sh = si_amd.stream_handle(stream)
+    ws_list = []
+    F, H = s.ffn, s.hidden
+    n, k = 2 * F, H
+    # the same K-range split the layer uses (decode_splits in si_api.hip)
+    tiles = (n + 63) // 64
+    sp = max(1, min((512 + tiles - 1) // tiles, (k // 32) // 4))
+    wsb = L.si_matvec_workspace(n, k, sp)
+    ws = torch.zeros(max(wsb, 4), dtype=torch.uint8, device="cuda")
+    xq = torch.randint(-127, 128, (k,), dtype=torch.int8, device="cuda")
+    xd = torch.full((k // 32,), 0x2c00, dtype=torch.int16, device="cuda")  # fp16 0.0625
+    xs = xq.view(-1, 32).sum(1, dtype=torch.int32).to(torch.int16)
+    out = torch.empty(n, device="cuda")
+    mats = [lay.weights(2) for lay in layers]
+
+    def launch(i):
+        qs, d, nn, kk = mats[i % len(mats)]
+        rc = L.si_matvec_q4q8(ctypes.c_void_p(qs), ctypes.c_void_p(d), nn, kk, si_amd.ptr(xq),
+                              si_amd.ptr(xd), si_amd.ptr(xs), None, None, si_amd.ptr(out), sp,
+                              si_amd.ptr(ws), sh)
+        if rc:
+            raise si_amd.SiError(rc, L.si_last_error().decode())
+
+    with torch.cuda.stream(stream):
+        for i in range(20):
+            launch(i)
+        t = Timer(torch, stream)
+        t.start()
+        for i in range(launches):
+            launch(i)
+        ms = t.stop_ms() / launches
+    alg = n * k // 32 * 18 + k + (k // 32) * 4 + n * 4
+    achieved = alg / (ms * 1e-3) / 1e9
+    del ws_list
+    return dict(kernel="k_gemv_q4q8 (gate|up, N=9728 K=896)", us=ms * 1e3, alg_bytes=alg,
+                achieved_gbs=achieved, splits=sp)
+
+
+def bench_qkv_gemv(torch, si_amd, stream, launches=2000):
+    """fused QKV mat-vec, K=896 N=1152, one token."""
+    from_seed = np.random.default_rng(11)
+    n, k = 1152, 896
+    w = si_amd.quantize_q4_0(from_seed.normal(0, 0.02, (n, k)).astype(np.float32))
+    L = si_amd.lib()
+    sh = si_amd.stream_handle(stream)
+    per = n * k // 32 * 18
+    copies = int(np.ceil(1.25 * MALL_BYTES / per))
+    wdev = torch.from_numpy(w).cuda()
+    mats = []
+    for _ in range(copies):
+        qs = torch.empty(n * k // 2, dtype=torch.uint8, device="cuda")
+        d = torch.empty(n * k // 32, dtype=torch.int16, device="cuda")
+        si_amd.call("si_q4_repack", si_amd.ptr(wdev), n, k, si_amd.ptr(qs), si_amd.ptr(d), sh)
+        mats.append((qs, d))
+    x = torch.randn(k, device="cuda")
+    xq = torch.empty(k, dtype=torch.int8, device="cuda")
+    xd = torch.empty(k // 32, dtype=torch.int16, device="cuda")
+    xs = torch.empty(k // 32, dtype=torch.int16, device="cuda")
+    si_amd.call("si_quantize_q8_rows", si_amd.ptr(x), 1, k, si_amd.ptr(xq), si_amd.ptr(xd),
+                si_amd.ptr(xs), sh)
+    bias = torch.randn(n, device="cuda") * 0.02
+    out = torch.empty(n, device="cuda")
+    tiles = (n + 63) // 64
+    sp = max(1, min((512 + tiles - 1) // tiles, (k // 32) // 4))
+    ws = torch.zeros(max(L.si_matvec_workspace(n, k, sp), 4), dtype=torch.uint8, device="cuda")
+
+    def launch(i):
+        qs, d = mats[i % copies]
+        rc = L.si_matvec_q4q8(si_amd.ptr(qs), si_amd.ptr(d), n, k, si_amd.ptr(xq),
+                              si_amd.ptr(xd), si_amd.ptr(xs), si_amd.ptr(bias), None,
+                              si_amd.ptr(out), sp, si_amd.ptr(ws), sh)
+        if rc:
+            raise si_amd.SiError(rc, L.si_last_error().decode())
+
+    with torch.cuda.stream(stream):
+        for i in range(50):
+            launch(i)
+        t = Timer(torch, stream)
+        t.start()
+        for i in range(launches):
+            launch(i)
+        ms = t.stop_ms() / launches
+    alg = 586168  # W 580,608 + x 952 + y 4,608
+    return dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, copies=copies, splits=sp)
+
+
+def bench_prefill(torch, si_amd, stream, shape_name, ntok, steps):
+    """BASELINE configs 3 (0.5B, 512 tokens) and 4 (7B, 2048 tokens)."""
+    s = si_amd.make_shape(**si_amd.SHAPES[shape_name])
+    tens = make_layer_tensors(si_amd, s, 5)
+    lay = si_amd.Layer(s, tens, ntok, ntok)
+    kvd = s.kvheads * s.hdim
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    x = torch.randn(ntok * s.hidden, generator=gen, device="cuda")
+    kc = torch.zeros(ntok * kvd, dtype=torch.float16, device="cuda")
+    vc = torch.zeros_like(kc)
+    out = torch.empty(ntok * s.hidden, device="cuda")
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            lay.prefill(x, ntok, 0, kc, vc, out, stream=stream)
+        t = Timer(torch, stream)
+        t.start()
+        for _ in range(steps):
+            lay.prefill(x, ntok, 0, kc, vc, out, stream=stream)
+        ms = t.stop_ms() / steps
+        lay.set_timing(True)
+        lay.prefill(x, ntok, 0, kc, vc, out, stream=stream)
+        ph = lay.phase_ms()
+        lay.set_timing(False)
+    gemm_ms = ph["qkv_proj"] + ph["out_proj"] + ph["gate_up"] + ph["down_proj"]
+    ops = gemm_int_ops(s, ntok)
+    lay.close()
+    return dict(ms=ms, tokens_per_s=ntok / (ms * 1e-3),
+                gemm_ms=gemm_ms, gemm_tops=ops / (gemm_ms * 1e-3) / 1e12,
+                mfma_pct_gemm=100.0 * ops / (gemm_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
+                mfma_pct_layer=100.0 * ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
+                phases_ms={k: round(v, 4) for k, v in ph.items()})
+
+
+def bench_batched_decode(torch, si_amd, stream, steps, nseq=64, ctx=4096):
+    """7B layer, 64 sequences x 1 token, 4096-position caches."""
+    s = si_amd.make_shape(**si_amd.SHAPES["7b"])
+    tens = make_layer_tensors(si_amd, s, 7)
+    lay = si_amd.Layer(s, tens, nseq, ctx)
+    kvd = s.kvheads * s.hdim
+    stride = ctx * kvd
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    kc = torch.randn(nseq * stride, generator=gen, device="cuda").half()
+    vc = torch.randn(nseq * stride, generator=gen, device="cuda").half()
+    x = torch.randn(nseq * s.hidden, generator=gen, device="cuda")
+    out = torch.empty(nseq * s.hidden, device="cuda")
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            lay.decode_batch(x, nseq, kc, vc, stride, ctx, ctx, out, stream=stream)
+        t = Timer(torch, stream)
+        t.start()
+        for _ in range(steps):
+            lay.decode_batch(x, nseq, kc, vc, stride, ctx, ctx, out, stream=stream)
+        ms = t.stop_ms() / steps
+        lay.set_timing(True)
+        lay.decode_batch(x, nseq, kc, vc, stride, ctx, ctx, out, stream=stream)
+        ph = lay.phase_ms()
+        lay.set_timing(False)
+    alg = weight_bytes(s) + nseq * 2 * ctx * kvd * 2 + small_bytes(s)
+    lay.close()
+    return dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, alg_bytes=alg,
+                phases_us={k: round(v * 1e3, 2) for k, v in ph.items()})
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle (C restatement of the reference's portable path)
+# ---------------------------------------------------------------------------
+def cpu_baseline(budget_s=12.0, ctx=1024):
+    from oracle.oracle_py import Oracle, make_shape as or_shape
+    import si_amd
+    o = Oracle()
+    sd = si_amd.SHAPES["0.5b"]
+    s = or_shape(**sd)
+    tens = make_layer_tensors(si_amd, si_amd.make_shape(**sd), 1)
+    rng = np.random.default_rng(3)
+    kvd = s.kvheads * s.hdim
+    kc = o.f32_to_f16(rng.standard_normal(ctx * kvd).astype(np.float32))
+    vc = o.f32_to_f16(rng.standard_normal(ctx * kvd).astype(np.float32))
+    x = rng.standard_normal(s.hidden).astype(np.float32)
+    old = os.sched_getaffinity(0)
+    core = sorted(old)[0]
+    os.sched_setaffinity(0, {core})
+    try:
+        o.layer_decode(s, tens, x, kc, vc, ctx)  # warm-up
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while time.perf_counter() < t_end and len(times) < 2000:
+            t0 = time.perf_counter()
+            o.layer_decode(s, tens, x, kc, vc, ctx)
+            times.append(time.perf_counter() - t0)
+    finally:
+        os.sched_setaffinity(0, old)
+    med = float(np.median(times))
+    alg = weight_bytes(si_amd.make_shape(**sd)) + 2 * ctx * kvd * 2 + small_bytes(s)
+    cpu = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return dict(value=alg / med / 1e9, unit="GB/s", cores=1, kind="port",
+                sample=f"{len(times)} full 0.5B layer decodes at context 1024 "
+                       f"(median {med * 1e3:.2f} ms/token) on core {core} of '{cpu}', "
+                       f"oracle/libsi_oracle.so built -O2 -ffp-contract=off")
+
+
+# ---------------------------------------------------------------------------
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--quick", action="store_true", help="skip the other configurations")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); "
+              "multi-GPU sharding is described in DESIGN.md, not run.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import si_amd
+    assert torch.cuda.is_available(), "bench.py needs an MI355X"
+    torch.cuda.set_device(0)
+    stream = torch.cuda.Stream()
+    t0 = time.time()
+    log("config 2: 0.5B decode layer, ctx 1024 ...")
+    dec, ctxobj = bench_decode_layer(torch, si_amd, stream, args.steps, args.warmup)
+    log(f"  {dec['us']:.2f} us/token, {dec['gbs']:.1f} GB/s ({time.time() - t0:.0f} s)")
+    log("roofline: dominant kernel ...")
+    dom = bench_dominant_gemv(torch, si_amd, stream, ctxobj)
+    log(f"  {dom['us']:.2f} us/launch, {dom['achieved_gbs']:.1f} GB/s")
+    extra = {}
+    if not args.quick:
+        log("config 1: QKV GEMV ...")
+        extra["cfg1_qkv_gemv_0.5b"] = bench_qkv_gemv(torch, si_amd, stream)
+        log(f"  {extra['cfg1_qkv_gemv_0.5b']}")
+        log("config 3: 0.5B prefill 512 ...")
+        extra["cfg3_prefill_0.5b_512"] = bench_prefill(torch, si_amd, stream, "0.5b", 512, 10)
+        log(f"  {extra['cfg3_prefill_0.5b_512']}")
+        log("config 4: 7B prefill 2048 ...")
+        extra["cfg4_prefill_7b_2048"] = bench_prefill(torch, si_amd, stream, "7b", 2048, 3)
+        log(f"  {extra['cfg4_prefill_7b_2048']}")
+        log("config 5: 7B batched decode 64 x 4096 ...")
+        extra["cfg5_batched_decode_7b_64x4096"] = bench_batched_decode(torch, si_amd, stream, 5)
+        log(f"  {extra['cfg5_batched_decode_7b_64x4096']}")
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (oracle, 1 core) ...")
+        cpu = cpu_baseline()
+        log(f"  {cpu}")
+    line = {
+        "metric": METRIC,
+        "value": round(dec["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["us"] / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8xint4 (fp32 accumulate)",
+        "data": "synthetic (seeded N(0,0.02) weights -> Q4_0, N(0,1) activations and fp16 KV)",
+        "config": {"workload": "full Qwen2.5-0.5B-shaped layer, decode of 1 token at context "
+                               "1024 (BASELINE configs[1])",
+                   "hidden": 896, "qheads": 14, "kvheads": 2, "head_dim": 64, "ffn": 4864,
+                   "context": 1024, "layer_copies_rotated": dec["copies"],
+                   "alg_bytes_per_step": dec["alg_bytes"]},
+        "decode_layer_us": round(dec["us"], 3),
+        "phases_us": dec["phases_us"],
+        "roofline": {"bound": "hbm", "achieved": round(dom["achieved_gbs"], 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": dom["kernel"], "kernel_us": round(dom["us"], 3),
+                     "alg_bytes_per_launch": dom["alg_bytes"]},
+        "cpu_baseline": cpu,
+        "other_configs": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

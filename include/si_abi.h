@@ -1,0 +1,266 @@
+/*
+ * si_abi.h -- C ABI of the MI355X (gfx950) one-Qwen-layer hot path.
+ *
+ * The reference is one C translation unit of static functions over raw
+ * pointers with compile-time shapes (qwen_one_layer.c, attention_kernels.h,
+ * fused_layer.h).  This ABI replaces its hot-path functions with HIP kernels:
+ *
+ *   - plain C types only: device pointers, sizes, an opaque stream handle
+ *     (a hipStream_t passed as void*; NULL = the default stream);
+ *   - the caller owns every buffer (as in the reference); nothing here
+ *     allocates device memory except si_layer_create / si_layer_destroy;
+ *   - shapes are runtime values (si_shape_t) instead of defines.h:16-25;
+ *   - every call returns 0 on success or an SI_ERR_* code, with a message in
+ *     si_last_error(); the reference's die() (qwen_one_layer.c:26-28) is the
+ *     host mirror's job (include/si_host.h);
+ *   - calls only enqueue work on the stream; none synchronizes the host.
+ *
+ * Device data formats
+ *   Q4_0 weights (the reference's row-major [N][K/32] 18-byte blocks,
+ *   repack_weights.py:43-52) are repacked losslessly once (si_q4_repack) into
+ *       qs : uint8  [K/32][N][16]   byte j = element j | element j+16 << 4
+ *       d  : uint16 [K/32][N]       fp16 scale bits
+ *   so one wavefront reads 64 rows x 16 B of one block as 1 KiB contiguous.
+ *   Q8_0 activations are planar:
+ *       qs : int8   [M][K]          d : uint16 [M][K/32]
+ *       s  : int16  [M][K/32]       sum of the block's 32 int8 values
+ *   (s lets the Q4_0 offset of 8 be applied once per block:
+ *    sum((n-8)*a) = sum(n*a) - 8*sum(a), an exact integer identity).
+ *   The KV cache is the reference's fp16 [ctx][kvheads][hdim] K and V arrays
+ *   (attention_kernels.h:43-44, :101-105).
+ */
+#ifndef SI_ABI_H
+#define SI_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    SI_OK = 0,
+    SI_ERR_ARG = 1,    /* invalid size, shape or pointer */
+    SI_ERR_HIP = 2,    /* a HIP runtime call failed */
+    SI_ERR_STATE = 3,  /* object not ready / wrong mode */
+    SI_ERR_NOMEM = 4   /* device allocation failed (create only) */
+};
+
+/* Message of the last failing call on this host thread. */
+const char *si_last_error(void);
+
+/* defines.h:16-25 (HIDDEN, QHEADS, KVHEADS, HDIM, ROPE_BASE, RMS_EPS) as
+ * runtime values; ffn is the build-defined SwiGLU width (0 = none). */
+typedef struct si_shape {
+    int hidden;
+    int qheads;
+    int kvheads;
+    int hdim;
+    int ffn;
+    float rope_base;
+    float rms_eps;
+} si_shape_t;
+
+/* ------------------------------------------------------------------ */
+/* Formats                                                             */
+/* ------------------------------------------------------------------ */
+
+/* Lossless row-major Q4_0 -> device repack.  Replaces the role of
+ * repack_weights.py:43-52 (a lossless target-specific relayout). */
+int si_q4_repack(const uint8_t *src_rowmajor, int n, int k, uint8_t *qs,
+                 uint16_t *d, void *stream);
+/* Inverse of si_q4_repack (round-trip check, repack_weights.py:126-137). */
+int si_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k,
+                 uint8_t *dst_rowmajor, void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Primitive kernels (one per reference function)                      */
+/* ------------------------------------------------------------------ */
+
+/* quantize_q8 (qwen_one_layer.c:98-116): count fp32 values -> count/32
+ * block_q8_0 records of 34 bytes (defines.h:27-28), bit-exact. */
+int si_quantize_q8(const float *src, void *dst_blocks, int count, void *stream);
+
+/* quantize_q8 over rows x k values into the planar format (bit-exact). */
+int si_quantize_q8_rows(const float *src, int rows, int k, int8_t *qs,
+                        uint16_t *d, int16_t *s, void *stream);
+
+/* rmsnorm (qwen_one_layer.c:164-169) then quantize_q8, per row.  gain may be
+ * NULL (identity, :168); normed (fp32 copy) may be NULL. */
+int si_rmsnorm_q8(const float *x, const float *gain, int rows, int n, float eps,
+                  float *normed, int8_t *qs, uint16_t *d, int16_t *s, void *stream);
+
+/* Per-(row, block) int32 Q4_0 x Q8_0 dots, dots[n][k/32] (dot_32_q4q8,
+ * qwen_one_layer.c:118-146).  Test entry point for the integer core. */
+int si_q4q8_block_dots(const uint8_t *wqs, const uint16_t *wd, int n, int k,
+                       const int8_t *xqs, const int16_t *xs, int32_t *dots,
+                       void *stream);
+
+/* matvec_q4q8 (qwen_one_layer.c:148-162), one activation row:
+ *   out[r] = residual[r] + (bias[r] + sum_b ((float)dot_b * w.d) * x.d)
+ * bias and residual may be NULL.  With splits == 1 the blocks of a row are
+ * accumulated in order with the reference's rounding (bit-exact); splits > 1
+ * divides K into that many contiguous ranges for parallelism; the range sums
+ * are then added in range order inside the same kernel (within fp32 rounding
+ * of the reference).  splits > 1 needs a workspace of
+ * si_matvec_workspace(n, k, splits) bytes whose contents are zero before its
+ * first use; every call leaves it ready for the next (calls sharing one
+ * workspace must not run concurrently). */
+int si_matvec_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k,
+                   const int8_t *xqs, const uint16_t *xd, const int16_t *xs,
+                   const float *bias, const float *residual, float *out,
+                   int splits, void *workspace, void *stream);
+size_t si_matvec_workspace(int n, int k, int splits);
+
+/* matvec_q4q8 applied to m activation rows (prefill / batched decode):
+ * out[i][r] (row stride ldo) = residual + bias + sum over blocks.  int8
+ * matrix-core tiles with fp32 scale epilogues; within fp32 rounding. */
+int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k,
+                 const int8_t *xqs, const uint16_t *xd, int m,
+                 const float *bias, const float *residual, float *out, int ldo,
+                 void *stream);
+
+/* RoPE (qwen_one_layer.c:172-183) + fp16 K/V append (:262-266) for ntok
+ * rows of the fused projection output qkv[t] = [q | k | v]
+ * (qheads*hdim + 2*kvheads*hdim floats, row stride ldqkv).  Token t is at
+ * position ctx_dev[t]-1 when ctx_dev (device ints) is given, else
+ * pos0 + t*pos_step (1 for a prefill batch, 0 for one position per row).
+ * Writes rotated q to q_out[t] (qheads*hdim), K/V rows into kc/vc
+ * (+ t*kv_seq_stride elements when kv_seq_stride != 0, i.e. one cache per
+ * sequence; kv_seq_stride == 0 means one shared cache; a multiple of 8).
+ * rope_cos/rope_sin: [max_pos][hdim/2] tables (si_rope_table); rows whose
+ * position falls outside 0..max_pos-1 are skipped. */
+int si_rope_kv_append(const si_shape_t *s, const float *qkv, int ldqkv, int ntok,
+                      int pos0, int pos_step, int max_pos, const int *ctx_dev,
+                      const float *rope_cos,
+                      const float *rope_sin, float *q_out, uint16_t *kc,
+                      uint16_t *vc, size_t kv_seq_stride, void *stream);
+
+/* Host-side RoPE table, theta = pos / powf(base, 2i/hdim) with libm
+ * cosf/sinf exactly as qwen_one_layer.c:176-177; [npos][hdim/2] each. */
+int si_rope_table(int npos, int hdim, float base, float *cos_host, float *sin_host);
+
+/* attention_flash (attention_kernels.h:80-164) for nq queries, GQA.
+ * q: [nq][qheads*hdim] fp32.  Query i attends to positions [0, ctx_i) of
+ * cache kc/vc + i*kv_seq_stride, where ctx_i = ctx_dev[i] if ctx_dev != NULL,
+ * else ctx0 + i*ctx_step (decode: ctx_step 0; causal prefill: ctx_step 1).
+ * Contexts above max_ctx are clamped to it; a context <= 0 gives zeros
+ * (attention_kernels.h:95-98).  Output attn fp32 [nq][qheads*hdim] and its
+ * Q8_0 quantization (planar, optional: pass NULL qs to skip).
+ * workspace: si_attention_workspace bytes. */
+int si_attention(const si_shape_t *s, const float *q, int nq, const uint16_t *kc,
+                 const uint16_t *vc, size_t kv_seq_stride, const int *ctx_dev,
+                 int ctx0, int ctx_step, int max_ctx, float *attn, int8_t *qs,
+                 uint16_t *d, int16_t *bsum, void *workspace, size_t workspace_bytes,
+                 void *stream);
+size_t si_attention_workspace(const si_shape_t *s, int nq, int max_ctx);
+
+/* Build-defined SwiGLU + quantize_q8: act = silu(gate)*up with
+ * silu(g) = g/(1+expf(-g)); gate = gu[r][0..f), up = gu[r][f..2f). */
+int si_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs,
+                 uint16_t *d, int16_t *s, void *stream);
+
+/* h = x + y (residual) then rmsnorm + quantize_q8 of h. */
+int si_residual_rmsnorm_q8(const float *x, const float *y, const float *gain,
+                           int rows, int n, float eps, float *h, float *normed,
+                           int8_t *qs, uint16_t *d, int16_t *s, void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Layer level (run_layer / run_layer_fused / pf_run_batch)            */
+/* ------------------------------------------------------------------ */
+
+/* Host-side layer tensors in the reference's file formats
+ * (qwen_one_layer.c:210-221): row-major Q4_0 matrices, optional fp32
+ * norm/bias vectors (NULL = identity/zero).  post_norm, wgate, wup, wdown
+ * are the build-defined FFN (all NULL = attention sublayer only). */
+typedef struct si_layer_host {
+    const uint8_t *wq, *wk, *wv, *wo;
+    const float *norm, *bq, *bk, *bv;
+    const float *post_norm;
+    const uint8_t *wgate, *wup, *wdown;
+} si_layer_host_t;
+
+typedef struct si_layer si_layer_t; /* opaque: device weights + workspaces */
+
+/* Uploads and repacks the weights, builds RoPE tables for max_pos
+ * positions and sizes workspaces for up to max_tokens rows per call.
+ * The only calls that allocate device memory. */
+int si_layer_create(const si_shape_t *s, const si_layer_host_t *w, int max_tokens,
+                    int max_pos, si_layer_t **out);
+int si_layer_destroy(si_layer_t *l);
+
+enum {
+    SI_LAYER_FULL = 0,      /* attention + residual + norm + SwiGLU FFN + residual */
+    SI_LAYER_ATTN_ONLY = 1, /* reference run_layer: out = W_O . Q8(attn)          */
+    SI_LAYER_EXACT = 2      /* decode GEMVs without K splits (bit-exact projections) */
+};
+
+/* run_layer (qwen_one_layer.c:237-281) for one token at position context-1:
+ * x [hidden] -> out [hidden]; appends K/V at row context-1 of kc/vc. */
+int si_layer_decode(si_layer_t *l, const float *x, uint16_t *kc, uint16_t *vc,
+                    int context, float *out, int flags, void *stream);
+
+/* Batched decode: nseq independent sequences, one new token each.
+ * x, out: [nseq][hidden]; sequence i's cache is kc/vc + i*kv_seq_stride,
+ * its new token sits at position ctx_dev[i]-1 (device int array; NULL = all
+ * context).  max_ctx bounds every context. */
+int si_layer_decode_batch(si_layer_t *l, const float *x, int nseq, uint16_t *kc,
+                          uint16_t *vc, size_t kv_seq_stride, const int *ctx_dev,
+                          int context, int max_ctx, float *out, int flags,
+                          void *stream);
+
+/* pf_run_batch (prefill_weight_stationary.h:183-311): causal prefill of
+ * ntok tokens after prefix cached positions.  Appends K/V rows
+ * prefix..prefix+ntok-1; token t attends with context prefix+t+1. */
+int si_layer_prefill(si_layer_t *l, const float *x, int ntok, int prefix,
+                     uint16_t *kc, uint16_t *vc, float *out, int flags, void *stream);
+
+/* Device pointers to a layer's intermediates of the last call, for parity
+ * checks and captures (run_layer's attn_copy/q8_copy, :278-279). */
+enum {
+    SI_BUF_NORMED = 0,  /* fp32 [rows][hidden]                  */
+    SI_BUF_XQ_QS, SI_BUF_XQ_D, SI_BUF_XQ_S,
+    SI_BUF_QKV,         /* fp32 [rows][qd + 2 kvd] (pre-RoPE)   */
+    SI_BUF_Q,           /* fp32 [rows][qd] rotated q            */
+    SI_BUF_ATTN,        /* fp32 [rows][qd]                      */
+    SI_BUF_ATTQ_QS, SI_BUF_ATTQ_D, SI_BUF_ATTQ_S,
+    SI_BUF_ATTN_OUT,    /* fp32 [rows][hidden] W_O output       */
+    SI_BUF_H,           /* fp32 [rows][hidden] residual 1       */
+    SI_BUF_NORMED2,
+    SI_BUF_XQ2_QS, SI_BUF_XQ2_D, SI_BUF_XQ2_S,
+    SI_BUF_GU,          /* fp32 [rows][2 ffn] gate | up         */
+    SI_BUF_ACT,         /* fp32 [rows][ffn]                     */
+    SI_BUF_ACTQ_QS, SI_BUF_ACTQ_D, SI_BUF_ACTQ_S,
+    SI_BUF_COUNT
+};
+void *si_layer_buffer(si_layer_t *l, int which);
+
+/* Per-phase GPU timing of layer calls (hipEvents between stages), the
+ * device analogue of phase_t (defines.h:35-37, qwen_one_layer.c:245-276).
+ * RMSNorm+Q8, attention+Q8, SwiGLU+Q8 are single fused kernels. */
+enum {
+    SI_PHASE_RMS_Q8 = 0,
+    SI_PHASE_QKV,
+    SI_PHASE_ROPE_KV,
+    SI_PHASE_ATTENTION_Q8,
+    SI_PHASE_OUT_PROJ,
+    SI_PHASE_POST_NORM_Q8,
+    SI_PHASE_GATE_UP,
+    SI_PHASE_SWIGLU_Q8,
+    SI_PHASE_DOWN,
+    SI_PHASE_COUNT
+};
+int si_layer_set_timing(si_layer_t *l, int enable);
+/* Milliseconds per phase of the last timed call; waits for it to finish. */
+int si_layer_phase_ms(si_layer_t *l, float *ms);
+
+/* Device weights of a created layer, for kernel-level benchmarks:
+ * which = 0 QKV (fused rows q|k|v), 1 O, 2 gate|up, 3 down. */
+int si_layer_weights(si_layer_t *l, int which, const uint8_t **qs,
+                     const uint16_t **d, int *n, int *k);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SI_ABI_H */

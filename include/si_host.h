@@ -1,0 +1,119 @@
+/*
+ * si_host.h -- C11 host mirror of the reference's layer and kernel entry
+ * points, running on the MI355X through include/si_abi.h.
+ *
+ * Same names, argument meaning and error behaviour as the reference:
+ *   - run_layer           qwen_one_layer.c:237-281
+ *   - run_layer_fused     register_fusion.h:344-411 (same math on the GPU)
+ *   - pf_run_batch        prefill_weight_stationary.h:183-311
+ *   - attention_compute   attention_kernels.h:166-173
+ *   - attention_flash     attention_kernels.h:80-164
+ *   - quantize_q8         qwen_one_layer.c:98-116
+ *   - load_layer / free_layer  qwen_one_layer.c:188-226
+ * Differences, all forced by the device boundary:
+ *   - shapes are runtime (si_shape_t) and travel inside si_model_t, which
+ *     replaces the compile-time macros of defines.h:16-25;
+ *   - activations, KV caches and outputs are DEVICE pointers (the caller
+ *     owns them, as in the reference); weights are uploaded once by
+ *     load_layer;
+ *   - errors still never return: they print and exit(1) like die()
+ *     (qwen_one_layer.c:26-28);
+ *   - timings (phase_t) are GPU event times in seconds; phases the GPU
+ *     fuses (RMSNorm+Q8, attention+Q8) report the fused time in the first
+ *     phase and 0 in the second; the fused Q/K/V projection is apportioned
+ *     by output rows, as fused_layer.h:424-426 splits its fused K/V time.
+ */
+#ifndef SI_HOST_H
+#define SI_HOST_H
+
+#include <stdint.h>
+
+#include "si_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* defines.h:27-28 */
+typedef struct { uint16_t d; int8_t qs[32]; } block_q8_0;
+
+/* defines.h:35-37 */
+typedef struct {
+    float rms, q8_input, q_proj, k_proj, v_proj, rope_cache, attention, q8_output, out_proj;
+} phase_t;
+
+/* fused_layer.h:68-71 */
+typedef struct {
+    phase_t phase;
+    double tcm_stage; /* no scratchpad staging on the GPU: always 0 */
+} fused_stats_t;
+
+/* attention_kernels.h:24-27 */
+typedef enum { ATTENTION_STANDARD = 0, ATTENTION_FLASH = 1 } attention_method_t;
+
+/* A loaded layer: shape + device weights + stream (replaces layer_t and
+ * fused_weights_t, defines.h:30-33, fused_layer.h:60-66). */
+typedef struct {
+    si_shape_t shape;
+    si_layer_t *layer;
+    void *stream;      /* hipStream_t; NULL = default stream */
+    int max_tokens;
+    int max_pos;
+    void *attn_ws;     /* device workspace for attention_compute/_flash */
+    size_t attn_ws_bytes;
+} si_model_t;
+
+/* load_layer (qwen_one_layer.c:210-221): reads q.q4_0 k.q4_0 v.q4_0 o.q4_0
+ * and the optional norm.f32 q_bias.f32 k_bias.f32 v_bias.f32 from dir with
+ * the reference's exact size checks, plus the build-defined FFN files
+ * post_norm.f32 gate.q4_0 up.q4_0 down.q4_0 when present. */
+si_model_t *load_layer(const si_shape_t *shape, const char *dir, int max_tokens, int max_pos);
+
+/* Same, from host tensors already in memory. */
+si_model_t *si_model_from_host(const si_shape_t *shape, const si_layer_host_t *w,
+                               int max_tokens, int max_pos);
+void free_layer(si_model_t *m);
+
+/* qwen_one_layer.c:237-281 with device x/kc/vc/output.  scores is unused
+ * (both methods run the streaming kernel).  attn_copy (fp32 [qheads*hdim])
+ * and q8_copy (block_q8_0 [qheads*hdim/32]) are HOST buffers or NULL,
+ * filled after the timed work as the reference's captures are (:277-279). */
+phase_t run_layer(const si_model_t *l, const float *x, uint16_t *kc, uint16_t *vc,
+                  int context, float *output, attention_method_t method, float *scores,
+                  float *attn_copy, block_q8_0 *q8_copy);
+
+/* register_fusion.h:344-411: identical result contract to run_layer. */
+fused_stats_t run_layer_fused(const si_model_t *l, const float *x, uint16_t *kc,
+                              uint16_t *vc, int context, float *output, float *attn_capture,
+                              block_q8_0 *q8_capture);
+
+/* Full build-defined Qwen2 layer (attention + residual + post-norm + SwiGLU
+ * FFN + residual) for one token. */
+phase_t run_layer_full(const si_model_t *l, const float *x, uint16_t *kc, uint16_t *vc,
+                       int context, float *output);
+
+/* pf_run_batch (prefill_weight_stationary.h:183-311): x [ntok][hidden]
+ * device, K/V appended at prefix..prefix+ntok-1, output [ntok][hidden].
+ * full != 0 runs the build-defined full layer per token. */
+void pf_run_batch(const si_model_t *l, const float *x, int ntok, int prefix, uint16_t *kc,
+                  uint16_t *vc, float *output, int full);
+
+/* attention_kernels.h:80-164 / :166-173 for one token (device q/kc/vc/out). */
+void attention_flash(const si_model_t *l, const float *q, const uint16_t *kc,
+                     const uint16_t *vc, int context, float *out);
+void attention_compute(const si_model_t *l, attention_method_t method, const float *q,
+                       const uint16_t *kc, const uint16_t *vc, int context, float *out,
+                       float *score_workspace);
+
+/* qwen_one_layer.c:98-116 on device buffers (dst: block_q8_0 records). */
+void quantize_q8(const float *src, block_q8_0 *dst, int count);
+
+/* Offline weight preparation (host memory): ggml's Q4_0 rule, the format
+ * extract_weights.py copies from GGUF.  Per 32 values: d = m/-8 for the
+ * signed value m of largest magnitude, nibble = min(15, trunc(x/d + 8.5)). */
+void si_quantize_q4_0_host(const float *src, uint8_t *dst, int count);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,624 @@
+// si_api.hip -- extern "C" entry points of include/si_abi.h.
+//
+// Argument checking, the layer object (device weights, RoPE tables,
+// workspaces) and the three layer schedules: single-token decode
+// (run_layer, qwen_one_layer.c:237-281), batched decode, and causal prefill
+// (pf_run_batch, prefill_weight_stationary.h:183-311).
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/si_abi.h"
+#include "si_kernels.hpp"
+
+using namespace si;
+
+static thread_local std::string g_err;
+
+static int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+static int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+static int check_launch(const char *what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(SI_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return SI_OK;
+}
+
+#define SI_REQUIRE(cond, ...) \
+    do {                      \
+        if (!(cond)) return fail(SI_ERR_ARG, __VA_ARGS__); \
+    } while (0)
+
+#define HIP_TRY(call)                                                                    \
+    do {                                                                                 \
+        hipError_t e_ = (call);                                                          \
+        if (e_ != hipSuccess) return fail(SI_ERR_HIP, "%s: %s", #call, hipGetErrorString(e_)); \
+    } while (0)
+
+static inline hipStream_t S(void *stream) { return (hipStream_t)stream; }
+
+static int check_shape(const si_shape_t *s) {
+    SI_REQUIRE(s, "shape is NULL");
+    SI_REQUIRE(s->hidden > 0 && s->hidden % 32 == 0, "hidden %d must be a positive multiple of 32",
+               s->hidden);
+    SI_REQUIRE(attn_supported(s->qheads, s->kvheads, s->hdim),
+               "unsupported heads %d/%d x hdim %d (need qheads %% kvheads == 0, ratio <= 8, "
+               "hdim in 32..128 multiple of 32)",
+               s->qheads, s->kvheads, s->hdim);
+    SI_REQUIRE(s->ffn >= 0 && s->ffn % 32 == 0, "ffn %d must be a multiple of 32", s->ffn);
+    SI_REQUIRE(s->hidden <= 8192, "hidden %d exceeds 8192", s->hidden);
+    return SI_OK;
+}
+
+extern "C" {
+
+const char *si_last_error(void) { return g_err.c_str(); }
+
+int si_q4_repack(const uint8_t *src, int n, int k, uint8_t *qs, uint16_t *d, void *stream) {
+    SI_REQUIRE(n > 0 && k > 0 && k % 32 == 0, "repack: bad size n=%d k=%d", n, k);
+    SI_REQUIRE(src && qs && d, "repack: NULL pointer");
+    launch_q4_repack(src, n, k, qs, d, S(stream));
+    return check_launch("si_q4_repack");
+}
+
+int si_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k, uint8_t *dst, void *stream) {
+    SI_REQUIRE(n > 0 && k > 0 && k % 32 == 0, "unpack: bad size n=%d k=%d", n, k);
+    SI_REQUIRE(dst && qs && d, "unpack: NULL pointer");
+    launch_q4_unpack(qs, d, n, k, dst, S(stream));
+    return check_launch("si_q4_unpack");
+}
+
+int si_quantize_q8(const float *src, void *dst, int count, void *stream) {
+    // qwen_one_layer.c:99: the reference dies unless count % 32 == 0
+    SI_REQUIRE(count >= 0 && count % 32 == 0, "Q8 quantization length must be multiple of 32");
+    SI_REQUIRE(count == 0 || (src && dst), "quantize_q8: NULL pointer");
+    launch_quantize_q8_aos(src, dst, count, S(stream));
+    return check_launch("si_quantize_q8");
+}
+
+int si_quantize_q8_rows(const float *src, int rows, int k, int8_t *qs, uint16_t *d, int16_t *s,
+                        void *stream) {
+    SI_REQUIRE(rows >= 0 && k > 0 && k % 32 == 0, "Q8 quantization length must be multiple of 32");
+    SI_REQUIRE(rows == 0 || (src && qs && d), "quantize_q8_rows: NULL pointer");
+    launch_quantize_q8_rows(src, rows, k, qs, d, s, S(stream));
+    return check_launch("si_quantize_q8_rows");
+}
+
+int si_rmsnorm_q8(const float *x, const float *gain, int rows, int n, float eps, float *normed,
+                  int8_t *qs, uint16_t *d, int16_t *s, void *stream) {
+    SI_REQUIRE(rows >= 0 && n > 0 && n % 32 == 0 && n <= 8192, "rmsnorm: bad size n=%d", n);
+    SI_REQUIRE(rows == 0 || (x && qs && d), "rmsnorm: NULL pointer");
+    launch_rmsnorm_q8(x, nullptr, gain, rows, n, eps, nullptr, normed, qs, d, s, S(stream));
+    return check_launch("si_rmsnorm_q8");
+}
+
+int si_residual_rmsnorm_q8(const float *x, const float *y, const float *gain, int rows, int n,
+                           float eps, float *h, float *normed, int8_t *qs, uint16_t *d,
+                           int16_t *s, void *stream) {
+    SI_REQUIRE(rows >= 0 && n > 0 && n % 32 == 0 && n <= 8192, "rmsnorm: bad size n=%d", n);
+    SI_REQUIRE(rows == 0 || (x && y && h && qs && d), "residual_rmsnorm: NULL pointer");
+    launch_rmsnorm_q8(x, y, gain, rows, n, eps, h, normed, qs, d, s, S(stream));
+    return check_launch("si_residual_rmsnorm_q8");
+}
+
+int si_q4q8_block_dots(const uint8_t *wqs, const uint16_t *wd, int n, int k, const int8_t *xqs,
+                       const int16_t *xs, int32_t *dots, void *stream) {
+    (void)wd;
+    SI_REQUIRE(n > 0 && k > 0 && k % 32 == 0, "block_dots: bad size");
+    SI_REQUIRE(wqs && xqs && xs && dots, "block_dots: NULL pointer");
+    launch_block_dots(wqs, n, k, xqs, xs, dots, S(stream));
+    return check_launch("si_q4q8_block_dots");
+}
+
+size_t si_matvec_workspace(int n, int k, int splits) {
+    if (n <= 0 || k <= 0 || k % 32) return 0;
+    return gemv_workspace_bytes(n, k, splits);
+}
+
+int si_matvec_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k, const int8_t *xqs,
+                   const uint16_t *xd, const int16_t *xs, const float *bias,
+                   const float *residual, float *out, int splits, void *workspace,
+                   void *stream) {
+    SI_REQUIRE(n > 0 && k > 0 && k % 32 == 0, "matvec: bad size n=%d k=%d", n, k);
+    SI_REQUIRE(wqs && wd && xqs && xd && xs && out, "matvec: NULL pointer");
+    SI_REQUIRE(splits >= 1, "matvec: splits must be >= 1");
+    SI_REQUIRE(gemv_effective_splits(k, splits) == 1 || workspace,
+               "matvec: splits > 1 needs a workspace");
+    launch_gemv_q4q8(wqs, wd, n, k, xqs, xd, xs, bias, residual, out, splits, workspace,
+                     S(stream));
+    return check_launch("si_matvec_q4q8");
+}
+
+int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k, const int8_t *xqs,
+                 const uint16_t *xd, int m, const float *bias, const float *residual,
+                 float *out, int ldo, void *stream) {
+    SI_REQUIRE(n > 0 && k > 0 && k % 32 == 0 && m >= 0, "gemm: bad size m=%d n=%d k=%d", m, n,
+               k);
+    SI_REQUIRE(ldo >= n, "gemm: ldo %d < n %d", ldo, n);
+    SI_REQUIRE(m == 0 || (wqs && wd && xqs && xd && out), "gemm: NULL pointer");
+    launch_gemm_q4q8(wqs, wd, n, k, xqs, xd, m, bias, residual, out, ldo, S(stream));
+    return check_launch("si_gemm_q4q8");
+}
+
+int si_rope_table(int npos, int hdim, float base, float *c, float *s) {
+    SI_REQUIRE(npos > 0 && hdim > 0 && hdim % 2 == 0 && c && s, "rope_table: bad args");
+    const int half = hdim / 2;
+    for (int p = 0; p < npos; ++p)
+        for (int i = 0; i < half; ++i) {
+            // qwen_one_layer.c:176-177: float theta, libm powf/cosf/sinf
+            const float theta = (float)p / powf(base, (float)(2 * i) / (float)hdim);
+            c[(size_t)p * half + i] = cosf(theta);
+            s[(size_t)p * half + i] = sinf(theta);
+        }
+    return SI_OK;
+}
+
+int si_rope_kv_append(const si_shape_t *s, const float *qkv, int ldqkv, int ntok, int pos0,
+                      int pos_step, int max_pos, const int *ctx_dev, const float *rc,
+                      const float *rs, float *q_out, uint16_t *kc, uint16_t *vc,
+                      size_t kv_seq_stride, void *stream) {
+    int rc_ = check_shape(s);
+    if (rc_) return rc_;
+    SI_REQUIRE(ntok >= 0 && pos0 >= 0 && pos_step >= 0, "rope: bad ntok/pos0/pos_step");
+    SI_REQUIRE(max_pos >= 1, "rope: max_pos must be >= 1");
+    SI_REQUIRE(ctx_dev || ntok == 0 || (long)pos0 + (long)(ntok - 1) * pos_step < max_pos,
+               "rope: positions exceed max_pos");
+    SI_REQUIRE(ldqkv >= (s->qheads + 2 * s->kvheads) * s->hdim, "rope: ldqkv too small");
+    SI_REQUIRE(kv_seq_stride % 8 == 0, "rope: kv_seq_stride must be a multiple of 8");
+    SI_REQUIRE(ntok == 0 || (qkv && rc && rs && q_out && kc && vc), "rope: NULL pointer");
+    launch_rope_kv(qkv, ldqkv, ntok, s->qheads, s->kvheads, s->hdim, pos0, pos_step, max_pos,
+                   ctx_dev, rc, rs, q_out, kc, vc, kv_seq_stride, S(stream));
+    return check_launch("si_rope_kv_append");
+}
+
+size_t si_attention_workspace(const si_shape_t *s, int nq, int max_ctx) {
+    if (!s || nq <= 0 || max_ctx <= 0) return 0;
+    return attn_workspace_bytes(s->qheads, s->hdim, s->kvheads, nq, max_ctx);
+}
+
+int si_attention(const si_shape_t *s, const float *q, int nq, const uint16_t *kc,
+                 const uint16_t *vc, size_t kv_seq_stride, const int *ctx_dev, int ctx0,
+                 int ctx_step, int max_ctx, float *attn, int8_t *qs, uint16_t *d,
+                 int16_t *bsum, void *ws, size_t ws_bytes, void *stream) {
+    int r = check_shape(s);
+    if (r) return r;
+    SI_REQUIRE(nq >= 0 && max_ctx >= 1, "attention: bad nq/max_ctx");
+    SI_REQUIRE(kv_seq_stride % 8 == 0, "attention: kv_seq_stride must be a multiple of 8");
+    if (!ctx_dev) {
+        // attention_kernels.h:95 handles context <= 0 by zeroing; a layer call
+        // always has context >= 1 (qwen_one_layer.c:608), required here.
+        SI_REQUIRE(ctx0 >= 1 && ctx_step >= 0, "attention: contexts must be >= 1");
+        SI_REQUIRE((long)ctx0 + (long)(nq - 1) * ctx_step <= max_ctx,
+                   "attention: context exceeds max_ctx");
+    }
+    SI_REQUIRE(nq == 0 || (q && kc && vc && attn && ws), "attention: NULL pointer");
+    SI_REQUIRE(!qs || d, "attention: qs without d");
+    SI_REQUIRE(ws_bytes >= si_attention_workspace(s, nq, max_ctx), "attention: workspace too small");
+    launch_attention(q, nq, s->qheads, s->kvheads, s->hdim, kc, vc, kv_seq_stride, ctx_dev, ctx0,
+                     ctx_step, max_ctx, attn, qs, d, bsum, ws, S(stream));
+    return check_launch("si_attention");
+}
+
+int si_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs, uint16_t *d,
+                 int16_t *s, void *stream) {
+    SI_REQUIRE(rows >= 0 && f > 0 && f % 32 == 0, "swiglu: bad size");
+    SI_REQUIRE(rows == 0 || (gu && qs && d), "swiglu: NULL pointer");
+    launch_swiglu_q8(gu, rows, f, act, qs, d, s, S(stream));
+    return check_launch("si_swiglu_q8");
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Layer object
+// ---------------------------------------------------------------------------
+struct Q4Dev {
+    uint8_t *qs = nullptr;
+    uint16_t *d = nullptr;
+    int n = 0, k = 0;
+};
+
+struct Q8Buf {
+    int8_t *qs = nullptr;
+    uint16_t *d = nullptr;
+    int16_t *s = nullptr;
+};
+
+struct si_layer {
+    si_shape_t s;
+    int max_tokens = 0, max_pos = 0;
+    bool ffn = false;
+    Q4Dev wqkv, wo, wgu, wdown;
+    float *norm = nullptr, *bqkv = nullptr, *post_norm = nullptr;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    // workspaces, sized for max_tokens rows
+    float *normed = nullptr, *qkv = nullptr, *q = nullptr, *attn = nullptr;
+    float *attn_out = nullptr, *h = nullptr, *normed2 = nullptr, *gu = nullptr, *act = nullptr;
+    Q8Buf xq, attq, xq2, actq;
+    void *gemv_ws = nullptr;  // split-K partials + arrival counters (kept zeroed)
+    size_t gemv_ws_bytes = 0;
+    void *attn_ws = nullptr;
+    size_t attn_ws_bytes = 0;
+    std::vector<void *> allocs;
+    // phase timing: events[i] marks the start of phase i, events[COUNT] the end
+    bool timing = false;
+    hipEvent_t events[SI_PHASE_COUNT + 1] = {};
+    bool phase_hit[SI_PHASE_COUNT] = {};
+    int last_phase = -1;
+};
+
+static void mark(si_layer *L, int phase, hipStream_t st) {
+    if (!L->timing) return;
+    (void)hipEventRecord(L->events[phase], st);
+    if (phase < SI_PHASE_COUNT) L->phase_hit[phase] = true;
+    L->last_phase = phase;
+}
+
+template <typename T>
+static int dev_alloc(si_layer *L, T **p, size_t count) {
+    *p = nullptr;
+    if (count == 0) return SI_OK;
+    void *q = nullptr;
+    if (hipMalloc(&q, count * sizeof(T)) != hipSuccess)
+        return fail(SI_ERR_NOMEM, "hipMalloc(%zu bytes) failed", count * sizeof(T));
+    L->allocs.push_back(q);
+    *p = (T *)q;
+    return SI_OK;
+}
+
+#define TRY(x)               \
+    do {                     \
+        int r_ = (x);        \
+        if (r_) return r_;   \
+    } while (0)
+
+// Uploads row-major Q4_0 matrices stacked along N and repacks them.
+static int upload_q4(si_layer *L, Q4Dev *w, const std::vector<const uint8_t *> &parts,
+                     const std::vector<int> &rows, int k) {
+    int n = 0;
+    for (int r : rows) n += r;
+    const size_t row_bytes = (size_t)(k / 32) * 18;
+    w->n = n;
+    w->k = k;
+    TRY(dev_alloc(L, &w->qs, (size_t)n * k / 2));
+    TRY(dev_alloc(L, &w->d, (size_t)n * (k / 32)));
+    uint8_t *tmp = nullptr;
+    HIP_TRY(hipMalloc(&tmp, (size_t)n * row_bytes));
+    size_t off = 0;
+    for (size_t i = 0; i < parts.size(); ++i) {
+        hipError_t e = hipMemcpy(tmp + off, parts[i], rows[i] * row_bytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            (void)hipFree(tmp);
+            return fail(SI_ERR_HIP, "weight upload: %s", hipGetErrorString(e));
+        }
+        off += rows[i] * row_bytes;
+    }
+    launch_q4_repack(tmp, n, k, w->qs, w->d, 0);
+    hipError_t e = hipDeviceSynchronize();
+    (void)hipFree(tmp);
+    if (e != hipSuccess) return fail(SI_ERR_HIP, "repack: %s", hipGetErrorString(e));
+    return SI_OK;
+}
+
+static int upload_f32(si_layer *L, float **dst, const float *src, size_t n) {
+    *dst = nullptr;
+    if (!src) return SI_OK;
+    TRY(dev_alloc(L, dst, n));
+    HIP_TRY(hipMemcpy(*dst, src, n * sizeof(float), hipMemcpyHostToDevice));
+    return SI_OK;
+}
+
+static void free_layer(si_layer *L) {
+    for (void *p : L->allocs) (void)hipFree(p);
+    L->allocs.clear();
+    for (hipEvent_t &e : L->events)
+        if (e) {
+            (void)hipEventDestroy(e);
+            e = nullptr;
+        }
+}
+
+// K-range splits for a decode mat-vec: enough wavefronts to cover the chip
+// (>= ~512 row-tile x range pairs) while keeping >= 4 blocks per range.
+static int decode_splits(const si_layer *L, int n, int k, int flags) {
+    if (flags & SI_LAYER_EXACT) return 1;
+    const int tiles = (n + 63) / 64;
+    const int nb = k / 32;
+    int sp = (512 + tiles - 1) / tiles;
+    if (sp > nb / 4) sp = nb / 4;
+    if (sp < 1) sp = 1;
+    (void)L;
+    return gemv_effective_splits(k, sp);
+}
+
+extern "C" {
+
+int si_layer_create(const si_shape_t *s, const si_layer_host_t *w, int max_tokens, int max_pos,
+                    si_layer_t **out) {
+    TRY(check_shape(s));
+    SI_REQUIRE(w && out, "layer_create: NULL pointer");
+    SI_REQUIRE(w->wq && w->wk && w->wv && w->wo, "layer_create: wq/wk/wv/wo are required");
+    SI_REQUIRE(max_tokens >= 1 && max_pos >= 1, "layer_create: bad max_tokens/max_pos");
+    const bool ffn = w->wgate || w->wup || w->wdown;
+    SI_REQUIRE(!ffn || (w->wgate && w->wup && w->wdown && s->ffn > 0),
+               "layer_create: FFN needs wgate, wup, wdown and shape.ffn > 0");
+    si_layer *L = new si_layer();
+    L->s = *s;
+    L->max_tokens = max_tokens;
+    L->max_pos = max_pos;
+    L->ffn = ffn;
+    const int H = s->hidden, QD = s->qheads * s->hdim, KVD = s->kvheads * s->hdim, F = s->ffn;
+    const int NQKV = QD + 2 * KVD;
+    const int M = max_tokens;
+    int r = SI_OK;
+    do {
+        if ((r = upload_q4(L, &L->wqkv, {w->wq, w->wk, w->wv}, {QD, KVD, KVD}, H))) break;
+        if ((r = upload_q4(L, &L->wo, {w->wo}, {H}, QD))) break;
+        if (ffn) {
+            if ((r = upload_q4(L, &L->wgu, {w->wgate, w->wup}, {F, F}, H))) break;
+            if ((r = upload_q4(L, &L->wdown, {w->wdown}, {H}, F))) break;
+        }
+        if ((r = upload_f32(L, &L->norm, w->norm, H))) break;
+        if ((r = upload_f32(L, &L->post_norm, w->post_norm, H))) break;
+        if (w->bq || w->bk || w->bv) {
+            std::vector<float> b(NQKV, 0.0f);  // absent bias = zero (qwen_one_layer.c:154)
+            if (w->bq) memcpy(b.data(), w->bq, QD * sizeof(float));
+            if (w->bk) memcpy(b.data() + QD, w->bk, KVD * sizeof(float));
+            if (w->bv) memcpy(b.data() + QD + KVD, w->bv, KVD * sizeof(float));
+            if ((r = upload_f32(L, &L->bqkv, b.data(), NQKV))) break;
+        }
+        {
+            const size_t te = (size_t)max_pos * (s->hdim / 2);
+            std::vector<float> c(te), sn(te);
+            si_rope_table(max_pos, s->hdim, s->rope_base, c.data(), sn.data());
+            if ((r = upload_f32(L, &L->rope_cos, c.data(), te))) break;
+            if ((r = upload_f32(L, &L->rope_sin, sn.data(), te))) break;
+        }
+        const size_t MH = (size_t)M * H;
+        if ((r = dev_alloc(L, &L->normed, MH))) break;
+        if ((r = dev_alloc(L, &L->qkv, (size_t)M * NQKV))) break;
+        if ((r = dev_alloc(L, &L->q, (size_t)M * QD))) break;
+        if ((r = dev_alloc(L, &L->attn, (size_t)M * QD))) break;
+        if ((r = dev_alloc(L, &L->attn_out, MH))) break;
+        if ((r = dev_alloc(L, &L->xq.qs, MH))) break;
+        if ((r = dev_alloc(L, &L->xq.d, MH / 32))) break;
+        if ((r = dev_alloc(L, &L->xq.s, MH / 32))) break;
+        if ((r = dev_alloc(L, &L->attq.qs, (size_t)M * QD))) break;
+        if ((r = dev_alloc(L, &L->attq.d, (size_t)M * QD / 32))) break;
+        if ((r = dev_alloc(L, &L->attq.s, (size_t)M * QD / 32))) break;
+        if (ffn) {
+            if ((r = dev_alloc(L, &L->h, MH))) break;
+            if ((r = dev_alloc(L, &L->normed2, MH))) break;
+            if ((r = dev_alloc(L, &L->gu, (size_t)M * 2 * F))) break;
+            if ((r = dev_alloc(L, &L->act, (size_t)M * F))) break;
+            if ((r = dev_alloc(L, &L->xq2.qs, MH))) break;
+            if ((r = dev_alloc(L, &L->xq2.d, MH / 32))) break;
+            if ((r = dev_alloc(L, &L->xq2.s, MH / 32))) break;
+            if ((r = dev_alloc(L, &L->actq.qs, (size_t)M * F))) break;
+            if ((r = dev_alloc(L, &L->actq.d, (size_t)M * F / 32))) break;
+            if ((r = dev_alloc(L, &L->actq.s, (size_t)M * F / 32))) break;
+        }
+        // decode mat-vec workspace: the largest need over the four matrices
+        size_t gb = 0;
+        const Q4Dev *mats[4] = {&L->wqkv, &L->wo, &L->wgu, &L->wdown};
+        for (const Q4Dev *m : mats)
+            if (m->n) {
+                const size_t e = gemv_workspace_bytes(m->n, m->k, decode_splits(L, m->n, m->k, 0));
+                if (e > gb) gb = e;
+            }
+        L->gemv_ws_bytes = gb;
+        {
+            uint8_t *ws = nullptr;
+            if ((r = dev_alloc(L, &ws, gb))) break;
+            L->gemv_ws = ws;
+            if (gb && hipMemset(ws, 0, gb) != hipSuccess) {
+                r = fail(SI_ERR_HIP, "hipMemset(gemv workspace) failed");
+                break;
+            }
+        }
+        // the split count depends on the row count: size for the worst one
+        L->attn_ws_bytes = 0;
+        for (int nq = 1; nq <= M; ++nq) {
+            const size_t b = si_attention_workspace(s, nq, max_pos);
+            if (b > L->attn_ws_bytes) L->attn_ws_bytes = b;
+        }
+        {
+            uint8_t *ws = nullptr;
+            if ((r = dev_alloc(L, &ws, L->attn_ws_bytes))) break;
+            L->attn_ws = ws;
+        }
+    } while (0);
+    if (r) {
+        free_layer(L);
+        delete L;
+        return r;
+    }
+    *out = L;
+    return SI_OK;
+}
+
+int si_layer_destroy(si_layer_t *L) {
+    if (!L) return SI_OK;
+    (void)hipDeviceSynchronize();
+    free_layer(L);
+    delete L;
+    return SI_OK;
+}
+
+void *si_layer_buffer(si_layer_t *L, int which) {
+    if (!L) return nullptr;
+    switch (which) {
+        case SI_BUF_NORMED: return L->normed;
+        case SI_BUF_XQ_QS: return L->xq.qs;
+        case SI_BUF_XQ_D: return L->xq.d;
+        case SI_BUF_XQ_S: return L->xq.s;
+        case SI_BUF_QKV: return L->qkv;
+        case SI_BUF_Q: return L->q;
+        case SI_BUF_ATTN: return L->attn;
+        case SI_BUF_ATTQ_QS: return L->attq.qs;
+        case SI_BUF_ATTQ_D: return L->attq.d;
+        case SI_BUF_ATTQ_S: return L->attq.s;
+        case SI_BUF_ATTN_OUT: return L->attn_out;
+        case SI_BUF_H: return L->h;
+        case SI_BUF_NORMED2: return L->normed2;
+        case SI_BUF_XQ2_QS: return L->xq2.qs;
+        case SI_BUF_XQ2_D: return L->xq2.d;
+        case SI_BUF_XQ2_S: return L->xq2.s;
+        case SI_BUF_GU: return L->gu;
+        case SI_BUF_ACT: return L->act;
+        case SI_BUF_ACTQ_QS: return L->actq.qs;
+        case SI_BUF_ACTQ_D: return L->actq.d;
+        case SI_BUF_ACTQ_S: return L->actq.s;
+        default: return nullptr;
+    }
+}
+
+int si_layer_set_timing(si_layer_t *L, int enable) {
+    SI_REQUIRE(L, "layer_set_timing: NULL layer");
+    if (enable && !L->events[0])
+        for (hipEvent_t &e : L->events) HIP_TRY(hipEventCreate(&e));
+    L->timing = enable != 0;
+    return SI_OK;
+}
+
+int si_layer_phase_ms(si_layer_t *L, float *ms) {
+    SI_REQUIRE(L && ms, "layer_phase_ms: NULL pointer");
+    SI_REQUIRE(L->timing && L->last_phase == SI_PHASE_COUNT, "no timed layer call recorded");
+    HIP_TRY(hipEventSynchronize(L->events[SI_PHASE_COUNT]));
+    for (int p = 0; p < SI_PHASE_COUNT; ++p) {
+        ms[p] = 0.0f;
+        if (!L->phase_hit[p]) continue;
+        int q = p + 1;
+        while (q < SI_PHASE_COUNT && !L->phase_hit[q]) ++q;
+        HIP_TRY(hipEventElapsedTime(&ms[p], L->events[p], L->events[q]));
+    }
+    return SI_OK;
+}
+
+int si_layer_weights(si_layer_t *L, int which, const uint8_t **qs, const uint16_t **d, int *n,
+                     int *k) {
+    SI_REQUIRE(L && qs && d && n && k, "layer_weights: NULL pointer");
+    const Q4Dev *w = which == 0 ? &L->wqkv : which == 1 ? &L->wo : which == 2 ? &L->wgu
+                   : which == 3 ? &L->wdown : nullptr;
+    SI_REQUIRE(w && w->n, "layer_weights: no matrix %d", which);
+    *qs = w->qs;
+    *d = w->d;
+    *n = w->n;
+    *k = w->k;
+    return SI_OK;
+}
+
+}  // extern "C"
+
+// Projection of rows activation rows: GEMV for one row, matrix-core GEMM
+// otherwise.
+static void project(si_layer *L, const Q4Dev &w, int rows, const Q8Buf &x, const float *bias,
+                    const float *residual, float *out, int flags, hipStream_t st) {
+    if (rows == 1)
+        launch_gemv_q4q8(w.qs, w.d, w.n, w.k, x.qs, x.d, x.s, bias, residual, out,
+                         decode_splits(L, w.n, w.k, flags), L->gemv_ws, st);
+    else
+        launch_gemm_q4q8(w.qs, w.d, w.n, w.k, x.qs, x.d, rows, bias, residual, out, w.n, st);
+}
+
+// Shared schedule.  rows activation rows; positions and attention contexts
+// come either from (pos0, ctx0, ctx_step) or from ctx_dev.
+static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_t *vc,
+                    size_t kv_seq_stride, int pos0, const int *ctx_dev, int ctx0, int ctx_step,
+                    int max_ctx, float *out, int flags, hipStream_t st) {
+    const int pos_step = ctx_step;  // positions advance with the contexts
+    const si_shape_t &s = L->s;
+    const int H = s.hidden, QD = s.qheads * s.hdim, NQKV = QD + 2 * s.kvheads * s.hdim;
+    const bool full = !(flags & SI_LAYER_ATTN_ONLY);
+    SI_REQUIRE(!full || L->ffn, "layer has no FFN weights: use SI_LAYER_ATTN_ONLY");
+    for (bool &h : L->phase_hit) h = false;
+    // qwen_one_layer.c:247-250: RMSNorm -> Q8
+    mark(L, SI_PHASE_RMS_Q8, st);
+    launch_rmsnorm_q8(x, nullptr, L->norm, rows, H, s.rms_eps, nullptr, L->normed, L->xq.qs,
+                      L->xq.d, L->xq.s, st);
+    // :253-258: Q, K, V projections (+bias), fused into one N = qd + 2 kvd matrix
+    mark(L, SI_PHASE_QKV, st);
+    project(L, L->wqkv, rows, L->xq, L->bqkv, nullptr, L->qkv, flags, st);
+    mark(L, SI_PHASE_ROPE_KV, st);
+    // :260-266: RoPE at the token's position, fp16 K/V append
+    launch_rope_kv(L->qkv, NQKV, rows, s.qheads, s.kvheads, s.hdim, pos0, pos_step, max_ctx,
+                   ctx_dev, L->rope_cos, L->rope_sin, L->q, kc, vc, kv_seq_stride, st);
+    // :268-272: attention over the fp16 cache -> Q8
+    mark(L, SI_PHASE_ATTENTION_Q8, st);
+    launch_attention(L->q, rows, s.qheads, s.kvheads, s.hdim, kc, vc, kv_seq_stride, ctx_dev,
+                     ctx0, ctx_step, max_ctx, L->attn, L->attq.qs, L->attq.d, L->attq.s,
+                     L->attn_ws, st);
+    mark(L, SI_PHASE_OUT_PROJ, st);
+    if (!full) {
+        // :275: W_O, no bias, no residual
+        project(L, L->wo, rows, L->attq, nullptr, nullptr, out, flags, st);
+        mark(L, SI_PHASE_COUNT, st);
+        return check_launch("layer (attention sublayer)");
+    }
+    project(L, L->wo, rows, L->attq, nullptr, nullptr, L->attn_out, flags, st);
+    mark(L, SI_PHASE_POST_NORM_Q8, st);
+    // build-defined FFN half: h = x + o; RMSNorm -> Q8; gate|up; SwiGLU -> Q8; down + h
+    launch_rmsnorm_q8(x, L->attn_out, L->post_norm, rows, H, s.rms_eps, L->h, L->normed2,
+                      L->xq2.qs, L->xq2.d, L->xq2.s, st);
+    mark(L, SI_PHASE_GATE_UP, st);
+    project(L, L->wgu, rows, L->xq2, nullptr, nullptr, L->gu, flags, st);
+    mark(L, SI_PHASE_SWIGLU_Q8, st);
+    launch_swiglu_q8(L->gu, rows, s.ffn, L->act, L->actq.qs, L->actq.d, L->actq.s, st);
+    mark(L, SI_PHASE_DOWN, st);
+    project(L, L->wdown, rows, L->actq, nullptr, L->h, out, flags, st);
+    mark(L, SI_PHASE_COUNT, st);
+    return check_launch("layer");
+}
+
+extern "C" {
+
+int si_layer_decode(si_layer_t *L, const float *x, uint16_t *kc, uint16_t *vc, int context,
+                    float *out, int flags, void *stream) {
+    SI_REQUIRE(L && x && kc && vc && out, "layer_decode: NULL pointer");
+    // qwen_one_layer.c:608: context 1..32768 (here bounded by the RoPE table)
+    SI_REQUIRE(context >= 1 && context <= L->max_pos, "context %d outside 1..%d", context,
+               L->max_pos);
+    return run_rows(L, x, 1, kc, vc, 0, context - 1, nullptr, context, 0, context, out, flags,
+                    S(stream));
+}
+
+int si_layer_decode_batch(si_layer_t *L, const float *x, int nseq, uint16_t *kc, uint16_t *vc,
+                          size_t kv_seq_stride, const int *ctx_dev, int context, int max_ctx,
+                          float *out, int flags, void *stream) {
+    SI_REQUIRE(L && x && kc && vc && out, "layer_decode_batch: NULL pointer");
+    SI_REQUIRE(nseq >= 1 && nseq <= L->max_tokens, "nseq %d outside 1..%d", nseq, L->max_tokens);
+    SI_REQUIRE(max_ctx >= 1 && max_ctx <= L->max_pos, "max_ctx %d outside 1..%d", max_ctx,
+               L->max_pos);
+    SI_REQUIRE(ctx_dev || (context >= 1 && context <= max_ctx), "context %d outside 1..%d",
+               context, max_ctx);
+    SI_REQUIRE(kv_seq_stride % 8 == 0 &&
+                   kv_seq_stride >= (size_t)max_ctx * L->s.kvheads * L->s.hdim,
+               "kv_seq_stride must hold max_ctx rows and be a multiple of 8");
+    return run_rows(L, x, nseq, kc, vc, kv_seq_stride, context - 1, ctx_dev, context, 0, max_ctx,
+                    out, flags, S(stream));
+}
+
+int si_layer_prefill(si_layer_t *L, const float *x, int ntok, int prefix, uint16_t *kc,
+                     uint16_t *vc, float *out, int flags, void *stream) {
+    SI_REQUIRE(L && x && kc && vc && out, "layer_prefill: NULL pointer");
+    // prefill_weight_stationary.h:187: 1 <= ntok, 0 <= prefix, prefix+ntok within range
+    SI_REQUIRE(ntok >= 1 && ntok <= L->max_tokens, "ntok %d outside 1..%d", ntok, L->max_tokens);
+    SI_REQUIRE(prefix >= 0 && prefix + ntok <= L->max_pos, "prefix+ntok exceeds %d", L->max_pos);
+    return run_rows(L, x, ntok, kc, vc, 0, prefix, nullptr, prefix + 1, 1, prefix + ntok, out,
+                    flags, S(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,44 @@
+// si_kernels.hpp -- launcher prototypes shared by the HIP translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+namespace si {
+void launch_quantize_q8_aos(const float *src, void *dst, int count, hipStream_t st);
+void launch_quantize_q8_rows(const float *src, int rows, int k, int8_t *qs, uint16_t *d,
+                             int16_t *s, hipStream_t st);
+void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int rows, int n,
+                       float eps, float *h, float *normed, int8_t *qs, uint16_t *d, int16_t *s,
+                       hipStream_t st);
+void launch_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs, uint16_t *d,
+                      int16_t *s, hipStream_t st);
+void launch_q4_repack(const uint8_t *src, int n, int k, uint8_t *qs, uint16_t *d,
+                      hipStream_t st);
+void launch_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k, uint8_t *dst,
+                      hipStream_t st);
+void launch_gemv_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k, const int8_t *xqs,
+                      const uint16_t *xd, const int16_t *xs, const float *bias,
+                      const float *residual, float *out, int splits, void *workspace,
+                      hipStream_t st);
+int gemv_effective_splits(int k, int splits);
+size_t gemv_workspace_bytes(int n, int k, int splits);
+void launch_block_dots(const uint8_t *wqs, int n, int k, const int8_t *xqs, const int16_t *xs,
+                       int32_t *dots, hipStream_t st);
+void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k, const int8_t *xqs,
+                      const uint16_t *xd, int m, const float *bias, const float *residual,
+                      float *out, int ldo, hipStream_t st);
+}  // namespace si
+namespace si {
+void launch_rope_kv(const float *qkv, int ldqkv, int ntok, int qheads, int kvheads, int hdim,
+                    int pos0, int pos_step, int max_pos, const int *ctx_dev, const float *rc,
+                    const float *rs, float *q_out, uint16_t *kc, uint16_t *vc,
+                    size_t kv_seq_stride, hipStream_t st);
+int attn_nsplit(int kvheads, int nq, int max_ctx);
+size_t attn_workspace_bytes(int qheads, int hdim, int kvheads, int nq, int max_ctx);
+bool attn_supported(int qheads, int kvheads, int hdim);
+void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
+                      const uint16_t *kc, const uint16_t *vc, size_t kv_seq_stride,
+                      const int *ctx_dev, int ctx0, int ctx_step, int max_ctx, float *attn,
+                      int8_t *qs, uint16_t *d, int16_t *bsum, void *workspace,
+                      hipStream_t st);
+}  // namespace si

@@ -1,0 +1,234 @@
+// si_quant.hip -- elementwise/normalisation kernels of the hot path, each
+// ending in the bit-exact Q8_0 quantizer (qwen_one_layer.c:98-116):
+//   quantize_q8 (AoS drop-in and planar), RMSNorm->Q8, residual+RMSNorm->Q8,
+//   SwiGLU->Q8, and the lossless Q4_0 repack.
+// All are HBM-streaming: one pass over the fp32 input, one write of the
+// int8 payload (+2 B scale, +2 B block sum per 32 values).
+#include "si_device.hpp"
+#include "si_kernels.hpp"
+
+namespace si {
+
+// One Q8 block per half wavefront; blocks of 256 threads = 8 blocks.
+__global__ void __launch_bounds__(256) k_quantize_q8_aos(const float *__restrict__ src,
+                                                         uint8_t *__restrict__ dst, int nblocks) {
+    const int blk = blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int j = threadIdx.x & 31;
+    if (blk >= nblocks) return;  // whole half-waves exit together
+    const float x = src[(size_t)blk * SI_QK + j];
+    uint16_t dbits;
+    int bsum;
+    const int q = quant_block_lane(x, dbits, bsum);
+    uint8_t *rec = dst + (size_t)blk * 34;  // block_q8_0: {uint16 d; int8 qs[32]}
+    rec[2 + j] = (uint8_t)(int8_t)q;
+    if (j == 0) {
+        rec[0] = (uint8_t)(dbits & 0xff);
+        rec[1] = (uint8_t)(dbits >> 8);
+    }
+}
+
+__global__ void __launch_bounds__(256) k_quantize_q8_rows(const float *__restrict__ src, int k,
+                                                          int nblocks_row, int total_blocks,
+                                                          int8_t *__restrict__ qs,
+                                                          uint16_t *__restrict__ d,
+                                                          int16_t *__restrict__ s) {
+    const int blk = blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int j = threadIdx.x & 31;
+    if (blk >= total_blocks) return;
+    const int r = blk / nblocks_row, b = blk - r * nblocks_row;
+    const size_t off = (size_t)r * k + (size_t)b * SI_QK + j;
+    uint16_t dbits;
+    int bsum;
+    const int q = quant_block_lane(src[off], dbits, bsum);
+    qs[off] = (int8_t)q;
+    if (j == 0) {
+        d[blk] = dbits;
+        if (s) s[blk] = (int16_t)bsum;
+    }
+}
+
+// Quantizes n values held in LDS (row r) into the planar Q8 layout.
+__device__ __forceinline__ void quantize_lds_row(const float *row_lds, int n, int r,
+                                                 int8_t *__restrict__ qs,
+                                                 uint16_t *__restrict__ d,
+                                                 int16_t *__restrict__ s) {
+    const int nb = n / SI_QK;
+    const int hw = threadIdx.x >> 5, j = threadIdx.x & 31;
+    const int nhw = blockDim.x >> 5;
+    for (int b = hw; b < nb; b += nhw) {
+        uint16_t dbits;
+        int bsum;
+        const int q = quant_block_lane(row_lds[b * SI_QK + j], dbits, bsum);
+        qs[(size_t)r * n + b * SI_QK + j] = (int8_t)q;
+        if (j == 0) {
+            d[(size_t)r * nb + b] = dbits;
+            if (s) s[(size_t)r * nb + b] = (int16_t)bsum;
+        }
+    }
+}
+
+// Block-wide double sum (256 threads = 4 wavefronts).
+__device__ __forceinline__ double block_sum_d(double v, double *scratch) {
+    v = wave_sum_d(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) scratch[w] = v;
+    __syncthreads();
+    double t = 0.0;
+    const int nw = blockDim.x >> 6;
+    for (int i = 0; i < nw; ++i) t += scratch[i];
+    return t;
+}
+
+// RMSNorm (qwen_one_layer.c:164-169): squares summed in binary64,
+// inv = 1/sqrt(float(ss/n) + eps) correctly rounded, out = (x*inv)*gain.
+// The binary64 partial sums are combined as a tree, not in index order;
+// the float result equals the reference's except when the binary64 sum
+// lands within a few ulp of a binary32 rounding boundary.
+// Optionally first forms h = x + y (residual) and stores it.
+template <bool RESIDUAL>
+__global__ void __launch_bounds__(256) k_rmsnorm_q8(const float *__restrict__ x,
+                                                    const float *__restrict__ y,
+                                                    const float *__restrict__ gain, int n,
+                                                    float eps, float *__restrict__ h_out,
+                                                    float *__restrict__ normed,
+                                                    int8_t *__restrict__ qs,
+                                                    uint16_t *__restrict__ d,
+                                                    int16_t *__restrict__ s) {
+    extern __shared__ float lds[];  // n floats
+    __shared__ double red[8];
+    const int r = blockIdx.x;
+    const float *xr = x + (size_t)r * n;
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = xr[i];
+        if (RESIDUAL) {
+            v = __fadd_rn(v, y[(size_t)r * n + i]);
+            h_out[(size_t)r * n + i] = v;
+        }
+        lds[i] = v;
+        ss += (double)v * (double)v;
+    }
+    const double tot = block_sum_d(ss, red);
+    const float ms = (float)(tot / (double)n);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(ms, eps)));
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = __fmul_rn(lds[i], inv);
+        v = __fmul_rn(v, gain ? gain[i] : 1.0f);
+        lds[i] = v;
+        if (normed) normed[(size_t)r * n + i] = v;
+    }
+    __syncthreads();
+    quantize_lds_row(lds, n, r, qs, d, s);
+}
+
+// Build-defined SwiGLU then quantize_q8: a = (g / (1 + expf(-g))) * u.
+__global__ void __launch_bounds__(256) k_swiglu_q8(const float *__restrict__ gu, int f,
+                                                   int nb_row, int total_blocks,
+                                                   float *__restrict__ act,
+                                                   int8_t *__restrict__ qs,
+                                                   uint16_t *__restrict__ d,
+                                                   int16_t *__restrict__ s) {
+    const int blk = blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int j = threadIdx.x & 31;
+    if (blk >= total_blocks) return;
+    const int r = blk / nb_row, b = blk - r * nb_row;
+    const float *row = gu + (size_t)r * 2 * f;
+    const float g = row[b * SI_QK + j];
+    const float u = row[f + b * SI_QK + j];
+    const float silu = __fdiv_rn(g, __fadd_rn(1.0f, expf(-g)));
+    const float a = __fmul_rn(silu, u);
+    const size_t off = (size_t)r * f + (size_t)b * SI_QK + j;
+    if (act) act[off] = a;
+    uint16_t dbits;
+    int bsum;
+    const int q = quant_block_lane(a, dbits, bsum);
+    qs[off] = (int8_t)q;
+    if (j == 0) {
+        d[blk] = dbits;
+        if (s) s[blk] = (int16_t)bsum;
+    }
+}
+
+// Row-major 18-byte Q4_0 blocks -> [K/32][N][16] nibbles + [K/32][N] scales.
+__global__ void k_q4_repack(const uint8_t *__restrict__ src, int n, int nb,
+                            uint8_t *__restrict__ qs, uint16_t *__restrict__ d) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // i = b*n + row
+    if (i >= (size_t)n * nb) return;
+    const int b = (int)(i / n), row = (int)(i - (size_t)b * n);
+    const uint8_t *blk = src + ((size_t)row * nb + b) * 18;
+    d[i] = (uint16_t)(blk[0] | (blk[1] << 8));
+    uint32_t w[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+        w[t] = (uint32_t)blk[2 + 4 * t] | ((uint32_t)blk[3 + 4 * t] << 8) |
+               ((uint32_t)blk[4 + 4 * t] << 16) | ((uint32_t)blk[5 + 4 * t] << 24);
+    *(uint4 *)(qs + i * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__global__ void k_q4_unpack(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ d,
+                            int n, int nb, uint8_t *__restrict__ dst) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)n * nb) return;
+    const int b = (int)(i / n), row = (int)(i - (size_t)b * n);
+    uint8_t *blk = dst + ((size_t)row * nb + b) * 18;
+    blk[0] = (uint8_t)(d[i] & 0xff);
+    blk[1] = (uint8_t)(d[i] >> 8);
+    for (int t = 0; t < 16; ++t) blk[2 + t] = qs[i * 16 + t];
+}
+
+// ----------------------------------------------------------------------
+// launchers
+// ----------------------------------------------------------------------
+void launch_quantize_q8_aos(const float *src, void *dst, int count, hipStream_t st) {
+    const int nb = count / SI_QK;
+    if (nb == 0) return;
+    hipLaunchKernelGGL(k_quantize_q8_aos, dim3((nb + 7) / 8), dim3(256), 0, st, src,
+                       (uint8_t *)dst, nb);
+}
+
+void launch_quantize_q8_rows(const float *src, int rows, int k, int8_t *qs, uint16_t *d,
+                             int16_t *s, hipStream_t st) {
+    const int nbr = k / SI_QK, tot = nbr * rows;
+    if (tot == 0) return;
+    hipLaunchKernelGGL(k_quantize_q8_rows, dim3((tot + 7) / 8), dim3(256), 0, st, src, k, nbr,
+                       tot, qs, d, s);
+}
+
+void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int rows, int n,
+                       float eps, float *h, float *normed, int8_t *qs, uint16_t *d, int16_t *s,
+                       hipStream_t st) {
+    if (rows == 0) return;
+    const size_t lds = (size_t)n * sizeof(float);
+    if (y)
+        hipLaunchKernelGGL(k_rmsnorm_q8<true>, dim3(rows), dim3(256), lds, st, x, y, gain, n,
+                           eps, h, normed, qs, d, s);
+    else
+        hipLaunchKernelGGL(k_rmsnorm_q8<false>, dim3(rows), dim3(256), lds, st, x, y, gain, n,
+                           eps, h, normed, qs, d, s);
+}
+
+void launch_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs, uint16_t *d,
+                      int16_t *s, hipStream_t st) {
+    const int nbr = f / SI_QK, tot = nbr * rows;
+    if (tot == 0) return;
+    hipLaunchKernelGGL(k_swiglu_q8, dim3((tot + 7) / 8), dim3(256), 0, st, gu, f, nbr, tot, act,
+                       qs, d, s);
+}
+
+void launch_q4_repack(const uint8_t *src, int n, int k, uint8_t *qs, uint16_t *d,
+                      hipStream_t st) {
+    const size_t tot = (size_t)n * (k / SI_QK);
+    if (!tot) return;
+    hipLaunchKernelGGL(k_q4_repack, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, src,
+                       n, k / SI_QK, qs, d);
+}
+
+void launch_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k, uint8_t *dst,
+                      hipStream_t st) {
+    const size_t tot = (size_t)n * (k / SI_QK);
+    if (!tot) return;
+    hipLaunchKernelGGL(k_q4_unpack, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, qs,
+                       d, n, k / SI_QK, dst);
+}
+
+}  // namespace si

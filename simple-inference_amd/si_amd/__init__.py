@@ -1,0 +1,234 @@
+"""Python plumbing over the MI355X hot-path libraries (ctypes).
+
+The product is the C ABI in lib/libsi_amd.so (include/si_abi.h) and the C11
+host mirror in lib/libsi_host.so (include/si_host.h).  This module only binds
+them for tests and the benchmark; torch supplies device memory and streams.
+It fails loudly when the native libraries are missing: there is no fallback.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.dirname(HERE)
+LIB_DIR = os.path.join(PKG, "lib")
+AMD_SO = os.path.join(LIB_DIR, "libsi_amd.so")
+HOST_SO = os.path.join(LIB_DIR, "libsi_host.so")
+ROOT = os.path.dirname(PKG)
+INCLUDE_DIR = os.path.join(ROOT, "include")
+
+QK = 32
+Q8_DTYPE = np.dtype([("d", "<u2"), ("qs", "i1", (QK,))])  # defines.h:27-28
+
+SI_OK, SI_ERR_ARG, SI_ERR_HIP, SI_ERR_STATE, SI_ERR_NOMEM = range(5)
+SI_LAYER_FULL, SI_LAYER_ATTN_ONLY, SI_LAYER_EXACT = 0, 1, 2
+BUFFERS = ["NORMED", "XQ_QS", "XQ_D", "XQ_S", "QKV", "Q", "ATTN", "ATTQ_QS", "ATTQ_D",
+           "ATTQ_S", "ATTN_OUT", "H", "NORMED2", "XQ2_QS", "XQ2_D", "XQ2_S", "GU", "ACT",
+           "ACTQ_QS", "ACTQ_D", "ACTQ_S"]
+BUF = {n: i for i, n in enumerate(BUFFERS)}
+PHASES = ["rms_q8", "qkv_proj", "rope_kv", "attention_q8", "out_proj", "post_norm_q8",
+          "gate_up", "swiglu_q8", "down_proj"]
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+_Z = ctypes.c_size_t
+
+
+class SiError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"si error {code}: {msg}")
+        self.code = code
+
+
+class Shape(ctypes.Structure):
+    """si_shape_t (include/si_abi.h)."""
+    _fields_ = [("hidden", _I), ("qheads", _I), ("kvheads", _I), ("hdim", _I), ("ffn", _I),
+                ("rope_base", _F), ("rms_eps", _F)]
+
+
+def make_shape(hidden, qheads, kvheads, hdim, ffn=0, rope_base=1e6, rms_eps=1e-6):
+    return Shape(hidden, qheads, kvheads, hdim, ffn, rope_base, rms_eps)
+
+
+SHAPES = {
+    "0.5b": dict(hidden=896, qheads=14, kvheads=2, hdim=64, ffn=4864),
+    "7b": dict(hidden=3584, qheads=28, kvheads=4, hdim=128, ffn=18944),
+    "1.5b_ref": dict(hidden=1536, qheads=12, kvheads=2, hdim=128, ffn=0),
+}
+
+
+class LayerHost(ctypes.Structure):
+    """si_layer_host_t: host pointers to row-major Q4_0 / fp32 tensors."""
+    _fields_ = [(n, _P) for n in ("wq", "wk", "wv", "wo", "norm", "bq", "bk", "bv",
+                                  "post_norm", "wgate", "wup", "wdown")]
+
+
+_SIGS = {
+    "si_last_error": (ctypes.c_char_p, []),
+    "si_q4_repack": (_I, [_P, _I, _I, _P, _P, _P]),
+    "si_q4_unpack": (_I, [_P, _P, _I, _I, _P, _P]),
+    "si_quantize_q8": (_I, [_P, _P, _I, _P]),
+    "si_quantize_q8_rows": (_I, [_P, _I, _I, _P, _P, _P, _P]),
+    "si_rmsnorm_q8": (_I, [_P, _P, _I, _I, _F, _P, _P, _P, _P, _P]),
+    "si_residual_rmsnorm_q8": (_I, [_P, _P, _P, _I, _I, _F, _P, _P, _P, _P, _P, _P]),
+    "si_q4q8_block_dots": (_I, [_P, _P, _I, _I, _P, _P, _P, _P]),
+    "si_matvec_q4q8": (_I, [_P, _P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P]),
+    "si_matvec_workspace": (_Z, [_I, _I, _I]),
+    "si_gemm_q4q8": (_I, [_P, _P, _I, _I, _P, _P, _I, _P, _P, _P, _I, _P]),
+    "si_rope_kv_append": (_I, [ctypes.POINTER(Shape), _P, _I, _I, _I, _I, _I, _P, _P, _P, _P,
+                               _P, _P, _Z, _P]),
+    "si_rope_table": (_I, [_I, _I, _F, _P, _P]),
+    "si_attention": (_I, [ctypes.POINTER(Shape), _P, _I, _P, _P, _Z, _P, _I, _I, _I, _P, _P,
+                          _P, _P, _P, _Z, _P]),
+    "si_attention_workspace": (_Z, [ctypes.POINTER(Shape), _I, _I]),
+    "si_swiglu_q8": (_I, [_P, _I, _I, _P, _P, _P, _P, _P]),
+    "si_layer_create": (_I, [ctypes.POINTER(Shape), ctypes.POINTER(LayerHost), _I, _I,
+                             ctypes.POINTER(_P)]),
+    "si_layer_destroy": (_I, [_P]),
+    "si_layer_decode": (_I, [_P, _P, _P, _P, _I, _P, _I, _P]),
+    "si_layer_decode_batch": (_I, [_P, _P, _I, _P, _P, _Z, _P, _I, _I, _P, _I, _P]),
+    "si_layer_prefill": (_I, [_P, _P, _I, _I, _P, _P, _P, _I, _P]),
+    "si_layer_buffer": (_P, [_P, _I]),
+    "si_layer_set_timing": (_I, [_P, _I]),
+    "si_layer_phase_ms": (_I, [_P, _P]),
+    "si_layer_weights": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P),
+                              ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+}
+
+_lib = None
+_host = None
+
+
+def lib():
+    """The ABI library; raises if it was not built (no fallback exists)."""
+    global _lib
+    if _lib is None:
+        try:  # bind to the HIP runtime torch already carries (same SONAME)
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        if not os.path.exists(AMD_SO):
+            raise RuntimeError(f"{AMD_SO} missing: run __graft_entry__.build() "
+                               "(make -C simple-inference_amd)")
+        L = ctypes.CDLL(AMD_SO)
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def host_lib():
+    global _host
+    if _host is None:
+        if not os.path.exists(HOST_SO):
+            raise RuntimeError(f"{HOST_SO} missing: run __graft_entry__.build()")
+        H = ctypes.CDLL(HOST_SO)
+        H.si_quantize_q4_0_host.argtypes = [_P, _P, _I]
+        H.si_quantize_q4_0_host.restype = None
+        _host = H
+    return _host
+
+
+def call(name, *args):
+    rc = getattr(lib(), name)(*args)
+    if rc != SI_OK:
+        raise SiError(rc, lib().si_last_error().decode())
+    return rc
+
+
+def ptr(t):
+    """Device (torch) or host (numpy) buffer address; None stays NULL."""
+    if t is None:
+        return None
+    if hasattr(t, "data_ptr"):
+        return ctypes.c_void_p(t.data_ptr())
+    return t.ctypes.data_as(ctypes.c_void_p)
+
+
+def stream_handle(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def quantize_q4_0(w):
+    """Product-side ggml Q4_0 quantizer (host C): fp32 [rows][k] -> uint8 rows."""
+    w = np.ascontiguousarray(w, np.float32)
+    rows = w.shape[0] if w.ndim == 2 else 1
+    out = np.empty((rows, w.size // rows // QK * 18), np.uint8)
+    host_lib().si_quantize_q4_0_host(ptr(w), ptr(out), w.size)
+    return out
+
+
+def declared_functions():
+    """Function names declared in include/*.h (for the export check)."""
+    import re
+    names = []
+    for fn in sorted(os.listdir(INCLUDE_DIR)):
+        if not fn.endswith(".h"):
+            continue
+        text = open(os.path.join(INCLUDE_DIR, fn)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b(\w+)\s*\([^;{]*\)\s*;", text, flags=re.M):
+            if not m.group(0).lstrip().startswith("typedef"):
+                names.append((fn, m.group(1)))
+    return names
+
+
+class Layer:
+    """si_layer_t owner built from host tensors (dict of numpy arrays)."""
+
+    def __init__(self, shape, tensors, max_tokens, max_pos):
+        self.shape = shape
+        self._keep = {k: np.ascontiguousarray(v) for k, v in tensors.items() if v is not None}
+        host = LayerHost(**{k: v.ctypes.data for k, v in self._keep.items()})
+        h = _P()
+        call("si_layer_create", ctypes.byref(shape), ctypes.byref(host), max_tokens, max_pos,
+             ctypes.byref(h))
+        self.h = h
+        self.max_tokens, self.max_pos = max_tokens, max_pos
+
+    def close(self):
+        if self.h:
+            lib().si_layer_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def buffer(self, name):
+        return lib().si_layer_buffer(self.h, BUF[name])
+
+    def weights(self, which):
+        qs, d, n, k = _P(), _P(), _I(), _I()
+        call("si_layer_weights", self.h, which, ctypes.byref(qs), ctypes.byref(d),
+             ctypes.byref(n), ctypes.byref(k))
+        return qs.value, d.value, n.value, k.value
+
+    def decode(self, x, kc, vc, context, out, flags=SI_LAYER_FULL, stream=None):
+        call("si_layer_decode", self.h, ptr(x), ptr(kc), ptr(vc), context, ptr(out), flags,
+             stream_handle(stream))
+
+    def decode_batch(self, x, nseq, kc, vc, kv_seq_stride, context, max_ctx, out,
+                     ctx_dev=None, flags=SI_LAYER_FULL, stream=None):
+        call("si_layer_decode_batch", self.h, ptr(x), nseq, ptr(kc), ptr(vc), kv_seq_stride,
+             ptr(ctx_dev), context, max_ctx, ptr(out), flags, stream_handle(stream))
+
+    def prefill(self, x, ntok, prefix, kc, vc, out, flags=SI_LAYER_FULL, stream=None):
+        call("si_layer_prefill", self.h, ptr(x), ntok, prefix, ptr(kc), ptr(vc), ptr(out),
+             flags, stream_handle(stream))
+
+    def set_timing(self, on=True):
+        call("si_layer_set_timing", self.h, int(on))
+
+    def phase_ms(self):
+        ms = np.zeros(len(PHASES), np.float32)
+        call("si_layer_phase_ms", self.h, ptr(ms))
+        return dict(zip(PHASES, ms.tolist()))

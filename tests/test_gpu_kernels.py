@@ -1,0 +1,398 @@
+"""GPU parity of each hot-path kernel against the oracle, through the C ABI.
+
+Bar: bit-exact for Q8_0 quantization (on identical fp32 input), Q4_0 repack
+and per-block int32 dots, and for the single-range mat-vec (the reference's
+own summation order); fp32 within 1e-3 (attention 2e-3) otherwise."""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+import si_amd
+from oracle.oracle_py import Q8_DTYPE, make_shape as or_shape
+from tests.gpu_helpers import (aos_to_planar, close, dev, empty, host, kv_history,
+                               planar_to_aos, q4)
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ref_golden.npz")
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _q8_inputs(case, n=32 * 96):
+    rng = np.random.default_rng(11)
+    if case == "normal":
+        return rng.standard_normal(n).astype(np.float32)
+    if case == "tiny":
+        return (rng.standard_normal(n) * 10.0 ** rng.integers(-44, -3, n)).astype(np.float32)
+    if case == "ties":
+        x = (rng.integers(-254, 255, n) / 2.0).astype(np.float32)
+        x[::32] = 127.0
+        return x
+    if case == "zeros":
+        x = np.zeros(n, np.float32)
+        x[64:96] = rng.standard_normal(32)
+        return x
+    if case == "huge":
+        x = (rng.standard_normal(n) * 1e6).astype(np.float32)
+        x[:32] *= np.float32(1e30)
+        return x
+    if case == "nonfinite":
+        x = rng.standard_normal(n).astype(np.float32)
+        x[5], x[40], x[100] = np.nan, np.inf, -np.inf
+        x[128:160] = np.nan
+        return x
+    return (rng.standard_normal(n) * np.repeat(10.0 ** rng.uniform(-6, 6, n // 32), 32)
+            ).astype(np.float32)
+
+
+@pytest.mark.parametrize("case", ["normal", "tiny", "ties", "zeros", "huge", "mixed",
+                                  "nonfinite"])
+def test_quantize_q8_aos_bit_exact(oracle, case):
+    x = _q8_inputs(case)
+    want = oracle.quantize_q8(x)
+    out = empty(x.size // 32 * 34, _torch().uint8)
+    si_amd.call("si_quantize_q8", si_amd.ptr(dev(x)), si_amd.ptr(out), x.size, None)
+    got = host(out).view(Q8_DTYPE)
+    assert got.tobytes() == want.tobytes()
+
+
+def test_quantize_q8_golden_fixture():
+    g = np.load(GOLDEN, allow_pickle=False)
+    torch = _torch()
+    for x, want in zip(g["q8_in"], g["q8_out"]):
+        out = empty(x.size // 32 * 34, torch.uint8)
+        si_amd.call("si_quantize_q8", si_amd.ptr(dev(x)), si_amd.ptr(out), x.size, None)
+        assert host(out).tobytes() == want.tobytes()
+
+
+def test_quantize_q8_rows_planar(oracle):
+    torch = _torch()
+    rows, k = 7, 4864
+    x = (np.random.default_rng(3).standard_normal((rows, k)) * 3).astype(np.float32)
+    qs, d, s = empty(rows * k, torch.int8), empty(rows * k // 32, torch.int16), \
+        empty(rows * k // 32, torch.int16)
+    si_amd.call("si_quantize_q8_rows", si_amd.ptr(dev(x)), rows, k, si_amd.ptr(qs),
+                si_amd.ptr(d), si_amd.ptr(s), None)
+    want = oracle.quantize_q8(x)
+    wq, wd, ws = aos_to_planar(want)
+    assert np.array_equal(host(qs), wq)
+    assert np.array_equal(host(d).view(np.uint16), wd)
+    assert np.array_equal(host(s), ws)
+
+
+@pytest.mark.parametrize("n,gain", [(896, True), (1536, False), (3584, True)])
+def test_rmsnorm_q8(oracle, n, gain):
+    torch = _torch()
+    rows = 5
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal((rows, n)) * rng.uniform(0.01, 50, (rows, 1))).astype(np.float32)
+    w = rng.normal(1, 0.1, n).astype(np.float32) if gain else None
+    normed = empty(rows * n, torch.float32)
+    qs, d, s = empty(rows * n, torch.int8), empty(rows * n // 32, torch.int16), \
+        empty(rows * n // 32, torch.int16)
+    si_amd.call("si_rmsnorm_q8", si_amd.ptr(dev(x)), si_amd.ptr(None if w is None else dev(w)),
+                rows, n, 1e-6, si_amd.ptr(normed), si_amd.ptr(qs), si_amd.ptr(d),
+                si_amd.ptr(s), None)
+    got = host(normed).reshape(rows, n)
+    for r in range(rows):
+        want = oracle.rmsnorm(x[r], w)
+        # the binary64 sum is a tree sum: equal unless a float boundary is hit
+        close(got[r], want, 1e-6, "rmsnorm")
+    # the quantizer is bit-exact on the device's own normed values
+    wq, wd, ws = aos_to_planar(oracle.quantize_q8(got))
+    assert np.array_equal(host(qs), wq) and np.array_equal(host(d).view(np.uint16), wd)
+    assert np.array_equal(host(s), ws)
+
+
+def test_rmsnorm_bit_exact_on_golden():
+    g = np.load(GOLDEN, allow_pickle=False)
+    torch = _torch()
+    n = g["rms_in"].size
+    normed = empty(n, torch.float32)
+    qs, d = empty(n, torch.int8), empty(n // 32, torch.int16)
+    si_amd.call("si_rmsnorm_q8", si_amd.ptr(dev(g["rms_in"])), si_amd.ptr(dev(g["rms_w"])), 1,
+                n, 1e-6, si_amd.ptr(normed), si_amd.ptr(qs), si_amd.ptr(d), None, None)
+    assert np.array_equal(host(normed).view(np.uint32), g["rms_out"].view(np.uint32))
+
+
+def test_residual_rmsnorm_q8(oracle):
+    torch = _torch()
+    rows, n = 3, 896
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    y = rng.standard_normal((rows, n)).astype(np.float32)
+    w = rng.normal(1, 0.1, n).astype(np.float32)
+    h, normed = empty(rows * n, torch.float32), empty(rows * n, torch.float32)
+    qs, d = empty(rows * n, torch.int8), empty(rows * n // 32, torch.int16)
+    si_amd.call("si_residual_rmsnorm_q8", si_amd.ptr(dev(x)), si_amd.ptr(dev(y)),
+                si_amd.ptr(dev(w)), rows, n, 1e-6, si_amd.ptr(h), si_amd.ptr(normed),
+                si_amd.ptr(qs), si_amd.ptr(d), None, None)
+    assert np.array_equal(host(h).reshape(rows, n), x + y)
+    got = host(normed).reshape(rows, n)
+    for r in range(rows):
+        close(got[r], oracle.rmsnorm(x[r] + y[r], w), 1e-6, "post-norm")
+
+
+def test_swiglu_q8(oracle):
+    torch = _torch()
+    rows, f = 4, 4864
+    rng = np.random.default_rng(1)
+    gu = (rng.standard_normal((rows, 2 * f)) * 3).astype(np.float32)
+    act = empty(rows * f, torch.float32)
+    qs, d, s = empty(rows * f, torch.int8), empty(rows * f // 32, torch.int16), \
+        empty(rows * f // 32, torch.int16)
+    si_amd.call("si_swiglu_q8", si_amd.ptr(dev(gu)), rows, f, si_amd.ptr(act), si_amd.ptr(qs),
+                si_amd.ptr(d), si_amd.ptr(s), None)
+    got = host(act).reshape(rows, f)
+    for r in range(rows):
+        close(got[r], oracle.swiglu(gu[r, :f], gu[r, f:]), 1e-5, "swiglu")
+    wq, wd, ws = aos_to_planar(oracle.quantize_q8(got))
+    assert np.array_equal(host(qs), wq) and np.array_equal(host(d).view(np.uint16), wd)
+
+
+def _upload_q4(w_rowmajor, n, k):
+    torch = _torch()
+    qs, d = empty(n * k // 2, torch.uint8), empty(n * k // 32, torch.int16)
+    si_amd.call("si_q4_repack", si_amd.ptr(dev(w_rowmajor)), n, k, si_amd.ptr(qs),
+                si_amd.ptr(d), None)
+    return qs, d
+
+
+def test_q4_repack_round_trip(oracle):
+    torch = _torch()
+    rng = np.random.default_rng(2)
+    n, k = 300, 1024
+    w = q4(oracle, rng, n, k)
+    qs, d = _upload_q4(w, n, k)
+    back = empty(w.size, torch.uint8)
+    si_amd.call("si_q4_unpack", si_amd.ptr(qs), si_amd.ptr(d), n, k, si_amd.ptr(back), None)
+    assert np.array_equal(host(back), w.reshape(-1))
+    # the repacked layout: block-major nibbles and scales
+    hq = host(qs).reshape(k // 32, n, 16)
+    blocks = w.reshape(n, k // 32, 18)
+    assert np.array_equal(hq, blocks[:, :, 2:].transpose(1, 0, 2))
+    assert np.array_equal(host(d).view(np.uint16).reshape(k // 32, n),
+                          blocks[:, :, :2].copy().view(np.uint16)[..., 0].T)
+
+
+def _q8_dev(oracle, x):
+    xq = oracle.quantize_q8(x)
+    qs, d, s = aos_to_planar(xq)
+    return xq, dev(qs), dev(d.view(np.int16)), dev(s)
+
+
+@pytest.mark.parametrize("n,k", [(1152, 896), (64, 32), (200, 4864)])
+def test_block_dots_bit_exact(oracle, n, k):
+    torch = _torch()
+    rng = np.random.default_rng(n + k)
+    w = rng.integers(0, 256, (n, k // 32 * 18), dtype=np.uint8)
+    w.reshape(n, k // 32, 18)[:, :, 1] &= 0x3b  # keep scales finite
+    x = (rng.standard_normal(k) * 2).astype(np.float32)
+    x[:32] = 1000.0  # q = +127 block
+    xq, xqs, xd, xs = _q8_dev(oracle, x)
+    wqs, wd = _upload_q4(w, n, k)
+    dots = empty(n * (k // 32), torch.int32)
+    si_amd.call("si_q4q8_block_dots", si_amd.ptr(wqs), si_amd.ptr(wd), n, k, si_amd.ptr(xqs),
+                si_amd.ptr(xs), si_amd.ptr(dots), None)
+    assert np.array_equal(host(dots).reshape(n, k // 32), oracle.block_dots(w, xq, k, n))
+
+
+@pytest.mark.parametrize("n,k,bias", [(1152, 896, True), (896, 896, False), (9728, 896, False),
+                                      (896, 4864, False), (4608, 3584, True),
+                                      (3584, 18944, False), (77, 96, True)])
+def test_matvec_exact_single_range(oracle, n, k, bias):
+    """One K range per row: the reference's block order and roundings."""
+    torch = _torch()
+    rng = np.random.default_rng(n * 7 + k)
+    w = q4(oracle, rng, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    b = rng.normal(0, 0.02, n).astype(np.float32) if bias else None
+    xq, xqs, xd, xs = _q8_dev(oracle, x)
+    wqs, wd = _upload_q4(w, n, k)
+    out = empty(n, torch.float32)
+    si_amd.call("si_matvec_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), n, k, si_amd.ptr(xqs),
+                si_amd.ptr(xd), si_amd.ptr(xs), si_amd.ptr(None if b is None else dev(b)), None,
+                si_amd.ptr(out), 1, None, None)
+    want = oracle.matvec(w, xq, k, n, b)
+    assert np.array_equal(host(out).view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("n,k,splits", [(1152, 896, 7), (896, 4864, 19), (3584, 18944, 37)])
+def test_matvec_split_ranges(oracle, n, k, splits):
+    torch = _torch()
+    rng = np.random.default_rng(n + splits)
+    w = q4(oracle, rng, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    b = rng.normal(0, 0.02, n).astype(np.float32)
+    res = rng.standard_normal(n).astype(np.float32)
+    xq, xqs, xd, xs = _q8_dev(oracle, x)
+    wqs, wd = _upload_q4(w, n, k)
+    out = empty(n, torch.float32)
+    part = empty(splits * n, torch.float32)
+    si_amd.call("si_matvec_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), n, k, si_amd.ptr(xqs),
+                si_amd.ptr(xd), si_amd.ptr(xs), si_amd.ptr(dev(b)), si_amd.ptr(dev(res)),
+                si_amd.ptr(out), splits, si_amd.ptr(part), None)
+    want = res + oracle.matvec(w, xq, k, n, b)
+    close(host(out), want, 1e-5, "split matvec")
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 64), (5, 200, 96), (64, 1152, 896),
+                                   (130, 896, 4864), (512, 384, 896)])
+def test_gemm_matches_oracle_rows(oracle, m, n, k):
+    torch = _torch()
+    rng = np.random.default_rng(m * 31 + n)
+    w = q4(oracle, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.normal(0, 0.02, n).astype(np.float32)
+    xq = oracle.quantize_q8(x)
+    qs, d, _ = aos_to_planar(xq)
+    wqs, wd = _upload_q4(w, n, k)
+    out = empty(m * n, torch.float32)
+    si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), n, k, si_amd.ptr(dev(qs)),
+                si_amd.ptr(dev(d.view(np.int16))), m, si_amd.ptr(dev(b)), None,
+                si_amd.ptr(out), n, None)
+    got = host(out).reshape(m, n)
+    nb = k // 32
+    for r in sorted({0, m // 2, m - 1}):
+        want = oracle.matvec(w, xq[r * nb:(r + 1) * nb], k, n, b)
+        close(got[r], want, 1e-5, f"gemm row {r}")
+
+
+def test_gemm_residual(oracle):
+    torch = _torch()
+    m, n, k = 70, 256, 512
+    rng = np.random.default_rng(5)
+    w = q4(oracle, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    xq = oracle.quantize_q8(x)
+    qs, d, _ = aos_to_planar(xq)
+    wqs, wd = _upload_q4(w, n, k)
+    out = empty(m * n, torch.float32)
+    si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), n, k, si_amd.ptr(dev(qs)),
+                si_amd.ptr(dev(d.view(np.int16))), m, None, si_amd.ptr(dev(res)),
+                si_amd.ptr(out), n, None)
+    got = host(out).reshape(m, n)
+    nb = k // 32
+    for r in (0, 69):
+        close(got[r], res[r] + oracle.matvec(w, xq[r * nb:(r + 1) * nb], k, n), 1e-5, "res")
+
+
+@pytest.mark.parametrize("shape,ntok,pos0", [("0.5b", 1, 1023), ("7b", 5, 0), ("7b", 3, 4093)])
+def test_rope_kv_append_bit_exact(oracle, shape, ntok, pos0):
+    torch = _torch()
+    sd = si_amd.SHAPES[shape]
+    s = si_amd.make_shape(**sd)
+    D, QD, KVD = s.hdim, s.qheads * s.hdim, s.kvheads * s.hdim
+    NQ = QD + 2 * KVD
+    rng = np.random.default_rng(ntok)
+    qkv = rng.standard_normal((ntok, NQ)).astype(np.float32)
+    maxpos = pos0 + ntok
+    c = np.empty((maxpos, D // 2), np.float32)
+    sn = np.empty_like(c)
+    si_amd.call("si_rope_table", maxpos, D, 1e6, si_amd.ptr(c), si_amd.ptr(sn))
+    kc = dev(np.zeros(maxpos * KVD, np.uint16).view(np.int16))
+    vc = dev(np.zeros(maxpos * KVD, np.uint16).view(np.int16))
+    qo = empty(ntok * QD, torch.float32)
+    si_amd.call("si_rope_kv_append", ctypes.byref(s), si_amd.ptr(dev(qkv)), NQ, ntok, pos0, 1,
+                maxpos, None, si_amd.ptr(dev(c)), si_amd.ptr(dev(sn)), si_amd.ptr(qo), si_amd.ptr(kc),
+                si_amd.ptr(vc), 0, None)
+    gq = host(qo).reshape(ntok, QD)
+    gk = host(kc).view(np.uint16).reshape(maxpos, KVD)
+    gv = host(vc).view(np.uint16).reshape(maxpos, KVD)
+    for t in range(ntok):
+        wq = oracle.rope(qkv[t, :QD], s.qheads, D, pos0 + t)
+        wk = oracle.rope(qkv[t, QD:QD + KVD], s.kvheads, D, pos0 + t)
+        assert np.array_equal(gq[t].view(np.uint32), wq.view(np.uint32))
+        assert np.array_equal(gk[pos0 + t], oracle.f32_to_f16(wk))
+        assert np.array_equal(gv[pos0 + t], oracle.f32_to_f16(qkv[t, QD + KVD:]))
+
+
+def _attention_case(oracle, shape_name, ctx, kmul=1.0, seed=0):
+    sd = si_amd.SHAPES[shape_name]
+    s = si_amd.make_shape(**sd)
+    os_ = or_shape(**sd)
+    rng = np.random.default_rng(seed + ctx)
+    KVD = s.kvheads * s.hdim
+    q = rng.standard_normal(s.qheads * s.hdim).astype(np.float32)
+    kc = kv_history(oracle, rng, ctx, KVD, kmul)
+    vc = kv_history(oracle, rng, ctx, KVD)
+    return s, os_, q, kc, vc
+
+
+@pytest.mark.parametrize("shape,ctx,kmul", [("0.5b", 1, 1.0), ("0.5b", 2, 0.0125),
+                                            ("0.5b", 17, 1.0), ("0.5b", 64, 0.0),
+                                            ("0.5b", 1024, 1.0), ("7b", 4096, 1.0),
+                                            ("7b", 300, 3.0), ("1.5b_ref", 1000, 0.5),
+                                            ("7b", 4097, 1.0)])
+def test_attention_decode(oracle, shape, ctx, kmul):
+    torch = _torch()
+    s, os_, q, kc, vc = _attention_case(oracle, shape, ctx, kmul)
+    QD = s.qheads * s.hdim
+    ws_bytes = si_amd.lib().si_attention_workspace(ctypes.byref(s), 1, ctx)
+    ws = empty(ws_bytes, torch.uint8)
+    out = empty(QD, torch.float32)
+    qs, d = empty(QD, torch.int8), empty(QD // 32, torch.int16)
+    si_amd.call("si_attention", ctypes.byref(s), si_amd.ptr(dev(q)), 1,
+                si_amd.ptr(dev(kc.view(np.int16))), si_amd.ptr(dev(vc.view(np.int16))), 0, None,
+                ctx, 0, ctx, si_amd.ptr(out), si_amd.ptr(qs), si_amd.ptr(d), None,
+                si_amd.ptr(ws), ws_bytes, None)
+    got = host(out)
+    close(got, oracle.attention_flash(os_, q, kc, vc, ctx), 2e-3, "attention")
+    wq, wd, _ = aos_to_planar(oracle.quantize_q8(got))
+    assert np.array_equal(host(qs), wq) and np.array_equal(host(d).view(np.uint16), wd)
+
+
+def test_attention_batched_sequences(oracle):
+    """nq sequences, each with its own cache (kv_seq_stride) and context."""
+    torch = _torch()
+    sd = si_amd.SHAPES["7b"]
+    s, os_ = si_amd.make_shape(**sd), or_shape(**sd)
+    nseq, maxctx = 6, 700
+    KVD, QD = s.kvheads * s.hdim, s.qheads * s.hdim
+    rng = np.random.default_rng(42)
+    ctxs = np.array([1, 2, 37, 256, 257, 700], np.int32)
+    q = rng.standard_normal((nseq, QD)).astype(np.float32)
+    kc = kv_history(oracle, rng, nseq * maxctx, KVD).reshape(nseq, maxctx * KVD)
+    vc = kv_history(oracle, rng, nseq * maxctx, KVD).reshape(nseq, maxctx * KVD)
+    ws_bytes = si_amd.lib().si_attention_workspace(ctypes.byref(s), nseq, maxctx)
+    ws = empty(ws_bytes, torch.uint8)
+    out = empty(nseq * QD, torch.float32)
+    si_amd.call("si_attention", ctypes.byref(s), si_amd.ptr(dev(q)), nseq,
+                si_amd.ptr(dev(kc.view(np.int16))), si_amd.ptr(dev(vc.view(np.int16))),
+                maxctx * KVD, si_amd.ptr(dev(ctxs)), 0, 0, maxctx, si_amd.ptr(out), None, None,
+                None, si_amd.ptr(ws), ws_bytes, None)
+    got = host(out).reshape(nseq, QD)
+    for i in range(nseq):
+        want = oracle.attention_flash(os_, q[i], kc[i], vc[i], int(ctxs[i]))
+        close(got[i], want, 2e-3, f"seq {i}")
+
+
+def test_attention_causal_prefill(oracle):
+    """nq query rows over one cache: row t attends to prefix+t+1 positions."""
+    torch = _torch()
+    sd = si_amd.SHAPES["0.5b"]
+    s, os_ = si_amd.make_shape(**sd), or_shape(**sd)
+    ntok, prefix = 40, 300
+    KVD, QD = s.kvheads * s.hdim, s.qheads * s.hdim
+    rng = np.random.default_rng(7)
+    total = prefix + ntok
+    q = rng.standard_normal((ntok, QD)).astype(np.float32)
+    kc = kv_history(oracle, rng, total, KVD)
+    vc = kv_history(oracle, rng, total, KVD)
+    ws_bytes = si_amd.lib().si_attention_workspace(ctypes.byref(s), ntok, total)
+    ws = empty(ws_bytes, torch.uint8)
+    out = empty(ntok * QD, torch.float32)
+    si_amd.call("si_attention", ctypes.byref(s), si_amd.ptr(dev(q)), ntok,
+                si_amd.ptr(dev(kc.view(np.int16))), si_amd.ptr(dev(vc.view(np.int16))), 0, None,
+                prefix + 1, 1, total, si_amd.ptr(out), None, None, None, si_amd.ptr(ws),
+                ws_bytes, None)
+    got = host(out).reshape(ntok, QD)
+    for t in (0, 1, 17, ntok - 1):
+        want = oracle.attention_flash(os_, q[t], kc, vc, prefix + t + 1)
+        close(got[t], want, 2e-3, f"row {t}")

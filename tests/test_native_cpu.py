@@ -1,0 +1,66 @@
+"""CPU-side checks of the native libraries (no GPU needed): they load, export
+every function include/*.h declares, their host-side code (RoPE tables, the
+Q4_0 weight quantizer) matches the oracle bit for bit, and argument errors
+are reported without touching the device."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import si_amd
+
+
+def test_libraries_export_every_declared_symbol():
+    amd = ctypes.CDLL(si_amd.AMD_SO)
+    host = ctypes.CDLL(si_amd.HOST_SO)
+    decl = si_amd.declared_functions()
+    assert len(decl) > 30
+    missing = [(h, n) for h, n in decl
+               if not hasattr(amd if h == "si_abi.h" else host, n)]
+    assert not missing, missing
+
+
+@pytest.mark.parametrize("hdim,npos", [(64, 1100), (128, 4097)])
+def test_rope_table_matches_oracle(oracle, hdim, npos):
+    c = np.empty((npos, hdim // 2), np.float32)
+    s = np.empty_like(c)
+    si_amd.call("si_rope_table", npos, hdim, 1e6, si_amd.ptr(c), si_amd.ptr(s))
+    oc, os_ = oracle.rope_table(0, npos, hdim)
+    assert np.array_equal(c.view(np.uint32), oc.view(np.uint32))
+    assert np.array_equal(s.view(np.uint32), os_.view(np.uint32))
+
+
+def test_product_q4_0_quantizer_matches_oracle(oracle):
+    rng = np.random.default_rng(0)
+    w = rng.normal(0, 0.02, (64, 896)).astype(np.float32)
+    w[3, :32] = 0.0
+    w[5, 64:96] = 1e-9
+    assert np.array_equal(si_amd.quantize_q4_0(w), oracle.quantize_q4_0(w))
+
+
+def test_argument_errors_do_not_launch():
+    L = si_amd.lib()
+    assert L.si_quantize_q8(None, None, 33, None) == si_amd.SI_ERR_ARG
+    assert b"multiple of 32" in L.si_last_error()
+    assert L.si_gemm_q4q8(None, None, 64, 30, None, None, 4, None, None, None, 64,
+                          None) == si_amd.SI_ERR_ARG
+    assert L.si_matvec_q4q8(None, None, 64, 64, None, None, None, None, None, None, 1, None,
+                            None) == si_amd.SI_ERR_ARG
+    bad = si_amd.make_shape(896, 14, 3, 64)  # 14 % 3 != 0
+    assert L.si_rope_kv_append(ctypes.byref(bad), None, 0, 0, 0, 0, 1, None, None, None, None,
+                               None, None, 0, None) == si_amd.SI_ERR_ARG
+    assert b"unsupported heads" in L.si_last_error()
+    s = si_amd.make_shape(**si_amd.SHAPES["0.5b"])
+    assert L.si_attention(ctypes.byref(s), None, 1, None, None, 0, None, 0, 0, 16, None, None,
+                          None, None, None, 0, None) == si_amd.SI_ERR_ARG
+    h = ctypes.c_void_p()
+    host = si_amd.LayerHost()
+    assert L.si_layer_create(ctypes.byref(s), ctypes.byref(host), 1, 16,
+                             ctypes.byref(h)) == si_amd.SI_ERR_ARG
+    assert L.si_layer_decode(None, None, None, None, 1, None, 0, None) == si_amd.SI_ERR_ARG
+
+
+def test_attention_workspace_sizing():
+    s = si_amd.make_shape(**si_amd.SHAPES["7b"])
+    ws = si_amd.lib().si_attention_workspace(ctypes.byref(s), 64, 4096)
+    assert ws > 0 and ws % 4 == 0
