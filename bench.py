@@ -72,6 +72,38 @@ def gemm_int_ops(shape, m):
     return 2 * m * ((QD + 2 * KVD) * H + H * QD + 2 * F * H + H * F)
 
 
+def graph_time_ms(torch, stream, fn, count, replays=3):
+    """Capture fn(0..count-1) into one HIP graph on `stream`, replay it and
+    return the mean milliseconds per fn call (HIP events on that stream).
+    The launches are enqueued by C code through ctypes; replaying the graph
+    removes the host-side issue cost so the events time the GPU work."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(count):
+            fn(i)
+    g.replay()  # warm
+    stream.synchronize()
+    t = Timer(torch, stream)
+    t.start()
+    for _ in range(replays):
+        g.replay()
+    ms = t.stop_ms() / (replays * count)
+    del g
+    return ms
+
+
+class _DevArray:
+    def __init__(self, addr, count, typestr):
+        self.__cuda_array_interface__ = {"shape": (count,), "typestr": typestr,
+                                         "data": (int(addr), False), "version": 2}
+
+
+def si_amd_view(torch, addr, count, dtype):
+    """torch tensor aliasing a device buffer owned by the library."""
+    typestr = {torch.uint8: "|u1", torch.int16: "<i2", torch.float32: "<f4"}[dtype]
+    return torch.as_tensor(_DevArray(addr, count, typestr), device="cuda")
+
+
 class Timer:
     """HIP events on a given torch stream."""
 
@@ -115,7 +147,8 @@ def bench_decode_layer(torch, si_amd, stream, steps, warmup, ctx=1024):
         lay = layers[i % copies]
         kc, vc = caches[i % copies]
         rc = L.si_layer_decode(lay.h, si_amd.ptr(x), si_amd.ptr(kc), si_amd.ptr(vc), ctx,
-                               si_amd.ptr(out), si_amd.SI_LAYER_FULL, sh)
+                               si_amd.ptr(out), si_amd.SI_LAYER_FULL,
+                               si_amd.stream_handle(torch.cuda.current_stream()))
         if rc:
             raise si_amd.SiError(rc, L.si_last_error().decode())
 
@@ -123,13 +156,14 @@ def bench_decode_layer(torch, si_amd, stream, steps, warmup, ctx=1024):
         for i in range(warmup):
             step(i)
         torch.cuda.synchronize()
+        # eager: one C call per step from Python (host launch cost included)
         t = Timer(torch, stream)
         t.start()
         for i in range(steps):
             step(i)
-        ms = t.stop_ms() / steps
+        eager_ms = t.stop_ms() / steps
         torch.cuda.synchronize()
-        # per-phase breakdown (events between stages), averaged
+        # per-phase breakdown (events between stages, eager), averaged
         layers[0].set_timing(True)
         acc = {}
         for i in range(20):
@@ -137,22 +171,35 @@ def bench_decode_layer(torch, si_amd, stream, steps, warmup, ctx=1024):
             for k, v in layers[0].phase_ms().items():
                 acc[k] = acc.get(k, 0.0) + v / 20
         layers[0].set_timing(False)
+        torch.cuda.synchronize()
+    # timed region: exactly `steps` decode steps, captured as one HIP graph
+    ms = graph_time_ms(torch, stream, step, steps, replays=3)
     alg = per_copy
     res = dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, alg_bytes=alg, copies=copies,
-               phases_us={k: round(v * 1e3, 2) for k, v in acc.items()})
+               eager_us=eager_ms * 1e3,
+               phases_us_eager={k: round(v * 1e3, 2) for k, v in acc.items()})
     return res, (layers, caches, s, x)
 
 
 def bench_dominant_gemv(torch, si_amd, stream, ctxobj, launches=400):
     """Roofline of the decode step's dominant kernel: the fused gate|up
     mat-vec (k_gemv_q4q8, 4.9 MB of the layer's 8.9 MB), launched alone on the
-    bench stream, cycling through the layer copies (cold weights)."""
+    bench stream, cycling through enough repacked copies of that matrix to
+    exceed the Infinity Cache (cold weights)."""
     layers, caches, s, x = ctxobj
     L = si_amd.lib()
-    sh = si_amd.stream_handle(stream)
-    ws_list = []
     F, H = s.ffn, s.hidden
     n, k = 2 * F, H
+    per = n * k // 32 * 18
+    ncopy = int(np.ceil(1.25 * MALL_BYTES / per))
+    src_qs, src_d, _, _ = layers[0].weights(2)
+    mats = []
+    for _ in range(ncopy):
+        qs = torch.empty(n * k // 2, dtype=torch.uint8, device="cuda")
+        d = torch.empty(n * k // 32, dtype=torch.int16, device="cuda")
+        qs.copy_(si_amd_view(torch, src_qs, n * k // 2, torch.uint8))
+        d.copy_(si_amd_view(torch, src_d, n * k // 32, torch.int16))
+        mats.append((qs.data_ptr(), d.data_ptr(), n, k, qs, d))
     # the same K-range split the layer uses (decode_splits in si_api.hip)
     tiles = (n + 63) // 64
     sp = max(1, min((512 + tiles - 1) // tiles, (k // 32) // 4))
@@ -162,32 +209,27 @@ def bench_dominant_gemv(torch, si_amd, stream, ctxobj, launches=400):
     xd = torch.full((k // 32,), 0x2c00, dtype=torch.int16, device="cuda")  # fp16 0.0625
     xs = xq.view(-1, 32).sum(1, dtype=torch.int32).to(torch.int16)
     out = torch.empty(n, device="cuda")
-    mats = [lay.weights(2) for lay in layers]
 
     def launch(i):
-        qs, d, nn, kk = mats[i % len(mats)]
+        qs, d, nn, kk = mats[i % len(mats)][:4]
         rc = L.si_matvec_q4q8(ctypes.c_void_p(qs), ctypes.c_void_p(d), nn, kk, si_amd.ptr(xq),
                               si_amd.ptr(xd), si_amd.ptr(xs), None, None, si_amd.ptr(out), sp,
-                              si_amd.ptr(ws), sh)
+                              si_amd.ptr(ws), si_amd.stream_handle(torch.cuda.current_stream()))
         if rc:
             raise si_amd.SiError(rc, L.si_last_error().decode())
 
     with torch.cuda.stream(stream):
         for i in range(20):
             launch(i)
-        t = Timer(torch, stream)
-        t.start()
-        for i in range(launches):
-            launch(i)
-        ms = t.stop_ms() / launches
+    torch.cuda.synchronize()
+    ms = graph_time_ms(torch, stream, launch, launches, replays=3)
     alg = n * k // 32 * 18 + k + (k // 32) * 4 + n * 4
     achieved = alg / (ms * 1e-3) / 1e9
-    del ws_list
     return dict(kernel="k_gemv_q4q8 (gate|up, N=9728 K=896)", us=ms * 1e3, alg_bytes=alg,
-                achieved_gbs=achieved, splits=sp)
+                achieved_gbs=achieved, splits=sp, copies=ncopy)
 
 
-def bench_qkv_gemv(torch, si_amd, stream, launches=2000):
+def bench_qkv_gemv(torch, si_amd, stream, launches=1000):
     """fused QKV mat-vec, K=896 N=1152, one token."""
     from_seed = np.random.default_rng(11)
     n, k = 1152, 896
@@ -219,18 +261,16 @@ def bench_qkv_gemv(torch, si_amd, stream, launches=2000):
         qs, d = mats[i % copies]
         rc = L.si_matvec_q4q8(si_amd.ptr(qs), si_amd.ptr(d), n, k, si_amd.ptr(xq),
                               si_amd.ptr(xd), si_amd.ptr(xs), si_amd.ptr(bias), None,
-                              si_amd.ptr(out), sp, si_amd.ptr(ws), sh)
+                              si_amd.ptr(out), sp, si_amd.ptr(ws),
+                              si_amd.stream_handle(torch.cuda.current_stream()))
         if rc:
             raise si_amd.SiError(rc, L.si_last_error().decode())
 
     with torch.cuda.stream(stream):
         for i in range(50):
             launch(i)
-        t = Timer(torch, stream)
-        t.start()
-        for i in range(launches):
-            launch(i)
-        ms = t.stop_ms() / launches
+    torch.cuda.synchronize()
+    ms = graph_time_ms(torch, stream, launch, launches, replays=3)
     alg = 586168  # W 580,608 + x 952 + y 4,608
     return dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, copies=copies, splits=sp)
 
@@ -246,18 +286,18 @@ def bench_prefill(torch, si_amd, stream, shape_name, ntok, steps):
     kc = torch.zeros(ntok * kvd, dtype=torch.float16, device="cuda")
     vc = torch.zeros_like(kc)
     out = torch.empty(ntok * s.hidden, device="cuda")
+    def call(i):
+        lay.prefill(x, ntok, 0, kc, vc, out, stream=torch.cuda.current_stream())
+
     with torch.cuda.stream(stream):
-        for _ in range(2):
-            lay.prefill(x, ntok, 0, kc, vc, out, stream=stream)
-        t = Timer(torch, stream)
-        t.start()
-        for _ in range(steps):
-            lay.prefill(x, ntok, 0, kc, vc, out, stream=stream)
-        ms = t.stop_ms() / steps
+        for i in range(2):
+            call(i)
         lay.set_timing(True)
-        lay.prefill(x, ntok, 0, kc, vc, out, stream=stream)
+        call(0)
         ph = lay.phase_ms()
         lay.set_timing(False)
+    torch.cuda.synchronize()
+    ms = graph_time_ms(torch, stream, call, steps, replays=2)
     gemm_ms = ph["qkv_proj"] + ph["out_proj"] + ph["gate_up"] + ph["down_proj"]
     ops = gemm_int_ops(s, ntok)
     lay.close()
@@ -280,18 +320,19 @@ def bench_batched_decode(torch, si_amd, stream, steps, nseq=64, ctx=4096):
     vc = torch.randn(nseq * stride, generator=gen, device="cuda").half()
     x = torch.randn(nseq * s.hidden, generator=gen, device="cuda")
     out = torch.empty(nseq * s.hidden, device="cuda")
+    def call(i):
+        lay.decode_batch(x, nseq, kc, vc, stride, ctx, ctx, out,
+                         stream=torch.cuda.current_stream())
+
     with torch.cuda.stream(stream):
-        for _ in range(2):
-            lay.decode_batch(x, nseq, kc, vc, stride, ctx, ctx, out, stream=stream)
-        t = Timer(torch, stream)
-        t.start()
-        for _ in range(steps):
-            lay.decode_batch(x, nseq, kc, vc, stride, ctx, ctx, out, stream=stream)
-        ms = t.stop_ms() / steps
+        for i in range(2):
+            call(i)
         lay.set_timing(True)
-        lay.decode_batch(x, nseq, kc, vc, stride, ctx, ctx, out, stream=stream)
+        call(0)
         ph = lay.phase_ms()
         lay.set_timing(False)
+    torch.cuda.synchronize()
+    ms = graph_time_ms(torch, stream, call, steps, replays=2)
     alg = weight_bytes(s) + nseq * 2 * ctx * kvd * 2 + small_bytes(s)
     lay.close()
     return dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, alg_bytes=alg,
@@ -406,7 +447,9 @@ def main():
                    "context": 1024, "layer_copies_rotated": dec["copies"],
                    "alg_bytes_per_step": dec["alg_bytes"]},
         "decode_layer_us": round(dec["us"], 3),
-        "phases_us": dec["phases_us"],
+        "decode_layer_us_eager": round(dec["eager_us"], 3),
+        "phases_us_eager": dec["phases_us_eager"],
+        "timing": "HIP graph replay of the K steps (one graph), HIP events on the bench stream",
         "roofline": {"bound": "hbm", "achieved": round(dom["achieved_gbs"], 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,

@@ -132,7 +132,8 @@ int si_matvec_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k, const i
                    const uint16_t *xd, const int16_t *xs, const float *bias,
                    const float *residual, float *out, int splits, void *workspace,
                    void *stream) {
-    SI_REQUIRE(n > 0 && k > 0 && k % 32 == 0, "matvec: bad size n=%d k=%d", n, k);
+    SI_REQUIRE(n > 0 && k > 0 && k % 32 == 0 && n <= 262144, "matvec: bad size n=%d k=%d", n,
+               k);
     SI_REQUIRE(wqs && wd && xqs && xd && xs && out, "matvec: NULL pointer");
     SI_REQUIRE(splits >= 1, "matvec: splits must be >= 1");
     SI_REQUIRE(gemv_effective_splits(k, splits) == 1 || workspace,

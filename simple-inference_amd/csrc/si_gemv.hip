@@ -121,11 +121,15 @@ __global__ void __launch_bounds__(64) k_block_dots(const uint8_t *__restrict__ w
         q4q8_block_dot(w, *(const int4 *)xb, *(const int4 *)(xb + 16), xs[b]);
 }
 
+// Workspace: a fixed block of arrival counters first (so one workspace can
+// serve mat-vecs of different shapes: partial sums never overlap counters),
+// then splits * n partial sums.
+constexpr size_t GEMV_COUNTERS = 4096;  // row tiles: n <= 262144
+
 size_t gemv_workspace_bytes(int n, int k, int splits) {
     splits = gemv_effective_splits(k, splits);
     if (splits == 1) return 0;
-    const size_t floats = ((size_t)splits * n + 63) / 64 * 64;
-    return floats * sizeof(float) + (size_t)((n + 63) / 64) * sizeof(unsigned int);
+    return GEMV_COUNTERS * sizeof(unsigned int) + (size_t)splits * n * sizeof(float);
 }
 
 void launch_gemv_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k, const int8_t *xqs,
@@ -134,9 +138,8 @@ void launch_gemv_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k, cons
                       hipStream_t st) {
     const int nb = k / SI_QK;
     splits = gemv_effective_splits(k, splits);
-    float *partial = (float *)workspace;
-    unsigned int *counters =
-        splits > 1 ? (unsigned int *)(partial + ((size_t)splits * n + 63) / 64 * 64) : nullptr;
+    unsigned int *counters = splits > 1 ? (unsigned int *)workspace : nullptr;
+    float *partial = splits > 1 ? (float *)(counters + GEMV_COUNTERS) : nullptr;
     const int bps = (nb + splits - 1) / splits;
     const dim3 grid((n + 63) / 64, splits);
     hipLaunchKernelGGL(k_gemv_q4q8<4>, grid, dim3(64), 0, st, wqs, wd, n, nb, xqs, xd, xs, bias,

@@ -26,3 +26,12 @@ def ref():
     if not have_reference():
         pytest.skip("oracle/_ref not built (reference sources absent on this host)")
     return Reference()
+
+
+@pytest.fixture(autouse=True)
+def _release_device_tensors():
+    yield
+    import sys
+    h = sys.modules.get("tests.gpu_helpers")
+    if h is not None:
+        h.KEEP.clear()

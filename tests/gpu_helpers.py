@@ -14,14 +14,46 @@ def torch_cuda():
     return torch
 
 
+# Device tensors made by dev() stay referenced until the test ends: a
+# temporary freed right after its address is taken would let torch's caching
+# allocator hand the same block to the next tensor before the kernel runs.
+KEEP = []
+
+
 def dev(a):
     torch = torch_cuda()
-    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    KEEP.append(t)
+    return t
 
 
 def empty(shape, dtype):
     torch = torch_cuda()
-    return torch.empty(shape, dtype=dtype, device="cuda")
+    t = torch.empty(shape, dtype=dtype, device="cuda")
+    KEEP.append(t)
+    return t
+
+
+def zeros(shape, dtype):
+    torch = torch_cuda()
+    t = torch.zeros(shape, dtype=dtype, device="cuda")
+    KEEP.append(t)
+    return t
+
+
+def dequant_q4(w_rowmajor, n, k):
+    """float64 [n][k] values of row-major Q4_0 bytes."""
+    b = np.asarray(w_rowmajor, np.uint8).reshape(n, k // 32, 18)
+    d = b[:, :, :2].copy().view(np.uint16)[..., 0].view(np.float16).astype(np.float64)
+    nib = np.concatenate([b[:, :, 2:] & 15, b[:, :, 2:] >> 4], axis=2).astype(np.float64) - 8
+    return (nib * d[:, :, None]).reshape(n, k)
+
+
+def dequant_q8(blocks, rows, k):
+    """float64 [rows][k] values of block_q8_0 records."""
+    q = blocks["qs"].astype(np.float64).reshape(rows, k // 32, 32)
+    d = blocks["d"].view(np.float16).astype(np.float64).reshape(rows, k // 32, 1)
+    return (q * d).reshape(rows, k)
 
 
 class _DeviceArray:

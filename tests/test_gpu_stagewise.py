@@ -1,0 +1,226 @@
+"""Stage-by-stage parity of the multi-row layer schedules (prefill and batched
+decode): every stage is checked on the GPU's OWN inputs to that stage, so a
+failure names the kernel that diverged instead of the end of the layer.
+
+Quantization stages are bit-exact; projection stages are compared with the
+float64 product of the dequantized operands; RoPE/K-V append bit-exact;
+attention within 2e-3."""
+import numpy as np
+import pytest
+
+import si_amd
+from oracle.oracle_py import Q8_DTYPE, make_shape as or_shape
+from tests.gpu_helpers import (close, dequant_q4, dev, device_view, empty, host, kv_history,
+                               make_layer, planar_to_aos)
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _buf(L, name, count, dtype):
+    return host(device_view(L.buffer(name), count, dtype).clone())
+
+
+def _q8_rows(L, prefix, rows, k):
+    torch = _torch()
+    qs = _buf(L, prefix + "_QS", rows * k, torch.int8)
+    d = _buf(L, prefix + "_D", rows * k // 32, torch.int16).view(np.uint16)
+    return planar_to_aos(qs, d)
+
+
+def _rows_off(got, want, rtol):
+    rms = np.sqrt(np.mean(want.astype(np.float64) ** 2))
+    err = np.abs(got.astype(np.float64) - want).max(axis=1) / max(rms, 1e-30)
+    return np.nonzero(err > rtol)[0], err
+
+
+def _check_rows(what, got, want, rtol):
+    bad, err = _rows_off(got, want, rtol)
+    assert bad.size == 0, (f"{what}: {bad.size} rows off (row mod 64: "
+                           f"{sorted(set((bad % 64).tolist()))[:12]}, first {bad[:8].tolist()},"
+                           f" worst {err.max():.3g} of rms)")
+
+
+def _dequant_act(blocks, rows, k):
+    q = blocks["qs"].astype(np.float64).reshape(rows, k // 32, 32)
+    d = blocks["d"].view(np.float16).astype(np.float64).reshape(rows, k // 32, 1)
+    return (q * d).reshape(rows, k)
+
+
+def _stagewise(oracle, L, lay, s, os_, x, rows, kc_host, vc_host, positions, ctxs, kv_base,
+               out):
+    """kc_host/vc_host: fp16 caches after the call (GPU's), positions[t]:
+    cache row of token t, ctxs[t]: its attention context, kv_base[t]: element
+    offset of its cache."""
+    torch = _torch()
+    H, D = s.hidden, s.hdim
+    QD, KVD, F = s.qheads * D, s.kvheads * D, s.ffn
+    NQKV = QD + 2 * KVD
+    # 1. RMSNorm -> Q8
+    normed = _buf(L, "NORMED", rows * H, torch.float32).reshape(rows, H)
+    want = np.stack([oracle.rmsnorm(x[t], lay["norm"]) for t in range(rows)])
+    _check_rows("rmsnorm", normed, want, 1e-6)
+    xq = _q8_rows(L, "XQ", rows, H)
+    assert xq.tobytes() == oracle.quantize_q8(normed).tobytes(), "input Q8"
+    # 2. QKV projection (+bias) on the GPU's Q8
+    qkv = _buf(L, "QKV", rows * NQKV, torch.float32).reshape(rows, NQKV)
+    wqkv = np.concatenate([lay["wq"], lay["wk"], lay["wv"]])
+    bias = np.concatenate([lay["bq"], lay["bk"], lay["bv"]]).astype(np.float64)
+    want = _dequant_act(xq, rows, H) @ dequant_q4(wqkv, NQKV, H).T + bias
+    _check_rows("qkv projection", qkv, want, 1e-5)
+    # 3. RoPE + fp16 K/V append on the GPU's projections
+    q = _buf(L, "Q", rows * QD, torch.float32).reshape(rows, QD)
+    for t in range(rows):
+        p = int(positions[t])
+        wq = oracle.rope(qkv[t, :QD], s.qheads, D, p)
+        wk = oracle.rope(qkv[t, QD:QD + KVD], s.kvheads, D, p)
+        assert np.array_equal(q[t].view(np.uint32), wq.view(np.uint32)), f"rope q row {t}"
+        base = int(kv_base[t]) + p * KVD
+        assert np.array_equal(kc_host[base:base + KVD], oracle.f32_to_f16(wk)), f"K row {t}"
+        assert np.array_equal(vc_host[base:base + KVD],
+                              oracle.f32_to_f16(qkv[t, QD + KVD:])), f"V row {t}"
+    # 4. attention over the GPU's cache, sampled rows (incl. every 63 mod 64)
+    attn = _buf(L, "ATTN", rows * QD, torch.float32).reshape(rows, QD)
+    sample = sorted({0, 1, rows - 1, rows // 2} | {t for t in range(63, rows, 64)})
+    for t in sample:
+        b = int(kv_base[t])
+        want = oracle.attention_flash(os_, q[t], kc_host[b:], vc_host[b:], int(ctxs[t]))
+        close(attn[t], want, 2e-3, f"attention row {t}")
+    attq = _q8_rows(L, "ATTQ", rows, QD)
+    assert attq.tobytes() == oracle.quantize_q8(attn).tobytes(), "attention Q8"
+    # 5. W_O
+    ao = _buf(L, "ATTN_OUT", rows * H, torch.float32).reshape(rows, H)
+    want = _dequant_act(attq, rows, QD) @ dequant_q4(lay["wo"], H, QD).T
+    _check_rows("o projection", ao, want, 1e-5)
+    # 6. residual + post-norm -> Q8
+    h = _buf(L, "H", rows * H, torch.float32).reshape(rows, H)
+    assert np.array_equal(h, x + ao), "residual 1"
+    n2 = _buf(L, "NORMED2", rows * H, torch.float32).reshape(rows, H)
+    want = np.stack([oracle.rmsnorm(h[t], lay["post_norm"]) for t in range(rows)])
+    _check_rows("post-norm", n2, want, 1e-6)
+    xq2 = _q8_rows(L, "XQ2", rows, H)
+    assert xq2.tobytes() == oracle.quantize_q8(n2).tobytes(), "post-norm Q8"
+    # 7. gate|up, SwiGLU -> Q8
+    gu = _buf(L, "GU", rows * 2 * F, torch.float32).reshape(rows, 2 * F)
+    wgu = np.concatenate([lay["wgate"], lay["wup"]])
+    want = _dequant_act(xq2, rows, H) @ dequant_q4(wgu, 2 * F, H).T
+    _check_rows("gate|up projection", gu, want, 1e-5)
+    act = _buf(L, "ACT", rows * F, torch.float32).reshape(rows, F)
+    want = np.stack([oracle.swiglu(gu[t, :F], gu[t, F:]) for t in range(rows)])
+    _check_rows("swiglu", act, want, 1e-5)
+    actq = _q8_rows(L, "ACTQ", rows, F)
+    assert actq.tobytes() == oracle.quantize_q8(act).tobytes(), "swiglu Q8"
+    # 8. down + residual
+    want = h + _dequant_act(actq, rows, F) @ dequant_q4(lay["wdown"], H, F).T
+    _check_rows("down projection + residual", out, want, 1e-5)
+
+
+def test_prefill_stagewise_0_5b():
+    from oracle.oracle_py import Oracle
+    oracle = Oracle()
+    torch = _torch()
+    sd = si_amd.SHAPES["0.5b"]
+    s, os_ = si_amd.make_shape(**sd), or_shape(**sd)
+    lay = make_layer(oracle, os_, 21)
+    ntok, prefix = 200, 30
+    kvd = s.kvheads * s.hdim
+    rng = np.random.default_rng(22)
+    total = prefix + ntok
+    x = rng.standard_normal((ntok, s.hidden)).astype(np.float32)
+    kc0 = np.zeros(total * kvd, np.uint16)
+    vc0 = np.zeros_like(kc0)
+    kc0[:prefix * kvd] = kv_history(oracle, rng, prefix, kvd)
+    vc0[:prefix * kvd] = kv_history(oracle, rng, prefix, kvd)
+    L = si_amd.Layer(s, lay, ntok, total)
+    kc, vc = dev(kc0.view(np.int16)), dev(vc0.view(np.int16))
+    out = empty(ntok * s.hidden, torch.float32)
+    L.prefill(dev(x), ntok, prefix, kc, vc, out)
+    _stagewise(oracle, L, lay, s, os_, x, ntok, host(kc).view(np.uint16),
+               host(vc).view(np.uint16), prefix + np.arange(ntok), prefix + 1 + np.arange(ntok),
+               np.zeros(ntok, np.int64), host(out).reshape(ntok, s.hidden))
+    L.close()
+
+
+def test_batched_decode_stagewise_7b():
+    from oracle.oracle_py import Oracle
+    oracle = Oracle()
+    torch = _torch()
+    sd = si_amd.SHAPES["7b"]
+    s, os_ = si_amd.make_shape(**sd), or_shape(**sd)
+    lay = make_layer(oracle, os_, 23)
+    nseq, ctx = 70, 160
+    kvd = s.kvheads * s.hdim
+    stride = ctx * kvd
+    rng = np.random.default_rng(24)
+    x = rng.standard_normal((nseq, s.hidden)).astype(np.float32)
+    kc0 = kv_history(oracle, rng, nseq * ctx, kvd)
+    vc0 = kv_history(oracle, rng, nseq * ctx, kvd)
+    L = si_amd.Layer(s, lay, nseq, ctx)
+    kc, vc = dev(kc0.view(np.int16)), dev(vc0.view(np.int16))
+    out = empty(nseq * s.hidden, torch.float32)
+    L.decode_batch(dev(x), nseq, kc, vc, stride, ctx, ctx, out)
+    _stagewise(oracle, L, lay, s, os_, x, nseq, host(kc).view(np.uint16),
+               host(vc).view(np.uint16), np.full(nseq, ctx - 1), np.full(nseq, ctx),
+               np.arange(nseq) * stride, host(out).reshape(nseq, s.hidden))
+    L.close()
+
+
+def _first_divergence(oracle, L, s, os_, lay, x_row, hk, hv, ctx, row, rows):
+    """Compare the GPU's intermediates of one row with the oracle's decode
+    captures; returns (stage, relative error) per stage in pipeline order."""
+    torch = _torch()
+    H, QD, KVD, F = s.hidden, s.qheads * s.hdim, s.kvheads * s.hdim, s.ffn
+    want_out, cap = oracle.layer_decode(os_, lay, x_row, hk, hv, ctx, capture=True)
+    got = {
+        "normed": _buf(L, "NORMED", rows * H, torch.float32).reshape(rows, H)[row],
+        "q": _buf(L, "Q", rows * QD, torch.float32).reshape(rows, QD)[row],
+        "attn": _buf(L, "ATTN", rows * QD, torch.float32).reshape(rows, QD)[row],
+        "attn_out": _buf(L, "ATTN_OUT", rows * H, torch.float32).reshape(rows, H)[row],
+        "h": _buf(L, "H", rows * H, torch.float32).reshape(rows, H)[row],
+        "normed2": _buf(L, "NORMED2", rows * H, torch.float32).reshape(rows, H)[row],
+        "act": _buf(L, "ACT", rows * F, torch.float32).reshape(rows, F)[row],
+    }
+    res = []
+    for k in ("normed", "q", "attn", "attn_out", "h", "normed2", "act"):
+        w = cap[k].astype(np.float64)
+        rms = np.sqrt(np.mean(w ** 2))
+        res.append((k, float(np.abs(got[k] - w).max() / rms)))
+    return res, want_out
+
+
+@pytest.mark.parametrize("nseq,ctx,row", [(64, 4096, 63), (64, 4096, 0), (64, 300, 63)])
+def test_batched_decode_divergence_7b(nseq, ctx, row):
+    """End-to-end vs the oracle, stage by stage, for one sequence of a batch."""
+    from oracle.oracle_py import Oracle
+    oracle = Oracle()
+    torch = _torch()
+    sd = si_amd.SHAPES["7b"]
+    s, os_ = si_amd.make_shape(**sd), or_shape(**sd)
+    lay = make_layer(oracle, os_, 7)
+    kvd = s.kvheads * s.hdim
+    stride = ctx * kvd
+    x = np.random.default_rng(8).standard_normal((nseq, s.hidden)).astype(np.float32)
+    rng = np.random.default_rng(100 + row)
+    hk = kv_history(oracle, rng, ctx, kvd)
+    hv = kv_history(oracle, rng, ctx, kvd)
+    kc = torch.zeros(nseq * stride, dtype=torch.int16, device="cuda")
+    vc = torch.zeros(nseq * stride, dtype=torch.int16, device="cuda")
+    kc[row * stride:(row + 1) * stride] = dev(hk.view(np.int16))
+    vc[row * stride:(row + 1) * stride] = dev(hv.view(np.int16))
+    L = si_amd.Layer(s, lay, nseq, ctx)
+    out = empty(nseq * s.hidden, torch.float32)
+    L.decode_batch(dev(x), nseq, kc, vc, stride, ctx, ctx, out)
+    stages, want = _first_divergence(oracle, L, s, os_, lay, x[row], hk.copy(), hv.copy(), ctx,
+                                     row, nseq)
+    got = host(out).reshape(nseq, s.hidden)[row]
+    rms = np.sqrt(np.mean(want.astype(np.float64) ** 2))
+    report = ", ".join(f"{k} {e:.2e}" for k, e in stages) + \
+        f", out {np.abs(got - want).max() / rms:.2e}"
+    print(report)
+    assert all(e < 2e-3 for _, e in stages), report
+    close(got, want, 1e-3, f"sequence {row}: {report}")
+    L.close()
