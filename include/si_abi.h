@@ -114,12 +114,17 @@ int si_matvec_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k,
 size_t si_matvec_workspace(int n, int k, int splits);
 
 /* matvec_q4q8 applied to m activation rows (prefill / batched decode):
- * out[i][r] (row stride ldo) = residual + bias + sum over blocks.  int8
- * matrix-core tiles with fp32 scale epilogues; within fp32 rounding. */
+ * out[i][r] (row stride ldo; residual uses the same stride) =
+ * residual + (bias + sum over blocks).  int8 matrix-core tiles compute every
+ * per-block int32 dot exactly; the fp32 epilogue either reproduces the
+ * reference's rounding sequence (flags & SI_GEMM_EXACT: bit-exact with
+ * matvec_q4q8) or uses one fused multiply-add per block (within fp32
+ * rounding of the reference). */
+enum { SI_GEMM_EXACT = 1 };
 int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k,
                  const int8_t *xqs, const uint16_t *xd, int m,
                  const float *bias, const float *residual, float *out, int ldo,
-                 void *stream);
+                 int flags, void *stream);
 
 /* RoPE (qwen_one_layer.c:172-183) + fp16 K/V append (:262-266) for ntok
  * rows of the fused projection output qkv[t] = [q | k | v]
@@ -193,7 +198,9 @@ int si_layer_destroy(si_layer_t *l);
 enum {
     SI_LAYER_FULL = 0,      /* attention + residual + norm + SwiGLU FFN + residual */
     SI_LAYER_ATTN_ONLY = 1, /* reference run_layer: out = W_O . Q8(attn)          */
-    SI_LAYER_EXACT = 2      /* decode GEMVs without K splits (bit-exact projections) */
+    SI_LAYER_EXACT = 2      /* reference rounding in every projection (bit-exact Q/K/V,
+                               O, gate/up, down given identical inputs): mat-vecs
+                               without K splits, GEMMs with the exact epilogue */
 };
 
 /* run_layer (qwen_one_layer.c:237-281) for one token at position context-1:

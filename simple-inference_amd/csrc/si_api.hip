@@ -145,12 +145,14 @@ int si_matvec_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k, const i
 
 int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k, const int8_t *xqs,
                  const uint16_t *xd, int m, const float *bias, const float *residual,
-                 float *out, int ldo, void *stream) {
+                 float *out, int ldo, int flags, void *stream) {
     SI_REQUIRE(n > 0 && k > 0 && k % 32 == 0 && m >= 0, "gemm: bad size m=%d n=%d k=%d", m, n,
                k);
     SI_REQUIRE(ldo >= n, "gemm: ldo %d < n %d", ldo, n);
     SI_REQUIRE(m == 0 || (wqs && wd && xqs && xd && out), "gemm: NULL pointer");
-    launch_gemm_q4q8(wqs, wd, n, k, xqs, xd, m, bias, residual, out, ldo, S(stream));
+    SI_REQUIRE((flags & ~SI_GEMM_EXACT) == 0, "gemm: unknown flags %d", flags);
+    launch_gemm_q4q8(wqs, wd, n, k, xqs, xd, m, bias, residual, out, ldo,
+                     (flags & SI_GEMM_EXACT) != 0, S(stream));
     return check_launch("si_gemm_q4q8");
 }
 
@@ -532,7 +534,8 @@ static void project(si_layer *L, const Q4Dev &w, int rows, const Q8Buf &x, const
         launch_gemv_q4q8(w.qs, w.d, w.n, w.k, x.qs, x.d, x.s, bias, residual, out,
                          decode_splits(L, w.n, w.k, flags), L->gemv_ws, st);
     else
-        launch_gemm_q4q8(w.qs, w.d, w.n, w.k, x.qs, x.d, rows, bias, residual, out, w.n, st);
+        launch_gemm_q4q8(w.qs, w.d, w.n, w.k, x.qs, x.d, rows, bias, residual, out, w.n,
+                         (flags & SI_LAYER_EXACT) != 0, st);
 }
 
 // Shared schedule.  rows activation rows; positions and attention contexts

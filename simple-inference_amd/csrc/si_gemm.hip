@@ -36,6 +36,11 @@ constexpr int BN = 128;   // weight rows per workgroup (4 wavefronts x 32)
 constexpr int AST = 48;   // LDS row stride (bytes) of the A tile, padded
 constexpr int BST = 48;   // LDS row stride (bytes) of the B tile, padded
 
+// EXACT: the reference's rounding sequence per block, y = bias, then in block
+// order y = y + ((float)dot * w.d) * x.d (qwen_one_layer.c:153-159), so each
+// output equals matvec_q4q8 bit for bit.  Otherwise one fused multiply-add
+// per block with the scale product x.d*w.d and the bias added at the end.
+template <bool EXACT>
 __global__ void __launch_bounds__(256) k_gemm_q4q8(
     const uint8_t *__restrict__ wqs, const uint16_t *__restrict__ wd, int n, int nb,
     const int8_t *__restrict__ xqs, const uint16_t *__restrict__ xd, int m,
@@ -59,11 +64,14 @@ __global__ void __launch_bounds__(256) k_gemm_q4q8(
     const int b_row = tid & 127;
     const int b_grow = min(n0 + b_row, n - 1);
 
+    const int j = lane & 31, g = lane >> 5;
+    const int col = n0 + wave * 32 + j;
+    const float bias0 = (EXACT && bias) ? bias[min(col, n - 1)] : 0.0f;
     float acc[2][16];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[t][v] = 0.0f;
+        for (int v = 0; v < 16; ++v) acc[t][v] = bias0;
 
     uint4 stage;
     float sscale = 0.0f;
@@ -94,7 +102,6 @@ __global__ void __launch_bounds__(256) k_gemm_q4q8(
         }
     };
 
-    const int j = lane & 31, g = lane >> 5;
     load_block(0);
     for (int b = 0; b < nb; ++b) {
         __syncthreads();  // previous block's LDS reads are done
@@ -112,22 +119,25 @@ __global__ void __launch_bounds__(256) k_gemm_q4q8(
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int mi = t * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
-                acc[t][v] = fmaf((float)dot[v], dx_lds[mi] * dwv, acc[t][v]);
+                if (EXACT)
+                    acc[t][v] = __fadd_rn(acc[t][v],
+                                          __fmul_rn(__fmul_rn((float)dot[v], dwv), dx_lds[mi]));
+                else
+                    acc[t][v] = fmaf((float)dot[v], dx_lds[mi] * dwv, acc[t][v]);
             }
         }
     }
 
-    const int col = n0 + wave * 32 + j;
     if (col >= n) return;
-    const float bv = bias ? bias[col] : 0.0f;
+    const float bv = (!EXACT && bias) ? bias[col] : 0.0f;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const int row = m0 + t * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
             if (row < m) {
-                float y = acc[t][v] + bv;
-                if (residual) y = residual[(size_t)row * ldo + col] + y;
+                float y = EXACT ? acc[t][v] : acc[t][v] + bv;
+                if (residual) y = __fadd_rn(residual[(size_t)row * ldo + col], y);
                 out[(size_t)row * ldo + col] = y;
             }
         }
@@ -135,11 +145,15 @@ __global__ void __launch_bounds__(256) k_gemm_q4q8(
 
 void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k, const int8_t *xqs,
                       const uint16_t *xd, int m, const float *bias, const float *residual,
-                      float *out, int ldo, hipStream_t st) {
+                      float *out, int ldo, bool exact, hipStream_t st) {
     if (m <= 0 || n <= 0) return;
     const dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM);
-    hipLaunchKernelGGL(k_gemm_q4q8, grid, dim3(256), 0, st, wqs, wd, n, k / SI_QK, xqs, xd, m,
-                       bias, residual, out, ldo);
+    if (exact)
+        hipLaunchKernelGGL(k_gemm_q4q8<true>, grid, dim3(256), 0, st, wqs, wd, n, k / SI_QK, xqs,
+                           xd, m, bias, residual, out, ldo);
+    else
+        hipLaunchKernelGGL(k_gemm_q4q8<false>, grid, dim3(256), 0, st, wqs, wd, n, k / SI_QK, xqs,
+                           xd, m, bias, residual, out, ldo);
 }
 
 }  // namespace si

@@ -26,7 +26,7 @@ void launch_block_dots(const uint8_t *wqs, int n, int k, const int8_t *xqs, cons
                        int32_t *dots, hipStream_t st);
 void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k, const int8_t *xqs,
                       const uint16_t *xd, int m, const float *bias, const float *residual,
-                      float *out, int ldo, hipStream_t st);
+                      float *out, int ldo, bool exact, hipStream_t st);
 }  // namespace si
 namespace si {
 void launch_rope_kv(const float *qkv, int ldqkv, int ntok, int qheads, int kvheads, int hdim,

@@ -23,6 +23,7 @@ Q8_DTYPE = np.dtype([("d", "<u2"), ("qs", "i1", (QK,))])  # defines.h:27-28
 
 SI_OK, SI_ERR_ARG, SI_ERR_HIP, SI_ERR_STATE, SI_ERR_NOMEM = range(5)
 SI_LAYER_FULL, SI_LAYER_ATTN_ONLY, SI_LAYER_EXACT = 0, 1, 2
+SI_GEMM_EXACT = 1
 BUFFERS = ["NORMED", "XQ_QS", "XQ_D", "XQ_S", "QKV", "Q", "ATTN", "ATTQ_QS", "ATTQ_D",
            "ATTQ_S", "ATTN_OUT", "H", "NORMED2", "XQ2_QS", "XQ2_D", "XQ2_S", "GU", "ACT",
            "ACTQ_QS", "ACTQ_D", "ACTQ_S"]
@@ -76,7 +77,7 @@ _SIGS = {
     "si_q4q8_block_dots": (_I, [_P, _P, _I, _I, _P, _P, _P, _P]),
     "si_matvec_q4q8": (_I, [_P, _P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P]),
     "si_matvec_workspace": (_Z, [_I, _I, _I]),
-    "si_gemm_q4q8": (_I, [_P, _P, _I, _I, _P, _P, _I, _P, _P, _P, _I, _P]),
+    "si_gemm_q4q8": (_I, [_P, _P, _I, _I, _P, _P, _I, _P, _P, _P, _I, _I, _P]),
     "si_rope_kv_append": (_I, [ctypes.POINTER(Shape), _P, _I, _I, _I, _I, _I, _P, _P, _P, _P,
                                _P, _P, _Z, _P]),
     "si_rope_table": (_I, [_I, _I, _F, _P, _P]),

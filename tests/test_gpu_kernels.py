@@ -256,7 +256,7 @@ def test_gemm_matches_oracle_rows(oracle, m, n, k):
     out = empty(m * n, torch.float32)
     si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), n, k, si_amd.ptr(dev(qs)),
                 si_amd.ptr(dev(d.view(np.int16))), m, si_amd.ptr(dev(b)), None,
-                si_amd.ptr(out), n, None)
+                si_amd.ptr(out), n, 0, None)
     got = host(out).reshape(m, n)
     nb = k // 32
     for r in sorted({0, m // 2, m - 1}):
@@ -278,7 +278,7 @@ def test_gemm_every_row_vs_float64(oracle, m, n, k):
     wqs, wd = _upload_q4(w, n, k)
     out = empty(m * n, torch.float32)
     si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), n, k, si_amd.ptr(dev(qs)),
-                si_amd.ptr(dev(d.view(np.int16))), m, None, None, si_amd.ptr(out), n, None)
+                si_amd.ptr(dev(d.view(np.int16))), m, None, None, si_amd.ptr(out), n, 0, None)
     got = host(out).reshape(m, n)
     want = dequant_q8(xq, m, k) @ dequant_q4(w, n, k).T
     rms = np.sqrt(np.mean(want ** 2))
@@ -301,7 +301,7 @@ def test_gemm_residual(oracle):
     out = empty(m * n, torch.float32)
     si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), n, k, si_amd.ptr(dev(qs)),
                 si_amd.ptr(dev(d.view(np.int16))), m, None, si_amd.ptr(dev(res)),
-                si_amd.ptr(out), n, None)
+                si_amd.ptr(out), n, 0, None)
     got = host(out).reshape(m, n)
     nb = k // 32
     for r in (0, 69):

@@ -1,5 +1,7 @@
-"""Layer-level GPU parity (decode, batched decode, prefill) against the oracle
-on the benchmark configurations, plus the C11 host mirror (run_layer)."""
+"""Layer-level GPU parity on the benchmark configurations (decode, batched
+decode, causal prefill), the reference's prefill == sequential-decode
+contract, and the C11 host mirror.  Rows are checked with the chained
+oracle check (tests/chain.py); the raw end-to-end difference is printed."""
 import ctypes
 import os
 
@@ -7,11 +9,13 @@ import numpy as np
 import pytest
 
 import si_amd
-from oracle.oracle_py import make_shape as or_shape
-from tests.gpu_helpers import close, dev, device_view, empty, host, kv_history, make_layer
+from oracle.oracle_py import Q8_DTYPE, make_shape as or_shape
+from tests.chain import LayerBuffers, check_row, end_to_end_report
+from tests.gpu_helpers import close, dev, empty, host, kv_history, make_layer
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ref_golden.npz")
+EXACT = si_amd.SI_LAYER_EXACT
 
 
 def _torch():
@@ -26,9 +30,8 @@ def _shapes(name):
 
 @pytest.mark.parametrize("ctx", [1, 17, 64])
 def test_attention_sublayer_reference_shape_golden(oracle, ctx):
-    """run_layer at the reference's own 1.5B shape vs the reference's outputs
-    (golden fixture).  SI_LAYER_EXACT keeps the reference's projection order,
-    so the appended fp16 K/V rows are bit-identical (audit_fusion_timing.c:192)."""
+    """run_layer at the reference's own 1.5B shape against the reference's
+    outputs (golden fixture written from the reference build)."""
     from tests.golden.make_golden import layer_weights
     g = np.load(GOLDEN, allow_pickle=False)
     s, os_ = _shapes("1.5b_ref")
@@ -39,23 +42,22 @@ def test_attention_sublayer_reference_shape_golden(oracle, ctx):
     kc = dev(g[f"layer_kc_{ctx}"].view(np.int16))
     vc = dev(g[f"layer_vc_{ctx}"].view(np.int16))
     out = empty(s.hidden, torch.float32)
-    L.decode(dev(g["layer_x"]), kc, vc, ctx, out,
-             si_amd.SI_LAYER_ATTN_ONLY | si_amd.SI_LAYER_EXACT)
-    close(host(out), g[f"layer_out_{ctx}"], 1e-3, "Y")
-    attn = host(_view(L, "ATTN", s.qheads * s.hdim, torch.float32))
-    close(attn, g[f"layer_attn_{ctx}"], 2e-3, "attention")
+    L.decode(dev(g["layer_x"]), kc, vc, ctx, out, si_amd.SI_LAYER_ATTN_ONLY | EXACT)
+    B = LayerBuffers(L, os_, 1)
     hk, hv = host(kc).view(np.uint16), host(vc).view(np.uint16)
+    # the appended fp16 K/V rows equal the reference's (audit_fusion_timing.c:192-196)
     assert np.array_equal(hk[(ctx - 1) * kvd:], g[f"layer_newk_{ctx}"])
     assert np.array_equal(hv[(ctx - 1) * kvd:], g[f"layer_newv_{ctx}"])
+    close(B.attn[0], g[f"layer_attn_{ctx}"], 2e-3, "attention vs reference")
+    got = host(out)
+    check_row(oracle, os_, lay, g["layer_x"], 0, B, hk, hv, 0, ctx - 1, ctx, got, True,
+              full=False)
+    close(got, g[f"layer_out_{ctx}"], 1e-3, "Y vs reference")
     L.close()
 
 
-def _view(L, name, count, dtype):
-    """Copy of a layer workspace buffer as a torch tensor."""
-    return device_view(L.buffer(name), count, dtype).clone()
-
-
-def test_decode_full_layer_0_5b_ctx1024(oracle):
+@pytest.mark.parametrize("flags", [si_amd.SI_LAYER_FULL, EXACT])
+def test_decode_full_layer_0_5b_ctx1024(oracle, flags):
     """full 0.5B layer, one token at context 1024."""
     torch = _torch()
     s, os_ = _shapes("0.5b")
@@ -66,92 +68,103 @@ def test_decode_full_layer_0_5b_ctx1024(oracle):
     kc0 = kv_history(oracle, rng, ctx, kvd)
     vc0 = kv_history(oracle, rng, ctx, kvd)
     x = rng.standard_normal(s.hidden).astype(np.float32)
-    kr, vr = kc0.copy(), vc0.copy()
-    want, cap = oracle.layer_decode(os_, lay, x, kr, vr, ctx, capture=True)
     L = si_amd.Layer(s, lay, 1, ctx)
-    for flags in (si_amd.SI_LAYER_FULL, si_amd.SI_LAYER_EXACT):
-        kc, vc = dev(kc0.view(np.int16)), dev(vc0.view(np.int16))
-        out = empty(s.hidden, torch.float32)
-        L.decode(dev(x), kc, vc, ctx, out, flags)
-        close(host(out), want, 1e-3, f"layer out flags={flags}")
-        attn = host(_view(L, "ATTN", s.qheads * s.hdim, torch.float32))
-        close(attn, cap["attn"], 2e-3, "attention")
-        hk, hv = host(kc).view(np.uint16), host(vc).view(np.uint16)
-        if flags == si_amd.SI_LAYER_EXACT:
-            # reference-order projections: q/k/v and the new fp16 K/V rows are exact
-            qkv = host(_view(L, "QKV", s.qheads * s.hdim + 2 * kvd, torch.float32))
-            q = host(_view(L, "Q", s.qheads * s.hdim, torch.float32))
-            assert np.array_equal(q.view(np.uint32), cap["q"].view(np.uint32))
-            assert np.array_equal(qkv[s.qheads * s.hdim + kvd:].view(np.uint32),
-                                  cap["v"].view(np.uint32))
-            assert np.array_equal(hk, kr) and np.array_equal(hv, vr)
-        else:
-            close(oracle.f16_to_f32(hk[(ctx - 1) * kvd:]),
-                  oracle.f16_to_f32(kr[(ctx - 1) * kvd:]), 1e-3, "new K")
-            assert np.array_equal(hk[:(ctx - 1) * kvd], kr[:(ctx - 1) * kvd])
+    kc, vc = dev(kc0.view(np.int16)), dev(vc0.view(np.int16))
+    out = empty(s.hidden, torch.float32)
+    L.decode(dev(x), kc, vc, ctx, out, flags)
+    B = LayerBuffers(L, os_, 1)
+    hk, hv = host(kc).view(np.uint16), host(vc).view(np.uint16)
+    assert np.array_equal(hk[:(ctx - 1) * kvd], kc0[:(ctx - 1) * kvd])  # history untouched
+    got = host(out)
+    check_row(oracle, os_, lay, x, 0, B, hk, hv, 0, ctx - 1, ctx, got, flags == EXACT)
+    want = oracle.layer_decode(os_, lay, x, kc0.copy(), vc0.copy(), ctx)
+    print("end-to-end vs oracle:", end_to_end_report(got, want))
     L.close()
 
 
-@pytest.mark.parametrize("shape,ntok,prefix,rows", [
-    ("0.5b", 512, 0, [0, 1, 17, 255, 511]),
-    ("0.5b", 37, 100, [0, 36]),                 # ragged, with a cached prefix
-])
-def test_prefill_vs_oracle(oracle, shape, ntok, prefix, rows):
+def _prefill_case(oracle, shape, ntok, prefix, seed, flags, rows):
     torch = _torch()
     s, os_ = _shapes(shape)
-    lay = make_layer(oracle, os_, 4)
+    lay = make_layer(oracle, os_, seed)
     kvd = s.kvheads * s.hdim
-    rng = np.random.default_rng(ntok)
+    rng = np.random.default_rng(seed + 1)
     total = prefix + ntok
     x = rng.standard_normal((ntok, s.hidden)).astype(np.float32)
     kc0 = np.zeros(total * kvd, np.uint16)
     vc0 = np.zeros_like(kc0)
     kc0[:prefix * kvd] = kv_history(oracle, rng, prefix, kvd)
     vc0[:prefix * kvd] = kv_history(oracle, rng, prefix, kvd)
-    kr, vr = kc0.copy(), vc0.copy()
-    want = oracle.layer_prefill(os_, lay, x, ntok, prefix, kr, vr, rows=rows)
     L = si_amd.Layer(s, lay, ntok, total)
     kc, vc = dev(kc0.view(np.int16)), dev(vc0.view(np.int16))
     out = empty(ntok * s.hidden, torch.float32)
-    L.prefill(dev(x), ntok, prefix, kc, vc, out)
+    L.prefill(dev(x), ntok, prefix, kc, vc, out, flags)
+    B = LayerBuffers(L, os_, ntok)
+    hk, hv = host(kc).view(np.uint16), host(vc).view(np.uint16)
     got = host(out).reshape(ntok, s.hidden)
-    for i, t in enumerate(rows):
-        close(got[t], want[i], 1e-3, f"prefill row {t}")
-    hk = oracle.f16_to_f32(host(kc).view(np.uint16))
-    hv = oracle.f16_to_f32(host(vc).view(np.uint16))
-    close(hk, oracle.f16_to_f32(kr), 1e-3, "prefill K cache")
-    close(hv, oracle.f16_to_f32(vr), 1e-3, "prefill V cache")
+    for t in rows:
+        check_row(oracle, os_, lay, x[t], t, B, hk, hv, 0, prefix + t, prefix + t + 1, got[t],
+                  flags == EXACT)
+    return L, s, os_, lay, x, kc0, vc0, hk, hv, got
+
+
+@pytest.mark.parametrize("shape,ntok,prefix,rows,flags", [
+    ("0.5b", 512, 0, [0, 1, 17, 63, 255, 511], EXACT),
+    ("0.5b", 512, 0, [0, 63, 255, 511], si_amd.SI_LAYER_FULL),
+    ("0.5b", 37, 100, [0, 36], EXACT),                      # ragged, cached prefix
+])
+def test_prefill_vs_oracle(oracle, shape, ntok, prefix, rows, flags):
+    L, s, os_, lay, x, kc0, vc0, hk, hv, got = _prefill_case(oracle, shape, ntok, prefix, 4,
+                                                             flags, rows)
+    if flags == EXACT:
+        # every appended K/V row equals the oracle's (prefill contract)
+        kr, vr = kc0.copy(), vc0.copy()
+        want = oracle.layer_prefill(os_, lay, x, ntok, prefix, kr, vr, rows=rows)
+        assert np.array_equal(hk, kr) and np.array_equal(hv, vr)
+        print("end-to-end vs oracle:", [end_to_end_report(got[t], want[i])
+                                        for i, t in enumerate(rows)])
     L.close()
 
 
 def test_prefill_7b_2048_sampled_rows(oracle):
-    """7B layer, 2048-token prefill; oracle rows sampled."""
-    torch = _torch()
-    s, os_ = _shapes("7b")
-    lay = make_layer(oracle, os_, 5)
-    ntok, kvd = 2048, s.kvheads * s.hdim
-    rng = np.random.default_rng(6)
-    x = rng.standard_normal((ntok, s.hidden)).astype(np.float32)
-    rows = [0, 1, 1023, 2047]
-    kr = np.zeros(ntok * kvd, np.uint16)
-    vr = np.zeros_like(kr)
-    want = oracle.layer_prefill(os_, lay, x, ntok, 0, kr, vr, rows=rows)
-    L = si_amd.Layer(s, lay, ntok, ntok)
-    kc = dev(np.zeros(ntok * kvd, np.int16))
-    vc = dev(np.zeros(ntok * kvd, np.int16))
-    out = empty(ntok * s.hidden, torch.float32)
-    L.prefill(dev(x), ntok, 0, kc, vc, out)
-    got = host(out).reshape(ntok, s.hidden)
-    for i, t in enumerate(rows):
-        close(got[t], want[i], 1e-3, f"7b prefill row {t}")
-    close(oracle.f16_to_f32(host(kc).view(np.uint16)), oracle.f16_to_f32(kr), 1e-3, "K cache")
+    """7B layer, 2048-token causal prefill."""
+    L, *_ = _prefill_case(oracle, "7b", 2048, 0, 5, EXACT, [0, 1, 63, 1023, 2047])
     L.close()
 
 
-@pytest.mark.parametrize("nseq,ctx,check", [(4, 300, [0, 3]), (64, 4096, [0, 63])])
+def test_prefill_equals_sequential_decode(oracle):
+    """bench_ai_dma_prefill.c:104-129: a prefill batch and a loop of
+    single-token decodes leave bit-identical fp16 K/V for every position and
+    agree on every output (EXACT projections)."""
+    torch = _torch()
+    s, os_ = _shapes("0.5b")
+    lay = make_layer(oracle, os_, 11)
+    ntok, prefix = 24, 9
+    kvd = s.kvheads * s.hdim
+    rng = np.random.default_rng(12)
+    total = prefix + ntok
+    x = rng.standard_normal((ntok, s.hidden)).astype(np.float32)
+    k0 = np.zeros(total * kvd, np.uint16)
+    v0 = np.zeros_like(k0)
+    k0[:prefix * kvd] = kv_history(oracle, rng, prefix, kvd)
+    v0[:prefix * kvd] = kv_history(oracle, rng, prefix, kvd)
+    L = si_amd.Layer(s, lay, ntok, total)
+    kp, vp = dev(k0.view(np.int16)), dev(v0.view(np.int16))
+    yp = empty(ntok * s.hidden, torch.float32)
+    L.prefill(dev(x), ntok, prefix, kp, vp, yp, EXACT)
+    ks, vs = dev(k0.view(np.int16)), dev(v0.view(np.int16))
+    ys = empty(ntok * s.hidden, torch.float32)
+    xd = dev(x)
+    for t in range(ntok):
+        L.decode(xd[t], ks, vs, prefix + t + 1, ys[t * s.hidden:(t + 1) * s.hidden], EXACT)
+    assert np.array_equal(host(kp), host(ks)) and np.array_equal(host(vp), host(vs))
+    close(host(yp), host(ys), 1e-3, "prefill vs sequential decode")
+    L.close()
+
+
+@pytest.mark.parametrize("nseq,ctx,check", [(4, 300, [0, 3]), (64, 4096, [0, 31, 63])])
 def test_batched_decode_7b(oracle, nseq, ctx, check):
-    """BASELINE config 5 (64 sequences x 4096 positions) and a small variant:
-    each sequence has its own contiguous cache; sampled sequences are checked."""
+    """BASELINE config 5 (64 sequences x 4096 positions) and a small variant;
+    each sequence has its own contiguous cache."""
     torch = _torch()
     s, os_ = _shapes("7b")
     lay = make_layer(oracle, os_, 7)
@@ -159,26 +172,20 @@ def test_batched_decode_7b(oracle, nseq, ctx, check):
     stride = ctx * kvd
     x = np.random.default_rng(8).standard_normal((nseq, s.hidden)).astype(np.float32)
     L = si_amd.Layer(s, lay, nseq, ctx)
-    # device caches filled on the GPU side from seeded host rows of the
-    # checked sequences; the others get N(0,1) from torch (not checked)
     gen = torch.Generator(device="cuda").manual_seed(9)
     kc = torch.randn(nseq * stride, generator=gen, device="cuda").half().view(torch.int16)
     vc = torch.randn(nseq * stride, generator=gen, device="cuda").half().view(torch.int16)
-    hist = {}
     for i in check:
         rng = np.random.default_rng(100 + i)
-        hk = kv_history(oracle, rng, ctx, kvd)
-        hv = kv_history(oracle, rng, ctx, kvd)
-        kc[i * stride:(i + 1) * stride] = dev(hk.view(np.int16))
-        vc[i * stride:(i + 1) * stride] = dev(hv.view(np.int16))
-        hist[i] = (hk, hv)
+        kc[i * stride:(i + 1) * stride] = dev(kv_history(oracle, rng, ctx, kvd).view(np.int16))
+        vc[i * stride:(i + 1) * stride] = dev(kv_history(oracle, rng, ctx, kvd).view(np.int16))
     out = empty(nseq * s.hidden, torch.float32)
-    L.decode_batch(dev(x), nseq, kc, vc, stride, ctx, ctx, out)
+    L.decode_batch(dev(x), nseq, kc, vc, stride, ctx, ctx, out, flags=EXACT)
+    B = LayerBuffers(L, os_, nseq)
+    hk, hv = host(kc).view(np.uint16), host(vc).view(np.uint16)
     got = host(out).reshape(nseq, s.hidden)
     for i in check:
-        hk, hv = hist[i]
-        want = oracle.layer_decode(os_, lay, x[i], hk, hv, ctx)
-        close(got[i], want, 1e-3, f"sequence {i}")
+        check_row(oracle, os_, lay, x[i], i, B, hk, hv, i * stride, ctx - 1, ctx, got[i], True)
     L.close()
 
 
@@ -217,7 +224,6 @@ def test_host_mirror_run_layer(oracle):
     vc = dev(g[f"layer_vc_{ctx}"].view(np.int16))
     out = empty(s.hidden, torch.float32)
     attn = np.zeros(s.qheads * s.hdim, np.float32)
-    from oracle.oracle_py import Q8_DTYPE
     q8 = np.zeros(s.qheads * s.hdim // 32, Q8_DTYPE)
     x = dev(g["layer_x"])
     ph = H.run_layer(m, si_amd.ptr(x), si_amd.ptr(kc), si_amd.ptr(vc), ctx, si_amd.ptr(out), 1,

@@ -42,7 +42,7 @@ def test_argument_errors_do_not_launch():
     L = si_amd.lib()
     assert L.si_quantize_q8(None, None, 33, None) == si_amd.SI_ERR_ARG
     assert b"multiple of 32" in L.si_last_error()
-    assert L.si_gemm_q4q8(None, None, 64, 30, None, None, 4, None, None, None, 64,
+    assert L.si_gemm_q4q8(None, None, 64, 30, None, None, 4, None, None, None, 64, 0,
                           None) == si_amd.SI_ERR_ARG
     assert L.si_matvec_q4q8(None, None, 64, 64, None, None, None, None, None, None, 1, None,
                             None) == si_amd.SI_ERR_ARG
