@@ -73,21 +73,24 @@ def gemm_int_ops(shape, m):
 
 
 def graph_time_ms(torch, stream, fn, count, replays=3):
-    """Capture fn(0..count-1) into one HIP graph on `stream`, replay it and
-    return the mean milliseconds per fn call (HIP events on that stream).
-    The launches are enqueued by C code through ctypes; replaying the graph
-    removes the host-side issue cost so the events time the GPU work."""
+    """Capture fn(0..count-1) into one HIP graph on `stream`, replay it on the
+    same stream and return the mean milliseconds per fn call, timed with HIP
+    events recorded on that stream around the replays.  The launches are
+    enqueued by C code through ctypes; replaying the graph removes the
+    host-side issue cost, so the events time the GPU work."""
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
         for i in range(count):
             fn(i)
-    g.replay()  # warm
-    stream.synchronize()
-    t = Timer(torch, stream)
-    t.start()
-    for _ in range(replays):
-        g.replay()
-    ms = t.stop_ms() / (replays * count)
+    with torch.cuda.stream(stream):
+        g.replay()  # warm
+        stream.synchronize()
+        t = Timer(torch, stream)
+        t.start()
+        for _ in range(replays):
+            g.replay()
+        ms = t.stop_ms() / (replays * count)
+    torch.cuda.synchronize()
     del g
     return ms
 

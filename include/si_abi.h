@@ -161,6 +161,12 @@ int si_attention(const si_shape_t *s, const float *q, int nq, const uint16_t *kc
                  void *stream);
 size_t si_attention_workspace(const si_shape_t *s, int nq, int max_ctx);
 
+/* Test entry for the fp16 matrix-core lane layouts the attention kernels
+ * rely on: a [16][32] and b [32][16] fp16 (row-major) -> d32 = a.b with the
+ * 16x16x32 shape and d16 = a[:, :16].b[:16, :] with the 16x16x16 shape
+ * (fp32 [16][16] row-major).  No counterpart in the reference. */
+int si_debug_mfma_f16(const void *a, const void *b, float *d32, float *d16, void *stream);
+
 /* Build-defined SwiGLU + quantize_q8: act = silu(gate)*up with
  * silu(g) = g/(1+expf(-g)); gate = gu[r][0..f), up = gu[r][f..2f). */
 int si_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs,

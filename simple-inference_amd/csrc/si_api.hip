@@ -55,8 +55,8 @@ static int check_shape(const si_shape_t *s) {
     SI_REQUIRE(s->hidden > 0 && s->hidden % 32 == 0, "hidden %d must be a positive multiple of 32",
                s->hidden);
     SI_REQUIRE(attn_supported(s->qheads, s->kvheads, s->hdim),
-               "unsupported heads %d/%d x hdim %d (need qheads %% kvheads == 0, ratio <= 8, "
-               "hdim in 32..128 multiple of 32)",
+               "unsupported heads %d/%d x hdim %d (need qheads %% kvheads == 0, ratio <= 16, "
+               "hdim 32, 64, 96 or 128)",
                s->qheads, s->kvheads, s->hdim);
     SI_REQUIRE(s->ffn >= 0 && s->ffn % 32 == 0, "ffn %d must be a multiple of 32", s->ffn);
     SI_REQUIRE(s->hidden <= 8192, "hidden %d exceeds 8192", s->hidden);
@@ -213,6 +213,12 @@ int si_attention(const si_shape_t *s, const float *q, int nq, const uint16_t *kc
     launch_attention(q, nq, s->qheads, s->kvheads, s->hdim, kc, vc, kv_seq_stride, ctx_dev, ctx0,
                      ctx_step, max_ctx, attn, qs, d, bsum, ws, S(stream));
     return check_launch("si_attention");
+}
+
+int si_debug_mfma_f16(const void *a, const void *b, float *d32, float *d16, void *stream) {
+    SI_REQUIRE(a && b && d32 && d16, "debug_mfma: NULL pointer");
+    launch_debug_mfma_f16(a, b, d32, d16, S(stream));
+    return check_launch("si_debug_mfma_f16");
 }
 
 int si_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs, uint16_t *d,

@@ -9,10 +9,11 @@
 // Attention (attention_flash, attention_kernels.h:80-164) is split over the
 // context ("flash-decoding"): each workgroup owns one query, one KV group
 // (all qheads/kvheads query heads that share it, so every K/V byte is read
-// once per query) and one context chunk, streams 256-position tiles with an
-// online softmax, and leaves (max, sum, unnormalised output) partials; a
-// second kernel merges the chunks, normalises and quantizes the result to
-// Q8_0 (the reference's next step, qwen_one_layer.c:272).
+// once per query) and one context chunk, runs the scores and the weighted
+// V sum on the fp16 matrix cores with an online softmax, and leaves
+// (max, sum, unnormalised output) partials; a second kernel merges the
+// chunks, normalises and quantizes the result to Q8_0 (the reference's next
+// step, qwen_one_layer.c:272).
 #include "si_device.hpp"
 #include "si_kernels.hpp"
 
@@ -60,119 +61,7 @@ void launch_rope_kv(const float *qkv, int ldqkv, int ntok, int qheads, int kvhea
                        q_out, kc, vc, kv_seq_stride);
 }
 
-constexpr int ATT_TILE = 256;  // positions per tile (= threads per workgroup)
-constexpr int ATT_MAXPER = 8;  // query heads per KV group supported
-constexpr int ATT_MAXD = 128;  // head dim supported
-
-// grid (nsplit, kvheads, nq), block 256.
-__global__ void __launch_bounds__(256) k_attn_partial(
-    const float *__restrict__ q, int qheads, int kvheads, int hdim,
-    const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, size_t kv_seq_stride,
-    const int *__restrict__ ctx_dev, int ctx0, int ctx_step, int max_ctx, int chunk, float scale,
-    float *__restrict__ ws_m, float *__restrict__ ws_l, float *__restrict__ ws_o) {
-    __shared__ float q_s[ATT_MAXPER * ATT_MAXD];
-    __shared__ float p_s[ATT_MAXPER][ATT_TILE];
-    __shared__ float m_s[ATT_MAXPER], l_s[ATT_MAXPER], a_s[ATT_MAXPER];
-
-    const int sp = blockIdx.x, g = blockIdx.y, qi = blockIdx.z;
-    const int nsplit = gridDim.x;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int per = qheads / kvheads;
-    int ctx = ctx_dev ? ctx_dev[qi] : ctx0 + qi * ctx_step;
-    ctx = min(ctx, max_ctx);  // device-supplied contexts are not host-checked
-    const int p0 = sp * chunk;
-    const int p1 = min(ctx, p0 + chunk);
-    const int kvd = kvheads * hdim;
-    const uint16_t *kbase = kc + (size_t)qi * kv_seq_stride + (size_t)g * hdim;
-    const uint16_t *vbase = vc + (size_t)qi * kv_seq_stride + (size_t)g * hdim;
-
-    for (int i = tid; i < per * hdim; i += 256)
-        q_s[i] = q[(size_t)qi * qheads * hdim + (size_t)g * per * hdim + i];
-    if (tid < per) {
-        m_s[tid] = -INFINITY;
-        l_s[tid] = 0.0f;
-    }
-    // outputs owned by this thread: o_idx = tid + 256*r over per*hdim
-    float o[4] = {0.f, 0.f, 0.f, 0.f};
-    __syncthreads();
-
-    for (int t0 = p0; t0 < p1; t0 += ATT_TILE) {
-        const int p = t0 + tid;
-        // scores for position p, all heads of the group
-        float sc[ATT_MAXPER];
-#pragma unroll
-        for (int hh = 0; hh < ATT_MAXPER; ++hh) sc[hh] = 0.0f;
-        if (p < p1) {
-            const uint16_t *kr = kbase + (size_t)p * kvd;
-            for (int d0 = 0; d0 < hdim; d0 += 8) {
-                const uint4 kv8 = *(const uint4 *)(kr + d0);
-                const uint32_t kw[4] = {kv8.x, kv8.y, kv8.z, kv8.w};
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float kf = h2f_fast((uint16_t)(kw[e >> 1] >> (16 * (e & 1))));
-#pragma unroll
-                    for (int hh = 0; hh < ATT_MAXPER; ++hh)
-                        if (hh < per) sc[hh] = fmaf(q_s[hh * hdim + d0 + e], kf, sc[hh]);
-                }
-            }
-        }
-#pragma unroll
-        for (int hh = 0; hh < ATT_MAXPER; ++hh)
-            if (hh < per) p_s[hh][tid] = p < p1 ? sc[hh] * scale : -INFINITY;
-        __syncthreads();
-        // per-head online-softmax update (one wavefront per head)
-        for (int hh = wave; hh < per; hh += 4) {
-            float mx = -INFINITY;
-            for (int i = lane; i < ATT_TILE; i += 64) mx = fmaxf(mx, p_s[hh][i]);
-            mx = wave_max(mx);
-            const float mold = m_s[hh];
-            const float mnew = fmaxf(mold, mx);
-            float sum = 0.0f;
-            for (int i = lane; i < ATT_TILE; i += 64) {
-                const float e = expf(p_s[hh][i] - mnew);
-                p_s[hh][i] = e;
-                sum += e;
-            }
-            sum = wave_sum(sum);
-            if (lane == 0) {
-                const float alpha = expf(mold - mnew);  // 0 on the first tile
-                a_s[hh] = alpha;
-                l_s[hh] = l_s[hh] * alpha + sum;
-                m_s[hh] = mnew;
-            }
-        }
-        __syncthreads();
-        const int np = min(ATT_TILE, p1 - t0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int oi = tid + 256 * r;
-            if (oi < per * hdim) {
-                const int hh = oi / hdim, jj = oi - hh * hdim;
-                float acc = o[r] * a_s[hh];
-                const uint16_t *vr = vbase + (size_t)t0 * kvd + jj;
-                for (int t = 0; t < np; ++t)
-                    acc = fmaf(p_s[hh][t], h2f_fast(vr[(size_t)t * kvd]), acc);
-                o[r] = acc;
-            }
-        }
-        __syncthreads();
-    }
-    // partials: [qi][h][sp]
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int oi = tid + 256 * r;
-        if (oi < per * hdim) {
-            const int hh = oi / hdim, jj = oi - hh * hdim;
-            const int h = g * per + hh;
-            ws_o[(((size_t)qi * qheads + h) * nsplit + sp) * hdim + jj] = o[r];
-        }
-    }
-    if (tid < per) {
-        const int h = g * per + tid;
-        ws_m[((size_t)qi * qheads + h) * nsplit + sp] = m_s[tid];
-        ws_l[((size_t)qi * qheads + h) * nsplit + sp] = l_s[tid];
-    }
-}
+constexpr int ATT_MAXPER = 16;  // query heads per KV group (the 16 MFMA columns)
 
 // grid (qheads, nq), block hdim: merge chunks, normalise, quantize to Q8_0.
 __global__ void k_attn_combine(int qheads, int hdim, int nsplit, const float *__restrict__ ws_m,
@@ -207,24 +96,188 @@ __global__ void k_attn_combine(int qheads, int hdim, int nsplit, const float *__
     }
 }
 
+// ===========================================================================
+// Matrix-core decode attention.
+//
+// One workgroup owns (query, KV group, context chunk); its 4 wavefronts take
+// every 4th 16-position tile of the chunk.  Per tile a wavefront computes
+//     S^T[pos][head] = K[pos][:] . Q[head][:]        (v_mfma_f32_16x16x32_f16)
+// with the GQA group's query heads as the 16 MFMA columns (padded), then an
+// online-softmax update per head, then
+//     O^T[d][head] += V^T[d][pos] . P[pos][head]     (v_mfma_f32_16x16x16_f16)
+// K is read straight from HBM as the MFMA A operand (16 B per lane); V rows
+// are staged through LDS and read transposed (the MFMA reduction runs over
+// positions).  Q and P are fp32 values split into fp16 hi + lo halves
+// (x = hi + lo to 22 bits), each product done twice, so the result keeps
+// fp32-level accuracy although the matrix cores take fp16.  Each wavefront's
+// (max, sum, unnormalised O) is one partial; k_attn_combine merges them.
+//
+// Layouts (16x16 tiles): MFMA output element (i, j) is held by lane
+// j + 16*(i/4), register i%4.  The A/B operands give lane l row/column l%16
+// and the k-slice (l/16); A and B use the same k-slice per lane, so any
+// consistent assignment of reduction indices to slices is exact.
+// ===========================================================================
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int MA_TILE = 16;            // positions per wavefront tile
+constexpr int MA_SUPER = 4 * MA_TILE;  // positions per workgroup step
+constexpr int MA_VPAD = 16;            // halves of LDS row padding (bank spread)
+
+__device__ __forceinline__ void split_hi_lo(float x, _Float16 &hi, _Float16 &lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
+
+template <int D>
+__global__ void __launch_bounds__(256) k_attn_decode_mfma(
+    const float *__restrict__ q, int qheads, int kvheads, const uint16_t *__restrict__ kc,
+    const uint16_t *__restrict__ vc, size_t kv_seq_stride, const int *__restrict__ ctx_dev,
+    int ctx0, int ctx_step, int max_ctx, int chunk, float scale, float *__restrict__ ws_m,
+    float *__restrict__ ws_l, float *__restrict__ ws_o) {
+    constexpr int KS = D / 32;  // k-steps of the score MFMA
+    constexpr int DT = D / 16;  // d-tiles of the PV MFMA
+    constexpr int VROW = D + MA_VPAD;
+    __shared__ __attribute__((aligned(16))) _Float16 v_lds[MA_SUPER * VROW];
+
+    const int sp = blockIdx.x, g = blockIdx.y, qi = blockIdx.z;
+    const int nsplit4 = gridDim.x * 4;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int per = qheads / kvheads;
+    int ctx = ctx_dev ? ctx_dev[qi] : ctx0 + qi * ctx_step;
+    ctx = min(ctx, max_ctx);
+    const int p0 = sp * chunk;
+    const int p1 = min(ctx, p0 + chunk);
+    const int kvd = kvheads * D;
+    const uint16_t *kbase = kc + (size_t)qi * kv_seq_stride + (size_t)g * D;
+    const uint16_t *vbase = vc + (size_t)qi * kv_seq_stride + (size_t)g * D;
+
+    // Q^T as the B operand: lane holds Q[head = col][d = 8*grp + 32*ks + 0..7]
+    h8 qh[KS], ql[KS];
+    {
+        const bool hv = col < per;
+        const float *qrow = q + (size_t)qi * qheads * D + (size_t)(g * per + (hv ? col : 0)) * D;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float x = hv ? qrow[32 * ks + 8 * grp + e] : 0.0f;
+                _Float16 hi, lo;
+                split_hi_lo(x, hi, lo);
+                qh[ks][e] = hi;
+                ql[ks][e] = lo;
+            }
+    }
+    float m = -INFINITY, lsum = 0.0f;  // running state of head `col`
+    f4 o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = (f4){0.f, 0.f, 0.f, 0.f};
+
+    for (int s0 = p0; s0 < p1; s0 += MA_SUPER) {
+        // stage the step's V rows (clamped to valid rows) into LDS
+        constexpr int CHUNKS = MA_SUPER * D / 8;  // 16-byte pieces
+#pragma unroll
+        for (int c = tid; c < CHUNKS; c += 256) {
+            const int r = c / (D / 8), e = (c % (D / 8)) * 8;
+            const int pos = min(s0 + r, p1 - 1);
+            const uint4 v8 = *(const uint4 *)(vbase + (size_t)pos * kvd + e);
+            *(uint4 *)(&v_lds[r * VROW + e]) = v8;
+        }
+        __syncthreads();
+        const int t0 = s0 + MA_TILE * wave;
+        if (t0 < p1) {
+            // scores: A = K rows (pos = t0 + col), k-slice grp
+            const int kpos = min(t0 + col, p1 - 1);
+            const uint16_t *krow = kbase + (size_t)kpos * kvd + 8 * grp;
+            f4 sacc = (f4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const uint4 kraw = *(const uint4 *)(krow + 32 * ks);
+                const h8 ka = __builtin_bit_cast(h8, kraw);
+                sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[ks], sacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[ks], sacc, 0, 0, 0);
+            }
+            // lane holds S^T[pos = t0 + 4*grp + r][head = col]
+            float s[4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int pos = t0 + 4 * grp + r;
+                s[r] = pos < p1 ? sacc[r] * scale : -INFINITY;
+                mx = fmaxf(mx, s[r]);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mnew = fmaxf(m, mx);
+            const float alpha = expf(m - mnew);  // 0 while m is -inf
+            float p[4], ps = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                p[r] = expf(s[r] - mnew);
+                ps += p[r];
+            }
+            ps += __shfl_xor(ps, 16, 64);
+            ps += __shfl_xor(ps, 32, 64);
+            lsum = lsum * alpha + ps;
+            m = mnew;
+            h4 ph, pl;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                _Float16 hi, lo;
+                split_hi_lo(p[r], hi, lo);
+                ph[r] = hi;
+                pl[r] = lo;
+            }
+            // PV: A = V^T[d = 16*dt + col][pos = 4*grp + r] from this wave's LDS rows
+            const _Float16 *vw = &v_lds[(MA_TILE * wave + 4 * grp) * VROW + col];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                h4 va;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) va[r] = vw[r * VROW + 16 * dt];
+                f4 acc = o[dt] * alpha;
+                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ph, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pl, acc, 0, 0, 0);
+                o[dt] = acc;
+            }
+        }
+        __syncthreads();  // V rows are overwritten by the next step
+    }
+    // this wavefront's partial: split index sp*4 + wave
+    if (col < per) {
+        const int h = g * per + col;
+        const size_t pi = ((size_t)qi * qheads + h) * nsplit4 + sp * 4 + wave;
+        if (grp == 0) {
+            ws_m[pi] = m;
+            ws_l[pi] = lsum;
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ws_o[pi * D + 16 * dt + 4 * grp + r] = o[dt][r];
+    }
+}
+
+// Context chunks per (query, KV group): enough workgroups to cover the chip
+// (>= ~512) while every chunk keeps at least one 64-position step.
 int attn_nsplit(int kvheads, int nq, int max_ctx) {
-    // aim for >= ~512 workgroups, chunks of at least one 256-position tile
     const int base = kvheads * nq;
     int ns = (512 + base - 1) / base;
-    const int maxs = (max_ctx + ATT_TILE - 1) / ATT_TILE;
+    const int maxs = (max_ctx + MA_SUPER - 1) / MA_SUPER;
     if (ns > maxs) ns = maxs;
-    if (ns < 1) ns = 1;
-    return ns;
+    return ns < 1 ? 1 : ns;
 }
 
 size_t attn_workspace_bytes(int qheads, int hdim, int kvheads, int nq, int max_ctx) {
-    const int ns = attn_nsplit(kvheads, nq, max_ctx);
+    const int ns = attn_nsplit(kvheads, nq, max_ctx) * 4;  // one partial per wavefront
     return (size_t)nq * qheads * ns * (hdim + 2) * sizeof(float);
 }
 
 bool attn_supported(int qheads, int kvheads, int hdim) {
     return kvheads > 0 && qheads % kvheads == 0 && qheads / kvheads <= ATT_MAXPER &&
-           hdim <= ATT_MAXD && hdim % 32 == 0 && hdim >= 32;
+           (hdim == 32 || hdim == 64 || hdim == 96 || hdim == 128);
 }
 
 void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
@@ -235,16 +288,52 @@ void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
     if (nq <= 0) return;
     const int ns = attn_nsplit(kvheads, nq, max_ctx);
     int chunk = (max_ctx + ns - 1) / ns;
-    chunk = (chunk + ATT_TILE - 1) / ATT_TILE * ATT_TILE;
+    chunk = (chunk + MA_SUPER - 1) / MA_SUPER * MA_SUPER;
+    const int ns4 = ns * 4;
     float *ws_m = (float *)workspace;
-    float *ws_l = ws_m + (size_t)nq * qheads * ns;
-    float *ws_o = ws_l + (size_t)nq * qheads * ns;
+    float *ws_l = ws_m + (size_t)nq * qheads * ns4;
+    float *ws_o = ws_l + (size_t)nq * qheads * ns4;
     const float scale = 1.0f / sqrtf((float)hdim);  // attention_kernels.h:86
-    hipLaunchKernelGGL(k_attn_partial, dim3(ns, kvheads, nq), dim3(256), 0, st, q, qheads,
-                       kvheads, hdim, kc, vc, kv_seq_stride, ctx_dev, ctx0, ctx_step, max_ctx,
-                       chunk, scale, ws_m, ws_l, ws_o);
-    hipLaunchKernelGGL(k_attn_combine, dim3(qheads, nq), dim3(hdim), 0, st, qheads, hdim, ns,
+    const dim3 grid(ns, kvheads, nq);
+#define SI_ATTN_LAUNCH(DIM)                                                                  \
+    hipLaunchKernelGGL(k_attn_decode_mfma<DIM>, grid, dim3(256), 0, st, q, qheads, kvheads, kc, \
+                       vc, kv_seq_stride, ctx_dev, ctx0, ctx_step, max_ctx, chunk, scale, ws_m, \
+                       ws_l, ws_o)
+    switch (hdim) {
+        case 32: SI_ATTN_LAUNCH(32); break;
+        case 64: SI_ATTN_LAUNCH(64); break;
+        case 96: SI_ATTN_LAUNCH(96); break;
+        default: SI_ATTN_LAUNCH(128); break;
+    }
+#undef SI_ATTN_LAUNCH
+    hipLaunchKernelGGL(k_attn_combine, dim3(qheads, nq), dim3(hdim), 0, st, qheads, hdim, ns4,
                        ws_m, ws_l, ws_o, attn, qs, d, bsum);
+}
+
+// Test entry: one 16x16 tile with each of the two f16 matrix-core shapes,
+// operands placed with the lane layouts above, output scattered back to
+// row-major with the assumed output layout.  A [16][32], B [32][16] halves.
+__global__ void k_debug_mfma_f16(const _Float16 *A, const _Float16 *B, float *D32, float *D16) {
+    const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
+    h8 a8, b8;
+    for (int e = 0; e < 8; ++e) {
+        a8[e] = A[col * 32 + 8 * grp + e];
+        b8[e] = B[(8 * grp + e) * 16 + col];
+    }
+    f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8, b8, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    for (int r = 0; r < 4; ++r) D32[(4 * grp + r) * 16 + col] = d[r];
+    h4 a4, b4;
+    for (int e = 0; e < 4; ++e) {
+        a4[e] = A[col * 32 + 4 * grp + e];
+        b4[e] = B[(4 * grp + e) * 16 + col];
+    }
+    f4 d2 = __builtin_amdgcn_mfma_f32_16x16x16f16(a4, b4, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    for (int r = 0; r < 4; ++r) D16[(4 * grp + r) * 16 + col] = d2[r];
+}
+
+void launch_debug_mfma_f16(const void *A, const void *B, float *D32, float *D16, hipStream_t st) {
+    hipLaunchKernelGGL(k_debug_mfma_f16, dim3(1), dim3(64), 0, st, (const _Float16 *)A,
+                       (const _Float16 *)B, D32, D16);
 }
 
 }  // namespace si

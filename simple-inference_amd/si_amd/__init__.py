@@ -85,6 +85,7 @@ _SIGS = {
                           _P, _P, _P, _Z, _P]),
     "si_attention_workspace": (_Z, [ctypes.POINTER(Shape), _I, _I]),
     "si_swiglu_q8": (_I, [_P, _I, _I, _P, _P, _P, _P, _P]),
+    "si_debug_mfma_f16": (_I, [_P, _P, _P, _P, _P]),
     "si_layer_create": (_I, [ctypes.POINTER(Shape), ctypes.POINTER(LayerHost), _I, _I,
                              ctypes.POINTER(_P)]),
     "si_layer_destroy": (_I, [_P]),

@@ -421,3 +421,17 @@ def test_attention_causal_prefill(oracle):
     for t in (0, 1, 17, ntok - 1):
         want = oracle.attention_flash(os_, q[t], kc, vc, prefix + t + 1)
         close(got[t], want, 2e-3, f"row {t}")
+
+
+def test_mfma_f16_lane_layouts():
+    """The fp16 16x16 matrix-core layouts assumed by the attention kernels."""
+    torch = _torch()
+    rng = np.random.default_rng(0)
+    a = rng.integers(-8, 8, (16, 32)).astype(np.float16)
+    b = rng.integers(-8, 8, (32, 16)).astype(np.float16)
+    d32, d16 = empty(256, torch.float32), empty(256, torch.float32)
+    si_amd.call("si_debug_mfma_f16", si_amd.ptr(dev(a.view(np.int16))),
+                si_amd.ptr(dev(b.view(np.int16))), si_amd.ptr(d32), si_amd.ptr(d16), None)
+    af, bf = a.astype(np.float64), b.astype(np.float64)
+    assert np.array_equal(host(d32).reshape(16, 16), af @ bf)
+    assert np.array_equal(host(d16).reshape(16, 16), af[:, :16] @ bf[:16, :])
