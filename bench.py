@@ -136,8 +136,9 @@ def bench_decode_layer(torch, si_amd, stream, steps, warmup, ctx=1024):
     copies = int(np.ceil(1.25 * MALL_BYTES / per_copy))
     gen = torch.Generator(device="cuda").manual_seed(3)
     layers, caches = [], []
+    ws = si_amd.Workspace(s, 1, ctx)  # one workspace for all layers, as in a model
     for _ in range(copies):
-        layers.append(si_amd.Layer(s, tens, 1, ctx))
+        layers.append(si_amd.Layer(s, tens, workspace=ws))
         kc = torch.randn(ctx * kvd, generator=gen, device="cuda").half()
         vc = torch.randn(ctx * kvd, generator=gen, device="cuda").half()
         caches.append((kc, vc))
@@ -181,33 +182,29 @@ def bench_decode_layer(torch, si_amd, stream, steps, warmup, ctx=1024):
     res = dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, alg_bytes=alg, copies=copies,
                eager_us=eager_ms * 1e3,
                phases_us_eager={k: round(v * 1e3, 2) for k, v in acc.items()})
-    return res, (layers, caches, s, x)
+    return res, (layers, caches, s, x, ws)
 
 
 def bench_dominant_gemv(torch, si_amd, stream, ctxobj, launches=400):
     """Roofline of the decode step's dominant kernel: the fused gate|up
-    mat-vec (k_gemv_q4q8, 4.9 MB of the layer's 8.9 MB), launched alone on the
+    mat-vec shape (4.9 MB of the layer's 8.9 MB) as k_matvec, launched alone on the
     bench stream, cycling through enough repacked copies of that matrix to
     exceed the Infinity Cache (cold weights)."""
-    layers, caches, s, x = ctxobj
+    layers, caches, s, x, _ = ctxobj
     L = si_amd.lib()
     F, H = s.ffn, s.hidden
     n, k = 2 * F, H
     per = n * k // 32 * 18
     ncopy = int(np.ceil(1.25 * MALL_BYTES / per))
-    src_qs, src_d, _, _ = layers[0].weights(2)
+    src_qs, src_d, _, _, _ = layers[0].weights(2)
+    tile = L.si_q4_tile(n, k)  # stand-alone mat-vec tile (the layer pairs gate|up rows)
+    nd = L.si_q4_scale_count(n, k, tile)
     mats = []
     for _ in range(ncopy):
         qs = torch.empty(n * k // 2, dtype=torch.uint8, device="cuda")
-        d = torch.empty(n * k // 32, dtype=torch.int16, device="cuda")
+        d = torch.full((nd,), 0x2000, dtype=torch.int16, device="cuda")
         qs.copy_(si_amd_view(torch, src_qs, n * k // 2, torch.uint8))
-        d.copy_(si_amd_view(torch, src_d, n * k // 32, torch.int16))
         mats.append((qs.data_ptr(), d.data_ptr(), n, k, qs, d))
-    # the same K-range split the layer uses (decode_splits in si_api.hip)
-    tiles = (n + 63) // 64
-    sp = max(1, min((512 + tiles - 1) // tiles, (k // 32) // 4))
-    wsb = L.si_matvec_workspace(n, k, sp)
-    ws = torch.zeros(max(wsb, 4), dtype=torch.uint8, device="cuda")
     xq = torch.randint(-127, 128, (k,), dtype=torch.int8, device="cuda")
     xd = torch.full((k // 32,), 0x2c00, dtype=torch.int16, device="cuda")  # fp16 0.0625
     xs = xq.view(-1, 32).sum(1, dtype=torch.int32).to(torch.int16)
@@ -215,9 +212,10 @@ def bench_dominant_gemv(torch, si_amd, stream, ctxobj, launches=400):
 
     def launch(i):
         qs, d, nn, kk = mats[i % len(mats)][:4]
-        rc = L.si_matvec_q4q8(ctypes.c_void_p(qs), ctypes.c_void_p(d), nn, kk, si_amd.ptr(xq),
-                              si_amd.ptr(xd), si_amd.ptr(xs), None, None, si_amd.ptr(out), sp,
-                              si_amd.ptr(ws), si_amd.stream_handle(torch.cuda.current_stream()))
+        rc = L.si_matvec_q4q8(ctypes.c_void_p(qs), ctypes.c_void_p(d), tile, nn, kk,
+                              si_amd.ptr(xq),
+                              si_amd.ptr(xd), si_amd.ptr(xs), None, None, si_amd.ptr(out), 0,
+                              si_amd.stream_handle(torch.cuda.current_stream()))
         if rc:
             raise si_amd.SiError(rc, L.si_last_error().decode())
 
@@ -228,8 +226,8 @@ def bench_dominant_gemv(torch, si_amd, stream, ctxobj, launches=400):
     ms = graph_time_ms(torch, stream, launch, launches, replays=3)
     alg = n * k // 32 * 18 + k + (k // 32) * 4 + n * 4
     achieved = alg / (ms * 1e-3) / 1e9
-    return dict(kernel="k_gemv_q4q8 (gate|up, N=9728 K=896)", us=ms * 1e3, alg_bytes=alg,
-                achieved_gbs=achieved, splits=sp, copies=ncopy)
+    return dict(kernel="k_matvec (gate|up shape, N=9728 K=896)", us=ms * 1e3, alg_bytes=alg,
+                achieved_gbs=achieved, copies=ncopy)
 
 
 def bench_qkv_gemv(torch, si_amd, stream, launches=1000):
@@ -243,10 +241,12 @@ def bench_qkv_gemv(torch, si_amd, stream, launches=1000):
     copies = int(np.ceil(1.25 * MALL_BYTES / per))
     wdev = torch.from_numpy(w).cuda()
     mats = []
+    tile = L.si_q4_tile(n, k)
     for _ in range(copies):
         qs = torch.empty(n * k // 2, dtype=torch.uint8, device="cuda")
-        d = torch.empty(n * k // 32, dtype=torch.int16, device="cuda")
-        si_amd.call("si_q4_repack", si_amd.ptr(wdev), n, k, si_amd.ptr(qs), si_amd.ptr(d), sh)
+        d = torch.zeros(L.si_q4_scale_count(n, k, tile), dtype=torch.int16, device="cuda")
+        si_amd.call("si_q4_repack", si_amd.ptr(wdev), n, k, tile, si_amd.ptr(qs), si_amd.ptr(d),
+                    sh)
         mats.append((qs, d))
     x = torch.randn(k, device="cuda")
     xq = torch.empty(k, dtype=torch.int8, device="cuda")
@@ -256,15 +256,12 @@ def bench_qkv_gemv(torch, si_amd, stream, launches=1000):
                 si_amd.ptr(xs), sh)
     bias = torch.randn(n, device="cuda") * 0.02
     out = torch.empty(n, device="cuda")
-    tiles = (n + 63) // 64
-    sp = max(1, min((512 + tiles - 1) // tiles, (k // 32) // 4))
-    ws = torch.zeros(max(L.si_matvec_workspace(n, k, sp), 4), dtype=torch.uint8, device="cuda")
 
     def launch(i):
         qs, d = mats[i % copies]
-        rc = L.si_matvec_q4q8(si_amd.ptr(qs), si_amd.ptr(d), n, k, si_amd.ptr(xq),
+        rc = L.si_matvec_q4q8(si_amd.ptr(qs), si_amd.ptr(d), tile, n, k, si_amd.ptr(xq),
                               si_amd.ptr(xd), si_amd.ptr(xs), si_amd.ptr(bias), None,
-                              si_amd.ptr(out), sp, si_amd.ptr(ws),
+                              si_amd.ptr(out), 0,
                               si_amd.stream_handle(torch.cuda.current_stream()))
         if rc:
             raise si_amd.SiError(rc, L.si_last_error().decode())
@@ -275,7 +272,54 @@ def bench_qkv_gemv(torch, si_amd, stream, launches=1000):
     torch.cuda.synchronize()
     ms = graph_time_ms(torch, stream, launch, launches, replays=3)
     alg = 586168  # W 580,608 + x 952 + y 4,608
-    return dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, copies=copies, splits=sp)
+    return dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, copies=copies)
+
+
+def bench_gemv_7b(torch, si_amd, stream, launches=200):
+    """Qwen2.5-7B decode projections as stand-alone mat-vecs (si_matvec_q4q8,
+    k_matvec) on cold weights: the north-star target is >= 70 % of HBM peak.
+    Weights are random Q4_0 bytes (values do not affect the timing), copies
+    rotated to exceed the Infinity Cache."""
+    L = si_amd.lib()
+    gen = torch.Generator(device="cuda").manual_seed(12)
+    res = {}
+    for name, n, k in (("qkv", 4608, 3584), ("o", 3584, 3584), ("gate_up", 37888, 3584),
+                       ("down", 3584, 18944)):
+        per = n * k // 32 * 18
+        copies = int(np.ceil(1.25 * MALL_BYTES / per))
+        tile = L.si_q4_tile(n, k)
+        mats = []
+        for _ in range(copies):
+            qs = torch.randint(0, 256, (n * k // 2,), generator=gen, device="cuda",
+                               dtype=torch.uint8)
+            d = torch.full((L.si_q4_scale_count(n, k, tile),), 0x2000, dtype=torch.int16,
+                           device="cuda")
+            mats.append((qs, d))
+        xq = torch.randint(-127, 128, (k,), generator=gen, device="cuda", dtype=torch.int8)
+        xd = torch.full((k // 32,), 0x2c00, dtype=torch.int16, device="cuda")
+        xs = xq.view(-1, 32).sum(1, dtype=torch.int32).to(torch.int16)
+        out = torch.empty(n, device="cuda")
+
+        def launch(i):
+            qs, d = mats[i % copies]
+            rc = L.si_matvec_q4q8(si_amd.ptr(qs), si_amd.ptr(d), tile, n, k, si_amd.ptr(xq),
+                                  si_amd.ptr(xd), si_amd.ptr(xs), None, None, si_amd.ptr(out), 0,
+                                  si_amd.stream_handle(torch.cuda.current_stream()))
+            if rc:
+                raise si_amd.SiError(rc, L.si_last_error().decode())
+
+        with torch.cuda.stream(stream):
+            for i in range(copies + 5):
+                launch(i)
+        torch.cuda.synchronize()
+        ms = graph_time_ms(torch, stream, launch, launches, replays=2)
+        alg = per + k + (k // 32) * 4 + n * 4
+        gbs = alg / (ms * 1e-3) / 1e9
+        res[name] = dict(n=n, k=k, tile=tile, us=round(ms * 1e3, 3), gbs=round(gbs, 1),
+                         hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
+        del mats
+        torch.cuda.empty_cache()
+    return res
 
 
 def bench_prefill(torch, si_amd, stream, shape_name, ntok, steps):
@@ -413,6 +457,9 @@ def main():
     dom = bench_dominant_gemv(torch, si_amd, stream, ctxobj)
     log(f"  {dom['us']:.2f} us/launch, {dom['achieved_gbs']:.1f} GB/s")
     extra = {}
+    log("7B decode projections (k_matvec) ...")
+    extra["gemv_7b_cold"] = bench_gemv_7b(torch, si_amd, stream)
+    log(f"  {extra['gemv_7b_cold']}")
     if not args.quick:
         log("config 1: QKV GEMV ...")
         extra["cfg1_qkv_gemv_0.5b"] = bench_qkv_gemv(torch, si_amd, stream)

@@ -8,7 +8,7 @@
  *   - plain C types only: device pointers, sizes, an opaque stream handle
  *     (a hipStream_t passed as void*; NULL = the default stream);
  *   - the caller owns every buffer (as in the reference); nothing here
- *     allocates device memory except si_layer_create / si_layer_destroy;
+ *     allocates device memory except the layer and workspace create calls;
  *   - shapes are runtime values (si_shape_t) instead of defines.h:16-25;
  *   - every call returns 0 on success or an SI_ERR_* code, with a message in
  *     si_last_error(); the reference's die() (qwen_one_layer.c:26-28) is the
@@ -19,8 +19,12 @@
  *   Q4_0 weights (the reference's row-major [N][K/32] 18-byte blocks,
  *   repack_weights.py:43-52) are repacked losslessly once (si_q4_repack) into
  *       qs : uint8  [K/32][N][16]   byte j = element j | element j+16 << 4
- *       d  : uint16 [K/32][N]       fp16 scale bits
- *   so one wavefront reads 64 rows x 16 B of one block as 1 KiB contiguous.
+ *       d  : uint16 [N/tile][K/32][tile]  fp16 scale bits, tile-major
+ *   so a wavefront reads consecutive rows of one block as one contiguous run
+ *   of 16 B each, and the scales of a workgroup's `tile` rows form one run
+ *   per block that no other workgroup reads.  tile is 8, 16, 32 or 64
+ *   (si_q4_tile gives the mat-vec's choice for a shape); d holds
+ *   si_q4_scale_count(n, k, tile) entries (N rounded up to the tile).
  *   Q8_0 activations are planar:
  *       qs : int8   [M][K]          d : uint16 [M][K/32]
  *       s  : int16  [M][K/32]       sum of the block's 32 int8 values
@@ -68,10 +72,14 @@ typedef struct si_shape {
 
 /* Lossless row-major Q4_0 -> device repack.  Replaces the role of
  * repack_weights.py:43-52 (a lossless target-specific relayout). */
-int si_q4_repack(const uint8_t *src_rowmajor, int n, int k, uint8_t *qs,
+int si_q4_repack(const uint8_t *src_rowmajor, int n, int k, int tile, uint8_t *qs,
                  uint16_t *d, void *stream);
+/* Scale tile the mat-vec uses for an n x k matrix (its rows per workgroup). */
+int si_q4_tile(int n, int k);
+/* Entries of the scale array d for an n x k matrix with a given tile. */
+size_t si_q4_scale_count(int n, int k, int tile);
 /* Inverse of si_q4_repack (round-trip check, repack_weights.py:126-137). */
-int si_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k,
+int si_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k, int tile,
                  uint8_t *dst_rowmajor, void *stream);
 
 /* ------------------------------------------------------------------ */
@@ -97,21 +105,20 @@ int si_q4q8_block_dots(const uint8_t *wqs, const uint16_t *wd, int n, int k,
                        const int8_t *xqs, const int16_t *xs, int32_t *dots,
                        void *stream);
 
+enum { SI_GEMM_EXACT = 1 }; /* flags of si_matvec_q4q8 / si_gemm_q4q8 */
+
 /* matvec_q4q8 (qwen_one_layer.c:148-162), one activation row:
  *   out[r] = residual[r] + (bias[r] + sum_b ((float)dot_b * w.d) * x.d)
- * bias and residual may be NULL.  With splits == 1 the blocks of a row are
- * accumulated in order with the reference's rounding (bit-exact); splits > 1
- * divides K into that many contiguous ranges for parallelism; the range sums
- * are then added in range order inside the same kernel (within fp32 rounding
- * of the reference).  splits > 1 needs a workspace of
- * si_matvec_workspace(n, k, splits) bytes whose contents are zero before its
- * first use; every call leaves it ready for the next (calls sharing one
- * workspace must not run concurrently). */
-int si_matvec_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k,
+ * bias and residual may be NULL; wqs and xqs 16-byte aligned.  With
+ * flags & SI_GEMM_EXACT the blocks of a row are accumulated in order with
+ * the reference's rounding (bit-exact); otherwise K is spread over the
+ * threads of a workgroup and the partial sums are added in a fixed order
+ * (deterministic, within fp32 rounding of the reference).  A workgroup
+ * owns `tile` rows (at most 64), the tile the weights were repacked with. */
+int si_matvec_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
                    const int8_t *xqs, const uint16_t *xd, const int16_t *xs,
                    const float *bias, const float *residual, float *out,
-                   int splits, void *workspace, void *stream);
-size_t si_matvec_workspace(int n, int k, int splits);
+                   int flags, void *stream);
 
 /* matvec_q4q8 applied to m activation rows (prefill / batched decode):
  * out[i][r] (row stride ldo; residual uses the same stride) =
@@ -120,8 +127,7 @@ size_t si_matvec_workspace(int n, int k, int splits);
  * reference's rounding sequence (flags & SI_GEMM_EXACT: bit-exact with
  * matvec_q4q8) or uses one fused multiply-add per block (within fp32
  * rounding of the reference). */
-enum { SI_GEMM_EXACT = 1 };
-int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k,
+int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
                  const int8_t *xqs, const uint16_t *xd, int m,
                  const float *bias, const float *residual, float *out, int ldo,
                  int flags, void *stream);
@@ -167,6 +173,12 @@ size_t si_attention_workspace(const si_shape_t *s, int nq, int max_ctx);
  * (fp32 [16][16] row-major).  No counterpart in the reference. */
 int si_debug_mfma_f16(const void *a, const void *b, float *d32, float *d16, void *stream);
 
+/* Test entry for the cross-lane moves the kernels' reductions use (DPP
+ * quad_perm / row_ror / row_half_mirror, v_permlane16/32_swap): each lane
+ * of one wavefront feeds its index; out[k*64 + lane] (18 x 64 ints) is what
+ * lane received from operation k.  No counterpart in the reference. */
+int si_debug_lane_ops(int *out, void *stream);
+
 /* Build-defined SwiGLU + quantize_q8: act = silu(gate)*up with
  * silu(g) = g/(1+expf(-g)); gate = gu[r][0..f), up = gu[r][f..2f). */
 int si_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs,
@@ -192,13 +204,26 @@ typedef struct si_layer_host {
     const uint8_t *wgate, *wup, *wdown;
 } si_layer_host_t;
 
-typedef struct si_layer si_layer_t; /* opaque: device weights + workspaces */
+typedef struct si_layer si_layer_t; /* opaque: device weights + a workspace */
+typedef struct si_workspace si_workspace_t; /* opaque: activations, partials, RoPE */
 
-/* Uploads and repacks the weights, builds RoPE tables for max_pos
- * positions and sizes workspaces for up to max_tokens rows per call.
- * The only calls that allocate device memory. */
+/* A workspace: activation buffers for up to max_tokens rows per call,
+ * attention partials and RoPE tables for max_pos positions: the intermediate
+ * vectors run_layer keeps on its stack (qwen_one_layer.c:242-243).  Layers of
+ * one model may share one; calls on layers sharing a workspace must not run
+ * concurrently.  The memory is released when the workspace handle and every
+ * layer using it are gone. */
+int si_workspace_create(const si_shape_t *s, int max_tokens, int max_pos,
+                        si_workspace_t **out);
+int si_workspace_destroy(si_workspace_t *ws);
+
+/* Uploads and repacks the weights (load_layer, qwen_one_layer.c:210-221,
+ * plus the build's FFN weights).  si_layer_create also creates a private
+ * workspace; si_layer_create_in uses a shared one.  With the workspace calls,
+ * the only calls that allocate device memory. */
 int si_layer_create(const si_shape_t *s, const si_layer_host_t *w, int max_tokens,
                     int max_pos, si_layer_t **out);
+int si_layer_create_in(si_workspace_t *ws, const si_layer_host_t *w, si_layer_t **out);
 int si_layer_destroy(si_layer_t *l);
 
 enum {
@@ -271,7 +296,7 @@ int si_layer_phase_ms(si_layer_t *l, float *ms);
 /* Device weights of a created layer, for kernel-level benchmarks:
  * which = 0 QKV (fused rows q|k|v), 1 O, 2 gate|up, 3 down. */
 int si_layer_weights(si_layer_t *l, int which, const uint8_t **qs,
-                     const uint16_t **d, int *n, int *k);
+                     const uint16_t **d, int *tile, int *n, int *k);
 
 #ifdef __cplusplus
 }

@@ -10,10 +10,13 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <memory>
 #include <string>
 #include <vector>
 
 #include "../../include/si_abi.h"
+#include "si_device.hpp"
+#include "si_gemv.hpp"
 #include "si_kernels.hpp"
 
 using namespace si;
@@ -67,17 +70,33 @@ extern "C" {
 
 const char *si_last_error(void) { return g_err.c_str(); }
 
-int si_q4_repack(const uint8_t *src, int n, int k, uint8_t *qs, uint16_t *d, void *stream) {
+static bool tile_ok(int tile) { return tile == 8 || tile == 16 || tile == 32 || tile == 64; }
+
+int si_q4_tile(int n, int k) {
+    (void)k;
+    return n > 0 ? gemv_tile_for(n) : 8;
+}
+
+size_t si_q4_scale_count(int n, int k, int tile) {
+    if (n <= 0 || k <= 0 || k % 32 || !tile_ok(tile)) return 0;
+    return q4_scale_count(n, k / 32, tile);
+}
+
+int si_q4_repack(const uint8_t *src, int n, int k, int tile, uint8_t *qs, uint16_t *d,
+                 void *stream) {
     SI_REQUIRE(n > 0 && k > 0 && k % 32 == 0, "repack: bad size n=%d k=%d", n, k);
+    SI_REQUIRE(tile_ok(tile), "repack: tile %d not 8, 16, 32 or 64", tile);
     SI_REQUIRE(src && qs && d, "repack: NULL pointer");
-    launch_q4_repack(src, n, k, qs, d, S(stream));
+    launch_q4_repack(src, n, k, tile, qs, d, S(stream));
     return check_launch("si_q4_repack");
 }
 
-int si_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k, uint8_t *dst, void *stream) {
+int si_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k, int tile, uint8_t *dst,
+                 void *stream) {
     SI_REQUIRE(n > 0 && k > 0 && k % 32 == 0, "unpack: bad size n=%d k=%d", n, k);
+    SI_REQUIRE(tile_ok(tile), "unpack: tile %d not 8, 16, 32 or 64", tile);
     SI_REQUIRE(dst && qs && d, "unpack: NULL pointer");
-    launch_q4_unpack(qs, d, n, k, dst, S(stream));
+    launch_q4_unpack(qs, d, n, k, tile, dst, S(stream));
     return check_launch("si_q4_unpack");
 }
 
@@ -123,35 +142,30 @@ int si_q4q8_block_dots(const uint8_t *wqs, const uint16_t *wd, int n, int k, con
     return check_launch("si_q4q8_block_dots");
 }
 
-size_t si_matvec_workspace(int n, int k, int splits) {
-    if (n <= 0 || k <= 0 || k % 32) return 0;
-    return gemv_workspace_bytes(n, k, splits);
-}
-
-int si_matvec_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k, const int8_t *xqs,
-                   const uint16_t *xd, const int16_t *xs, const float *bias,
-                   const float *residual, float *out, int splits, void *workspace,
-                   void *stream) {
-    SI_REQUIRE(n > 0 && k > 0 && k % 32 == 0 && n <= 262144, "matvec: bad size n=%d k=%d", n,
-               k);
+int si_matvec_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
+                   const int8_t *xqs, const uint16_t *xd, const int16_t *xs, const float *bias,
+                   const float *residual, float *out, int flags, void *stream) {
+    SI_REQUIRE(n > 0 && k > 0 && k % 32 == 0, "matvec: bad size n=%d k=%d", n, k);
+    SI_REQUIRE(tile_ok(tile), "matvec: tile %d not 8, 16, 32 or 64", tile);
     SI_REQUIRE(wqs && wd && xqs && xd && xs && out, "matvec: NULL pointer");
-    SI_REQUIRE(splits >= 1, "matvec: splits must be >= 1");
-    SI_REQUIRE(gemv_effective_splits(k, splits) == 1 || workspace,
-               "matvec: splits > 1 needs a workspace");
-    launch_gemv_q4q8(wqs, wd, n, k, xqs, xd, xs, bias, residual, out, splits, workspace,
-                     S(stream));
+    SI_REQUIRE(((uintptr_t)wqs & 15) == 0 && ((uintptr_t)xqs & 15) == 0,
+               "matvec: wqs and xqs must be 16-byte aligned");
+    SI_REQUIRE((flags & ~SI_GEMM_EXACT) == 0, "matvec: unknown flags %d", flags);
+    launch_matvec(xqs, xd, xs, k, wqs, wd, tile, n, bias, residual, out,
+                  (flags & SI_GEMM_EXACT) != 0, S(stream));
     return check_launch("si_matvec_q4q8");
 }
 
-int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k, const int8_t *xqs,
-                 const uint16_t *xd, int m, const float *bias, const float *residual,
-                 float *out, int ldo, int flags, void *stream) {
+int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
+                 const int8_t *xqs, const uint16_t *xd, int m, const float *bias,
+                 const float *residual, float *out, int ldo, int flags, void *stream) {
     SI_REQUIRE(n > 0 && k > 0 && k % 32 == 0 && m >= 0, "gemm: bad size m=%d n=%d k=%d", m, n,
                k);
+    SI_REQUIRE(tile_ok(tile), "gemm: tile %d not 8, 16, 32 or 64", tile);
     SI_REQUIRE(ldo >= n, "gemm: ldo %d < n %d", ldo, n);
     SI_REQUIRE(m == 0 || (wqs && wd && xqs && xd && out), "gemm: NULL pointer");
     SI_REQUIRE((flags & ~SI_GEMM_EXACT) == 0, "gemm: unknown flags %d", flags);
-    launch_gemm_q4q8(wqs, wd, n, k, xqs, xd, m, bias, residual, out, ldo,
+    launch_gemm_q4q8(wqs, wd, tile, n, k, xqs, xd, m, bias, residual, out, ldo,
                      (flags & SI_GEMM_EXACT) != 0, S(stream));
     return check_launch("si_gemm_q4q8");
 }
@@ -215,6 +229,12 @@ int si_attention(const si_shape_t *s, const float *q, int nq, const uint16_t *kc
     return check_launch("si_attention");
 }
 
+int si_debug_lane_ops(int *out, void *stream) {
+    SI_REQUIRE(out, "debug_lane_ops: NULL pointer");
+    launch_debug_lane_ops(out, S(stream));
+    return check_launch("si_debug_lane_ops");
+}
+
 int si_debug_mfma_f16(const void *a, const void *b, float *d32, float *d16, void *stream) {
     SI_REQUIRE(a && b && d32 && d16, "debug_mfma: NULL pointer");
     launch_debug_mfma_f16(a, b, d32, d16, S(stream));
@@ -237,7 +257,7 @@ int si_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs, uint1
 struct Q4Dev {
     uint8_t *qs = nullptr;
     uint16_t *d = nullptr;
-    int n = 0, k = 0;
+    int n = 0, k = 0, tile = 8;
 };
 
 struct Q8Buf {
@@ -246,27 +266,144 @@ struct Q8Buf {
     int16_t *s = nullptr;
 };
 
+// Device allocations owned by one object, released with it.
+struct DevArena {
+    std::vector<void *> allocs;
+    DevArena() = default;
+    DevArena(const DevArena &) = delete;
+    DevArena &operator=(const DevArena &) = delete;
+    ~DevArena() {
+        for (void *p : allocs) (void)hipFree(p);
+    }
+    template <typename T>
+    int alloc(T **p, size_t count) {
+        *p = nullptr;
+        if (count == 0) return SI_OK;
+        void *q = nullptr;
+        if (hipMalloc(&q, count * sizeof(T)) != hipSuccess)
+            return fail(SI_ERR_NOMEM, "hipMalloc(%zu bytes) failed", count * sizeof(T));
+        allocs.push_back(q);
+        *p = (T *)q;
+        return SI_OK;
+    }
+};
+
+#define TRY(x)               \
+    do {                     \
+        int r_ = (x);        \
+        if (r_) return r_;   \
+    } while (0)
+
+// Activation buffers, attention partials and RoPE tables: everything a
+// layer call uses besides its weights and the KV cache.  Layers of one
+// model can share one workspace (they run one after another on a stream).
+struct Workspace {
+    si_shape_t s;
+    int max_tokens = 0, max_pos = 0;
+    bool ffn = false;
+    DevArena mem;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    float *normed = nullptr, *qkv = nullptr, *q = nullptr, *attn = nullptr;
+    float *attn_out = nullptr, *h = nullptr, *normed2 = nullptr, *gu = nullptr, *act = nullptr;
+    Q8Buf xq, attq, xq2, actq;
+    void *attn_ws = nullptr;
+    size_t attn_ws_bytes = 0;
+};
+
+struct si_workspace {
+    std::shared_ptr<Workspace> p;
+};
+
+static int upload_f32(DevArena &mem, float **dst, const float *src, size_t n) {
+    *dst = nullptr;
+    if (!src) return SI_OK;
+    TRY(mem.alloc(dst, n));
+    HIP_TRY(hipMemcpy(*dst, src, n * sizeof(float), hipMemcpyHostToDevice));
+    return SI_OK;
+}
+
+static int make_workspace(const si_shape_t *s, int max_tokens, int max_pos,
+                          std::shared_ptr<Workspace> *out) {
+    TRY(check_shape(s));
+    SI_REQUIRE(max_tokens >= 1 && max_pos >= 1, "workspace: bad max_tokens/max_pos");
+    auto W = std::make_shared<Workspace>();
+    W->s = *s;
+    W->max_tokens = max_tokens;
+    W->max_pos = max_pos;
+    W->ffn = s->ffn > 0;
+    const int H = s->hidden, QD = s->qheads * s->hdim, KVD = s->kvheads * s->hdim, F = s->ffn;
+    const int NQKV = QD + 2 * KVD;
+    const size_t M = max_tokens, MH = M * H;
+    DevArena &m = W->mem;
+    {
+        const size_t te = (size_t)max_pos * (s->hdim / 2);
+        std::vector<float> c(te), sn(te);
+        si_rope_table(max_pos, s->hdim, s->rope_base, c.data(), sn.data());
+        TRY(upload_f32(m, &W->rope_cos, c.data(), te));
+        TRY(upload_f32(m, &W->rope_sin, sn.data(), te));
+    }
+    TRY(m.alloc(&W->normed, MH));
+    TRY(m.alloc(&W->qkv, M * NQKV));
+    TRY(m.alloc(&W->q, M * QD));
+    TRY(m.alloc(&W->attn, M * QD));
+    TRY(m.alloc(&W->attn_out, MH));
+    TRY(m.alloc(&W->xq.qs, MH));
+    TRY(m.alloc(&W->xq.d, MH / 32));
+    TRY(m.alloc(&W->xq.s, MH / 32));
+    TRY(m.alloc(&W->attq.qs, M * QD));
+    TRY(m.alloc(&W->attq.d, M * QD / 32));
+    TRY(m.alloc(&W->attq.s, M * QD / 32));
+    if (W->ffn) {
+        TRY(m.alloc(&W->h, MH));
+        TRY(m.alloc(&W->normed2, MH));
+        TRY(m.alloc(&W->gu, M * 2 * F));
+        TRY(m.alloc(&W->act, M * F));
+        TRY(m.alloc(&W->xq2.qs, MH));
+        TRY(m.alloc(&W->xq2.d, MH / 32));
+        TRY(m.alloc(&W->xq2.s, MH / 32));
+        TRY(m.alloc(&W->actq.qs, M * F));
+        TRY(m.alloc(&W->actq.d, M * F / 32));
+        TRY(m.alloc(&W->actq.s, M * F / 32));
+    }
+    // attention partials: the split count depends on the row count, so the
+    // size is the worst case over 1..max_tokens rows of either schedule
+    for (int nq = 1; nq <= max_tokens; ++nq) {
+        size_t b = si_attention_workspace(s, nq, max_pos);
+        const size_t bd = dec_attn_workspace_bytes(s->qheads, s->hdim, s->kvheads, nq, max_pos);
+        if (bd > b) b = bd;
+        if (b > W->attn_ws_bytes) W->attn_ws_bytes = b;
+    }
+    uint8_t *ws = nullptr;
+    TRY(m.alloc(&ws, W->attn_ws_bytes));
+    W->attn_ws = ws;
+    *out = std::move(W);
+    return SI_OK;
+}
+
 struct si_layer {
     si_shape_t s;
     int max_tokens = 0, max_pos = 0;
     bool ffn = false;
+    DevArena mem;  // weights
     Q4Dev wqkv, wo, wgu, wdown;
     float *norm = nullptr, *bqkv = nullptr, *post_norm = nullptr;
+    std::shared_ptr<Workspace> ws;
+    // views of the workspace buffers
     float *rope_cos = nullptr, *rope_sin = nullptr;
-    // workspaces, sized for max_tokens rows
     float *normed = nullptr, *qkv = nullptr, *q = nullptr, *attn = nullptr;
     float *attn_out = nullptr, *h = nullptr, *normed2 = nullptr, *gu = nullptr, *act = nullptr;
     Q8Buf xq, attq, xq2, actq;
-    void *gemv_ws = nullptr;  // split-K partials + arrival counters (kept zeroed)
-    size_t gemv_ws_bytes = 0;
     void *attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
-    std::vector<void *> allocs;
     // phase timing: events[i] marks the start of phase i, events[COUNT] the end
     bool timing = false;
     hipEvent_t events[SI_PHASE_COUNT + 1] = {};
     bool phase_hit[SI_PHASE_COUNT] = {};
     int last_phase = -1;
+    ~si_layer() {
+        for (hipEvent_t &e : events)
+            if (e) (void)hipEventDestroy(e);
+    }
 };
 
 static void mark(si_layer *L, int phase, hipStream_t st) {
@@ -276,34 +413,17 @@ static void mark(si_layer *L, int phase, hipStream_t st) {
     L->last_phase = phase;
 }
 
-template <typename T>
-static int dev_alloc(si_layer *L, T **p, size_t count) {
-    *p = nullptr;
-    if (count == 0) return SI_OK;
-    void *q = nullptr;
-    if (hipMalloc(&q, count * sizeof(T)) != hipSuccess)
-        return fail(SI_ERR_NOMEM, "hipMalloc(%zu bytes) failed", count * sizeof(T));
-    L->allocs.push_back(q);
-    *p = (T *)q;
-    return SI_OK;
-}
-
-#define TRY(x)               \
-    do {                     \
-        int r_ = (x);        \
-        if (r_) return r_;   \
-    } while (0)
-
 // Uploads row-major Q4_0 matrices stacked along N and repacks them.
-static int upload_q4(si_layer *L, Q4Dev *w, const std::vector<const uint8_t *> &parts,
-                     const std::vector<int> &rows, int k) {
+static int upload_q4(DevArena &mem, Q4Dev *w, const std::vector<const uint8_t *> &parts,
+                     const std::vector<int> &rows, int k, int tile) {
     int n = 0;
     for (int r : rows) n += r;
     const size_t row_bytes = (size_t)(k / 32) * 18;
     w->n = n;
     w->k = k;
-    TRY(dev_alloc(L, &w->qs, (size_t)n * k / 2));
-    TRY(dev_alloc(L, &w->d, (size_t)n * (k / 32)));
+    w->tile = tile;
+    TRY(mem.alloc(&w->qs, (size_t)n * k / 2));
+    TRY(mem.alloc(&w->d, q4_scale_count(n, k / 32, tile)));
     uint8_t *tmp = nullptr;
     HIP_TRY(hipMalloc(&tmp, (size_t)n * row_bytes));
     size_t off = 0;
@@ -315,154 +435,110 @@ static int upload_q4(si_layer *L, Q4Dev *w, const std::vector<const uint8_t *> &
         }
         off += rows[i] * row_bytes;
     }
-    launch_q4_repack(tmp, n, k, w->qs, w->d, 0);
+    launch_q4_repack(tmp, n, k, tile, w->qs, w->d, 0);
     hipError_t e = hipDeviceSynchronize();
     (void)hipFree(tmp);
     if (e != hipSuccess) return fail(SI_ERR_HIP, "repack: %s", hipGetErrorString(e));
     return SI_OK;
 }
 
-static int upload_f32(si_layer *L, float **dst, const float *src, size_t n) {
-    *dst = nullptr;
-    if (!src) return SI_OK;
-    TRY(dev_alloc(L, dst, n));
-    HIP_TRY(hipMemcpy(*dst, src, n * sizeof(float), hipMemcpyHostToDevice));
+// Argument checks of a layer's host weights, before anything is allocated.
+static int check_host(const si_shape_t *s, const si_layer_host_t *w, si_layer_t **out) {
+    TRY(check_shape(s));
+    SI_REQUIRE(w && out, "layer_create: NULL pointer");
+    SI_REQUIRE(w->wq && w->wk && w->wv && w->wo, "layer_create: wq/wk/wv/wo are required");
+    const bool ffn = w->wgate || w->wup || w->wdown;
+    SI_REQUIRE(!ffn || (w->wgate && w->wup && w->wdown && s->ffn > 0),
+               "layer_create: FFN needs wgate, wup, wdown and shape.ffn > 0");
     return SI_OK;
 }
 
-static void free_layer(si_layer *L) {
-    for (void *p : L->allocs) (void)hipFree(p);
-    L->allocs.clear();
-    for (hipEvent_t &e : L->events)
-        if (e) {
-            (void)hipEventDestroy(e);
-            e = nullptr;
-        }
-}
-
-// K-range splits for a decode mat-vec: enough wavefronts to cover the chip
-// (>= ~512 row-tile x range pairs) while keeping >= 4 blocks per range.
-static int decode_splits(const si_layer *L, int n, int k, int flags) {
-    if (flags & SI_LAYER_EXACT) return 1;
-    const int tiles = (n + 63) / 64;
-    const int nb = k / 32;
-    int sp = (512 + tiles - 1) / tiles;
-    if (sp > nb / 4) sp = nb / 4;
-    if (sp < 1) sp = 1;
-    (void)L;
-    return gemv_effective_splits(k, sp);
+static int build_layer(const si_layer_host_t *w, std::shared_ptr<Workspace> W,
+                       si_layer_t **out) {
+    const si_shape_t *s = &W->s;
+    TRY(check_host(s, w, out));
+    const bool ffn = w->wgate || w->wup || w->wdown;
+    std::unique_ptr<si_layer> L(new si_layer());
+    L->s = *s;
+    L->max_tokens = W->max_tokens;
+    L->max_pos = W->max_pos;
+    L->ffn = ffn;
+    const int H = s->hidden, QD = s->qheads * s->hdim, KVD = s->kvheads * s->hdim, F = s->ffn;
+    const int NQKV = QD + 2 * KVD;
+    // scale tiles: the decode mat-vec's rows per workgroup; gate|up pairs 32
+    // gate with 32 up rows per workgroup (tile 32)
+    TRY(upload_q4(L->mem, &L->wqkv, {w->wq, w->wk, w->wv}, {QD, KVD, KVD}, H,
+                  gemv_tile_for(NQKV)));
+    TRY(upload_q4(L->mem, &L->wo, {w->wo}, {H}, QD, gemv_tile_for(H)));
+    if (ffn) {
+        TRY(upload_q4(L->mem, &L->wgu, {w->wgate, w->wup}, {F, F}, H, 32));
+        TRY(upload_q4(L->mem, &L->wdown, {w->wdown}, {H}, F, gemv_tile_for(H)));
+    }
+    TRY(upload_f32(L->mem, &L->norm, w->norm, H));
+    TRY(upload_f32(L->mem, &L->post_norm, w->post_norm, H));
+    if (w->bq || w->bk || w->bv) {
+        std::vector<float> b(NQKV, 0.0f);  // absent bias = zero (qwen_one_layer.c:154)
+        if (w->bq) memcpy(b.data(), w->bq, QD * sizeof(float));
+        if (w->bk) memcpy(b.data() + QD, w->bk, KVD * sizeof(float));
+        if (w->bv) memcpy(b.data() + QD + KVD, w->bv, KVD * sizeof(float));
+        TRY(upload_f32(L->mem, &L->bqkv, b.data(), NQKV));
+    }
+    L->rope_cos = W->rope_cos;
+    L->rope_sin = W->rope_sin;
+    L->normed = W->normed;
+    L->qkv = W->qkv;
+    L->q = W->q;
+    L->attn = W->attn;
+    L->attn_out = W->attn_out;
+    L->h = W->h;
+    L->normed2 = W->normed2;
+    L->gu = W->gu;
+    L->act = W->act;
+    L->xq = W->xq;
+    L->attq = W->attq;
+    L->xq2 = W->xq2;
+    L->actq = W->actq;
+    L->attn_ws = W->attn_ws;
+    L->attn_ws_bytes = W->attn_ws_bytes;
+    L->ws = std::move(W);
+    *out = L.release();
+    return SI_OK;
 }
 
 extern "C" {
 
+int si_workspace_create(const si_shape_t *s, int max_tokens, int max_pos,
+                        si_workspace_t **out) {
+    SI_REQUIRE(out, "workspace_create: NULL pointer");
+    std::shared_ptr<Workspace> W;
+    TRY(make_workspace(s, max_tokens, max_pos, &W));
+    *out = new si_workspace{std::move(W)};
+    return SI_OK;
+}
+
+int si_workspace_destroy(si_workspace_t *ws) {
+    if (!ws) return SI_OK;
+    (void)hipDeviceSynchronize();
+    delete ws;  // the memory goes when the last layer using it is destroyed
+    return SI_OK;
+}
+
 int si_layer_create(const si_shape_t *s, const si_layer_host_t *w, int max_tokens, int max_pos,
                     si_layer_t **out) {
-    TRY(check_shape(s));
-    SI_REQUIRE(w && out, "layer_create: NULL pointer");
-    SI_REQUIRE(w->wq && w->wk && w->wv && w->wo, "layer_create: wq/wk/wv/wo are required");
-    SI_REQUIRE(max_tokens >= 1 && max_pos >= 1, "layer_create: bad max_tokens/max_pos");
-    const bool ffn = w->wgate || w->wup || w->wdown;
-    SI_REQUIRE(!ffn || (w->wgate && w->wup && w->wdown && s->ffn > 0),
-               "layer_create: FFN needs wgate, wup, wdown and shape.ffn > 0");
-    si_layer *L = new si_layer();
-    L->s = *s;
-    L->max_tokens = max_tokens;
-    L->max_pos = max_pos;
-    L->ffn = ffn;
-    const int H = s->hidden, QD = s->qheads * s->hdim, KVD = s->kvheads * s->hdim, F = s->ffn;
-    const int NQKV = QD + 2 * KVD;
-    const int M = max_tokens;
-    int r = SI_OK;
-    do {
-        if ((r = upload_q4(L, &L->wqkv, {w->wq, w->wk, w->wv}, {QD, KVD, KVD}, H))) break;
-        if ((r = upload_q4(L, &L->wo, {w->wo}, {H}, QD))) break;
-        if (ffn) {
-            if ((r = upload_q4(L, &L->wgu, {w->wgate, w->wup}, {F, F}, H))) break;
-            if ((r = upload_q4(L, &L->wdown, {w->wdown}, {H}, F))) break;
-        }
-        if ((r = upload_f32(L, &L->norm, w->norm, H))) break;
-        if ((r = upload_f32(L, &L->post_norm, w->post_norm, H))) break;
-        if (w->bq || w->bk || w->bv) {
-            std::vector<float> b(NQKV, 0.0f);  // absent bias = zero (qwen_one_layer.c:154)
-            if (w->bq) memcpy(b.data(), w->bq, QD * sizeof(float));
-            if (w->bk) memcpy(b.data() + QD, w->bk, KVD * sizeof(float));
-            if (w->bv) memcpy(b.data() + QD + KVD, w->bv, KVD * sizeof(float));
-            if ((r = upload_f32(L, &L->bqkv, b.data(), NQKV))) break;
-        }
-        {
-            const size_t te = (size_t)max_pos * (s->hdim / 2);
-            std::vector<float> c(te), sn(te);
-            si_rope_table(max_pos, s->hdim, s->rope_base, c.data(), sn.data());
-            if ((r = upload_f32(L, &L->rope_cos, c.data(), te))) break;
-            if ((r = upload_f32(L, &L->rope_sin, sn.data(), te))) break;
-        }
-        const size_t MH = (size_t)M * H;
-        if ((r = dev_alloc(L, &L->normed, MH))) break;
-        if ((r = dev_alloc(L, &L->qkv, (size_t)M * NQKV))) break;
-        if ((r = dev_alloc(L, &L->q, (size_t)M * QD))) break;
-        if ((r = dev_alloc(L, &L->attn, (size_t)M * QD))) break;
-        if ((r = dev_alloc(L, &L->attn_out, MH))) break;
-        if ((r = dev_alloc(L, &L->xq.qs, MH))) break;
-        if ((r = dev_alloc(L, &L->xq.d, MH / 32))) break;
-        if ((r = dev_alloc(L, &L->xq.s, MH / 32))) break;
-        if ((r = dev_alloc(L, &L->attq.qs, (size_t)M * QD))) break;
-        if ((r = dev_alloc(L, &L->attq.d, (size_t)M * QD / 32))) break;
-        if ((r = dev_alloc(L, &L->attq.s, (size_t)M * QD / 32))) break;
-        if (ffn) {
-            if ((r = dev_alloc(L, &L->h, MH))) break;
-            if ((r = dev_alloc(L, &L->normed2, MH))) break;
-            if ((r = dev_alloc(L, &L->gu, (size_t)M * 2 * F))) break;
-            if ((r = dev_alloc(L, &L->act, (size_t)M * F))) break;
-            if ((r = dev_alloc(L, &L->xq2.qs, MH))) break;
-            if ((r = dev_alloc(L, &L->xq2.d, MH / 32))) break;
-            if ((r = dev_alloc(L, &L->xq2.s, MH / 32))) break;
-            if ((r = dev_alloc(L, &L->actq.qs, (size_t)M * F))) break;
-            if ((r = dev_alloc(L, &L->actq.d, (size_t)M * F / 32))) break;
-            if ((r = dev_alloc(L, &L->actq.s, (size_t)M * F / 32))) break;
-        }
-        // decode mat-vec workspace: the largest need over the four matrices
-        size_t gb = 0;
-        const Q4Dev *mats[4] = {&L->wqkv, &L->wo, &L->wgu, &L->wdown};
-        for (const Q4Dev *m : mats)
-            if (m->n) {
-                const size_t e = gemv_workspace_bytes(m->n, m->k, decode_splits(L, m->n, m->k, 0));
-                if (e > gb) gb = e;
-            }
-        L->gemv_ws_bytes = gb;
-        {
-            uint8_t *ws = nullptr;
-            if ((r = dev_alloc(L, &ws, gb))) break;
-            L->gemv_ws = ws;
-            if (gb && hipMemset(ws, 0, gb) != hipSuccess) {
-                r = fail(SI_ERR_HIP, "hipMemset(gemv workspace) failed");
-                break;
-            }
-        }
-        // the split count depends on the row count: size for the worst one
-        L->attn_ws_bytes = 0;
-        for (int nq = 1; nq <= M; ++nq) {
-            const size_t b = si_attention_workspace(s, nq, max_pos);
-            if (b > L->attn_ws_bytes) L->attn_ws_bytes = b;
-        }
-        {
-            uint8_t *ws = nullptr;
-            if ((r = dev_alloc(L, &ws, L->attn_ws_bytes))) break;
-            L->attn_ws = ws;
-        }
-    } while (0);
-    if (r) {
-        free_layer(L);
-        delete L;
-        return r;
-    }
-    *out = L;
-    return SI_OK;
+    TRY(check_host(s, w, out));
+    std::shared_ptr<Workspace> W;
+    TRY(make_workspace(s, max_tokens, max_pos, &W));
+    return build_layer(w, std::move(W), out);
+}
+
+int si_layer_create_in(si_workspace_t *ws, const si_layer_host_t *w, si_layer_t **out) {
+    SI_REQUIRE(ws && ws->p, "layer_create_in: NULL workspace");
+    return build_layer(w, ws->p, out);
 }
 
 int si_layer_destroy(si_layer_t *L) {
     if (!L) return SI_OK;
     (void)hipDeviceSynchronize();
-    free_layer(L);
     delete L;
     return SI_OK;
 }
@@ -517,14 +593,15 @@ int si_layer_phase_ms(si_layer_t *L, float *ms) {
     return SI_OK;
 }
 
-int si_layer_weights(si_layer_t *L, int which, const uint8_t **qs, const uint16_t **d, int *n,
-                     int *k) {
-    SI_REQUIRE(L && qs && d && n && k, "layer_weights: NULL pointer");
+int si_layer_weights(si_layer_t *L, int which, const uint8_t **qs, const uint16_t **d,
+                     int *tile, int *n, int *k) {
+    SI_REQUIRE(L && qs && d && tile && n && k, "layer_weights: NULL pointer");
     const Q4Dev *w = which == 0 ? &L->wqkv : which == 1 ? &L->wo : which == 2 ? &L->wgu
                    : which == 3 ? &L->wdown : nullptr;
     SI_REQUIRE(w && w->n, "layer_weights: no matrix %d", which);
     *qs = w->qs;
     *d = w->d;
+    *tile = w->tile;
     *n = w->n;
     *k = w->k;
     return SI_OK;
@@ -532,20 +609,69 @@ int si_layer_weights(si_layer_t *L, int which, const uint8_t **qs, const uint16_
 
 }  // extern "C"
 
-// Projection of rows activation rows: GEMV for one row, matrix-core GEMM
-// otherwise.
+// Projection of rows activation rows: mat-vec for one row, matrix-core
+// GEMM otherwise.
 static void project(si_layer *L, const Q4Dev &w, int rows, const Q8Buf &x, const float *bias,
                     const float *residual, float *out, int flags, hipStream_t st) {
     if (rows == 1)
-        launch_gemv_q4q8(w.qs, w.d, w.n, w.k, x.qs, x.d, x.s, bias, residual, out,
-                         decode_splits(L, w.n, w.k, flags), L->gemv_ws, st);
+        launch_matvec(x.qs, x.d, x.s, w.k, w.qs, w.d, w.tile, w.n, bias, residual, out,
+                      (flags & SI_LAYER_EXACT) != 0, st);
     else
-        launch_gemm_q4q8(w.qs, w.d, w.n, w.k, x.qs, x.d, rows, bias, residual, out, w.n,
+        launch_gemm_q4q8(w.qs, w.d, w.tile, w.n, w.k, x.qs, x.d, rows, bias, residual, out, w.n,
                          (flags & SI_LAYER_EXACT) != 0, st);
 }
 
-// Shared schedule.  rows activation rows; positions and attention contexts
-// come either from (pos0, ctx0, ctx_step) or from ctx_dev.
+// Single-token decode: five fused kernels (si_decode.hip).
+static int run_decode(si_layer *L, const float *x, uint16_t *kc, uint16_t *vc, int ctx,
+                      float *out, int flags, hipStream_t st) {
+    const si_shape_t &s = L->s;
+    const int H = s.hidden, QD = s.qheads * s.hdim, NQKV = QD + 2 * s.kvheads * s.hdim;
+    const bool full = !(flags & SI_LAYER_ATTN_ONLY);
+    const bool exact = (flags & SI_LAYER_EXACT) != 0;
+    SI_REQUIRE(!full || L->ffn, "layer has no FFN weights: use SI_LAYER_ATTN_ONLY");
+    for (bool &h : L->phase_hit) h = false;
+    // qwen_one_layer.c:247-258: RMSNorm -> Q8 -> Q, K, V (+bias)
+    mark(L, SI_PHASE_QKV, st);
+    launch_dec_qkv(x, L->norm, H, s.rms_eps, L->wqkv.qs, L->wqkv.d, L->wqkv.tile, NQKV, L->bqkv,
+                   L->normed,
+                   L->xq.qs, L->xq.d, L->xq.s, L->qkv, exact, st);
+    // :260-270: RoPE, fp16 K/V append at context-1, attention over the cache
+    mark(L, SI_PHASE_ATTENTION_Q8, st);
+    const int ns = dec_attn_chunks(s.kvheads, 1, ctx);
+    launch_dec_attn(L->qkv, NQKV, 1, s.qheads, s.kvheads, s.hdim, L->rope_cos, L->rope_sin, kc,
+                    vc, 0, nullptr, ctx, ctx, L->q, ns, L->attn_ws, nullptr, nullptr, nullptr,
+                    nullptr, st);
+    // :272-275: Q8 of the attention output, W_O (no bias); + x in the full layer
+    mark(L, SI_PHASE_OUT_PROJ, st);
+    const float *pm = (const float *)L->attn_ws;
+    const float *pl = pm + (size_t)s.qheads * ns;
+    const float *po = pl + (size_t)s.qheads * ns;
+    launch_dec_wo(pm, pl, po, ns, s.qheads, s.hdim, L->wo.qs, L->wo.d, L->wo.tile, H,
+                  full ? x : nullptr,
+                  L->attn, L->attq.qs, L->attq.d, L->attq.s, full ? L->attn_out : nullptr,
+                  full ? L->h : out, exact, st);
+    if (!full) {
+        mark(L, SI_PHASE_COUNT, st);
+        return check_launch("layer decode (attention sublayer)");
+    }
+    // FFN half: RMSNorm(h) -> Q8 -> gate|up -> SwiGLU -> Q8 -> down + h
+    mark(L, SI_PHASE_GATE_UP, st);
+    launch_dec_gateup(L->h, L->post_norm, H, s.rms_eps, L->wgu.qs, L->wgu.d, L->wgu.tile, s.ffn,
+                      L->normed2,
+                      L->xq2.qs, L->xq2.d, L->xq2.s, L->gu, L->act, L->actq.qs, L->actq.d,
+                      L->actq.s, exact, st);
+    mark(L, SI_PHASE_DOWN, st);
+    launch_matvec(L->actq.qs, L->actq.d, L->actq.s, s.ffn, L->wdown.qs, L->wdown.d,
+                  L->wdown.tile, H, nullptr,
+                  L->h, out, exact, st);
+    mark(L, SI_PHASE_COUNT, st);
+    return check_launch("layer decode");
+}
+
+// Shared schedule of the matrix-core paths.  rows activation rows;
+// positions and attention contexts come either from (pos0, ctx0, ctx_step)
+// or from ctx_dev.  ctx_step 0 is batched decode (one new token per
+// sequence), ctx_step 1 causal prefill.
 static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_t *vc,
                     size_t kv_seq_stride, int pos0, const int *ctx_dev, int ctx0, int ctx_step,
                     int max_ctx, float *out, int flags, hipStream_t st) {
@@ -562,15 +688,32 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
     // :253-258: Q, K, V projections (+bias), fused into one N = qd + 2 kvd matrix
     mark(L, SI_PHASE_QKV, st);
     project(L, L->wqkv, rows, L->xq, L->bqkv, nullptr, L->qkv, flags, st);
-    mark(L, SI_PHASE_ROPE_KV, st);
-    // :260-266: RoPE at the token's position, fp16 K/V append
-    launch_rope_kv(L->qkv, NQKV, rows, s.qheads, s.kvheads, s.hdim, pos0, pos_step, max_ctx,
-                   ctx_dev, L->rope_cos, L->rope_sin, L->q, kc, vc, kv_seq_stride, st);
-    // :268-272: attention over the fp16 cache -> Q8
-    mark(L, SI_PHASE_ATTENTION_Q8, st);
-    launch_attention(L->q, rows, s.qheads, s.kvheads, s.hdim, kc, vc, kv_seq_stride, ctx_dev,
-                     ctx0, ctx_step, max_ctx, L->attn, L->attq.qs, L->attq.d, L->attq.s,
-                     L->attn_ws, st);
+    if (ctx_step == 0) {
+        // batched decode: RoPE + K/V append inside the attention kernel
+        mark(L, SI_PHASE_ATTENTION_Q8, st);
+        const int ns = dec_attn_chunks(s.kvheads, rows, max_ctx);
+        if (ns == 1) {
+            launch_dec_attn(L->qkv, NQKV, rows, s.qheads, s.kvheads, s.hdim, L->rope_cos,
+                            L->rope_sin, kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx, L->q, 1,
+                            L->attn_ws, L->attn, L->attq.qs, L->attq.d, L->attq.s, st);
+        } else {
+            launch_dec_attn(L->qkv, NQKV, rows, s.qheads, s.kvheads, s.hdim, L->rope_cos,
+                            L->rope_sin, kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx, L->q, ns,
+                            L->attn_ws, nullptr, nullptr, nullptr, nullptr, st);
+            launch_attn_combine(rows, s.qheads, s.hdim, ns, L->attn_ws, L->attn, L->attq.qs,
+                                L->attq.d, L->attq.s, st);
+        }
+    } else {
+        mark(L, SI_PHASE_ROPE_KV, st);
+        // :260-266: RoPE at the token's position, fp16 K/V append
+        launch_rope_kv(L->qkv, NQKV, rows, s.qheads, s.kvheads, s.hdim, pos0, pos_step, max_ctx,
+                       ctx_dev, L->rope_cos, L->rope_sin, L->q, kc, vc, kv_seq_stride, st);
+        // :268-272: attention over the fp16 cache -> Q8
+        mark(L, SI_PHASE_ATTENTION_Q8, st);
+        launch_attention(L->q, rows, s.qheads, s.kvheads, s.hdim, kc, vc, kv_seq_stride, ctx_dev,
+                         ctx0, ctx_step, max_ctx, L->attn, L->attq.qs, L->attq.d, L->attq.s,
+                         L->attn_ws, st);
+    }
     mark(L, SI_PHASE_OUT_PROJ, st);
     if (!full) {
         // :275: W_O, no bias, no residual
@@ -601,8 +744,7 @@ int si_layer_decode(si_layer_t *L, const float *x, uint16_t *kc, uint16_t *vc, i
     // qwen_one_layer.c:608: context 1..32768 (here bounded by the RoPE table)
     SI_REQUIRE(context >= 1 && context <= L->max_pos, "context %d outside 1..%d", context,
                L->max_pos);
-    return run_rows(L, x, 1, kc, vc, 0, context - 1, nullptr, context, 0, context, out, flags,
-                    S(stream));
+    return run_decode(L, x, kc, vc, context, out, flags, S(stream));
 }
 
 int si_layer_decode_batch(si_layer_t *L, const float *x, int nseq, uint16_t *kc, uint16_t *vc,

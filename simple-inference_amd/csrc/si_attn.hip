@@ -208,8 +208,8 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(
                 s[r] = pos < p1 ? sacc[r] * scale : -INFINITY;
                 mx = fmaxf(mx, s[r]);
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = fmaxf(mx, swap16_f(mx));
+            mx = fmaxf(mx, swap32_f(mx));
             const float mnew = fmaxf(m, mx);
             const float alpha = expf(m - mnew);  // 0 while m is -inf
             float p[4], ps = 0.0f;
@@ -218,8 +218,8 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(
                 p[r] = expf(s[r] - mnew);
                 ps += p[r];
             }
-            ps += __shfl_xor(ps, 16, 64);
-            ps += __shfl_xor(ps, 32, 64);
+            ps += swap16_f(ps);
+            ps += swap32_f(ps);
             lsum = lsum * alpha + ps;
             m = mnew;
             h4 ph, pl;
@@ -307,6 +307,17 @@ void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
     }
 #undef SI_ATTN_LAUNCH
     hipLaunchKernelGGL(k_attn_combine, dim3(qheads, nq), dim3(hdim), 0, st, qheads, hdim, ns4,
+                       ws_m, ws_l, ws_o, attn, qs, d, bsum);
+}
+
+// Merge of nsplit partials laid out as [nq][qheads][nsplit] (m, l) and
+// [nq][qheads][nsplit][hdim] (o) in one workspace.
+void launch_attn_combine(int nq, int qheads, int hdim, int nsplit, const void *workspace,
+                         float *attn, int8_t *qs, uint16_t *d, int16_t *bsum, hipStream_t st) {
+    const float *ws_m = (const float *)workspace;
+    const float *ws_l = ws_m + (size_t)nq * qheads * nsplit;
+    const float *ws_o = ws_l + (size_t)nq * qheads * nsplit;
+    hipLaunchKernelGGL(k_attn_combine, dim3(qheads, nq), dim3(hdim), 0, st, qheads, hdim, nsplit,
                        ws_m, ws_l, ws_o, attn, qs, d, bsum);
 }
 

@@ -1,0 +1,826 @@
+// si_decode.hip -- decode layer (one new token per sequence) in five fused
+// kernels.
+//
+// A decode layer is latency-bound at small shapes (8.9 MB of weights and KV
+// for the 0.5B layer stream in ~1.1 us at HBM peak, while a kernel boundary
+// costs ~2 us) and HBM-bound at 7B.  The reference's staged run_layer
+// (qwen_one_layer.c:237-281: RMSNorm, Q8, Q/K/V, RoPE + KV append,
+// attention, Q8, W_O) plus the build-defined FFN runs as:
+//
+//   1 k_dec_qkv    RMSNorm -> Q8 (recomputed by every workgroup into LDS),
+//                  Q|K|V mat-vec (+bias)                         -> qkv fp32
+//   2 k_dec_attn   RoPE of q and of the new K row, fp16 K/V append, matrix-
+//                  core attention over a context chunk           -> partials
+//   3 k_dec_wo     merge of the attention partials, Q8, W_O mat-vec
+//                  (+ residual x)                                -> h
+//   4 k_dec_gateup post-attention RMSNorm -> Q8, gate|up mat-vec,
+//                  SwiGLU -> Q8                                  -> act Q8
+//   5 k_matvec     down mat-vec + residual h                     -> out
+//                  (si_gemv.hip)
+//
+// The mat-vec core is GemvRows (si_gemv.hpp); with SI_LAYER_EXACT every
+// projection runs its bit-exact instantiation.
+#include "si_device.hpp"
+#include "si_gemv.hpp"
+#include "si_kernels.hpp"
+
+namespace si {
+
+// ---------------------------------------------------------------------------
+// Activation prologues: the row a workgroup's mat-vec consumes, built in LDS.
+// ---------------------------------------------------------------------------
+struct Q8Lds {
+    int8_t *qs;
+    uint16_t *d;
+    int16_t *s;
+};
+
+// quantize_q8 of one block held by one thread (bit-exact, same rules as
+// quant_block_lane).
+__device__ __forceinline__ void quant_block_serial(const float (&v)[32], uint32_t (&q)[8],
+                                                   uint16_t &dbits, int &bsum) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));  // NaN ignored
+    const float d = __fdiv_rn(amax, 127.0f);
+    dbits = f2h(d);
+    const float inv = (d == 0.0f) ? 0.0f : __fdiv_rn(1.0f, d);
+    int sum = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = 0;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        const float y = __fmul_rn(v[j], inv);
+        int qq;
+        if (!(fabsf(y) <= 3.0e38f)) {
+            qq = -127;  // NaN or +-inf: lrintf gives LONG_MIN on x86-64
+        } else {
+            qq = (int)rintf(fminf(fmaxf(y, -200.0f), 200.0f));
+            qq = qq > 127 ? 127 : (qq < -127 ? -127 : qq);
+        }
+        sum += qq;
+        q[j >> 2] |= (uint32_t)(qq & 0xff) << (8 * (j & 3));
+    }
+    bsum = sum;
+}
+
+// RMSNorm (qwen_one_layer.c:164-169) then quantize_q8 (:98-116) of one
+// activation row into LDS.  Thread t owns 4 consecutive values (t + T*i
+// groups of 4), so a Q8 block is 8 consecutive lanes and its max and sum
+// are three DPP steps.  The sum of squares is taken in binary64 (4 values
+// per lane, then a fixed tree); the Q8 blocks are bit-exact given the
+// normalised values.  Two steps so a kernel can order its memory requests
+// as it consumes them (loads retire in issue order): load() requests the
+// thread's first x and gain values, the kernel then requests its weights,
+// and run() waits only for x and gain.  Workgroup 0 stores the captures.
+template <int T>
+struct NormQ8Prologue {
+    const float *x, *gain;
+    int n;
+    float4 v, g;
+
+    __device__ __forceinline__ NormQ8Prologue(const float *__restrict__ x_,
+                                              const float *__restrict__ gain_, int n_)
+        : x(x_), gain(gain_), n(n_) {}
+
+    __device__ __forceinline__ void load4(int e4, float4 &xv, float4 &gv) const {
+        xv = *(const float4 *)(x + 4 * e4);
+        gv = gain ? *(const float4 *)(gain + 4 * e4) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    }
+    __device__ __forceinline__ void load() {  // branch-free (clamped index)
+        load4(min((int)threadIdx.x, n / 4 - 1), v, g);
+    }
+
+    __device__ void run(float eps, Q8Lds xq, double *dscr, float *__restrict__ cap_normed,
+                        int8_t *__restrict__ cap_qs, uint16_t *__restrict__ cap_d,
+                        int16_t *__restrict__ cap_s) {
+        const int t = threadIdx.x;
+        const int n4 = n / 4;
+        double ss = 0.0;
+        for (int e4 = t; e4 < n4; e4 += T) {
+            float4 xv = v, gv;
+            if (e4 != t) load4(e4, xv, gv);  // more values than 4 per thread
+            ss += (double)xv.x * xv.x + (double)xv.y * xv.y + (double)xv.z * xv.z +
+                  (double)xv.w * xv.w;
+        }
+        ss = wave_sum_d(ss);
+        if ((t & 63) == 0) dscr[t >> 6] = ss;
+        __syncthreads();
+        double tot = 0.0;
+#pragma unroll
+        for (int w = 0; w < T / 64; ++w) tot += dscr[w];
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn((float)(tot / (double)n), eps)));
+        const bool cap = blockIdx.x == 0;
+        for (int e4 = t; e4 < n4; e4 += T) {  // whole 8-lane groups (n4 % 8 == 0)
+            float4 xv = v, gv = g;
+            if (e4 != t) load4(e4, xv, gv);
+            const float y[4] = {__fmul_rn(__fmul_rn(xv.x, inv), gv.x),
+                                __fmul_rn(__fmul_rn(xv.y, inv), gv.y),
+                                __fmul_rn(__fmul_rn(xv.z, inv), gv.z),
+                                __fmul_rn(__fmul_rn(xv.w, inv), gv.w)};
+            uint16_t dbits;
+            int bsum;
+            const uint32_t q = quant_block_oct(y, dbits, bsum);
+            *(uint32_t *)(xq.qs + 4 * e4) = q;
+            const int blk = e4 >> 3;
+            if ((e4 & 7) == 0) {
+                xq.d[blk] = dbits;
+                xq.s[blk] = (int16_t)bsum;
+            }
+            if (cap) {
+                if (cap_normed) *(float4 *)(cap_normed + 4 * e4) = make_float4(y[0], y[1], y[2], y[3]);
+                if (cap_qs) *(uint32_t *)(cap_qs + 4 * e4) = q;
+                if ((e4 & 7) == 0) {
+                    if (cap_d) cap_d[blk] = dbits;
+                    if (cap_s) cap_s[blk] = (int16_t)bsum;
+                }
+            }
+        }
+        __syncthreads();
+    }
+};
+
+// LDS carve-up for the kernels that build their activation row in LDS:
+// [dscr: 16 doubles][red][y: R floats][xf: k floats + extra][d][s][qs]
+template <int R, int T>
+struct DecLds {
+    double *dscr;
+    float *red, *y, *xf;
+    Q8Lds xq;
+    static constexpr size_t bytes(int k, bool with_xf, int extra_floats) {
+        return 16 * 8 + (size_t)red_floats<R, T>() * 4 + R * 4 + (with_xf ? (size_t)k * 4 : 0) +
+               (size_t)extra_floats * 4 + (size_t)(k / 32) * 4 + 16 + k;
+    }
+    __device__ DecLds(char *p, int k, bool with_xf, int extra_floats) {
+        dscr = (double *)p;
+        p += 16 * 8;
+        red = (float *)p;
+        p += red_floats<R, T>() * 4;
+        y = (float *)p;
+        p += R * 4;
+        xf = (float *)p;
+        p += (with_xf ? (size_t)k * 4 : 0) + (size_t)extra_floats * 4;
+        xq.d = (uint16_t *)p;
+        p += (k / 32) * 2;
+        xq.s = (int16_t *)p;
+        p += (k / 32) * 2;
+        p = (char *)(((uintptr_t)p + 15) & ~(uintptr_t)15);
+        xq.qs = (int8_t *)p;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// 1: RMSNorm -> Q8 -> Q|K|V (+bias) -> qkv fp32
+// ---------------------------------------------------------------------------
+template <int R, int T, bool EXACT>
+__global__ void __launch_bounds__(T) k_dec_qkv(
+    const float *__restrict__ x, const float *__restrict__ gain, int hidden, float eps,
+    const uint8_t *__restrict__ wqs, const uint16_t *__restrict__ wd, int tile, int n,
+    const float *__restrict__ bias, float *__restrict__ cap_normed, int8_t *__restrict__ cap_qs,
+    uint16_t *__restrict__ cap_d, int16_t *__restrict__ cap_s, float *__restrict__ qkv) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    DecLds<R, T> L(smem, hidden, false, 0);
+    const int tile0 = blockIdx.x * R;
+    const int t = threadIdx.x;
+    const int row = tile0 + (t % R);
+    NormQ8Prologue<T> pro(x, gain, hidden);
+    pro.load();  // requested in the order they are consumed
+    const float b0 = bias ? bias[min(row, n - 1)] : 0.0f;
+    GemvRows<R, T, EXACT, RowIdentity> g(wqs, wd, tile, n, n, hidden / SI_QK, tile0,
+                                         RowIdentity{});
+    g.start();  // weights in flight while the activation row is built
+    pro.run(eps, L.xq, L.dscr, cap_normed, cap_qs, cap_d, cap_s);
+    const float y = g.finish(Q8Row{L.xq.qs, L.xq.d, L.xq.s}, EXACT ? b0 : 0.0f, L.red);
+    if (t < R && row < n) qkv[row] = EXACT ? y : y + b0;
+}
+
+// ---------------------------------------------------------------------------
+// 3: merge attention partials -> attn fp32 -> Q8 -> W_O mat-vec (+ residual)
+// ---------------------------------------------------------------------------
+// Partials per (head, chunk s): running max m, sum l, unnormalised o[D].
+// attn[h][d] = sum_s o_s[d] e^(m_s - M) * (1 / sum_s l_s e^(m_s - M)),
+// M = max_s m_s; a head with no context (M = -inf) gives 0
+// (attention_kernels.h:95-98).
+template <int R, int T, bool EXACT>
+__global__ void __launch_bounds__(T) k_dec_wo(
+    const float *__restrict__ pm, const float *__restrict__ pl, const float *__restrict__ po,
+    int ns, int qheads, int hdim, const uint8_t *__restrict__ wqs,
+    const uint16_t *__restrict__ wd, int tile, int n, const float *__restrict__ residual,
+    float *__restrict__ cap_attn, int8_t *__restrict__ cap_qs, uint16_t *__restrict__ cap_d,
+    int16_t *__restrict__ cap_s, float *__restrict__ cap_y, float *__restrict__ out) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const int qd = qheads * hdim;
+    DecLds<R, T> L(smem, qd, false, 0);
+    const int tile0 = blockIdx.x * R;
+    const int t = threadIdx.x;
+    const bool cap = blockIdx.x == 0;
+    GemvRows<R, T, EXACT, RowIdentity> g(wqs, wd, tile, n, n, qd / SI_QK, tile0,
+                                         RowIdentity{});
+    // Thread t merges the 4 consecutive elements 4*e4.. (e4 = t + T*i), 8
+    // chunks at a time, with the online rule (m, l, o) <- (M',
+    // l e^(m-M') + l_s e^(m_s-M'), o e^(m-M') + o_s e^(m_s-M')), then
+    // quantizes: 8 consecutive lanes hold one Q8_0 block of the output
+    // (qwen_one_layer.c:272).  The first group of partials is requested
+    // before the weights, which then load while the merge runs.
+    constexpr int SC = 8;
+    bool started = false;
+    const int qd4 = qd / 4;
+    for (int e40 = 0; e40 < qd4; e40 += T) {
+        const int e4 = e40 + t;
+        const bool eok = e4 < qd4;
+        const int ec = 4 * min(e4, qd4 - 1);
+        const int h = ec / hdim, d = ec - h * hdim;
+        float M = -INFINITY, Ls = 0.0f;
+        float A[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s0 = 0; s0 < ns; s0 += SC) {
+            float om[SC], ol[SC];
+            float4 oo[SC];
+#pragma unroll
+            for (int u = 0; u < SC; ++u) {  // branch-free loads, clamped index
+                const size_t pi = (size_t)h * ns + min(s0 + u, ns - 1);
+                om[u] = pm[pi];
+                ol[u] = pl[pi];
+                oo[u] = *(const float4 *)(po + pi * hdim + d);
+            }
+            if (!started) {
+                g.start();
+                started = true;
+            }
+#pragma unroll
+            for (int u = 0; u < SC; ++u) {
+                if (s0 + u >= ns || om[u] == -INFINITY) continue;  // empty chunk
+                const float mn = fmaxf(M, om[u]);
+                const float a = M == -INFINITY ? 0.0f : expf(M - mn);
+                const float bw = expf(om[u] - mn);
+                A[0] = fmaf(oo[u].x, bw, A[0] * a);
+                A[1] = fmaf(oo[u].y, bw, A[1] * a);
+                A[2] = fmaf(oo[u].z, bw, A[2] * a);
+                A[3] = fmaf(oo[u].w, bw, A[3] * a);
+                Ls = fmaf(ol[u], bw, Ls * a);
+                M = mn;
+            }
+        }
+        if (e40 + (t & ~7) < qd4) {  // whole 8-lane groups
+            // normalise (attention_kernels.h:163); no context gives 0 (:95-98)
+            const float r = M == -INFINITY ? 0.0f : 1.0f / Ls;
+            const float y[4] = {A[0] * r, A[1] * r, A[2] * r, A[3] * r};
+            uint16_t dbits;
+            int bsum;
+            const uint32_t q = quant_block_oct(y, dbits, bsum);
+            if (eok) {
+                *(uint32_t *)(L.xq.qs + 4 * e4) = q;
+                if ((e4 & 7) == 0) {
+                    L.xq.d[e4 >> 3] = dbits;
+                    L.xq.s[e4 >> 3] = (int16_t)bsum;
+                }
+                if (cap) {
+                    if (cap_attn) *(float4 *)(cap_attn + 4 * e4) = make_float4(y[0], y[1], y[2], y[3]);
+                    if (cap_qs) *(uint32_t *)(cap_qs + 4 * e4) = q;
+                    if ((e4 & 7) == 0) {
+                        if (cap_d) cap_d[e4 >> 3] = dbits;
+                        if (cap_s) cap_s[e4 >> 3] = (int16_t)bsum;
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+    const float y = g.finish(Q8Row{L.xq.qs, L.xq.d, L.xq.s}, 0.0f, L.red);
+    const int row = tile0 + t;
+    if (t < R && row < n) {
+        if (cap_y) cap_y[row] = y;
+        out[row] = residual ? __fadd_rn(residual[row], y) : y;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 4: post-attention RMSNorm -> Q8 -> gate|up -> SwiGLU -> Q8
+// ---------------------------------------------------------------------------
+template <int R, int T, bool EXACT>
+__global__ void __launch_bounds__(T) k_dec_gateup(
+    const float *__restrict__ h, const float *__restrict__ gain, int hidden, float eps,
+    const uint8_t *__restrict__ wqs, const uint16_t *__restrict__ wd, int tile, int f,
+    float *__restrict__ cap_normed, int8_t *__restrict__ cap_qs, uint16_t *__restrict__ cap_d,
+    int16_t *__restrict__ cap_s, float *__restrict__ gu, float *__restrict__ act,
+    int8_t *__restrict__ aqs, uint16_t *__restrict__ ad, int16_t *__restrict__ as) {
+    static_assert(R % 64 == 0, "gate|up rows pair within a wavefront");
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    DecLds<R, T> L(smem, hidden, false, 0);
+    const int tile0 = blockIdx.x * R;
+    const int t = threadIdx.x;
+    NormQ8Prologue<T> pro(h, gain, hidden);
+    pro.load();  // requested in the order they are consumed
+    GemvRows<R, T, EXACT, RowGateUp> g(wqs, wd, tile, 2 * f, 2 * f, hidden / SI_QK, tile0,
+                                       RowGateUp{f});
+    g.start();  // weights in flight while the activation row is built
+    pro.run(eps, L.xq, L.dscr, cap_normed, cap_qs, cap_d, cap_s);
+    const float y = g.finish(Q8Row{L.xq.qs, L.xq.d, L.xq.s}, 0.0f, L.red);
+    if (t < R) L.y[t] = y;
+    __syncthreads();
+    if (t >= R) return;
+    const int lrow = tile0 + t;  // logical row (f is a multiple of 32: whole wavefronts)
+    if (lrow >= 2 * f) return;
+    const int j = 32 * (lrow >> 6) + (lrow & 31);
+    if (gu) gu[(lrow & 32) ? f + j : j] = y;
+    if (t & 32) return;  // lanes 0..31 of each wavefront hold the gate rows
+    // SwiGLU (silu(g) = g / (1 + e^-g), then * u) and quantize_q8 of the block
+    const float gv = y, u = L.y[t + 32];
+    const float a = __fmul_rn(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv))), u);
+    uint16_t dbits;
+    int bsum;
+    const int q = quant_block_lane(a, dbits, bsum);
+    if (act) act[j] = a;
+    aqs[j] = (int8_t)q;
+    if ((t & 31) == 0) {
+        ad[j / SI_QK] = dbits;
+        as[j / SI_QK] = (int16_t)bsum;
+    }
+}
+
+// ===========================================================================
+// 2: decode attention with RoPE and the K/V append folded in.
+//
+// Workgroup (chunk sp, KV group g, sequence qi), NW wavefronts.  The new
+// token sits at position p = ctx - 1.  Every workgroup rotates the group's
+// query heads itself (RoPE, qwen_one_layer.c:260-261); the workgroup whose
+// chunk holds p also rotates the group's K row, narrows K and V to fp16 and
+// appends them to the cache (:262-266), and uses those fp16 values for
+// position p (the reference reads the new row back from the fp16 cache).
+//
+// Wavefront w takes the 16-position tiles w, w + NW, ... of the chunk:
+//   S^T[pos][head] = K[pos][:] . Q[head][:]      v_mfma_f32_16x16x32_f16
+//   online softmax per head (one head per MFMA column)
+//   O^T[d][head] += V^T[d][pos] . P[pos][head]   v_mfma_f32_16x16x16f16
+// fp32 Q and P enter the fp16 matrix cores as hi + lo halves, so products
+// keep fp32-level accuracy.  K tiles are MFMA A operands loaded straight
+// from HBM; V tiles pass through the wavefront's own LDS rows to be read
+// transposed.  The next tile's K and V loads are issued before the current
+// tile is computed.  The wavefronts' (m, l, o) are merged in LDS into one
+// partial per workgroup; with FINAL (single chunk) the workgroup normalises
+// and quantizes the output itself.
+// MFMA 16x16 output element (i, j): lane j + 16*(i/4), register i%4.
+// ===========================================================================
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int DA_TILE = 16;
+constexpr int DA_VPAD = 8;  // halves of padding per LDS V row
+
+__device__ __forceinline__ void hi_lo(float x, _Float16 &hi, _Float16 &lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
+
+template <int D, int NW>
+struct AttnLds {
+    static constexpr int VROW = D + DA_VPAD;
+    static constexpr size_t v_bytes = (size_t)NW * DA_TILE * VROW * 2;
+    static constexpr size_t merge_bytes(int per) {
+        return ((size_t)NW * per * (D + 3) + 2 * per) * 4;
+    }
+    static constexpr size_t raw_bytes(int per) { return (size_t)(per * D + 3 * D) * 4; }
+    static constexpr size_t bytes(int per) {
+        size_t m = merge_bytes(per);
+        if (raw_bytes(per) > m) m = raw_bytes(per);
+        return 2 * D * 2 + (v_bytes > m ? v_bytes : m);
+    }
+};
+
+template <int D, int NW, bool FINAL>
+__global__ void __launch_bounds__(NW * 64) k_dec_attn(
+    const float *__restrict__ qkv, int ldqkv, int qheads, int kvheads,
+    const float *__restrict__ rc, const float *__restrict__ rs, uint16_t *__restrict__ kc,
+    uint16_t *__restrict__ vc, size_t kv_seq_stride, const int *__restrict__ ctx_dev, int ctx0,
+    int max_ctx, int chunk, float scale, float *__restrict__ q_cap, float *__restrict__ ws_m,
+    float *__restrict__ ws_l, float *__restrict__ ws_o, float *__restrict__ attn,
+    int8_t *__restrict__ aqs, uint16_t *__restrict__ ad, int16_t *__restrict__ as) {
+    constexpr int KS = D / 32, DT = D / 16, HALF = D / 2;
+    constexpr int VROW = AttnLds<D, NW>::VROW;
+    constexpr int VL = DA_TILE * D / (64 * 8);  // 16-byte V pieces per lane per tile
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    uint16_t *newk = (uint16_t *)smem;  // fp16 K and V rows of the new token
+    uint16_t *newv = newk + D;
+    char *big = smem + 2 * D * 2;
+    _Float16 *vbuf = (_Float16 *)big;
+
+    const int sp = blockIdx.x, g = blockIdx.y, qi = blockIdx.z, ns = gridDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int per = qheads / kvheads;
+    const int qd = qheads * D, kvd = kvheads * D;
+    int ctx = ctx_dev ? ctx_dev[qi] : ctx0;
+    ctx = min(ctx, max_ctx);
+    const int pnew = ctx - 1;  // < 0: empty context (device-supplied only)
+    const int p0 = sp * chunk;
+    const int p1 = min(ctx, p0 + chunk);
+    const bool owner = pnew >= p0 && pnew < p1;
+    const float *row = qkv + (size_t)qi * ldqkv;
+    const float *cr = rc + (size_t)max(pnew, 0) * HALF;
+    const float *sr = rs + (size_t)max(pnew, 0) * HALF;
+    const size_t sbase = (size_t)qi * kv_seq_stride;
+
+    const uint16_t *kbase = kc + sbase + (size_t)g * D;
+    const uint16_t *vbase = vc + sbase + (size_t)g * D;
+    _Float16 *vw = vbuf + (size_t)wave * DA_TILE * VROW;
+
+    // K pieces of the lane's row (pos = t0 + col), V pieces of the tile
+    // (branch-free: positions past the chunk re-read its last row, or row 0
+    // for an empty context; such rows are masked out of the scores)
+    auto load_k = [&](int t0, uint4(&kr)[KS]) {
+        const int pos = max(min(t0 + col, p1 - 1), 0);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            kr[ks] = *(const uint4 *)(kbase + (size_t)pos * kvd + 32 * ks + 8 * grp);
+    };
+    auto load_v = [&](int t0, uint4(&vr)[VL]) {
+#pragma unroll
+        for (int j = 0; j < VL; ++j) {
+            const int c = lane + 64 * j;
+            const int r = c / (D / 8), e = (c % (D / 8)) * 8;
+            vr[j] = *(const uint4 *)(vbase + (size_t)max(min(t0 + r, p1 - 1), 0) * kvd + e);
+        }
+    };
+    // The new token's row is taken from LDS (its cache row may not be
+    // written yet: the global value read for it is discarded).  Applied when
+    // a tile is consumed, so prefetched loads stay in flight until then.
+    auto sel = [](bool c, uint4 a, uint4 b) {
+        return make_uint4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
+    };
+    auto fix = [&](int t0, uint4(&kr)[KS], uint4(&vr)[VL]) {
+        const int pos = min(t0 + col, p1 - 1);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            kr[ks] = sel(pos == pnew, *(const uint4 *)(newk + 32 * ks + 8 * grp), kr[ks]);
+#pragma unroll
+        for (int j = 0; j < VL; ++j) {
+            const int c = lane + 64 * j;
+            const int r = c / (D / 8), e = (c % (D / 8)) * 8;
+            vr[j] = sel(min(t0 + r, p1 - 1) == pnew, *(const uint4 *)(newv + e), vr[j]);
+        }
+    };
+
+    // Requests in the order they are consumed (loads retire in issue order):
+    // 1. the group's raw q rows, the raw K and V rows of the new token and
+    //    the RoPE row at its position, one or a few floats per thread;
+    float *qraw = (float *)big;   // [per][D]; these LDS rows are reused for
+    float *kraw = qraw + per * D; // the V tiles once Q is in registers
+    float *vraw = kraw + D;
+    float *csr = vraw + D;        // [HALF] cos, then [HALF] sin
+    const int nraw = per * D + 3 * D;
+    constexpr int RAWPT = (16 * D + 3 * D + NW * 64 - 1) / (NW * 64);
+    float rv[RAWPT];
+#pragma unroll
+    for (int u = 0; u < RAWPT; ++u) {  // branch-free: clamped index
+        const int i = min(tid + u * NW * 64, nraw - 1);
+        {
+            const float *src;
+            if (i < per * D)
+                src = row + (size_t)g * per * D + i;
+            else if (i < per * D + D)
+                src = row + qd + g * D + (i - per * D);
+            else if (i < per * D + 2 * D)
+                src = row + qd + kvd + g * D + (i - per * D - D);
+            else {
+                const int j = i - per * D - 2 * D;
+                src = j < HALF ? cr + j : sr + (j - HALF);
+            }
+            rv[u] = *src;
+        }
+    }
+    // 2. the wavefront's first K and V tile
+    int t0 = p0 + DA_TILE * wave;
+    uint4 kr[KS], vr[VL];
+    load_k(t0, kr);
+    load_v(t0, vr);
+#pragma unroll
+    for (int u = 0; u < RAWPT; ++u) {
+        const int i = tid + u * NW * 64;
+        if (i < nraw) qraw[i] = rv[u];
+    }
+    __syncthreads();
+    // rotate-half RoPE (qwen_one_layer.c:172-183) of element dd of a head row
+    auto rot = [&](const float *v, int dd) {
+        const int i = dd < HALF ? dd : dd - HALF;
+        const float a = v[i], b = v[i + HALF], c = csr[i], s = csr[HALF + i];
+        return dd < HALF ? __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s))
+                         : __fadd_rn(__fmul_rn(b, c), __fmul_rn(a, s));
+    };
+    if (owner) {  // the new token's K (rotated) and V rows, fp16, into the cache
+        for (int dd = tid; dd < D; dd += NW * 64) {
+            const uint16_t kh = f2h(rot(kraw, dd));
+            const uint16_t vh = f2h(vraw[dd]);
+            newk[dd] = kh;
+            newv[dd] = vh;
+            kc[sbase + (size_t)pnew * kvd + g * D + dd] = kh;
+            vc[sbase + (size_t)pnew * kvd + g * D + dd] = vh;
+        }
+    }
+    // Q^T as the B operand: lane holds Q[head col][d = 32*ks + 8*grp + e]
+    h8 qh[KS], ql[KS];
+    {
+        const bool hv = col < per && pnew >= 0;
+        const int hc = col < per ? col : 0;
+        const bool capq = q_cap && sp == 0 && wave == 0 && hv;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int dd = 32 * ks + 8 * grp + e;
+                const float v = hv ? rot(qraw + hc * D, dd) : 0.0f;
+                if (capq) q_cap[(size_t)qi * qd + (size_t)(g * per + hc) * D + dd] = v;
+                _Float16 hi, lo;
+                hi_lo(v, hi, lo);
+                qh[ks][e] = hi;
+                ql[ks][e] = lo;
+            }
+    }
+    __syncthreads();  // newk/newv visible; the raw rows are no longer read
+
+    float m = -INFINITY, lsum = 0.0f;
+    f4 o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = (f4){0.f, 0.f, 0.f, 0.f};
+
+    for (; t0 < p1; t0 += DA_TILE * NW) {
+        fix(t0, kr, vr);
+        // stage V rows into this wavefront's LDS rows
+#pragma unroll
+        for (int j = 0; j < VL; ++j) {
+            const int c = lane + 64 * j;
+            const int r = c / (D / 8), e = (c % (D / 8)) * 8;
+            *(uint4 *)(vw + r * VROW + e) = vr[j];
+        }
+        h8 ka[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) ka[ks] = __builtin_bit_cast(h8, kr[ks]);
+        // prefetch the wavefront's next tile
+        const int tn = t0 + DA_TILE * NW;
+        load_k(tn, kr);  // (past the chunk on the last tile: unused)
+        load_v(tn, vr);
+        f4 sacc = (f4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[ks], qh[ks], sacc, 0, 0, 0);
+            sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[ks], ql[ks], sacc, 0, 0, 0);
+        }
+        // lane holds S^T[pos = t0 + 4*grp + r][head col]
+        float s[4], mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            s[r] = (t0 + 4 * grp + r < p1) ? sacc[r] * scale : -INFINITY;
+            mx = fmaxf(mx, s[r]);
+        }
+        mx = fmaxf(mx, swap16_f(mx));
+        mx = fmaxf(mx, swap32_f(mx));
+        const float mnew = fmaxf(m, mx);
+        const float alpha = expf(m - mnew);  // 0 while m is -inf
+        float p[4], ps = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            p[r] = expf(s[r] - mnew);
+            ps += p[r];
+        }
+        ps += swap16_f(ps);
+        ps += swap32_f(ps);
+        lsum = lsum * alpha + ps;
+        m = mnew;
+        h4 ph, pl;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            _Float16 hi, lo;
+            hi_lo(p[r], hi, lo);
+            ph[r] = hi;
+            pl[r] = lo;
+        }
+        // the V rows written above by other lanes of this wavefront
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // A = V^T[d = 16*dt + col][pos = 4*grp + r]
+        const _Float16 *vcol = vw + (4 * grp) * VROW + col;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            h4 va;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) va[r] = vcol[r * VROW + 16 * dt];
+            f4 acc = o[dt] * alpha;
+            acc = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ph, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pl, acc, 0, 0, 0);
+            o[dt] = acc;
+        }
+        // V rows are read before the next tile overwrites them
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+
+    // merge the NW wavefront states in LDS (reusing the V rows)
+    __syncthreads();
+    float *mm = (float *)big;   // [NW][per]
+    float *ml = mm + NW * per;  // [NW][per]
+    float *mo = ml + NW * per;  // [NW][per][D]
+    if (col < per) {
+        if (grp == 0) {
+            mm[wave * per + col] = m;
+            ml[wave * per + col] = lsum;
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                mo[((size_t)wave * per + col) * D + 16 * dt + 4 * grp + r] = o[dt][r];
+    }
+    __syncthreads();
+    // per head: M = max over wavefronts, their scale factors e^(m_w - M) and
+    // the total l, once per head
+    float *sc = mo + (size_t)NW * per * D;  // [per][NW]
+    float *ltot = sc + per * NW;            // [per]
+    float *mtot = ltot + per;               // [per]
+    if (tid < per) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, mm[w * per + tid]);
+        float l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float f = M == -INFINITY ? 0.0f : expf(mm[w * per + tid] - M);
+            sc[tid * NW + w] = f;
+            l = fmaf(ml[w * per + tid], f, l);
+        }
+        ltot[tid] = l;
+        mtot[tid] = M;
+    }
+    __syncthreads();
+    // 4 consecutive elements per thread; 8 lanes = 32 elements = one Q8_0
+    // block of one head (D is a multiple of 32)
+    const int nel4 = per * D / 4;
+    for (int e40 = 0; e40 < nel4; e40 += NW * 64) {
+        const int e4 = e40 + tid;
+        const bool ok = e4 < nel4;
+        const int ec = 4 * min(e4, nel4 - 1);
+        const int hc = ec / D, dd = ec - hc * D;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float4 ov = *(const float4 *)(mo + ((size_t)w * per + hc) * D + dd);
+            const float f = sc[hc * NW + w];
+            acc[0] = fmaf(ov.x, f, acc[0]);
+            acc[1] = fmaf(ov.y, f, acc[1]);
+            acc[2] = fmaf(ov.z, f, acc[2]);
+            acc[3] = fmaf(ov.w, f, acc[3]);
+        }
+        const int h = g * per + hc;
+        if (!FINAL) {
+            if (ok) {
+                const size_t pi = ((size_t)qi * qheads + h) * ns + sp;
+                if (dd == 0) {
+                    ws_m[pi] = mtot[hc];
+                    ws_l[pi] = ltot[hc];
+                }
+                *(float4 *)(ws_o + pi * D + dd) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+            }
+        } else if (e40 + (tid & ~7) < nel4) {
+            // normalise (attention_kernels.h:163; no context: 0, :95-98) and
+            // quantize_q8
+            const float r = mtot[hc] == -INFINITY ? 0.0f : 1.0f / ltot[hc];
+            const float y[4] = {acc[0] * r, acc[1] * r, acc[2] * r, acc[3] * r};
+            uint16_t dbits;
+            int bsum;
+            const uint32_t q = quant_block_oct(y, dbits, bsum);
+            if (ok) {
+                const size_t off = (size_t)qi * qd + (size_t)h * D + dd;
+                *(float4 *)(attn + off) = make_float4(y[0], y[1], y[2], y[3]);
+                *(uint32_t *)(aqs + off) = q;
+                if ((e4 & 7) == 0) {
+                    ad[off / SI_QK] = dbits;
+                    if (as) as[off / SI_QK] = (int16_t)bsum;
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// launch policy
+// ---------------------------------------------------------------------------
+void launch_dec_qkv(const float *x, const float *gain, int hidden, float eps, const uint8_t *wqs,
+                    const uint16_t *wd, int tile, int n, const float *bias, float *cap_normed,
+                    int8_t *cap_qs, uint16_t *cap_d, int16_t *cap_s, float *qkv, bool exact,
+                    hipStream_t st) {
+#define CALL(R, T, E)                                                                            \
+    hipLaunchKernelGGL((k_dec_qkv<R, T, E>), dim3((n + R - 1) / R), dim3(T),                      \
+                       (DecLds<R, T>::bytes(hidden, false, 0)), st, x, gain, hidden, eps, wqs,    \
+                       wd, tile, n, bias, cap_normed, cap_qs, cap_d, cap_s, qkv)
+    if (exact) {
+        CALL(64, 64, true);
+    } else {
+        const int r = tile < 64 ? tile : 64;
+        SI_GEMV_SWITCH(r, dec_threads(r, hidden / SI_QK), CALL)
+    }
+#undef CALL
+}
+
+void launch_dec_wo(const float *pm, const float *pl, const float *po, int ns, int qheads,
+                   int hdim, const uint8_t *wqs, const uint16_t *wd, int tile, int n,
+                   const float *residual, float *cap_attn, int8_t *cap_qs, uint16_t *cap_d,
+                   int16_t *cap_s, float *cap_y, float *out, bool exact, hipStream_t st) {
+    const int qd = qheads * hdim;
+#define CALL(R, T, E)                                                                            \
+    hipLaunchKernelGGL((k_dec_wo<R, T, E>), dim3((n + R - 1) / R), dim3(T),                       \
+                       (DecLds<R, T>::bytes(qd, false, 0)), st, pm, pl, po, ns,                    \
+                       qheads, hdim, wqs, wd, tile, n, residual, cap_attn, cap_qs, cap_d, cap_s,  \
+                       cap_y, out)
+    if (exact) {
+        CALL(64, 64, true);
+    } else {
+        const int r = tile < 64 ? tile : 64;
+        SI_GEMV_SWITCH(r, dec_threads(r, qd / SI_QK), CALL)
+    }
+#undef CALL
+}
+
+// gate|up: 64 logical rows per workgroup (32 gate + 32 up rows, one scale
+// tile of 32 each), 8 K lanes per row when K has >= 8 blocks.
+void launch_dec_gateup(const float *h, const float *gain, int hidden, float eps,
+                       const uint8_t *wqs, const uint16_t *wd, int tile, int f,
+                       float *cap_normed, int8_t *cap_qs, uint16_t *cap_d, int16_t *cap_s,
+                       float *gu, float *act, int8_t *aqs, uint16_t *ad, int16_t *as, bool exact,
+                       hipStream_t st) {
+    const int n = 2 * f;
+#define CALL(R, T, E)                                                                            \
+    hipLaunchKernelGGL((k_dec_gateup<R, T, E>), dim3((n + R - 1) / R), dim3(T),                   \
+                       (DecLds<R, T>::bytes(hidden, false, 0)), st, h, gain, hidden, eps, wqs,    \
+                       wd, tile, f, cap_normed, cap_qs, cap_d, cap_s, gu, act, aqs, ad, as)
+    if (exact) {
+        CALL(64, 64, true);
+    } else if (hidden / SI_QK >= 8) {
+        CALL(64, 512, false);
+    } else {
+        CALL(64, 256, false);
+    }
+#undef CALL
+}
+
+// Decode attention: DA_NW wavefronts per workgroup; chunks so that every
+// wavefront has about two 16-position tiles, at most 32 chunks, and no more
+// than ~1024 workgroups in total.
+constexpr int DA_NW = 8;
+
+int dec_attn_chunks(int kvheads, int nq, int max_ctx) {
+    const int tiles = (max_ctx + DA_TILE - 1) / DA_TILE;
+    int ns = (tiles + 2 * DA_NW - 1) / (2 * DA_NW);
+    if (ns * kvheads * nq > 1024) ns = (1024 + kvheads * nq - 1) / (kvheads * nq);
+    if (ns > 32) ns = 32;
+    return ns < 1 ? 1 : ns;
+}
+
+size_t dec_attn_workspace_bytes(int qheads, int hdim, int kvheads, int nq, int max_ctx) {
+    const int ns = dec_attn_chunks(kvheads, nq, max_ctx);
+    return (size_t)nq * qheads * ns * (hdim + 2) * sizeof(float);
+}
+
+void launch_dec_attn(const float *qkv, int ldqkv, int nq, int qheads, int kvheads, int hdim,
+                     const float *rc, const float *rs, uint16_t *kc, uint16_t *vc,
+                     size_t kv_seq_stride, const int *ctx_dev, int ctx0, int max_ctx,
+                     float *q_cap, int ns, void *workspace, float *attn, int8_t *aqs,
+                     uint16_t *ad, int16_t *as, hipStream_t st) {
+    if (nq <= 0) return;
+    int chunk = (max_ctx + ns - 1) / ns;
+    chunk = (chunk + DA_TILE - 1) / DA_TILE * DA_TILE;
+    float *ws_m = (float *)workspace;
+    float *ws_l = ws_m + (size_t)nq * qheads * ns;
+    float *ws_o = ws_l + (size_t)nq * qheads * ns;
+    const float scale = 1.0f / sqrtf((float)hdim);  // attention_kernels.h:86
+    const int per = qheads / kvheads;
+    const dim3 grid(ns, kvheads, nq);
+    const bool fin = attn != nullptr;
+#define CALL(DIM, NW, FIN)                                                                     \
+    hipLaunchKernelGGL((k_dec_attn<DIM, NW, FIN>), grid, dim3(NW * 64),                        \
+                       (AttnLds<DIM, NW>::bytes(per)), st, qkv, ldqkv, qheads, kvheads, rc, rs,  \
+                       kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx, chunk, scale, q_cap,     \
+                       ws_m, ws_l, ws_o, attn, aqs, ad, as)
+    // 8 wavefronts unless the merge buffers of a wide GQA group exceed 64 KiB
+#define CALLD(DIM)                                           \
+    if (AttnLds<DIM, DA_NW>::bytes(per) <= 65536) {          \
+        if (fin) {                                           \
+            CALL(DIM, DA_NW, true);                          \
+        } else {                                             \
+            CALL(DIM, DA_NW, false);                         \
+        }                                                    \
+    } else if (fin) {                                        \
+        CALL(DIM, 4, true);                                  \
+    } else {                                                 \
+        CALL(DIM, 4, false);                                 \
+    }
+    switch (hdim) {
+        case 32: CALLD(32); break;
+        case 64: CALLD(64); break;
+        case 96: CALLD(96); break;
+        default: CALLD(128); break;
+    }
+#undef CALLD
+#undef CALL
+}
+
+}  // namespace si

@@ -58,35 +58,111 @@ __device__ __forceinline__ uint16_t f2h(float x) {
 }
 
 // ---------------------------------------------------------------------
-// Cross-lane reductions inside a 32-lane half wavefront (one Q8 block).
+// Cross-lane data movement without the LDS crossbar.  A wavefront is four
+// rows of 16 lanes.  DPP moves within a row (quad_perm, row_ror,
+// row_half_mirror); gfx950's v_permlane16_swap / v_permlane32_swap exchange
+// rows 0<->1, 2<->3 and halves 0<->1.  (__shfl_xor lowers to
+// ds_bpermute_b32, a round trip through LDS, ten of which per Q8 block
+// dominated the small decode kernels.)  Every lane of a group must be
+// active.  The lane layouts are checked on the device by
+// si_debug_lane_ops.
 // ---------------------------------------------------------------------
+enum : int {
+    DPP_XOR1 = 0xB1,      // quad_perm [1,0,3,2]
+    DPP_XOR2 = 0x4E,      // quad_perm [2,3,0,1]
+    DPP_ROR4 = 0x124,     // row_ror:4  (lane i <- lane (i-4) % 16 of its row)
+    DPP_ROR8 = 0x128,     // row_ror:8
+    DPP_HMIRROR = 0x141,  // row_half_mirror (lane i <- 7-i within 8)
+};
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+// partner value of the lane 16 (swap16) or 32 (swap32) lanes away
+__device__ __forceinline__ int swap16_i(int v) {
+    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+    return (int)((threadIdx.x & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ int swap32_i(int v) {
+    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+    return (int)((threadIdx.x & 32) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float swap16_f(float v) { return __int_as_float(swap16_i(__float_as_int(v))); }
+__device__ __forceinline__ float swap32_f(float v) { return __int_as_float(swap32_i(__float_as_int(v))); }
+
+// Reductions over groups of 8 lanes (i & ~7), 32 lanes and the wavefront;
+// every lane of the group gets the result.
+__device__ __forceinline__ float oct_max(float v) {
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    return fmaxf(v, dpp_f<DPP_HMIRROR>(v));
+}
+__device__ __forceinline__ int oct_sum(int v) {
+    v += dpp_i<DPP_XOR1>(v);
+    v += dpp_i<DPP_XOR2>(v);
+    return v + dpp_i<DPP_HMIRROR>(v);
+}
 __device__ __forceinline__ float half_wave_max(float v) {
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 32));
-    return v;
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_ROR4>(v));
+    v = fmaxf(v, dpp_f<DPP_ROR8>(v));
+    return fmaxf(v, swap16_f(v));
 }
-
 __device__ __forceinline__ int half_wave_sum(int v) {
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 32);
-    return v;
+    v += dpp_i<DPP_XOR1>(v);
+    v += dpp_i<DPP_XOR2>(v);
+    v += dpp_i<DPP_ROR4>(v);
+    v += dpp_i<DPP_ROR8>(v);
+    return v + swap16_i(v);
 }
-
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += dpp_f<DPP_XOR1>(v);
+    v += dpp_f<DPP_XOR2>(v);
+    v += dpp_f<DPP_ROR4>(v);
+    v += dpp_f<DPP_ROR8>(v);
+    v += swap16_f(v);
+    return v + swap32_f(v);
 }
-
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_ROR4>(v));
+    v = fmaxf(v, dpp_f<DPP_ROR8>(v));
+    v = fmaxf(v, swap16_f(v));
+    return fmaxf(v, swap32_f(v));
 }
-
+__device__ __forceinline__ double dpp_d_add(double v, int which) {
+    const long long b = __double_as_longlong(v);
+    int lo = (int)b, hi = (int)(b >> 32);
+    switch (which) {
+        case 0: lo = dpp_i<DPP_XOR1>(lo); hi = dpp_i<DPP_XOR1>(hi); break;
+        case 1: lo = dpp_i<DPP_XOR2>(lo); hi = dpp_i<DPP_XOR2>(hi); break;
+        case 2: lo = dpp_i<DPP_ROR4>(lo); hi = dpp_i<DPP_ROR4>(hi); break;
+        case 3: lo = dpp_i<DPP_ROR8>(lo); hi = dpp_i<DPP_ROR8>(hi); break;
+        case 4: lo = swap16_i(lo); hi = swap16_i(hi); break;
+        default: lo = swap32_i(lo); hi = swap32_i(hi); break;
+    }
+    return v + __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
 __device__ __forceinline__ double wave_sum_d(double v) {
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    for (int w = 0; w < 6; ++w) v = dpp_d_add(v, w);
+    return v;
+}
+// Sum over the lanes r, r+R, r+2R, ... of a wavefront (R = 4..32), for the
+// mat-vec's K lanes of one row; lane r (and every partner) gets the total.
+template <int R>
+__device__ __forceinline__ float fold_rows(float v) {
+    if (R <= 4) v += dpp_f<DPP_ROR4>(v);
+    if (R <= 8) v += dpp_f<DPP_ROR8>(v);
+    if (R <= 16) v += swap16_f(v);
+    if (R <= 32) v += swap32_f(v);
     return v;
 }
 
@@ -116,6 +192,50 @@ __device__ __forceinline__ int quant_block_lane(float x, uint16_t &dbits, int &b
     }
     bsum = half_wave_sum(q);
     return q;
+}
+
+// quantize_q8 of one 32-value block spread over a group of 8 lanes, 4
+// consecutive values per lane (lane i & 7 holds values 4*(i&7) .. +3), with
+// exactly quant_block_lane's rules.  Returns the lane's 4 int8 values packed
+// little-endian; every lane gets the fp16 scale bits and the block sum.
+__device__ __forceinline__ uint32_t quant_block_oct(const float (&x)[4], uint16_t &dbits,
+                                                    int &bsum) {
+    float a = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a = fmaxf(a, fabsf(x[k]));  // NaN ignored
+    const float amax = oct_max(a);
+    const float d = __fdiv_rn(amax, 127.0f);
+    dbits = f2h(d);
+    const float inv = (d == 0.0f) ? 0.0f : __fdiv_rn(1.0f, d);
+    uint32_t packed = 0;
+    int sum = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float y = __fmul_rn(x[k], inv);
+        int q;
+        if (!(fabsf(y) <= 3.0e38f)) {
+            q = -127;
+        } else {
+            q = (int)rintf(fminf(fmaxf(y, -200.0f), 200.0f));
+            q = q > 127 ? 127 : (q < -127 ? -127 : q);
+        }
+        sum += q;
+        packed |= (uint32_t)(q & 0xff) << (8 * k);
+    }
+    bsum = oct_sum(sum);
+    return packed;
+}
+
+// Scale layout of a repacked Q4_0 matrix (n rows, nb blocks per row): tiles
+// of `tile` rows (a power of two), tile-major, so the scales of the rows a
+// mat-vec workgroup owns are one contiguous run per block:
+//   index(row, b) = (row / tile) * nb * tile + b * tile + row % tile.
+// The array holds round_up(n, tile) * nb entries.
+__host__ __device__ __forceinline__ size_t q4_scale_index(int row, int b, int nb, int tile) {
+    return (size_t)(row / tile) * nb * tile + (size_t)b * tile + (row % tile);
+}
+__host__ __device__ __forceinline__ size_t q4_scale_count(int n, int nb, int tile) {
+    return (size_t)((n + tile - 1) / tile) * tile * nb;
 }
 
 // Signed 8-bit 4-way dot product with int32 accumulate (v_dot4_i32_i8).

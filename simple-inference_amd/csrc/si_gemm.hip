@@ -42,7 +42,7 @@ constexpr int BST = 48;   // LDS row stride (bytes) of the B tile, padded
 // per block with the scale product x.d*w.d and the bias added at the end.
 template <bool EXACT>
 __global__ void __launch_bounds__(256) k_gemm_q4q8(
-    const uint8_t *__restrict__ wqs, const uint16_t *__restrict__ wd, int n, int nb,
+    const uint8_t *__restrict__ wqs, const uint16_t *__restrict__ wd, int tile, int n, int nb,
     const int8_t *__restrict__ xqs, const uint16_t *__restrict__ xd, int m,
     const float *__restrict__ bias, const float *__restrict__ residual,
     float *__restrict__ out, int ldo) {
@@ -81,7 +81,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4q8(
             if (a_half == 0) sscale = h2f(xd[(size_t)a_grow * nb + b]);
         } else {
             stage = *(const uint4 *)(wqs + ((size_t)b * n + b_grow) * 16);
-            sscale = h2f(wd[(size_t)b * n + b_grow]);
+            sscale = h2f(wd[q4_scale_index(b_grow, b, nb, tile)]);
         }
     };
     auto store_block = [&]() {
@@ -143,16 +143,17 @@ __global__ void __launch_bounds__(256) k_gemm_q4q8(
         }
 }
 
-void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k, const int8_t *xqs,
+void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
+                      const int8_t *xqs,
                       const uint16_t *xd, int m, const float *bias, const float *residual,
                       float *out, int ldo, bool exact, hipStream_t st) {
     if (m <= 0 || n <= 0) return;
     const dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM);
     if (exact)
-        hipLaunchKernelGGL(k_gemm_q4q8<true>, grid, dim3(256), 0, st, wqs, wd, n, k / SI_QK, xqs,
+        hipLaunchKernelGGL(k_gemm_q4q8<true>, grid, dim3(256), 0, st, wqs, wd, tile, n, k / SI_QK, xqs,
                            xd, m, bias, residual, out, ldo);
     else
-        hipLaunchKernelGGL(k_gemm_q4q8<false>, grid, dim3(256), 0, st, wqs, wd, n, k / SI_QK, xqs,
+        hipLaunchKernelGGL(k_gemm_q4q8<false>, grid, dim3(256), 0, st, wqs, wd, tile, n, k / SI_QK, xqs,
                            xd, m, bias, residual, out, ldo);
 }
 

@@ -12,19 +12,18 @@ void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int ro
                        hipStream_t st);
 void launch_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs, uint16_t *d,
                       int16_t *s, hipStream_t st);
-void launch_q4_repack(const uint8_t *src, int n, int k, uint8_t *qs, uint16_t *d,
+void launch_debug_lane_ops(int *out, hipStream_t st);
+void launch_q4_repack(const uint8_t *src, int n, int k, int tile, uint8_t *qs, uint16_t *d,
                       hipStream_t st);
-void launch_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k, uint8_t *dst,
-                      hipStream_t st);
-void launch_gemv_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k, const int8_t *xqs,
-                      const uint16_t *xd, const int16_t *xs, const float *bias,
-                      const float *residual, float *out, int splits, void *workspace,
-                      hipStream_t st);
-int gemv_effective_splits(int k, int splits);
-size_t gemv_workspace_bytes(int n, int k, int splits);
+void launch_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k, int tile,
+                      uint8_t *dst, hipStream_t st);
+void launch_matvec(const int8_t *xqs, const uint16_t *xd, const int16_t *xs, int k,
+                   const uint8_t *wqs, const uint16_t *wd, int tile, int n, const float *bias,
+                   const float *residual, float *out, bool exact, hipStream_t st);
 void launch_block_dots(const uint8_t *wqs, int n, int k, const int8_t *xqs, const int16_t *xs,
                        int32_t *dots, hipStream_t st);
-void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int n, int k, const int8_t *xqs,
+void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
+                      const int8_t *xqs,
                       const uint16_t *xd, int m, const float *bias, const float *residual,
                       float *out, int ldo, bool exact, hipStream_t st);
 }  // namespace si
@@ -42,4 +41,29 @@ void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
                       const int *ctx_dev, int ctx0, int ctx_step, int max_ctx, float *attn,
                       int8_t *qs, uint16_t *d, int16_t *bsum, void *workspace,
                       hipStream_t st);
+}  // namespace si
+namespace si {
+// fused decode kernels (si_decode.hip)
+void launch_dec_qkv(const float *x, const float *gain, int hidden, float eps, const uint8_t *wqs,
+                    const uint16_t *wd, int tile, int n, const float *bias, float *cap_normed,
+                    int8_t *cap_qs, uint16_t *cap_d, int16_t *cap_s, float *qkv, bool exact,
+                    hipStream_t st);
+void launch_dec_wo(const float *pm, const float *pl, const float *po, int ns, int qheads,
+                   int hdim, const uint8_t *wqs, const uint16_t *wd, int tile, int n,
+                   const float *residual, float *cap_attn, int8_t *cap_qs, uint16_t *cap_d,
+                   int16_t *cap_s, float *cap_y, float *out, bool exact, hipStream_t st);
+void launch_dec_gateup(const float *h, const float *gain, int hidden, float eps,
+                       const uint8_t *wqs, const uint16_t *wd, int tile, int f,
+                       float *cap_normed,
+                       int8_t *cap_qs, uint16_t *cap_d, int16_t *cap_s, float *gu, float *act,
+                       int8_t *aqs, uint16_t *ad, int16_t *as, bool exact, hipStream_t st);
+int dec_attn_chunks(int kvheads, int nq, int max_ctx);
+size_t dec_attn_workspace_bytes(int qheads, int hdim, int kvheads, int nq, int max_ctx);
+void launch_dec_attn(const float *qkv, int ldqkv, int nq, int qheads, int kvheads, int hdim,
+                     const float *rc, const float *rs, uint16_t *kc, uint16_t *vc,
+                     size_t kv_seq_stride, const int *ctx_dev, int ctx0, int max_ctx,
+                     float *q_cap, int ns, void *workspace, float *attn, int8_t *aqs,
+                     uint16_t *ad, int16_t *as, hipStream_t st);
+void launch_attn_combine(int nq, int qheads, int hdim, int nsplit, const void *workspace,
+                         float *attn, int8_t *qs, uint16_t *d, int16_t *bsum, hipStream_t st);
 }  // namespace si

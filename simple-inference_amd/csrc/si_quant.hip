@@ -150,13 +150,13 @@ __global__ void __launch_bounds__(256) k_swiglu_q8(const float *__restrict__ gu,
 }
 
 // Row-major 18-byte Q4_0 blocks -> [K/32][N][16] nibbles + [K/32][N] scales.
-__global__ void k_q4_repack(const uint8_t *__restrict__ src, int n, int nb,
+__global__ void k_q4_repack(const uint8_t *__restrict__ src, int n, int nb, int tile,
                             uint8_t *__restrict__ qs, uint16_t *__restrict__ d) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // i = b*n + row
     if (i >= (size_t)n * nb) return;
     const int b = (int)(i / n), row = (int)(i - (size_t)b * n);
     const uint8_t *blk = src + ((size_t)row * nb + b) * 18;
-    d[i] = (uint16_t)(blk[0] | (blk[1] << 8));
+    d[q4_scale_index(row, b, nb, tile)] = (uint16_t)(blk[0] | (blk[1] << 8));
     uint32_t w[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -166,14 +166,44 @@ __global__ void k_q4_repack(const uint8_t *__restrict__ src, int n, int nb,
 }
 
 __global__ void k_q4_unpack(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ d,
-                            int n, int nb, uint8_t *__restrict__ dst) {
+                            int n, int nb, int tile, uint8_t *__restrict__ dst) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (size_t)n * nb) return;
     const int b = (int)(i / n), row = (int)(i - (size_t)b * n);
     uint8_t *blk = dst + ((size_t)row * nb + b) * 18;
-    blk[0] = (uint8_t)(d[i] & 0xff);
-    blk[1] = (uint8_t)(d[i] >> 8);
+    const uint16_t dv = d[q4_scale_index(row, b, nb, tile)];
+    blk[0] = (uint8_t)(dv & 0xff);
+    blk[1] = (uint8_t)(dv >> 8);
     for (int t = 0; t < 16; ++t) blk[2 + t] = qs[i * 16 + t];
+}
+
+// Test entry for the cross-lane helpers of si_device.hpp: every lane feeds
+// its lane index; out[k*64 + lane] is what lane received from operation k.
+__global__ void __launch_bounds__(64) k_debug_lane_ops(int *__restrict__ out) {
+    const int l = threadIdx.x;
+    const float f = (float)l;
+    out[0 * 64 + l] = dpp_i<DPP_XOR1>(l);
+    out[1 * 64 + l] = dpp_i<DPP_XOR2>(l);
+    out[2 * 64 + l] = dpp_i<DPP_ROR4>(l);
+    out[3 * 64 + l] = dpp_i<DPP_ROR8>(l);
+    out[4 * 64 + l] = dpp_i<DPP_HMIRROR>(l);
+    out[5 * 64 + l] = swap16_i(l);
+    out[6 * 64 + l] = swap32_i(l);
+    out[7 * 64 + l] = oct_sum(l);
+    out[8 * 64 + l] = half_wave_sum(l);
+    out[9 * 64 + l] = (int)wave_sum(f);
+    out[10 * 64 + l] = (int)half_wave_max(f);
+    out[11 * 64 + l] = (int)wave_max(f);
+    out[12 * 64 + l] = (int)oct_max(f);
+    out[13 * 64 + l] = (int)fold_rows<4>(f);
+    out[14 * 64 + l] = (int)fold_rows<8>(f);
+    out[15 * 64 + l] = (int)fold_rows<16>(f);
+    out[16 * 64 + l] = (int)fold_rows<32>(f);
+    out[17 * 64 + l] = (int)wave_sum_d((double)l);
+}
+
+void launch_debug_lane_ops(int *out, hipStream_t st) {
+    hipLaunchKernelGGL(k_debug_lane_ops, dim3(1), dim3(64), 0, st, out);
 }
 
 // ----------------------------------------------------------------------
@@ -215,20 +245,20 @@ void launch_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs, 
                        qs, d, s);
 }
 
-void launch_q4_repack(const uint8_t *src, int n, int k, uint8_t *qs, uint16_t *d,
+void launch_q4_repack(const uint8_t *src, int n, int k, int tile, uint8_t *qs, uint16_t *d,
                       hipStream_t st) {
     const size_t tot = (size_t)n * (k / SI_QK);
     if (!tot) return;
     hipLaunchKernelGGL(k_q4_repack, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, src,
-                       n, k / SI_QK, qs, d);
+                       n, k / SI_QK, tile, qs, d);
 }
 
-void launch_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k, uint8_t *dst,
-                      hipStream_t st) {
+void launch_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k, int tile,
+                      uint8_t *dst, hipStream_t st) {
     const size_t tot = (size_t)n * (k / SI_QK);
     if (!tot) return;
     hipLaunchKernelGGL(k_q4_unpack, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, qs,
-                       d, n, k / SI_QK, dst);
+                       d, n, k / SI_QK, tile, dst);
 }
 
 }  // namespace si

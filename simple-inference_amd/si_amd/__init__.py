@@ -68,16 +68,17 @@ class LayerHost(ctypes.Structure):
 
 _SIGS = {
     "si_last_error": (ctypes.c_char_p, []),
-    "si_q4_repack": (_I, [_P, _I, _I, _P, _P, _P]),
-    "si_q4_unpack": (_I, [_P, _P, _I, _I, _P, _P]),
+    "si_q4_repack": (_I, [_P, _I, _I, _I, _P, _P, _P]),
+    "si_q4_unpack": (_I, [_P, _P, _I, _I, _I, _P, _P]),
+    "si_q4_tile": (_I, [_I, _I]),
+    "si_q4_scale_count": (_Z, [_I, _I, _I]),
     "si_quantize_q8": (_I, [_P, _P, _I, _P]),
     "si_quantize_q8_rows": (_I, [_P, _I, _I, _P, _P, _P, _P]),
     "si_rmsnorm_q8": (_I, [_P, _P, _I, _I, _F, _P, _P, _P, _P, _P]),
     "si_residual_rmsnorm_q8": (_I, [_P, _P, _P, _I, _I, _F, _P, _P, _P, _P, _P, _P]),
     "si_q4q8_block_dots": (_I, [_P, _P, _I, _I, _P, _P, _P, _P]),
-    "si_matvec_q4q8": (_I, [_P, _P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P]),
-    "si_matvec_workspace": (_Z, [_I, _I, _I]),
-    "si_gemm_q4q8": (_I, [_P, _P, _I, _I, _P, _P, _I, _P, _P, _P, _I, _I, _P]),
+    "si_matvec_q4q8": (_I, [_P, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P]),
+    "si_gemm_q4q8": (_I, [_P, _P, _I, _I, _I, _P, _P, _I, _P, _P, _P, _I, _I, _P]),
     "si_rope_kv_append": (_I, [ctypes.POINTER(Shape), _P, _I, _I, _I, _I, _I, _P, _P, _P, _P,
                                _P, _P, _Z, _P]),
     "si_rope_table": (_I, [_I, _I, _F, _P, _P]),
@@ -86,9 +87,13 @@ _SIGS = {
     "si_attention_workspace": (_Z, [ctypes.POINTER(Shape), _I, _I]),
     "si_swiglu_q8": (_I, [_P, _I, _I, _P, _P, _P, _P, _P]),
     "si_debug_mfma_f16": (_I, [_P, _P, _P, _P, _P]),
+    "si_debug_lane_ops": (_I, [_P, _P]),
     "si_layer_create": (_I, [ctypes.POINTER(Shape), ctypes.POINTER(LayerHost), _I, _I,
                              ctypes.POINTER(_P)]),
     "si_layer_destroy": (_I, [_P]),
+    "si_workspace_create": (_I, [ctypes.POINTER(Shape), _I, _I, ctypes.POINTER(_P)]),
+    "si_workspace_destroy": (_I, [_P]),
+    "si_layer_create_in": (_I, [_P, ctypes.POINTER(LayerHost), ctypes.POINTER(_P)]),
     "si_layer_decode": (_I, [_P, _P, _P, _P, _I, _P, _I, _P]),
     "si_layer_decode_batch": (_I, [_P, _P, _I, _P, _P, _Z, _P, _I, _I, _P, _I, _P]),
     "si_layer_prefill": (_I, [_P, _P, _I, _I, _P, _P, _P, _I, _P]),
@@ -96,7 +101,7 @@ _SIGS = {
     "si_layer_set_timing": (_I, [_P, _I]),
     "si_layer_phase_ms": (_I, [_P, _P]),
     "si_layer_weights": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P),
-                              ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+                              ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
 }
 
 _lib = None
@@ -181,16 +186,42 @@ def declared_functions():
     return names
 
 
-class Layer:
-    """si_layer_t owner built from host tensors (dict of numpy arrays)."""
+class Workspace:
+    """si_workspace_t owner: activation buffers shared by the layers of a model."""
 
-    def __init__(self, shape, tensors, max_tokens, max_pos):
+    def __init__(self, shape, max_tokens, max_pos):
+        self.shape, self.max_tokens, self.max_pos = shape, max_tokens, max_pos
+        h = _P()
+        call("si_workspace_create", ctypes.byref(shape), max_tokens, max_pos, ctypes.byref(h))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().si_workspace_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Layer:
+    """si_layer_t owner built from host tensors (dict of numpy arrays), on a
+    private workspace or on a shared Workspace."""
+
+    def __init__(self, shape, tensors, max_tokens=None, max_pos=None, workspace=None):
         self.shape = shape
         self._keep = {k: np.ascontiguousarray(v) for k, v in tensors.items() if v is not None}
         host = LayerHost(**{k: v.ctypes.data for k, v in self._keep.items()})
         h = _P()
-        call("si_layer_create", ctypes.byref(shape), ctypes.byref(host), max_tokens, max_pos,
-             ctypes.byref(h))
+        if workspace is not None:
+            call("si_layer_create_in", workspace.h, ctypes.byref(host), ctypes.byref(h))
+            max_tokens, max_pos = workspace.max_tokens, workspace.max_pos
+        else:
+            call("si_layer_create", ctypes.byref(shape), ctypes.byref(host), max_tokens, max_pos,
+                 ctypes.byref(h))
         self.h = h
         self.max_tokens, self.max_pos = max_tokens, max_pos
 
@@ -209,10 +240,11 @@ class Layer:
         return lib().si_layer_buffer(self.h, BUF[name])
 
     def weights(self, which):
-        qs, d, n, k = _P(), _P(), _I(), _I()
+        """(qs, d, tile, n, k) device pointers and shape of matrix `which`."""
+        qs, d, tile, n, k = _P(), _P(), _I(), _I(), _I()
         call("si_layer_weights", self.h, which, ctypes.byref(qs), ctypes.byref(d),
-             ctypes.byref(n), ctypes.byref(k))
-        return qs.value, d.value, n.value, k.value
+             ctypes.byref(tile), ctypes.byref(n), ctypes.byref(k))
+        return qs.value, d.value, tile.value, n.value, k.value
 
     def decode(self, x, kc, vc, context, out, flags=SI_LAYER_FULL, stream=None):
         call("si_layer_decode", self.h, ptr(x), ptr(kc), ptr(vc), context, ptr(out), flags,

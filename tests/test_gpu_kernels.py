@@ -155,29 +155,40 @@ def test_swiglu_q8(oracle):
     assert np.array_equal(host(qs), wq) and np.array_equal(host(d).view(np.uint16), wd)
 
 
-def _upload_q4(w_rowmajor, n, k):
+def _upload_q4(w_rowmajor, n, k, tile=None):
+    """Repack row-major Q4_0 on the device; returns (qs, d, tile)."""
     torch = _torch()
-    qs, d = empty(n * k // 2, torch.uint8), empty(n * k // 32, torch.int16)
-    si_amd.call("si_q4_repack", si_amd.ptr(dev(w_rowmajor)), n, k, si_amd.ptr(qs),
+    L = si_amd.lib()
+    tile = tile or L.si_q4_tile(n, k)
+    qs = empty(n * k // 2, torch.uint8)
+    d = zeros(L.si_q4_scale_count(n, k, tile), torch.int16)
+    si_amd.call("si_q4_repack", si_amd.ptr(dev(w_rowmajor)), n, k, tile, si_amd.ptr(qs),
                 si_amd.ptr(d), None)
-    return qs, d
+    return qs, d, tile
 
 
-def test_q4_repack_round_trip(oracle):
+@pytest.mark.parametrize("tile", [8, 16, 32, 64])
+def test_q4_repack_round_trip(oracle, tile):
     torch = _torch()
     rng = np.random.default_rng(2)
-    n, k = 300, 1024
+    n, k = 300, 1024  # 300 rows: the last scale tile is partial for every tile size
     w = q4(oracle, rng, n, k)
-    qs, d = _upload_q4(w, n, k)
+    qs, d, _ = _upload_q4(w, n, k, tile)
     back = empty(w.size, torch.uint8)
-    si_amd.call("si_q4_unpack", si_amd.ptr(qs), si_amd.ptr(d), n, k, si_amd.ptr(back), None)
+    si_amd.call("si_q4_unpack", si_amd.ptr(qs), si_amd.ptr(d), n, k, tile, si_amd.ptr(back),
+                None)
     assert np.array_equal(host(back), w.reshape(-1))
-    # the repacked layout: block-major nibbles and scales
-    hq = host(qs).reshape(k // 32, n, 16)
-    blocks = w.reshape(n, k // 32, 18)
+    # the repacked layout: block-major nibbles, tile-major scales
+    nb = k // 32
+    hq = host(qs).reshape(nb, n, 16)
+    blocks = w.reshape(n, nb, 18)
     assert np.array_equal(hq, blocks[:, :, 2:].transpose(1, 0, 2))
-    assert np.array_equal(host(d).view(np.uint16).reshape(k // 32, n),
-                          blocks[:, :, :2].copy().view(np.uint16)[..., 0].T)
+    scales = blocks[:, :, :2].copy().view(np.uint16)[..., 0]  # [n][nb]
+    npad = -(-n // tile) * tile
+    padded = np.zeros((npad, nb), np.uint16)
+    padded[:n] = scales
+    want = padded.reshape(npad // tile, tile, nb).transpose(0, 2, 1).reshape(-1)
+    assert np.array_equal(host(d).view(np.uint16), want)
 
 
 def _q8_dev(oracle, x):
@@ -195,7 +206,7 @@ def test_block_dots_bit_exact(oracle, n, k):
     x = (rng.standard_normal(k) * 2).astype(np.float32)
     x[:32] = 1000.0  # q = +127 block
     xq, xqs, xd, xs = _q8_dev(oracle, x)
-    wqs, wd = _upload_q4(w, n, k)
+    wqs, wd, tile = _upload_q4(w, n, k)
     dots = empty(n * (k // 32), torch.int32)
     si_amd.call("si_q4q8_block_dots", si_amd.ptr(wqs), si_amd.ptr(wd), n, k, si_amd.ptr(xqs),
                 si_amd.ptr(xs), si_amd.ptr(dots), None)
@@ -213,33 +224,42 @@ def test_matvec_exact_single_range(oracle, n, k, bias):
     x = rng.standard_normal(k).astype(np.float32)
     b = rng.normal(0, 0.02, n).astype(np.float32) if bias else None
     xq, xqs, xd, xs = _q8_dev(oracle, x)
-    wqs, wd = _upload_q4(w, n, k)
+    wqs, wd, tile = _upload_q4(w, n, k)
     out = empty(n, torch.float32)
-    si_amd.call("si_matvec_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), n, k, si_amd.ptr(xqs),
+    si_amd.call("si_matvec_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), tile, n, k, si_amd.ptr(xqs),
                 si_amd.ptr(xd), si_amd.ptr(xs), si_amd.ptr(None if b is None else dev(b)), None,
-                si_amd.ptr(out), 1, None, None)
+                si_amd.ptr(out), si_amd.SI_GEMM_EXACT, None)
     want = oracle.matvec(w, xq, k, n, b)
     assert np.array_equal(host(out).view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("n,k,splits", [(1152, 896, 7), (896, 4864, 19), (3584, 18944, 37)])
-def test_matvec_split_ranges(oracle, n, k, splits):
+@pytest.mark.parametrize("n,k,tile", [(1152, 896, 8), (896, 4864, 8), (3584, 18944, 8),
+                                      (37888, 3584, 32), (4608, 3584, 16), (9728, 896, 64),
+                                      (96, 64, 8), (200, 96, 64), (77, 160, 16)])
+def test_matvec_parallel_k(oracle, n, k, tile):
+    """K spread over the workgroup (every row-count variant): fp32 rounding of
+    the reference, identical results on repeated calls (fixed order)."""
     torch = _torch()
-    rng = np.random.default_rng(n + splits)
+    rng = np.random.default_rng(n + k)
     w = q4(oracle, rng, n, k)
     x = rng.standard_normal(k).astype(np.float32)
     b = rng.normal(0, 0.02, n).astype(np.float32)
     res = rng.standard_normal(n).astype(np.float32)
     xq, xqs, xd, xs = _q8_dev(oracle, x)
-    wqs, wd = _upload_q4(w, n, k)
-    out = empty(n, torch.float32)
-    ws = zeros(si_amd.lib().si_matvec_workspace(n, k, splits), torch.uint8)
-    for rep in range(2):  # the workspace is left ready for the next call
-        si_amd.call("si_matvec_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), n, k, si_amd.ptr(xqs),
+    wqs, wd, tile = _upload_q4(w, n, k, tile)
+    want = res + oracle.matvec(w, xq, k, n, b)
+    first = None
+    for rep in range(2):
+        out = empty(n, torch.float32)
+        si_amd.call("si_matvec_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), tile, n, k, si_amd.ptr(xqs),
                     si_amd.ptr(xd), si_amd.ptr(xs), si_amd.ptr(dev(b)), si_amd.ptr(dev(res)),
-                    si_amd.ptr(out), splits, si_amd.ptr(ws), None)
-        want = res + oracle.matvec(w, xq, k, n, b)
-        close(host(out), want, 1e-5, f"split matvec call {rep}")
+                    si_amd.ptr(out), 0, None)
+        got = host(out)
+        close(got, want, 1e-5, f"matvec call {rep}")
+        if first is None:
+            first = got
+        else:
+            assert np.array_equal(first.view(np.uint32), got.view(np.uint32)), "not deterministic"
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 64, 64), (5, 200, 96), (64, 1152, 896),
@@ -252,9 +272,9 @@ def test_gemm_matches_oracle_rows(oracle, m, n, k):
     b = rng.normal(0, 0.02, n).astype(np.float32)
     xq = oracle.quantize_q8(x)
     qs, d, _ = aos_to_planar(xq)
-    wqs, wd = _upload_q4(w, n, k)
+    wqs, wd, tile = _upload_q4(w, n, k)
     out = empty(m * n, torch.float32)
-    si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), n, k, si_amd.ptr(dev(qs)),
+    si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), tile, n, k, si_amd.ptr(dev(qs)),
                 si_amd.ptr(dev(d.view(np.int16))), m, si_amd.ptr(dev(b)), None,
                 si_amd.ptr(out), n, 0, None)
     got = host(out).reshape(m, n)
@@ -275,9 +295,9 @@ def test_gemm_every_row_vs_float64(oracle, m, n, k):
     x = rng.standard_normal((m, k)).astype(np.float32)
     xq = oracle.quantize_q8(x)
     qs, d, _ = aos_to_planar(xq)
-    wqs, wd = _upload_q4(w, n, k)
+    wqs, wd, tile = _upload_q4(w, n, k)
     out = empty(m * n, torch.float32)
-    si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), n, k, si_amd.ptr(dev(qs)),
+    si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), tile, n, k, si_amd.ptr(dev(qs)),
                 si_amd.ptr(dev(d.view(np.int16))), m, None, None, si_amd.ptr(out), n, 0, None)
     got = host(out).reshape(m, n)
     want = dequant_q8(xq, m, k) @ dequant_q4(w, n, k).T
@@ -297,9 +317,9 @@ def test_gemm_residual(oracle):
     res = rng.standard_normal((m, n)).astype(np.float32)
     xq = oracle.quantize_q8(x)
     qs, d, _ = aos_to_planar(xq)
-    wqs, wd = _upload_q4(w, n, k)
+    wqs, wd, tile = _upload_q4(w, n, k)
     out = empty(m * n, torch.float32)
-    si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), n, k, si_amd.ptr(dev(qs)),
+    si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), tile, n, k, si_amd.ptr(dev(qs)),
                 si_amd.ptr(dev(d.view(np.int16))), m, None, si_amd.ptr(dev(res)),
                 si_amd.ptr(out), n, 0, None)
     got = host(out).reshape(m, n)
@@ -435,3 +455,34 @@ def test_mfma_f16_lane_layouts():
     af, bf = a.astype(np.float64), b.astype(np.float64)
     assert np.array_equal(host(d32).reshape(16, 16), af @ bf)
     assert np.array_equal(host(d16).reshape(16, 16), af[:, :16] @ bf[:16, :])
+
+
+def test_cross_lane_ops_layouts():
+    """The DPP / permlane moves behind every in-kernel reduction, checked
+    against their documented lane maps."""
+    torch = _torch()
+    out = zeros(18 * 64, torch.int32)
+    si_amd.call("si_debug_lane_ops", si_amd.ptr(out), None)
+    got = host(out).reshape(18, 64)
+    lane = np.arange(64)
+    row0 = lane & ~15
+    expect = {
+        0: lane ^ 1, 1: lane ^ 2,
+        2: row0 + ((lane - 4) & 15), 3: row0 + ((lane - 8) & 15),
+        4: (lane & ~7) + 7 - (lane & 7),
+        5: lane ^ 16, 6: lane ^ 32,
+    }
+    for k, want in expect.items():
+        assert np.array_equal(got[k], want), f"op {k}: {got[k]}"
+    grp = lambda size: np.repeat(lane.reshape(-1, size).sum(1), size)
+    gmax = lambda size: np.repeat(lane.reshape(-1, size).max(1), size)
+    assert np.array_equal(got[7], grp(8)), "oct_sum"
+    assert np.array_equal(got[8], grp(32)), "half_wave_sum"
+    assert np.array_equal(got[9], grp(64)), "wave_sum"
+    assert np.array_equal(got[10], gmax(32)), "half_wave_max"
+    assert np.array_equal(got[11], gmax(64)), "wave_max"
+    assert np.array_equal(got[12], gmax(8)), "oct_max"
+    for k, r in ((13, 4), (14, 8), (15, 16), (16, 32)):
+        want = np.array([lane[lane % r == l % r].sum() for l in lane])
+        assert np.array_equal(got[k], want), f"fold_rows<{r}>"
+    assert np.array_equal(got[17], grp(64)), "wave_sum_d"

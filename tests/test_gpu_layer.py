@@ -82,6 +82,62 @@ def test_decode_full_layer_0_5b_ctx1024(oracle, flags):
     L.close()
 
 
+@pytest.mark.parametrize("shape,ctx", [("0.5b", 1), ("0.5b", 2), ("0.5b", 16), ("0.5b", 17),
+                                       ("0.5b", 129), ("0.5b", 500), ("7b", 33), ("7b", 4096)])
+def test_decode_contexts(oracle, shape, ctx):
+    """Single-token decode over contexts that put the new token at every kind
+    of place in the attention chunks (first tile, tile edge, last chunk)."""
+    torch = _torch()
+    s, os_ = _shapes(shape)
+    lay = make_layer(oracle, os_, 40 + ctx)
+    kvd = s.kvheads * s.hdim
+    rng = np.random.default_rng(ctx)
+    kc0 = kv_history(oracle, rng, ctx, kvd)
+    vc0 = kv_history(oracle, rng, ctx, kvd)
+    x = rng.standard_normal(s.hidden).astype(np.float32)
+    L = si_amd.Layer(s, lay, 1, ctx)
+    for flags in (si_amd.SI_LAYER_FULL, EXACT):
+        kc, vc = dev(kc0.view(np.int16)), dev(vc0.view(np.int16))
+        out = empty(s.hidden, torch.float32)
+        L.decode(dev(x), kc, vc, ctx, out, flags)
+        B = LayerBuffers(L, os_, 1)
+        hk, hv = host(kc).view(np.uint16), host(vc).view(np.uint16)
+        check_row(oracle, os_, lay, x, 0, B, hk, hv, 0, ctx - 1, ctx, host(out), flags == EXACT)
+    L.close()
+
+
+def test_shared_workspace_layers(oracle):
+    """Layers created on one workspace give the same bits as layers with
+    private workspaces, when their calls interleave."""
+    torch = _torch()
+    s, os_ = _shapes("0.5b")
+    ctx = 300
+    kvd = s.kvheads * s.hdim
+    rng = np.random.default_rng(9)
+    lays = [make_layer(oracle, os_, 70 + i) for i in range(2)]
+    ws = si_amd.Workspace(s, 1, ctx)
+    shared = [si_amd.Layer(s, lay, workspace=ws) for lay in lays]
+    ws.close()  # the layers keep the workspace alive
+    private = [si_amd.Layer(s, lay, 1, ctx) for lay in lays]
+    caches = [(kv_history(oracle, rng, ctx, kvd), kv_history(oracle, rng, ctx, kvd))
+              for _ in range(2)]
+    x = rng.standard_normal(s.hidden).astype(np.float32)
+    outs = {}
+    for name, layers in (("shared", shared), ("private", private)):
+        for rep in range(2):
+            for i in (0, 1):
+                kc, vc = (dev(c.view(np.int16)) for c in caches[i])
+                out = empty(s.hidden, torch.float32)
+                layers[i].decode(dev(x), kc, vc, ctx, out)
+                outs[(name, rep, i)] = (host(out), host(kc), host(vc))
+    for rep in range(2):
+        for i in (0, 1):
+            for a, b in zip(outs[("shared", rep, i)], outs[("private", rep, i)]):
+                assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+    for L in shared + private:
+        L.close()
+
+
 def _prefill_case(oracle, shape, ntok, prefix, seed, flags, rows):
     torch = _torch()
     s, os_ = _shapes(shape)

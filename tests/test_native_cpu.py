@@ -42,10 +42,15 @@ def test_argument_errors_do_not_launch():
     L = si_amd.lib()
     assert L.si_quantize_q8(None, None, 33, None) == si_amd.SI_ERR_ARG
     assert b"multiple of 32" in L.si_last_error()
-    assert L.si_gemm_q4q8(None, None, 64, 30, None, None, 4, None, None, None, 64, 0,
+    assert L.si_gemm_q4q8(None, None, 8, 64, 30, None, None, 4, None, None, None, 64, 0,
                           None) == si_amd.SI_ERR_ARG
-    assert L.si_matvec_q4q8(None, None, 64, 64, None, None, None, None, None, None, 1, None,
+    assert L.si_matvec_q4q8(None, None, 8, 64, 64, None, None, None, None, None, None, 0,
                             None) == si_amd.SI_ERR_ARG
+    assert L.si_matvec_q4q8(None, None, 12, 64, 64, None, None, None, None, None, None, 0,
+                            None) == si_amd.SI_ERR_ARG
+    assert b"tile 12" in L.si_last_error()
+    assert L.si_q4_scale_count(300, 64, 16) == 304 * 2
+    assert L.si_q4_tile(37888, 3584) == 32 and L.si_q4_tile(896, 896) == 8
     bad = si_amd.make_shape(896, 14, 3, 64)  # 14 % 3 != 0
     assert L.si_rope_kv_append(ctypes.byref(bad), None, 0, 0, 0, 0, 1, None, None, None, None,
                                None, None, 0, None) == si_amd.SI_ERR_ARG
@@ -58,6 +63,8 @@ def test_argument_errors_do_not_launch():
     assert L.si_layer_create(ctypes.byref(s), ctypes.byref(host), 1, 16,
                              ctypes.byref(h)) == si_amd.SI_ERR_ARG
     assert L.si_layer_decode(None, None, None, None, 1, None, 0, None) == si_amd.SI_ERR_ARG
+    assert L.si_layer_create_in(None, ctypes.byref(host), ctypes.byref(h)) == si_amd.SI_ERR_ARG
+    assert L.si_workspace_create(ctypes.byref(bad), 1, 16, ctypes.byref(h)) == si_amd.SI_ERR_ARG
 
 
 def test_attention_workspace_sizing():
