@@ -489,10 +489,14 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
         }
     }
     // 2. the wavefront's first K and V tile
+    // 2. the wavefront's first two K and V tiles (two in flight throughout)
+    constexpr int STEP = DA_TILE * NW;
     int t0 = p0 + DA_TILE * wave;
-    uint4 kr[KS], vr[VL];
-    load_k(t0, kr);
-    load_v(t0, vr);
+    uint4 kA[KS], vA[VL], kB[KS], vB[VL];
+    load_k(t0, kA);
+    load_v(t0, vA);
+    load_k(t0 + STEP, kB);
+    load_v(t0 + STEP, vB);
 #pragma unroll
     for (int u = 0; u < RAWPT; ++u) {
         const int i = tid + u * NW * 64;
@@ -516,24 +520,44 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
             vc[sbase + (size_t)pnew * kvd + g * D + dd] = vh;
         }
     }
-    // Q^T as the B operand: lane holds Q[head col][d = 32*ks + 8*grp + e]
+    // Q^T as the B operand: lane holds Q[head col][d = 32*ks + 8*grp + e],
+    // rotated from 8 consecutive pairs read as 16-byte LDS vectors
     h8 qh[KS], ql[KS];
     {
         const bool hv = col < per && pnew >= 0;
         const int hc = col < per ? col : 0;
         const bool capq = q_cap && sp == 0 && wave == 0 && hv;
+        const float *qh_row = qraw + hc * D;
+        auto ld8 = [](const float *p, float (&v)[8]) {
+            const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        };
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
+        for (int ks = 0; ks < KS; ++ks) {
+            const int d0 = 32 * ks + 8 * grp;
+            const int i0 = d0 < HALF ? d0 : d0 - HALF;
+            float a[8], b[8], c[8], sn[8], v[8];
+            ld8(qh_row + i0, a);
+            ld8(qh_row + i0 + HALF, b);
+            ld8(csr + i0, c);
+            ld8(csr + HALF + i0, sn);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const int dd = 32 * ks + 8 * grp + e;
-                const float v = hv ? rot(qraw + hc * D, dd) : 0.0f;
-                if (capq) q_cap[(size_t)qi * qd + (size_t)(g * per + hc) * D + dd] = v;
+                v[e] = !hv ? 0.0f
+                           : (d0 < HALF ? __fsub_rn(__fmul_rn(a[e], c[e]), __fmul_rn(b[e], sn[e]))
+                                        : __fadd_rn(__fmul_rn(b[e], c[e]), __fmul_rn(a[e], sn[e])));
                 _Float16 hi, lo;
-                hi_lo(v, hi, lo);
+                hi_lo(v[e], hi, lo);
                 qh[ks][e] = hi;
                 ql[ks][e] = lo;
             }
+            if (capq) {
+                float *qc = q_cap + (size_t)qi * qd + (size_t)(g * per + hc) * D + d0;
+                *(float4 *)qc = make_float4(v[0], v[1], v[2], v[3]);
+                *(float4 *)(qc + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            }
+        }
     }
     __syncthreads();  // newk/newv visible; the raw rows are no longer read
 
@@ -542,7 +566,8 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[dt] = (f4){0.f, 0.f, 0.f, 0.f};
 
-    for (; t0 < p1; t0 += DA_TILE * NW) {
+    // one 16-position tile: scores, online softmax, weighted V sum
+    auto tile = [&](int t0, uint4(&kr)[KS], uint4(&vr)[VL]) {
         fix(t0, kr, vr);
         // stage V rows into this wavefront's LDS rows
 #pragma unroll
@@ -554,10 +579,6 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
         h8 ka[KS];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) ka[ks] = __builtin_bit_cast(h8, kr[ks]);
-        // prefetch the wavefront's next tile
-        const int tn = t0 + DA_TILE * NW;
-        load_k(tn, kr);  // (past the chunk on the last tile: unused)
-        load_v(tn, vr);
         f4 sacc = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
@@ -613,6 +634,17 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    // tiles t0, t0 + STEP, ... alternate between the A and B registers; each
+    // is refilled two tiles ahead once consumed (past the chunk: unused)
+    for (; t0 < p1; t0 += 2 * STEP) {
+        tile(t0, kA, vA);
+        load_k(t0 + 2 * STEP, kA);
+        load_v(t0 + 2 * STEP, vA);
+        if (t0 + STEP >= p1) break;
+        tile(t0 + STEP, kB, vB);
+        load_k(t0 + 3 * STEP, kB);
+        load_v(t0 + 3 * STEP, vB);
     }
 
     // merge the NW wavefront states in LDS (reusing the V rows)
