@@ -32,6 +32,11 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, GB/s
 INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA, TOP/s
 MALL_BYTES = 256 << 20      # Infinity Cache
 METRIC = "decode layer µs + HBM GB/s; prefill tokens/s + int8 MFMA % (one GPU)"
+# HBM bytes per launch of the dominant kernel (k_dec_gateup, 0.5B), from two
+# rocprofv3 --pmc runs of `bench.py --dominant-only` (FETCH_SIZE 2497.0 KiB,
+# WRITE_SIZE 9.8 KiB per dispatch, medians) scaled by what the counters read
+# for a 256 MiB copy (FETCH_SIZE x2.000, WRITE_SIZE x1.000).
+DOMINANT_TRAFFIC_BYTES = (2497.0 * 2.000 + 9.8 * 1.000) * 1024
 
 
 def log(*a):
@@ -185,49 +190,50 @@ def bench_decode_layer(torch, si_amd, stream, steps, warmup, ctx=1024):
     return res, (layers, caches, s, x, ws)
 
 
-def bench_dominant_gemv(torch, si_amd, stream, ctxobj, launches=400):
-    """Roofline of the decode step's dominant kernel: the fused gate|up
-    mat-vec shape (4.9 MB of the layer's 8.9 MB) as k_matvec, launched alone on the
-    bench stream, cycling through enough repacked copies of that matrix to
-    exceed the Infinity Cache (cold weights)."""
-    layers, caches, s, x, _ = ctxobj
+def bench_dominant_kernel(torch, si_amd, stream, launches=400):
+    """Roofline of the decode step's dominant kernel: k_dec_gateup, the fused
+    post-norm -> Q8 -> gate|up mat-vec -> SwiGLU -> Q8 stage that moves 4.9 MB
+    of the 0.5B layer's 8.9 MB, launched alone (si_ffn_gateup_q8) on the bench
+    stream, cycling through enough copies of its weights to exceed the
+    Infinity Cache (cold weights, as in the layer)."""
     L = si_amd.lib()
+    s = si_amd.make_shape(**si_amd.SHAPES["0.5b"])
     F, H = s.ffn, s.hidden
     n, k = 2 * F, H
     per = n * k // 32 * 18
     ncopy = int(np.ceil(1.25 * MALL_BYTES / per))
-    src_qs, src_d, _, _, _ = layers[0].weights(2)
-    tile = L.si_q4_tile(n, k)  # stand-alone mat-vec tile (the layer pairs gate|up rows)
-    nd = L.si_q4_scale_count(n, k, tile)
+    gen = torch.Generator(device="cuda").manual_seed(21)
+    nd = L.si_q4_scale_count(n, k, 32)
     mats = []
     for _ in range(ncopy):
-        qs = torch.empty(n * k // 2, dtype=torch.uint8, device="cuda")
-        d = torch.full((nd,), 0x2000, dtype=torch.int16, device="cuda")
-        qs.copy_(si_amd_view(torch, src_qs, n * k // 2, torch.uint8))
-        mats.append((qs.data_ptr(), d.data_ptr(), n, k, qs, d))
-    xq = torch.randint(-127, 128, (k,), dtype=torch.int8, device="cuda")
-    xd = torch.full((k // 32,), 0x2c00, dtype=torch.int16, device="cuda")  # fp16 0.0625
-    xs = xq.view(-1, 32).sum(1, dtype=torch.int32).to(torch.int16)
-    out = torch.empty(n, device="cuda")
+        qs = torch.randint(0, 256, (n * k // 2,), generator=gen, device="cuda", dtype=torch.uint8)
+        d = torch.full((nd,), 0x2000, dtype=torch.int16, device="cuda")  # fp16 2^-7
+        mats.append((qs, d))
+    h = torch.randn(H, generator=gen, device="cuda")
+    gain = torch.ones(H, device="cuda")
+    aq = torch.empty(F, dtype=torch.int8, device="cuda")
+    ad = torch.empty(F // 32, dtype=torch.int16, device="cuda")
+    asum = torch.empty(F // 32, dtype=torch.int16, device="cuda")
 
     def launch(i):
-        qs, d, nn, kk = mats[i % len(mats)][:4]
-        rc = L.si_matvec_q4q8(ctypes.c_void_p(qs), ctypes.c_void_p(d), tile, nn, kk,
-                              si_amd.ptr(xq),
-                              si_amd.ptr(xd), si_amd.ptr(xs), None, None, si_amd.ptr(out), 0,
-                              si_amd.stream_handle(torch.cuda.current_stream()))
+        qs, d = mats[i % ncopy]
+        rc = L.si_ffn_gateup_q8(si_amd.ptr(h), si_amd.ptr(gain), H, ctypes.c_float(1e-6),
+                                si_amd.ptr(qs), si_amd.ptr(d), 32, F, None, si_amd.ptr(aq),
+                                si_amd.ptr(ad), si_amd.ptr(asum), 0,
+                                si_amd.stream_handle(torch.cuda.current_stream()))
         if rc:
             raise si_amd.SiError(rc, L.si_last_error().decode())
 
     with torch.cuda.stream(stream):
-        for i in range(20):
+        for i in range(ncopy + 5):
             launch(i)
     torch.cuda.synchronize()
     ms = graph_time_ms(torch, stream, launch, launches, replays=3)
-    alg = n * k // 32 * 18 + k + (k // 32) * 4 + n * 4
+    # weights + h + gain in, Q8 activation (values, scales, sums) out
+    alg = per + 2 * H * 4 + F + (F // 32) * 4
     achieved = alg / (ms * 1e-3) / 1e9
-    return dict(kernel="k_matvec (gate|up shape, N=9728 K=896)", us=ms * 1e3, alg_bytes=alg,
-                achieved_gbs=achieved, copies=ncopy)
+    return dict(kernel="k_dec_gateup<64, 512> (0.5B gate|up + SwiGLU, N=9728 K=896)",
+                us=ms * 1e3, alg_bytes=alg, achieved_gbs=achieved, copies=ncopy)
 
 
 def bench_qkv_gemv(torch, si_amd, stream, launches=1000):
@@ -438,10 +444,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--quick", action="store_true", help="skip the other configurations")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--dominant-only", action="store_true",
+                    help="run only the dominant-kernel leg (for rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); "
-              "multi-GPU sharding is described in DESIGN.md, not run.", file=sys.stderr)
+              "the path is measured on one GPU's share and no multi-GPU run exists.",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -449,12 +458,17 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs an MI355X"
     torch.cuda.set_device(0)
     stream = torch.cuda.Stream()
+    if args.dominant_only:
+        dom = bench_dominant_kernel(torch, si_amd, stream)
+        print(json.dumps({"dominant_kernel": dom["kernel"], "us": round(dom["us"], 3),
+                          "achieved_gbs": round(dom["achieved_gbs"], 2)}), flush=True)
+        return
     t0 = time.time()
     log("config 2: 0.5B decode layer, ctx 1024 ...")
     dec, ctxobj = bench_decode_layer(torch, si_amd, stream, args.steps, args.warmup)
     log(f"  {dec['us']:.2f} us/token, {dec['gbs']:.1f} GB/s ({time.time() - t0:.0f} s)")
     log("roofline: dominant kernel ...")
-    dom = bench_dominant_gemv(torch, si_amd, stream, ctxobj)
+    dom = bench_dominant_kernel(torch, si_amd, stream)
     log(f"  {dom['us']:.2f} us/launch, {dom['achieved_gbs']:.1f} GB/s")
     extra = {}
     log("7B decode projections (k_matvec) ...")
@@ -502,7 +516,8 @@ def main():
         "timing": "HIP graph replay of the K steps (one graph), HIP events on the bench stream",
         "roofline": {"bound": "hbm", "achieved": round(dom["achieved_gbs"], 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(dom["achieved_gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": round(DOMINANT_TRAFFIC_BYTES),
                      "kernel": dom["kernel"], "kernel_us": round(dom["us"], 3),
                      "alg_bytes_per_launch": dom["alg_bytes"]},
         "cpu_baseline": cpu,

@@ -132,6 +132,17 @@ int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
                  const float *bias, const float *residual, float *out, int ldo,
                  int flags, void *stream);
 
+/* The decode FFN front half for one row, fused: rmsnorm(h, gain)
+ * (qwen_one_layer.c:164-169) -> quantize_q8 (:98-116) -> gate and up
+ * projections (matvec_q4q8, :148-162) -> act = silu(gate)*up ->
+ * quantize_q8(act) into planar qs/d/bsum (f values; act, the fp32 copy,
+ * may be NULL).  wqs/wd: the 2f x hidden matrix [gate rows; up rows]
+ * repacked with tile 32 (each workgroup pairs 32 gate with 32 up rows).
+ * flags: SI_GEMM_EXACT for the reference's block order and roundings. */
+int si_ffn_gateup_q8(const float *h, const float *gain, int hidden, float eps,
+                     const uint8_t *wqs, const uint16_t *wd, int tile, int f, float *act,
+                     int8_t *qs, uint16_t *d, int16_t *bsum, int flags, void *stream);
+
 /* RoPE (qwen_one_layer.c:172-183) + fp16 K/V append (:262-266) for ntok
  * rows of the fused projection output qkv[t] = [q | k | v]
  * (qheads*hdim + 2*kvheads*hdim floats, row stride ldqkv).  Token t is at

@@ -18,10 +18,12 @@
  *     load_layer;
  *   - errors still never return: they print and exit(1) like die()
  *     (qwen_one_layer.c:26-28);
- *   - timings (phase_t) are GPU event times in seconds; phases the GPU
- *     fuses (RMSNorm+Q8, attention+Q8) report the fused time in the first
- *     phase and 0 in the second; the fused Q/K/V projection is apportioned
- *     by output rows, as fused_layer.h:424-426 splits its fused K/V time.
+ *   - timings (phase_t) are GPU event times in seconds.  The decode kernels
+ *     fuse RMSNorm + Q8 into the Q/K/V projection, RoPE + K/V append into
+ *     attention and the attention output's Q8 into W_O: a fused phase is
+ *     reported under the projection or attention it runs in, the others
+ *     read 0.  The fused Q/K/V time is apportioned by output rows, as
+ *     fused_layer.h:424-426 splits its fused K/V time.
  */
 #ifndef SI_HOST_H
 #define SI_HOST_H

@@ -156,6 +156,23 @@ int si_matvec_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int 
     return check_launch("si_matvec_q4q8");
 }
 
+int si_ffn_gateup_q8(const float *h, const float *gain, int hidden, float eps,
+                     const uint8_t *wqs, const uint16_t *wd, int tile, int f, float *act,
+                     int8_t *qs, uint16_t *d, int16_t *bsum, int flags, void *stream) {
+    SI_REQUIRE(hidden > 0 && hidden % 32 == 0 && hidden <= 8192, "ffn_gateup: bad hidden %d",
+               hidden);
+    SI_REQUIRE(f > 0 && f % 32 == 0, "ffn_gateup: ffn %d must be a multiple of 32", f);
+    SI_REQUIRE(tile == 32, "ffn_gateup: the gate|up weights need scale tile 32 (got %d)", tile);
+    SI_REQUIRE(h && wqs && wd && qs && d && bsum, "ffn_gateup: NULL pointer");
+    SI_REQUIRE(((uintptr_t)wqs & 15) == 0 && ((uintptr_t)h & 15) == 0 &&
+                   (!gain || ((uintptr_t)gain & 15) == 0),
+               "ffn_gateup: wqs, h and gain must be 16-byte aligned");
+    SI_REQUIRE((flags & ~SI_GEMM_EXACT) == 0, "ffn_gateup: unknown flags %d", flags);
+    launch_dec_gateup(h, gain, hidden, eps, wqs, wd, tile, f, nullptr, nullptr, nullptr, nullptr,
+                      nullptr, act, qs, d, bsum, (flags & SI_GEMM_EXACT) != 0, S(stream));
+    return check_launch("si_ffn_gateup_q8");
+}
+
 int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
                  const int8_t *xqs, const uint16_t *xd, int m, const float *bias,
                  const float *residual, float *out, int ldo, int flags, void *stream) {

@@ -486,3 +486,34 @@ def test_cross_lane_ops_layouts():
         want = np.array([lane[lane % r == l % r].sum() for l in lane])
         assert np.array_equal(got[k], want), f"fold_rows<{r}>"
     assert np.array_equal(got[17], grp(64)), "wave_sum_d"
+
+
+@pytest.mark.parametrize("shape,flags", [("0.5b", 0), ("0.5b", si_amd.SI_GEMM_EXACT),
+                                         ("7b", 0)])
+def test_ffn_gateup_q8(oracle, shape, flags):
+    """The fused decode FFN front half against the oracle, chained: the
+    projections of the GPU's own quantized input (bit-exact with EXACT),
+    SwiGLU within 1e-6, its Q8 bit-exact on the GPU's own activations."""
+    torch = _torch()
+    from oracle.oracle_py import make_shape as or_shape
+    os_ = or_shape(**si_amd.SHAPES[shape])
+    H, F = os_.hidden, os_.ffn
+    rng = np.random.default_rng(F + flags)
+    wg, wu = q4(oracle, rng, F, H), q4(oracle, rng, F, H)
+    gain = rng.normal(1, 0.1, H).astype(np.float32)
+    h = rng.standard_normal(H).astype(np.float32)
+    wqs, wd, _ = _upload_q4(np.concatenate([wg, wu]), 2 * F, H, 32)
+    act = empty(F, torch.float32)
+    aq, ad, asum = empty(F, torch.int8), empty(F // 32, torch.int16), empty(F // 32, torch.int16)
+    si_amd.call("si_ffn_gateup_q8", si_amd.ptr(dev(h)), si_amd.ptr(dev(gain)), H, 1e-6,
+                si_amd.ptr(wqs), si_amd.ptr(wd), 32, F, si_amd.ptr(act), si_amd.ptr(aq),
+                si_amd.ptr(ad), si_amd.ptr(asum), flags, None)
+    xq = oracle.quantize_q8(oracle.rmsnorm(h, gain))
+    g = oracle.matvec(wg, xq, H, F)
+    u = oracle.matvec(wu, xq, H, F)
+    got = host(act)
+    close(got, oracle.swiglu(g, u), 1e-5 if flags == 0 else 1e-6, "SwiGLU")
+    want_q, want_d, want_s = aos_to_planar(oracle.quantize_q8(got))
+    assert np.array_equal(host(aq), want_q)
+    assert np.array_equal(host(ad).view(np.uint16), want_d)
+    assert np.array_equal(host(asum), want_s)
