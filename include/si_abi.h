@@ -123,14 +123,18 @@ int si_matvec_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int 
 /* matvec_q4q8 applied to m activation rows (prefill / batched decode):
  * out[i][r] (row stride ldo; residual uses the same stride) =
  * residual + (bias + sum over blocks).  int8 matrix-core tiles compute every
- * per-block int32 dot exactly; the fp32 epilogue either reproduces the
- * reference's rounding sequence (flags & SI_GEMM_EXACT: bit-exact with
- * matvec_q4q8) or uses one fused multiply-add per block (within fp32
- * rounding of the reference). */
+ * per-block int32 dot exactly.  With flags & SI_GEMM_EXACT the fp32
+ * epilogue reproduces the reference's rounding sequence (bit-exact with
+ * matvec_q4q8); otherwise each block adds dot * (x.d * w.d) in one fused
+ * multiply-add, the scale product exact in fp32 (within fp32 rounding of
+ * the reference).  A grid too small for the chip splits K: that needs
+ * si_gemm_workspace(m, n, k) bytes of workspace (NULL or smaller: no split);
+ * the split sums are added in a fixed order (deterministic). */
 int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
                  const int8_t *xqs, const uint16_t *xd, int m,
                  const float *bias, const float *residual, float *out, int ldo,
-                 int flags, void *stream);
+                 int flags, void *workspace, size_t ws_bytes, void *stream);
+size_t si_gemm_workspace(int m, int n, int k);
 
 /* The decode FFN front half for one row, fused: rmsnorm(h, gain)
  * (qwen_one_layer.c:164-169) -> quantize_q8 (:98-116) -> gate and up

@@ -175,16 +175,25 @@ int si_ffn_gateup_q8(const float *h, const float *gain, int hidden, float eps,
 
 int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
                  const int8_t *xqs, const uint16_t *xd, int m, const float *bias,
-                 const float *residual, float *out, int ldo, int flags, void *stream) {
+                 const float *residual, float *out, int ldo, int flags, void *workspace,
+                 size_t ws_bytes, void *stream) {
     SI_REQUIRE(n > 0 && k > 0 && k % 32 == 0 && m >= 0, "gemm: bad size m=%d n=%d k=%d", m, n,
                k);
     SI_REQUIRE(tile_ok(tile), "gemm: tile %d not 8, 16, 32 or 64", tile);
     SI_REQUIRE(ldo >= n, "gemm: ldo %d < n %d", ldo, n);
     SI_REQUIRE(m == 0 || (wqs && wd && xqs && xd && out), "gemm: NULL pointer");
+    SI_REQUIRE(((uintptr_t)wqs & 15) == 0 && ((uintptr_t)xqs & 15) == 0,
+               "gemm: wqs and xqs must be 16-byte aligned");
     SI_REQUIRE((flags & ~SI_GEMM_EXACT) == 0, "gemm: unknown flags %d", flags);
     launch_gemm_q4q8(wqs, wd, tile, n, k, xqs, xd, m, bias, residual, out, ldo,
-                     (flags & SI_GEMM_EXACT) != 0, S(stream));
+                     (flags & SI_GEMM_EXACT) != 0, workspace, workspace ? ws_bytes : 0,
+                     S(stream));
     return check_launch("si_gemm_q4q8");
+}
+
+size_t si_gemm_workspace(int m, int n, int k) {
+    if (m <= 0 || n <= 0 || k <= 0 || k % 32) return 0;
+    return gemm_workspace_bytes(m, n, k);
 }
 
 int si_rope_table(int npos, int hdim, float base, float *c, float *s) {
@@ -325,6 +334,8 @@ struct Workspace {
     Q8Buf xq, attq, xq2, actq;
     void *attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
+    void *gemm_ws = nullptr;  // split-K partial sums of the matrix-core GEMMs
+    size_t gemm_ws_bytes = 0;
 };
 
 struct si_workspace {
@@ -393,6 +404,20 @@ static int make_workspace(const si_shape_t *s, int max_tokens, int max_pos,
     uint8_t *ws = nullptr;
     TRY(m.alloc(&ws, W->attn_ws_bytes));
     W->attn_ws = ws;
+    // GEMM split-K partials: the largest need over the layer's projections
+    // and every row count up to max_tokens (the split depends on both)
+    {
+        const int dims[4][2] = {{NQKV, H}, {H, QD}, {2 * F, H}, {H, F}};
+        for (int r = 2; r <= max_tokens; ++r)
+            for (const auto &d : dims)
+                if (d[0] > 0 && d[1] > 0) {
+                    const size_t b = gemm_workspace_bytes(r, d[0], d[1]);
+                    if (b > W->gemm_ws_bytes) W->gemm_ws_bytes = b;
+                }
+        uint8_t *gw = nullptr;
+        TRY(m.alloc(&gw, W->gemm_ws_bytes));
+        W->gemm_ws = gw;
+    }
     *out = std::move(W);
     return SI_OK;
 }
@@ -412,6 +437,8 @@ struct si_layer {
     Q8Buf xq, attq, xq2, actq;
     void *attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
+    void *gemm_ws = nullptr;
+    size_t gemm_ws_bytes = 0;
     // phase timing: events[i] marks the start of phase i, events[COUNT] the end
     bool timing = false;
     hipEvent_t events[SI_PHASE_COUNT + 1] = {};
@@ -517,6 +544,8 @@ static int build_layer(const si_layer_host_t *w, std::shared_ptr<Workspace> W,
     L->actq = W->actq;
     L->attn_ws = W->attn_ws;
     L->attn_ws_bytes = W->attn_ws_bytes;
+    L->gemm_ws = W->gemm_ws;
+    L->gemm_ws_bytes = W->gemm_ws_bytes;
     L->ws = std::move(W);
     *out = L.release();
     return SI_OK;
@@ -635,7 +664,7 @@ static void project(si_layer *L, const Q4Dev &w, int rows, const Q8Buf &x, const
                       (flags & SI_LAYER_EXACT) != 0, st);
     else
         launch_gemm_q4q8(w.qs, w.d, w.tile, w.n, w.k, x.qs, x.d, rows, bias, residual, out, w.n,
-                         (flags & SI_LAYER_EXACT) != 0, st);
+                         (flags & SI_LAYER_EXACT) != 0, L->gemm_ws, L->gemm_ws_bytes, st);
 }
 
 // Single-token decode: five fused kernels (si_decode.hip).

@@ -143,18 +143,311 @@ __global__ void __launch_bounds__(256) k_gemm_q4q8(
         }
 }
 
+// ===========================================================================
+// Fast path (everything but SI_GEMM_EXACT).
+//
+// The VALU epilogue bounds this GEMM: each (m, n, 32-wide block) needs an
+// int->float conversion and an FMA with the scale product dx*dw, and the
+// VALU retires 16 lanes per clock per SIMD against 1024 int8 MACs for the
+// matrix core.  So everything else is moved off the VALU:
+//   * the scale product of a 32x32 output tile is one f16 MFMA
+//     (v_mfma_f32_32x32x8_f16 with dx as the only nonzero column of A and
+//     dw as the only nonzero row of B: an outer product, exact in fp32);
+//   * the epilogue is then cvt + fma per output and block, the fp32 FMA
+//     rounding once where the reference rounds twice;
+//   * operands stream through LDS stages of G_KB blocks, the next stage's
+//     global loads in flight in registers while the current one is used.
+// Tiles: WM x WN wavefronts, each TM x TN MFMA tiles of 32x32, so the
+// workgroup covers BM = 32*WM*TM rows by BN = 32*WN*TN columns.  A grid too
+// small for the chip splits K over gridDim.z; the split partial sums go to
+// a workspace and k_gemm_reduce adds them in split order (deterministic).
+// ===========================================================================
+typedef _Float16 gh4 __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int G_KB = 4;   // K blocks per LDS stage
+constexpr int G_ST = 48;  // LDS bytes per (row, block): 32 data + 16 padding
+
+template <int WM, int WN, int TM, int TN>
+struct GemmCfg {
+    static constexpr int BM = 32 * WM * TM, BN = 32 * WN * TN;
+    static constexpr int A_PIECES = BM * G_KB * 2;  // 16-byte pieces per stage
+    static constexpr int B_PIECES = BN * G_KB;      // 16-byte nibble pieces per stage
+    static constexpr int A_PT = (A_PIECES + 255) / 256, B_PT = (B_PIECES + 255) / 256;
+    static constexpr int SX_PT = (BM * G_KB + 255) / 256, SW_PT = (BN * G_KB + 255) / 256;
+    static constexpr size_t lds_bytes() {
+        return (size_t)G_KB * (BM + BN) * G_ST + (size_t)G_KB * (BM + BN) * 2;
+    }
+};
+
+// Register staging of one LDS stage of k_gemm_fast (branch-free loads:
+// clamped rows and blocks).
+template <int BM, int BN, int A_PT, int B_PT, int SX_PT, int SW_PT>
+struct GemmStage {
+    v4i ra[A_PT], rb[B_PT];  // clang vectors: kept in registers
+    uint16_t rsx[SX_PT], rsw[SW_PT];
+
+    __device__ __forceinline__ void load(const uint8_t *__restrict__ wqs,
+                                         const uint16_t *__restrict__ wd, int tile, int n, int nb,
+                                         const int8_t *__restrict__ xqs,
+                                         const uint16_t *__restrict__ xd, int m, int m0, int n0,
+                                         int bs, int b_end) {
+        const int tid = threadIdx.x, k = nb * SI_QK;
+        constexpr int A_PIECES = BM * G_KB * 2, B_PIECES = BN * G_KB;
+#pragma unroll
+        for (int i = 0; i < A_PT; ++i) {
+            const int p = min(tid + 256 * i, A_PIECES - 1);
+            const int row = p / (G_KB * 2), blk = (p >> 1) % G_KB, half = p & 1;
+            const int gr = min(m0 + row, m - 1), gb = min(bs + blk, b_end - 1);
+            ra[i] = *(const v4i *)(xqs + (size_t)gr * k + (size_t)gb * SI_QK + half * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < B_PT; ++i) {
+            const int p = min(tid + 256 * i, B_PIECES - 1);
+            const int row = p / G_KB, blk = p % G_KB;
+            const int gr = min(n0 + row, n - 1), gb = min(bs + blk, b_end - 1);
+            rb[i] = *(const v4i *)(wqs + ((size_t)gb * n + gr) * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < SX_PT; ++i) {
+            const int p = min(tid + 256 * i, BM * G_KB - 1);
+            const int row = p / G_KB, blk = p % G_KB;
+            rsx[i] = xd[(size_t)min(m0 + row, m - 1) * nb + min(bs + blk, b_end - 1)];
+        }
+#pragma unroll
+        for (int i = 0; i < SW_PT; ++i) {
+            const int p = min(tid + 256 * i, BN * G_KB - 1);
+            const int row = p / G_KB, blk = p % G_KB;
+            rsw[i] = wd[q4_scale_index(min(n0 + row, n - 1), min(bs + blk, b_end - 1), nb, tile)];
+        }
+    }
+
+    __device__ __forceinline__ void store(uint8_t *a_l, uint8_t *b_l, uint16_t *sx_l,
+                                          uint16_t *sw_l, int buf) const {
+        const int tid = threadIdx.x;
+        constexpr int A_PIECES = BM * G_KB * 2, B_PIECES = BN * G_KB;
+#pragma unroll
+        for (int i = 0; i < A_PT; ++i) {
+            const int p = tid + 256 * i;
+            if (A_PIECES % 256 == 0 || p < A_PIECES) {
+                const int row = p / (G_KB * 2), blk = (p >> 1) % G_KB, half = p & 1;
+                *(v4i *)(a_l + (((size_t)buf * G_KB + blk) * BM + row) * G_ST + half * 16) = ra[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < B_PT; ++i) {
+            const int p = tid + 256 * i;
+            if (B_PIECES % 256 == 0 || p < B_PIECES) {
+                const int row = p / G_KB, blk = p % G_KB;
+                const uint32_t w[4] = {(uint32_t)rb[i][0], (uint32_t)rb[i][1], (uint32_t)rb[i][2],
+                                       (uint32_t)rb[i][3]};
+                uint32_t lo[4], hi[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    lo[t] = nib_to_s8(w[t] & 0x0f0f0f0fu);
+                    hi[t] = nib_to_s8((w[t] >> 4) & 0x0f0f0f0fu);
+                }
+                uint8_t *dst = b_l + (((size_t)buf * G_KB + blk) * BN + row) * G_ST;
+                *(uint4 *)dst = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+                *(uint4 *)(dst + 16) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < SX_PT; ++i) {
+            const int p = tid + 256 * i;
+            if ((BM * G_KB) % 256 == 0 || p < BM * G_KB) {
+                const int row = p / G_KB, blk = p % G_KB;
+                sx_l[((size_t)buf * G_KB + blk) * BM + row] = rsx[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < SW_PT; ++i) {
+            const int p = tid + 256 * i;
+            if ((BN * G_KB) % 256 == 0 || p < BN * G_KB) {
+                const int row = p / G_KB, blk = p % G_KB;
+                sw_l[((size_t)buf * G_KB + blk) * BN + row] = rsw[i];
+            }
+        }
+    }
+};
+
+template <int WM, int WN, int TM, int TN>
+__global__ void __launch_bounds__(256) k_gemm_fast(
+    const uint8_t *__restrict__ wqs, const uint16_t *__restrict__ wd, int tile, int n, int nb,
+    const int8_t *__restrict__ xqs, const uint16_t *__restrict__ xd, int m,
+    const float *__restrict__ bias, const float *__restrict__ residual, float *__restrict__ out,
+    int ldo, float *__restrict__ part, int bps) {
+    using C = GemmCfg<WM, WN, TM, TN>;
+    constexpr int BM = C::BM, BN = C::BN;
+    extern __shared__ __attribute__((aligned(16))) uint8_t gsm[];
+    uint8_t *a_l = gsm;                                   // [G_KB][BM][G_ST]
+    uint8_t *b_l = a_l + G_KB * BM * G_ST;                // [G_KB][BN][G_ST]
+    uint16_t *sx_l = (uint16_t *)(b_l + G_KB * BN * G_ST);  // [G_KB][BM]
+    uint16_t *sw_l = sx_l + G_KB * BM;                    // [G_KB][BN]
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int j = lane & 31, g = lane >> 5;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int b_begin = blockIdx.z * bps, b_end = min(nb, b_begin + bps);
+
+    GemmStage<BM, BN, C::A_PT, C::B_PT, C::SX_PT, C::SW_PT> stg;
+    float acc[TM][TN][16];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+
+    const int nstage = (b_end - b_begin + G_KB - 1) / G_KB;
+    stg.load(wqs, wd, tile, n, nb, xqs, xd, m, m0, n0, b_begin, b_end);
+    // One LDS stage: the next stage's global loads are in flight in registers
+    // while this one is consumed; the trailing barrier frees the LDS.
+    for (int st = 0; st < nstage; ++st) {
+        const int buf = 0;
+        stg.store(a_l, b_l, sx_l, sw_l, buf);
+        __syncthreads();
+        const int bs = b_begin + st * G_KB;
+        // next stage in flight (branch-free: the last iteration re-reads
+        // its own stage, clamped, and never stores it)
+        stg.load(wqs, wd, tile, n, nb, xqs, xd, m, m0, n0,
+                 min(bs + G_KB, b_begin + (nstage - 1) * G_KB), b_end);
+#pragma unroll
+        for (int blk = 0; blk < G_KB; ++blk) {
+            if (bs + blk >= b_end) break;
+            const uint8_t *ab = a_l + ((size_t)buf * G_KB + blk) * BM * G_ST;
+            const uint8_t *bb = b_l + ((size_t)buf * G_KB + blk) * BN * G_ST;
+            const uint16_t *sxb = sx_l + ((size_t)buf * G_KB + blk) * BM;
+            const uint16_t *swb = sw_l + ((size_t)buf * G_KB + blk) * BN;
+            v4i aop[TM], bop[TN];
+            gh4 asc[TM], bsc[TN];
+#pragma unroll
+            for (int a = 0; a < TM; ++a) {
+                const int r = (wm * TM + a) * 32 + j;
+                aop[a] = *(const v4i *)(ab + r * G_ST + g * 16);
+                const _Float16 x = __builtin_bit_cast(_Float16, sxb[r]);
+                asc[a] = (gh4){g == 0 ? x : (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f,
+                               (_Float16)0.0f};
+            }
+#pragma unroll
+            for (int b = 0; b < TN; ++b) {
+                const int c = (wn * TN + b) * 32 + j;
+                bop[b] = *(const v4i *)(bb + c * G_ST + g * 16);
+                const _Float16 w = __builtin_bit_cast(_Float16, swb[c]);
+                bsc[b] = (gh4){g == 0 ? w : (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f,
+                               (_Float16)0.0f};
+            }
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+#pragma unroll
+                for (int b = 0; b < TN; ++b) {
+                    v16i z = {};
+                    const v16i dot = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[a], bop[b], z, 0, 0, 0);
+                    v16f zf = {};
+                    const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(asc[a], bsc[b], zf, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[a][b][v] = fmaf((float)dot[v], sc[v], acc[a][b][v]);
+                }
+        }
+        __syncthreads();  // the stage's LDS is rewritten next
+    }
+
+    // output (i, j) of a 32x32 tile: lane j + 32*((i/4)%2), register (i%4) + 4*(i/8)
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const int col = n0 + (wn * TN + b) * 32 + j;
+            if (col >= n) continue;
+            const float bv = (part == nullptr && bias) ? bias[col] : 0.0f;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int row = m0 + (wm * TM + a) * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
+                if (row >= m) continue;
+                if (part) {
+                    part[((size_t)blockIdx.z * m + row) * n + col] = acc[a][b][v];
+                } else {
+                    float y = acc[a][b][v] + bv;
+                    if (residual) y = __fadd_rn(residual[(size_t)row * ldo + col], y);
+                    out[(size_t)row * ldo + col] = y;
+                }
+            }
+        }
+}
+
+// out = residual + (bias + sum_s part[s]), the split partial sums in order.
+__global__ void __launch_bounds__(256) k_gemm_reduce(const float *__restrict__ part, int splits,
+                                                     int m, int n, const float *__restrict__ bias,
+                                                     const float *__restrict__ residual,
+                                                     float *__restrict__ out, int ldo) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)m * n) return;
+    const int row = (int)(i / n), col = (int)(i - (size_t)row * n);
+    float y = part[i];
+    for (int s = 1; s < splits; ++s) y += part[(size_t)s * m * n + i];
+    if (bias) y += bias[col];
+    if (residual) y = __fadd_rn(residual[(size_t)row * ldo + col], y);
+    out[(size_t)row * ldo + col] = y;
+}
+
+// Tile choice and K splits of the fast path for an m x n x nb problem.
+struct GemmPlan {
+    int bm, bn, splits, bps;
+};
+static GemmPlan gemm_plan(int m, int n, int nb) {
+    GemmPlan p;
+    p.bm = m <= 64 ? 64 : 128;
+    p.bn = 128;
+    const int tiles = ((n + p.bn - 1) / p.bn) * ((m + p.bm - 1) / p.bm);
+    int s = (256 + tiles - 1) / tiles;  // >= one workgroup per CU
+    const int maxs = nb / (2 * G_KB);   // >= 2 stages per split
+    if (s > maxs) s = maxs;
+    if (s < 1) s = 1;
+    p.bps = (nb + s - 1) / s;
+    p.bps = (p.bps + G_KB - 1) / G_KB * G_KB;
+    p.splits = (nb + p.bps - 1) / p.bps;
+    return p;
+}
+
+size_t gemm_workspace_bytes(int m, int n, int k) {
+    const GemmPlan p = gemm_plan(m, n, k / SI_QK);
+    return p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0;
+}
+
 void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
-                      const int8_t *xqs,
-                      const uint16_t *xd, int m, const float *bias, const float *residual,
-                      float *out, int ldo, bool exact, hipStream_t st) {
+                      const int8_t *xqs, const uint16_t *xd, int m, const float *bias,
+                      const float *residual, float *out, int ldo, bool exact, void *workspace,
+                      size_t ws_bytes, hipStream_t st) {
     if (m <= 0 || n <= 0) return;
-    const dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM);
-    if (exact)
-        hipLaunchKernelGGL(k_gemm_q4q8<true>, grid, dim3(256), 0, st, wqs, wd, tile, n, k / SI_QK, xqs,
+    const int nb = k / SI_QK;
+    if (exact) {
+        const dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM);
+        hipLaunchKernelGGL(k_gemm_q4q8<true>, grid, dim3(256), 0, st, wqs, wd, tile, n, nb, xqs,
                            xd, m, bias, residual, out, ldo);
+        return;
+    }
+    GemmPlan p = gemm_plan(m, n, nb);
+    if (p.splits > 1 && (!workspace || ws_bytes < (size_t)p.splits * m * n * sizeof(float))) {
+        p.splits = 1;  // no workspace: one pass over K
+        p.bps = nb;
+    }
+    float *part = p.splits > 1 ? (float *)workspace : nullptr;
+    const dim3 grid((n + p.bn - 1) / p.bn, (m + p.bm - 1) / p.bm, p.splits);
+#define CALL(WM, WN, TM, TN)                                                                   \
+    hipLaunchKernelGGL((k_gemm_fast<WM, WN, TM, TN>), grid, dim3(256),                         \
+                       (GemmCfg<WM, WN, TM, TN>::lds_bytes()), st, wqs, wd, tile, n, nb, xqs,   \
+                       xd, m, bias, residual, out, ldo, part, p.bps)
+    if (p.bm == 64)
+        CALL(1, 4, 2, 1);
     else
-        hipLaunchKernelGGL(k_gemm_q4q8<false>, grid, dim3(256), 0, st, wqs, wd, tile, n, k / SI_QK, xqs,
-                           xd, m, bias, residual, out, ldo);
+        CALL(2, 2, 2, 2);
+#undef CALL
+    if (part) {
+        const size_t tot = (size_t)m * n;
+        hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st,
+                           part, p.splits, m, n, bias, residual, out, ldo);
+    }
 }
 
 }  // namespace si

@@ -23,9 +23,10 @@ void launch_matvec(const int8_t *xqs, const uint16_t *xd, const int16_t *xs, int
 void launch_block_dots(const uint8_t *wqs, int n, int k, const int8_t *xqs, const int16_t *xs,
                        int32_t *dots, hipStream_t st);
 void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
-                      const int8_t *xqs,
-                      const uint16_t *xd, int m, const float *bias, const float *residual,
-                      float *out, int ldo, bool exact, hipStream_t st);
+                      const int8_t *xqs, const uint16_t *xd, int m, const float *bias,
+                      const float *residual, float *out, int ldo, bool exact, void *workspace,
+                      size_t ws_bytes, hipStream_t st);
+size_t gemm_workspace_bytes(int m, int n, int k);
 }  // namespace si
 namespace si {
 void launch_rope_kv(const float *qkv, int ldqkv, int ntok, int qheads, int kvheads, int hdim,

@@ -276,7 +276,7 @@ def test_gemm_matches_oracle_rows(oracle, m, n, k):
     out = empty(m * n, torch.float32)
     si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), tile, n, k, si_amd.ptr(dev(qs)),
                 si_amd.ptr(dev(d.view(np.int16))), m, si_amd.ptr(dev(b)), None,
-                si_amd.ptr(out), n, 0, None)
+                si_amd.ptr(out), n, 0, None, 0, None)
     got = host(out).reshape(m, n)
     nb = k // 32
     for r in sorted({0, m // 2, m - 1}):
@@ -285,10 +285,14 @@ def test_gemm_matches_oracle_rows(oracle, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(512, 1152, 896), (64, 4608, 3584), (130, 896, 4864),
-                                   (100, 9728, 896)])
-def test_gemm_every_row_vs_float64(oracle, m, n, k):
+                                   (100, 9728, 896), (64, 3584, 18944), (2048, 384, 896),
+                                   (130, 200, 96), (1, 4608, 3584)])
+@pytest.mark.parametrize("split", [False, True])
+def test_gemm_every_row_vs_float64(oracle, m, n, k, split):
     """Every output row of the layer-shaped GEMMs against the float64 product
-    of the dequantized operands (the value the fp32 path approximates)."""
+    of the dequantized operands (the value the fp32 path approximates), in
+    one pass over K and with K split over workgroups (twice: the split sums
+    are added in a fixed order, so both calls give the same bits)."""
     torch = _torch()
     rng = np.random.default_rng(m + n + k)
     w = q4(oracle, rng, n, k)
@@ -296,16 +300,24 @@ def test_gemm_every_row_vs_float64(oracle, m, n, k):
     xq = oracle.quantize_q8(x)
     qs, d, _ = aos_to_planar(xq)
     wqs, wd, tile = _upload_q4(w, n, k)
-    out = empty(m * n, torch.float32)
-    si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), tile, n, k, si_amd.ptr(dev(qs)),
-                si_amd.ptr(dev(d.view(np.int16))), m, None, None, si_amd.ptr(out), n, 0, None)
-    got = host(out).reshape(m, n)
+    wsb = si_amd.lib().si_gemm_workspace(m, n, k) if split else 0
+    ws = empty(max(wsb, 4), torch.uint8) if split else None
     want = dequant_q8(xq, m, k) @ dequant_q4(w, n, k).T
     rms = np.sqrt(np.mean(want ** 2))
-    err = np.abs(got - want).max(axis=1) / rms
-    bad = np.nonzero(err > 1e-5)[0]
-    assert bad.size == 0, f"rows off (row mod 64 -> {sorted(set((bad % 64).tolist()))[:16]}), " \
-                          f"first {bad[:8].tolist()}, worst {err.max():.3g}"
+    prev = None
+    for rep in range(2 if split else 1):
+        out = empty(m * n, torch.float32)
+        si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), tile, n, k,
+                    si_amd.ptr(dev(qs)), si_amd.ptr(dev(d.view(np.int16))), m, None, None,
+                    si_amd.ptr(out), n, 0, si_amd.ptr(ws), wsb, None)
+        got = host(out).reshape(m, n)
+        err = np.abs(got - want).max(axis=1) / rms
+        bad = np.nonzero(err > 1e-5)[0]
+        assert bad.size == 0, f"rows off (row mod 64 -> {sorted(set((bad % 64).tolist()))[:16]}), " \
+                              f"first {bad[:8].tolist()}, worst {err.max():.3g}"
+        if prev is not None:
+            assert np.array_equal(prev.view(np.uint32), got.view(np.uint32)), "not deterministic"
+        prev = got
 
 
 def test_gemm_residual(oracle):
@@ -321,7 +333,7 @@ def test_gemm_residual(oracle):
     out = empty(m * n, torch.float32)
     si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), tile, n, k, si_amd.ptr(dev(qs)),
                 si_amd.ptr(dev(d.view(np.int16))), m, None, si_amd.ptr(dev(res)),
-                si_amd.ptr(out), n, 0, None)
+                si_amd.ptr(out), n, 0, None, 0, None)
     got = host(out).reshape(m, n)
     nb = k // 32
     for r in (0, 69):
