@@ -156,7 +156,14 @@ __global__ void __launch_bounds__(256) k_gemm_q4q8(
 //   * the epilogue is then cvt + fma per output and block, the fp32 FMA
 //     rounding once where the reference rounds twice;
 //   * operands stream through LDS stages of G_KB blocks, the next stage's
-//     global loads in flight in registers while the current one is used.
+//     global loads in flight in registers while the current one is used;
+//     two blocks per stage keep the kernel under 168 VGPRs (3 waves per
+//     SIMD), which hides more latency than deeper stages do;
+//   * MFMA results are written to VGPRs (-amdgpu-mfma-vgpr-form), so the
+//     epilogue reads them without a v_accvgpr_read per element.
+// Counters on the 7B gate|up GEMM (2048 x 37888 x 3584): the VALU is ~90%
+// busy, 73% of its instructions are the cvt + fma epilogue, the matrix
+// pipe ~33% (i8 and f16 MFMA 32 cycles each per 32x32 tile and block).
 // Tiles: WM x WN wavefronts, each TM x TN MFMA tiles of 32x32, so the
 // workgroup covers BM = 32*WM*TM rows by BN = 32*WN*TN columns.  A grid too
 // small for the chip splits K over gridDim.z; the split partial sums go to
@@ -165,7 +172,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4q8(
 typedef _Float16 gh4 __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int G_KB = 4;   // K blocks per LDS stage
+constexpr int G_KB = 2;   // K blocks per LDS stage (deeper stages cost occupancy)
 constexpr int G_ST = 48;  // LDS bytes per (row, block): 32 data + 16 padding
 
 template <int WM, int WN, int TM, int TN>
