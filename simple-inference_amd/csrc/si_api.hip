@@ -756,9 +756,13 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
                        ctx_dev, L->rope_cos, L->rope_sin, L->q, kc, vc, kv_seq_stride, st);
         // :268-272: attention over the fp16 cache -> Q8
         mark(L, SI_PHASE_ATTENTION_Q8, st);
-        launch_attention(L->q, rows, s.qheads, s.kvheads, s.hdim, kc, vc, kv_seq_stride, ctx_dev,
-                         ctx0, ctx_step, max_ctx, L->attn, L->attq.qs, L->attq.d, L->attq.s,
-                         L->attn_ws, st);
+        if (ctx_dev == nullptr && attn_prefill_supported(s.qheads, s.kvheads, s.hdim))
+            launch_attn_prefill(L->q, rows, s.qheads, s.kvheads, s.hdim, pos0, kc, vc, L->attn,
+                                L->attq.qs, L->attq.d, L->attq.s, st);
+        else
+            launch_attention(L->q, rows, s.qheads, s.kvheads, s.hdim, kc, vc, kv_seq_stride,
+                             ctx_dev, ctx0, ctx_step, max_ctx, L->attn, L->attq.qs, L->attq.d,
+                             L->attq.s, L->attn_ws, st);
     }
     mark(L, SI_PHASE_OUT_PROJ, st);
     if (!full) {

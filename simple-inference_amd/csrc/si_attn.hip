@@ -260,6 +260,275 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(
     }
 }
 
+// ===========================================================================
+// Causal prefill attention (flash attention over 32 x 32 tiles).
+//
+// One workgroup owns one KV group and 32 consecutive query tokens; wavefront
+// w < per computes query head g*per + w for those tokens, so each K/V tile
+// staged in LDS serves the whole GQA group.  Per 32-position K/V tile a
+// wavefront computes
+//     S^T[pos][tok] = K[pos][:] . Q[tok][:]          (v_mfma_f32_32x32x16_f16)
+// (Q split into fp16 hi + lo halves, each product done twice, for fp32-level
+// scores), applies the causal mask and the online softmax per token (a
+// token's 32 scores sit in one lane and its partner lane ^ 32), then
+//     O^T[d][tok] += V^T[d][pos] . P^T[pos][tok]     (v_mfma_f32_32x32x16_f16)
+// The running max and sum of a token then live in the lanes that hold its O^T
+// column, so the rescale is a per-lane multiply.  P is split into fp16 hi +
+// lo halves like Q (an fp16-only P moves outputs by ~1e-3 relative, enough
+// to break the prefill == sequential decode agreement the reference tests).
+// V is staged transposed so the A operand of the PV product is two 8-byte
+// LDS reads per lane.  The epilogue normalises, stores fp32 and quantizes
+// every 32-dim block to Q8_0 (qwen_one_layer.c:272) in registers.
+//
+// 32x32 layouts: output (i, j) is held by lane j + 32*((i/4)%2), register
+// (i%4) + 4*(i/8); operand lane l supplies row (or column) l%32 and k-slice
+// l/32.  A and B use the same k assignment, so any consistent assignment of
+// reduction indices to (slice, element) is exact.
+// ===========================================================================
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+constexpr int PF_T = 32;      // query tokens per workgroup, positions per K/V tile
+constexpr int PF_KPAD = 8;    // halves of padding per K row
+constexpr int PF_VPAD = 4;    // halves of padding per V^T row (18-dword rows)
+
+template <int D, int NW>
+struct PrefillLds {
+    static constexpr int KROW = D + PF_KPAD, VROW = PF_T + PF_VPAD;
+    static constexpr size_t bytes() { return (size_t)(PF_T * KROW + D * VROW) * 2; }
+};
+
+template <int D, int NW>
+__global__ void __launch_bounds__(NW * 64) k_attn_prefill(
+    const float *__restrict__ q, int ntok, int qheads, int kvheads, int pos0,
+    const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, float scale,
+    float *__restrict__ attn, int8_t *__restrict__ qs, uint16_t *__restrict__ qd,
+    int16_t *__restrict__ bsum) {
+    using Lds = PrefillLds<D, NW>;
+    constexpr int NT = NW * 64, KS = D / 16, DT = D / 32;
+    constexpr int KPIECES = PF_T * D / 8;        // 16-byte K pieces per tile
+    constexpr int VITEMS = (PF_T / 2) * (D / 8); // (position pair, 8 dims) per tile
+    constexpr int KPT = (KPIECES + NT - 1) / NT, VPT = (VITEMS + NT - 1) / NT;
+    extern __shared__ __attribute__((aligned(16))) uint8_t pf_sm[];
+    _Float16 *k_l = (_Float16 *)pf_sm;                  // [PF_T][KROW]
+    _Float16 *vt_l = k_l + PF_T * Lds::KROW;            // [D][VROW]
+
+    const int nqt = gridDim.x;
+    const int qt = nqt - 1 - (int)blockIdx.x;  // longest tiles first
+    const int g = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int t = lane & 31, hh = lane >> 5;
+    const int per = qheads / kvheads;
+    const bool active = w < per;
+    const int h = g * per + (active ? w : 0);
+    const int tq = qt * PF_T + t;  // this lane's query token
+    const int ptq = pos0 + tq;     // its position: it sees cache rows 0..ptq
+    const int kvd = kvheads * D;
+    const int last = min(pos0 + qt * PF_T + PF_T - 1, pos0 + ntok - 1);  // last cache row used
+    const int ntiles = last / PF_T + 1;
+
+    // Q^T as the B operand of the score MFMA: column tok = t, k-slice hh
+    h8 qh[KS], ql[KS];
+    {
+        const bool ok = active && tq < ntok;
+        const float *qrow = q + ((size_t)(ok ? tq : 0) * qheads + h) * D;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const float4 a = *(const float4 *)(qrow + 16 * ks + 8 * hh);
+            const float4 b = *(const float4 *)(qrow + 16 * ks + 8 * hh + 4);
+            const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                _Float16 hi, lo;
+                split_hi_lo(ok ? x[e] : 0.0f, hi, lo);
+                qh[ks][e] = hi;
+                ql[ks][e] = lo;
+            }
+        }
+    }
+
+    // register staging of one K/V tile (rows clamped to `last`; the clamped
+    // duplicates lie past every token's causal limit and are masked)
+    uint4 rk[KPT], rv[VPT][2];
+    auto load_tile = [&](int kv0) {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int c = min(tid + NT * i, KPIECES - 1);
+            const int r = c / (D / 8), e8 = c % (D / 8);
+            const int pos = min(kv0 + r, last);
+            rk[i] = *(const uint4 *)(kc + (size_t)pos * kvd + (size_t)g * D + 8 * e8);
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int c = min(tid + NT * i, VITEMS - 1);
+            const int pr = c % (PF_T / 2), e8 = c / (PF_T / 2);
+            const int p0 = min(kv0 + 2 * pr, last), p1 = min(kv0 + 2 * pr + 1, last);
+            rv[i][0] = *(const uint4 *)(vc + (size_t)p0 * kvd + (size_t)g * D + 8 * e8);
+            rv[i][1] = *(const uint4 *)(vc + (size_t)p1 * kvd + (size_t)g * D + 8 * e8);
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int c = tid + NT * i;
+            if (KPIECES % NT == 0 || c < KPIECES) {
+                const int r = c / (D / 8), e8 = c % (D / 8);
+                *(uint4 *)(k_l + r * Lds::KROW + 8 * e8) = rk[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int c = tid + NT * i;
+            if (VITEMS % NT == 0 || c < VITEMS) {
+                // position pairs fastest: with 18-dword V^T rows the 64
+                // lanes' 4-byte writes hit 64 distinct banks
+                const int pr = c % (PF_T / 2), e8 = c / (PF_T / 2);
+                const uint32_t a[4] = {rv[i][0].x, rv[i][0].y, rv[i][0].z, rv[i][0].w};
+                const uint32_t b[4] = {rv[i][1].x, rv[i][1].y, rv[i][1].z, rv[i][1].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    // dims 8*e8 + 2j (low halves) and + 2j + 1 (high halves)
+                    const uint32_t lo = __builtin_amdgcn_perm(b[j], a[j], 0x05040100u);
+                    const uint32_t hi = __builtin_amdgcn_perm(b[j], a[j], 0x07060302u);
+                    *(uint32_t *)(vt_l + (8 * e8 + 2 * j) * Lds::VROW + 2 * pr) = lo;
+                    *(uint32_t *)(vt_l + (8 * e8 + 2 * j + 1) * Lds::VROW + 2 * pr) = hi;
+                }
+            }
+        }
+    };
+
+    float m = -INFINITY, lsum = 0.0f;  // softmax state of token t (same in both halves)
+    f16v o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = (f16v){};
+
+    load_tile(0);
+    for (int it = 0; it < ntiles; ++it) {
+        const int kv0 = it * PF_T;
+        store_tile();
+        __syncthreads();
+        if (it + 1 < ntiles) load_tile(kv0 + PF_T);  // next tile in flight
+        if (active) {
+            // scores S^T[pos = kv0 + i][tok = t]
+            f16v sh = (f16v){}, sl = (f16v){};  // two independent MFMA chains
+            const _Float16 *krow = k_l + t * Lds::KROW + 8 * hh;  // A row pos = lane % 32
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const h8 ka = *(const h8 *)(krow + 16 * ks);
+                sh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[ks], sh, 0, 0, 0);
+                sl = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[ks], sl, 0, 0, 0);
+            }
+            const f16v sacc = sh + sl;
+            float sv[16];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int pos = kv0 + 8 * (r >> 2) + 4 * hh + (r & 3);
+                sv[r] = pos <= ptq ? sacc[r] * scale : -INFINITY;
+                mx = fmaxf(mx, sv[r]);
+            }
+            mx = fmaxf(mx, swap32_f(mx));
+            const float mnew = fmaxf(m, mx);  // finite: row 0 is in every token's range
+            const float alpha = __expf(m - mnew);
+            float ps = 0.0f;
+            h8 pbh[2], pbl[2];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float pr = __expf(sv[r] - mnew);
+                ps += pr;
+                _Float16 hi, lo;
+                split_hi_lo(pr, hi, lo);
+                pbh[r >> 3][r & 7] = hi;
+                pbl[r >> 3][r & 7] = lo;
+            }
+            ps += swap32_f(ps);
+            lsum = fmaf(lsum, alpha, ps);
+            m = mnew;
+            // O^T[d][tok] += V^T[d][pos] P^T[pos][tok]; k-step s2 covers
+            // positions 16*s2 + 8*(e/4) + 4*hh + e%4 (e = element 0..7), the
+            // positions of registers 8*s2 + e of the score output
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                f16v acc = o[dt] * alpha;
+                const _Float16 *vrow = vt_l + (32 * dt + t) * Lds::VROW + 4 * hh;
+#pragma unroll
+                for (int s2 = 0; s2 < 2; ++s2) {
+                    const h4 v0 = *(const h4 *)(vrow + 16 * s2);
+                    const h4 v1 = *(const h4 *)(vrow + 16 * s2 + 8);
+                    const h8 va = (h8){v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pbh[s2], acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pbl[s2], acc, 0, 0, 0);
+                }
+                o[dt] = acc;
+            }
+        }
+        __syncthreads();  // the tile's LDS is rewritten next
+    }
+
+    if (!active || tq >= ntok) return;
+    // lane holds O[tok][32*dt + 8*(r/4) + 4*hh + r%4] in o[dt][r]
+    const float inv = 1.0f / lsum;
+    const size_t rowoff = ((size_t)tq * qheads + h) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+        float y[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) y[r] = o[dt][r] * inv;
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+            *(float4 *)(attn + rowoff + 32 * dt + 8 * r4 + 4 * hh) =
+                make_float4(y[4 * r4], y[4 * r4 + 1], y[4 * r4 + 2], y[4 * r4 + 3]);
+        if (qs) {
+            int qv[16];
+            uint16_t dbits;
+            int sum;
+            quant_block_pair16(y, qv, dbits, sum);
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+                *(uint32_t *)(qs + rowoff + 32 * dt + 8 * r4 + 4 * hh) =
+                    (uint32_t)(qv[4 * r4] & 0xff) | (uint32_t)(qv[4 * r4 + 1] & 0xff) << 8 |
+                    (uint32_t)(qv[4 * r4 + 2] & 0xff) << 16 | (uint32_t)(qv[4 * r4 + 3] & 0xff) << 24;
+            if (hh == 0) {
+                const size_t bi = (rowoff + 32 * dt) / SI_QK;
+                qd[bi] = dbits;
+                if (bsum) bsum[bi] = (int16_t)sum;
+            }
+        }
+    }
+}
+
+// Causal prefill of ntok tokens at positions pos0.. of one sequence whose
+// cache rows 0..pos0+ntok-1 are in place (RoPE'd K, V).
+bool attn_prefill_supported(int qheads, int kvheads, int hdim) {
+    return kvheads > 0 && qheads % kvheads == 0 && qheads / kvheads <= 16 &&
+           (hdim == 32 || hdim == 64 || hdim == 96 || hdim == 128);
+}
+
+void launch_attn_prefill(const float *q, int ntok, int qheads, int kvheads, int hdim, int pos0,
+                         const uint16_t *kc, const uint16_t *vc, float *attn, int8_t *qs,
+                         uint16_t *qd, int16_t *bsum, hipStream_t st) {
+    if (ntok <= 0) return;
+    const int per = qheads / kvheads;
+    const dim3 grid((ntok + PF_T - 1) / PF_T, kvheads);
+    const float scale = 1.0f / sqrtf((float)hdim);  // attention_kernels.h:86
+#define PF_CALL(DIM, NW)                                                                      \
+    hipLaunchKernelGGL((k_attn_prefill<DIM, NW>), grid, dim3(NW * 64),                        \
+                       (PrefillLds<DIM, NW>::bytes()), st, q, ntok, qheads, kvheads, pos0, kc, \
+                       vc, scale, attn, qs, qd, bsum)
+#define PF_DIM(DIM)                     \
+    if (per <= 8)                       \
+        PF_CALL(DIM, 8);                \
+    else                                \
+        PF_CALL(DIM, 16);
+    switch (hdim) {
+        case 32: PF_DIM(32); break;
+        case 64: PF_DIM(64); break;
+        case 96: PF_DIM(96); break;
+        default: PF_DIM(128); break;
+    }
+#undef PF_DIM
+#undef PF_CALL
+}
+
 // Context chunks per (query, KV group): enough workgroups to cover the chip
 // (>= ~512) while every chunk keeps at least one 64-position step.
 int attn_nsplit(int kvheads, int nq, int max_ctx) {

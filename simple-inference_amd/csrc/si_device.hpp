@@ -226,6 +226,36 @@ __device__ __forceinline__ uint32_t quant_block_oct(const float (&x)[4], uint16_
     return packed;
 }
 
+// quantize_q8 of one 32-value block held as 16 values in lane l and 16 in
+// lane l ^ 32 (the two halves of a 32x32 MFMA output column), with exactly
+// quant_block_lane's rules.  q[k] receives the lane's int8 values; every
+// lane of the pair gets the fp16 scale bits and the block sum.
+__device__ __forceinline__ void quant_block_pair16(const float (&x)[16], int (&q)[16],
+                                                   uint16_t &dbits, int &bsum) {
+    float a = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) a = fmaxf(a, fabsf(x[k]));  // NaN ignored
+    const float amax = fmaxf(a, swap32_f(a));
+    const float d = __fdiv_rn(amax, 127.0f);
+    dbits = f2h(d);
+    const float inv = (d == 0.0f) ? 0.0f : __fdiv_rn(1.0f, d);
+    int sum = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const float y = __fmul_rn(x[k], inv);
+        int v;
+        if (!(fabsf(y) <= 3.0e38f)) {
+            v = -127;
+        } else {
+            v = (int)rintf(fminf(fmaxf(y, -200.0f), 200.0f));
+            v = v > 127 ? 127 : (v < -127 ? -127 : v);
+        }
+        q[k] = v;
+        sum += v;
+    }
+    bsum = sum + swap32_i(sum);
+}
+
 // Scale layout of a repacked Q4_0 matrix (n rows, nb blocks per row): tiles
 // of `tile` rows (a power of two), tile-major, so the scales of the rows a
 // mat-vec workgroup owns are one contiguous run per block:

@@ -187,6 +187,42 @@ def test_prefill_7b_2048_sampled_rows(oracle):
     L.close()
 
 
+@pytest.mark.parametrize("shape,ntok,prefix", [
+    ("0.5b", 100, 45),      # hdim 64, 7 heads per KV group; ragged last tile
+    ("7b", 70, 30),         # hdim 128, 7 heads per group
+    ("1.5b_ref", 33, 0),    # hdim 128, 6 heads per group; one token past a tile
+    ("0.5b", 1, 0),         # a single token
+])
+def test_prefill_attention_every_row(oracle, shape, ntok, prefix):
+    """Causal prefill attention of every token of the batch (tiles of 32
+    tokens, cached prefix rows) against attention_flash on the same q and
+    cache, and its Q8_0 quantization bit-exact."""
+    torch = _torch()
+    s, os_ = _shapes(shape)
+    lay = make_layer(oracle, os_, 21, ffn=False)
+    kvd, QD = s.kvheads * s.hdim, s.qheads * s.hdim
+    rng = np.random.default_rng(22)
+    total = prefix + ntok
+    x = rng.standard_normal((ntok, s.hidden)).astype(np.float32)
+    kc0 = np.zeros(total * kvd, np.uint16)
+    vc0 = np.zeros_like(kc0)
+    kc0[:prefix * kvd] = kv_history(oracle, rng, prefix, kvd)
+    vc0[:prefix * kvd] = kv_history(oracle, rng, prefix, kvd)
+    L = si_amd.Layer(s, lay, ntok, total)
+    kc, vc = dev(kc0.view(np.int16)), dev(vc0.view(np.int16))
+    out = empty(ntok * s.hidden, torch.float32)
+    L.prefill(dev(x), ntok, prefix, kc, vc, out, si_amd.SI_LAYER_ATTN_ONLY)
+    B = LayerBuffers(L, os_, ntok)
+    hk, hv = host(kc).view(np.uint16), host(vc).view(np.uint16)
+    for t in range(ntok):
+        want = oracle.attention_flash(os_, B.q[t], hk, hv, prefix + t + 1)
+        close(B.attn[t], want, 2e-3, f"row {t} attention")
+        assert np.array_equal(B.attq[t].view(np.uint8),
+                              oracle.quantize_q8(B.attn[t]).view(np.uint8)), f"row {t} Q8"
+    assert QD == B.attn.shape[1]
+    L.close()
+
+
 def test_prefill_equals_sequential_decode(oracle):
     """bench_ai_dma_prefill.c:104-129: a prefill batch and a loop of
     single-token decodes leave bit-identical fp16 K/V for every position and
