@@ -181,6 +181,10 @@ int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
                k);
     SI_REQUIRE(tile_ok(tile), "gemm: tile %d not 8, 16, 32 or 64", tile);
     SI_REQUIRE(ldo >= n, "gemm: ldo %d < n %d", ldo, n);
+    // the kernels address each operand with 32-bit byte offsets
+    SI_REQUIRE((size_t)m * k < ((size_t)1 << 31) && (size_t)n * k / 2 < ((size_t)1 << 31) &&
+                   q4_scale_count(n, k / 32, tile) * 2 < ((size_t)1 << 31),
+               "gemm: operands beyond 2 GiB (m=%d n=%d k=%d)", m, n, k);
     SI_REQUIRE(m == 0 || (wqs && wd && xqs && xd && out), "gemm: NULL pointer");
     SI_REQUIRE(((uintptr_t)wqs & 15) == 0 && ((uintptr_t)xqs & 15) == 0,
                "gemm: wqs and xqs must be 16-byte aligned");

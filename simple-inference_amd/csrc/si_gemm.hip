@@ -187,46 +187,74 @@ struct GemmCfg {
     }
 };
 
-// Register staging of one LDS stage of k_gemm_fast (branch-free loads:
-// clamped rows and blocks).
+// Buffer descriptor of `bytes` bytes at p (raw buffer: a load whose offset
+// lies at or past the end returns zero instead of faulting).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+// Register staging of one LDS stage of k_gemm_fast.  Each thread's byte
+// offsets inside a stage are fixed (rows clamped once); a stage moves the
+// buffer bases, scalar work, so a stage costs no per-load VALU address math.
+// Blocks past the split (read, never used) stay in bounds or read as zero.
 template <int BM, int BN, int A_PT, int B_PT, int SX_PT, int SW_PT>
 struct GemmStage {
     v4i ra[A_PT], rb[B_PT];  // clang vectors: kept in registers
     uint16_t rsx[SX_PT], rsw[SW_PT];
+    uint32_t oa[A_PT], ob[B_PT], osx[SX_PT], osw[SW_PT];
 
-    __device__ __forceinline__ void load(const uint8_t *__restrict__ wqs,
-                                         const uint16_t *__restrict__ wd, int tile, int n, int nb,
-                                         const int8_t *__restrict__ xqs,
-                                         const uint16_t *__restrict__ xd, int m, int m0, int n0,
-                                         int bs, int b_end) {
+    __device__ __forceinline__ void init(int tile, int n, int nb, int m, int m0, int n0) {
         const int tid = threadIdx.x, k = nb * SI_QK;
         constexpr int A_PIECES = BM * G_KB * 2, B_PIECES = BN * G_KB;
 #pragma unroll
         for (int i = 0; i < A_PT; ++i) {
             const int p = min(tid + 256 * i, A_PIECES - 1);
             const int row = p / (G_KB * 2), blk = (p >> 1) % G_KB, half = p & 1;
-            const int gr = min(m0 + row, m - 1), gb = min(bs + blk, b_end - 1);
-            ra[i] = *(const v4i *)(xqs + (size_t)gr * k + (size_t)gb * SI_QK + half * 16);
+            oa[i] = (uint32_t)(min(m0 + row, m - 1) * k + blk * SI_QK + half * 16);
         }
 #pragma unroll
         for (int i = 0; i < B_PT; ++i) {
             const int p = min(tid + 256 * i, B_PIECES - 1);
             const int row = p / G_KB, blk = p % G_KB;
-            const int gr = min(n0 + row, n - 1), gb = min(bs + blk, b_end - 1);
-            rb[i] = *(const v4i *)(wqs + ((size_t)gb * n + gr) * 16);
+            ob[i] = (uint32_t)((blk * n + min(n0 + row, n - 1)) * 16);
         }
 #pragma unroll
         for (int i = 0; i < SX_PT; ++i) {
             const int p = min(tid + 256 * i, BM * G_KB - 1);
             const int row = p / G_KB, blk = p % G_KB;
-            rsx[i] = xd[(size_t)min(m0 + row, m - 1) * nb + min(bs + blk, b_end - 1)];
+            osx[i] = (uint32_t)((min(m0 + row, m - 1) * nb + blk) * 2);
         }
 #pragma unroll
         for (int i = 0; i < SW_PT; ++i) {
             const int p = min(tid + 256 * i, BN * G_KB - 1);
             const int row = p / G_KB, blk = p % G_KB;
-            rsw[i] = wd[q4_scale_index(min(n0 + row, n - 1), min(bs + blk, b_end - 1), nb, tile)];
+            osw[i] = (uint32_t)(q4_scale_index(min(n0 + row, n - 1), blk, nb, tile) * 2);
         }
+    }
+
+    // stage starting at block bs (< nb)
+    __device__ __forceinline__ void load(const uint8_t *__restrict__ wqs,
+                                         const uint16_t *__restrict__ wd, int tile, int n, int nb,
+                                         const int8_t *__restrict__ xqs,
+                                         const uint16_t *__restrict__ xd, int m, int bs) {
+        const uint32_t k = (uint32_t)nb * SI_QK;
+        const __amdgpu_buffer_rsrc_t ra_s = buf_rsrc(xqs + (size_t)bs * SI_QK,
+                                                     (uint32_t)m * k - (uint32_t)bs * SI_QK);
+        const __amdgpu_buffer_rsrc_t rb_s = buf_rsrc(wqs + (size_t)bs * n * 16,
+                                                     (uint32_t)(nb - bs) * (uint32_t)n * 16);
+        const __amdgpu_buffer_rsrc_t rx_s = buf_rsrc(xd + bs, ((uint32_t)m * nb - bs) * 2);
+        const uint32_t wcount = (uint32_t)q4_scale_count(n, nb, tile);
+        const __amdgpu_buffer_rsrc_t rw_s = buf_rsrc(wd + (size_t)bs * tile,
+                                                     (wcount - (uint32_t)bs * tile) * 2);
+#pragma unroll
+        for (int i = 0; i < A_PT; ++i) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(ra_s, oa[i], 0, 0);
+#pragma unroll
+        for (int i = 0; i < B_PT; ++i) rb[i] = __builtin_amdgcn_raw_buffer_load_b128(rb_s, ob[i], 0, 0);
+#pragma unroll
+        for (int i = 0; i < SX_PT; ++i) rsx[i] = __builtin_amdgcn_raw_buffer_load_b16(rx_s, osx[i], 0, 0);
+#pragma unroll
+        for (int i = 0; i < SW_PT; ++i) rsw[i] = __builtin_amdgcn_raw_buffer_load_b16(rw_s, osw[i], 0, 0);
     }
 
     __device__ __forceinline__ void store(uint8_t *a_l, uint8_t *b_l, uint16_t *sx_l,
@@ -308,7 +336,8 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
             for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
 
     const int nstage = (b_end - b_begin + G_KB - 1) / G_KB;
-    stg.load(wqs, wd, tile, n, nb, xqs, xd, m, m0, n0, b_begin, b_end);
+    stg.init(tile, n, nb, m, m0, n0);
+    stg.load(wqs, wd, tile, n, nb, xqs, xd, m, b_begin);
     // One LDS stage: the next stage's global loads are in flight in registers
     // while this one is consumed; the trailing barrier frees the LDS.
     for (int st = 0; st < nstage; ++st) {
@@ -317,9 +346,8 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
         __syncthreads();
         const int bs = b_begin + st * G_KB;
         // next stage in flight (branch-free: the last iteration re-reads
-        // its own stage, clamped, and never stores it)
-        stg.load(wqs, wd, tile, n, nb, xqs, xd, m, m0, n0,
-                 min(bs + G_KB, b_begin + (nstage - 1) * G_KB), b_end);
+        // its own stage and never stores it)
+        stg.load(wqs, wd, tile, n, nb, xqs, xd, m, min(bs + G_KB, b_begin + (nstage - 1) * G_KB));
 #pragma unroll
         for (int blk = 0; blk < G_KB; ++blk) {
             if (bs + blk >= b_end) break;
