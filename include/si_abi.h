@@ -136,6 +136,18 @@ int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
                  int flags, void *workspace, size_t ws_bytes, void *stream);
 size_t si_gemm_workspace(int m, int n, int k);
 
+/* The FFN gate|up projection of m activation rows with SwiGLU and Q8_0:
+ * gu = [gate | up] = matvec_q4q8 of each row (qwen_one_layer.c:148-162)
+ * against the 2f x k matrix [gate rows; up rows], act = silu(gate)*up,
+ * quantize_q8(act) (:98-116) into planar qs/d/bsum ([m][f], [m][f/32]).
+ * gu ([m][2f] fp32) is written too and serves as the intermediate when the
+ * plan splits K (workspace from si_gemm_workspace(m, 2f, k)); act and bsum
+ * may be NULL.  flags: SI_GEMM_EXACT as for si_gemm_q4q8. */
+int si_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, int k,
+                      const int8_t *xqs, const uint16_t *xd, int m, float *gu, float *act,
+                      int8_t *qs, uint16_t *d, int16_t *bsum, int flags, void *workspace,
+                      size_t ws_bytes, void *stream);
+
 /* The decode FFN front half for one row, fused: rmsnorm(h, gain)
  * (qwen_one_layer.c:164-169) -> quantize_q8 (:98-116) -> gate and up
  * projections (matvec_q4q8, :148-162) -> act = silu(gate)*up ->

@@ -195,6 +195,26 @@ int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
     return check_launch("si_gemm_q4q8");
 }
 
+int si_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, int k,
+                      const int8_t *xqs, const uint16_t *xd, int m, float *gu, float *act,
+                      int8_t *qs, uint16_t *d, int16_t *bsum, int flags, void *workspace,
+                      size_t ws_bytes, void *stream) {
+    SI_REQUIRE(f > 0 && f % 32 == 0 && k > 0 && k % 32 == 0 && m >= 0,
+               "gemm_gateup: bad size m=%d f=%d k=%d", m, f, k);
+    SI_REQUIRE(tile_ok(tile), "gemm_gateup: tile %d not 8, 16, 32 or 64", tile);
+    SI_REQUIRE((size_t)m * k < ((size_t)1 << 31) && (size_t)f * k < ((size_t)1 << 31) &&
+                   q4_scale_count(2 * f, k / 32, tile) * 2 < ((size_t)1 << 31),
+               "gemm_gateup: operands beyond 2 GiB (m=%d f=%d k=%d)", m, f, k);
+    SI_REQUIRE(m == 0 || (wqs && wd && xqs && xd && gu && qs && d), "gemm_gateup: NULL pointer");
+    SI_REQUIRE(((uintptr_t)wqs & 15) == 0 && ((uintptr_t)xqs & 15) == 0,
+               "gemm_gateup: wqs and xqs must be 16-byte aligned");
+    SI_REQUIRE((flags & ~SI_GEMM_EXACT) == 0, "gemm_gateup: unknown flags %d", flags);
+    launch_gemm_gateup_q8(wqs, wd, tile, f, k, xqs, xd, m, gu, act, qs, d, bsum,
+                          (flags & SI_GEMM_EXACT) != 0, workspace, workspace ? ws_bytes : 0,
+                          S(stream));
+    return check_launch("si_gemm_gateup_q8");
+}
+
 size_t si_gemm_workspace(int m, int n, int k) {
     if (m <= 0 || n <= 0 || k <= 0 || k % 32) return 0;
     return gemm_workspace_bytes(m, n, k);
@@ -781,9 +801,18 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
     launch_rmsnorm_q8(x, L->attn_out, L->post_norm, rows, H, s.rms_eps, L->h, L->normed2,
                       L->xq2.qs, L->xq2.d, L->xq2.s, st);
     mark(L, SI_PHASE_GATE_UP, st);
-    project(L, L->wgu, rows, L->xq2, nullptr, nullptr, L->gu, flags, st);
-    mark(L, SI_PHASE_SWIGLU_Q8, st);
-    launch_swiglu_q8(L->gu, rows, s.ffn, L->act, L->actq.qs, L->actq.d, L->actq.s, st);
+    if (rows == 1) {
+        project(L, L->wgu, rows, L->xq2, nullptr, nullptr, L->gu, flags, st);
+        mark(L, SI_PHASE_SWIGLU_Q8, st);
+        launch_swiglu_q8(L->gu, rows, s.ffn, L->act, L->actq.qs, L->actq.d, L->actq.s, st);
+    } else {
+        // SwiGLU -> Q8 in the gate|up GEMM's epilogue (the swiglu_q8 phase
+        // is then empty)
+        launch_gemm_gateup_q8(L->wgu.qs, L->wgu.d, L->wgu.tile, s.ffn, H, L->xq2.qs, L->xq2.d,
+                              rows, L->gu, L->act, L->actq.qs, L->actq.d, L->actq.s,
+                              (flags & SI_LAYER_EXACT) != 0, L->gemm_ws, L->gemm_ws_bytes, st);
+        mark(L, SI_PHASE_SWIGLU_Q8, st);
+    }
     mark(L, SI_PHASE_DOWN, st);
     project(L, L->wdown, rows, L->actq, nullptr, L->h, out, flags, st);
     mark(L, SI_PHASE_COUNT, st);

@@ -187,6 +187,23 @@ struct GemmCfg {
     }
 };
 
+// Gate|up fusion order: logical rows alternate 32 gate rows (physical
+// 0..f-1) and the 32 up rows of the same features (physical f..2f-1), so a
+// wavefront's two 32-column tiles hold gate and up of the same 32 features.
+__device__ __forceinline__ int gate_up_row(int r, int f) {
+    const int j = 32 * (r >> 6) + (r & 31);
+    return (r & 32) ? f + j : j;
+}
+
+// Outputs of the fused SwiGLU + Q8_0 epilogue.
+struct GateUpOut {
+    int f;
+    float *act;     // optional fp32 SwiGLU output [m][f]
+    int8_t *qs;     // Q8_0 of the SwiGLU output, planar [m][f]
+    uint16_t *d;    // [m][f/32] fp16 scale bits
+    int16_t *s;     // optional [m][f/32] block sums
+};
+
 // Buffer descriptor of `bytes` bytes at p (raw buffer: a load whose offset
 // lies at or past the end returns zero instead of faulting).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes) {
@@ -204,7 +221,9 @@ struct GemmStage {
     uint16_t rsx[SX_PT], rsw[SW_PT];
     uint32_t oa[A_PT], ob[B_PT], osx[SX_PT], osw[SW_PT];
 
-    __device__ __forceinline__ void init(int tile, int n, int nb, int m, int m0, int n0) {
+    // gu_f > 0: logical weight row r is physical row gate_up_row(r, gu_f)
+    __device__ __forceinline__ void init(int tile, int n, int nb, int m, int m0, int n0,
+                                         int gu_f) {
         const int tid = threadIdx.x, k = nb * SI_QK;
         constexpr int A_PIECES = BM * G_KB * 2, B_PIECES = BN * G_KB;
 #pragma unroll
@@ -217,7 +236,8 @@ struct GemmStage {
         for (int i = 0; i < B_PT; ++i) {
             const int p = min(tid + 256 * i, B_PIECES - 1);
             const int row = p / G_KB, blk = p % G_KB;
-            ob[i] = (uint32_t)((blk * n + min(n0 + row, n - 1)) * 16);
+            const int lr = min(n0 + row, n - 1);
+            ob[i] = (uint32_t)((blk * n + (gu_f ? gate_up_row(lr, gu_f) : lr)) * 16);
         }
 #pragma unroll
         for (int i = 0; i < SX_PT; ++i) {
@@ -229,7 +249,8 @@ struct GemmStage {
         for (int i = 0; i < SW_PT; ++i) {
             const int p = min(tid + 256 * i, BN * G_KB - 1);
             const int row = p / G_KB, blk = p % G_KB;
-            osw[i] = (uint32_t)(q4_scale_index(min(n0 + row, n - 1), blk, nb, tile) * 2);
+            const int lr = min(n0 + row, n - 1);
+            osw[i] = (uint32_t)(q4_scale_index(gu_f ? gate_up_row(lr, gu_f) : lr, blk, nb, tile) * 2);
         }
     }
 
@@ -306,12 +327,17 @@ struct GemmStage {
     }
 };
 
-template <int WM, int WN, int TM, int TN>
+// FUSE: the weights are a gate|up pair (n = 2f, the physical rows gate then
+// up), read in gate_up_row order; the epilogue writes the gate|up outputs in
+// physical order to out (optional) and SwiGLU + Q8_0 (k_swiglu_q8's rules)
+// to go.  Needs TN == 2 and one K split.
+template <int WM, int WN, int TM, int TN, bool FUSE>
 __global__ void __launch_bounds__(256) k_gemm_fast(
     const uint8_t *__restrict__ wqs, const uint16_t *__restrict__ wd, int tile, int n, int nb,
     const int8_t *__restrict__ xqs, const uint16_t *__restrict__ xd, int m,
     const float *__restrict__ bias, const float *__restrict__ residual, float *__restrict__ out,
-    int ldo, float *__restrict__ part, int bps) {
+    int ldo, float *__restrict__ part, int bps, GateUpOut go) {
+    static_assert(!FUSE || TN == 2, "gate|up fusion pairs two column tiles per wavefront");
     using C = GemmCfg<WM, WN, TM, TN>;
     constexpr int BM = C::BM, BN = C::BN;
     extern __shared__ __attribute__((aligned(16))) uint8_t gsm[];
@@ -336,7 +362,7 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
             for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
 
     const int nstage = (b_end - b_begin + G_KB - 1) / G_KB;
-    stg.init(tile, n, nb, m, m0, n0);
+    stg.init(tile, n, nb, m, m0, n0, FUSE ? go.f : 0);
     stg.load(wqs, wd, tile, n, nb, xqs, xd, m, b_begin);
     // One LDS stage: the next stage's global loads are in flight in registers
     // while this one is consumed; the trailing barrier frees the LDS.
@@ -389,6 +415,39 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
     }
 
     // output (i, j) of a 32x32 tile: lane j + 32*((i/4)%2), register (i%4) + 4*(i/8)
+    if (FUSE) {
+        const int f = go.f;
+        const int feat = (n0 + wn * 64) / 2 + j;  // this lane's feature
+        const bool fok = feat < f;                // a 32-feature block is all in or all out
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int row = m0 + (wm * TM + a) * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
+                const float gv = acc[a][0][v], uv = acc[a][TN - 1][v];
+                // SwiGLU exactly as k_swiglu_q8, then the block's Q8_0 over
+                // the 32 lanes of this half (every lane takes part)
+                const float silu = __fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)));
+                const float av = __fmul_rn(silu, uv);
+                uint16_t dbits;
+                int bsum;
+                const int q = quant_block_lane(av, dbits, bsum);
+                if (row < m && fok) {
+                    const size_t o = (size_t)row * f + feat;
+                    if (out) {
+                        out[(size_t)row * ldo + feat] = gv;
+                        out[(size_t)row * ldo + f + feat] = uv;
+                    }
+                    if (go.act) go.act[o] = av;
+                    go.qs[o] = (int8_t)q;
+                    if (j == 0) {
+                        go.d[o / SI_QK] = dbits;
+                        if (go.s) go.s[o / SI_QK] = (int16_t)bsum;
+                    }
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int a = 0; a < TM; ++a)
 #pragma unroll
@@ -470,9 +529,9 @@ void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, i
     float *part = p.splits > 1 ? (float *)workspace : nullptr;
     const dim3 grid((n + p.bn - 1) / p.bn, (m + p.bm - 1) / p.bm, p.splits);
 #define CALL(WM, WN, TM, TN)                                                                   \
-    hipLaunchKernelGGL((k_gemm_fast<WM, WN, TM, TN>), grid, dim3(256),                         \
+    hipLaunchKernelGGL((k_gemm_fast<WM, WN, TM, TN, false>), grid, dim3(256),                  \
                        (GemmCfg<WM, WN, TM, TN>::lds_bytes()), st, wqs, wd, tile, n, nb, xqs,   \
-                       xd, m, bias, residual, out, ldo, part, p.bps)
+                       xd, m, bias, residual, out, ldo, part, p.bps, GateUpOut{})
     if (p.bm == 64)
         CALL(1, 4, 2, 1);
     else
@@ -483,6 +542,35 @@ void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, i
         hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st,
                            part, p.splits, m, n, bias, residual, out, ldo);
     }
+}
+
+// gate|up GEMM with SwiGLU + Q8_0: f features, weights the physical
+// [gate; up] rows.  One fused kernel when the plan needs no K split;
+// otherwise (and in exact mode) the GEMM into gu, then k_swiglu_q8.
+void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, int k,
+                           const int8_t *xqs, const uint16_t *xd, int m, float *gu, float *act,
+                           int8_t *qs, uint16_t *d, int16_t *s, bool exact, void *workspace,
+                           size_t ws_bytes, hipStream_t st) {
+    if (m <= 0) return;
+    const int n = 2 * f, nb = k / SI_QK;
+    const GemmPlan p = gemm_plan(m, n, nb);
+    if (exact || p.splits > 1) {
+        launch_gemm_q4q8(wqs, wd, tile, n, k, xqs, xd, m, nullptr, nullptr, gu, n, exact,
+                         workspace, ws_bytes, st);
+        launch_swiglu_q8(gu, m, f, act, qs, d, s, st);
+        return;
+    }
+    const GateUpOut go{f, act, qs, d, s};
+    const dim3 grid((n + p.bn - 1) / p.bn, (m + p.bm - 1) / p.bm, 1);
+#define CALL(WM, WN, TM, TN)                                                                   \
+    hipLaunchKernelGGL((k_gemm_fast<WM, WN, TM, TN, true>), grid, dim3(256),                   \
+                       (GemmCfg<WM, WN, TM, TN>::lds_bytes()), st, wqs, wd, tile, n, nb, xqs,   \
+                       xd, m, nullptr, nullptr, gu, n, nullptr, nb, go)
+    if (p.bm == 64)
+        CALL(2, 2, 1, 2);
+    else
+        CALL(2, 2, 2, 2);
+#undef CALL
 }
 
 }  // namespace si

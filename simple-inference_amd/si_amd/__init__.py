@@ -81,6 +81,8 @@ _SIGS = {
     "si_ffn_gateup_q8": (_I, [_P, _P, _I, _F, _P, _P, _I, _I, _P, _P, _P, _P, _I, _P]),
     "si_gemm_q4q8": (_I, [_P, _P, _I, _I, _I, _P, _P, _I, _P, _P, _P, _I, _I, _P, _Z, _P]),
     "si_gemm_workspace": (_Z, [_I, _I, _I]),
+    "si_gemm_gateup_q8": (_I, [_P, _P, _I, _I, _I, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _Z,
+                               _P]),
     "si_rope_kv_append": (_I, [ctypes.POINTER(Shape), _P, _I, _I, _I, _I, _I, _P, _P, _P, _P,
                                _P, _P, _Z, _P]),
     "si_rope_table": (_I, [_I, _I, _F, _P, _P]),

@@ -529,3 +529,63 @@ def test_ffn_gateup_q8(oracle, shape, flags):
     assert np.array_equal(host(aq), want_q)
     assert np.array_equal(host(ad).view(np.uint16), want_d)
     assert np.array_equal(host(asum), want_s)
+
+
+@pytest.mark.parametrize("m,f,k,tile,flags,act_out", [
+    (130, 96, 256, 8, 0, True),          # ragged rows, f an odd number of 32-blocks
+    (64, 4864, 896, 32, 0, True),        # 0.5B batched-decode shape (64-row tiles)
+    (512, 4864, 896, 32, 0, False),      # 0.5B prefill shape; also without act and sums
+    (2, 160, 96, 16, 0, True),           # tiny: the plan splits K (GEMM + SwiGLU kernel)
+    (300, 4864, 896, 32, si_amd.SI_GEMM_EXACT, True),
+])
+def test_gemm_gateup_q8(oracle, m, f, k, tile, flags, act_out):
+    """gate|up GEMM with the SwiGLU + Q8_0 epilogue: every row's gate|up
+    against the float64 product of the dequantized operands (bit-exact with
+    the reference's matvec under SI_GEMM_EXACT), SwiGLU on the GPU's own
+    gate|up within 1e-6, and its Q8_0 bit-exact."""
+    torch = _torch()
+    rng = np.random.default_rng(m + f + k)
+    wg, wu = q4(oracle, rng, f, k), q4(oracle, rng, f, k)
+    w = np.concatenate([wg, wu])
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    xq = oracle.quantize_q8(x)
+    qs, d, _ = aos_to_planar(xq)
+    wqs, wd, _ = _upload_q4(w, 2 * f, k, tile)
+    wsb = si_amd.lib().si_gemm_workspace(m, 2 * f, k)
+    ws = empty(max(wsb, 4), torch.uint8)
+    xqs_d, xd_d = dev(qs), dev(d.view(np.int16))
+
+    def run(with_act):
+        gu = empty(m * 2 * f, torch.float32)
+        act = empty(m * f, torch.float32) if with_act else None
+        aq, ad = empty(m * f, torch.int8), empty(m * f // 32, torch.int16)
+        asum = empty(m * f // 32, torch.int16) if with_act else None
+        si_amd.call("si_gemm_gateup_q8", si_amd.ptr(wqs), si_amd.ptr(wd), tile, f, k,
+                    si_amd.ptr(xqs_d), si_amd.ptr(xd_d), m, si_amd.ptr(gu), si_amd.ptr(act),
+                    si_amd.ptr(aq), si_amd.ptr(ad), si_amd.ptr(asum), flags, si_amd.ptr(ws),
+                    wsb, None)
+        return gu, act, aq, ad, asum
+
+    gu, act, aq, ad, asum = run(True)
+    if not act_out:  # NULL act and block sums: the same gate|up and Q8_0
+        gu2, _, aq2, ad2, _ = run(False)
+        assert np.array_equal(host(gu2).view(np.uint32), host(gu).view(np.uint32))
+        assert np.array_equal(host(aq2), host(aq))
+        assert np.array_equal(host(ad2), host(ad))
+    g = host(gu).reshape(m, 2 * f)
+    nb = k // 32
+    if flags:
+        for r in sorted({0, m // 2, m - 1}):
+            want = oracle.matvec(w, xq[r * nb:(r + 1) * nb], k, 2 * f)
+            assert np.array_equal(g[r].view(np.uint32), want.view(np.uint32)), f"row {r}"
+    else:
+        want = dequant_q8(xq, m, k) @ dequant_q4(w, 2 * f, k).T
+        rms = np.sqrt(np.mean(want ** 2))
+        err = np.abs(g - want).max(axis=1) / rms
+        assert err.max() <= 1e-5, f"gate|up rows off: worst {err.max():.3g} at {int(err.argmax())}"
+    sw = np.stack([oracle.swiglu(g[r, :f], g[r, f:]) for r in range(m)])
+    close(host(act), sw, 1e-6, "SwiGLU")
+    want_q, want_d, want_s = aos_to_planar(oracle.quantize_q8(host(act)))
+    assert np.array_equal(host(aq), want_q)
+    assert np.array_equal(host(ad).view(np.uint16), want_d)
+    assert np.array_equal(host(asum), want_s)

@@ -44,6 +44,14 @@ def test_argument_errors_do_not_launch():
     assert b"multiple of 32" in L.si_last_error()
     assert L.si_gemm_q4q8(None, None, 8, 64, 30, None, None, 4, None, None, None, 64, 0,
                           None, 0, None) == si_amd.SI_ERR_ARG
+    assert L.si_gemm_gateup_q8(None, None, 8, 48, 64, None, None, 4, None, None, None, None,
+                               None, 0, None, 0, None) == si_amd.SI_ERR_ARG  # f % 32
+    assert L.si_gemm_gateup_q8(None, None, 8, 64, 64, None, None, 4, None, None, None, None,
+                               None, 0, None, 0, None) == si_amd.SI_ERR_ARG  # NULL
+    assert b"NULL" in L.si_last_error()
+    assert L.si_gemm_q4q8(None, None, 8, 1 << 20, 8192, None, None, 4, None, None, None,
+                          1 << 20, 0, None, 0, None) == si_amd.SI_ERR_ARG
+    assert b"2 GiB" in L.si_last_error()
     assert L.si_gemm_workspace(64, 3584, 18944) > 0  # small grid: K is split
     assert L.si_gemm_workspace(2048, 3584, 3584) == 0
     assert L.si_matvec_q4q8(None, None, 8, 64, 64, None, None, None, None, None, None, 0,
