@@ -494,8 +494,17 @@ static GemmPlan gemm_plan(int m, int n, int nb) {
     p.bm = m <= 64 ? 64 : 128;
     p.bn = 128;
     const int tiles = ((n + p.bn - 1) / p.bn) * ((m + p.bm - 1) / p.bm);
-    int s = (256 + tiles - 1) / tiles;  // >= one workgroup per CU
-    const int maxs = nb / (2 * G_KB);   // >= 2 stages per split
+    // K splits: a grid of W ~ 4.5 sqrt(tiles * nb) workgroups balances the
+    // CUs against the split partial-sum traffic (fitted on the 7B and 0.5B
+    // projections at 64 and 2048 rows); a grid that already fills the chip
+    // over a short K is not split (the partials would cost more than the
+    // tail they remove).
+    int s = 1;
+    if (!(tiles >= 384 && nb < 256)) {
+        const double w = 4.5 * sqrt((double)tiles * nb);
+        s = (int)lround(w / tiles);
+    }
+    const int maxs = nb / (2 * G_KB);  // >= 2 stages per split
     if (s > maxs) s = maxs;
     if (s < 1) s = 1;
     p.bps = (nb + s - 1) / s;
