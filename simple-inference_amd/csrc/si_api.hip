@@ -274,8 +274,15 @@ int si_attention(const si_shape_t *s, const float *q, int nq, const uint16_t *kc
     SI_REQUIRE(nq == 0 || (q && kc && vc && attn && ws), "attention: NULL pointer");
     SI_REQUIRE(!qs || d, "attention: qs without d");
     SI_REQUIRE(ws_bytes >= si_attention_workspace(s, nq, max_ctx), "attention: workspace too small");
-    launch_attention(q, nq, s->qheads, s->kvheads, s->hdim, kc, vc, kv_seq_stride, ctx_dev, ctx0,
-                     ctx_step, max_ctx, attn, qs, d, bsum, ws, S(stream));
+    if (!ctx_dev && ctx_step == 1 && kv_seq_stride == 0 && nq > 1 &&
+        attn_prefill_supported(s->qheads, s->kvheads, s->hdim))
+        // causal prefill of one sequence: the flash kernel (query i at
+        // cache row ctx0 - 1 + i)
+        launch_attn_prefill(q, nq, s->qheads, s->kvheads, s->hdim, ctx0 - 1, kc, vc, attn, qs, d,
+                            bsum, S(stream));
+    else
+        launch_attention(q, nq, s->qheads, s->kvheads, s->hdim, kc, vc, kv_seq_stride, ctx_dev,
+                         ctx0, ctx_step, max_ctx, attn, qs, d, bsum, ws, S(stream));
     return check_launch("si_attention");
 }
 

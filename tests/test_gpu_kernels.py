@@ -430,12 +430,13 @@ def test_attention_batched_sequences(oracle):
         close(got[i], want, 2e-3, f"seq {i}")
 
 
-def test_attention_causal_prefill(oracle):
-    """nq query rows over one cache: row t attends to prefix+t+1 positions."""
+@pytest.mark.parametrize("shape,ntok,prefix", [("0.5b", 40, 300), ("7b", 45, 17)])
+def test_attention_causal_prefill(oracle, shape, ntok, prefix):
+    """nq query rows over one cache (the flash prefill kernel): row t attends
+    to prefix+t+1 positions; every row and its Q8_0."""
     torch = _torch()
-    sd = si_amd.SHAPES["0.5b"]
+    sd = si_amd.SHAPES[shape]
     s, os_ = si_amd.make_shape(**sd), or_shape(**sd)
-    ntok, prefix = 40, 300
     KVD, QD = s.kvheads * s.hdim, s.qheads * s.hdim
     rng = np.random.default_rng(7)
     total = prefix + ntok
@@ -445,14 +446,18 @@ def test_attention_causal_prefill(oracle):
     ws_bytes = si_amd.lib().si_attention_workspace(ctypes.byref(s), ntok, total)
     ws = empty(ws_bytes, torch.uint8)
     out = empty(ntok * QD, torch.float32)
+    aq, ad = empty(ntok * QD, torch.int8), empty(ntok * QD // 32, torch.int16)
     si_amd.call("si_attention", ctypes.byref(s), si_amd.ptr(dev(q)), ntok,
                 si_amd.ptr(dev(kc.view(np.int16))), si_amd.ptr(dev(vc.view(np.int16))), 0, None,
-                prefix + 1, 1, total, si_amd.ptr(out), None, None, None, si_amd.ptr(ws),
-                ws_bytes, None)
+                prefix + 1, 1, total, si_amd.ptr(out), si_amd.ptr(aq), si_amd.ptr(ad), None,
+                si_amd.ptr(ws), ws_bytes, None)
     got = host(out).reshape(ntok, QD)
-    for t in (0, 1, 17, ntok - 1):
+    for t in range(ntok):
         want = oracle.attention_flash(os_, q[t], kc, vc, prefix + t + 1)
         close(got[t], want, 2e-3, f"row {t}")
+    want_q, want_d, _ = aos_to_planar(oracle.quantize_q8(got.reshape(-1)))
+    assert np.array_equal(host(aq), want_q)
+    assert np.array_equal(host(ad).view(np.uint16), want_d)
 
 
 def test_mfma_f16_lane_layouts():
