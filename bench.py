@@ -446,6 +446,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--dominant-only", action="store_true",
                     help="run only the dominant-kernel leg (for rocprofv3)")
+    ap.add_argument("--only", choices=["prefill-0.5b", "prefill-7b", "batched-7b"],
+                    help="run only this configuration and print its result (for rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); "
@@ -458,6 +460,14 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs an MI355X"
     torch.cuda.set_device(0)
     stream = torch.cuda.Stream()
+    if args.only:
+        if args.only == "batched-7b":
+            r = bench_batched_decode(torch, si_amd, stream, 5)
+        else:
+            name, ntok = ("0.5b", 512) if args.only == "prefill-0.5b" else ("7b", 2048)
+            r = bench_prefill(torch, si_amd, stream, name, ntok, 3)
+        print(json.dumps({"only": args.only, **r}), flush=True)
+        return
     if args.dominant_only:
         dom = bench_dominant_kernel(torch, si_amd, stream)
         print(json.dumps({"dominant_kernel": dom["kernel"], "us": round(dom["us"], 3),

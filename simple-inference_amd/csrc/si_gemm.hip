@@ -485,6 +485,35 @@ __global__ void __launch_bounds__(256) k_gemm_reduce(const float *__restrict__ p
     out[(size_t)row * ldo + col] = y;
 }
 
+// k_gemm_reduce over 4 consecutive outputs per thread (n % 4 == 0, ldo % 4
+// == 0, 16-byte aligned buffers): the split sums stream as float4.
+__global__ void __launch_bounds__(256) k_gemm_reduce4(const float *__restrict__ part, int splits,
+                                                      int m, int n, const float *__restrict__ bias,
+                                                      const float *__restrict__ residual,
+                                                      float *__restrict__ out, int ldo) {
+    const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t tot4 = (size_t)m * n / 4;
+    if (i4 >= tot4) return;
+    const size_t i = 4 * i4;
+    const int row = (int)(i / n), col = (int)(i - (size_t)row * n);
+    float4 y = *(const float4 *)(part + i);
+    for (int s = 1; s < splits; ++s) {
+        const float4 p = *(const float4 *)(part + (size_t)s * m * n + i);
+        y.x += p.x; y.y += p.y; y.z += p.z; y.w += p.w;
+    }
+    if (bias) {
+        const float4 b = *(const float4 *)(bias + col);
+        y.x += b.x; y.y += b.y; y.z += b.z; y.w += b.w;
+    }
+    float *o = out + (size_t)row * ldo + col;
+    if (residual) {
+        const float4 r = *(const float4 *)(residual + (size_t)row * ldo + col);
+        y = make_float4(__fadd_rn(r.x, y.x), __fadd_rn(r.y, y.y), __fadd_rn(r.z, y.z),
+                        __fadd_rn(r.w, y.w));
+    }
+    *(float4 *)o = y;
+}
+
 // Tile choice and K splits of the fast path for an m x n x nb problem.
 struct GemmPlan {
     int bm, bn, splits, bps;
@@ -548,8 +577,13 @@ void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, i
 #undef CALL
     if (part) {
         const size_t tot = (size_t)m * n;
-        hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st,
-                           part, p.splits, m, n, bias, residual, out, ldo);
+        const auto al = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
+        if (n % 4 == 0 && ldo % 4 == 0 && al(out) && al(bias) && al(residual))
+            hipLaunchKernelGGL(k_gemm_reduce4, dim3((unsigned)((tot / 4 + 255) / 256)), dim3(256),
+                               0, st, part, p.splits, m, n, bias, residual, out, ldo);
+        else
+            hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0,
+                               st, part, p.splits, m, n, bias, residual, out, ldo);
     }
 }
 

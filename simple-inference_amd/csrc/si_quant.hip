@@ -121,6 +121,66 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8(const float *__restrict__ x,
     quantize_lds_row(lds, n, r, qs, d, s);
 }
 
+// The same RMSNorm + Q8_0 with the row held in registers: thread t owns the
+// float4 chunks t + 256*i (i < NPT) of its workgroup's row, so 8 consecutive
+// threads hold one 32-value block and quantize it with quant_block_oct.  One
+// pass over global memory, no LDS staging; needs 16-byte aligned rows.
+template <bool RESIDUAL, int NPT>
+__global__ void __launch_bounds__(256) k_rmsnorm_q8_v4(const float *__restrict__ x,
+                                                       const float *__restrict__ y,
+                                                       const float *__restrict__ gain, int n,
+                                                       float eps, float *__restrict__ h_out,
+                                                       float *__restrict__ normed,
+                                                       int8_t *__restrict__ qs,
+                                                       uint16_t *__restrict__ d,
+                                                       int16_t *__restrict__ s) {
+    __shared__ double red[4];
+    const int r = blockIdx.x, tid = threadIdx.x, n4 = n / 4;
+    const size_t base = (size_t)r * n;
+    float v[NPT][4];
+    double ss = 0.0;
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+        const int c = min(tid + 256 * i, n4 - 1);  // clamped: branch-free loads
+        float4 a = *(const float4 *)(x + base + 4 * c);
+        if (RESIDUAL) {
+            const float4 b = *(const float4 *)(y + base + 4 * c);
+            a = make_float4(__fadd_rn(a.x, b.x), __fadd_rn(a.y, b.y), __fadd_rn(a.z, b.z),
+                            __fadd_rn(a.w, b.w));
+        }
+        v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
+        if (tid + 256 * i < n4) {
+            if (RESIDUAL) *(float4 *)(h_out + base + 4 * c) = a;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) ss += (double)v[i][k] * (double)v[i][k];
+        }
+    }
+    const double tot = block_sum_d(ss, red);
+    const float ms = (float)(tot / (double)n);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(ms, eps)));
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+        const int c = tid + 256 * i;
+        if (c < n4) {  // whole 8-thread groups (n is a multiple of 32)
+            const float4 gv = gain ? *(const float4 *)(gain + 4 * c) : make_float4(1.f, 1.f, 1.f, 1.f);
+            const float g4[4] = {gv.x, gv.y, gv.z, gv.w};
+            float o[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] = __fmul_rn(__fmul_rn(v[i][k], inv), g4[k]);
+            if (normed) *(float4 *)(normed + base + 4 * c) = make_float4(o[0], o[1], o[2], o[3]);
+            uint16_t dbits;
+            int bsum;
+            const uint32_t packed = quant_block_oct(o, dbits, bsum);
+            *(uint32_t *)(qs + base + 4 * c) = packed;
+            if ((tid & 7) == 0) {
+                const size_t bi = (base + 4 * c) / SI_QK;
+                d[bi] = dbits;
+                if (s) s[bi] = (int16_t)bsum;
+            }
+        }
+    }
+}
+
 // Build-defined SwiGLU then quantize_q8: a = (g / (1 + expf(-g))) * u.
 __global__ void __launch_bounds__(256) k_swiglu_q8(const float *__restrict__ gu, int f,
                                                    int nb_row, int total_blocks,
@@ -228,6 +288,29 @@ void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int ro
                        float eps, float *h, float *normed, int8_t *qs, uint16_t *d, int16_t *s,
                        hipStream_t st) {
     if (rows == 0) return;
+    const auto al = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    const int n4 = n / 4;
+    if (n4 <= 2048 && al(x) && al(y) && al(h) && al(normed) && al(gain) && al(qs)) {
+        const int npt = n4 <= 256 ? 1 : n4 <= 512 ? 2 : n4 <= 1024 ? 4 : 8;
+#define RMS_V4(RES, NPT)                                                                          \
+    hipLaunchKernelGGL((k_rmsnorm_q8_v4<RES, NPT>), dim3(rows), dim3(256), 0, st, x, y, gain, n, \
+                       eps, h, normed, qs, d, s)
+#define RMS_V4N(RES)                     \
+    switch (npt) {                       \
+        case 1: RMS_V4(RES, 1); break;   \
+        case 2: RMS_V4(RES, 2); break;   \
+        case 4: RMS_V4(RES, 4); break;   \
+        default: RMS_V4(RES, 8); break;  \
+    }
+        if (y) {
+            RMS_V4N(true);
+        } else {
+            RMS_V4N(false);
+        }
+#undef RMS_V4N
+#undef RMS_V4
+        return;
+    }
     const size_t lds = (size_t)n * sizeof(float);
     if (y)
         hipLaunchKernelGGL(k_rmsnorm_q8<true>, dim3(rows), dim3(256), lds, st, x, y, gain, n,
