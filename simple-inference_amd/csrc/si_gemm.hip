@@ -171,6 +171,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4q8(
 // ===========================================================================
 typedef _Float16 gh4 __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
 
 constexpr int G_KB = 2;   // K blocks per LDS stage (deeper stages cost occupancy)
 constexpr int G_ST = 48;  // LDS bytes per (row, block): 32 data + 16 padding
@@ -182,8 +183,12 @@ struct GemmCfg {
     static constexpr int B_PIECES = BN * G_KB;      // 16-byte nibble pieces per stage
     static constexpr int A_PT = (A_PIECES + 255) / 256, B_PT = (B_PIECES + 255) / 256;
     static constexpr int SX_PT = (BM * G_KB + 255) / 256, SW_PT = (BN * G_KB + 255) / 256;
+    // scales as 8-byte {fp16 bits, 0} entries: x.d [G_KB][BM]; w.d [G_KB][BN],
+    // 8 entries of padding, then a zero copy of the same shape that lanes
+    // 32..63 read (16 banks away from the real one)
+    static constexpr int SW_TWIN = G_KB * BN + 8;
     static constexpr size_t lds_bytes() {
-        return (size_t)G_KB * (BM + BN) * G_ST + (size_t)G_KB * (BM + BN) * 2;
+        return (size_t)G_KB * (BM + BN) * G_ST + (size_t)(G_KB * BM + SW_TWIN + G_KB * BN) * 8;
     }
 };
 
@@ -278,8 +283,8 @@ struct GemmStage {
         for (int i = 0; i < SW_PT; ++i) rsw[i] = __builtin_amdgcn_raw_buffer_load_b16(rw_s, osw[i], 0, 0);
     }
 
-    __device__ __forceinline__ void store(uint8_t *a_l, uint8_t *b_l, uint16_t *sx_l,
-                                          uint16_t *sw_l, int buf) const {
+    __device__ __forceinline__ void store(uint8_t *a_l, uint8_t *b_l, v2u *sx_l, v2u *sw_l,
+                                          int buf) const {
         const int tid = threadIdx.x;
         constexpr int A_PIECES = BM * G_KB * 2, B_PIECES = BN * G_KB;
 #pragma unroll
@@ -313,7 +318,7 @@ struct GemmStage {
             const int p = tid + 256 * i;
             if ((BM * G_KB) % 256 == 0 || p < BM * G_KB) {
                 const int row = p / G_KB, blk = p % G_KB;
-                sx_l[((size_t)buf * G_KB + blk) * BM + row] = rsx[i];
+                sx_l[((size_t)buf * G_KB + blk) * BM + row] = (v2u){(unsigned)rsx[i], 0u};
             }
         }
 #pragma unroll
@@ -321,7 +326,7 @@ struct GemmStage {
             const int p = tid + 256 * i;
             if ((BN * G_KB) % 256 == 0 || p < BN * G_KB) {
                 const int row = p / G_KB, blk = p % G_KB;
-                sw_l[((size_t)buf * G_KB + blk) * BN + row] = rsw[i];
+                sw_l[((size_t)buf * G_KB + blk) * BN + row] = (v2u){(unsigned)rsw[i], 0u};
             }
         }
     }
@@ -343,8 +348,10 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
     extern __shared__ __attribute__((aligned(16))) uint8_t gsm[];
     uint8_t *a_l = gsm;                                   // [G_KB][BM][G_ST]
     uint8_t *b_l = a_l + G_KB * BM * G_ST;                // [G_KB][BN][G_ST]
-    uint16_t *sx_l = (uint16_t *)(b_l + G_KB * BN * G_ST);  // [G_KB][BM]
-    uint16_t *sw_l = sx_l + G_KB * BM;                    // [G_KB][BN]
+    // fp16 scale bits zero-extended to 64 bits: an LDS read is then a
+    // ready f16x4 MFMA operand {scale, 0, 0, 0}
+    v2u *sx_l = (v2u *)(b_l + G_KB * BN * G_ST);  // [G_KB][BM]
+    v2u *sw_l = sx_l + G_KB * BM;                 // [G_KB][BN], pad, zero copy
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
@@ -352,6 +359,10 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int b_begin = blockIdx.z * bps, b_end = min(nb, b_begin + bps);
 
+#pragma unroll
+    for (int i = 0; i < (G_KB * BN + 255) / 256; ++i)  // the zero copy (before the first barrier)
+        if ((G_KB * BN) % 256 == 0 || tid + 256 * i < G_KB * BN)
+            sw_l[C::SW_TWIN + tid + 256 * i] = (v2u){0u, 0u};
     GemmStage<BM, BN, C::A_PT, C::B_PT, C::SX_PT, C::SW_PT> stg;
     float acc[TM][TN][16];
 #pragma unroll
@@ -379,25 +390,26 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
             if (bs + blk >= b_end) break;
             const uint8_t *ab = a_l + ((size_t)buf * G_KB + blk) * BM * G_ST;
             const uint8_t *bb = b_l + ((size_t)buf * G_KB + blk) * BN * G_ST;
-            const uint16_t *sxb = sx_l + ((size_t)buf * G_KB + blk) * BM;
-            const uint16_t *swb = sw_l + ((size_t)buf * G_KB + blk) * BN;
+            const v2u *sxb = sx_l + ((size_t)buf * G_KB + blk) * BM;
+            const v2u *swb = sw_l + ((size_t)buf * G_KB + blk) * BN;
             v4i aop[TM], bop[TN];
             gh4 asc[TM], bsc[TN];
+            // scale-product operands: A carries x.d at k = 0 (lanes 0..31)
+            // and k = 4 (lanes 32..63), B carries w.d at k = 0 and, from the
+            // zero copy, 0 at k = 4, so the product is x.d[row] * w.d[col]
+            // with no per-lane select
+            const v2u *swl = swb + g * C::SW_TWIN;
 #pragma unroll
             for (int a = 0; a < TM; ++a) {
                 const int r = (wm * TM + a) * 32 + j;
                 aop[a] = *(const v4i *)(ab + r * G_ST + g * 16);
-                const _Float16 x = __builtin_bit_cast(_Float16, sxb[r]);
-                asc[a] = (gh4){g == 0 ? x : (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f,
-                               (_Float16)0.0f};
+                asc[a] = __builtin_bit_cast(gh4, sxb[r]);
             }
 #pragma unroll
             for (int b = 0; b < TN; ++b) {
                 const int c = (wn * TN + b) * 32 + j;
                 bop[b] = *(const v4i *)(bb + c * G_ST + g * 16);
-                const _Float16 w = __builtin_bit_cast(_Float16, swb[c]);
-                bsc[b] = (gh4){g == 0 ? w : (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f,
-                               (_Float16)0.0f};
+                bsc[b] = __builtin_bit_cast(gh4, swl[c]);
             }
 #pragma unroll
             for (int a = 0; a < TM; ++a)
