@@ -253,7 +253,10 @@ int si_rope_kv_append(const si_shape_t *s, const float *qkv, int ldqkv, int ntok
 
 size_t si_attention_workspace(const si_shape_t *s, int nq, int max_ctx) {
     if (!s || nq <= 0 || max_ctx <= 0) return 0;
-    return attn_workspace_bytes(s->qheads, s->hdim, s->kvheads, nq, max_ctx);
+    // either schedule: context splits, or the causal prefill's split tiles
+    const size_t a = attn_workspace_bytes(s->qheads, s->hdim, s->kvheads, nq, max_ctx);
+    const size_t p = attn_prefill_workspace_bytes(s->qheads, s->hdim, nq);
+    return a > p ? a : p;
 }
 
 int si_attention(const si_shape_t *s, const float *q, int nq, const uint16_t *kc,
@@ -279,7 +282,7 @@ int si_attention(const si_shape_t *s, const float *q, int nq, const uint16_t *kc
         // causal prefill of one sequence: the flash kernel (query i at
         // cache row ctx0 - 1 + i)
         launch_attn_prefill(q, nq, s->qheads, s->kvheads, s->hdim, ctx0 - 1, kc, vc, attn, qs, d,
-                            bsum, S(stream));
+                            bsum, ws, ws_bytes, S(stream));
     else
         launch_attention(q, nq, s->qheads, s->kvheads, s->hdim, kc, vc, kv_seq_stride, ctx_dev,
                          ctx0, ctx_step, max_ctx, attn, qs, d, bsum, ws, S(stream));
@@ -789,7 +792,8 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
         mark(L, SI_PHASE_ATTENTION_Q8, st);
         if (ctx_dev == nullptr && attn_prefill_supported(s.qheads, s.kvheads, s.hdim))
             launch_attn_prefill(L->q, rows, s.qheads, s.kvheads, s.hdim, pos0, kc, vc, L->attn,
-                                L->attq.qs, L->attq.d, L->attq.s, st);
+                                L->attq.qs, L->attq.d, L->attq.s, L->attn_ws, L->attn_ws_bytes,
+                                st);
         else
             launch_attention(L->q, rows, s.qheads, s.kvheads, s.hdim, kc, vc, kv_seq_stride,
                              ctx_dev, ctx0, ctx_step, max_ctx, L->attn, L->attq.qs, L->attq.d,

@@ -291,6 +291,15 @@ constexpr int PF_T = 32;      // query tokens per workgroup, positions per K/V t
 constexpr int PF_KPAD = 8;    // halves of padding per K row
 constexpr int PF_VPAD = 4;    // halves of padding per V^T row (18-dword rows)
 
+// Causal balance: query tiles qsplit..nqt-1 (nsplit of them) run as two
+// workgroups each, over K/V tiles [0, cap) and [cap, end); their partial
+// states go to ws_* as [token - 32*qsplit][head][2] and k_attn_combine
+// merges them.
+struct PrefillSplit {
+    int nqt, qsplit, nsplit, cap;
+    float *ws_m, *ws_l, *ws_o;
+};
+
 template <int D, int NW>
 struct PrefillLds {
     static constexpr int KROW = D + PF_KPAD, VROW = PF_T + PF_VPAD;
@@ -302,7 +311,7 @@ __global__ void __launch_bounds__(NW * 64) k_attn_prefill(
     const float *__restrict__ q, int ntok, int qheads, int kvheads, int pos0,
     const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, float scale,
     float *__restrict__ attn, int8_t *__restrict__ qs, uint16_t *__restrict__ qd,
-    int16_t *__restrict__ bsum) {
+    int16_t *__restrict__ bsum, PrefillSplit sp) {
     using Lds = PrefillLds<D, NW>;
     constexpr int NT = NW * 64, KS = D / 16, DT = D / 32;
     constexpr int KPIECES = PF_T * D / 8;        // 16-byte K pieces per tile
@@ -312,8 +321,28 @@ __global__ void __launch_bounds__(NW * 64) k_attn_prefill(
     _Float16 *k_l = (_Float16 *)pf_sm;                  // [PF_T][KROW]
     _Float16 *vt_l = k_l + PF_T * Lds::KROW;            // [D][VROW]
 
-    const int nqt = gridDim.x;
-    const int qt = nqt - 1 - (int)blockIdx.x;  // longest tiles first
+    // work unit of this workgroup, longest first: the first K/V halves of
+    // the split query tiles, then their second halves interleaved with the
+    // unsplit tiles (unit -1: whole range, 0: [0, cap), 1: [cap, end))
+    int qt, unit;
+    {
+        const int b = blockIdx.x, S = sp.nsplit, Q0 = sp.qsplit;
+        if (b < S) {
+            qt = sp.nqt - 1 - b;
+            unit = 0;
+        } else {
+            const int bp = b - S, m2 = min(S, Q0);
+            if (bp < 2 * m2) {
+                const int k = bp >> 1;
+                qt = (bp & 1) ? Q0 - 1 - k : sp.nqt - 1 - k;
+                unit = (bp & 1) ? -1 : 1;
+            } else {
+                const int r = m2 + (bp - 2 * m2);
+                qt = S > Q0 ? sp.nqt - 1 - r : Q0 - 1 - r;
+                unit = S > Q0 ? 1 : -1;
+            }
+        }
+    }
     const int g = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int t = lane & 31, hh = lane >> 5;
@@ -324,7 +353,8 @@ __global__ void __launch_bounds__(NW * 64) k_attn_prefill(
     const int ptq = pos0 + tq;     // its position: it sees cache rows 0..ptq
     const int kvd = kvheads * D;
     const int last = min(pos0 + qt * PF_T + PF_T - 1, pos0 + ntok - 1);  // last cache row used
-    const int ntiles = last / PF_T + 1;
+    const int it0 = unit == 1 ? sp.cap : 0;
+    const int it1 = unit == 0 ? sp.cap : last / PF_T + 1;
 
     // Q^T as the B operand of the score MFMA: column tok = t, k-slice hh
     h8 qh[KS], ql[KS];
@@ -401,12 +431,12 @@ __global__ void __launch_bounds__(NW * 64) k_attn_prefill(
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[dt] = (f16v){};
 
-    load_tile(0);
-    for (int it = 0; it < ntiles; ++it) {
+    load_tile(it0 * PF_T);
+    for (int it = it0; it < it1; ++it) {
         const int kv0 = it * PF_T;
         store_tile();
         __syncthreads();
-        if (it + 1 < ntiles) load_tile(kv0 + PF_T);  // next tile in flight
+        if (it + 1 < it1) load_tile(kv0 + PF_T);  // next tile in flight
         if (active) {
             // scores S^T[pos = kv0 + i][tok = t]
             f16v sh = (f16v){}, sl = (f16v){};  // two independent MFMA chains
@@ -427,13 +457,16 @@ __global__ void __launch_bounds__(NW * 64) k_attn_prefill(
                 mx = fmaxf(mx, sv[r]);
             }
             mx = fmaxf(mx, swap32_f(mx));
-            const float mnew = fmaxf(m, mx);  // finite: row 0 is in every token's range
-            const float alpha = __expf(m - mnew);
+            const float mnew = fmaxf(m, mx);
+            // a second K/V half can be entirely past a token's causal limit:
+            // its state stays (-inf, 0, 0) instead of turning NaN
+            const float mref = mnew == -INFINITY ? 0.0f : mnew;
+            const float alpha = __expf(m - mref);
             float ps = 0.0f;
             h8 pbh[2], pbl[2];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float pr = __expf(sv[r] - mnew);
+                const float pr = __expf(sv[r] - mref);
                 ps += pr;
                 _Float16 hi, lo;
                 split_hi_lo(pr, hi, lo);
@@ -466,6 +499,21 @@ __global__ void __launch_bounds__(NW * 64) k_attn_prefill(
 
     if (!active || tq >= ntok) return;
     // lane holds O[tok][32*dt + 8*(r/4) + 4*hh + r%4] in o[dt][r]
+    if (unit >= 0) {  // a half of a split tile: (max, sum, unnormalised O) for the merge
+        const size_t pi = ((size_t)(tq - sp.qsplit * PF_T) * qheads + h) * 2 + unit;
+        if (hh == 0) {
+            sp.ws_m[pi] = m;
+            sp.ws_l[pi] = lsum;
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+                *(float4 *)(sp.ws_o + pi * D + 32 * dt + 8 * r4 + 4 * hh) =
+                    make_float4(o[dt][4 * r4], o[dt][4 * r4 + 1], o[dt][4 * r4 + 2],
+                                o[dt][4 * r4 + 3]);
+        return;
+    }
     const float inv = 1.0f / lsum;
     const size_t rowoff = ((size_t)tq * qheads + h) * D;
 #pragma unroll
@@ -503,17 +551,53 @@ bool attn_prefill_supported(int qheads, int kvheads, int hdim) {
            (hdim == 32 || hdim == 64 || hdim == 96 || hdim == 128);
 }
 
+// Split plan of a causal prefill: when the tiles do not fill the CUs, a
+// query tile whose K/V range exceeds half of the longest one is cut in two
+// (more workgroups, each at most half the longest range).  A grid that
+// already fills the chip is not split: measured at 7B / 2048 tokens (256
+// workgroups), the split ran slower (164 + 19 us merge vs 148 us).
+static PrefillSplit prefill_split(int ntok, int pos0, int kvheads) {
+    PrefillSplit p{};
+    p.nqt = (ntok + PF_T - 1) / PF_T;
+    auto tiles = [&](int qt) { return min(pos0 + qt * PF_T + PF_T - 1, pos0 + ntok - 1) / PF_T + 1; };
+    const int longest = tiles(p.nqt - 1);
+    p.cap = (longest + 1) / 2;
+    p.qsplit = p.nqt;
+    if (longest >= 4 && p.nqt * kvheads < 256)  // short ranges or a full grid: unsplit
+        while (p.qsplit > 0 && tiles(p.qsplit - 1) > p.cap) --p.qsplit;
+    p.nsplit = p.nqt - p.qsplit;
+    return p;
+}
+
+size_t attn_prefill_workspace_bytes(int qheads, int hdim, int ntok) {
+    return (size_t)ntok * qheads * 2 * (hdim + 2) * sizeof(float);
+}
+
 void launch_attn_prefill(const float *q, int ntok, int qheads, int kvheads, int hdim, int pos0,
                          const uint16_t *kc, const uint16_t *vc, float *attn, int8_t *qs,
-                         uint16_t *qd, int16_t *bsum, hipStream_t st) {
+                         uint16_t *qd, int16_t *bsum, void *workspace, size_t ws_bytes,
+                         hipStream_t st) {
     if (ntok <= 0) return;
     const int per = qheads / kvheads;
-    const dim3 grid((ntok + PF_T - 1) / PF_T, kvheads);
+    PrefillSplit sp = prefill_split(ntok, pos0, kvheads);
+    const int rows_split = ntok - sp.qsplit * PF_T;
+    if (sp.nsplit > 0 &&
+        (!workspace || ws_bytes < attn_prefill_workspace_bytes(qheads, hdim, rows_split))) {
+        sp.qsplit = sp.nqt;  // no room for the partial states: unsplit
+        sp.nsplit = 0;
+    }
+    if (sp.nsplit > 0) {
+        const size_t np = (size_t)rows_split * qheads * 2;
+        sp.ws_m = (float *)workspace;
+        sp.ws_l = sp.ws_m + np;
+        sp.ws_o = sp.ws_l + np;
+    }
+    const dim3 grid(2 * sp.nsplit + sp.qsplit, kvheads);
     const float scale = 1.0f / sqrtf((float)hdim);  // attention_kernels.h:86
 #define PF_CALL(DIM, NW)                                                                      \
     hipLaunchKernelGGL((k_attn_prefill<DIM, NW>), grid, dim3(NW * 64),                        \
                        (PrefillLds<DIM, NW>::bytes()), st, q, ntok, qheads, kvheads, pos0, kc, \
-                       vc, scale, attn, qs, qd, bsum)
+                       vc, scale, attn, qs, qd, bsum, sp)
 #define PF_DIM(DIM)                     \
     if (per <= 8)                       \
         PF_CALL(DIM, 8);                \
@@ -527,6 +611,13 @@ void launch_attn_prefill(const float *q, int ntok, int qheads, int kvheads, int 
     }
 #undef PF_DIM
 #undef PF_CALL
+    if (sp.nsplit > 0) {
+        const size_t t0 = (size_t)sp.qsplit * PF_T, qd_ = (size_t)qheads * hdim;
+        hipLaunchKernelGGL(k_attn_combine, dim3(qheads, rows_split), dim3(hdim), 0, st, qheads,
+                           hdim, 2, sp.ws_m, sp.ws_l, sp.ws_o, attn + t0 * qd_,
+                           qs ? qs + t0 * qd_ : nullptr, qs ? qd + t0 * qd_ / SI_QK : nullptr,
+                           bsum ? bsum + t0 * qd_ / SI_QK : nullptr);
+    }
 }
 
 // Context chunks per (query, KV group): enough workgroups to cover the chip

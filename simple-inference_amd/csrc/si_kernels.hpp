@@ -47,9 +47,11 @@ void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
                       int8_t *qs, uint16_t *d, int16_t *bsum, void *workspace,
                       hipStream_t st);
 bool attn_prefill_supported(int qheads, int kvheads, int hdim);
+size_t attn_prefill_workspace_bytes(int qheads, int hdim, int ntok);
 void launch_attn_prefill(const float *q, int ntok, int qheads, int kvheads, int hdim, int pos0,
                          const uint16_t *kc, const uint16_t *vc, float *attn, int8_t *qs,
-                         uint16_t *qd, int16_t *bsum, hipStream_t st);
+                         uint16_t *qd, int16_t *bsum, void *workspace, size_t ws_bytes,
+                         hipStream_t st);
 }  // namespace si
 namespace si {
 // fused decode kernels (si_decode.hip)
