@@ -717,7 +717,7 @@ static int run_decode(si_layer *L, const float *x, uint16_t *kc, uint16_t *vc, i
                    L->xq.qs, L->xq.d, L->xq.s, L->qkv, exact, st);
     // :260-270: RoPE, fp16 K/V append at context-1, attention over the cache
     mark(L, SI_PHASE_ATTENTION_Q8, st);
-    const int ns = dec_attn_chunks(s.kvheads, 1, ctx);
+    const int ns = dec_attn_chunks(s.qheads, s.kvheads, s.hdim, 1, ctx);
     launch_dec_attn(L->qkv, NQKV, 1, s.qheads, s.kvheads, s.hdim, L->rope_cos, L->rope_sin, kc,
                     vc, 0, nullptr, ctx, ctx, L->q, ns, L->attn_ws, nullptr, nullptr, nullptr,
                     nullptr, st);
@@ -771,7 +771,7 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
     if (ctx_step == 0) {
         // batched decode: RoPE + K/V append inside the attention kernel
         mark(L, SI_PHASE_ATTENTION_Q8, st);
-        const int ns = dec_attn_chunks(s.kvheads, rows, max_ctx);
+        const int ns = dec_attn_chunks(s.qheads, s.kvheads, s.hdim, rows, max_ctx);
         if (ns == 1) {
             launch_dec_attn(L->qkv, NQKV, rows, s.qheads, s.kvheads, s.hdim, L->rope_cos,
                             L->rope_sin, kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx, L->q, 1,

@@ -70,9 +70,12 @@ __global__ void k_attn_combine(int qheads, int hdim, int nsplit, const float *__
                                uint16_t *__restrict__ d, int16_t *__restrict__ bsum) {
     const int h = blockIdx.x, qi = blockIdx.y, jj = threadIdx.x;
     const size_t base = ((size_t)qi * qheads + h) * nsplit;
+    // unrolled: the loads of 8 splits are in flight together
     float mx = -INFINITY;
+#pragma unroll 8
     for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, ws_m[base + s]);
     float l = 0.0f, acc = 0.0f;
+#pragma unroll 8
     for (int s = 0; s < nsplit; ++s) {
         const float w = expf(ws_m[base + s] - mx);  // empty chunk: m = -inf -> 0
         l = fmaf(ws_l[base + s], w, l);

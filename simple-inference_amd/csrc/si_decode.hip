@@ -624,14 +624,20 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // A = V^T[d = 16*dt + col][pos = 4*grp + r]
-        const _Float16 *vcol = vw + (4 * grp) * VROW + col;
+        // A = V^T[d = 16*dt + col][pos = 4*grp + r], gathered by the
+        // transposing read: lane (col, grp) points at V row 4*grp + col/4,
+        // dims 16*dt + 4*(col%4) .. +3
+        const _Float16 *vsrc = vw + (4 * grp + (col >> 2)) * VROW + 4 * (col & 3);
+        // rescale only when some column's running max moved (alpha == 1
+        // exactly otherwise: exp of 0), a wavefront-uniform branch
+        if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+        }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-            h4 va;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) va[r] = vcol[r * VROW + 16 * dt];
-            f4 acc = o[dt] * alpha;
+            const h4 va = __builtin_bit_cast(h4, lds_read_tr16(vsrc + 16 * dt));
+            f4 acc = o[dt];
             acc = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ph, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pl, acc, 0, 0, 0);
             o[dt] = acc;
@@ -643,12 +649,14 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
     };
     // tiles t0, t0 + STEP, ... rotate through the DA_DEPTH register sets;
     // each set is refilled DA_DEPTH tiles ahead once consumed (past the
-    // chunk: clamped, unused)
+    // chunk: clamped, unused).  Every set of a round is consumed, also when
+    // its tile lies past the chunk (all scores masked: the state is
+    // unchanged): a conditional exit between the sets makes the compiler
+    // wait for every load in flight at the loop head.
     for (; t0 < p1; t0 += DA_DEPTH * STEP) {
 #pragma unroll
         for (int b = 0; b < DA_DEPTH; ++b) {
             const int tb = t0 + b * STEP;
-            if (tb >= p1) break;
             tile(tb, kr[b], vr[b]);
             load_k(tb + DA_DEPTH * STEP, kr[b]);
             load_v(tb + DA_DEPTH * STEP, vr[b]);
@@ -741,6 +749,399 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
     }
 }
 
+// ===========================================================================
+// Decode attention over whole cache rows (kvheads <= 4).
+//
+// One workgroup of 4 wavefronts owns (query, context chunk) and every KV
+// group: wavefront w serves group w % G over every (4/G)-th 16-position tile
+// of the chunk.  Per step the workgroup stages 16*(4/G) whole cache rows
+// (every group, K and V) in LDS with row-contiguous loads, then each
+// wavefront runs k_dec_attn's MFMA scores, online softmax and PV on its
+// group's columns (V^T operands by the transposing LDS read).  Reading
+// whole rows is the point: one group's 2*hdim-byte slice of each row
+// streams at ~4.0 TB/s, whole rows at ~6.4 TB/s (7B, 64 x 4096 cache,
+// measured).  The new token's K/V row is substituted in LDS.
+// ===========================================================================
+template <int D, int G>
+struct RowsLds {
+    static constexpr int NWG = 4 / G;            // wavefronts per group
+    static constexpr int ROWS = DA_TILE * NWG;  // positions per step
+    static constexpr int RW = G * D + 8;        // halves per LDS row (padded)
+    static constexpr size_t tile_bytes = (size_t)2 * ROWS * RW * 2;  // K and V
+    static constexpr size_t raw_bytes(int per) {
+        return (size_t)(G * per * D + 2 * G * D + D) * 4;
+    }
+    static constexpr size_t merge_bytes(int per) {  // NWG states per group + factors
+        return (size_t)G * (NWG * per * (D + 2) + per * (NWG + 2)) * 4;
+    }
+    static constexpr size_t bytes(int per) {
+        size_t m = tile_bytes;
+        if (raw_bytes(per) > m) m = raw_bytes(per);
+        if (merge_bytes(per) > m) m = merge_bytes(per);
+        return (size_t)2 * G * D * 2 + m;  // new K|V row (fp16) + the shared region
+    }
+};
+
+template <int D, int G, bool FINAL>
+__global__ void __launch_bounds__(256) k_dec_attn_rows(
+    const float *__restrict__ qkv, int ldqkv, int qheads, const float *__restrict__ rc,
+    const float *__restrict__ rs, uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
+    size_t kv_seq_stride, const int *__restrict__ ctx_dev, int ctx0, int max_ctx, int chunk,
+    float scale, float *__restrict__ q_cap, float *__restrict__ ws_m, float *__restrict__ ws_l,
+    float *__restrict__ ws_o, float *__restrict__ attn, int8_t *__restrict__ aqs,
+    uint16_t *__restrict__ ad, int16_t *__restrict__ as) {
+    using L = RowsLds<D, G>;
+    constexpr int KS = D / 32, DT = D / 16, HALF = D / 2, NWG = L::NWG, ROWS = L::ROWS;
+    constexpr int RW = L::RW, KVD = G * D;
+    constexpr int RP = KVD / 8;                     // 16-byte pieces per row
+    constexpr int PT = ROWS * RP / 256;             // pieces per thread per step (K; same for V)
+    static_assert(ROWS * RP % 256 == 0, "whole pieces per thread");
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    uint16_t *newk = (uint16_t *)smem;  // [G*D] fp16 K row of the new token (RoPE'd)
+    uint16_t *newv = newk + KVD;        // [G*D] its V row
+    char *big = smem + 2 * KVD * 2;
+    _Float16 *kt = (_Float16 *)big;     // [ROWS][RW]
+    _Float16 *vt = kt + ROWS * RW;      // [ROWS][RW]
+
+    const int sp = blockIdx.x, qi = blockIdx.y, ns = gridDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int g = wave % G, wj = wave / G;  // group, tile slot within the step
+    const int per = qheads / G;
+    const int qd = qheads * D;
+    int ctx = ctx_dev ? ctx_dev[qi] : ctx0;
+    ctx = min(ctx, max_ctx);
+    const int pnew = ctx - 1;  // < 0: empty context (device-supplied only)
+    const int p0 = sp * chunk;
+    const int p1 = min(ctx, p0 + chunk);
+    // rows the loads may touch: known at launch, so the first loads need not
+    // wait for ctx_dev (the cache holds max_ctx rows per sequence)
+    const int pmax = min(max_ctx, p0 + chunk);
+    const bool owner = pnew >= p0 && pnew < p1;
+    const float *row = qkv + (size_t)qi * ldqkv;
+    const float *cr = rc + (size_t)max(pnew, 0) * HALF;
+    const float *sr = rs + (size_t)max(pnew, 0) * HALF;
+    const size_t sbase = (size_t)qi * kv_seq_stride;
+    const uint16_t *kbase = kc + sbase, *vbase = vc + sbase;
+
+    // 1. the fused q|k|v row (q of every head, then the new token's raw K
+    //    and V rows) and the RoPE cos|sin row at its position, as float4
+    //    pieces with clamped indices (no branches)
+    float *qraw = (float *)big;        // [G*per][D]
+    float *kraw = qraw + G * per * D;  // [G][D]
+    float *vraw = kraw + KVD;          // [G][D]
+    float *csr = vraw + KVD;           // [HALF] cos, [HALF] sin
+    const int nrow4 = (qd + 2 * KVD) / 4;
+    constexpr int ROW4PT = ((16 + 2) * G * D / 4 + 255) / 256;  // per <= 16
+    float4 rv[ROW4PT];
+#pragma unroll
+    for (int u = 0; u < ROW4PT; ++u)
+        rv[u] = ((const float4 *)row)[min(tid + u * 256, nrow4 - 1)];
+    float4 csv;
+    {
+        const int t = min(tid, D / 4 - 1);
+        const float4 *cp = t < HALF / 4 ? (const float4 *)cr + t : (const float4 *)sr + (t - HALF / 4);
+        csv = *cp;
+    }
+    // 2. the first two steps' whole rows (positions clamped into the chunk,
+    //    or row 0 for an empty context; such rows are masked out of the
+    //    scores): two register buffers keep two steps of loads in flight
+    uint4 ak[PT], av[PT], bk[PT], bv[PT];
+    auto load_step = [&](uint4 (&rk)[PT], uint4 (&rvv)[PT], int ps) {
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            const int c = (wave * PT + i) * 64 + lane;  // a wavefront's pieces are contiguous
+            const int r = c / RP, e = (c % RP) * 8;
+            const size_t pos = (size_t)max(min(ps + r, pmax - 1), 0);
+            rk[i] = *(const uint4 *)(kbase + pos * KVD + e);
+            rvv[i] = *(const uint4 *)(vbase + pos * KVD + e);
+        }
+    };
+    load_step(ak, av, p0);
+    // issue order A then B, as in the loop (interleaved loads here would make
+    // the compiler's wait counts for the loop conservative)
+    __builtin_amdgcn_sched_barrier(0);
+    load_step(bk, bv, p0 + ROWS);
+    // unconditional stores at the clamped index (duplicates write equal
+    // values): a guarded store lets the compiler sink its load behind the
+    // K/V loads above and wait for all of them
+#pragma unroll
+    for (int u = 0; u < ROW4PT; ++u) ((float4 *)qraw)[min(tid + u * 256, nrow4 - 1)] = rv[u];
+    ((float4 *)csr)[min(tid, D / 4 - 1)] = csv;
+    __syncthreads();
+    // rotate-half RoPE (qwen_one_layer.c:172-183) of element dd of a head row
+    auto rot = [&](const float *v, int dd) {
+        const int i = dd < HALF ? dd : dd - HALF;
+        const float a = v[i], b = v[i + HALF], c = csr[i], s = csr[HALF + i];
+        return dd < HALF ? __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s))
+                         : __fadd_rn(__fmul_rn(b, c), __fmul_rn(a, s));
+    };
+    // the new token's K (rotated) and V rows in fp16, for every group (a
+    // constant trip count: a loop with stores and no loads makes the
+    // compiler drain every load in flight before it)
+#pragma unroll
+    for (int u = 0; u < (KVD + 255) / 256; ++u) {
+        const int i = tid + 256 * u;
+        if (i >= KVD) break;
+        const uint16_t kh = f2h(rot(kraw + (i / D) * D, i % D));
+        const uint16_t vh = f2h(vraw[i]);
+        newk[i] = kh;
+        newv[i] = vh;
+        if (owner) {
+            kc[sbase + (size_t)pnew * KVD + i] = kh;
+            vc[sbase + (size_t)pnew * KVD + i] = vh;
+        }
+    }
+    // Q^T of this wavefront's group as the B operand: lane holds
+    // Q[head col][d = 32*ks + 8*grp + e]
+    h8 qh[KS], ql[KS];
+    {
+        const bool hv = col < per && pnew >= 0;
+        const int hc = col < per ? col : 0;
+        const bool capq = q_cap && sp == 0 && wj == 0 && hv;
+        const float *qh_row = qraw + (size_t)(g * per + hc) * D;
+        auto ld8 = [](const float *p, float (&v)[8]) {
+            const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        };
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int d0 = 32 * ks + 8 * grp;
+            const int i0 = d0 < HALF ? d0 : d0 - HALF;
+            float a[8], b[8], c[8], sn[8], v[8];
+            ld8(qh_row + i0, a);
+            ld8(qh_row + i0 + HALF, b);
+            ld8(csr + i0, c);
+            ld8(csr + HALF + i0, sn);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                v[e] = !hv ? 0.0f
+                           : (d0 < HALF ? __fsub_rn(__fmul_rn(a[e], c[e]), __fmul_rn(b[e], sn[e]))
+                                        : __fadd_rn(__fmul_rn(b[e], c[e]), __fmul_rn(a[e], sn[e])));
+                _Float16 hi, lo;
+                hi_lo(v[e], hi, lo);
+                qh[ks][e] = hi;
+                ql[ks][e] = lo;
+            }
+            if (capq) {
+                float *qc = q_cap + (size_t)qi * qd + (size_t)(g * per + hc) * D + d0;
+                *(float4 *)qc = make_float4(v[0], v[1], v[2], v[3]);
+                *(float4 *)(qc + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            }
+        }
+    }
+    __syncthreads();  // newk/newv visible; the raw rows are no longer read
+
+    float m = -INFINITY, lsum = 0.0f;
+    f4 o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = (f4){0.f, 0.f, 0.f, 0.f};
+    const int nsteps = (p1 - p0 + ROWS - 1) / ROWS;  // 0 for an empty chunk
+    auto step = [&](uint4 (&rk)[PT], uint4 (&rvv)[PT], int st) {
+        const int ps = p0 + st * ROWS;
+        const bool tail = ps + ROWS > p1;  // workgroup-uniform
+        // stage the step's rows; V rows past the context as zeros (their
+        // scores are masked); the new token's row from LDS, since its cache
+        // row may not be written yet
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            const int c = (wave * PT + i) * 64 + lane;
+            const int r = c / RP, e = (c % RP) * 8;
+            uint4 kv = rk[i], vv = rvv[i];
+            if (tail) {  // rows past the context may hold any bits (NaN * 0 = NaN)
+                const bool live = ps + r < p1;
+                vv.x = live ? vv.x : 0u; vv.y = live ? vv.y : 0u;
+                vv.z = live ? vv.z : 0u; vv.w = live ? vv.w : 0u;
+            }
+            if (owner) {  // workgroup-uniform
+                const bool isnew = ps + r == pnew;
+                const uint4 nk = *(const uint4 *)(newk + e), nv = *(const uint4 *)(newv + e);
+                // per component: a select of whole uint4 values becomes a
+                // select of stack addresses (scratch traffic)
+                kv.x = isnew ? nk.x : kv.x; kv.y = isnew ? nk.y : kv.y;
+                kv.z = isnew ? nk.z : kv.z; kv.w = isnew ? nk.w : kv.w;
+                vv.x = isnew ? nv.x : vv.x; vv.y = isnew ? nv.y : vv.y;
+                vv.z = isnew ? nv.z : vv.z; vv.w = isnew ? nv.w : vv.w;
+            }
+            *(uint4 *)(kt + r * RW + e) = kv;
+            *(uint4 *)(vt + r * RW + e) = vv;
+        }
+        __syncthreads();
+        // the step after next, unconditionally: clamped positions stay in
+        // the chunk, and a branch here would make the compiler wait for both
+        // buffers at every step
+        load_step(rk, rvv, ps + 2 * ROWS);
+        // this wavefront's tile: rows 16*wj .. +15 of the step, group g
+        const int t0 = ps + DA_TILE * wj;
+        h8 ka[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            ka[ks] = *(const h8 *)(kt + (DA_TILE * wj + col) * RW + g * D + 32 * ks + 8 * grp);
+        f4 sacc = (f4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[ks], qh[ks], sacc, 0, 0, 0);
+            sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[ks], ql[ks], sacc, 0, 0, 0);
+        }
+        // lane holds S^T[pos = t0 + 4*grp + r][head col]
+        float s[4], mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            s[r] = (t0 + 4 * grp + r < p1) ? sacc[r] * scale : -INFINITY;
+            mx = fmaxf(mx, s[r]);
+        }
+        mx = fmaxf(mx, swap16_f(mx));
+        mx = fmaxf(mx, swap32_f(mx));
+        const float mnew = fmaxf(m, mx);
+        // a tile past the chunk end leaves the state as it is (no NaN)
+        const float mref = mnew == -INFINITY ? 0.0f : mnew;
+        const float alpha = __expf(m - mref);
+        float p[4], ps_ = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            p[r] = __expf(s[r] - mref);
+            ps_ += p[r];
+        }
+        ps_ += swap16_f(ps_);
+        ps_ += swap32_f(ps_);
+        lsum = lsum * alpha + ps_;
+        m = mnew;
+        h4 ph, pl;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            _Float16 hi, lo;
+            hi_lo(p[r], hi, lo);
+            ph[r] = hi;
+            pl[r] = lo;
+        }
+        // A = V^T[d = g*D + 16*dt + col][pos = 4*grp + r] by the transposing
+        // read: lane (col, grp) points at row 16*wj + 4*grp + col/4
+        const _Float16 *vsrc = vt + (DA_TILE * wj + 4 * grp + (col >> 2)) * RW + g * D + 4 * (col & 3);
+        // rescale only when some column's running max moved (alpha == 1
+        // exactly otherwise: exp of 0), a wavefront-uniform branch
+        if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const h4 va = __builtin_bit_cast(h4, lds_read_tr16(vsrc + 16 * dt));
+            f4 acc = o[dt];
+            acc = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ph, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pl, acc, 0, 0, 0);
+            o[dt] = acc;
+        }
+        __syncthreads();  // the step's rows are rewritten next
+    };
+    // steps in pairs (workgroup-uniform); the second step of the last pair
+    // of an odd count lies past the chunk, is masked out entirely and
+    // leaves the softmax state as it is
+    for (int st = 0; st < nsteps; st += 2) {
+        step(ak, av, st);
+        step(bk, bv, st + 1);
+    }
+
+    if constexpr (NWG == 1 && !FINAL) {
+        // one wavefront per group: its state is the chunk's partial, written
+        // from registers (lane (col, grp) holds O^T[16*dt + 4*grp + r][col])
+        if (col < per) {
+            const size_t pi = ((size_t)qi * qheads + g * per + col) * ns + sp;
+            if (grp == 0) {
+                ws_m[pi] = m;
+                ws_l[pi] = lsum;
+            }
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+                *(float4 *)(ws_o + pi * D + 16 * dt + 4 * grp) =
+                    make_float4(o[dt][0], o[dt][1], o[dt][2], o[dt][3]);
+        }
+        return;
+    }
+    // merge the NWG wavefront states of each group in LDS (reusing the rows)
+    float *mm = (float *)big;                   // [G][NWG][per]
+    float *ml = mm + G * NWG * per;             // [G][NWG][per]
+    float *mo = ml + G * NWG * per;             // [G][NWG][per][D]
+    float *sc = mo + (size_t)G * NWG * per * D;  // [G][per][NWG]
+    float *ltot = sc + G * per * NWG;           // [G][per]
+    float *mtot = ltot + G * per;               // [G][per]
+    if (col < per) {
+        const int si = (g * NWG + wj) * per + col;
+        if (grp == 0) {
+            mm[si] = m;
+            ml[si] = lsum;
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mo[(size_t)si * D + 16 * dt + 4 * grp + r] = o[dt][r];
+    }
+    __syncthreads();
+    if (tid < G * per) {
+        const int gg = tid / per, hc = tid % per;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NWG; ++w) M = fmaxf(M, mm[(gg * NWG + w) * per + hc]);
+        float l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NWG; ++w) {
+            const float f = M == -INFINITY ? 0.0f : expf(mm[(gg * NWG + w) * per + hc] - M);
+            sc[tid * NWG + w] = f;
+            l = fmaf(ml[(gg * NWG + w) * per + hc], f, l);
+        }
+        ltot[tid] = l;
+        mtot[tid] = M;
+    }
+    __syncthreads();
+    // 4 consecutive elements per thread; 8 lanes = 32 elements = one Q8_0
+    // block of one head (D is a multiple of 32); heads in global order
+    const int nel4 = qd / 4;
+    for (int e40 = 0; e40 < nel4; e40 += 256) {
+        const int e4 = e40 + tid;
+        const bool ok = e4 < nel4;
+        const int ec = 4 * min(e4, nel4 - 1);
+        const int h = ec / D, dd = ec - h * D;  // h = gg * per + hc
+        const int gg = h / per, hc = h - gg * per;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int w = 0; w < NWG; ++w) {
+            const float4 ov = *(const float4 *)(mo + ((size_t)(gg * NWG + w) * per + hc) * D + dd);
+            const float f = sc[h * NWG + w];
+            acc[0] = fmaf(ov.x, f, acc[0]);
+            acc[1] = fmaf(ov.y, f, acc[1]);
+            acc[2] = fmaf(ov.z, f, acc[2]);
+            acc[3] = fmaf(ov.w, f, acc[3]);
+        }
+        if (!FINAL) {
+            if (ok) {
+                const size_t pi = ((size_t)qi * qheads + h) * ns + sp;
+                if (dd == 0) {
+                    ws_m[pi] = mtot[h];
+                    ws_l[pi] = ltot[h];
+                }
+                *(float4 *)(ws_o + pi * D + dd) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+            }
+        } else if (e40 + (tid & ~7) < nel4) {
+            // normalise (attention_kernels.h:163; no context: 0, :95-98) and
+            // quantize_q8
+            const float r = mtot[h] == -INFINITY ? 0.0f : 1.0f / ltot[h];
+            const float y[4] = {acc[0] * r, acc[1] * r, acc[2] * r, acc[3] * r};
+            uint16_t dbits;
+            int bsum;
+            const uint32_t q = quant_block_oct(y, dbits, bsum);
+            if (ok) {
+                const size_t off = (size_t)qi * qd + (size_t)h * D + dd;
+                *(float4 *)(attn + off) = make_float4(y[0], y[1], y[2], y[3]);
+                *(uint32_t *)(aqs + off) = q;
+                if ((e4 & 7) == 0) {
+                    ad[off / SI_QK] = dbits;
+                    if (as) as[off / SI_QK] = (int16_t)bsum;
+                }
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // launch policy
 // ---------------------------------------------------------------------------
@@ -807,7 +1208,40 @@ void launch_dec_gateup(const float *h, const float *gain, int hidden, float eps,
 // than ~1024 workgroups in total.
 constexpr int DA_NW = 8;
 
-int dec_attn_chunks(int kvheads, int nq, int max_ctx) {
+// The whole-row kernel serves batches (>= 8 queries: one query is latency
+// bound and k_dec_attn's shorter chain wins) of 1, 2 or 4 KV groups of up to
+// 16 query heads.
+static bool dec_rows_ok(int qheads, int kvheads, int hdim, int nq) {
+    if (nq < 8 || !(kvheads == 1 || kvheads == 2 || kvheads == 4)) return false;
+    if (qheads % kvheads || qheads / kvheads > 16) return false;
+    const int per = qheads / kvheads;
+    size_t b = 0;
+#define RB(DIM)                                                             \
+    b = kvheads == 1 ? RowsLds<DIM, 1>::bytes(per)                          \
+                     : kvheads == 2 ? RowsLds<DIM, 2>::bytes(per) : RowsLds<DIM, 4>::bytes(per)
+    switch (hdim) {
+        case 32: RB(32); break;
+        case 64: RB(64); break;
+        case 96: RB(96); break;
+        case 128: RB(128); break;
+        default: return false;
+    }
+#undef RB
+    return b <= 65536;
+}
+
+int dec_attn_chunks(int qheads, int kvheads, int hdim, int nq, int max_ctx) {
+    if (dec_rows_ok(qheads, kvheads, hdim, nq)) {
+        // >= 4 steps of 16*(4/kvheads) positions per chunk (fewer partials
+        // for the consumer to merge), <= ~512 workgroups (2 per CU), <= 32
+        // chunks
+        const int rows = DA_TILE * (4 / kvheads);
+        int ns = (max_ctx + 4 * rows - 1) / (4 * rows);
+        const int cap = (512 + nq - 1) / nq;
+        if (ns > cap) ns = cap;
+        if (ns > 32) ns = 32;
+        return ns < 1 ? 1 : ns;
+    }
     const int tiles = (max_ctx + DA_TILE - 1) / DA_TILE;
     int ns = (tiles + 2 * DA_NW - 1) / (2 * DA_NW);
     // enough workgroups to cover the CUs once; a context split beyond that
@@ -818,7 +1252,7 @@ int dec_attn_chunks(int kvheads, int nq, int max_ctx) {
 }
 
 size_t dec_attn_workspace_bytes(int qheads, int hdim, int kvheads, int nq, int max_ctx) {
-    const int ns = dec_attn_chunks(kvheads, nq, max_ctx);
+    const int ns = dec_attn_chunks(qheads, kvheads, hdim, nq, max_ctx);
     return (size_t)nq * qheads * ns * (hdim + 2) * sizeof(float);
 }
 
@@ -835,8 +1269,32 @@ void launch_dec_attn(const float *qkv, int ldqkv, int nq, int qheads, int kvhead
     float *ws_o = ws_l + (size_t)nq * qheads * ns;
     const float scale = 1.0f / sqrtf((float)hdim);  // attention_kernels.h:86
     const int per = qheads / kvheads;
-    const dim3 grid(ns, kvheads, nq);
     const bool fin = attn != nullptr;
+    if (dec_rows_ok(qheads, kvheads, hdim, nq)) {
+#define RCALL(DIM, GG, FIN)                                                                       \
+    hipLaunchKernelGGL((k_dec_attn_rows<DIM, GG, FIN>), dim3(ns, nq), dim3(256),                \
+                       (RowsLds<DIM, GG>::bytes(per)), st, qkv, ldqkv, qheads, rc, rs, kc, vc,   \
+                       kv_seq_stride, ctx_dev, ctx0, max_ctx, chunk, scale, q_cap, ws_m, ws_l,    \
+                       ws_o, attn, aqs, ad, as)
+#define RCALLG(DIM)                                                \
+    if (kvheads == 1) {                                            \
+        if (fin) RCALL(DIM, 1, true); else RCALL(DIM, 1, false);   \
+    } else if (kvheads == 2) {                                     \
+        if (fin) RCALL(DIM, 2, true); else RCALL(DIM, 2, false);   \
+    } else {                                                       \
+        if (fin) RCALL(DIM, 4, true); else RCALL(DIM, 4, false);   \
+    }
+        switch (hdim) {
+            case 32: RCALLG(32); break;
+            case 64: RCALLG(64); break;
+            case 96: RCALLG(96); break;
+            default: RCALLG(128); break;
+        }
+#undef RCALLG
+#undef RCALL
+        return;
+    }
+    const dim3 grid(ns, kvheads, nq);
 #define CALL(DIM, NW, FIN)                                                                     \
     hipLaunchKernelGGL((k_dec_attn<DIM, NW, FIN>), grid, dim3(NW * 64),                        \
                        (AttnLds<DIM, NW>::bytes(per)), st, qkv, ldqkv, qheads, kvheads, rc, rs,  \

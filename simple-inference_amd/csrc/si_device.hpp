@@ -95,6 +95,20 @@ __device__ __forceinline__ int swap32_i(int v) {
 __device__ __forceinline__ float swap16_f(float v) { return __int_as_float(swap16_i(__float_as_int(v))); }
 __device__ __forceinline__ float swap32_f(float v) { return __int_as_float(swap32_i(__float_as_int(v))); }
 
+// gfx950 transposing LDS read (ds_read_b64_tr_b16).  Within each group of
+// 16 lanes, lane i receives as element e (0..3) the 16-bit value i % 4 of
+// the 8 bytes read at the address of lane 4*e + i/4 of its group (lane
+// layout measured on the device).  So if lane s of a group points at
+// row[r0 + s/4][c0 + 4*(s%4)] of a row-major fp16 matrix, lane i receives
+// column c0 + i of rows r0..r0+3: the A/B operand of a 16x16x16 f16 MFMA
+// whose reduction runs down the rows.  p must be 8-byte aligned.
+typedef short tr_s4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ tr_s4 lds_read_tr16(const void *p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) tr_s4 *)(__attribute__((address_space(3))) void *)
+            const_cast<void *>(p));
+}
+
 // Reductions over groups of 8 lanes (i & ~7), 32 lanes and the wavefront;
 // every lane of the group gets the result.
 __device__ __forceinline__ float oct_max(float v) {

@@ -68,7 +68,7 @@ void launch_dec_gateup(const float *h, const float *gain, int hidden, float eps,
                        float *cap_normed,
                        int8_t *cap_qs, uint16_t *cap_d, int16_t *cap_s, float *gu, float *act,
                        int8_t *aqs, uint16_t *ad, int16_t *as, bool exact, hipStream_t st);
-int dec_attn_chunks(int kvheads, int nq, int max_ctx);
+int dec_attn_chunks(int qheads, int kvheads, int hdim, int nq, int max_ctx);
 size_t dec_attn_workspace_bytes(int qheads, int hdim, int kvheads, int nq, int max_ctx);
 void launch_dec_attn(const float *qkv, int ldqkv, int nq, int qheads, int kvheads, int hdim,
                      const float *rc, const float *rs, uint16_t *kc, uint16_t *vc,

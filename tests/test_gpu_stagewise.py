@@ -168,3 +168,69 @@ def test_batched_decode_stagewise_7b():
                np.arange(nseq) * stride, host(out).reshape(nseq, s.hidden))
     L.close()
 
+
+
+# Batched decode over ragged per-sequence contexts (ctx_dev), for every KV
+# group count and head size the whole-row batched decode attention kernel
+# serves (1, 2 or 4 groups; hdim 32..128; up to 16 query heads per group).
+# Contexts fall on both sides of the 16-position tiles, the per-step rows and
+# the context chunks, and include a context of 1.
+_RAGGED = {
+    "g1_d32": dict(hidden=256, qheads=8, kvheads=1, hdim=32, ffn=0),
+    "0.5b": si_amd.SHAPES["0.5b"],
+    "1.5b_ref": si_amd.SHAPES["1.5b_ref"],
+    "g4_d96": dict(hidden=768, qheads=8, kvheads=4, hdim=96, ffn=0),
+    "g1_d128_16heads": dict(hidden=2048, qheads=16, kvheads=1, hdim=128, ffn=0),
+    "7b": si_amd.SHAPES["7b"],
+}
+
+
+_CTXS = {  # max_ctx -> contexts; 60 leaves one chunk (normalised in-kernel)
+    333: [1, 2, 15, 16, 17, 63, 64, 65, 128, 129, 200, 331, 332, 333],
+    60: [1, 2, 15, 16, 17, 31, 32, 33, 47, 48, 49, 58, 59, 60],
+}
+
+
+@pytest.mark.parametrize("max_ctx", list(_CTXS))
+@pytest.mark.parametrize("name", list(_RAGGED))
+def test_batched_decode_ragged_attention(name, max_ctx):
+    from oracle.oracle_py import Oracle
+    oracle = Oracle()
+    torch = _torch()
+    sd = _RAGGED[name]
+    s, os_ = si_amd.make_shape(**sd), or_shape(**sd)
+    lay = make_layer(oracle, os_, 31, ffn=s.ffn > 0)
+    ctxs = np.array(_CTXS[max_ctx], np.int32)
+    nseq = ctxs.size
+    D, QD, KVD = s.hdim, s.qheads * s.hdim, s.kvheads * s.hdim
+    stride = max_ctx * KVD
+    rng = np.random.default_rng(32)
+    x = rng.standard_normal((nseq, s.hidden)).astype(np.float32)
+    kc0 = kv_history(oracle, rng, nseq * max_ctx, KVD)
+    vc0 = kv_history(oracle, rng, nseq * max_ctx, KVD)
+    L = si_amd.Layer(s, lay, nseq, max_ctx)
+    kc, vc = dev(kc0.view(np.int16)), dev(vc0.view(np.int16))
+    out = empty(nseq * s.hidden, torch.float32)
+    flags = si_amd.SI_LAYER_FULL if s.ffn > 0 else si_amd.SI_LAYER_ATTN_ONLY
+    L.decode_batch(dev(x), nseq, kc, vc, stride, 0, max_ctx, out, ctx_dev=dev(ctxs), flags=flags)
+    kh, vh = host(kc).view(np.uint16), host(vc).view(np.uint16)
+    NQKV = QD + 2 * KVD
+    qkv = _buf(L, "QKV", nseq * NQKV, torch.float32).reshape(nseq, NQKV)
+    q = _buf(L, "Q", nseq * QD, torch.float32).reshape(nseq, QD)
+    attn = _buf(L, "ATTN", nseq * QD, torch.float32).reshape(nseq, QD)
+    for t in range(nseq):
+        p, b = int(ctxs[t]) - 1, t * stride
+        assert np.array_equal(q[t].view(np.uint32),
+                              oracle.rope(qkv[t, :QD], s.qheads, D, p).view(np.uint32)), t
+        wk = oracle.f32_to_f16(oracle.rope(qkv[t, QD:QD + KVD], s.kvheads, D, p))
+        assert np.array_equal(kh[b + p * KVD:b + (p + 1) * KVD], wk), f"K row of seq {t}"
+        assert np.array_equal(vh[b + p * KVD:b + (p + 1) * KVD],
+                              oracle.f32_to_f16(qkv[t, QD + KVD:])), f"V row of seq {t}"
+        # the rest of the cache is untouched
+        rest = np.r_[0:p * KVD, (p + 1) * KVD:stride]
+        assert np.array_equal(kh[b:b + stride][rest], kc0[b:b + stride][rest]), t
+        want = oracle.attention_flash(os_, q[t], kh[b:b + stride], vh[b:b + stride], int(ctxs[t]))
+        close(attn[t], want, 2e-3, f"{name} attention seq {t} (context {ctxs[t]})")
+    attq = _q8_rows(L, "ATTQ", nseq, QD)
+    assert attq.tobytes() == oracle.quantize_q8(attn).tobytes(), "attention Q8"
+    L.close()
