@@ -53,6 +53,10 @@ static int check_launch(const char *what) {
 
 static inline hipStream_t S(void *stream) { return (hipStream_t)stream; }
 
+// Q4_0 nibble bytes of an n x k matrix: the mat-vec kernels address a
+// weight array with 32-bit buffer offsets
+static bool q4_fits(long long n, long long k) { return n * (k / 32) * 16 < (1ll << 32); }
+
 static int check_shape(const si_shape_t *s) {
     SI_REQUIRE(s, "shape is NULL");
     SI_REQUIRE(s->hidden > 0 && s->hidden % 32 == 0, "hidden %d must be a positive multiple of 32",
@@ -63,6 +67,13 @@ static int check_shape(const si_shape_t *s) {
                s->qheads, s->kvheads, s->hdim);
     SI_REQUIRE(s->ffn >= 0 && s->ffn % 32 == 0, "ffn %d must be a multiple of 32", s->ffn);
     SI_REQUIRE(s->hidden <= 8192, "hidden %d exceeds 8192", s->hidden);
+    {
+        const long long h = s->hidden, qd = (long long)s->qheads * s->hdim,
+                        kvd = (long long)s->kvheads * s->hdim, f = s->ffn;
+        SI_REQUIRE(q4_fits(qd + 2 * kvd, h) && q4_fits(h, qd) && q4_fits(2 * f, h) &&
+                       q4_fits(h, f),
+                   "a weight matrix reaches 4 GiB of Q4_0 nibbles");
+    }
     return SI_OK;
 }
 
@@ -147,6 +158,7 @@ int si_matvec_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int 
                    const float *residual, float *out, int flags, void *stream) {
     SI_REQUIRE(n > 0 && k > 0 && k % 32 == 0, "matvec: bad size n=%d k=%d", n, k);
     SI_REQUIRE(tile_ok(tile), "matvec: tile %d not 8, 16, 32 or 64", tile);
+    SI_REQUIRE(q4_fits(n, k), "matvec: %d x %d reaches 4 GiB of Q4_0 nibbles", n, k);
     SI_REQUIRE(wqs && wd && xqs && xd && xs && out, "matvec: NULL pointer");
     SI_REQUIRE(((uintptr_t)wqs & 15) == 0 && ((uintptr_t)xqs & 15) == 0,
                "matvec: wqs and xqs must be 16-byte aligned");
@@ -162,6 +174,7 @@ int si_ffn_gateup_q8(const float *h, const float *gain, int hidden, float eps,
     SI_REQUIRE(hidden > 0 && hidden % 32 == 0 && hidden <= 8192, "ffn_gateup: bad hidden %d",
                hidden);
     SI_REQUIRE(f > 0 && f % 32 == 0, "ffn_gateup: ffn %d must be a multiple of 32", f);
+    SI_REQUIRE(q4_fits(2ll * f, hidden), "ffn_gateup: gate|up reaches 4 GiB of Q4_0 nibbles");
     SI_REQUIRE(tile == 32, "ffn_gateup: the gate|up weights need scale tile 32 (got %d)", tile);
     SI_REQUIRE(h && wqs && wd && qs && d && bsum, "ffn_gateup: NULL pointer");
     SI_REQUIRE(((uintptr_t)wqs & 15) == 0 && ((uintptr_t)h & 15) == 0 &&

@@ -282,6 +282,14 @@ __host__ __device__ __forceinline__ size_t q4_scale_count(int n, int nb, int til
     return (size_t)((n + tile - 1) / tile) * tile * nb;
 }
 
+// Buffer descriptor of `bytes` bytes at p (raw buffer: a load whose offset
+// lies at or past the end returns zero without a memory access, instead of
+// faulting).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
 // Signed 8-bit 4-way dot product with int32 accumulate (v_dot4_i32_i8).
 __device__ __forceinline__ int sdot4(int a, int b, int c) {
     return __builtin_amdgcn_sdot4(a, b, c, false);

@@ -209,13 +209,6 @@ struct GateUpOut {
     int16_t *s;     // optional [m][f/32] block sums
 };
 
-// Buffer descriptor of `bytes` bytes at p (raw buffer: a load whose offset
-// lies at or past the end returns zero instead of faulting).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
-                                             0x00020000);
-}
-
 // Register staging of one LDS stage of k_gemm_fast.  Each thread's byte
 // offsets inside a stage are fixed (rows clamped once); a stage moves the
 // buffer bases, scalar work, so a stage costs no per-load VALU address math.

@@ -7,9 +7,10 @@
 // (KL = T / R).  Weights are block-major ([K/32][N][16] nibble bytes,
 // [K/32][N] fp16 scales), so one wavefront load of a block touches R
 // consecutive rows (R*16 contiguous bytes) for 64/R blocks.  Each thread
-// keeps U = 8 blocks of loads in flight.  Per block: 8 AND/shift unpacks,
-// 8 v_dot4 int8 dots and one -8*sum(a) correction give the exact int32
-// dot; the fp32 epilogue applies both fp16 scales.  Partial sums meet
+// loads U blocks at a time (U = 2: deeper batches measured slower).
+// Per block: 8 AND/shift unpacks, 8 v_dot4 int8 dots and one -8*sum(a)
+// correction give the exact int32 dot; the fp32 epilogue applies both fp16
+// scales.  Partial sums meet
 // through wavefront shuffles and LDS in a fixed order (deterministic).
 // With R = T (one thread per row, KL = 1) a row's blocks are accumulated in
 // order with the reference's roundings, y = bias; y = y + ((float)dot *
@@ -70,14 +71,13 @@ struct RowGateUp {
 // per tile (mat-vec workgroups use R = tile, so the scales of a wavefront's
 // rows and blocks are one contiguous run that no other workgroup reads).
 // red: LDS scratch of red_floats<R, T>() floats.
-template <int R, int T, bool EXACT, typename Map>
+template <int R, int T, bool EXACT, typename Map, int U = 2>
 struct GemvRows {
     static_assert(!EXACT || R == T, "exact mode keeps one thread per row");
     static constexpr int KL = T / R;  // K lanes per row
-    static constexpr int U = 8;       // blocks in flight per thread
-    const uint8_t *wp;
-    const uint16_t *dp;
-    size_t bstride, sstride;
+    __amdgpu_buffer_rsrc_t wrs, drs;  // the whole weight and scale arrays
+    uint32_t woff, doff;              // this row's block-0 byte offsets
+    uint32_t bstride, sstride;        // bytes per block step
     int nb, kl, r;
     uint4 w[U];
     uint16_t ws[U];
@@ -90,20 +90,25 @@ struct GemvRows {
         kl = t / R;
         nb = nb_;
         const int srow = map(min(tile0 + r, n - 1));
-        wp = wqs + (size_t)srow * 16;
-        dp = wd + q4_scale_index(srow, 0, nb, tile);
-        bstride = (size_t)nstore * 16;  // bytes per block plane
-        sstride = (size_t)tile;         // scale step per block
+        bstride = (uint32_t)nstore * 16;  // bytes per block plane
+        sstride = (uint32_t)tile * 2;     // scale bytes per block
+        wrs = buf_rsrc(wqs, (uint32_t)nb * bstride);
+        drs = buf_rsrc(wd, (uint32_t)(q4_scale_count(nstore, nb, tile) * 2));
+        woff = (uint32_t)srow * 16;
+        doff = (uint32_t)(q4_scale_index(srow, 0, nb, tile) * 2);
     }
-    // Branch-free: blocks past the end re-read the last block (a cache hit)
-    // and are skipped by finish(), so the compiler can count the loads in
-    // flight exactly (a load under a branch makes later waits drain all).
+    // Branch-free buffer loads: a block past the end lies past the weight
+    // array and reads as zero with no memory access (skipped by finish()),
+    // so the compiler can count the loads in flight exactly (a load under a
+    // branch makes later waits drain all).  The caller keeps the weight and
+    // scale arrays under 4 GiB.
     __device__ __forceinline__ void load(int b0) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int b = min(b0 + u * KL, nb - 1);
-            w[u] = *(const uint4 *)(wp + (size_t)b * bstride);
-            ws[u] = dp[(size_t)b * sstride];
+            const uint32_t b = (uint32_t)(b0 + u * KL);
+            w[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 wrs, woff + b * bstride, 0, 0));
+            ws[u] = __builtin_amdgcn_raw_buffer_load_b16(drs, doff + b * sstride, 0, 0);
         }
     }
     __device__ __forceinline__ void start() { load(kl); }

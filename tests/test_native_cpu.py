@@ -59,6 +59,14 @@ def test_argument_errors_do_not_launch():
     assert L.si_matvec_q4q8(None, None, 12, 64, 64, None, None, None, None, None, None, 0,
                             None) == si_amd.SI_ERR_ARG
     assert b"tile 12" in L.si_last_error()
+    # the mat-vec kernels address weights with 32-bit buffer offsets
+    assert L.si_matvec_q4q8(None, None, 8, 1 << 20, 8192, None, None, None, None, None, None,
+                            0, None) == si_amd.SI_ERR_ARG
+    assert b"4 GiB" in L.si_last_error()
+    huge = si_amd.make_shape(8192, 64, 8, 128, ffn=1 << 20)
+    assert L.si_layer_create(ctypes.byref(huge), ctypes.byref(si_amd.LayerHost()), 1, 16,
+                             ctypes.byref(ctypes.c_void_p())) == si_amd.SI_ERR_ARG
+    assert b"4 GiB" in L.si_last_error()
     assert L.si_q4_scale_count(300, 64, 16) == 304 * 2
     assert L.si_q4_tile(37888, 3584) == 32 and L.si_q4_tile(896, 896) == 8
     bad = si_amd.make_shape(896, 14, 3, 64)  # 14 % 3 != 0
