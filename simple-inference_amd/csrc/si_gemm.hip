@@ -475,6 +475,44 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
         }
 }
 
+// The gate|up split partials [splits][m][2f] summed in split order (as
+// k_gemm_reduce4), gate|up written to gu (optional), then SwiGLU and Q8_0
+// exactly as k_swiglu_q8: half a wavefront per 32-feature block of a row.
+__global__ void __launch_bounds__(256) k_gemm_reduce_swiglu_q8(
+    const float *__restrict__ part, int splits, int m, int f, float *__restrict__ gu,
+    float *__restrict__ act, int8_t *__restrict__ qs, uint16_t *__restrict__ d,
+    int16_t *__restrict__ bs) {
+    const int nbr = f / SI_QK;
+    const int blk = blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int j = threadIdx.x & 31;
+    if (blk >= m * nbr) return;  // whole half-wavefronts leave together
+    const int r = blk / nbr, b = blk - r * nbr;
+    const size_t mn = (size_t)m * 2 * f;
+    const size_t og = (size_t)r * 2 * f + (size_t)b * SI_QK + j, ou = og + f;
+    float g = part[og], u = part[ou];
+#pragma unroll 4
+    for (int sp = 1; sp < splits; ++sp) {
+        g += part[sp * mn + og];
+        u += part[sp * mn + ou];
+    }
+    if (gu) {
+        gu[og] = g;
+        gu[ou] = u;
+    }
+    const float silu = __fdiv_rn(g, __fadd_rn(1.0f, expf(-g)));
+    const float a = __fmul_rn(silu, u);
+    const size_t off = (size_t)r * f + (size_t)b * SI_QK + j;
+    if (act) act[off] = a;
+    uint16_t dbits;
+    int bsum;
+    const int q = quant_block_lane(a, dbits, bsum);
+    qs[off] = (int8_t)q;
+    if (j == 0) {
+        d[blk] = dbits;
+        if (bs) bs[blk] = (int16_t)bsum;
+    }
+}
+
 // out = residual + (bias + sum_s part[s]), the split partial sums in order.
 __global__ void __launch_bounds__(256) k_gemm_reduce(const float *__restrict__ part, int splits,
                                                      int m, int n, const float *__restrict__ bias,
@@ -552,17 +590,33 @@ size_t gemm_workspace_bytes(int m, int n, int k) {
     return p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0;
 }
 
+// The GEMM of launch_gemm_q4q8; with split partials and want_part, the
+// reduction is left to the caller (returns the number of splits written to
+// the workspace, else 0).
+static int gemm_core(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
+                     const int8_t *xqs, const uint16_t *xd, int m, const float *bias,
+                     const float *residual, float *out, int ldo, bool exact, void *workspace,
+                     size_t ws_bytes, bool want_part, hipStream_t st);
+
 void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
                       const int8_t *xqs, const uint16_t *xd, int m, const float *bias,
                       const float *residual, float *out, int ldo, bool exact, void *workspace,
                       size_t ws_bytes, hipStream_t st) {
-    if (m <= 0 || n <= 0) return;
+    gemm_core(wqs, wd, tile, n, k, xqs, xd, m, bias, residual, out, ldo, exact, workspace,
+              ws_bytes, false, st);
+}
+
+static int gemm_core(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
+                     const int8_t *xqs, const uint16_t *xd, int m, const float *bias,
+                     const float *residual, float *out, int ldo, bool exact, void *workspace,
+                     size_t ws_bytes, bool want_part, hipStream_t st) {
+    if (m <= 0 || n <= 0) return 0;
     const int nb = k / SI_QK;
     if (exact) {
         const dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM);
         hipLaunchKernelGGL(k_gemm_q4q8<true>, grid, dim3(256), 0, st, wqs, wd, tile, n, nb, xqs,
                            xd, m, bias, residual, out, ldo);
-        return;
+        return 0;
     }
     GemmPlan p = gemm_plan(m, n, nb);
     if (p.splits > 1 && (!workspace || ws_bytes < (size_t)p.splits * m * n * sizeof(float))) {
@@ -580,6 +634,7 @@ void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, i
     else
         CALL(2, 2, 2, 2);
 #undef CALL
+    if (part && want_part) return p.splits;
     if (part) {
         const size_t tot = (size_t)m * n;
         const auto al = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
@@ -590,11 +645,14 @@ void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, i
             hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0,
                                st, part, p.splits, m, n, bias, residual, out, ldo);
     }
+    return 0;
 }
 
 // gate|up GEMM with SwiGLU + Q8_0: f features, weights the physical
-// [gate; up] rows.  One fused kernel when the plan needs no K split;
-// otherwise (and in exact mode) the GEMM into gu, then k_swiglu_q8.
+// [gate; up] rows.  One fused kernel when the plan needs no K split; with a
+// split, the GEMM's partials then k_gemm_reduce_swiglu_q8 (split sums,
+// gate|up, SwiGLU and Q8 in one pass); in exact mode the GEMM into gu, then
+// k_swiglu_q8.
 void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, int k,
                            const int8_t *xqs, const uint16_t *xd, int m, float *gu, float *act,
                            int8_t *qs, uint16_t *d, int16_t *s, bool exact, void *workspace,
@@ -603,9 +661,15 @@ void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int
     const int n = 2 * f, nb = k / SI_QK;
     const GemmPlan p = gemm_plan(m, n, nb);
     if (exact || p.splits > 1) {
-        launch_gemm_q4q8(wqs, wd, tile, n, k, xqs, xd, m, nullptr, nullptr, gu, n, exact,
-                         workspace, ws_bytes, st);
-        launch_swiglu_q8(gu, m, f, act, qs, d, s, st);
+        const int splits = gemm_core(wqs, wd, tile, n, k, xqs, xd, m, nullptr, nullptr, gu, n,
+                                     exact, workspace, ws_bytes, true, st);
+        if (splits > 1) {
+            const int tot = m * (f / SI_QK);
+            hipLaunchKernelGGL(k_gemm_reduce_swiglu_q8, dim3((tot + 7) / 8), dim3(256), 0, st,
+                               (const float *)workspace, splits, m, f, gu, act, qs, d, s);
+        } else {
+            launch_swiglu_q8(gu, m, f, act, qs, d, s, st);
+        }
         return;
     }
     const GateUpOut go{f, act, qs, d, s};
