@@ -819,11 +819,21 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
         mark(L, SI_PHASE_COUNT, st);
         return check_launch("layer (attention sublayer)");
     }
-    project(L, L->wo, rows, L->attq, nullptr, nullptr, L->attn_out, flags, st);
+    // W_O; a K-split leaves its partials to the post-norm kernel, which sums
+    // them (o, kept in attn_out) on the way
+    const int osplits = launch_gemm_q4q8_parts(L->wo.qs, L->wo.d, L->wo.tile, L->wo.n, L->wo.k,
+                                               L->attq.qs, L->attq.d, rows, L->attn_out,
+                                               (flags & SI_LAYER_EXACT) != 0, L->gemm_ws,
+                                               L->gemm_ws_bytes, st);
     mark(L, SI_PHASE_POST_NORM_Q8, st);
     // build-defined FFN half: h = x + o; RMSNorm -> Q8; gate|up; SwiGLU -> Q8; down + h
-    launch_rmsnorm_q8(x, L->attn_out, L->post_norm, rows, H, s.rms_eps, L->h, L->normed2,
-                      L->xq2.qs, L->xq2.d, L->xq2.s, st);
+    if (osplits > 1)
+        launch_rmsnorm_q8_parts(x, (const float *)L->gemm_ws, osplits, L->post_norm, rows, H,
+                                s.rms_eps, L->attn_out, L->h, L->normed2, L->xq2.qs, L->xq2.d,
+                                L->xq2.s, st);
+    else
+        launch_rmsnorm_q8(x, L->attn_out, L->post_norm, rows, H, s.rms_eps, L->h, L->normed2,
+                          L->xq2.qs, L->xq2.d, L->xq2.s, st);
     mark(L, SI_PHASE_GATE_UP, st);
     if (rows == 1) {
         project(L, L->wgu, rows, L->xq2, nullptr, nullptr, L->gu, flags, st);

@@ -590,13 +590,25 @@ size_t gemm_workspace_bytes(int m, int n, int k) {
     return p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0;
 }
 
-// The GEMM of launch_gemm_q4q8; with split partials and want_part, the
-// reduction is left to the caller (returns the number of splits written to
-// the workspace, else 0).
 static int gemm_core(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
                      const int8_t *xqs, const uint16_t *xd, int m, const float *bias,
                      const float *residual, float *out, int ldo, bool exact, void *workspace,
                      size_t ws_bytes, bool want_part, hipStream_t st);
+
+int launch_gemm_q4q8_parts(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
+                           const int8_t *xqs, const uint16_t *xd, int m, float *out, bool exact,
+                           void *workspace, size_t ws_bytes, hipStream_t st) {
+    return gemm_core(wqs, wd, tile, n, k, xqs, xd, m, nullptr, nullptr, out, n, exact, workspace,
+                     ws_bytes, true, st);
+}
+
+void launch_gemm_reduce(const float *part, int splits, int m, int n, float *out,
+                        hipStream_t st) {
+    const size_t tot = (size_t)m * n;
+    if (!tot) return;
+    hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st,
+                       part, splits, m, n, nullptr, nullptr, out, n);
+}
 
 void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
                       const int8_t *xqs, const uint16_t *xd, int m, const float *bias,

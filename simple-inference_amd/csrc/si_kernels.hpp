@@ -22,6 +22,20 @@ void launch_matvec(const int8_t *xqs, const uint16_t *xd, const int16_t *xs, int
                    const float *residual, float *out, bool exact, hipStream_t st);
 void launch_block_dots(const uint8_t *wqs, int n, int k, const int8_t *xqs, const int16_t *xs,
                        int32_t *dots, hipStream_t st);
+// The GEMM of launch_gemm_q4q8 without bias or residual; when the plan
+// splits K, the split partial sums stay in workspace as [splits][m][n] for
+// the caller to reduce and the number of splits is returned, else 0 (out
+// holds the product).
+int launch_gemm_q4q8_parts(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
+                           const int8_t *xqs, const uint16_t *xd, int m, float *out, bool exact,
+                           void *workspace, size_t ws_bytes, hipStream_t st);
+// out[m][n] = sum of part[s][m][n] in split order.
+void launch_gemm_reduce(const float *part, int splits, int m, int n, float *out, hipStream_t st);
+// launch_rmsnorm_q8 with y = the split-order sum of part[splits][rows][n],
+// written to y_out as well.
+void launch_rmsnorm_q8_parts(const float *x, const float *part, int splits, const float *gain,
+                             int rows, int n, float eps, float *y_out, float *h, float *normed,
+                             int8_t *qs, uint16_t *d, int16_t *s, hipStream_t st);
 void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
                       const int8_t *xqs, const uint16_t *xd, int m, const float *bias,
                       const float *residual, float *out, int ldo, bool exact, void *workspace,

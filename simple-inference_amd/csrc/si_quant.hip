@@ -125,7 +125,9 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8(const float *__restrict__ x,
 // float4 chunks t + 256*i (i < NPT) of its workgroup's row, so 8 consecutive
 // threads hold one 32-value block and quantize it with quant_block_oct.  One
 // pass over global memory, no LDS staging; needs 16-byte aligned rows.
-template <bool RESIDUAL, int NPT>
+// PARTS (with RESIDUAL): y is the split-order sum of y[sp * rows * n + ...]
+// for sp < splits (a K-split GEMM's partials), also written to y_out.
+template <bool RESIDUAL, int NPT, bool PARTS = false>
 __global__ void __launch_bounds__(256) k_rmsnorm_q8_v4(const float *__restrict__ x,
                                                        const float *__restrict__ y,
                                                        const float *__restrict__ gain, int n,
@@ -133,7 +135,8 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8_v4(const float *__restrict__
                                                        float *__restrict__ normed,
                                                        int8_t *__restrict__ qs,
                                                        uint16_t *__restrict__ d,
-                                                       int16_t *__restrict__ s) {
+                                                       int16_t *__restrict__ s, int splits = 1,
+                                                       float *__restrict__ y_out = nullptr) {
     __shared__ double red[4];
     const int r = blockIdx.x, tid = threadIdx.x, n4 = n / 4;
     const size_t base = (size_t)r * n;
@@ -144,7 +147,27 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8_v4(const float *__restrict__
         const int c = min(tid + 256 * i, n4 - 1);  // clamped: branch-free loads
         float4 a = *(const float4 *)(x + base + 4 * c);
         if (RESIDUAL) {
-            const float4 b = *(const float4 *)(y + base + 4 * c);
+            float4 b = *(const float4 *)(y + base + 4 * c);
+            if (PARTS) {
+                // groups of 8 splits, loads branch-free (clamped split,
+                // selected out of the sum) so a group is in flight together
+                const size_t ps = (size_t)gridDim.x * n;
+                for (int s0 = 1; s0 < splits; s0 += 8) {
+                    float4 p[8];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k)
+                        p[k] = *(const float4 *)(y + min(s0 + k, splits - 1) * ps + base + 4 * c);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const bool on = s0 + k < splits;
+                        b.x = on ? b.x + p[k].x : b.x;
+                        b.y = on ? b.y + p[k].y : b.y;
+                        b.z = on ? b.z + p[k].z : b.z;
+                        b.w = on ? b.w + p[k].w : b.w;
+                    }
+                }
+                if (tid + 256 * i < n4) *(float4 *)(y_out + base + 4 * c) = b;
+            }
             a = make_float4(__fadd_rn(a.x, b.x), __fadd_rn(a.y, b.y), __fadd_rn(a.z, b.z),
                             __fadd_rn(a.w, b.w));
         }
@@ -282,6 +305,28 @@ void launch_quantize_q8_rows(const float *src, int rows, int k, int8_t *qs, uint
     if (tot == 0) return;
     hipLaunchKernelGGL(k_quantize_q8_rows, dim3((tot + 7) / 8), dim3(256), 0, st, src, k, nbr,
                        tot, qs, d, s);
+}
+
+void launch_rmsnorm_q8_parts(const float *x, const float *part, int splits, const float *gain,
+                             int rows, int n, float eps, float *y_out, float *h, float *normed,
+                             int8_t *qs, uint16_t *d, int16_t *s, hipStream_t st) {
+    if (rows == 0) return;
+    const auto al = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    const int n4 = n / 4;
+    if (!(n4 <= 2048 && al(x) && al(part) && al(y_out) && al(h) && al(normed) && al(gain) &&
+          al(qs))) {
+        launch_gemm_reduce(part, splits, rows, n, y_out, st);
+        launch_rmsnorm_q8(x, y_out, gain, rows, n, eps, h, normed, qs, d, s, st);
+        return;
+    }
+#define RMS_P(NPT)                                                                              \
+    hipLaunchKernelGGL((k_rmsnorm_q8_v4<true, NPT, true>), dim3(rows), dim3(256), 0, st, x, part, \
+                       gain, n, eps, h, normed, qs, d, s, splits, y_out)
+    if (n4 <= 256) RMS_P(1);
+    else if (n4 <= 512) RMS_P(2);
+    else if (n4 <= 1024) RMS_P(4);
+    else RMS_P(8);
+#undef RMS_P
 }
 
 void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int rows, int n,
