@@ -132,9 +132,10 @@ class Timer:
 # ---------------------------------------------------------------------------
 # configurations
 # ---------------------------------------------------------------------------
-def bench_decode_layer(torch, si_amd, stream, steps, warmup, ctx=1024):
-    """BASELINE config 2 (default workload)."""
-    s = si_amd.make_shape(**si_amd.SHAPES["0.5b"])
+def bench_decode_layer(torch, si_amd, stream, steps, warmup, ctx=1024, shape_name="0.5b"):
+    """BASELINE config 2 (default workload); with shape_name="7b" the same
+    single-token decode step of a Qwen2.5-7B-shaped layer."""
+    s = si_amd.make_shape(**si_amd.SHAPES[shape_name])
     tens = make_layer_tensors(si_amd, s, 1)
     kvd = s.kvheads * s.hdim
     per_copy = weight_bytes(s) + 2 * ctx * kvd * 2 + small_bytes(s)
@@ -479,7 +480,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--dominant-only", action="store_true",
                     help="run only the dominant-kernel leg (for rocprofv3)")
-    ap.add_argument("--only", choices=["prefill-0.5b", "prefill-7b", "batched-7b"],
+    ap.add_argument("--only", choices=["prefill-0.5b", "prefill-7b", "batched-7b", "decode-7b"],
                     help="run only this configuration and print its result (for rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -494,7 +495,9 @@ def main():
     torch.cuda.set_device(0)
     stream = torch.cuda.Stream()
     if args.only:
-        if args.only == "batched-7b":
+        if args.only == "decode-7b":
+            r, _ = bench_decode_layer(torch, si_amd, stream, 100, 10, ctx=4096, shape_name="7b")
+        elif args.only == "batched-7b":
             r = bench_batched_decode(torch, si_amd, stream, 5)
         else:
             name, ntok = ("0.5b", 512) if args.only == "prefill-0.5b" else ("7b", 2048)
@@ -517,6 +520,18 @@ def main():
     log("7B decode projections (k_matvec) ...")
     extra["gemv_7b_cold"] = bench_gemv_7b(torch, si_amd, stream)
     log(f"  {extra['gemv_7b_cold']}")
+    log("7B decode layer, ctx 4096 ...")
+    d7, held = bench_decode_layer(torch, si_amd, stream, 100, 10, ctx=4096, shape_name="7b")
+    for lay in held[0]:
+        lay.close()
+    held[4].close()
+    del held
+    extra["decode_7b_ctx4096"] = {k: (round(v, 2) if isinstance(v, float) else v)
+                                  for k, v in d7.items()}
+    extra["decode_7b_ctx4096"]["hbm_frac"] = round(d7["gbs"] / HBM_PEAK_GBS, 4)
+    log(f"  {extra['decode_7b_ctx4096']}")
+    del d7
+    torch.cuda.empty_cache()
     if not args.quick:
         log("config 1: QKV GEMV ...")
         extra["cfg1_qkv_gemv_0.5b"] = bench_qkv_gemv(torch, si_amd, stream)

@@ -739,10 +739,19 @@ static int run_decode(si_layer *L, const float *x, uint16_t *kc, uint16_t *vc, i
     const float *pm = (const float *)L->attn_ws;
     const float *pl = pm + (size_t)s.qheads * ns;
     const float *po = pl + (size_t)s.qheads * ns;
-    launch_dec_wo(pm, pl, po, ns, s.qheads, s.hdim, L->wo.qs, L->wo.d, L->wo.tile, H,
-                  full ? x : nullptr,
-                  L->attn, L->attq.qs, L->attq.d, L->attq.s, full ? L->attn_out : nullptr,
-                  full ? L->h : out, exact, st);
+    if ((size_t)s.qheads * ns * (s.hdim + 2) * sizeof(float) > 32 * 1024) {
+        // many chunk partials (7B at long contexts): merge them once instead
+        // of in every W_O workgroup (each would re-read all of them)
+        launch_attn_combine(1, s.qheads, s.hdim, ns, L->attn_ws, L->attn, L->attq.qs, L->attq.d,
+                            L->attq.s, st);
+        launch_matvec(L->attq.qs, L->attq.d, L->attq.s, QD, L->wo.qs, L->wo.d, L->wo.tile, H,
+                      nullptr, full ? x : nullptr, full ? L->h : out, exact, st,
+                      full ? L->attn_out : nullptr);
+    } else {
+        launch_dec_wo(pm, pl, po, ns, s.qheads, s.hdim, L->wo.qs, L->wo.d, L->wo.tile, H,
+                      full ? x : nullptr, L->attn, L->attq.qs, L->attq.d, L->attq.s,
+                      full ? L->attn_out : nullptr, full ? L->h : out, exact, st);
+    }
     if (!full) {
         mark(L, SI_PHASE_COUNT, st);
         return check_launch("layer decode (attention sublayer)");

@@ -25,7 +25,7 @@ __global__ void __launch_bounds__(T) k_matvec(
     const int8_t *__restrict__ xqs, const uint16_t *__restrict__ xd,
     const int16_t *__restrict__ xs, int k, const uint8_t *__restrict__ wqs,
     const uint16_t *__restrict__ wd, int tile, int n, const float *__restrict__ bias,
-    const float *__restrict__ residual, float *__restrict__ out) {
+    const float *__restrict__ residual, float *__restrict__ out, float *__restrict__ pre) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int nb = k / SI_QK;
     float *red = (float *)smem;
@@ -70,18 +70,19 @@ __global__ void __launch_bounds__(T) k_matvec(
     const float y = g.finish(Q8Row{lq, ld, ls}, EXACT ? b0 : 0.0f, red);
     if (t < R && row < n) {
         const float v = EXACT ? y : y + b0;
+        if (pre) pre[row] = v;
         out[row] = residual ? __fadd_rn(residual[row], v) : v;
     }
 }
 
 void launch_matvec(const int8_t *xqs, const uint16_t *xd, const int16_t *xs, int k,
                    const uint8_t *wqs, const uint16_t *wd, int tile, int n, const float *bias,
-                   const float *residual, float *out, bool exact, hipStream_t st) {
+                   const float *residual, float *out, bool exact, hipStream_t st, float *pre) {
     if (n <= 0) return;
 #define CALL(R, T, E)                                                                        \
     hipLaunchKernelGGL((k_matvec<R, T, E>), dim3((n + R - 1) / R), dim3(T),                  \
                        (matvec_lds_bytes<R, T>(k)), st, xqs, xd, xs, k, wqs, wd, tile, n, bias,  \
-                       residual, out)
+                       residual, out, pre)
     if (exact) {
         CALL(64, 64, true);
     } else {

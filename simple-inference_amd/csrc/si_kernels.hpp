@@ -17,9 +17,11 @@ void launch_q4_repack(const uint8_t *src, int n, int k, int tile, uint8_t *qs, u
                       hipStream_t st);
 void launch_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k, int tile,
                       uint8_t *dst, hipStream_t st);
+// pre (optional): the value before the residual is added
 void launch_matvec(const int8_t *xqs, const uint16_t *xd, const int16_t *xs, int k,
                    const uint8_t *wqs, const uint16_t *wd, int tile, int n, const float *bias,
-                   const float *residual, float *out, bool exact, hipStream_t st);
+                   const float *residual, float *out, bool exact, hipStream_t st,
+                   float *pre = nullptr);
 void launch_block_dots(const uint8_t *wqs, int n, int k, const int8_t *xqs, const int16_t *xs,
                        int32_t *dots, hipStream_t st);
 // The GEMM of launch_gemm_q4q8 without bias or residual; when the plan

@@ -83,10 +83,13 @@ def test_decode_full_layer_0_5b_ctx1024(oracle, flags):
 
 
 @pytest.mark.parametrize("shape,ctx", [("0.5b", 1), ("0.5b", 2), ("0.5b", 16), ("0.5b", 17),
-                                       ("0.5b", 129), ("0.5b", 500), ("7b", 33), ("7b", 4096)])
+                                       ("0.5b", 129), ("0.5b", 500), ("0.5b", 5000), ("7b", 33),
+                                       ("7b", 4096)])
 def test_decode_contexts(oracle, shape, ctx):
     """Single-token decode over contexts that put the new token at every kind
-    of place in the attention chunks (first tile, tile edge, last chunk)."""
+    of place in the attention chunks (first tile, tile edge, last chunk); at
+    0.5B 5000 and 7B 4096 the chunk partials exceed 32 KB and are merged once
+    before W_O instead of inside it."""
     torch = _torch()
     s, os_ = _shapes(shape)
     lay = make_layer(oracle, os_, 40 + ctx)
