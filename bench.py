@@ -329,6 +329,40 @@ def bench_gemv_7b(torch, si_amd, stream, launches=200):
     return res
 
 
+def bench_gguf_ingest(torch, si_amd, shape_name="7b", reps=3):
+    """GGUF ingest of one layer (si_amd.gguf): a Q4_0 GGUF written to a
+    temporary file, then, timed, index + memory map + si_amd.Layer (host to
+    device copy and the GPU repack), synchronized.  The file is in the page
+    cache (just written): this is the parse + copy + repack rate."""
+    import shutil
+    import tempfile
+    from si_amd import gguf
+    sd = dict(si_amd.SHAPES[shape_name])
+    s = si_amd.make_shape(**sd)
+    tens = make_layer_tensors(si_amd, s, 31)
+    tmp = tempfile.mkdtemp()
+    try:
+        path = os.path.join(tmp, "layer.gguf")
+        gguf.write_gguf(path, gguf.layer_meta(sd), gguf.layer_tensors_gguf(sd, tens, layer=0))
+        size = os.path.getsize(path)
+        best = None
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            with gguf.GGUFFile(path) as gf:
+                gsd, gt = gguf.load_layer(gf, 0)
+                lay = si_amd.Layer(si_amd.make_shape(**gsd), gt, 1, 16)
+                torch.cuda.synchronize()
+                dt = time.perf_counter() - t0
+                lay.close()
+                del gt
+            best = dt if best is None else min(best, dt)
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    return dict(shape=shape_name, file_bytes=size, ms=round(best * 1e3, 2),
+                gbs=round(size / best / 1e9, 2))
+
+
 def bench_prefill(torch, si_amd, stream, shape_name, ntok, steps):
     """BASELINE configs 3 (0.5B, 512 tokens) and 4 (7B, 2048 tokens)."""
     s = si_amd.make_shape(**si_amd.SHAPES[shape_name])
@@ -480,7 +514,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--dominant-only", action="store_true",
                     help="run only the dominant-kernel leg (for rocprofv3)")
-    ap.add_argument("--only", choices=["prefill-0.5b", "prefill-7b", "batched-7b", "decode-7b"],
+    ap.add_argument("--only", choices=["prefill-0.5b", "prefill-7b", "batched-7b", "decode-7b",
+                                       "gguf-7b"],
                     help="run only this configuration and print its result (for rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -495,7 +530,9 @@ def main():
     torch.cuda.set_device(0)
     stream = torch.cuda.Stream()
     if args.only:
-        if args.only == "decode-7b":
+        if args.only == "gguf-7b":
+            r = bench_gguf_ingest(torch, si_amd)
+        elif args.only == "decode-7b":
             r, _ = bench_decode_layer(torch, si_amd, stream, 100, 10, ctx=4096, shape_name="7b")
         elif args.only == "batched-7b":
             r = bench_batched_decode(torch, si_amd, stream, 5)
@@ -542,6 +579,9 @@ def main():
         log("config 4: 7B prefill 2048 ...")
         extra["cfg4_prefill_7b_2048"] = bench_prefill(torch, si_amd, stream, "7b", 2048, 3)
         log(f"  {extra['cfg4_prefill_7b_2048']}")
+        log("GGUF ingest, 7B-shaped layer ...")
+        extra["gguf_ingest_7b_layer"] = bench_gguf_ingest(torch, si_amd)
+        log(f"  {extra['gguf_ingest_7b_layer']}")
         log("config 5: 7B batched decode 64 x 4096 ...")
         extra["cfg5_batched_decode_7b_64x4096"] = bench_batched_decode(torch, si_amd, stream, 5)
         log(f"  {extra['cfg5_batched_decode_7b_64x4096']}")

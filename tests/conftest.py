@@ -3,6 +3,15 @@ import sys
 
 import pytest
 
+# torch first: its wheel carries its own HIP runtime, and the native
+# libraries (libsi_amd.so, libsi_host.so) must bind to that copy.  Loaded
+# before torch, they would bring the system runtime and the two would
+# compete for the device (whichever initializes second fails).
+try:
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 for p in (ROOT, os.path.join(ROOT, "simple-inference_amd")):
     if p not in sys.path:
