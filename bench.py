@@ -329,6 +329,61 @@ def bench_gemv_7b(torch, si_amd, stream, launches=200):
     return res
 
 
+def bench_attention_modes(torch, si_amd, shape_name="7b", ctx=4096, count=100):
+    """The two attention methods of one decode step (attention_kernels.h:33-78
+    and :80-164) on the same query and cache, each call's K/V rotated over
+    enough copies to defeat the Infinity Cache: si_attention_standard (scores
+    materialized in a [qheads][ctx] buffer, softmax in place, weighted V sum)
+    and si_attention (the streaming flash-decoding kernels, Q8 of the output
+    included).  Algorithmic bytes: K and V read once per KV group, plus the
+    standard method's score buffer (written, read and written by the
+    softmax, read by the V sum)."""
+    s = si_amd.make_shape(**si_amd.SHAPES[shape_name])
+    kvd, QD = s.kvheads * s.hdim, s.qheads * s.hdim
+    kv_bytes = 2 * ctx * kvd * 2
+    copies = int(np.ceil(1.25 * MALL_BYTES / kv_bytes))
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    caches = [(torch.randn(ctx * kvd, generator=gen, device="cuda").half(),
+               torch.randn(ctx * kvd, generator=gen, device="cuda").half())
+              for _ in range(copies)]
+    q = torch.randn(QD, generator=gen, device="cuda")
+    out = torch.empty(QD, device="cuda")
+    scores = torch.empty(s.qheads * ctx, device="cuda")
+    wsb = si_amd.lib().si_attention_workspace(ctypes.byref(s), 1, ctx)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    qs = torch.empty(QD, dtype=torch.int8, device="cuda")
+    qd = torch.empty(QD // 32, dtype=torch.int16, device="cuda")
+    cur = lambda: si_amd.stream_handle(torch.cuda.current_stream())  # noqa: E731
+
+    def standard(i):
+        kc, vc = caches[i % copies]
+        si_amd.call("si_attention_standard", ctypes.byref(s), si_amd.ptr(q), si_amd.ptr(kc),
+                    si_amd.ptr(vc), ctx, si_amd.ptr(out), si_amd.ptr(scores), cur())
+
+    def flash(i):
+        kc, vc = caches[i % copies]
+        si_amd.call("si_attention", ctypes.byref(s), si_amd.ptr(q), 1, si_amd.ptr(kc),
+                    si_amd.ptr(vc), 0, None, ctx, 0, ctx, si_amd.ptr(out), si_amd.ptr(qs),
+                    si_amd.ptr(qd), None, si_amd.ptr(ws), wsb, cur())
+
+    stream = torch.cuda.Stream()
+    res = {"shape": shape_name, "context": ctx, "kv_copies_rotated": copies}
+    score_bytes = 4 * s.qheads * ctx * 4
+    for name, fn, alg in (("standard", standard, kv_bytes + score_bytes),
+                          ("flash", flash, kv_bytes)):
+        with torch.cuda.stream(stream):
+            for i in range(4):
+                fn(i)
+        torch.cuda.synchronize()
+        ms = graph_time_ms(torch, stream, fn, count)
+        res[name + "_us"] = round(ms * 1e3, 3)
+        res[name + "_gbs"] = round(alg / (ms * 1e-3) / 1e9, 1)
+    res["speedup_flash"] = round(res["standard_us"] / res["flash_us"], 3)
+    del caches
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_gguf_ingest(torch, si_amd, shape_name="7b", reps=3):
     """GGUF ingest of one layer (si_amd.gguf): a Q4_0 GGUF written to a
     temporary file, then, timed, index + memory map + si_amd.Layer (host to
@@ -515,7 +570,7 @@ def main():
     ap.add_argument("--dominant-only", action="store_true",
                     help="run only the dominant-kernel leg (for rocprofv3)")
     ap.add_argument("--only", choices=["prefill-0.5b", "prefill-7b", "batched-7b", "decode-7b",
-                                       "gguf-7b"],
+                                       "gguf-7b", "attention-7b"],
                     help="run only this configuration and print its result (for rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -532,6 +587,8 @@ def main():
     if args.only:
         if args.only == "gguf-7b":
             r = bench_gguf_ingest(torch, si_amd)
+        elif args.only == "attention-7b":
+            r = bench_attention_modes(torch, si_amd)
         elif args.only == "decode-7b":
             r, _ = bench_decode_layer(torch, si_amd, stream, 100, 10, ctx=4096, shape_name="7b")
         elif args.only == "batched-7b":
@@ -579,6 +636,9 @@ def main():
         log("config 4: 7B prefill 2048 ...")
         extra["cfg4_prefill_7b_2048"] = bench_prefill(torch, si_amd, stream, "7b", 2048, 3)
         log(f"  {extra['cfg4_prefill_7b_2048']}")
+        log("attention methods, 7B-shaped, ctx 4096 ...")
+        extra["attention_standard_vs_flash_7b_ctx4096"] = bench_attention_modes(torch, si_amd)
+        log(f"  {extra['attention_standard_vs_flash_7b_ctx4096']}")
         log("GGUF ingest, 7B-shaped layer ...")
         extra["gguf_ingest_7b_layer"] = bench_gguf_ingest(torch, si_amd)
         log(f"  {extra['gguf_ingest_7b_layer']}")

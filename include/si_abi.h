@@ -194,6 +194,16 @@ int si_attention(const si_shape_t *s, const float *q, int nq, const uint16_t *kc
                  void *stream);
 size_t si_attention_workspace(const si_shape_t *s, int nq, int max_ctx);
 
+/* attention_standard (attention_kernels.h:33-78) for one query: scores
+ * [qheads][context] fp32 (device, caller-owned like the reference's
+ * score_workspace) receive the scaled Q.K products (the reference's bits:
+ * sequential sum over the head dimension), are normalised in place by a
+ * softmax, and weight V into out [qheads][hdim].  kc/vc are [context][kvheads]
+ * [hdim] fp16, both 16-byte aligned.  context 0 gives a zero output. */
+int si_attention_standard(const si_shape_t *s, const float *q, const uint16_t *kc,
+                          const uint16_t *vc, int context, float *out, float *scores,
+                          void *stream);
+
 /* Test entry for the fp16 matrix-core lane layouts the attention kernels
  * rely on: a [16][32] and b [32][16] fp16 (row-major) -> d32 = a.b with the
  * 16x16x32 shape and d16 = a[:, :16].b[:16, :] with the 16x16x16 shape
@@ -256,9 +266,13 @@ int si_layer_destroy(si_layer_t *l);
 enum {
     SI_LAYER_FULL = 0,      /* attention + residual + norm + SwiGLU FFN + residual */
     SI_LAYER_ATTN_ONLY = 1, /* reference run_layer: out = W_O . Q8(attn)          */
-    SI_LAYER_EXACT = 2      /* reference rounding in every projection (bit-exact Q/K/V,
+    SI_LAYER_EXACT = 2,     /* reference rounding in every projection (bit-exact Q/K/V,
                                O, gate/up, down given identical inputs): mat-vecs
                                without K splits, GEMMs with the exact epilogue */
+    SI_LAYER_ATTN_STANDARD = 4 /* si_layer_decode only: the reference's staged order
+                               with ATTENTION_STANDARD (qwen_one_layer.c:260-275):
+                               RoPE + K/V append, si_attention_standard into the
+                               layer's [qheads][max_pos] score buffer, Q8, W_O */
 };
 
 /* run_layer (qwen_one_layer.c:237-281) for one token at position context-1:

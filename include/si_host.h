@@ -76,8 +76,10 @@ si_model_t *si_model_from_host(const si_shape_t *shape, const si_layer_host_t *w
                                int max_tokens, int max_pos);
 void free_layer(si_model_t *m);
 
-/* qwen_one_layer.c:237-281 with device x/kc/vc/output.  scores is unused
- * (both methods run the streaming kernel).  attn_copy (fp32 [qheads*hdim])
+/* qwen_one_layer.c:237-281 with device x/kc/vc/output.  ATTENTION_FLASH runs
+ * the fused streaming kernels; ATTENTION_STANDARD the staged order with the
+ * three-stage textbook attention (SI_LAYER_ATTN_STANDARD), whose scores live
+ * in the layer's own device buffer, so scores is unused.  attn_copy (fp32 [qheads*hdim])
  * and q8_copy (block_q8_0 [qheads*hdim/32]) are HOST buffers or NULL,
  * filled after the timed work as the reference's captures are (:277-279). */
 phase_t run_layer(const si_model_t *l, const float *x, uint16_t *kc, uint16_t *vc,
@@ -100,7 +102,8 @@ phase_t run_layer_full(const si_model_t *l, const float *x, uint16_t *kc, uint16
 void pf_run_batch(const si_model_t *l, const float *x, int ntok, int prefix, uint16_t *kc,
                   uint16_t *vc, float *output, int full);
 
-/* attention_kernels.h:80-164 / :166-173 for one token (device q/kc/vc/out). */
+/* attention_kernels.h:80-164 / :166-173 for one token (device q/kc/vc/out;
+ * score_workspace: device fp32 [qheads][context], used by ATTENTION_STANDARD). */
 void attention_flash(const si_model_t *l, const float *q, const uint16_t *kc,
                      const uint16_t *vc, int context, float *out);
 void attention_compute(const si_model_t *l, attention_method_t method, const float *q,

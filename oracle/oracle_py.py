@@ -164,11 +164,15 @@ class Oracle:
                                     context, _ptr(out))
         return out
 
-    def attention_standard(self, shape, q, kc, vc, context):
+    def attention_standard(self, shape, q, kc, vc, context, with_scores=False):
+        """out [qheads*hdim]; with_scores: also the normalised scores
+        [qheads][context] the reference leaves in its workspace."""
         out = np.empty(shape.qheads * shape.hdim, np.float32)
         scores = np.empty(shape.qheads * max(context, 1), np.float32)
         self.lib.or_attention_standard(ctypes.byref(shape), _ptr(q), _ptr(kc), _ptr(vc),
                                        context, _ptr(out), _ptr(scores))
+        if with_scores:
+            return out, scores[:shape.qheads * context].reshape(shape.qheads, context)
         return out
 
     def swiglu(self, g, u):
@@ -333,11 +337,13 @@ class Reference:
         self.lib.si_ref_attention_flash(_ptr(q), _ptr(kc), _ptr(vc), context, _ptr(out))
         return out
 
-    def attention_standard(self, q, kc, vc, context):
+    def attention_standard(self, q, kc, vc, context, with_scores=False):
         out = np.empty(self.qheads * self.hdim, np.float32)
         scores = np.empty(self.qheads * max(context, 1), np.float32)
         self.lib.si_ref_attention_standard(_ptr(q), _ptr(kc), _ptr(vc), context,
                                            _ptr(out), _ptr(scores))
+        if with_scores:
+            return out, scores[:self.qheads * context].reshape(self.qheads, context)
         return out
 
     def run_layer(self, layer, x, kc, vc, context, method=1):

@@ -302,6 +302,23 @@ int si_attention(const si_shape_t *s, const float *q, int nq, const uint16_t *kc
     return check_launch("si_attention");
 }
 
+int si_attention_standard(const si_shape_t *s, const float *q, const uint16_t *kc,
+                          const uint16_t *vc, int context, float *out, float *scores,
+                          void *stream) {
+    int r = check_shape(s);
+    if (r) return r;
+    SI_REQUIRE(context >= 0, "attention_standard: negative context");
+    SI_REQUIRE(attn_standard_supported(s->qheads, s->kvheads, s->hdim),
+               "attention_standard: unsupported head dimension %d", s->hdim);
+    SI_REQUIRE(out && (context == 0 || (q && kc && vc && scores)),
+               "attention_standard: NULL pointer");
+    SI_REQUIRE(context == 0 || ((uintptr_t)kc % 16 == 0 && (uintptr_t)vc % 16 == 0),
+               "attention_standard: kc and vc must be 16-byte aligned");
+    launch_attn_standard(q, s->qheads, s->kvheads, s->hdim, kc, vc, context, out, scores,
+                         S(stream));
+    return check_launch("si_attention_standard");
+}
+
 int si_debug_lane_ops(int *out, void *stream) {
     SI_REQUIRE(out, "debug_lane_ops: NULL pointer");
     launch_debug_lane_ops(out, S(stream));
@@ -383,6 +400,7 @@ struct Workspace {
     size_t attn_ws_bytes = 0;
     void *gemm_ws = nullptr;  // split-K partial sums of the matrix-core GEMMs
     size_t gemm_ws_bytes = 0;
+    float *scores = nullptr;  // [qheads][max_pos]: the standard attention mode
 };
 
 struct si_workspace {
@@ -451,6 +469,7 @@ static int make_workspace(const si_shape_t *s, int max_tokens, int max_pos,
     uint8_t *ws = nullptr;
     TRY(m.alloc(&ws, W->attn_ws_bytes));
     W->attn_ws = ws;
+    TRY(m.alloc(&W->scores, (size_t)s->qheads * max_pos));
     // GEMM split-K partials: the largest need over the layer's projections
     // and every row count up to max_tokens (the split depends on both)
     {
@@ -486,6 +505,7 @@ struct si_layer {
     size_t attn_ws_bytes = 0;
     void *gemm_ws = nullptr;
     size_t gemm_ws_bytes = 0;
+    float *scores = nullptr;
     // phase timing: events[i] marks the start of phase i, events[COUNT] the end
     bool timing = false;
     hipEvent_t events[SI_PHASE_COUNT + 1] = {};
@@ -593,6 +613,7 @@ static int build_layer(const si_layer_host_t *w, std::shared_ptr<Workspace> W,
     L->attn_ws_bytes = W->attn_ws_bytes;
     L->gemm_ws = W->gemm_ws;
     L->gemm_ws_bytes = W->gemm_ws_bytes;
+    L->scores = W->scores;
     L->ws = std::move(W);
     *out = L.release();
     return SI_OK;
@@ -714,6 +735,8 @@ static void project(si_layer *L, const Q4Dev &w, int rows, const Q8Buf &x, const
                          (flags & SI_LAYER_EXACT) != 0, L->gemm_ws, L->gemm_ws_bytes, st);
 }
 
+static int run_decode_ffn(si_layer *L, float *out, bool exact, hipStream_t st);
+
 // Single-token decode: five fused kernels (si_decode.hip).
 static int run_decode(si_layer *L, const float *x, uint16_t *kc, uint16_t *vc, int ctx,
                       float *out, int flags, hipStream_t st) {
@@ -728,6 +751,26 @@ static int run_decode(si_layer *L, const float *x, uint16_t *kc, uint16_t *vc, i
     launch_dec_qkv(x, L->norm, H, s.rms_eps, L->wqkv.qs, L->wqkv.d, L->wqkv.tile, NQKV, L->bqkv,
                    L->normed,
                    L->xq.qs, L->xq.d, L->xq.s, L->qkv, exact, st);
+    if (flags & SI_LAYER_ATTN_STANDARD) {
+        // the reference's staged order with attention_standard
+        // (qwen_one_layer.c:260-275, attention_kernels.h:33-78)
+        mark(L, SI_PHASE_ROPE_KV, st);
+        launch_rope_kv(L->qkv, NQKV, 1, s.qheads, s.kvheads, s.hdim, ctx - 1, 1, ctx, nullptr,
+                       L->rope_cos, L->rope_sin, L->q, kc, vc, 0, st);
+        mark(L, SI_PHASE_ATTENTION_Q8, st);
+        launch_attn_standard(L->q, s.qheads, s.kvheads, s.hdim, kc, vc, ctx, L->attn, L->scores,
+                             st);
+        launch_quantize_q8_rows(L->attn, 1, QD, L->attq.qs, L->attq.d, L->attq.s, st);
+        mark(L, SI_PHASE_OUT_PROJ, st);
+        launch_matvec(L->attq.qs, L->attq.d, L->attq.s, QD, L->wo.qs, L->wo.d, L->wo.tile, H,
+                      nullptr, full ? x : nullptr, full ? L->h : out, exact, st,
+                      full ? L->attn_out : nullptr);
+        if (!full) {
+            mark(L, SI_PHASE_COUNT, st);
+            return check_launch("layer decode (standard attention sublayer)");
+        }
+        return run_decode_ffn(L, out, exact, st);
+    }
     // :260-270: RoPE, fp16 K/V append at context-1, attention over the cache
     mark(L, SI_PHASE_ATTENTION_Q8, st);
     const int ns = dec_attn_chunks(s.qheads, s.kvheads, s.hdim, 1, ctx);
@@ -756,7 +799,14 @@ static int run_decode(si_layer *L, const float *x, uint16_t *kc, uint16_t *vc, i
         mark(L, SI_PHASE_COUNT, st);
         return check_launch("layer decode (attention sublayer)");
     }
-    // FFN half: RMSNorm(h) -> Q8 -> gate|up -> SwiGLU -> Q8 -> down + h
+    return run_decode_ffn(L, out, exact, st);
+}
+
+// FFN half of the decode layer: RMSNorm(h) -> Q8 -> gate|up -> SwiGLU -> Q8
+// -> down + h
+static int run_decode_ffn(si_layer *L, float *out, bool exact, hipStream_t st) {
+    const si_shape_t &s = L->s;
+    const int H = s.hidden;
     mark(L, SI_PHASE_GATE_UP, st);
     launch_dec_gateup(L->h, L->post_norm, H, s.rms_eps, L->wgu.qs, L->wgu.d, L->wgu.tile, s.ffn,
                       L->normed2,
@@ -867,6 +917,11 @@ extern "C" {
 int si_layer_decode(si_layer_t *L, const float *x, uint16_t *kc, uint16_t *vc, int context,
                     float *out, int flags, void *stream) {
     SI_REQUIRE(L && x && kc && vc && out, "layer_decode: NULL pointer");
+    SI_REQUIRE((flags & ~(SI_LAYER_ATTN_ONLY | SI_LAYER_EXACT | SI_LAYER_ATTN_STANDARD)) == 0,
+               "layer_decode: unknown flags %d", flags);
+    SI_REQUIRE(!(flags & SI_LAYER_ATTN_STANDARD) ||
+                   ((uintptr_t)kc % 16 == 0 && (uintptr_t)vc % 16 == 0),
+               "layer_decode: standard attention needs 16-byte aligned kc and vc");
     // qwen_one_layer.c:608: context 1..32768 (here bounded by the RoPE table)
     SI_REQUIRE(context >= 1 && context <= L->max_pos, "context %d outside 1..%d", context,
                L->max_pos);
@@ -877,6 +932,9 @@ int si_layer_decode_batch(si_layer_t *L, const float *x, int nseq, uint16_t *kc,
                           size_t kv_seq_stride, const int *ctx_dev, int context, int max_ctx,
                           float *out, int flags, void *stream) {
     SI_REQUIRE(L && x && kc && vc && out, "layer_decode_batch: NULL pointer");
+    SI_REQUIRE((flags & ~(SI_LAYER_ATTN_ONLY | SI_LAYER_EXACT)) == 0,
+               "layer_decode_batch: unsupported flags %d (standard attention is "
+               "single-token decode only)", flags);
     SI_REQUIRE(nseq >= 1 && nseq <= L->max_tokens, "nseq %d outside 1..%d", nseq, L->max_tokens);
     SI_REQUIRE(max_ctx >= 1 && max_ctx <= L->max_pos, "max_ctx %d outside 1..%d", max_ctx,
                L->max_pos);
@@ -892,6 +950,9 @@ int si_layer_decode_batch(si_layer_t *L, const float *x, int nseq, uint16_t *kc,
 int si_layer_prefill(si_layer_t *L, const float *x, int ntok, int prefix, uint16_t *kc,
                      uint16_t *vc, float *out, int flags, void *stream) {
     SI_REQUIRE(L && x && kc && vc && out, "layer_prefill: NULL pointer");
+    SI_REQUIRE((flags & ~(SI_LAYER_ATTN_ONLY | SI_LAYER_EXACT)) == 0,
+               "layer_prefill: unsupported flags %d (standard attention is "
+               "single-token decode only)", flags);
     // prefill_weight_stationary.h:187: 1 <= ntok, 0 <= prefix, prefix+ntok within range
     SI_REQUIRE(ntok >= 1 && ntok <= L->max_tokens, "ntok %d outside 1..%d", ntok, L->max_tokens);
     SI_REQUIRE(prefix >= 0 && prefix + ntok <= L->max_pos, "prefix+ntok exceeds %d", L->max_pos);

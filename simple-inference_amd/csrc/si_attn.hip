@@ -99,6 +99,85 @@ __global__ void k_attn_combine(int qheads, int hdim, int nsplit, const float *__
     }
 }
 
+// Block-wide max or sum of one value per thread (blockDim.x a multiple of
+// 64, at most 1024): wave reduction, then the wave results in wave order.
+__device__ __forceinline__ float block_reduce_1024(float v, float *red, bool is_max) {
+    // wave reduction, then the 16 wave results in a fixed order
+    for (int off = 32; off > 0; off >>= 1) {
+        const float o = __shfl_xor(v, off, 64);
+        v = is_max ? fmaxf(v, o) : v + o;
+    }
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();  // red[] may still be read from the previous reduction
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = is_max ? fmaxf(r, red[w]) : r + red[w];
+    return r;
+}
+
+// k_attn_combine for many partials (>= 32 per head): grid (qheads, nq),
+// block P*hdim, P = 1024/hdim.  The max is taken block-wide; thread
+// (group, column) merges the partials s = group, group + P, ... and the P
+// group sums are added in group order, so the loads of P partials are in
+// flight at once instead of one after another.
+__global__ __launch_bounds__(1024) void k_attn_combine_wide(
+    int qheads, int hdim, int nsplit, const float *__restrict__ ws_m,
+    const float *__restrict__ ws_l, const float *__restrict__ ws_o, float *__restrict__ attn,
+    int8_t *__restrict__ qs, uint16_t *__restrict__ d, int16_t *__restrict__ bsum) {
+    __shared__ float red_o[1024];
+    __shared__ float red_l[32];
+    __shared__ float red_m[16];
+    const int h = blockIdx.x, qi = blockIdx.y, tid = threadIdx.x;
+    const int P = blockDim.x / hdim, grp = tid / hdim, jj = tid % hdim;
+    const size_t base = ((size_t)qi * qheads + h) * nsplit;
+    float mx = -INFINITY;
+    for (int s = tid; s < nsplit; s += blockDim.x) mx = fmaxf(mx, ws_m[base + s]);
+    mx = block_reduce_1024(mx, red_m, true);
+    float l = 0.0f, acc = 0.0f;
+#pragma unroll 4
+    for (int s = grp; s < nsplit; s += P) {
+        const float w = expf(ws_m[base + s] - mx);  // empty chunk: m = -inf -> 0
+        l = fmaf(ws_l[base + s], w, l);
+        acc = fmaf(ws_o[(base + s) * hdim + jj], w, acc);
+    }
+    red_o[tid] = acc;
+    if (jj == 0) red_l[grp] = l;
+    __syncthreads();
+    if (tid >= hdim) return;  // no barrier below
+    float a = red_o[jj], lt = red_l[0];
+    for (int g = 1; g < P; ++g) {
+        a += red_o[g * hdim + jj];
+        lt += red_l[g];
+    }
+    const float y = mx == -INFINITY ? 0.0f : a * (1.0f / lt);
+    const size_t off = (size_t)qi * qheads * hdim + (size_t)h * hdim + jj;
+    attn[off] = y;
+    if (qs) {
+        uint16_t dbits;
+        int sum;
+        const int q = quant_block_lane(y, dbits, sum);
+        qs[off] = (int8_t)q;
+        if ((jj & 31) == 0) {
+            const size_t bi = off / SI_QK;
+            d[bi] = dbits;
+            if (bsum) bsum[bi] = (int16_t)sum;
+        }
+    }
+}
+
+// Either combine kernel by partial count.
+static void combine(int qheads, int hdim, int nq, int nsplit, const float *ws_m,
+                    const float *ws_l, const float *ws_o, float *attn, int8_t *qs, uint16_t *d,
+                    int16_t *bsum, hipStream_t st) {
+    if (nsplit >= 32)
+        hipLaunchKernelGGL(k_attn_combine_wide, dim3(qheads, nq), dim3(1024 / hdim * hdim), 0, st,
+                           qheads, hdim, nsplit, ws_m, ws_l, ws_o, attn, qs, d, bsum);
+    else
+        hipLaunchKernelGGL(k_attn_combine, dim3(qheads, nq), dim3(hdim), 0, st, qheads, hdim,
+                           nsplit, ws_m, ws_l, ws_o, attn, qs, d, bsum);
+}
+
 // ===========================================================================
 // Matrix-core decode attention.
 //
@@ -628,6 +707,9 @@ void launch_attn_prefill(const float *q, int ntok, int qheads, int kvheads, int 
 int attn_nsplit(int kvheads, int nq, int max_ctx) {
     const int base = kvheads * nq;
     int ns = (512 + base - 1) / base;
+    // down to one workgroup step per chunk: the many partials this leaves
+    // for a single query go to the wide combine kernel (7B, ctx 4096, cold
+    // cache: 4-step chunks 22.9 us, 1-step 19.9 us)
     const int maxs = (max_ctx + MA_SUPER - 1) / MA_SUPER;
     if (ns > maxs) ns = maxs;
     return ns < 1 ? 1 : ns;
@@ -669,8 +751,7 @@ void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
         default: SI_ATTN_LAUNCH(128); break;
     }
 #undef SI_ATTN_LAUNCH
-    hipLaunchKernelGGL(k_attn_combine, dim3(qheads, nq), dim3(hdim), 0, st, qheads, hdim, ns4,
-                       ws_m, ws_l, ws_o, attn, qs, d, bsum);
+    combine(qheads, hdim, nq, ns4, ws_m, ws_l, ws_o, attn, qs, d, bsum, st);
 }
 
 // Merge of nsplit partials laid out as [nq][qheads][nsplit] (m, l) and
@@ -680,8 +761,7 @@ void launch_attn_combine(int nq, int qheads, int hdim, int nsplit, const void *w
     const float *ws_m = (const float *)workspace;
     const float *ws_l = ws_m + (size_t)nq * qheads * nsplit;
     const float *ws_o = ws_l + (size_t)nq * qheads * nsplit;
-    hipLaunchKernelGGL(k_attn_combine, dim3(qheads, nq), dim3(hdim), 0, st, qheads, hdim, nsplit,
-                       ws_m, ws_l, ws_o, attn, qs, d, bsum);
+    combine(qheads, hdim, nq, nsplit, ws_m, ws_l, ws_o, attn, qs, d, bsum, st);
 }
 
 // Test entry: one 16x16 tile with each of the two f16 matrix-core shapes,
@@ -708,6 +788,139 @@ __global__ void k_debug_mfma_f16(const _Float16 *A, const _Float16 *B, float *D3
 void launch_debug_mfma_f16(const void *A, const void *B, float *D32, float *D16, hipStream_t st) {
     hipLaunchKernelGGL(k_debug_mfma_f16, dim3(1), dim3(64), 0, st, (const _Float16 *)A,
                        (const _Float16 *)B, D32, D16);
+}
+
+// ---------------------------------------------------------------------------
+// Textbook attention in three stages (attention_standard,
+// attention_kernels.h:33-78): the fp32 scores of every (head, position) are
+// materialized in a [qheads][context] buffer, normalised in place, then
+// weighted into V.  It is the comparison mode of the decode layer; the
+// streaming kernels above are the fast path.
+
+// Stage 1, grid (ceil(ctx/64), kvheads), block 256: a workgroup stages the
+// K rows of 64 positions of one KV group in LDS (coalesced 16-byte loads,
+// each K byte read once per group) and computes the scores of all the
+// group's query heads for them: thread (slot, r) owns position t0 + r and
+// heads slot, slot + 4, ...  Each dot product is summed in head-dimension
+// order with separate multiply and add (the reference's loop under
+// -ffp-contract=off), then scaled by 1/sqrt(hdim): the scores match the
+// reference's bits.
+template <int D>
+__global__ __launch_bounds__(256) void k_std_scores(const float *__restrict__ q,
+                                                    const uint16_t *__restrict__ kc, int qheads,
+                                                    int kvheads, int ctx, float inv,
+                                                    float *__restrict__ scores) {
+    __shared__ float ks[64][D + 1];  // +1: the dot loop's column reads hit distinct banks
+    __shared__ float qsh[ATT_MAXPER][D];
+    constexpr int CPR = D / 8;  // 16-byte chunks per K row
+    const int g = blockIdx.y, G = qheads / kvheads, t0 = blockIdx.x * 64, tid = threadIdx.x;
+    for (int i = tid; i < G * D; i += 256) qsh[i / D][i % D] = q[(size_t)g * G * D + i];
+    for (int i = tid; i < 64 * CPR; i += 256) {
+        const int r = i / CPR, c = i % CPR;
+        const int t = min(t0 + r, ctx - 1);  // rows past the context are loaded, never used
+        const uint4 u = *(const uint4 *)(kc + ((size_t)t * kvheads + g) * D + c * 8);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ks[r][c * 8 + e] = h2f((uint16_t)(w[e >> 1] >> (16 * (e & 1))));
+    }
+    __syncthreads();
+    const int r = tid & 63, slot = tid >> 6, t = t0 + r;
+    if (t >= ctx) return;
+    for (int j = slot; j < G; j += 4) {
+        float dot = 0.0f;
+#pragma unroll 16
+        for (int d = 0; d < D; ++d) dot = __fadd_rn(dot, __fmul_rn(qsh[j][d], ks[r][d]));
+        scores[(size_t)(g * G + j) * ctx + t] = __fmul_rn(dot, inv);
+    }
+}
+
+// Stage 2, grid qheads, block 1024: max, exp(s - max) written in place with
+// their sum, then multiplied by 1/sum (attention_kernels.h:50-62).
+__global__ __launch_bounds__(1024) void k_std_softmax(float *__restrict__ scores, int ctx) {
+    __shared__ float red[16];
+    float *row = scores + (size_t)blockIdx.x * ctx;
+    float m = -INFINITY;
+    for (int t = threadIdx.x; t < ctx; t += 1024) m = fmaxf(m, row[t]);
+    m = block_reduce_1024(m, red, true);
+    float sum = 0.0f;
+    for (int t = threadIdx.x; t < ctx; t += 1024) {
+        const float e = expf(row[t] - m);
+        row[t] = e;
+        sum += e;
+    }
+    const float inv = 1.0f / block_reduce_1024(sum, red, false);
+    for (int t = threadIdx.x; t < ctx; t += 1024) row[t] *= inv;
+}
+
+// Stage 3, grid (hdim/8, qheads), block 1024: workgroup c owns the 8
+// output columns 8c..8c+7 of one head (one 16-byte V load per position);
+// thread i sums p[t] v[t] over t = i, i + 1024, ... (four loads in flight),
+// then the 1024 partial sums are added by a fixed tree
+// (attention_kernels.h:64-77 up to the summation order).  The normalised
+// scores stay in place.
+__global__ __launch_bounds__(1024) void k_std_pv(const float *__restrict__ scores,
+                                                 const uint16_t *__restrict__ vc, int qheads,
+                                                 int kvheads, int hdim, int ctx,
+                                                 float *__restrict__ out) {
+    __shared__ float red[8][1024];
+    const int c = blockIdx.x, h = blockIdx.y, g = h / (qheads / kvheads), tid = threadIdx.x;
+    const float *p = scores + (size_t)h * ctx;
+    const size_t rstride = (size_t)kvheads * hdim / 8;  // uint4 per cache row
+    const uint4 *v = (const uint4 *)vc + (size_t)g * (hdim / 8) + c;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    auto add = [&](const uint4 u, float pt) {
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            acc[e] = __fadd_rn(acc[e], __fmul_rn(pt, h2f((uint16_t)(w[e >> 1] >> (16 * (e & 1))))));
+    };
+    int t = tid;
+    for (; t + 3 * 1024 < ctx; t += 4 * 1024) {
+        uint4 u[4];
+        float pt[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            u[k] = v[(size_t)(t + k * 1024) * rstride];
+            pt[k] = p[t + k * 1024];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) add(u[k], pt[k]);
+    }
+    for (; t < ctx; t += 1024) add(v[(size_t)t * rstride], p[t]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[e][tid] = acc[e];
+    __syncthreads();
+    for (int st = 512; st > 0; st >>= 1) {
+        if (tid < st)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) red[e][tid] += red[e][tid + st];
+        __syncthreads();
+    }
+    if (tid < 8) out[(size_t)h * hdim + c * 8 + tid] = red[tid][0];
+}
+
+bool attn_standard_supported(int qheads, int kvheads, int hdim) {
+    return kvheads >= 1 && qheads % kvheads == 0 && qheads / kvheads <= ATT_MAXPER &&
+           (hdim == 32 || hdim == 64 || hdim == 96 || hdim == 128);
+}
+
+void launch_attn_standard(const float *q, int qheads, int kvheads, int hdim, const uint16_t *kc,
+                          const uint16_t *vc, int ctx, float *out, float *scores,
+                          hipStream_t st) {
+    const float inv = 1.0f / sqrtf((float)hdim);
+    if (ctx > 0) {
+        const dim3 grid((ctx + 63) / 64, kvheads);
+        switch (hdim) {  // the head dimensions check_shape admits
+        case 32: hipLaunchKernelGGL(k_std_scores<32>, grid, dim3(256), 0, st, q, kc, qheads, kvheads, ctx, inv, scores); break;
+        case 64: hipLaunchKernelGGL(k_std_scores<64>, grid, dim3(256), 0, st, q, kc, qheads, kvheads, ctx, inv, scores); break;
+        case 96: hipLaunchKernelGGL(k_std_scores<96>, grid, dim3(256), 0, st, q, kc, qheads, kvheads, ctx, inv, scores); break;
+        default: hipLaunchKernelGGL(k_std_scores<128>, grid, dim3(256), 0, st, q, kc, qheads, kvheads, ctx, inv, scores); break;
+        }
+        hipLaunchKernelGGL(k_std_softmax, dim3(qheads), dim3(1024), 0, st, scores, ctx);
+    }
+    // context 0 leaves the output zero (attention_kernels.h:70)
+    hipLaunchKernelGGL(k_std_pv, dim3(hdim / 8, qheads), dim3(1024), 0, st, scores, vc, qheads,
+                       kvheads, hdim, ctx, out);
 }
 
 }  // namespace si

@@ -57,6 +57,10 @@ int attn_nsplit(int kvheads, int nq, int max_ctx);
 size_t attn_workspace_bytes(int qheads, int hdim, int kvheads, int nq, int max_ctx);
 bool attn_supported(int qheads, int kvheads, int hdim);
 void launch_debug_mfma_f16(const void *A, const void *B, float *D32, float *D16, hipStream_t st);
+// three-stage textbook attention for one query (scores: [qheads][ctx] fp32)
+bool attn_standard_supported(int qheads, int kvheads, int hdim);
+void launch_attn_standard(const float *q, int qheads, int kvheads, int hdim, const uint16_t *kc,
+                          const uint16_t *vc, int ctx, float *out, float *scores, hipStream_t st);
 void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
                       const uint16_t *kc, const uint16_t *vc, size_t kv_seq_stride,
                       const int *ctx_dev, int ctx0, int ctx_step, int max_ctx, float *attn,

@@ -162,9 +162,12 @@ static phase_t decode(const si_model_t *l, const float *x, uint16_t *kc, uint16_
 phase_t run_layer(const si_model_t *l, const float *x, uint16_t *kc, uint16_t *vc, int context,
                   float *output, attention_method_t method, float *scores, float *attn_copy,
                   block_q8_0 *q8_copy) {
+    /* the standard method materializes its scores in the layer's own
+     * [qheads][max_pos] device buffer; the caller's scores are not needed */
     (void)scores;
     if (method != ATTENTION_STANDARD && method != ATTENTION_FLASH) die("Unknown attention method");
-    return decode(l, x, kc, vc, context, output, SI_LAYER_ATTN_ONLY, attn_copy, q8_copy);
+    const int flags = SI_LAYER_ATTN_ONLY | (method == ATTENTION_STANDARD ? SI_LAYER_ATTN_STANDARD : 0);
+    return decode(l, x, kc, vc, context, output, flags, attn_copy, q8_copy);
 }
 
 fused_stats_t run_layer_fused(const si_model_t *l, const float *x, uint16_t *kc, uint16_t *vc,
@@ -209,9 +212,16 @@ void attention_flash(const si_model_t *l, const float *q, const uint16_t *kc, co
 void attention_compute(const si_model_t *l, attention_method_t method, const float *q,
                        const uint16_t *kc, const uint16_t *vc, int context, float *out,
                        float *score_workspace) {
-    (void)score_workspace;
     if (method != ATTENTION_STANDARD && method != ATTENTION_FLASH) die("Unknown attention method");
-    attention_flash(l, q, kc, vc, context, out);
+    if (method == ATTENTION_FLASH) {
+        attention_flash(l, q, kc, vc, context, out);
+        return;
+    }
+    /* attention_kernels.h:33-78; score_workspace: device [qheads][context] */
+    if (context < 0) context = 0;
+    if (context > 0 && !score_workspace) die("Standard attention needs a score workspace");
+    check(si_attention_standard(&l->shape, q, kc, vc, context, out, score_workspace, l->stream),
+          "si_attention_standard");
 }
 
 void quantize_q8(const float *src, block_q8_0 *dst, int count) {

@@ -22,7 +22,7 @@ QK = 32
 Q8_DTYPE = np.dtype([("d", "<u2"), ("qs", "i1", (QK,))])  # defines.h:27-28
 
 SI_OK, SI_ERR_ARG, SI_ERR_HIP, SI_ERR_STATE, SI_ERR_NOMEM = range(5)
-SI_LAYER_FULL, SI_LAYER_ATTN_ONLY, SI_LAYER_EXACT = 0, 1, 2
+SI_LAYER_FULL, SI_LAYER_ATTN_ONLY, SI_LAYER_EXACT, SI_LAYER_ATTN_STANDARD = 0, 1, 2, 4
 SI_GEMM_EXACT = 1
 BUFFERS = ["NORMED", "XQ_QS", "XQ_D", "XQ_S", "QKV", "Q", "ATTN", "ATTQ_QS", "ATTQ_D",
            "ATTQ_S", "ATTN_OUT", "H", "NORMED2", "XQ2_QS", "XQ2_D", "XQ2_S", "GU", "ACT",
@@ -89,6 +89,7 @@ _SIGS = {
     "si_attention": (_I, [ctypes.POINTER(Shape), _P, _I, _P, _P, _Z, _P, _I, _I, _I, _P, _P,
                           _P, _P, _P, _Z, _P]),
     "si_attention_workspace": (_Z, [ctypes.POINTER(Shape), _I, _I]),
+    "si_attention_standard": (_I, [ctypes.POINTER(Shape), _P, _P, _P, _I, _P, _P, _P]),
     "si_swiglu_q8": (_I, [_P, _I, _I, _P, _P, _P, _P, _P]),
     "si_debug_mfma_f16": (_I, [_P, _P, _P, _P, _P]),
     "si_debug_lane_ops": (_I, [_P, _P]),

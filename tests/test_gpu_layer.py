@@ -315,17 +315,35 @@ def test_host_mirror_run_layer(oracle):
     lh = si_amd.LayerHost(**{k: v.ctypes.data for k, v in keep.items()})
     m = H.si_model_from_host(ctypes.byref(s), ctypes.byref(lh), 1, 64)
     ctx = 17
-    kc = dev(g[f"layer_kc_{ctx}"].view(np.int16))
-    vc = dev(g[f"layer_vc_{ctx}"].view(np.int16))
-    out = empty(s.hidden, torch.float32)
-    attn = np.zeros(s.qheads * s.hdim, np.float32)
-    q8 = np.zeros(s.qheads * s.hdim // 32, Q8_DTYPE)
     x = dev(g["layer_x"])
-    ph = H.run_layer(m, si_amd.ptr(x), si_amd.ptr(kc), si_amd.ptr(vc), ctx, si_amd.ptr(out), 1,
-                     None, attn.ctypes.data, q8.ctypes.data)
-    close(host(out), g[f"layer_out_{ctx}"], 1e-3, "mirror Y")
-    close(attn, g[f"layer_attn_{ctx}"], 2e-3, "mirror attention capture")
-    # the captured Q8 is the quantization of the captured attention, bit-exact
-    assert oracle.quantize_q8(attn).tobytes() == q8.tobytes()
-    assert ph.q_proj > 0 and ph.attention > 0 and ph.out_proj > 0
+    for method in (1, 0):  # ATTENTION_FLASH, ATTENTION_STANDARD
+        kc = dev(g[f"layer_kc_{ctx}"].view(np.int16))
+        vc = dev(g[f"layer_vc_{ctx}"].view(np.int16))
+        out = empty(s.hidden, torch.float32)
+        attn = np.zeros(s.qheads * s.hdim, np.float32)
+        q8 = np.zeros(s.qheads * s.hdim // 32, Q8_DTYPE)
+        ph = H.run_layer(m, si_amd.ptr(x), si_amd.ptr(kc), si_amd.ptr(vc), ctx,
+                         si_amd.ptr(out), method, None, attn.ctypes.data, q8.ctypes.data)
+        close(host(out), g[f"layer_out_{ctx}"], 1e-3, f"mirror Y ({method})")
+        close(attn, g[f"layer_attn_{ctx}"], 2e-3, f"mirror attention capture ({method})")
+        # the captured Q8 is the quantization of the captured attention, bit-exact
+        assert oracle.quantize_q8(attn).tobytes() == q8.tobytes()
+        assert ph.q_proj > 0 and ph.attention > 0 and ph.out_proj > 0
+        # the staged standard order times RoPE + K/V append on its own
+        assert (ph.rope_cache > 0) == (method == 0)
+    # attention_compute with both methods on the same q and cache
+    H.attention_compute.argtypes = [ctypes.POINTER(Model), ctypes.c_int] + \
+        [ctypes.c_void_p] * 3 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal(s.qheads * s.hdim).astype(np.float32)
+    kh, vh = g[f"layer_kc_{ctx}"], g[f"layer_vc_{ctx}"]
+    scores = empty(s.qheads * ctx, torch.float32)
+    want = oracle.attention_standard(os_, q, kh, vh, ctx)
+    qd, kd, vd = dev(q), dev(kh.view(np.int16)), dev(vh.view(np.int16))
+    for method in (0, 1):
+        o = empty(s.qheads * s.hdim, torch.float32)
+        H.attention_compute(m, method, si_amd.ptr(qd), si_amd.ptr(kd), si_amd.ptr(vd), ctx,
+                            si_amd.ptr(o), si_amd.ptr(scores))
+        torch.cuda.synchronize()
+        close(host(o), want, 2e-3, f"attention_compute({method})")
     H.free_layer(m)

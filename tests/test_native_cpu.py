@@ -76,6 +76,14 @@ def test_argument_errors_do_not_launch():
     s = si_amd.make_shape(**si_amd.SHAPES["0.5b"])
     assert L.si_attention(ctypes.byref(s), None, 1, None, None, 0, None, 0, 0, 16, None, None,
                           None, None, None, 0, None) == si_amd.SI_ERR_ARG
+    assert L.si_attention_standard(ctypes.byref(s), None, None, None, -1, None, None,
+                                   None) == si_amd.SI_ERR_ARG
+    assert b"negative context" in L.si_last_error()
+    assert L.si_attention_standard(ctypes.byref(s), None, None, None, 4, ctypes.c_void_p(256),
+                                   None, None) == si_amd.SI_ERR_ARG
+    assert b"NULL" in L.si_last_error()
+    assert L.si_attention_standard(ctypes.byref(bad), None, None, None, 0, None, None,
+                                   None) == si_amd.SI_ERR_ARG
     h = ctypes.c_void_p()
     host = si_amd.LayerHost()
     assert L.si_layer_create(ctypes.byref(s), ctypes.byref(host), 1, 16,
