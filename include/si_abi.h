@@ -289,6 +289,34 @@ int si_layer_decode_batch(si_layer_t *l, const float *x, int nseq, uint16_t *kc,
                           int context, int max_ctx, float *out, int flags,
                           void *stream);
 
+/* Paged KV cache (no counterpart in the reference, which keeps one
+ * contiguous [ctx][kvheads][hdim] cache per layer, qwen_one_layer.c:262-266;
+ * this is the step after a single layer: many sequences of unequal length
+ * sharing one pool).  A pool holds npages pages of page_size (a power of
+ * two) fp16 rows of kvheads*hdim values, K and V in separate pools.
+ * pages (device int [nseq][max_pages]) maps sequence i's position p to pool
+ * row pages[i*max_pages + p/page_size]*page_size + p%page_size; page ids
+ * outside [0, npages) are clamped (they cannot address outside the pool).
+ * The pool bytes are npages*page_size*kvheads*hdim*2 each.
+ *
+ * si_layer_decode_batch over a paged cache: sequence i's new token sits at
+ * position ctx_dev[i]-1 (NULL = all context); its K/V row is appended
+ * through the table, then attention reads the sequence's rows through it.
+ * Prefill and single-token decode keep contiguous caches. */
+int si_layer_decode_paged(si_layer_t *l, const float *x, int nseq, uint16_t *k_pool,
+                          uint16_t *v_pool, int npages, int page_size, const int *pages,
+                          int max_pages, const int *ctx_dev, int context, int max_ctx,
+                          float *out, int flags, void *stream);
+
+/* si_attention for nq decode queries over a paged cache (ctx_dev required):
+ * the same kernels as the contiguous form, so the result is bit-identical to
+ * si_attention on the same rows laid out contiguously. */
+int si_attention_paged(const si_shape_t *s, const float *q, int nq, const uint16_t *k_pool,
+                       const uint16_t *v_pool, int npages, int page_size, const int *pages,
+                       int max_pages, const int *ctx_dev, int max_ctx, float *attn, int8_t *qs,
+                       uint16_t *d, int16_t *bsum, void *workspace, size_t workspace_bytes,
+                       void *stream);
+
 /* pf_run_batch (prefill_weight_stationary.h:183-311): causal prefill of
  * ntok tokens after prefix cached positions.  Appends K/V rows
  * prefix..prefix+ntok-1; token t attends with context prefix+t+1. */

@@ -113,6 +113,53 @@ void attention_compute(const si_model_t *l, attention_method_t method, const flo
 /* qwen_one_layer.c:98-116 on device buffers (dst: block_q8_0 records). */
 void quantize_q8(const float *src, block_q8_0 *dst, int count);
 
+/* ------------------------------------------------------------------ */
+/* Paged KV bookkeeping and a multi-layer decode stack (si_kvpages.c). */
+/* No counterpart in the reference (one layer, one contiguous cache,   */
+/* qwen_one_layer.c:237-281): the step after a single layer.           */
+/* ------------------------------------------------------------------ */
+
+/* A pool of npages pages of page_size positions (a power of two) and the
+ * page lists of up to max_seqs sequences of up to max_pages pages each.
+ * Free pages are handed out lowest id first and reused after
+ * si_kv_seq_free.  Misuse (unknown sequence, shrinking) dies. */
+typedef struct si_kv_pages si_kv_pages_t;
+si_kv_pages_t *si_kv_pages_create(int npages, int page_size, int max_seqs, int max_pages);
+void si_kv_pages_destroy(si_kv_pages_t *p);
+/* a new empty sequence: its id, or -1 when every slot is taken */
+int si_kv_seq_add(si_kv_pages_t *p);
+/* pages for len positions: 0, or -1 (nothing taken) when the pool or the
+ * sequence's max_pages cannot hold them */
+int si_kv_seq_grow(si_kv_pages_t *p, int seq, int len);
+void si_kv_seq_free(si_kv_pages_t *p, int seq);
+int si_kv_seq_len(const si_kv_pages_t *p, int seq);
+int si_kv_pages_free(const si_kv_pages_t *p);
+/* host [max_seqs][max_pages] page ids by sequence id (unused entries 0) */
+const int *si_kv_page_table(const si_kv_pages_t *p);
+
+/* nlayers full layers (or attention sublayers with ffn 0) sharing one
+ * workspace, each with its own K and V page pool (npages pages of
+ * page_size rows), one page table for all of them. */
+typedef struct si_stack si_stack_t;
+si_stack_t *si_stack_create(const si_shape_t *s, const si_layer_host_t *layers, int nlayers,
+                            int max_seqs, int max_ctx, int npages, int page_size);
+void si_stack_destroy(si_stack_t *st);
+si_kv_pages_t *si_stack_pages(si_stack_t *st);
+uint16_t *si_stack_k_pool(si_stack_t *st, int layer);
+uint16_t *si_stack_v_pool(si_stack_t *st, int layer);
+si_layer_t *si_stack_layer(si_stack_t *st, int layer);
+const int *si_stack_dev_table(const si_stack_t *st);
+const int *si_stack_dev_ctx(const si_stack_t *st);
+/* Grows each of the nseq distinct sequences seqs[] by one position (the
+ * token about to be decoded) and uploads their page lists and contexts in
+ * batch order (synchronous copies).  -1 when the pool is exhausted (the
+ * lengths are left as before; pages already taken stay with their
+ * sequences), else 0. */
+int si_stack_prepare(si_stack_t *st, const int *seqs, int nseq);
+/* x [nseq][hidden] (device) through every layer -> out [nseq][hidden]: the
+ * residual stream of a decode step; kernel launches only (capturable). */
+void si_stack_decode(si_stack_t *st, const float *x, float *out, int flags, void *stream);
+
 /* Offline weight preparation (host memory): ggml's Q4_0 rule, the format
  * extract_weights.py copies from GGUF.  Per 32 values: d = m/-8 for the
  * signed value m of largest magnitude, nibble = min(15, trunc(x/d + 8.5)). */

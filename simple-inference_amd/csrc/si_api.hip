@@ -826,7 +826,8 @@ static int run_decode_ffn(si_layer *L, float *out, bool exact, hipStream_t st) {
 // sequence), ctx_step 1 causal prefill.
 static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_t *vc,
                     size_t kv_seq_stride, int pos0, const int *ctx_dev, int ctx0, int ctx_step,
-                    int max_ctx, float *out, int flags, hipStream_t st) {
+                    int max_ctx, float *out, int flags, hipStream_t st,
+                    KvPages pg = KvPages()) {
     const int pos_step = ctx_step;  // positions advance with the contexts
     const si_shape_t &s = L->s;
     const int H = s.hidden, QD = s.qheads * s.hdim, NQKV = QD + 2 * s.kvheads * s.hdim;
@@ -840,7 +841,16 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
     // :253-258: Q, K, V projections (+bias), fused into one N = qd + 2 kvd matrix
     mark(L, SI_PHASE_QKV, st);
     project(L, L->wqkv, rows, L->xq, L->bqkv, nullptr, L->qkv, flags, st);
-    if (ctx_step == 0) {
+    if (ctx_step == 0 && pg.pages) {
+        // batched decode over a paged cache: RoPE + K/V append through the
+        // page table, then the split-context attention reading through it
+        mark(L, SI_PHASE_ROPE_KV, st);
+        launch_rope_kv(L->qkv, NQKV, rows, s.qheads, s.kvheads, s.hdim, pos0, 0, max_ctx, ctx_dev,
+                       L->rope_cos, L->rope_sin, L->q, kc, vc, 0, st, pg);
+        mark(L, SI_PHASE_ATTENTION_Q8, st);
+        launch_attention(L->q, rows, s.qheads, s.kvheads, s.hdim, kc, vc, 0, ctx_dev, ctx0, 0,
+                         max_ctx, L->attn, L->attq.qs, L->attq.d, L->attq.s, L->attn_ws, st, pg);
+    } else if (ctx_step == 0) {
         // batched decode: RoPE + K/V append inside the attention kernel
         mark(L, SI_PHASE_ATTENTION_Q8, st);
         const int ns = dec_attn_chunks(s.qheads, s.kvheads, s.hdim, rows, max_ctx);
@@ -945,6 +955,61 @@ int si_layer_decode_batch(si_layer_t *L, const float *x, int nseq, uint16_t *kc,
                "kv_seq_stride must hold max_ctx rows and be a multiple of 8");
     return run_rows(L, x, nseq, kc, vc, kv_seq_stride, context - 1, ctx_dev, context, 0, max_ctx,
                     out, flags, S(stream));
+}
+
+int si_layer_decode_paged(si_layer_t *L, const float *x, int nseq, uint16_t *k_pool,
+                          uint16_t *v_pool, int npages, int page_size, const int *pages,
+                          int max_pages, const int *ctx_dev, int context, int max_ctx, float *out,
+                          int flags, void *stream) {
+    SI_REQUIRE(L && x && k_pool && v_pool && pages && out, "layer_decode_paged: NULL pointer");
+    SI_REQUIRE((flags & ~(SI_LAYER_ATTN_ONLY | SI_LAYER_EXACT)) == 0,
+               "layer_decode_paged: unsupported flags %d (standard attention is "
+               "single-token decode only)", flags);
+    SI_REQUIRE(nseq >= 1 && nseq <= L->max_tokens, "nseq %d outside 1..%d", nseq, L->max_tokens);
+    SI_REQUIRE(page_size >= 1 && page_size <= (1 << 20) && (page_size & (page_size - 1)) == 0,
+               "page_size %d must be a power of two in 1..2^20", page_size);
+    SI_REQUIRE(npages >= 1 && max_pages >= 1, "npages and max_pages must be >= 1");
+    SI_REQUIRE(max_ctx >= 1 && max_ctx <= L->max_pos, "max_ctx %d outside 1..%d", max_ctx,
+               L->max_pos);
+    SI_REQUIRE((long long)max_pages * page_size >= max_ctx,
+               "max_pages * page_size must cover max_ctx");
+    SI_REQUIRE((long long)npages * page_size * L->s.kvheads * L->s.hdim < (1LL << 40),
+               "KV pool too large");
+    SI_REQUIRE(ctx_dev || (context >= 1 && context <= max_ctx), "context %d outside 1..%d",
+               context, max_ctx);
+    KvPages pg;
+    pg.pages = pages;
+    pg.max_pages = max_pages;
+    pg.npages = npages;
+    while ((1 << pg.shift) < page_size) ++pg.shift;
+    return run_rows(L, x, nseq, k_pool, v_pool, 0, context - 1, ctx_dev, context, 0, max_ctx,
+                    out, flags, S(stream), pg);
+}
+
+int si_attention_paged(const si_shape_t *s, const float *q, int nq, const uint16_t *k_pool,
+                       const uint16_t *v_pool, int npages, int page_size, const int *pages,
+                       int max_pages, const int *ctx_dev, int max_ctx, float *attn, int8_t *qs,
+                       uint16_t *d, int16_t *bsum, void *ws, size_t ws_bytes, void *stream) {
+    int r = check_shape(s);
+    if (r) return r;
+    SI_REQUIRE(nq >= 1 && max_ctx >= 1, "attention_paged: bad nq/max_ctx");
+    SI_REQUIRE(q && k_pool && v_pool && pages && ctx_dev && attn && ws,
+               "attention_paged: NULL pointer");
+    SI_REQUIRE(page_size >= 1 && page_size <= (1 << 20) && (page_size & (page_size - 1)) == 0,
+               "page_size %d must be a power of two in 1..2^20", page_size);
+    SI_REQUIRE(npages >= 1 && max_pages >= 1 && (long long)max_pages * page_size >= max_ctx,
+               "attention_paged: pages do not cover max_ctx");
+    SI_REQUIRE(!qs || d, "attention_paged: qs without d");
+    SI_REQUIRE(ws_bytes >= si_attention_workspace(s, nq, max_ctx),
+               "attention_paged: workspace too small");
+    KvPages pg;
+    pg.pages = pages;
+    pg.max_pages = max_pages;
+    pg.npages = npages;
+    while ((1 << pg.shift) < page_size) ++pg.shift;
+    launch_attention(q, nq, s->qheads, s->kvheads, s->hdim, k_pool, v_pool, 0, ctx_dev, max_ctx,
+                     0, max_ctx, attn, qs, d, bsum, ws, S(stream), pg);
+    return check_launch("si_attention_paged");
 }
 
 int si_layer_prefill(si_layer_t *L, const float *x, int ntok, int prefix, uint16_t *kc,

@@ -20,12 +20,14 @@
 namespace si {
 
 // grid (ntok, qheads + kvheads), block hdim/2: one thread per rotation pair.
+// With a page table (pg.pages != nullptr) token t's K/V row goes to the
+// pool row of sequence t's position pos (kv_seq_stride unused).
 __global__ void k_rope_kv(const float *__restrict__ qkv, int ldqkv, int qheads, int kvheads,
                           int hdim, int pos0, int pos_step, int max_pos,
                           const int *__restrict__ ctx_dev,
                           const float *__restrict__ rc, const float *__restrict__ rs,
                           float *__restrict__ q_out, uint16_t *__restrict__ kc,
-                          uint16_t *__restrict__ vc, size_t kv_seq_stride) {
+                          uint16_t *__restrict__ vc, size_t kv_seq_stride, KvPages pg) {
     const int t = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
     const int half = hdim >> 1;
     const int pos = ctx_dev ? ctx_dev[t] - 1 : pos0 + t * pos_step;
@@ -43,7 +45,7 @@ __global__ void k_rope_kv(const float *__restrict__ qkv, int ldqkv, int qheads, 
         const float a = row[qd + g * hdim + i], b = row[qd + g * hdim + i + half];
         const float ka = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
         const float kb = __fadd_rn(__fmul_rn(b, c), __fmul_rn(a, s));
-        const size_t base = (size_t)t * kv_seq_stride + (size_t)pos * kvd + (size_t)g * hdim;
+        const size_t base = pg.row(t, pos, kv_seq_stride, kvd) + (size_t)g * hdim;
         kc[base + i] = f2h(ka);
         kc[base + i + half] = f2h(kb);
         vc[base + i] = f2h(row[qd + kvd + g * hdim + i]);
@@ -54,11 +56,11 @@ __global__ void k_rope_kv(const float *__restrict__ qkv, int ldqkv, int qheads, 
 void launch_rope_kv(const float *qkv, int ldqkv, int ntok, int qheads, int kvheads, int hdim,
                     int pos0, int pos_step, int max_pos, const int *ctx_dev, const float *rc,
                     const float *rs, float *q_out, uint16_t *kc, uint16_t *vc,
-                    size_t kv_seq_stride, hipStream_t st) {
+                    size_t kv_seq_stride, hipStream_t st, KvPages pg) {
     if (ntok <= 0) return;
     hipLaunchKernelGGL(k_rope_kv, dim3(ntok, qheads + kvheads), dim3(hdim / 2), 0, st, qkv,
                        ldqkv, qheads, kvheads, hdim, pos0, pos_step, max_pos, ctx_dev, rc, rs,
-                       q_out, kc, vc, kv_seq_stride);
+                       q_out, kc, vc, kv_seq_stride, pg);
 }
 
 constexpr int ATT_MAXPER = 16;  // query heads per KV group (the 16 MFMA columns)
@@ -217,7 +219,7 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(
     const float *__restrict__ q, int qheads, int kvheads, const uint16_t *__restrict__ kc,
     const uint16_t *__restrict__ vc, size_t kv_seq_stride, const int *__restrict__ ctx_dev,
     int ctx0, int ctx_step, int max_ctx, int chunk, float scale, float *__restrict__ ws_m,
-    float *__restrict__ ws_l, float *__restrict__ ws_o) {
+    float *__restrict__ ws_l, float *__restrict__ ws_o, KvPages pg) {
     constexpr int KS = D / 32;  // k-steps of the score MFMA
     constexpr int DT = D / 16;  // d-tiles of the PV MFMA
     constexpr int VROW = D + MA_VPAD;
@@ -233,8 +235,8 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(
     const int p0 = sp * chunk;
     const int p1 = min(ctx, p0 + chunk);
     const int kvd = kvheads * D;
-    const uint16_t *kbase = kc + (size_t)qi * kv_seq_stride + (size_t)g * D;
-    const uint16_t *vbase = vc + (size_t)qi * kv_seq_stride + (size_t)g * D;
+    const uint16_t *kbase = kc + (size_t)g * D;  // + pg.row(qi, pos, ...) per row
+    const uint16_t *vbase = vc + (size_t)g * D;
 
     // Q^T as the B operand: lane holds Q[head = col][d = 8*grp + 32*ks + 0..7]
     h8 qh[KS], ql[KS];
@@ -264,7 +266,7 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(
         for (int c = tid; c < CHUNKS; c += 256) {
             const int r = c / (D / 8), e = (c % (D / 8)) * 8;
             const int pos = min(s0 + r, p1 - 1);
-            const uint4 v8 = *(const uint4 *)(vbase + (size_t)pos * kvd + e);
+            const uint4 v8 = *(const uint4 *)(vbase + pg.row(qi, pos, kv_seq_stride, kvd) + e);
             *(uint4 *)(&v_lds[r * VROW + e]) = v8;
         }
         __syncthreads();
@@ -272,7 +274,7 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(
         if (t0 < p1) {
             // scores: A = K rows (pos = t0 + col), k-slice grp
             const int kpos = min(t0 + col, p1 - 1);
-            const uint16_t *krow = kbase + (size_t)kpos * kvd + 8 * grp;
+            const uint16_t *krow = kbase + pg.row(qi, kpos, kv_seq_stride, kvd) + 8 * grp;
             f4 sacc = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
@@ -729,7 +731,7 @@ void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
                       const uint16_t *kc, const uint16_t *vc, size_t kv_seq_stride,
                       const int *ctx_dev, int ctx0, int ctx_step, int max_ctx, float *attn,
                       int8_t *qs, uint16_t *d, int16_t *bsum, void *workspace,
-                      hipStream_t st) {
+                      hipStream_t st, KvPages pg) {
     if (nq <= 0) return;
     const int ns = attn_nsplit(kvheads, nq, max_ctx);
     int chunk = (max_ctx + ns - 1) / ns;
@@ -743,7 +745,7 @@ void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
 #define SI_ATTN_LAUNCH(DIM)                                                                  \
     hipLaunchKernelGGL(k_attn_decode_mfma<DIM>, grid, dim3(256), 0, st, q, qheads, kvheads, kc, \
                        vc, kv_seq_stride, ctx_dev, ctx0, ctx_step, max_ctx, chunk, scale, ws_m, \
-                       ws_l, ws_o)
+                       ws_l, ws_o, pg)
     switch (hdim) {
         case 32: SI_ATTN_LAUNCH(32); break;
         case 64: SI_ATTN_LAUNCH(64); break;

@@ -49,10 +49,26 @@ void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int
 size_t gemm_workspace_bytes(int m, int n, int k);
 }  // namespace si
 namespace si {
+// A paged KV cache: sequence i's position p lives in pool row
+// pages[i*max_pages + p/page_size]*page_size + p%page_size (page_size =
+// 1 << shift).  Page ids are device data, clamped to [0, npages) so a bad
+// table cannot address outside the pool.  pages == nullptr: contiguous
+// caches, sequence i at i*kv_seq_stride.
+struct KvPages {
+    const int *pages = nullptr;
+    int max_pages = 0, shift = 0, npages = 0;
+    __device__ __forceinline__ size_t row(int seq, int pos, size_t kv_seq_stride,
+                                          int kvd) const {
+        if (!pages) return (size_t)seq * kv_seq_stride + (size_t)pos * kvd;
+        int pg = pages[(size_t)seq * max_pages + min(pos >> shift, max_pages - 1)];
+        pg = min(max(pg, 0), npages - 1);
+        return (((size_t)pg << shift) | (size_t)(pos & ((1 << shift) - 1))) * kvd;
+    }
+};
 void launch_rope_kv(const float *qkv, int ldqkv, int ntok, int qheads, int kvheads, int hdim,
                     int pos0, int pos_step, int max_pos, const int *ctx_dev, const float *rc,
                     const float *rs, float *q_out, uint16_t *kc, uint16_t *vc,
-                    size_t kv_seq_stride, hipStream_t st);
+                    size_t kv_seq_stride, hipStream_t st, KvPages pg = KvPages());
 int attn_nsplit(int kvheads, int nq, int max_ctx);
 size_t attn_workspace_bytes(int qheads, int hdim, int kvheads, int nq, int max_ctx);
 bool attn_supported(int qheads, int kvheads, int hdim);
@@ -65,7 +81,7 @@ void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
                       const uint16_t *kc, const uint16_t *vc, size_t kv_seq_stride,
                       const int *ctx_dev, int ctx0, int ctx_step, int max_ctx, float *attn,
                       int8_t *qs, uint16_t *d, int16_t *bsum, void *workspace,
-                      hipStream_t st);
+                      hipStream_t st, KvPages pg = KvPages());
 bool attn_prefill_supported(int qheads, int kvheads, int hdim);
 size_t attn_prefill_workspace_bytes(int qheads, int hdim, int ntok);
 void launch_attn_prefill(const float *q, int ntok, int qheads, int kvheads, int hdim, int pos0,

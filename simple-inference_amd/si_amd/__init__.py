@@ -102,6 +102,9 @@ _SIGS = {
     "si_layer_decode": (_I, [_P, _P, _P, _P, _I, _P, _I, _P]),
     "si_layer_decode_batch": (_I, [_P, _P, _I, _P, _P, _Z, _P, _I, _I, _P, _I, _P]),
     "si_layer_prefill": (_I, [_P, _P, _I, _I, _P, _P, _P, _I, _P]),
+    "si_layer_decode_paged": (_I, [_P, _P, _I, _P, _P, _I, _I, _P, _I, _P, _I, _I, _P, _I, _P]),
+    "si_attention_paged": (_I, [ctypes.POINTER(Shape), _P, _I, _P, _P, _I, _I, _P, _I, _P, _I,
+                                _P, _P, _P, _P, _P, _Z, _P]),
     "si_layer_buffer": (_P, [_P, _I]),
     "si_layer_set_timing": (_I, [_P, _I]),
     "si_layer_phase_ms": (_I, [_P, _P]),
@@ -141,6 +144,28 @@ def host_lib():
         H = ctypes.CDLL(HOST_SO)
         H.si_quantize_q4_0_host.argtypes = [_P, _P, _I]
         H.si_quantize_q4_0_host.restype = None
+        for name, res, args in (
+                ("si_kv_pages_create", _P, [_I, _I, _I, _I]),
+                ("si_kv_pages_destroy", None, [_P]),
+                ("si_kv_seq_add", _I, [_P]),
+                ("si_kv_seq_grow", _I, [_P, _I, _I]),
+                ("si_kv_seq_free", None, [_P, _I]),
+                ("si_kv_seq_len", _I, [_P, _I]),
+                ("si_kv_pages_free", _I, [_P]),
+                ("si_kv_page_table", ctypes.POINTER(_I), [_P]),
+                ("si_stack_create", _P, [ctypes.POINTER(Shape), _P, _I, _I, _I, _I, _I]),
+                ("si_stack_destroy", None, [_P]),
+                ("si_stack_pages", _P, [_P]),
+                ("si_stack_k_pool", _P, [_P, _I]),
+                ("si_stack_v_pool", _P, [_P, _I]),
+                ("si_stack_layer", _P, [_P, _I]),
+                ("si_stack_dev_table", _P, [_P]),
+                ("si_stack_dev_ctx", _P, [_P]),
+                ("si_stack_prepare", _I, [_P, _P, _I]),
+                ("si_stack_decode", None, [_P, _P, _P, _I, _P])):
+            f = getattr(H, name)
+            f.restype = res
+            f.argtypes = args
         _host = H
     return _host
 
@@ -259,6 +284,12 @@ class Layer:
                      ctx_dev=None, flags=SI_LAYER_FULL, stream=None):
         call("si_layer_decode_batch", self.h, ptr(x), nseq, ptr(kc), ptr(vc), kv_seq_stride,
              ptr(ctx_dev), context, max_ctx, ptr(out), flags, stream_handle(stream))
+
+    def decode_paged(self, x, nseq, k_pool, v_pool, npages, page_size, pages, max_pages,
+                     ctx_dev, max_ctx, out, flags=SI_LAYER_FULL, stream=None):
+        call("si_layer_decode_paged", self.h, ptr(x), nseq, ptr(k_pool), ptr(v_pool), npages,
+             page_size, ptr(pages), max_pages, ptr(ctx_dev), max_ctx, max_ctx, ptr(out), flags,
+             stream_handle(stream))
 
     def prefill(self, x, ntok, prefix, kc, vc, out, flags=SI_LAYER_FULL, stream=None):
         call("si_layer_prefill", self.h, ptr(x), ntok, prefix, ptr(kc), ptr(vc), ptr(out),
