@@ -515,6 +515,78 @@ def bench_batched_decode(torch, si_amd, stream, steps, nseq=64, ctx=4096):
                 phases_us={k: round(v * 1e3, 2) for k, v in ph.items()})
 
 
+def bench_paged_decode(torch, si_amd, stream, steps, nseq=64, ctx=4096, page_size=64,
+                       nlayers=2):
+    """Batched decode of BASELINE config 5's shape (7B layer, 64 sequences,
+    4096 positions) with the K/V rows in a paged pool (pages shuffled, so no
+    sequence is contiguous), per layer, next to the same call on contiguous
+    caches; then a decode step of an nlayers-deep stack (libsi_host.so
+    si_stack_*: one page table for every layer, residual stream between
+    layers)."""
+    s = si_amd.make_shape(**si_amd.SHAPES["7b"])
+    tens = make_layer_tensors(si_amd, s, 7)
+    lay = si_amd.Layer(s, tens, nseq, ctx)
+    kvd = s.kvheads * s.hdim
+    max_pages = ctx // page_size
+    npages = nseq * max_pages
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    kp = torch.randn(npages * page_size * kvd, generator=gen, device="cuda").half()
+    vp = torch.randn(npages * page_size * kvd, generator=gen, device="cuda").half()
+    perm = np.random.default_rng(5).permutation(npages).astype(np.int32)
+    table = torch.from_numpy(perm.reshape(nseq, max_pages)).cuda()
+    ctx_dev = torch.full((nseq,), ctx, dtype=torch.int32, device="cuda")
+    x = torch.randn(nseq * s.hidden, generator=gen, device="cuda")
+    out = torch.empty(nseq * s.hidden, device="cuda")
+
+    def call(i):
+        lay.decode_paged(x, nseq, kp, vp, npages, page_size, table, max_pages, ctx_dev, ctx, out,
+                         stream=torch.cuda.current_stream())
+
+    with torch.cuda.stream(stream):
+        for i in range(2):
+            call(i)
+        lay.set_timing(True)
+        call(0)
+        ph = lay.phase_ms()
+        lay.set_timing(False)
+    torch.cuda.synchronize()
+    ms = graph_time_ms(torch, stream, call, steps, replays=2)
+    alg = weight_bytes(s) + nseq * 2 * ctx * kvd * 2 + small_bytes(s)
+    lay.close()
+    del kp, vp
+    torch.cuda.empty_cache()
+    res = dict(page_size=page_size, us=round(ms * 1e3, 2),
+               gbs=round(alg / (ms * 1e-3) / 1e9, 1), alg_bytes=alg,
+               phases_us={k: round(v * 1e3, 2) for k, v in ph.items()})
+    # the stack: nlayers layers, sequences filled to ctx - 1 positions, one step
+    H = si_amd.host_lib()
+    keep = [dict((k, np.ascontiguousarray(v)) for k, v in tens.items() if v is not None)
+            for _ in range(nlayers)]
+    hosts = (si_amd.LayerHost * nlayers)(
+        *[si_amd.LayerHost(**{k: v.ctypes.data for k, v in kk.items()}) for kk in keep])
+    st = H.si_stack_create(ctypes.byref(s), ctypes.cast(hosts, ctypes.c_void_p), nlayers, nseq,
+                           ctx, npages, page_size)
+    pg = H.si_stack_pages(st)
+    ids = [H.si_kv_seq_add(pg) for _ in range(nseq)]
+    for i in ids:
+        assert H.si_kv_seq_grow(pg, i, ctx - 1) == 0
+    arr = (ctypes.c_int * nseq)(*ids)
+    assert H.si_stack_prepare(st, arr, nseq) == 0
+    sh = lambda: si_amd.stream_handle(torch.cuda.current_stream())  # noqa: E731
+
+    def step(i):
+        H.si_stack_decode(st, si_amd.ptr(x), si_amd.ptr(out), si_amd.SI_LAYER_FULL, sh())
+
+    with torch.cuda.stream(stream):
+        step(0)
+    torch.cuda.synchronize()
+    ms_s = graph_time_ms(torch, stream, step, max(1, steps // 2), replays=2)
+    H.si_stack_destroy(st)
+    res.update(stack_layers=nlayers, stack_step_us=round(ms_s * 1e3, 2),
+               stack_us_per_layer=round(ms_s * 1e3 / nlayers, 2))
+    return res
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline: the oracle (C restatement of the reference's portable path)
 # ---------------------------------------------------------------------------
@@ -570,7 +642,7 @@ def main():
     ap.add_argument("--dominant-only", action="store_true",
                     help="run only the dominant-kernel leg (for rocprofv3)")
     ap.add_argument("--only", choices=["prefill-0.5b", "prefill-7b", "batched-7b", "decode-7b",
-                                       "gguf-7b", "attention-7b"],
+                                       "gguf-7b", "attention-7b", "paged-7b"],
                     help="run only this configuration and print its result (for rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -589,6 +661,8 @@ def main():
             r = bench_gguf_ingest(torch, si_amd)
         elif args.only == "attention-7b":
             r = bench_attention_modes(torch, si_amd)
+        elif args.only == "paged-7b":
+            r = bench_paged_decode(torch, si_amd, stream, 5)
         elif args.only == "decode-7b":
             r, _ = bench_decode_layer(torch, si_amd, stream, 100, 10, ctx=4096, shape_name="7b")
         elif args.only == "batched-7b":
@@ -645,6 +719,9 @@ def main():
         log("config 5: 7B batched decode 64 x 4096 ...")
         extra["cfg5_batched_decode_7b_64x4096"] = bench_batched_decode(torch, si_amd, stream, 5)
         log(f"  {extra['cfg5_batched_decode_7b_64x4096']}")
+        log("config 5 shape over a paged KV pool, and a 2-layer stack ...")
+        extra["paged_batched_decode_7b_64x4096"] = bench_paged_decode(torch, si_amd, stream, 5)
+        log(f"  {extra['paged_batched_decode_7b_64x4096']}")
     cpu = None
     if not args.no_cpu:
         log("CPU baseline (oracle, 1 core) ...")

@@ -841,27 +841,19 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
     // :253-258: Q, K, V projections (+bias), fused into one N = qd + 2 kvd matrix
     mark(L, SI_PHASE_QKV, st);
     project(L, L->wqkv, rows, L->xq, L->bqkv, nullptr, L->qkv, flags, st);
-    if (ctx_step == 0 && pg.pages) {
-        // batched decode over a paged cache: RoPE + K/V append through the
-        // page table, then the split-context attention reading through it
-        mark(L, SI_PHASE_ROPE_KV, st);
-        launch_rope_kv(L->qkv, NQKV, rows, s.qheads, s.kvheads, s.hdim, pos0, 0, max_ctx, ctx_dev,
-                       L->rope_cos, L->rope_sin, L->q, kc, vc, 0, st, pg);
-        mark(L, SI_PHASE_ATTENTION_Q8, st);
-        launch_attention(L->q, rows, s.qheads, s.kvheads, s.hdim, kc, vc, 0, ctx_dev, ctx0, 0,
-                         max_ctx, L->attn, L->attq.qs, L->attq.d, L->attq.s, L->attn_ws, st, pg);
-    } else if (ctx_step == 0) {
-        // batched decode: RoPE + K/V append inside the attention kernel
+    if (ctx_step == 0) {
+        // batched decode: RoPE + K/V append inside the attention kernel,
+        // contiguous caches or a paged pool (pg)
         mark(L, SI_PHASE_ATTENTION_Q8, st);
         const int ns = dec_attn_chunks(s.qheads, s.kvheads, s.hdim, rows, max_ctx);
         if (ns == 1) {
             launch_dec_attn(L->qkv, NQKV, rows, s.qheads, s.kvheads, s.hdim, L->rope_cos,
                             L->rope_sin, kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx, L->q, 1,
-                            L->attn_ws, L->attn, L->attq.qs, L->attq.d, L->attq.s, st);
+                            L->attn_ws, L->attn, L->attq.qs, L->attq.d, L->attq.s, st, pg);
         } else {
             launch_dec_attn(L->qkv, NQKV, rows, s.qheads, s.kvheads, s.hdim, L->rope_cos,
                             L->rope_sin, kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx, L->q, ns,
-                            L->attn_ws, nullptr, nullptr, nullptr, nullptr, st);
+                            L->attn_ws, nullptr, nullptr, nullptr, nullptr, st, pg);
             launch_attn_combine(rows, s.qheads, s.hdim, ns, L->attn_ws, L->attn, L->attq.qs,
                                 L->attq.d, L->attq.s, st);
         }

@@ -392,14 +392,14 @@ struct AttnLds {
     }
 };
 
-template <int D, int NW, bool FINAL>
+template <int D, int NW, bool FINAL, bool PAGED>
 __global__ void __launch_bounds__(NW * 64) k_dec_attn(
     const float *__restrict__ qkv, int ldqkv, int qheads, int kvheads,
     const float *__restrict__ rc, const float *__restrict__ rs, uint16_t *__restrict__ kc,
     uint16_t *__restrict__ vc, size_t kv_seq_stride, const int *__restrict__ ctx_dev, int ctx0,
     int max_ctx, int chunk, float scale, float *__restrict__ q_cap, float *__restrict__ ws_m,
     float *__restrict__ ws_l, float *__restrict__ ws_o, float *__restrict__ attn,
-    int8_t *__restrict__ aqs, uint16_t *__restrict__ ad, int16_t *__restrict__ as) {
+    int8_t *__restrict__ aqs, uint16_t *__restrict__ ad, int16_t *__restrict__ as, KvPages pg) {
     constexpr int KS = D / 32, DT = D / 16, HALF = D / 2;
     constexpr int VROW = AttnLds<D, NW>::VROW;
     constexpr int VL = DA_TILE * D / (64 * 8);  // 16-byte V pieces per lane per tile
@@ -423,10 +423,9 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
     const float *row = qkv + (size_t)qi * ldqkv;
     const float *cr = rc + (size_t)max(pnew, 0) * HALF;
     const float *sr = rs + (size_t)max(pnew, 0) * HALF;
-    const size_t sbase = (size_t)qi * kv_seq_stride;
-
-    const uint16_t *kbase = kc + sbase + (size_t)g * D;
-    const uint16_t *vbase = vc + sbase + (size_t)g * D;
+    // cache row of position p: pg.at<PAGED>(qi, p, ...) (contiguous or paged)
+    const uint16_t *kbase = kc + (size_t)g * D;
+    const uint16_t *vbase = vc + (size_t)g * D;
     _Float16 *vw = vbuf + (size_t)wave * DA_TILE * VROW;
 
     // K pieces of the lane's row (pos = t0 + col), V pieces of the tile
@@ -436,14 +435,14 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
         const int pos = max(min(t0 + col, p1 - 1), 0);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
-            kr[ks] = *(const uint4 *)(kbase + (size_t)pos * kvd + 32 * ks + 8 * grp);
+            kr[ks] = *(const uint4 *)(kbase + pg.template at<PAGED>(qi, pos, kv_seq_stride, kvd) + 32 * ks + 8 * grp);
     };
     auto load_v = [&](int t0, uint4(&vr)[VL]) {
 #pragma unroll
         for (int j = 0; j < VL; ++j) {
             const int c = lane + 64 * j;
             const int r = c / (D / 8), e = (c % (D / 8)) * 8;
-            vr[j] = *(const uint4 *)(vbase + (size_t)max(min(t0 + r, p1 - 1), 0) * kvd + e);
+            vr[j] = *(const uint4 *)(vbase + pg.template at<PAGED>(qi, max(min(t0 + r, p1 - 1), 0), kv_seq_stride, kvd) + e);
         }
     };
     // The new token's row is taken from LDS (its cache row may not be
@@ -522,8 +521,8 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
             const uint16_t vh = f2h(vraw[dd]);
             newk[dd] = kh;
             newv[dd] = vh;
-            kc[sbase + (size_t)pnew * kvd + g * D + dd] = kh;
-            vc[sbase + (size_t)pnew * kvd + g * D + dd] = vh;
+            kc[pg.template at<PAGED>(qi, pnew, kv_seq_stride, kvd) + g * D + dd] = kh;
+            vc[pg.template at<PAGED>(qi, pnew, kv_seq_stride, kvd) + g * D + dd] = vh;
         }
     }
     // Q^T as the B operand: lane holds Q[head col][d = 32*ks + 8*grp + e],
@@ -786,14 +785,14 @@ struct RowsLds {
     }
 };
 
-template <int D, int G, bool FINAL>
+template <int D, int G, bool FINAL, bool PAGED>
 __global__ void __launch_bounds__(256) k_dec_attn_rows(
     const float *__restrict__ qkv, int ldqkv, int qheads, const float *__restrict__ rc,
     const float *__restrict__ rs, uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
     size_t kv_seq_stride, const int *__restrict__ ctx_dev, int ctx0, int max_ctx, int chunk,
     float scale, float *__restrict__ q_cap, float *__restrict__ ws_m, float *__restrict__ ws_l,
     float *__restrict__ ws_o, float *__restrict__ attn, int8_t *__restrict__ aqs,
-    uint16_t *__restrict__ ad, int16_t *__restrict__ as) {
+    uint16_t *__restrict__ ad, int16_t *__restrict__ as, KvPages pg) {
     using L = RowsLds<D, G>;
     constexpr int KS = D / 32, DT = D / 16, HALF = D / 2, NWG = L::NWG, ROWS = L::ROWS;
     constexpr int RW = L::RW, KVD = G * D;
@@ -825,8 +824,7 @@ __global__ void __launch_bounds__(256) k_dec_attn_rows(
     const float *row = qkv + (size_t)qi * ldqkv;
     const float *cr = rc + (size_t)max(pnew, 0) * HALF;
     const float *sr = rs + (size_t)max(pnew, 0) * HALF;
-    const size_t sbase = (size_t)qi * kv_seq_stride;
-    const uint16_t *kbase = kc + sbase, *vbase = vc + sbase;
+    // cache row of position p: pg.at<PAGED>(qi, p, ...) (contiguous or paged)
 
     // 1. the fused q|k|v row (q of every head, then the new token's raw K
     //    and V rows) and the RoPE cos|sin row at its position, as float4
@@ -856,9 +854,9 @@ __global__ void __launch_bounds__(256) k_dec_attn_rows(
         for (int i = 0; i < PT; ++i) {
             const int c = (wave * PT + i) * 64 + lane;  // a wavefront's pieces are contiguous
             const int r = c / RP, e = (c % RP) * 8;
-            const size_t pos = (size_t)max(min(ps + r, pmax - 1), 0);
-            rk[i] = *(const uint4 *)(kbase + pos * KVD + e);
-            rvv[i] = *(const uint4 *)(vbase + pos * KVD + e);
+            const size_t ro = pg.template at<PAGED>(qi, max(min(ps + r, pmax - 1), 0), kv_seq_stride, KVD);
+            rk[i] = *(const uint4 *)(kc + ro + e);
+            rvv[i] = *(const uint4 *)(vc + ro + e);
         }
     };
     load_step(ak, av, p0);
@@ -892,8 +890,8 @@ __global__ void __launch_bounds__(256) k_dec_attn_rows(
         newk[i] = kh;
         newv[i] = vh;
         if (owner) {
-            kc[sbase + (size_t)pnew * KVD + i] = kh;
-            vc[sbase + (size_t)pnew * KVD + i] = vh;
+            kc[pg.template at<PAGED>(qi, pnew, kv_seq_stride, KVD) + i] = kh;
+            vc[pg.template at<PAGED>(qi, pnew, kv_seq_stride, KVD) + i] = vh;
         }
     }
     // Q^T of this wavefront's group as the B operand: lane holds
@@ -1260,11 +1258,12 @@ size_t dec_attn_workspace_bytes(int qheads, int hdim, int kvheads, int nq, int m
     return (size_t)nq * qheads * ns * (hdim + 2) * sizeof(float);
 }
 
-void launch_dec_attn(const float *qkv, int ldqkv, int nq, int qheads, int kvheads, int hdim,
-                     const float *rc, const float *rs, uint16_t *kc, uint16_t *vc,
-                     size_t kv_seq_stride, const int *ctx_dev, int ctx0, int max_ctx,
-                     float *q_cap, int ns, void *workspace, float *attn, int8_t *aqs,
-                     uint16_t *ad, int16_t *as, hipStream_t st) {
+template <bool PAGED>
+static void dec_attn_impl(const float *qkv, int ldqkv, int nq, int qheads, int kvheads, int hdim,
+                          const float *rc, const float *rs, uint16_t *kc, uint16_t *vc,
+                          size_t kv_seq_stride, const int *ctx_dev, int ctx0, int max_ctx,
+                          float *q_cap, int ns, void *workspace, float *attn, int8_t *aqs,
+                          uint16_t *ad, int16_t *as, hipStream_t st, KvPages pg) {
     if (nq <= 0) return;
     int chunk = (max_ctx + ns - 1) / ns;
     chunk = (chunk + DA_TILE - 1) / DA_TILE * DA_TILE;
@@ -1276,10 +1275,10 @@ void launch_dec_attn(const float *qkv, int ldqkv, int nq, int qheads, int kvhead
     const bool fin = attn != nullptr;
     if (dec_rows_ok(qheads, kvheads, hdim, nq)) {
 #define RCALL(DIM, GG, FIN)                                                                       \
-    hipLaunchKernelGGL((k_dec_attn_rows<DIM, GG, FIN>), dim3(ns, nq), dim3(256),                \
+    hipLaunchKernelGGL((k_dec_attn_rows<DIM, GG, FIN, PAGED>), dim3(ns, nq), dim3(256),                \
                        (RowsLds<DIM, GG>::bytes(per)), st, qkv, ldqkv, qheads, rc, rs, kc, vc,   \
                        kv_seq_stride, ctx_dev, ctx0, max_ctx, chunk, scale, q_cap, ws_m, ws_l,    \
-                       ws_o, attn, aqs, ad, as)
+                       ws_o, attn, aqs, ad, as, pg)
 #define RCALLG(DIM)                                                \
     if (kvheads == 1) {                                            \
         if (fin) RCALL(DIM, 1, true); else RCALL(DIM, 1, false);   \
@@ -1300,10 +1299,10 @@ void launch_dec_attn(const float *qkv, int ldqkv, int nq, int qheads, int kvhead
     }
     const dim3 grid(ns, kvheads, nq);
 #define CALL(DIM, NW, FIN)                                                                     \
-    hipLaunchKernelGGL((k_dec_attn<DIM, NW, FIN>), grid, dim3(NW * 64),                        \
+    hipLaunchKernelGGL((k_dec_attn<DIM, NW, FIN, PAGED>), grid, dim3(NW * 64),                        \
                        (AttnLds<DIM, NW>::bytes(per)), st, qkv, ldqkv, qheads, kvheads, rc, rs,  \
                        kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx, chunk, scale, q_cap,     \
-                       ws_m, ws_l, ws_o, attn, aqs, ad, as)
+                       ws_m, ws_l, ws_o, attn, aqs, ad, as, pg)
     // 8 wavefronts unless the merge buffers of a wide GQA group exceed 64 KiB
 #define CALLD(DIM)                                           \
     if (AttnLds<DIM, DA_NW>::bytes(per) <= 65536) {          \
@@ -1325,6 +1324,21 @@ void launch_dec_attn(const float *qkv, int ldqkv, int nq, int qheads, int kvhead
     }
 #undef CALLD
 #undef CALL
+}
+
+void launch_dec_attn(const float *qkv, int ldqkv, int nq, int qheads, int kvheads, int hdim,
+                     const float *rc, const float *rs, uint16_t *kc, uint16_t *vc,
+                     size_t kv_seq_stride, const int *ctx_dev, int ctx0, int max_ctx,
+                     float *q_cap, int ns, void *workspace, float *attn, int8_t *aqs,
+                     uint16_t *ad, int16_t *as, hipStream_t st, KvPages pg) {
+    if (pg.pages)
+        dec_attn_impl<true>(qkv, ldqkv, nq, qheads, kvheads, hdim, rc, rs, kc, vc, kv_seq_stride,
+                            ctx_dev, ctx0, max_ctx, q_cap, ns, workspace, attn, aqs, ad, as, st,
+                            pg);
+    else
+        dec_attn_impl<false>(qkv, ldqkv, nq, qheads, kvheads, hdim, rc, rs, kc, vc,
+                             kv_seq_stride, ctx_dev, ctx0, max_ctx, q_cap, ns, workspace, attn,
+                             aqs, ad, as, st, pg);
 }
 
 }  // namespace si

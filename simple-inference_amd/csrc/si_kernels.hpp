@@ -57,12 +57,22 @@ namespace si {
 struct KvPages {
     const int *pages = nullptr;
     int max_pages = 0, shift = 0, npages = 0;
+    // element offset of the row; PAGED fixed at compile time (the tuned
+    // kernels are instantiated for both layouts)
+    template <bool PAGED>
+    __device__ __forceinline__ size_t at(int seq, int pos, size_t kv_seq_stride, int kvd) const {
+        if constexpr (!PAGED) {
+            return (size_t)seq * kv_seq_stride + (size_t)pos * kvd;
+        } else {
+            int pg = pages[(size_t)seq * max_pages + min(pos >> shift, max_pages - 1)];
+            pg = min(max(pg, 0), npages - 1);
+            return (((size_t)pg << shift) | (size_t)(pos & ((1 << shift) - 1))) * kvd;
+        }
+    }
     __device__ __forceinline__ size_t row(int seq, int pos, size_t kv_seq_stride,
                                           int kvd) const {
-        if (!pages) return (size_t)seq * kv_seq_stride + (size_t)pos * kvd;
-        int pg = pages[(size_t)seq * max_pages + min(pos >> shift, max_pages - 1)];
-        pg = min(max(pg, 0), npages - 1);
-        return (((size_t)pg << shift) | (size_t)(pos & ((1 << shift) - 1))) * kvd;
+        return pages ? at<true>(seq, pos, kv_seq_stride, kvd)
+                     : at<false>(seq, pos, kv_seq_stride, kvd);
     }
 };
 void launch_rope_kv(const float *qkv, int ldqkv, int ntok, int qheads, int kvheads, int hdim,
@@ -110,7 +120,7 @@ void launch_dec_attn(const float *qkv, int ldqkv, int nq, int qheads, int kvhead
                      const float *rc, const float *rs, uint16_t *kc, uint16_t *vc,
                      size_t kv_seq_stride, const int *ctx_dev, int ctx0, int max_ctx,
                      float *q_cap, int ns, void *workspace, float *attn, int8_t *aqs,
-                     uint16_t *ad, int16_t *as, hipStream_t st);
+                     uint16_t *ad, int16_t *as, hipStream_t st, KvPages pg = KvPages());
 void launch_attn_combine(int nq, int qheads, int hdim, int nsplit, const void *workspace,
                          float *attn, int8_t *qs, uint16_t *d, int16_t *bsum, hipStream_t st);
 }  // namespace si
