@@ -33,10 +33,10 @@ INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA, TOP/s
 MALL_BYTES = 256 << 20      # Infinity Cache
 METRIC = "decode layer µs + HBM GB/s; prefill tokens/s + int8 MFMA % (one GPU)"
 # HBM bytes per launch of the dominant kernel (k_dec_gateup, 0.5B), from two
-# rocprofv3 --pmc runs of `bench.py --dominant-only` (FETCH_SIZE 2497.0 KiB,
+# rocprofv3 --pmc runs of `bench.py --dominant-only` (FETCH_SIZE 2521.4 KiB,
 # WRITE_SIZE 9.8 KiB per dispatch, medians) scaled by what the counters read
 # for a 256 MiB copy (FETCH_SIZE x2.000, WRITE_SIZE x1.000).
-DOMINANT_TRAFFIC_BYTES = (2497.0 * 2.000 + 9.8 * 1.000) * 1024
+DOMINANT_TRAFFIC_BYTES = (2521.4 * 2.000 + 9.8 * 1.000) * 1024
 
 
 def log(*a):

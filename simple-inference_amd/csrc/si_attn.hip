@@ -193,8 +193,9 @@ static void combine(int qheads, int hdim, int nq, int nsplit, const float *ws_m,
 // are staged through LDS and read transposed (the MFMA reduction runs over
 // positions).  Q and P are fp32 values split into fp16 hi + lo halves
 // (x = hi + lo to 22 bits), each product done twice, so the result keeps
-// fp32-level accuracy although the matrix cores take fp16.  Each wavefront's
-// (max, sum, unnormalised O) is one partial; k_attn_combine merges them.
+// fp32-level accuracy although the matrix cores take fp16.  The 4 wavefronts'
+// (max, sum, unnormalised O) are merged in LDS into one partial per
+// workgroup; k_attn_combine merges the chunks.
 //
 // Layouts (16x16 tiles): MFMA output element (i, j) is held by lane
 // j + 16*(i/4), register i%4.  The A/B operands give lane l row/column l%16
@@ -226,7 +227,7 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(
     __shared__ __attribute__((aligned(16))) _Float16 v_lds[MA_SUPER * VROW];
 
     const int sp = blockIdx.x, g = blockIdx.y, qi = blockIdx.z;
-    const int nsplit4 = gridDim.x * 4;
+    const int nsplit = gridDim.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int per = qheads / kvheads;
@@ -329,19 +330,40 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(
         }
         __syncthreads();  // V rows are overwritten by the next step
     }
-    // this wavefront's partial: split index sp*4 + wave
-    if (col < per) {
-        const int h = g * per + col;
-        const size_t pi = ((size_t)qi * qheads + h) * nsplit4 + sp * 4 + wave;
-        if (grp == 0) {
-            ws_m[pi] = m;
-            ws_l[pi] = lsum;
-        }
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) ws_o[pi * D + 16 * dt + 4 * grp + r] = o[dt][r];
+    // merge the 4 wavefronts' states into the workgroup's partial (split
+    // index sp): each wave rescales its sums to the common max, and the
+    // scaled outputs are added in wave order through LDS
+    __shared__ float mrg_m[4][16], mrg_l[4][16];
+    __shared__ float mrg_o[16 * D];
+    if (grp == 0) {
+        mrg_m[wave][col] = m;
+        mrg_l[wave][col] = lsum;
     }
+    __syncthreads();
+    const float mall = fmaxf(fmaxf(mrg_m[0][col], mrg_m[1][col]), fmaxf(mrg_m[2][col], mrg_m[3][col]));
+    const float w = m == -INFINITY ? 0.0f : expf(m - mall);  // a wave with no positions adds 0
+    for (int k = 0; k < 4; ++k) {
+        if (wave == k)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int idx = col * D + 16 * dt + 4 * grp + r;
+                    const float v = o[dt][r] * w;
+                    mrg_o[idx] = k == 0 ? v : mrg_o[idx] + v;
+                }
+        __syncthreads();
+    }
+    const size_t pbase = ((size_t)qi * qheads + (size_t)g * per) * nsplit + sp;  // head col 0
+    if (wave == 0 && grp == 0 && col < per) {
+        float l = 0.0f;
+        for (int k = 0; k < 4; ++k)
+            if (mrg_m[k][col] != -INFINITY) l += mrg_l[k][col] * expf(mrg_m[k][col] - mall);
+        ws_m[pbase + (size_t)col * nsplit] = mall;
+        ws_l[pbase + (size_t)col * nsplit] = l;
+    }
+    for (int idx = tid; idx < per * D; idx += 256)
+        ws_o[(pbase + (size_t)(idx / D) * nsplit) * D + idx % D] = mrg_o[idx];
 }
 
 // ===========================================================================
@@ -711,14 +733,15 @@ int attn_nsplit(int kvheads, int nq, int max_ctx) {
     int ns = (512 + base - 1) / base;
     // down to one workgroup step per chunk: the many partials this leaves
     // for a single query go to the wide combine kernel (7B, ctx 4096, cold
-    // cache: 4-step chunks 22.9 us, 1-step 19.9 us)
+    // cache, before the in-workgroup merge: 4-step chunks 22.9 us, 1-step
+    // 19.9 us)
     const int maxs = (max_ctx + MA_SUPER - 1) / MA_SUPER;
     if (ns > maxs) ns = maxs;
     return ns < 1 ? 1 : ns;
 }
 
 size_t attn_workspace_bytes(int qheads, int hdim, int kvheads, int nq, int max_ctx) {
-    const int ns = attn_nsplit(kvheads, nq, max_ctx) * 4;  // one partial per wavefront
+    const int ns = attn_nsplit(kvheads, nq, max_ctx);  // one partial per workgroup
     return (size_t)nq * qheads * ns * (hdim + 2) * sizeof(float);
 }
 
@@ -736,10 +759,9 @@ void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
     const int ns = attn_nsplit(kvheads, nq, max_ctx);
     int chunk = (max_ctx + ns - 1) / ns;
     chunk = (chunk + MA_SUPER - 1) / MA_SUPER * MA_SUPER;
-    const int ns4 = ns * 4;
     float *ws_m = (float *)workspace;
-    float *ws_l = ws_m + (size_t)nq * qheads * ns4;
-    float *ws_o = ws_l + (size_t)nq * qheads * ns4;
+    float *ws_l = ws_m + (size_t)nq * qheads * ns;
+    float *ws_o = ws_l + (size_t)nq * qheads * ns;
     const float scale = 1.0f / sqrtf((float)hdim);  // attention_kernels.h:86
     const dim3 grid(ns, kvheads, nq);
 #define SI_ATTN_LAUNCH(DIM)                                                                  \
@@ -753,7 +775,7 @@ void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
         default: SI_ATTN_LAUNCH(128); break;
     }
 #undef SI_ATTN_LAUNCH
-    combine(qheads, hdim, nq, ns4, ws_m, ws_l, ws_o, attn, qs, d, bsum, st);
+    combine(qheads, hdim, nq, ns, ws_m, ws_l, ws_o, attn, qs, d, bsum, st);
 }
 
 // Merge of nsplit partials laid out as [nq][qheads][nsplit] (m, l) and
