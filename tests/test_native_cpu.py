@@ -97,3 +97,30 @@ def test_attention_workspace_sizing():
     s = si_amd.make_shape(**si_amd.SHAPES["7b"])
     ws = si_amd.lib().si_attention_workspace(ctypes.byref(s), 64, 4096)
     assert ws > 0 and ws % 4 == 0
+
+
+def test_command_line_argument_errors():
+    """lib/si_qwen_layer validates its arguments like qwen_one_layer.c:596-629
+    before touching the device: usage -> 2, bad values -> 1 with the
+    reference's messages."""
+    import os
+    import subprocess
+    cli = os.path.join(os.path.dirname(si_amd.AMD_SO), "si_qwen_layer")
+    assert os.path.exists(cli)
+
+    def run(*args, shape="1.5b"):
+        env = dict(os.environ, SI_SHAPE=shape)
+        return subprocess.run([cli, *map(str, args)], env=env, capture_output=True, text=True,
+                              timeout=60)
+
+    r = run()
+    assert r.returncode == 2 and "Usage:" in r.stderr
+    assert run("w", 1, 1, "standard", "extra").returncode == 2
+    for args, msg in (((0,), "Context must be 1..32768"), ((32769,), "Context must be 1..32768"),
+                      ((16, 0), "repeat 1..100000"), (("12x",), "Invalid context argument"),
+                      ((16, "3y"), "Invalid repeat argument"),
+                      ((16, 1, "bogus"), "Attention mode must be")):
+        r = run("synthetic", *args)
+        assert r.returncode == 1 and msg in r.stderr, (args, r.stderr)
+    r = run("synthetic", 16, 1, "flash", shape="13b")
+    assert r.returncode == 1 and "SI_SHAPE" in r.stderr
