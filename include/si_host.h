@@ -152,7 +152,8 @@ const int *si_stack_dev_table(const si_stack_t *st);
 const int *si_stack_dev_ctx(const si_stack_t *st);
 /* Grows each of the nseq distinct sequences seqs[] by one position (the
  * token about to be decoded) and uploads their page lists and contexts in
- * batch order (synchronous copies).  -1 when the pool is exhausted (the
+ * batch order (synchronous copies, after waiting for the stream of the
+ * previous si_stack_decode, whose kernels read them).  -1 when the pool is exhausted (the
  * lengths are left as before; pages already taken stay with their
  * sequences), else 0. */
 int si_stack_prepare(si_stack_t *st, const int *seqs, int nseq);

@@ -141,7 +141,8 @@ struct si_stack {
     int *host_table, *host_ctx;
     float *act[2];  /* ping-pong activations between layers */
     int nseq;       /* rows of the last prepare */
-    void *stream;
+    void *stream;   /* stream of the last si_stack_decode */
+    int pending;    /* a decode was enqueued since the last prepare */
 };
 
 si_stack_t *si_stack_create(const si_shape_t *s, const si_layer_host_t *layers, int nlayers,
@@ -210,6 +211,11 @@ const int *si_stack_dev_ctx(const si_stack_t *st) { return st->dev_ctx; }
 
 int si_stack_prepare(si_stack_t *st, const int *seqs, int nseq) {
     if (nseq < 1 || nseq > st->max_seqs) die("si_stack_prepare: nseq outside 1..max_seqs");
+    /* the previous step's kernels read the device table and contexts this
+     * call rewrites: wait for them */
+    if (st->pending)
+        hip_check(hipStreamSynchronize((hipStream_t)st->stream), "si_stack_prepare: wait");
+    st->pending = 0;
     si_kv_pages_t *p = st->pages;
     for (int i = 0; i < nseq; ++i) {
         const int len = si_kv_seq_len(p, seqs[i]) + 1;
@@ -248,4 +254,6 @@ void si_stack_decode(si_stack_t *st, const float *x, float *out, int flags, void
               "si_layer_decode_paged");
         in = o;
     }
+    st->stream = stream;
+    st->pending = 1;
 }
