@@ -876,18 +876,25 @@ __global__ __launch_bounds__(1024) void k_std_softmax(float *__restrict__ scores
     for (int t = threadIdx.x; t < ctx; t += 1024) row[t] *= inv;
 }
 
-// Stage 3, grid (hdim/8, qheads), block 1024: workgroup c owns the 8
-// output columns 8c..8c+7 of one head (one 16-byte V load per position);
+// Stage 3, 8 * ceil(qheads * hdim/8 / 8) workgroups of 1024 threads: a
+// workgroup owns the 8 output columns 8c..8c+7 of one head (one 16-byte V
+// load per position).  Workgroups are dealt to the 8 XCDs in turn (linear
+// id % 8), so (head, c) pairs are numbered head-major and each XCD takes a
+// contiguous range: the column workgroups of a head, and the heads of a KV
+// group, then share their V cache lines in one XCD's L2.
 // thread i sums p[t] v[t] over t = i, i + 1024, ... (four loads in flight),
-// then the 1024 partial sums are added by a fixed tree
+// then the 1024 partial sums are added in a fixed order
 // (attention_kernels.h:64-77 up to the summation order).  The normalised
 // scores stay in place.
 __global__ __launch_bounds__(1024) void k_std_pv(const float *__restrict__ scores,
                                                  const uint16_t *__restrict__ vc, int qheads,
                                                  int kvheads, int hdim, int ctx,
                                                  float *__restrict__ out) {
-    __shared__ float red[8][1024];
-    const int c = blockIdx.x, h = blockIdx.y, g = h / (qheads / kvheads), tid = threadIdx.x;
+    __shared__ float red[16][8];
+    const int cpr = hdim / 8, npair = qheads * cpr, per_xcd = (npair + 7) / 8;
+    const int pair = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (pair >= npair) return;  // whole workgroup: no barrier is skipped
+    const int h = pair / cpr, c = pair % cpr, g = h / (qheads / kvheads), tid = threadIdx.x;
     const float *p = scores + (size_t)h * ctx;
     const size_t rstride = (size_t)kvheads * hdim / 8;  // uint4 per cache row
     const uint4 *v = (const uint4 *)vc + (size_t)g * (hdim / 8) + c;
@@ -911,16 +918,21 @@ __global__ __launch_bounds__(1024) void k_std_pv(const float *__restrict__ score
         for (int k = 0; k < 4; ++k) add(u[k], pt[k]);
     }
     for (; t < ctx; t += 1024) add(v[(size_t)t * rstride], p[t]);
+    // fixed-order reduction: butterfly within each wavefront, then the 16
+    // wavefront sums in wave order
 #pragma unroll
-    for (int e = 0; e < 8; ++e) red[e][tid] = acc[e];
+    for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], off, 64);
+    if ((tid & 63) == 0)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) red[tid >> 6][e] = acc[e];
     __syncthreads();
-    for (int st = 512; st > 0; st >>= 1) {
-        if (tid < st)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) red[e][tid] += red[e][tid + st];
-        __syncthreads();
+    if (tid < 8) {
+        float r = red[0][tid];
+        for (int w = 1; w < 16; ++w) r += red[w][tid];
+        out[(size_t)h * hdim + c * 8 + tid] = r;
     }
-    if (tid < 8) out[(size_t)h * hdim + c * 8 + tid] = red[tid][0];
 }
 
 bool attn_standard_supported(int qheads, int kvheads, int hdim) {
@@ -943,8 +955,9 @@ void launch_attn_standard(const float *q, int qheads, int kvheads, int hdim, con
         hipLaunchKernelGGL(k_std_softmax, dim3(qheads), dim3(1024), 0, st, scores, ctx);
     }
     // context 0 leaves the output zero (attention_kernels.h:70)
-    hipLaunchKernelGGL(k_std_pv, dim3(hdim / 8, qheads), dim3(1024), 0, st, scores, vc, qheads,
-                       kvheads, hdim, ctx, out);
+    const int npair = qheads * (hdim / 8);
+    hipLaunchKernelGGL(k_std_pv, dim3(8 * ((npair + 7) / 8)), dim3(1024), 0, st, scores, vc,
+                       qheads, kvheads, hdim, ctx, out);
 }
 
 }  // namespace si
