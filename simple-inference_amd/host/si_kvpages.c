@@ -216,6 +216,9 @@ int si_stack_prepare(si_stack_t *st, const int *seqs, int nseq) {
     if (st->pending)
         hip_check(hipStreamSynchronize((hipStream_t)st->stream), "si_stack_prepare: wait");
     st->pending = 0;
+    for (int i = 0; i < nseq; ++i)
+        for (int j = 0; j < i; ++j)
+            if (seqs[i] == seqs[j]) die("si_stack_prepare: a sequence appears twice");
     si_kv_pages_t *p = st->pages;
     for (int i = 0; i < nseq; ++i) {
         const int len = si_kv_seq_len(p, seqs[i]) + 1;
