@@ -278,7 +278,7 @@ def bench_qkv_gemv(torch, si_amd, stream, launches=1000):
             launch(i)
     torch.cuda.synchronize()
     ms = graph_time_ms(torch, stream, launch, launches, replays=3)
-    alg = 586168  # W 580,608 + x 952 + y 4,608
+    alg = 586168  # W 580,608 + x 952 + y 4,608 bytes (config 1)
     return dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, copies=copies)
 
 
