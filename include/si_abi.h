@@ -204,18 +204,6 @@ int si_attention_standard(const si_shape_t *s, const float *q, const uint16_t *k
                           const uint16_t *vc, int context, float *out, float *scores,
                           void *stream);
 
-/* Test entry for the fp16 matrix-core lane layouts the attention kernels
- * rely on: a [16][32] and b [32][16] fp16 (row-major) -> d32 = a.b with the
- * 16x16x32 shape and d16 = a[:, :16].b[:16, :] with the 16x16x16 shape
- * (fp32 [16][16] row-major).  No counterpart in the reference. */
-int si_debug_mfma_f16(const void *a, const void *b, float *d32, float *d16, void *stream);
-
-/* Test entry for the cross-lane moves the kernels' reductions use (DPP
- * quad_perm / row_ror / row_half_mirror, v_permlane16/32_swap): each lane
- * of one wavefront feeds its index; out[k*64 + lane] (18 x 64 ints) is what
- * lane received from operation k.  No counterpart in the reference. */
-int si_debug_lane_ops(int *out, void *stream);
-
 /* Build-defined SwiGLU + quantize_q8: act = silu(gate)*up with
  * silu(g) = g/(1+expf(-g)); gate = gu[r][0..f), up = gu[r][f..2f). */
 int si_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs,

@@ -150,12 +150,15 @@ uint16_t *si_stack_v_pool(si_stack_t *st, int layer);
 si_layer_t *si_stack_layer(si_stack_t *st, int layer);
 const int *si_stack_dev_table(const si_stack_t *st);
 const int *si_stack_dev_ctx(const si_stack_t *st);
+/* sequences of the last successful si_stack_prepare (0: none, or it failed) */
+int si_stack_nseq(const si_stack_t *st);
 /* Grows each of the nseq distinct sequences seqs[] by one position (the
  * token about to be decoded) and uploads their page lists and contexts in
  * batch order (synchronous copies, after waiting for the stream of the
  * previous si_stack_decode, whose kernels read them).  -1 when the pool is exhausted (the
  * lengths are left as before; pages already taken stay with their
- * sequences), else 0. */
+ * sequences, and si_stack_decode dies until a later prepare succeeds),
+ * else 0. */
 int si_stack_prepare(si_stack_t *st, const int *seqs, int nseq);
 /* x [nseq][hidden] (device) through every layer -> out [nseq][hidden]: the
  * residual stream of a decode step; kernel launches only (capturable). */

@@ -319,18 +319,6 @@ int si_attention_standard(const si_shape_t *s, const float *q, const uint16_t *k
     return check_launch("si_attention_standard");
 }
 
-int si_debug_lane_ops(int *out, void *stream) {
-    SI_REQUIRE(out, "debug_lane_ops: NULL pointer");
-    launch_debug_lane_ops(out, S(stream));
-    return check_launch("si_debug_lane_ops");
-}
-
-int si_debug_mfma_f16(const void *a, const void *b, float *d32, float *d16, void *stream) {
-    SI_REQUIRE(a && b && d32 && d16, "debug_mfma: NULL pointer");
-    launch_debug_mfma_f16(a, b, d32, d16, S(stream));
-    return check_launch("si_debug_mfma_f16");
-}
-
 int si_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs, uint16_t *d,
                  int16_t *s, void *stream) {
     SI_REQUIRE(rows >= 0 && f > 0 && f % 32 == 0, "swiglu: bad size");

@@ -788,32 +788,6 @@ void launch_attn_combine(int nq, int qheads, int hdim, int nsplit, const void *w
     combine(qheads, hdim, nq, nsplit, ws_m, ws_l, ws_o, attn, qs, d, bsum, st);
 }
 
-// Test entry: one 16x16 tile with each of the two f16 matrix-core shapes,
-// operands placed with the lane layouts above, output scattered back to
-// row-major with the assumed output layout.  A [16][32], B [32][16] halves.
-__global__ void k_debug_mfma_f16(const _Float16 *A, const _Float16 *B, float *D32, float *D16) {
-    const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
-    h8 a8, b8;
-    for (int e = 0; e < 8; ++e) {
-        a8[e] = A[col * 32 + 8 * grp + e];
-        b8[e] = B[(8 * grp + e) * 16 + col];
-    }
-    f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8, b8, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-    for (int r = 0; r < 4; ++r) D32[(4 * grp + r) * 16 + col] = d[r];
-    h4 a4, b4;
-    for (int e = 0; e < 4; ++e) {
-        a4[e] = A[col * 32 + 4 * grp + e];
-        b4[e] = B[(4 * grp + e) * 16 + col];
-    }
-    f4 d2 = __builtin_amdgcn_mfma_f32_16x16x16f16(a4, b4, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-    for (int r = 0; r < 4; ++r) D16[(4 * grp + r) * 16 + col] = d2[r];
-}
-
-void launch_debug_mfma_f16(const void *A, const void *B, float *D32, float *D16, hipStream_t st) {
-    hipLaunchKernelGGL(k_debug_mfma_f16, dim3(1), dim3(64), 0, st, (const _Float16 *)A,
-                       (const _Float16 *)B, D32, D16);
-}
-
 // ---------------------------------------------------------------------------
 // Textbook attention in three stages (attention_standard,
 // attention_kernels.h:33-78): the fp32 scores of every (head, position) are

@@ -64,8 +64,8 @@ __device__ __forceinline__ uint16_t f2h(float x) {
 // rows 0<->1, 2<->3 and halves 0<->1.  (__shfl_xor lowers to
 // ds_bpermute_b32, a round trip through LDS, ten of which per Q8 block
 // dominated the small decode kernels.)  Every lane of a group must be
-// active.  The lane layouts are checked on the device by
-// si_debug_lane_ops.
+// active.  The lane layouts are checked on the device by the test-only
+// probe library (tests/probe).
 // ---------------------------------------------------------------------
 enum : int {
     DPP_XOR1 = 0xB1,      // quad_perm [1,0,3,2]

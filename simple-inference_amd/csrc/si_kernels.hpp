@@ -12,7 +12,6 @@ void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int ro
                        hipStream_t st);
 void launch_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs, uint16_t *d,
                       int16_t *s, hipStream_t st);
-void launch_debug_lane_ops(int *out, hipStream_t st);
 void launch_q4_repack(const uint8_t *src, int n, int k, int tile, uint8_t *qs, uint16_t *d,
                       hipStream_t st);
 void launch_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k, int tile,
@@ -82,7 +81,6 @@ void launch_rope_kv(const float *qkv, int ldqkv, int ntok, int qheads, int kvhea
 int attn_nsplit(int kvheads, int nq, int max_ctx);
 size_t attn_workspace_bytes(int qheads, int hdim, int kvheads, int nq, int max_ctx);
 bool attn_supported(int qheads, int kvheads, int hdim);
-void launch_debug_mfma_f16(const void *A, const void *B, float *D32, float *D16, hipStream_t st);
 // three-stage textbook attention for one query (scores: [qheads][ctx] fp32)
 bool attn_standard_supported(int qheads, int kvheads, int hdim);
 void launch_attn_standard(const float *q, int qheads, int kvheads, int hdim, const uint16_t *kc,

@@ -260,35 +260,6 @@ __global__ void k_q4_unpack(const uint8_t *__restrict__ qs, const uint16_t *__re
     for (int t = 0; t < 16; ++t) blk[2 + t] = qs[i * 16 + t];
 }
 
-// Test entry for the cross-lane helpers of si_device.hpp: every lane feeds
-// its lane index; out[k*64 + lane] is what lane received from operation k.
-__global__ void __launch_bounds__(64) k_debug_lane_ops(int *__restrict__ out) {
-    const int l = threadIdx.x;
-    const float f = (float)l;
-    out[0 * 64 + l] = dpp_i<DPP_XOR1>(l);
-    out[1 * 64 + l] = dpp_i<DPP_XOR2>(l);
-    out[2 * 64 + l] = dpp_i<DPP_ROR4>(l);
-    out[3 * 64 + l] = dpp_i<DPP_ROR8>(l);
-    out[4 * 64 + l] = dpp_i<DPP_HMIRROR>(l);
-    out[5 * 64 + l] = swap16_i(l);
-    out[6 * 64 + l] = swap32_i(l);
-    out[7 * 64 + l] = oct_sum(l);
-    out[8 * 64 + l] = half_wave_sum(l);
-    out[9 * 64 + l] = (int)wave_sum(f);
-    out[10 * 64 + l] = (int)half_wave_max(f);
-    out[11 * 64 + l] = (int)wave_max(f);
-    out[12 * 64 + l] = (int)oct_max(f);
-    out[13 * 64 + l] = (int)fold_rows<4>(f);
-    out[14 * 64 + l] = (int)fold_rows<8>(f);
-    out[15 * 64 + l] = (int)fold_rows<16>(f);
-    out[16 * 64 + l] = (int)fold_rows<32>(f);
-    out[17 * 64 + l] = (int)wave_sum_d((double)l);
-}
-
-void launch_debug_lane_ops(int *out, hipStream_t st) {
-    hipLaunchKernelGGL(k_debug_lane_ops, dim3(1), dim3(64), 0, st, out);
-}
-
 // ----------------------------------------------------------------------
 // launchers
 // ----------------------------------------------------------------------

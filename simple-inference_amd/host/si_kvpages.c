@@ -208,6 +208,7 @@ uint16_t *si_stack_v_pool(si_stack_t *st, int layer) { return st->vpool[layer]; 
 si_layer_t *si_stack_layer(si_stack_t *st, int layer) { return st->layers[layer]; }
 const int *si_stack_dev_table(const si_stack_t *st) { return st->dev_table; }
 const int *si_stack_dev_ctx(const si_stack_t *st) { return st->dev_ctx; }
+int si_stack_nseq(const si_stack_t *st) { return st->nseq; }
 
 int si_stack_prepare(si_stack_t *st, const int *seqs, int nseq) {
     if (nseq < 1 || nseq > st->max_seqs) die("si_stack_prepare: nseq outside 1..max_seqs");
@@ -224,8 +225,11 @@ int si_stack_prepare(si_stack_t *st, const int *seqs, int nseq) {
         const int len = si_kv_seq_len(p, seqs[i]) + 1;
         if (len > st->max_ctx) die("si_stack_prepare: a sequence exceeds max_ctx");
         if (si_kv_seq_grow(p, seqs[i], len) != 0) {
-            /* roll back this call's growth so the caller can preempt */
+            /* roll back this call's growth so the caller can preempt; the
+             * device table and contexts still describe the previous step, so
+             * no decode may run until a prepare succeeds */
             for (int j = 0; j < i; ++j) p->len[seqs[j]] -= 1;
+            st->nseq = 0;
             return -1;
         }
     }

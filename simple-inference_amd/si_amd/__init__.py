@@ -91,8 +91,6 @@ _SIGS = {
     "si_attention_workspace": (_Z, [ctypes.POINTER(Shape), _I, _I]),
     "si_attention_standard": (_I, [ctypes.POINTER(Shape), _P, _P, _P, _I, _P, _P, _P]),
     "si_swiglu_q8": (_I, [_P, _I, _I, _P, _P, _P, _P, _P]),
-    "si_debug_mfma_f16": (_I, [_P, _P, _P, _P, _P]),
-    "si_debug_lane_ops": (_I, [_P, _P]),
     "si_layer_create": (_I, [ctypes.POINTER(Shape), ctypes.POINTER(LayerHost), _I, _I,
                              ctypes.POINTER(_P)]),
     "si_layer_destroy": (_I, [_P]),
@@ -161,6 +159,7 @@ def host_lib():
                 ("si_stack_layer", _P, [_P, _I]),
                 ("si_stack_dev_table", _P, [_P]),
                 ("si_stack_dev_ctx", _P, [_P]),
+                ("si_stack_nseq", _I, [_P]),
                 ("si_stack_prepare", _I, [_P, _P, _I]),
                 ("si_stack_decode", None, [_P, _P, _P, _I, _P])):
             f = getattr(H, name)

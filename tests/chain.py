@@ -121,6 +121,15 @@ def check_row(oracle, os_, lay, x, t, B, kc_gpu, vc_gpu, base, pos, ctx, out_row
         close(out_row, down, 1e-5, tag + " down + residual")
 
 
+# Asserted bound on the raw (unchained) end-to-end difference of a layer
+# output from the oracle's, as max|got - want| / rms(want).  The chained
+# check above is the parity bar; this loose bound catches a regression that
+# moves every link while keeping each inside its own tolerance.  The 7B layer
+# amplifies a 2e-5 change of its attention output to ~3e-3 at its outputs
+# (test_oracle_sensitivity.py), so its bound is wider.
+E2E_BOUND = {"0.5b": 2e-3, "1.5b_ref": 2e-3, "7b": 2e-2}
+
+
 def end_to_end_report(got, want):
     """Statistics of the raw (unchained) difference, for reporting."""
     got = np.asarray(got, np.float64)

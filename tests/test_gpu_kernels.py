@@ -467,8 +467,9 @@ def test_mfma_f16_lane_layouts():
     a = rng.integers(-8, 8, (16, 32)).astype(np.float16)
     b = rng.integers(-8, 8, (32, 16)).astype(np.float16)
     d32, d16 = empty(256, torch.float32), empty(256, torch.float32)
-    si_amd.call("si_debug_mfma_f16", si_amd.ptr(dev(a.view(np.int16))),
-                si_amd.ptr(dev(b.view(np.int16))), si_amd.ptr(d32), si_amd.ptr(d16), None)
+    from tests.probe import call as probe_call
+    probe_call("si_probe_mfma_f16", si_amd.ptr(dev(a.view(np.int16))),
+               si_amd.ptr(dev(b.view(np.int16))), si_amd.ptr(d32), si_amd.ptr(d16), None)
     af, bf = a.astype(np.float64), b.astype(np.float64)
     assert np.array_equal(host(d32).reshape(16, 16), af @ bf)
     assert np.array_equal(host(d16).reshape(16, 16), af[:, :16] @ bf[:16, :])
@@ -479,7 +480,8 @@ def test_cross_lane_ops_layouts():
     against their documented lane maps."""
     torch = _torch()
     out = zeros(18 * 64, torch.int32)
-    si_amd.call("si_debug_lane_ops", si_amd.ptr(out), None)
+    from tests.probe import call as probe_call
+    probe_call("si_probe_lane_ops", si_amd.ptr(out), None)
     got = host(out).reshape(18, 64)
     lane = np.arange(64)
     row0 = lane & ~15
@@ -542,6 +544,8 @@ def test_ffn_gateup_q8(oracle, shape, flags):
     (512, 4864, 896, 32, 0, False),      # 0.5B prefill shape; also without act and sums
     (2, 160, 96, 16, 0, True),           # tiny: the plan splits K (GEMM + SwiGLU kernel)
     (300, 4864, 896, 32, si_amd.SI_GEMM_EXACT, True),
+    (600, 4864, 896, 32, 0, True),       # past 512 rows: 128-row tiles
+    (2048, 18944, 3584, 32, 0, True),    # 7B 2048-token prefill, the instance config 4 times
 ])
 def test_gemm_gateup_q8(oracle, m, f, k, tile, flags, act_out):
     """gate|up GEMM with the SwiGLU + Q8_0 epilogue: every row's gate|up
@@ -584,7 +588,12 @@ def test_gemm_gateup_q8(oracle, m, f, k, tile, flags, act_out):
             want = oracle.matvec(w, xq[r * nb:(r + 1) * nb], k, 2 * f)
             assert np.array_equal(g[r].view(np.uint32), want.view(np.uint32)), f"row {r}"
     else:
-        want = dequant_q8(xq, m, k) @ dequant_q4(w, 2 * f, k).T
+        # float64 product of the dequantized operands, on the GPU (rocBLAS
+        # dgemm) because at 2048 x 37888 x 3584 a host product takes minutes
+        a64 = torch.from_numpy(dequant_q8(xq, m, k)).cuda()
+        w64 = torch.from_numpy(dequant_q4(w, 2 * f, k)).cuda()
+        want = (a64 @ w64.T).cpu().numpy()
+        del a64, w64
         rms = np.sqrt(np.mean(want ** 2))
         err = np.abs(g - want).max(axis=1) / rms
         assert err.max() <= 1e-5, f"gate|up rows off: worst {err.max():.3g} at {int(err.argmax())}"

@@ -16,7 +16,7 @@ import pytest
 
 import si_amd
 from oracle.oracle_py import make_shape as or_shape
-from tests.chain import LayerBuffers, check_row
+from tests.chain import E2E_BOUND, LayerBuffers, check_row, end_to_end_report
 from tests.gpu_helpers import close, dev, device_view, empty, host, kv_history, make_layer
 
 pytestmark = pytest.mark.gpu
@@ -203,14 +203,28 @@ def test_stack_matches_layers_driven_one_by_one(oracle):
         ctx = np.array([H.si_kv_seq_len(pages, i) for i in active], np.int32)
         td, cd = dev(np.ascontiguousarray(tab)), dev(ctx)
         cur = x
+        ins = []
         for l in range(nl):
             o = empty(n * s.hidden, torch.float32)
+            ins.append(cur)
             mirror[l].decode_paged(cur, n, mk[l], mv[l], npages, ps, td, max_pages, cd,
                                    int(ctx.max()), o, si_amd.SI_LAYER_FULL)
             cur = o
         torch.cuda.synchronize()
         assert np.array_equal(host(out).view(np.uint32), host(cur).view(np.uint32)), step
         assert np.isfinite(host(out)).all()
+        if step in (0, 39):
+            # each layer of the last sequence against the oracle's layer on the
+            # same input and the same cache rows gathered from the pool
+            i, c = n - 1, int(ctx[n - 1])
+            for l in range(nl):
+                kc_i = _from_pool(host(mk[l]).view(np.uint16), c, tab[i], ps, kvd)
+                vc_i = _from_pool(host(mv[l]).view(np.uint16), c, tab[i], ps, kvd)
+                xin = host(ins[l]).reshape(n, s.hidden)[i]
+                yout = host(ins[l + 1] if l + 1 < nl else cur).reshape(n, s.hidden)[i]
+                want = oracle.layer_decode(os_, lays[l], xin, kc_i.copy(), vc_i.copy(), c)
+                e2e = end_to_end_report(yout, want)
+                assert e2e["max_over_rms"] <= E2E_BOUND["0.5b"], (step, l, e2e)
     for l in range(nl):
         assert torch.equal(device_view(H.si_stack_k_pool(st, l), pool_elems, torch.int16), mk[l])
         assert torch.equal(device_view(H.si_stack_v_pool(st, l), pool_elems, torch.int16), mv[l])
@@ -220,6 +234,24 @@ def test_stack_matches_layers_driven_one_by_one(oracle):
     assert H.si_kv_seq_grow(pages, active[0], max_ctx + 1) == -1
     assert H.si_kv_seq_len(pages, active[0]) == big
     assert H.si_kv_pages_free(pages) == free_before
+    # exhaustion through si_stack_prepare: steps until the pool runs dry,
+    # then the failed step leaves every length as it was and the stack
+    # refuses to decode until a prepare succeeds
+    assert H.si_stack_nseq(st) == len(active)
+    active.append(H.si_kv_seq_add(pages))  # a fourth sequence: 17 pages run out first
+    ids = (ctypes.c_int * len(active))(*active)
+    while True:
+        lens = [H.si_kv_seq_len(pages, a) for a in active]
+        if max(lens) >= max_ctx:
+            break
+        if H.si_stack_prepare(st, ids, len(active)) != 0:
+            assert [H.si_kv_seq_len(pages, a) for a in active] == lens
+            assert H.si_kv_pages_free(pages) == 0
+            assert H.si_stack_nseq(st) == 0
+            break
+    else:
+        raise AssertionError("unreachable")
+    assert H.si_stack_nseq(st) == 0, "the pool never ran dry"
     H.si_stack_destroy(st)
     for m in mirror:
         m.close()

@@ -45,6 +45,18 @@ def _check_rows(what, got, want, rtol):
                            f" worst {err.max():.3g} of rms)")
 
 
+def _mm(a, w):
+    """a @ w.T in float64 on the GPU (rocBLAS dgemm): the reference product
+    of dequantized operands, exact to ~1e-16 relative, at sizes (7B x 2048
+    rows) where a host float64 product would take minutes."""
+    torch = _torch()
+    at = torch.from_numpy(np.ascontiguousarray(a, np.float64)).cuda()
+    wt = torch.from_numpy(np.ascontiguousarray(w, np.float64)).cuda()
+    r = (at @ wt.T).cpu().numpy()
+    del at, wt
+    return r
+
+
 def _dequant_act(blocks, rows, k):
     q = blocks["qs"].astype(np.float64).reshape(rows, k // 32, 32)
     d = blocks["d"].view(np.float16).astype(np.float64).reshape(rows, k // 32, 1)
@@ -70,7 +82,7 @@ def _stagewise(oracle, L, lay, s, os_, x, rows, kc_host, vc_host, positions, ctx
     qkv = _buf(L, "QKV", rows * NQKV, torch.float32).reshape(rows, NQKV)
     wqkv = np.concatenate([lay["wq"], lay["wk"], lay["wv"]])
     bias = np.concatenate([lay["bq"], lay["bk"], lay["bv"]]).astype(np.float64)
-    want = _dequant_act(xq, rows, H) @ dequant_q4(wqkv, NQKV, H).T + bias
+    want = _mm(_dequant_act(xq, rows, H), dequant_q4(wqkv, NQKV, H)) + bias
     _check_rows("qkv projection", qkv, want, 1e-5)
     # 3. RoPE + fp16 K/V append on the GPU's projections
     q = _buf(L, "Q", rows * QD, torch.float32).reshape(rows, QD)
@@ -94,7 +106,7 @@ def _stagewise(oracle, L, lay, s, os_, x, rows, kc_host, vc_host, positions, ctx
     assert attq.tobytes() == oracle.quantize_q8(attn).tobytes(), "attention Q8"
     # 5. W_O
     ao = _buf(L, "ATTN_OUT", rows * H, torch.float32).reshape(rows, H)
-    want = _dequant_act(attq, rows, QD) @ dequant_q4(lay["wo"], H, QD).T
+    want = _mm(_dequant_act(attq, rows, QD), dequant_q4(lay["wo"], H, QD))
     _check_rows("o projection", ao, want, 1e-5)
     # 6. residual + post-norm -> Q8
     h = _buf(L, "H", rows * H, torch.float32).reshape(rows, H)
@@ -107,7 +119,7 @@ def _stagewise(oracle, L, lay, s, os_, x, rows, kc_host, vc_host, positions, ctx
     # 7. gate|up, SwiGLU -> Q8
     gu = _buf(L, "GU", rows * 2 * F, torch.float32).reshape(rows, 2 * F)
     wgu = np.concatenate([lay["wgate"], lay["wup"]])
-    want = _dequant_act(xq2, rows, H) @ dequant_q4(wgu, 2 * F, H).T
+    want = _mm(_dequant_act(xq2, rows, H), dequant_q4(wgu, 2 * F, H))
     _check_rows("gate|up projection", gu, want, 1e-5)
     act = _buf(L, "ACT", rows * F, torch.float32).reshape(rows, F)
     want = np.stack([oracle.swiglu(gu[t, :F], gu[t, F:]) for t in range(rows)])
@@ -115,18 +127,24 @@ def _stagewise(oracle, L, lay, s, os_, x, rows, kc_host, vc_host, positions, ctx
     actq = _q8_rows(L, "ACTQ", rows, F)
     assert actq.tobytes() == oracle.quantize_q8(act).tobytes(), "swiglu Q8"
     # 8. down + residual
-    want = h + _dequant_act(actq, rows, F) @ dequant_q4(lay["wdown"], H, F).T
+    want = h + _mm(_dequant_act(actq, rows, F), dequant_q4(lay["wdown"], H, F))
     _check_rows("down projection + residual", out, want, 1e-5)
 
 
-def test_prefill_stagewise_0_5b():
+@pytest.mark.parametrize("shape,ntok,prefix", [
+    ("0.5b", 200, 30),    # ragged last tile, cached prefix
+    ("7b", 2048, 0),      # BASELINE config 4 as the bench times it (default flags)
+])
+def test_prefill_stagewise(shape, ntok, prefix):
+    """Causal prefill with the default (fast) flags: at 7B x 2048 this runs
+    the 128-row gate|up GEMM with the fused SwiGLU + Q8 epilogue and the
+    fast-epilogue QKV/O/down GEMMs the bench times."""
     from oracle.oracle_py import Oracle
     oracle = Oracle()
     torch = _torch()
-    sd = si_amd.SHAPES["0.5b"]
+    sd = si_amd.SHAPES[shape]
     s, os_ = si_amd.make_shape(**sd), or_shape(**sd)
     lay = make_layer(oracle, os_, 21)
-    ntok, prefix = 200, 30
     kvd = s.kvheads * s.hdim
     rng = np.random.default_rng(22)
     total = prefix + ntok
@@ -145,14 +163,20 @@ def test_prefill_stagewise_0_5b():
     L.close()
 
 
-def test_batched_decode_stagewise_7b():
+@pytest.mark.parametrize("nseq,ctx", [
+    (70, 160),     # ragged 64-row tiles
+    (64, 4096),    # BASELINE config 5 as the bench times it (default flags)
+])
+def test_batched_decode_stagewise_7b(nseq, ctx):
+    """Batched decode with the default flags: the M = nseq GEMMs with their
+    K-split plans, the split sums folded into the post-norm and SwiGLU
+    kernels, and the whole-row batched decode attention."""
     from oracle.oracle_py import Oracle
     oracle = Oracle()
     torch = _torch()
     sd = si_amd.SHAPES["7b"]
     s, os_ = si_amd.make_shape(**sd), or_shape(**sd)
     lay = make_layer(oracle, os_, 23)
-    nseq, ctx = 70, 160
     kvd = s.kvheads * s.hdim
     stride = ctx * kvd
     rng = np.random.default_rng(24)
@@ -167,7 +191,6 @@ def test_batched_decode_stagewise_7b():
                host(vc).view(np.uint16), np.full(nseq, ctx - 1), np.full(nseq, ctx),
                np.arange(nseq) * stride, host(out).reshape(nseq, s.hidden))
     L.close()
-
 
 
 # Batched decode over ragged per-sequence contexts (ctx_dev), for every KV
