@@ -194,6 +194,22 @@ int si_attention(const si_shape_t *s, const float *q, int nq, const uint16_t *kc
                  void *stream);
 size_t si_attention_workspace(const si_shape_t *s, int nq, int max_ctx);
 
+/* si_attention without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * partial states live in one fixed buffer of SI_ATTENTION_STATIC_MAX bytes
+ * per GPU inside the library (held until the process ends); the call
+ * allocates nothing and returns SI_ERR_ARG when
+ * si_attention_workspace(s, nq, max_ctx) exceeds that size.  Every call on
+ * a GPU shares its buffer: calls that overlap on one GPU (other streams or
+ * host threads) race; calls ordered on one stream do not.  Results are
+ * bit-identical to si_attention's on the same inputs. */
+#define SI_ATTENTION_STATIC_MAX (16u << 20)
+int si_attention_static(const si_shape_t *s, const float *q, int nq, const uint16_t *kc,
+                        const uint16_t *vc, size_t kv_seq_stride, const int *ctx_dev, int ctx0,
+                        int ctx_step, int max_ctx, float *attn, int8_t *qs, uint16_t *d,
+                        int16_t *bsum, void *stream);
+
 /* attention_standard (attention_kernels.h:33-78) for one query: scores
  * [qheads][context] fp32 (device, caller-owned like the reference's
  * score_workspace) receive the scaled Q.K products (the reference's bits:

@@ -11,6 +11,7 @@
 #include <string.h>
 
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -272,24 +273,31 @@ size_t si_attention_workspace(const si_shape_t *s, int nq, int max_ctx) {
     return a > p ? a : p;
 }
 
-int si_attention(const si_shape_t *s, const float *q, int nq, const uint16_t *kc,
-                 const uint16_t *vc, size_t kv_seq_stride, const int *ctx_dev, int ctx0,
-                 int ctx_step, int max_ctx, float *attn, int8_t *qs, uint16_t *d,
-                 int16_t *bsum, void *ws, size_t ws_bytes, void *stream) {
+}  // extern "C"
+
+// Shared body of si_attention and si_attention_static: argument checks, then
+// the causal-prefill flash kernel or the split-context decode kernels with
+// their partial states in ws (ws_bytes of it).
+static int attention_impl(const char *what, const si_shape_t *s, const float *q, int nq,
+                          const uint16_t *kc, const uint16_t *vc, size_t kv_seq_stride,
+                          const int *ctx_dev, int ctx0, int ctx_step, int max_ctx, float *attn,
+                          int8_t *qs, uint16_t *d, int16_t *bsum, void *ws, size_t ws_bytes,
+                          void *stream) {
     int r = check_shape(s);
     if (r) return r;
-    SI_REQUIRE(nq >= 0 && max_ctx >= 1, "attention: bad nq/max_ctx");
-    SI_REQUIRE(kv_seq_stride % 8 == 0, "attention: kv_seq_stride must be a multiple of 8");
+    SI_REQUIRE(nq >= 0 && max_ctx >= 1, "%s: bad nq/max_ctx", what);
+    SI_REQUIRE(kv_seq_stride % 8 == 0, "%s: kv_seq_stride must be a multiple of 8", what);
     if (!ctx_dev) {
         // attention_kernels.h:95 handles context <= 0 by zeroing; a layer call
         // always has context >= 1 (qwen_one_layer.c:608), required here.
-        SI_REQUIRE(ctx0 >= 1 && ctx_step >= 0, "attention: contexts must be >= 1");
+        SI_REQUIRE(ctx0 >= 1 && ctx_step >= 0, "%s: contexts must be >= 1", what);
         SI_REQUIRE((long)ctx0 + (long)(nq - 1) * ctx_step <= max_ctx,
-                   "attention: context exceeds max_ctx");
+                   "%s: context exceeds max_ctx", what);
     }
-    SI_REQUIRE(nq == 0 || (q && kc && vc && attn && ws), "attention: NULL pointer");
-    SI_REQUIRE(!qs || d, "attention: qs without d");
-    SI_REQUIRE(ws_bytes >= si_attention_workspace(s, nq, max_ctx), "attention: workspace too small");
+    SI_REQUIRE(nq == 0 || (q && kc && vc && attn && ws), "%s: NULL pointer", what);
+    SI_REQUIRE(!qs || d, "%s: qs without d", what);
+    SI_REQUIRE(ws_bytes >= si_attention_workspace(s, nq, max_ctx), "%s: workspace too small",
+               what);
     if (!ctx_dev && ctx_step == 1 && kv_seq_stride == 0 && nq > 1 &&
         attn_prefill_supported(s->qheads, s->kvheads, s->hdim))
         // causal prefill of one sequence: the flash kernel (query i at
@@ -299,7 +307,67 @@ int si_attention(const si_shape_t *s, const float *q, int nq, const uint16_t *kc
     else
         launch_attention(q, nq, s->qheads, s->kvheads, s->hdim, kc, vc, kv_seq_stride, ctx_dev,
                          ctx0, ctx_step, max_ctx, attn, qs, d, bsum, ws, S(stream));
-    return check_launch("si_attention");
+    return check_launch(what);
+}
+
+// The attention partial states of si_attention_static: one fixed buffer per
+// GPU, in the code object's device memory, so the call allocates nothing.
+// Its host-side name is only a stand-in: kernels and copies use the device
+// address hipGetSymbolAddress returns, taken once per device (each GPU
+// holds its own copy of the array at its own address).
+static __device__ __align__(256) uint8_t scratch[SI_ATTENTION_STATIC_MAX];
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_dev[kMaxDevices];
+
+static int static_scratch(void **out) {
+    int dev = -1;
+    HIP_TRY(hipGetDevice(&dev));
+    SI_REQUIRE(dev >= 0 && dev < kMaxDevices, "attention_static: device %d beyond %d", dev,
+               kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(SI_ERR_HIP, "attention_static: hipGetSymbolAddress: %s",
+                        hipGetErrorString(e));
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return SI_OK;
+}
+
+extern "C" {
+
+int si_attention(const si_shape_t *s, const float *q, int nq, const uint16_t *kc,
+                 const uint16_t *vc, size_t kv_seq_stride, const int *ctx_dev, int ctx0,
+                 int ctx_step, int max_ctx, float *attn, int8_t *qs, uint16_t *d,
+                 int16_t *bsum, void *ws, size_t ws_bytes, void *stream) {
+    return attention_impl("si_attention", s, q, nq, kc, vc, kv_seq_stride, ctx_dev, ctx0,
+                          ctx_step, max_ctx, attn, qs, d, bsum, ws, ws_bytes, stream);
+}
+
+int si_attention_static(const si_shape_t *s, const float *q, int nq, const uint16_t *kc,
+                        const uint16_t *vc, size_t kv_seq_stride, const int *ctx_dev, int ctx0,
+                        int ctx_step, int max_ctx, float *attn, int8_t *qs, uint16_t *d,
+                        int16_t *bsum, void *stream) {
+    int r = check_shape(s);
+    if (r) return r;
+    SI_REQUIRE(nq >= 0 && max_ctx >= 1, "si_attention_static: bad nq/max_ctx");
+    const size_t need = si_attention_workspace(s, nq, max_ctx);
+    SI_REQUIRE(need <= (size_t)SI_ATTENTION_STATIC_MAX,
+               "si_attention_static: %d queries over max_ctx %d need %zu bytes of partial "
+               "states, beyond the static buffer's %zu (use si_attention with a workspace)",
+               nq, max_ctx, need, (size_t)SI_ATTENTION_STATIC_MAX);
+    void *ws = nullptr;
+    if (nq > 0) {
+        r = static_scratch(&ws);
+        if (r) return r;
+    }
+    return attention_impl("si_attention_static", s, q, nq, kc, vc, kv_seq_stride, ctx_dev,
+                          ctx0, ctx_step, max_ctx, attn, qs, d, bsum, ws,
+                          (size_t)SI_ATTENTION_STATIC_MAX, stream);
 }
 
 int si_attention_standard(const si_shape_t *s, const float *q, const uint16_t *kc,

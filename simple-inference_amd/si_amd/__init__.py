@@ -89,6 +89,8 @@ _SIGS = {
     "si_attention": (_I, [ctypes.POINTER(Shape), _P, _I, _P, _P, _Z, _P, _I, _I, _I, _P, _P,
                           _P, _P, _P, _Z, _P]),
     "si_attention_workspace": (_Z, [ctypes.POINTER(Shape), _I, _I]),
+    "si_attention_static": (_I, [ctypes.POINTER(Shape), _P, _I, _P, _P, _Z, _P, _I, _I, _I, _P,
+                                 _P, _P, _P, _P]),
     "si_attention_standard": (_I, [ctypes.POINTER(Shape), _P, _P, _P, _I, _P, _P, _P]),
     "si_swiglu_q8": (_I, [_P, _I, _I, _P, _P, _P, _P, _P]),
     "si_layer_create": (_I, [ctypes.POINTER(Shape), ctypes.POINTER(LayerHost), _I, _I,
