@@ -231,6 +231,57 @@ int si_residual_rmsnorm_q8(const float *x, const float *y, const float *gain,
                            int8_t *qs, uint16_t *d, int16_t *s, void *stream);
 
 /* ------------------------------------------------------------------ */
+/* The reference's own formats (behind the host mirror's drop-ins)     */
+/* ------------------------------------------------------------------ */
+
+/* f32_to_f16 / f16_to_f32 (qwen_one_layer.c:42-86) over n device values:
+ * round to nearest even with subnormals, NaN -> sign|0x7e00, overflow ->
+ * sign|inf; the widening is exact (bit-exact both ways). */
+int si_f32_to_f16(const float *src, uint16_t *dst, size_t n, void *stream);
+int si_f16_to_f32(const uint16_t *src, float *dst, size_t n, void *stream);
+
+/* matvec_q4q8 (qwen_one_layer.c:148-162) on the reference's formats:
+ * w row-major Q4_0 ([outputs][inputs/32] 18-byte blocks), x block_q8_0
+ * records ([inputs/32] x 34 bytes, defines.h:27-28), both 2-byte aligned;
+ * out[r] = bias[r] (0 when NULL) + sum over blocks in order of
+ * ((float)dot * w.d) * x.d, the reference's roundings (bit-exact). */
+int si_matvec_q4q8_rowmajor(const uint8_t *w, const void *x_blocks, int inputs, int outputs,
+                            const float *bias, float *out, void *stream);
+
+/* fused_column_matvec (fused_layer.h:169-245) over ntiles consecutive
+ * column-SoA tiles of nblocks 5120-byte groups (the layout
+ * repack_weights.py writes: per input block 32 columns x 128 packed bytes,
+ * low nibble = output j, high = output j+128, then 256 fp32 scales).  Tile
+ * t writes out[t*256 .. t*256+255]: with add == 0 it starts from
+ * bias_lo[t*256 + j] / bias_hi[t*256 + j] (0 when NULL), with add != 0 from
+ * the current out values; each block adds ((float)sum * scale) * x.d
+ * (bit-exact).  x_blocks: nblocks block_q8_0 records; tiles 4-byte aligned. */
+int si_colsoa_matvec(const uint8_t *tiles, int ntiles, const void *x_blocks, int nblocks,
+                     const float *bias_lo, const float *bias_hi, float *out, int add,
+                     void *stream);
+
+/* rmsnorm (qwen_one_layer.c:164-169) of rows x n values, without the Q8
+ * step: out = (x * inv) * gain (gain NULL = 1). */
+int si_rmsnorm(const float *x, const float *gain, int rows, int n, float eps, float *out,
+               void *stream);
+
+/* rope (qwen_one_layer.c:172-183) in place on nheads heads of s->hdim
+ * values at `position`, with si_rope_table cos/sin tables of max_pos rows
+ * on the device (bit-exact). */
+int si_rope(const si_shape_t *s, float *heads, int nheads, int position, const float *rope_cos,
+            const float *rope_sin, int max_pos, void *stream);
+
+/* attention_flash (attention_kernels.h:80-164) for nheads query heads that
+ * share KV group `group` of s's cache layout (fused_attention_pair,
+ * fused_layer.h:251-355, is nheads = 2): q [nheads][hdim], kc/vc the
+ * [context][kvheads][hdim] fp16 caches, out [nheads][hdim].  workspace:
+ * si_attention_group_workspace bytes. */
+int si_attention_group(const si_shape_t *s, const float *q, int nheads, int group,
+                       const uint16_t *kc, const uint16_t *vc, int context, float *out,
+                       void *workspace, size_t ws_bytes, void *stream);
+size_t si_attention_group_workspace(const si_shape_t *s, int nheads, int context);
+
+/* ------------------------------------------------------------------ */
 /* Layer level (run_layer / run_layer_fused / pf_run_batch)            */
 /* ------------------------------------------------------------------ */
 

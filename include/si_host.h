@@ -5,9 +5,14 @@
  * Same names, argument meaning and error behaviour as the reference:
  *   - run_layer           qwen_one_layer.c:237-281
  *   - run_layer_fused     register_fusion.h:344-411 (same math on the GPU)
+ *   - run_layer_legacy_fused, attention_wo_fused, fused_attention_pair,
+ *     fused_column_matvec    fused_layer.h:169-455 (column-SoA tiles)
+ *   - fused_weights_load / fused_weights_free  fused_layer.h:131-146
  *   - pf_run_batch        prefill_weight_stationary.h:183-311
  *   - attention_compute   attention_kernels.h:166-173
  *   - attention_flash     attention_kernels.h:80-164
+ *   - matvec_q4q8         qwen_one_layer.c:148-162
+ *   - rmsnorm, rope       qwen_one_layer.c:164-183
  *   - quantize_q8         qwen_one_layer.c:98-116
  *   - load_layer / free_layer  qwen_one_layer.c:188-226
  * Differences, all forced by the device boundary:
@@ -18,6 +23,9 @@
  *     load_layer;
  *   - errors still never return: they print and exit(1) like die()
  *     (qwen_one_layer.c:26-28);
+ *   - functions whose size the reference takes from defines.h (rmsnorm,
+ *     rope, the pair attention) take the loaded layer, whose runtime shape,
+ *     RoPE tables and stream they use;
  *   - timings (phase_t) are GPU event times in seconds.  The decode kernels
  *     fuse RMSNorm + Q8 into the Q/K/V projection, RoPE + K/V append into
  *     attention and the attention output's Q8 into W_O: a fused phase is
@@ -63,7 +71,24 @@ typedef struct {
     int max_pos;
     void *attn_ws;     /* device workspace for attention_compute/_flash */
     size_t attn_ws_bytes;
+    float *rope_cos, *rope_sin;  /* device [max_pos][hdim/2] (si_rope_table) */
+    float *norm, *bq, *bk, *bv;  /* device copies (NULL = identity / zero), for
+                                    the column-SoA path */
 } si_model_t;
+
+/* fused_layer.h:60-66: the column-SoA weights repack_weights.py writes
+ * (q.colsoa, kv.colsoa, o.colsoa), on the device, plus the device scratch
+ * of the legacy fused path.  There is no scratchpad (TCM) on the GPU.  The
+ * layout needs hdim 128 (a tile is one query-head pair, or one KV group's
+ * 128 K and 128 V rows), an even number of query heads per KV group and
+ * hidden a multiple of 256 (W_O output tiles); si_colsoa_bytes is 0 for
+ * other shapes. */
+typedef struct {
+    uint8_t *q, *kv, *o;
+    size_t q_bytes, kv_bytes, o_bytes;
+    float *normed, *kvpair, *qpair, *opair;
+    block_q8_0 *inq8, *oq;
+} fused_weights_t;
 
 /* load_layer (qwen_one_layer.c:210-221): reads q.q4_0 k.q4_0 v.q4_0 o.q4_0
  * and the optional norm.f32 q_bias.f32 k_bias.f32 v_bias.f32 from dir with
@@ -86,10 +111,62 @@ phase_t run_layer(const si_model_t *l, const float *x, uint16_t *kc, uint16_t *v
                   int context, float *output, attention_method_t method, float *scores,
                   float *attn_copy, block_q8_0 *q8_copy);
 
-/* register_fusion.h:344-411: identical result contract to run_layer. */
-fused_stats_t run_layer_fused(const si_model_t *l, const float *x, uint16_t *kc,
-                              uint16_t *vc, int context, float *output, float *attn_capture,
-                              block_q8_0 *q8_capture);
+/* register_fusion.h:344-411: identical result contract to run_layer, run by
+ * the fused decode kernels on the layer's own repacked weights (the GPU's
+ * counterpart of the register-resident path).  fw (the same weights as
+ * column-SoA tiles) may be NULL; run_layer_legacy_fused is the path that
+ * reads it. */
+fused_stats_t run_layer_fused(const si_model_t *l, const fused_weights_t *fw, const float *x,
+                              uint16_t *kc, uint16_t *vc, int context, float *output,
+                              float *attn_capture, block_q8_0 *q8_capture);
+
+/* fused_layer.h:397-455 on the device, over the column-SoA tiles of fw:
+ * per KV group the K/V tile (+bias), RoPE of K and the fp16 append at row
+ * context-1; per head pair the Q tile (+bias), RoPE, the pair's attention,
+ * Q8 of its 256 values and the W_O partial added into the zeroed output.
+ * Captures are HOST buffers or NULL.  Phase times are host wall-clock
+ * seconds around each synchronized stage. */
+fused_stats_t run_layer_legacy_fused(const si_model_t *l, const fused_weights_t *fw,
+                                     const float *x, uint16_t *kc, uint16_t *vc, int context,
+                                     float *output, float *attn_capture,
+                                     block_q8_0 *q8_capture);
+
+/* fused_layer.h:361-390: fused_attention_pair of qpair (device, the pair's
+ * two rotated query heads), quantize_q8 of the 256 outputs, and the pair's
+ * W_O tiles of fw added into output_y (device [hidden]).  The captures
+ * (HOST, or NULL) receive the pair's slice at pair*256 / pair*8. */
+void attention_wo_fused(const si_model_t *l, const fused_weights_t *fw, const float *qpair,
+                        const uint16_t *kc, const uint16_t *vc, int context, int group, int pair,
+                        float *output_y, fused_stats_t *stats, float *attention_capture,
+                        block_q8_0 *quantized_capture);
+
+/* fused_layer.h:251-355: attention of two query heads (qpair [2][hdim],
+ * device) over KV group `group` of the device caches into opair. */
+void fused_attention_pair(const si_model_t *l, const float *qpair, const uint16_t *kc,
+                          const uint16_t *vc, int context, int group, float *opair);
+
+/* fused_layer.h:169-245 on device buffers: one column-SoA tile of nblocks
+ * groups against nblocks block_q8_0 records into output[256]; add = 0
+ * starts from bias_lo/bias_hi (128 each, NULL = 0), add != 0 accumulates. */
+void fused_column_matvec(const uint8_t *tile, const block_q8_0 *x, int nblocks,
+                         const float *bias_lo, const float *bias_hi, float *output, int add);
+
+/* fused_layer.h:131-139: reads q.colsoa, kv.colsoa and o.colsoa from dir
+ * (exact sizes for the layer's shape) onto the device.  use_tcm must be 0:
+ * there is no scratchpad to stage tiles in. */
+fused_weights_t fused_weights_load(const si_model_t *l, const char *dir, int use_tcm, int block);
+/* Same from column-SoA tiles in host memory. */
+fused_weights_t si_fused_weights_from_host(const si_model_t *l, const uint8_t *q,
+                                           const uint8_t *kv, const uint8_t *o);
+void fused_weights_free(fused_weights_t *fw);
+
+/* Bytes of q.colsoa (which 0), kv.colsoa (1) or o.colsoa (2) for a shape;
+ * 0 when the shape has no column-SoA layout. */
+size_t si_colsoa_bytes(const si_shape_t *s, int which);
+/* repack_weights.py:55-120 in C: the three column-SoA files from the
+ * row-major Q4_0 matrices of w (host memory; sizes from si_colsoa_bytes). */
+void si_colsoa_repack_host(const si_shape_t *s, const si_layer_host_t *w, uint8_t *q,
+                           uint8_t *kv, uint8_t *o);
 
 /* Full build-defined Qwen2 layer (attention + residual + post-norm + SwiGLU
  * FFN + residual) for one token. */
@@ -112,6 +189,20 @@ void attention_compute(const si_model_t *l, attention_method_t method, const flo
 
 /* qwen_one_layer.c:98-116 on device buffers (dst: block_q8_0 records). */
 void quantize_q8(const float *src, block_q8_0 *dst, int count);
+
+/* qwen_one_layer.c:148-162 on device buffers: weights row-major Q4_0
+ * [outputs][inputs/32], input block_q8_0 [inputs/32], bias [outputs] or
+ * NULL; the reference's block order and roundings (bit-exact). */
+void matvec_q4q8(const uint8_t *weights, const block_q8_0 *input, int inputs, int outputs,
+                 const float *bias, float *out);
+
+/* qwen_one_layer.c:164-169: out = rmsnorm(input) * weight (NULL = 1) over
+ * the layer's hidden size, device buffers. */
+void rmsnorm(const si_model_t *l, const float *input, const float *weight, float *out);
+
+/* qwen_one_layer.c:172-183: rotates nheads heads of hdim values (device) in
+ * place at `position` (0..max_pos-1), angles from the layer's tables. */
+void rope(const si_model_t *l, float *heads, int nheads, int position);
 
 /* ------------------------------------------------------------------ */
 /* Paged KV bookkeeping and a multi-layer decode stack (si_kvpages.c). */

@@ -95,6 +95,15 @@ class Oracle:
         L.or_layer_prefill.argtypes = [ctypes.POINTER(Shape), ctypes.POINTER(_Layer), _P,
                                        ctypes.c_int, ctypes.c_int, _P, _P, _P,
                                        ctypes.c_int, ctypes.c_int, _P]
+        L.or_colsoa_bytes.restype = ctypes.c_size_t
+        L.or_colsoa_bytes.argtypes = [ctypes.POINTER(Shape), ctypes.c_int]
+        L.or_colsoa_repack.argtypes = [ctypes.POINTER(Shape)] + [_P] * 7
+        L.or_fused_column_matvec.argtypes = [_P, _P, ctypes.c_int, _P, _P, _P, ctypes.c_int]
+        L.or_attention_pair.argtypes = [ctypes.POINTER(Shape), _P, _P, _P, ctypes.c_int,
+                                        ctypes.c_int, _P]
+        L.or_run_layer_legacy_fused.argtypes = [ctypes.POINTER(Shape), ctypes.POINTER(_Layer),
+                                                _P, _P, _P, _P, _P, _P, ctypes.c_int, _P, _P,
+                                                _P]
         L.or_quantize_q4_0.argtypes = [_P, _P, ctypes.c_int]
         L.or_dequantize_q4_0.argtypes = [_P, _P, ctypes.c_int]
 
@@ -194,6 +203,45 @@ class Oracle:
         self.lib.or_dequantize_q4_0(_ptr(np.ascontiguousarray(q)), _ptr(out), count)
         return out
 
+    # ---- column-SoA tiles and the legacy fused path (hdim 128) ----
+    def colsoa_repack(self, shape, layer):
+        """(q, kv, o) tile bytes of repack_weights.py's layout."""
+        bufs = [np.zeros(self.lib.or_colsoa_bytes(ctypes.byref(shape), i), np.uint8)
+                for i in range(3)]
+        w = [np.ascontiguousarray(layer[k], np.uint8) for k in ("wq", "wk", "wv", "wo")]
+        self.lib.or_colsoa_repack(ctypes.byref(shape), *[_ptr(a) for a in w],
+                                  *[_ptr(b) for b in bufs])
+        return tuple(bufs)
+
+    def fused_column_matvec(self, tile, xq, nblocks, bias_lo=None, bias_hi=None, out=None,
+                            add=False):
+        y = np.zeros(256, np.float32) if out is None else np.array(out, np.float32, copy=True)
+        bl = None if bias_lo is None else np.ascontiguousarray(bias_lo, np.float32)
+        bh = None if bias_hi is None else np.ascontiguousarray(bias_hi, np.float32)
+        self.lib.or_fused_column_matvec(_ptr(np.ascontiguousarray(tile, np.uint8)),
+                                        _ptr(np.ascontiguousarray(xq)), nblocks, _ptr(bl),
+                                        _ptr(bh), _ptr(y), int(add))
+        return y
+
+    def attention_pair(self, shape, qpair, kc, vc, context, group):
+        out = np.empty(2 * shape.hdim, np.float32)
+        self.lib.or_attention_pair(ctypes.byref(shape),
+                                   _ptr(np.ascontiguousarray(qpair, np.float32)), _ptr(kc),
+                                   _ptr(vc), context, group, _ptr(out))
+        return out
+
+    def run_layer_legacy_fused(self, shape, layer, tiles, x, kc, vc, context):
+        """(out, attention capture, Q8 capture); kc/vc get the new row."""
+        lay, keep = self._layer(layer)
+        out = np.empty(shape.hidden, np.float32)
+        att = np.empty(shape.qheads * shape.hdim, np.float32)
+        q8 = np.zeros(shape.qheads * shape.hdim // QK, Q8_DTYPE)
+        self.lib.or_run_layer_legacy_fused(ctypes.byref(shape), ctypes.byref(lay),
+                                           *[_ptr(t) for t in tiles], _ptr(x), _ptr(kc),
+                                           _ptr(vc), context, _ptr(out), _ptr(att), _ptr(q8))
+        del keep
+        return out, att, q8
+
     # ---- layers ----
     @staticmethod
     def _layer(layer):
@@ -279,6 +327,10 @@ class Reference:
         L.si_ref_attention_flash.argtypes = [_P, _P, _P, ctypes.c_int, _P]
         L.si_ref_attention_standard.argtypes = [_P, _P, _P, ctypes.c_int, _P, _P]
         L.si_ref_run_layer.argtypes = [_P] * 11 + [ctypes.c_int, _P, ctypes.c_int, _P, _P, _P]
+        L.si_ref_fused_column_matvec.argtypes = [_P, _P, ctypes.c_int, _P, _P, _P,
+                                                 ctypes.c_int]
+        L.si_ref_fused_attention_pair.argtypes = [_P, _P, _P, ctypes.c_int, ctypes.c_int, _P]
+        L.si_ref_run_layer_fused.argtypes = [_P] * 14 + [ctypes.c_int, _P, _P, _P]
         self.hidden = L.si_ref_hidden()
         self.qheads = L.si_ref_qheads()
         self.kvheads = L.si_ref_kvheads()
@@ -356,6 +408,35 @@ class Reference:
                                   _ptr(g("norm")), _ptr(g("bq")), _ptr(g("bk")),
                                   _ptr(g("bv")), _ptr(x), _ptr(kc), _ptr(vc), context,
                                   _ptr(out), method, _ptr(scores), _ptr(attn), _ptr(q8))
+        return out, attn, q8
+
+
+    def fused_column_matvec(self, tile, xq, nblocks, bias_lo=None, bias_hi=None, out=None,
+                            add=False):
+        y = np.zeros(256, np.float32) if out is None else np.array(out, np.float32, copy=True)
+        bl = None if bias_lo is None else np.ascontiguousarray(bias_lo, np.float32)
+        bh = None if bias_hi is None else np.ascontiguousarray(bias_hi, np.float32)
+        self.lib.si_ref_fused_column_matvec(_ptr(np.ascontiguousarray(tile, np.uint8)),
+                                            _ptr(np.ascontiguousarray(xq)), nblocks, _ptr(bl),
+                                            _ptr(bh), _ptr(y), int(add))
+        return y
+
+    def attention_pair(self, qpair, kc, vc, context, group):
+        out = np.empty(2 * self.hdim, np.float32)
+        self.lib.si_ref_fused_attention_pair(_ptr(np.ascontiguousarray(qpair, np.float32)),
+                                             _ptr(kc), _ptr(vc), context, group, _ptr(out))
+        return out
+
+    def run_layer_fused(self, layer, tiles, x, kc, vc, context):
+        out = np.empty(self.hidden, np.float32)
+        attn = np.empty(self.qheads * self.hdim, np.float32)
+        q8 = np.zeros(self.qheads * self.hdim // QK, Q8_DTYPE)
+        g = layer.get
+        self.lib.si_ref_run_layer_fused(_ptr(g("wq")), _ptr(g("wk")), _ptr(g("wv")),
+                                        _ptr(g("wo")), _ptr(g("norm")), _ptr(g("bq")),
+                                        _ptr(g("bk")), _ptr(g("bv")), *[_ptr(t) for t in tiles],
+                                        _ptr(x), _ptr(kc), _ptr(vc), context, _ptr(out),
+                                        _ptr(attn), _ptr(q8))
         return out, attn, q8
 
 

@@ -70,3 +70,32 @@ void si_ref_run_layer(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv,
     (void)run_layer(&l, x, kc, vc, context, out, (attention_method_t)method,
                     scores, attn_copy, q8_copy);
 }
+
+/* The column-SoA path (fused_layer.h), portable build. */
+void si_ref_fused_column_matvec(const uint8_t *tile, const block_q8_0 *x, int nblocks,
+                                const float *bias_lo, const float *bias_hi, float *out,
+                                int add) {
+    fused_column_matvec(tile, x, nblocks, bias_lo, bias_hi, out, add);
+}
+void si_ref_fused_attention_pair(const float *qpair, const uint16_t *kc, const uint16_t *vc,
+                                 int context, int group, float *opair) {
+    fused_attention_pair(qpair, kc, vc, context, group, opair);
+}
+/* run_layer_fused (register_fusion.h:344-411): in the portable build it is
+ * run_layer_legacy_fused (fused_layer.h:397-455) over q/kv/o column-SoA
+ * tiles held in memory (no TCM). */
+void si_ref_run_layer_fused(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv,
+                            const uint8_t *wo, const float *norm, const float *bq,
+                            const float *bk, const float *bv, const uint8_t *qt,
+                            const uint8_t *kvt, const uint8_t *ot, const float *x, uint16_t *kc,
+                            uint16_t *vc, int context, float *out, float *attn_capture,
+                            block_q8_0 *q8_capture) {
+    layer_t l;
+    l.wq = (uint8_t *)wq; l.wk = (uint8_t *)wk; l.wv = (uint8_t *)wv; l.wo = (uint8_t *)wo;
+    l.norm = (float *)norm; l.bq = (float *)bq; l.bk = (float *)bk; l.bv = (float *)bv;
+    fused_weights_t fw;
+    memset(&fw, 0, sizeof fw);
+    fw.q = (uint8_t *)qt; fw.kv = (uint8_t *)kvt; fw.o = (uint8_t *)ot;
+    fw.tcm_fd = -1;
+    (void)run_layer_fused(&l, &fw, x, kc, vc, context, out, attn_capture, q8_capture);
+}

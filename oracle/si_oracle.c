@@ -536,3 +536,193 @@ void or_dequantize_q4_0(const uint8_t *src, float *dst, int count) {
         }
     }
 }
+
+/* ---- Column-SoA tiles (repack_weights.py) and the legacy fused decode path
+ *      (fused_layer.h:169-455).  Written for hdim 128: a tile holds 256
+ *      outputs, i.e. two query heads, or the 128 K and 128 V outputs of one KV
+ *      group; query heads pair up within their KV group; W_O splits into
+ *      256-row output tiles. ---- */
+
+#define OR_COL_GROUP 5120 /* fused_layer.h:33: 32 columns x 128 B + 256 fp32 scales */
+
+static void check_colsoa_shape(const or_shape_t *s) {
+    check_shape(s);
+    if (s->hdim != 128 || (s->qheads / s->kvheads) % 2 || s->hidden % 256)
+        or_die("column-SoA tiles need hdim 128, paired query heads and hidden % 256 == 0");
+}
+
+size_t or_colsoa_bytes(const or_shape_t *s, int which) {
+    const size_t nb = (size_t)s->hidden / OR_QK, pairs = (size_t)s->qheads / 2;
+    switch (which) {
+        case 0: return pairs * nb * OR_COL_GROUP;                           /* q.colsoa  */
+        case 1: return (size_t)s->kvheads * nb * OR_COL_GROUP;              /* kv.colsoa */
+        default: return pairs * ((size_t)s->hidden / 256) * 8 * OR_COL_GROUP; /* o.colsoa */
+    }
+}
+
+/* repack_weights.py:39-52 (nibble, scale_f32): element `col` of row `row`
+ * of a row-major Q4_0 matrix with `cols` inputs. */
+static unsigned q4_nibble(const uint8_t *w, int cols, int row, int col) {
+    const uint8_t *blk = w + ((size_t)row * (cols / OR_QK) + col / OR_QK) * OR_Q4_BYTES;
+    const int k = col % OR_QK;
+    const uint8_t byte = blk[2 + k % 16];
+    return k < 16 ? (byte & 15u) : (unsigned)(byte >> 4);
+}
+
+/* repack_weights.py:55-76 (pack_tile): nblocks groups from input block b0;
+ * low nibbles = rows lo_row..lo_row+127 of lo, high = hi_row.. of hi. */
+static void pack_tile(uint8_t *dst, const uint8_t *lo, const uint8_t *hi, int cols, int lo_row,
+                      int hi_row, int b0, int nblocks) {
+    for (int b = 0; b < nblocks; ++b) {
+        uint8_t *g = dst + (size_t)b * OR_COL_GROUP;
+        const int blk = b0 + b;
+        for (int k = 0; k < OR_QK; ++k)
+            for (int j = 0; j < 128; ++j)
+                g[k * 128 + j] = (uint8_t)(q4_nibble(lo, cols, lo_row + j, blk * OR_QK + k) |
+                                           q4_nibble(hi, cols, hi_row + j, blk * OR_QK + k) << 4);
+        for (int j = 0; j < 256; ++j) {
+            const uint8_t *src = j < 128 ? lo : hi;
+            const int row = j < 128 ? lo_row + j : hi_row + j - 128;
+            const uint8_t *e = src + ((size_t)row * (cols / OR_QK) + blk) * OR_Q4_BYTES;
+            const float sc = or_f16_to_f32((uint16_t)(e[0] | e[1] << 8));
+            memcpy(g + 4096 + 4 * j, &sc, 4);
+        }
+    }
+}
+
+/* repack_weights.py:96-120: q tiles per head pair, kv tiles per KV group
+ * (K rows low, V rows high), o tiles per input head pair x 256-row output
+ * tile (8 blocks each). */
+void or_colsoa_repack(const or_shape_t *s, const uint8_t *wq, const uint8_t *wk,
+                      const uint8_t *wv, const uint8_t *wo, uint8_t *q, uint8_t *kv,
+                      uint8_t *o) {
+    check_colsoa_shape(s);
+    const int H = s->hidden, QD = s->qheads * s->hdim, nb = H / OR_QK, pairs = s->qheads / 2;
+    const size_t tile = (size_t)nb * OR_COL_GROUP, sub = 8 * (size_t)OR_COL_GROUP;
+    for (int p = 0; p < pairs; ++p) pack_tile(q + p * tile, wq, wq, H, p * 256, p * 256 + 128, 0, nb);
+    for (int g = 0; g < s->kvheads; ++g)
+        pack_tile(kv + g * tile, wk, wv, H, g * 128, g * 128, 0, nb);
+    for (int p = 0; p < pairs; ++p)
+        for (int y = 0; y < H / 256; ++y)
+            pack_tile(o + ((size_t)p * (H / 256) + y) * sub, wo, wo, QD, y * 256, y * 256 + 128,
+                      p * 8, 8);
+}
+
+/* fused_column_matvec, scalar path (fused_layer.h:220-244). */
+void or_fused_column_matvec(const uint8_t *tile, const or_block_q8_0 *x, int nblocks,
+                            const float *bias_lo, const float *bias_hi, float *out, int add) {
+    if (!add)
+        for (int j = 0; j < 128; ++j) {
+            out[j] = bias_lo ? bias_lo[j] : 0.0f;
+            out[j + 128] = bias_hi ? bias_hi[j] : 0.0f;
+        }
+    for (int b = 0; b < nblocks; ++b) {
+        const uint8_t *g = tile + (size_t)b * OR_COL_GROUP;
+        int32_t acc[256];
+        memset(acc, 0, sizeof acc);
+        for (int k = 0; k < OR_QK; ++k) {
+            const int a = x[b].qs[k];
+            for (int j = 0; j < 128; ++j) {
+                const uint8_t w = g[k * 128 + j];
+                acc[j] += ((int)(w & 15) - 8) * a;
+                acc[j + 128] += ((int)(w >> 4) - 8) * a;
+            }
+        }
+        const float dx = or_f16_to_f32(x[b].d);
+        for (int j = 0; j < 256; ++j) {
+            float sc;
+            memcpy(&sc, g + 4096 + 4 * j, 4);
+            out[j] += ((float)acc[j] * sc) * dx;
+        }
+    }
+}
+
+/* fused_attention_pair, scalar path (fused_layer.h:251-355): query heads
+ * 2h' and 2h'+1 of qpair against KV group `group`; the one-exp-per-token
+ * recurrence of attention_flash. */
+void or_attention_pair(const or_shape_t *s, const float *qpair, const uint16_t *kc,
+                       const uint16_t *vc, int context, int group, float *opair) {
+    const int D = s->hdim;
+    const float inv_dim = 1.0f / sqrtf((float)D);
+    const size_t stride = (size_t)s->kvheads * D;
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
+    memset(opair, 0, sizeof(float) * 2 * D);
+    for (int t = 0; t < context; ++t) {
+        const uint16_t *k = kc + (size_t)t * stride + (size_t)group * D;
+        const uint16_t *v = vc + (size_t)t * stride + (size_t)group * D;
+        for (int h = 0; h < 2; ++h) {
+            const float *qh = qpair + h * D;
+            float *o = opair + h * D;
+            float sc = 0.0f;
+            for (int d = 0; d < D; ++d) sc += qh[d] * or_f16_to_f32(k[d]);
+            sc *= inv_dim;
+            if (t == 0) {
+                m[h] = sc;
+                l[h] = 1.0f;
+                for (int d = 0; d < D; ++d) o[d] = or_f16_to_f32(v[d]);
+            } else if (sc > m[h]) {
+                const float alpha = expf(m[h] - sc);
+                l[h] = l[h] * alpha + 1.0f;
+                for (int d = 0; d < D; ++d) o[d] = o[d] * alpha + or_f16_to_f32(v[d]);
+                m[h] = sc;
+            } else {
+                const float beta = expf(sc - m[h]);
+                l[h] += beta;
+                for (int d = 0; d < D; ++d) o[d] += beta * or_f16_to_f32(v[d]);
+            }
+        }
+    }
+    for (int h = 0; h < 2; ++h)
+        for (int d = 0; d < D; ++d) opair[h * D + d] *= 1.0f / l[h];
+}
+
+/* run_layer_legacy_fused (fused_layer.h:397-455) with attention_wo_fused
+ * (:361-390): per KV group the K/V tile (+bias), RoPE of K, fp16 append;
+ * per head pair the Q tile (+bias), RoPE, pair attention, Q8 of its 256
+ * values and the W_O partial added into the zeroed output, tile by tile.
+ * Captures (fp32 [qheads*hdim], Q8 [qheads*hdim/32]) may be NULL. */
+void or_run_layer_legacy_fused(const or_shape_t *s, const or_layer_t *l, const uint8_t *qt,
+                               const uint8_t *kvt, const uint8_t *ot, const float *x,
+                               uint16_t *kc, uint16_t *vc, int context, float *out,
+                               float *attn_capture, or_block_q8_0 *q8_capture) {
+    check_colsoa_shape(s);
+    if (context < 1) or_die("context must be >= 1");
+    const int H = s->hidden, D = s->hdim, KVD = s->kvheads * D, nb = H / OR_QK;
+    const int ppg = s->qheads / s->kvheads / 2, ytiles = H / 256;
+    const size_t tile = (size_t)nb * OR_COL_GROUP, sub = 8 * (size_t)OR_COL_GROUP;
+    float *normed = malloc(sizeof(float) * H);
+    or_block_q8_0 *inq8 = malloc(sizeof(or_block_q8_0) * nb);
+    if (!normed || !inq8) or_die("oom");
+    or_rmsnorm(x, l->norm, normed, H, s->rms_eps);
+    or_quantize_q8(normed, inq8, H);
+    memset(out, 0, sizeof(float) * H);
+    for (int g = 0; g < s->kvheads; ++g) {
+        float kvpair[256];
+        or_fused_column_matvec(kvt + g * tile, inq8, nb, l->bk ? l->bk + g * D : NULL,
+                               l->bv ? l->bv + g * D : NULL, kvpair, 0);
+        or_rope(kvpair, 1, D, context - 1, s->rope_base);
+        const size_t off = (size_t)(context - 1) * KVD + (size_t)g * D;
+        for (int d = 0; d < D; ++d) {
+            kc[off + d] = or_f32_to_f16(kvpair[d]);
+            vc[off + d] = or_f32_to_f16(kvpair[d + D]);
+        }
+        for (int p = 0; p < ppg; ++p) {
+            const int pair = g * ppg + p;
+            float qpair[256], opair[256];
+            or_block_q8_0 oq[8];
+            const float *bq = l->bq ? l->bq + (size_t)pair * 256 : NULL;
+            or_fused_column_matvec(qt + pair * tile, inq8, nb, bq, bq ? bq + 128 : NULL, qpair,
+                                   0);
+            or_rope(qpair, 2, D, context - 1, s->rope_base);
+            or_attention_pair(s, qpair, kc, vc, context, g, opair);
+            if (attn_capture) memcpy(attn_capture + (size_t)pair * 256, opair, sizeof opair);
+            or_quantize_q8(opair, oq, 256);
+            if (q8_capture) memcpy(q8_capture + (size_t)pair * 8, oq, sizeof oq);
+            for (int y = 0; y < ytiles; ++y)
+                or_fused_column_matvec(ot + ((size_t)pair * ytiles + y) * sub, oq, 8, NULL, NULL,
+                                       out + y * 256, 1);
+        }
+    }
+    free(normed);
+    free(inq8);
+}

@@ -130,6 +130,23 @@ void or_layer_prefill(const or_shape_t *s, const or_layer_t *l, const float *x,
                       const int *rows, int nrows, int full, float *out);
 
 /* ggml Q4_0 quantizer (quantize_row_q4_0_ref), build-side weight preparation. */
+/* ---- column-SoA tiles and the legacy fused path (hdim 128 shapes) ---- */
+size_t or_colsoa_bytes(const or_shape_t *s, int which);   /* 0 q, 1 kv, 2 o */
+void or_colsoa_repack(const or_shape_t *s, const uint8_t *wq, const uint8_t *wk,
+                      const uint8_t *wv, const uint8_t *wo, uint8_t *q, uint8_t *kv,
+                      uint8_t *o);                            /* repack_weights.py:55-120 */
+void or_fused_column_matvec(const uint8_t *tile, const or_block_q8_0 *x, int nblocks,
+                            const float *bias_lo, const float *bias_hi, float *out,
+                            int add);                         /* fused_layer.h:169-245 */
+void or_attention_pair(const or_shape_t *s, const float *qpair, const uint16_t *kc,
+                       const uint16_t *vc, int context, int group,
+                       float *opair);                         /* fused_layer.h:251-355 */
+void or_run_layer_legacy_fused(const or_shape_t *s, const or_layer_t *l, const uint8_t *qt,
+                               const uint8_t *kvt, const uint8_t *ot, const float *x,
+                               uint16_t *kc, uint16_t *vc, int context, float *out,
+                               float *attn_capture,
+                               or_block_q8_0 *q8_capture);    /* fused_layer.h:361-455 */
+
 void or_quantize_q4_0(const float *src, uint8_t *dst, int count);
 void or_dequantize_q4_0(const uint8_t *src, float *dst, int count);
 

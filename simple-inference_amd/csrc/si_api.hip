@@ -370,6 +370,94 @@ int si_attention_static(const si_shape_t *s, const float *q, int nq, const uint1
                           (size_t)SI_ATTENTION_STATIC_MAX, stream);
 }
 
+int si_f32_to_f16(const float *src, uint16_t *dst, size_t n, void *stream) {
+    SI_REQUIRE(n == 0 || (src && dst), "f32_to_f16: NULL pointer");
+    SI_REQUIRE(n < ((size_t)1 << 40), "f32_to_f16: %zu values", n);
+    launch_f16_convert(src, dst, n, true, S(stream));
+    return check_launch("si_f32_to_f16");
+}
+
+int si_f16_to_f32(const uint16_t *src, float *dst, size_t n, void *stream) {
+    SI_REQUIRE(n == 0 || (src && dst), "f16_to_f32: NULL pointer");
+    SI_REQUIRE(n < ((size_t)1 << 40), "f16_to_f32: %zu values", n);
+    launch_f16_convert(src, dst, n, false, S(stream));
+    return check_launch("si_f16_to_f32");
+}
+
+int si_matvec_q4q8_rowmajor(const uint8_t *w, const void *x, int inputs, int outputs,
+                            const float *bias, float *out, void *stream) {
+    // qwen_one_layer.c:150 takes inputs / QK blocks
+    SI_REQUIRE(inputs > 0 && inputs % 32 == 0 && outputs >= 0,
+               "matvec_q4q8: inputs %d must be a positive multiple of 32", inputs);
+    SI_REQUIRE((long long)outputs * (inputs / 32) * 18 < (1ll << 40),
+               "matvec_q4q8: %d x %d too large", outputs, inputs);
+    SI_REQUIRE(outputs == 0 || (w && x && out), "matvec_q4q8: NULL pointer");
+    SI_REQUIRE(((uintptr_t)w & 1) == 0 && ((uintptr_t)x & 1) == 0,
+               "matvec_q4q8: weights and blocks must be 2-byte aligned");
+    launch_matvec_rowmajor(w, x, inputs, outputs, bias, out, S(stream));
+    return check_launch("si_matvec_q4q8_rowmajor");
+}
+
+int si_colsoa_matvec(const uint8_t *tiles, int ntiles, const void *x, int nblocks,
+                     const float *bias_lo, const float *bias_hi, float *out, int add,
+                     void *stream) {
+    SI_REQUIRE(ntiles >= 0 && nblocks > 0, "colsoa_matvec: bad ntiles %d / nblocks %d", ntiles,
+               nblocks);
+    SI_REQUIRE(ntiles == 0 || (tiles && x && out), "colsoa_matvec: NULL pointer");
+    SI_REQUIRE(((uintptr_t)tiles & 3) == 0 && ((uintptr_t)x & 1) == 0,
+               "colsoa_matvec: tiles must be 4-byte and blocks 2-byte aligned");
+    launch_colsoa_matvec(tiles, ntiles, x, nblocks, add ? nullptr : bias_lo,
+                         add ? nullptr : bias_hi, out, add != 0, S(stream));
+    return check_launch("si_colsoa_matvec");
+}
+
+int si_rmsnorm(const float *x, const float *gain, int rows, int n, float eps, float *out,
+               void *stream) {
+    SI_REQUIRE(rows >= 0 && n > 0, "rmsnorm: bad size rows=%d n=%d", rows, n);
+    SI_REQUIRE(rows == 0 || (x && out), "rmsnorm: NULL pointer");
+    launch_rmsnorm(x, gain, rows, n, eps, out, S(stream));
+    return check_launch("si_rmsnorm");
+}
+
+int si_rope(const si_shape_t *s, float *heads, int nheads, int position, const float *rc,
+            const float *rs, int max_pos, void *stream) {
+    SI_REQUIRE(s && s->hdim > 0 && s->hdim % 2 == 0, "rope: bad shape");
+    SI_REQUIRE(nheads >= 0 && position >= 0 && position < max_pos,
+               "rope: position %d outside the table's 0..%d", position, max_pos - 1);
+    SI_REQUIRE(nheads == 0 || (heads && rc && rs), "rope: NULL pointer");
+    launch_rope_inplace(heads, nheads, s->hdim, position, rc, rs, S(stream));
+    return check_launch("si_rope");
+}
+
+size_t si_attention_group_workspace(const si_shape_t *s, int nheads, int context) {
+    if (!s || nheads <= 0 || context <= 0) return 0;
+    return attn_workspace_bytes(nheads, s->hdim, 1, 1, context);
+}
+
+int si_attention_group(const si_shape_t *s, const float *q, int nheads, int group,
+                       const uint16_t *kc, const uint16_t *vc, int context, float *out,
+                       void *ws, size_t ws_bytes, void *stream) {
+    int r = check_shape(s);
+    if (r) return r;
+    SI_REQUIRE(nheads >= 1 && nheads <= s->qheads / s->kvheads,
+               "attention_group: %d heads, a KV group serves %d", nheads,
+               s->qheads / s->kvheads);
+    SI_REQUIRE(group >= 0 && group < s->kvheads, "attention_group: group %d outside 0..%d",
+               group, s->kvheads - 1);
+    SI_REQUIRE(context >= 1, "attention_group: context must be >= 1");
+    SI_REQUIRE(q && kc && vc && out && ws, "attention_group: NULL pointer");
+    SI_REQUIRE(((uintptr_t)kc & 15) == 0 && ((uintptr_t)vc & 15) == 0,
+               "attention_group: kc and vc must be 16-byte aligned");
+    SI_REQUIRE(ws_bytes >= si_attention_group_workspace(s, nheads, context),
+               "attention_group: workspace too small");
+    // the group's heads as a one-group shape over the wider cache rows
+    const int kvd = s->kvheads * s->hdim;
+    launch_attention(q, 1, nheads, 1, s->hdim, kc + (size_t)group * s->hdim,
+                     vc + (size_t)group * s->hdim, 0, nullptr, context, 0, context, out, nullptr,
+                     nullptr, nullptr, ws, S(stream), KvPages(), kvd);
+    return check_launch("si_attention_group");
+}
+
 int si_attention_standard(const si_shape_t *s, const float *q, const uint16_t *kc,
                           const uint16_t *vc, int context, float *out, float *scores,
                           void *stream) {

@@ -220,7 +220,7 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(
     const float *__restrict__ q, int qheads, int kvheads, const uint16_t *__restrict__ kc,
     const uint16_t *__restrict__ vc, size_t kv_seq_stride, const int *__restrict__ ctx_dev,
     int ctx0, int ctx_step, int max_ctx, int chunk, float scale, float *__restrict__ ws_m,
-    float *__restrict__ ws_l, float *__restrict__ ws_o, KvPages pg) {
+    float *__restrict__ ws_l, float *__restrict__ ws_o, KvPages pg, int kv_row) {
     constexpr int KS = D / 32;  // k-steps of the score MFMA
     constexpr int DT = D / 16;  // d-tiles of the PV MFMA
     constexpr int VROW = D + MA_VPAD;
@@ -235,7 +235,8 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(
     ctx = min(ctx, max_ctx);
     const int p0 = sp * chunk;
     const int p1 = min(ctx, p0 + chunk);
-    const int kvd = kvheads * D;
+    const int kvd = kv_row;  // elements per cache row (kvheads * D unless a caller
+                             // passes one KV group of a wider cache)
     const uint16_t *kbase = kc + (size_t)g * D;  // + pg.row(qi, pos, ...) per row
     const uint16_t *vbase = vc + (size_t)g * D;
 
@@ -754,8 +755,9 @@ void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
                       const uint16_t *kc, const uint16_t *vc, size_t kv_seq_stride,
                       const int *ctx_dev, int ctx0, int ctx_step, int max_ctx, float *attn,
                       int8_t *qs, uint16_t *d, int16_t *bsum, void *workspace,
-                      hipStream_t st, KvPages pg) {
+                      hipStream_t st, KvPages pg, int kv_row) {
     if (nq <= 0) return;
+    if (kv_row <= 0) kv_row = kvheads * hdim;
     const int ns = attn_nsplit(kvheads, nq, max_ctx);
     int chunk = (max_ctx + ns - 1) / ns;
     chunk = (chunk + MA_SUPER - 1) / MA_SUPER * MA_SUPER;
@@ -767,7 +769,7 @@ void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
 #define SI_ATTN_LAUNCH(DIM)                                                                  \
     hipLaunchKernelGGL(k_attn_decode_mfma<DIM>, grid, dim3(256), 0, st, q, qheads, kvheads, kc, \
                        vc, kv_seq_stride, ctx_dev, ctx0, ctx_step, max_ctx, chunk, scale, ws_m, \
-                       ws_l, ws_o, pg)
+                       ws_l, ws_o, pg, kv_row)
     switch (hdim) {
         case 32: SI_ATTN_LAUNCH(32); break;
         case 64: SI_ATTN_LAUNCH(64); break;

@@ -89,7 +89,7 @@ void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
                       const uint16_t *kc, const uint16_t *vc, size_t kv_seq_stride,
                       const int *ctx_dev, int ctx0, int ctx_step, int max_ctx, float *attn,
                       int8_t *qs, uint16_t *d, int16_t *bsum, void *workspace,
-                      hipStream_t st, KvPages pg = KvPages());
+                      hipStream_t st, KvPages pg = KvPages(), int kv_row = 0);
 bool attn_prefill_supported(int qheads, int kvheads, int hdim);
 size_t attn_prefill_workspace_bytes(int qheads, int hdim, int ntok);
 void launch_attn_prefill(const float *q, int ntok, int qheads, int kvheads, int hdim, int pos0,
@@ -121,4 +121,16 @@ void launch_dec_attn(const float *qkv, int ldqkv, int nq, int qheads, int kvhead
                      uint16_t *ad, int16_t *as, hipStream_t st, KvPages pg = KvPages());
 void launch_attn_combine(int nq, int qheads, int hdim, int nsplit, const void *workspace,
                          float *attn, int8_t *qs, uint16_t *d, int16_t *bsum, hipStream_t st);
+// Kernels over the reference's own formats (si_mirror.hip): row-major Q4_0
+// with block_q8_0 records, column-SoA tiles, stand-alone rmsnorm and rope.
+void launch_matvec_rowmajor(const uint8_t *w, const void *x, int inputs, int outputs,
+                            const float *bias, float *out, hipStream_t st);
+void launch_colsoa_matvec(const uint8_t *tiles, int ntiles, const void *x, int nblocks,
+                          const float *bias_lo, const float *bias_hi, float *out, int add,
+                          hipStream_t st);
+void launch_rmsnorm(const float *x, const float *gain, int rows, int n, float eps, float *out,
+                    hipStream_t st);
+void launch_rope_inplace(float *heads, int nheads, int hdim, int position, const float *rc,
+                         const float *rs, hipStream_t st);
+void launch_f16_convert(const void *src, void *dst, size_t n, bool to_half, hipStream_t st);
 }  // namespace si

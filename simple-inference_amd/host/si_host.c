@@ -6,10 +6,14 @@
 #include "si_host.h"
 
 #include <errno.h>
+#include <fcntl.h>
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <sys/stat.h>
+#include <time.h>
+#include <unistd.h>
 
 #include <hip/hip_runtime_api.h>
 
@@ -33,27 +37,61 @@ static void hip_check(hipError_t e, const char *what) {
     }
 }
 
-/* load_file (qwen_one_layer.c:188-208): exact size check, optional files
- * may be absent (ENOENT), anything else is fatal. */
-static void *load_file(const char *dir, const char *name, size_t expected, int optional) {
-    char path[1024];
-    int n = snprintf(path, sizeof path, "%s/%s", dir, name);
-    if (n < 0 || (size_t)n >= sizeof path) die("Weights directory path too long");
-    FILE *f = fopen(path, "rb");
-    if (!f) {
-        if (optional && errno == ENOENT) return NULL;
-        perror(path);
+static void *dev_alloc(size_t bytes, const char *what) {
+    void *p = NULL;
+    hip_check(hipMalloc(&p, bytes ? bytes : 1), what);
+    return p;
+}
+
+static double wall_seconds(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+/* A weight file of exactly `want` bytes under dir, read whole into host
+ * memory.  A missing optional file gives NULL; a missing required file, a
+ * size mismatch or a read error ends the process (the loading contract of
+ * qwen_one_layer.c:188-208). */
+static void *read_weight_file(const char *dir, const char *name, size_t want, int optional) {
+    char *path = NULL;
+    if (asprintf(&path, "%s/%s", dir, name) < 0) die("Out of memory building a weight path");
+    const int fd = open(path, O_RDONLY | O_CLOEXEC);
+    if (fd < 0) {
+        if (optional && errno == ENOENT) {
+            free(path);
+            return NULL;
+        }
+        fprintf(stderr, "error: cannot open %s: %s\n", path, strerror(errno));
         exit(1);
     }
-    if (fseek(f, 0, SEEK_END) != 0 || ftell(f) != (long)expected || fseek(f, 0, SEEK_SET) != 0) {
-        fprintf(stderr, "Wrong size for %s (expected %zu bytes)\n", path, expected);
+    struct stat st;
+    if (fstat(fd, &st) != 0 || !S_ISREG(st.st_mode) || (size_t)st.st_size != want) {
+        fprintf(stderr, "error: %s holds %lld bytes; this shape needs exactly %zu\n", path,
+                (long long)st.st_size, want);
         exit(1);
     }
-    void *buf = malloc(expected);
-    if (!buf) die("Out of memory loading weights");
-    if (fread(buf, 1, expected, f) != expected) die("Failed to read weight file");
-    fclose(f);
+    unsigned char *buf = malloc(want ? want : 1);
+    if (!buf) die("Out of memory reading weights");
+    for (size_t got = 0; got < want;) {
+        const ssize_t r = read(fd, buf + got, want - got);
+        if (r < 0 && errno == EINTR) continue;
+        if (r <= 0) {
+            fprintf(stderr, "error: short read of %s\n", path);
+            exit(1);
+        }
+        got += (size_t)r;
+    }
+    close(fd);
+    free(path);
     return buf;
+}
+
+static float *upload_opt(const float *src, size_t n) {
+    if (!src) return NULL;
+    float *d = dev_alloc(n * sizeof(float), "hipMalloc(layer vector)");
+    hip_check(hipMemcpy(d, src, n * sizeof(float), hipMemcpyHostToDevice), "upload vector");
+    return d;
 }
 
 si_model_t *si_model_from_host(const si_shape_t *shape, const si_layer_host_t *w,
@@ -65,7 +103,23 @@ si_model_t *si_model_from_host(const si_shape_t *shape, const si_layer_host_t *w
     m->max_pos = max_pos;
     check(si_layer_create(shape, w, max_tokens, max_pos, &m->layer), "si_layer_create");
     m->attn_ws_bytes = si_attention_workspace(shape, 1, max_pos);
-    hip_check(hipMalloc(&m->attn_ws, m->attn_ws_bytes), "hipMalloc(attention workspace)");
+    const size_t pair_ws = si_attention_group_workspace(shape, 2, max_pos);
+    if (pair_ws > m->attn_ws_bytes) m->attn_ws_bytes = pair_ws;
+    m->attn_ws = dev_alloc(m->attn_ws_bytes, "hipMalloc(attention workspace)");
+    /* RoPE angle tables for rope() and the column-SoA path */
+    const size_t te = (size_t)max_pos * (shape->hdim / 2);
+    float *c = malloc(te * sizeof(float)), *sn = malloc(te * sizeof(float));
+    if (!c || !sn) die("Out of memory");
+    check(si_rope_table(max_pos, shape->hdim, shape->rope_base, c, sn), "si_rope_table");
+    m->rope_cos = upload_opt(c, te);
+    m->rope_sin = upload_opt(sn, te);
+    free(c);
+    free(sn);
+    const size_t QD = (size_t)shape->qheads * shape->hdim, KVD = (size_t)shape->kvheads * shape->hdim;
+    m->norm = upload_opt(w->norm, (size_t)shape->hidden);
+    m->bq = upload_opt(w->bq, QD);
+    m->bk = upload_opt(w->bk, KVD);
+    m->bv = upload_opt(w->bv, KVD);
     check(si_layer_set_timing(m->layer, 1), "si_layer_set_timing");
     return m;
 }
@@ -73,35 +127,41 @@ si_model_t *si_model_from_host(const si_shape_t *shape, const si_layer_host_t *w
 si_model_t *load_layer(const si_shape_t *s, const char *dir, int max_tokens, int max_pos) {
     const size_t H = (size_t)s->hidden, QD = (size_t)s->qheads * s->hdim;
     const size_t KVD = (size_t)s->kvheads * s->hdim, F = (size_t)s->ffn;
-    si_layer_host_t w;
-    memset(&w, 0, sizeof w);
-    /* qwen_one_layer.c:212-219 with runtime sizes */
-    w.wq = load_file(dir, "q.q4_0", QD * H / 32 * 18, 0);
-    w.wk = load_file(dir, "k.q4_0", KVD * H / 32 * 18, 0);
-    w.wv = load_file(dir, "v.q4_0", KVD * H / 32 * 18, 0);
-    w.wo = load_file(dir, "o.q4_0", H * QD / 32 * 18, 0);
-    w.norm = load_file(dir, "norm.f32", H * sizeof(float), 1);
-    w.bq = load_file(dir, "q_bias.f32", QD * sizeof(float), 1);
-    w.bk = load_file(dir, "k_bias.f32", KVD * sizeof(float), 1);
-    w.bv = load_file(dir, "v_bias.f32", KVD * sizeof(float), 1);
-    if (F) {
-        w.post_norm = load_file(dir, "post_norm.f32", H * sizeof(float), 1);
-        w.wgate = load_file(dir, "gate.q4_0", F * H / 32 * 18, 1);
-        w.wup = load_file(dir, "up.q4_0", F * H / 32 * 18, 1);
-        w.wdown = load_file(dir, "down.q4_0", H * F / 32 * 18, 1);
-    }
+    const size_t f32 = sizeof(float);
+    /* the files of qwen_one_layer.c:212-219 at the runtime shape, then the
+     * build-defined FFN's */
+    struct {
+        const char *name;
+        size_t bytes;
+        int optional;
+    } const files[12] = {
+        {"q.q4_0", QD * H / 32 * 18, 0},      {"k.q4_0", KVD * H / 32 * 18, 0},
+        {"v.q4_0", KVD * H / 32 * 18, 0},     {"o.q4_0", H * QD / 32 * 18, 0},
+        {"norm.f32", H * f32, 1},             {"q_bias.f32", QD * f32, 1},
+        {"k_bias.f32", KVD * f32, 1},         {"v_bias.f32", KVD * f32, 1},
+        {"post_norm.f32", H * f32, 1},        {"gate.q4_0", F * H / 32 * 18, 1},
+        {"up.q4_0", F * H / 32 * 18, 1},      {"down.q4_0", H * F / 32 * 18, 1},
+    };
+    void *data[12] = {0};
+    const int nfiles = F ? 12 : 8;
+    for (int i = 0; i < nfiles; ++i)
+        data[i] = read_weight_file(dir, files[i].name, files[i].bytes, files[i].optional);
+    si_layer_host_t w = {
+        .wq = data[0], .wk = data[1], .wv = data[2], .wo = data[3],
+        .norm = data[4], .bq = data[5], .bk = data[6], .bv = data[7],
+        .post_norm = data[8], .wgate = data[9], .wup = data[10], .wdown = data[11],
+    };
     si_model_t *m = si_model_from_host(s, &w, max_tokens, max_pos);
-    free((void *)w.wq); free((void *)w.wk); free((void *)w.wv); free((void *)w.wo);
-    free((void *)w.norm); free((void *)w.bq); free((void *)w.bk); free((void *)w.bv);
-    free((void *)w.post_norm); free((void *)w.wgate); free((void *)w.wup);
-    free((void *)w.wdown);
+    for (int i = 0; i < 12; ++i) free(data[i]);
     return m;
 }
 
 void free_layer(si_model_t *m) {
     if (!m) return;
     si_layer_destroy(m->layer);
-    if (m->attn_ws) (void)hipFree(m->attn_ws);
+    void *dev[] = {m->attn_ws, m->rope_cos, m->rope_sin, m->norm, m->bq, m->bk, m->bv};
+    for (size_t i = 0; i < sizeof dev / sizeof dev[0]; ++i)
+        if (dev[i]) (void)hipFree(dev[i]);
     free(m);
 }
 
@@ -170,9 +230,10 @@ phase_t run_layer(const si_model_t *l, const float *x, uint16_t *kc, uint16_t *v
     return decode(l, x, kc, vc, context, output, flags, attn_copy, q8_copy);
 }
 
-fused_stats_t run_layer_fused(const si_model_t *l, const float *x, uint16_t *kc, uint16_t *vc,
-                              int context, float *output, float *attn_capture,
-                              block_q8_0 *q8_capture) {
+fused_stats_t run_layer_fused(const si_model_t *l, const fused_weights_t *fw, const float *x,
+                              uint16_t *kc, uint16_t *vc, int context, float *output,
+                              float *attn_capture, block_q8_0 *q8_capture) {
+    (void)fw; /* the fused kernels read the layer's own repack of the same weights */
     fused_stats_t st;
     st.phase = decode(l, x, kc, vc, context, output, SI_LAYER_ATTN_ONLY, attn_capture, q8_capture);
     st.tcm_stage = 0.0;
@@ -227,6 +288,253 @@ void attention_compute(const si_model_t *l, attention_method_t method, const flo
 void quantize_q8(const float *src, block_q8_0 *dst, int count) {
     if (count % 32) die("Q8 quantization length must be multiple of 32"); /* :99 */
     check(si_quantize_q8(src, dst, count, NULL), "si_quantize_q8");
+}
+
+void matvec_q4q8(const uint8_t *weights, const block_q8_0 *input, int inputs, int outputs,
+                 const float *bias, float *out) {
+    if (inputs <= 0 || inputs % 32 || outputs < 0) die("matvec_q4q8: bad size");
+    check(si_matvec_q4q8_rowmajor(weights, input, inputs, outputs, bias, out, NULL),
+          "si_matvec_q4q8_rowmajor");
+}
+
+void rmsnorm(const si_model_t *l, const float *input, const float *weight, float *out) {
+    check(si_rmsnorm(input, weight, 1, l->shape.hidden, l->shape.rms_eps, out, l->stream),
+          "si_rmsnorm");
+}
+
+void rope(const si_model_t *l, float *heads, int nheads, int position) {
+    if (position < 0 || position >= l->max_pos) die("rope: position outside the layer's tables");
+    check(si_rope(&l->shape, heads, nheads, position, l->rope_cos, l->rope_sin, l->max_pos,
+                  l->stream),
+          "si_rope");
+}
+
+/* ------------------------------------------------------------------ */
+/* Column-SoA tiles and the legacy fused path (fused_layer.h)          */
+/* ------------------------------------------------------------------ */
+
+#define COL_GROUP 5120u /* 32 columns x 128 packed bytes + 256 fp32 scales */
+
+static int colsoa_shape(const si_shape_t *s) {
+    return s->hdim == 128 && s->kvheads > 0 && s->qheads % s->kvheads == 0 &&
+           (s->qheads / s->kvheads) % 2 == 0 && s->hidden > 0 && s->hidden % 256 == 0;
+}
+
+size_t si_colsoa_bytes(const si_shape_t *s, int which) {
+    if (!s || !colsoa_shape(s)) return 0;
+    const size_t blocks = (size_t)s->hidden / 32, pairs = (size_t)s->qheads / 2;
+    if (which == 0) return pairs * blocks * COL_GROUP;
+    if (which == 1) return (size_t)s->kvheads * blocks * COL_GROUP;
+    if (which == 2) return pairs * ((size_t)s->hidden / 256) * 8 * COL_GROUP;
+    return 0;
+}
+
+/* Nibble of input `col` of row `row` in a row-major Q4_0 matrix. */
+static unsigned nibble_at(const uint8_t *w, int ncols, int row, int col) {
+    const uint8_t *blk = w + ((size_t)row * (ncols / 32) + col / 32) * 18;
+    const int e = col % 32;
+    return e < 16 ? (blk[2 + e] & 15u) : (unsigned)(blk[2 + e - 16] >> 4);
+}
+
+/* One tile: `nblocks` groups from input block b0 whose low nibbles are rows
+ * lo..lo+127 of wlo and high nibbles rows hi..hi+127 of whi, followed per
+ * group by the 256 scales widened to fp32 (exact). */
+static void colsoa_tile(uint8_t *dst, const uint8_t *wlo, const uint8_t *whi, int ncols, int lo,
+                        int hi, int b0, int nblocks) {
+    for (int b = 0; b < nblocks; ++b) {
+        uint8_t *grp = dst + (size_t)b * COL_GROUP;
+        for (int k = 0; k < 32; ++k) {
+            const int col = (b0 + b) * 32 + k;
+            for (int j = 0; j < 128; ++j)
+                grp[k * 128 + j] =
+                    (uint8_t)(nibble_at(wlo, ncols, lo + j, col) | nibble_at(whi, ncols, hi + j, col) << 4);
+        }
+        float *sc = (float *)(void *)(grp + 4096);
+        for (int half = 0; half < 2; ++half)
+            for (int j = 0; j < 128; ++j) {
+                const uint8_t *w = half ? whi : wlo;
+                const int row = (half ? hi : lo) + j;
+                const uint8_t *blk = w + ((size_t)row * (ncols / 32) + b0 + b) * 18;
+                const uint16_t h = (uint16_t)(blk[0] | blk[1] << 8);
+                float v;
+                /* binary16 -> binary32 is exact: rebuild the value */
+                const int e = (h >> 10) & 31, m = h & 1023;
+                if (e == 0) v = ldexpf((float)m, -24);
+                else if (e == 31) v = m ? NAN : INFINITY;
+                else v = ldexpf((float)(m | 1024), e - 25);
+                sc[half * 128 + j] = (h & 0x8000u) ? -v : v;
+            }
+    }
+}
+
+void si_colsoa_repack_host(const si_shape_t *s, const si_layer_host_t *w, uint8_t *q,
+                           uint8_t *kv, uint8_t *o) {
+    if (!colsoa_shape(s)) die("Column-SoA tiles need hdim 128, paired heads, hidden % 256 == 0");
+    const int H = s->hidden, QD = s->qheads * s->hdim, nb = H / 32;
+    const size_t tile = (size_t)nb * COL_GROUP, sub = 8 * (size_t)COL_GROUP;
+    for (int p = 0; p < s->qheads / 2; ++p)
+        colsoa_tile(q + p * tile, w->wq, w->wq, H, 256 * p, 256 * p + 128, 0, nb);
+    for (int g = 0; g < s->kvheads; ++g)
+        colsoa_tile(kv + g * tile, w->wk, w->wv, H, 128 * g, 128 * g, 0, nb);
+    const int yt = H / 256;
+    for (int p = 0; p < s->qheads / 2; ++p)
+        for (int y = 0; y < yt; ++y)
+            colsoa_tile(o + ((size_t)p * yt + y) * sub, w->wo, w->wo, QD, 256 * y, 256 * y + 128,
+                        8 * p, 8);
+}
+
+static fused_weights_t fused_alloc(const si_model_t *l) {
+    const si_shape_t *s = &l->shape;
+    if (!colsoa_shape(s)) die("This shape has no column-SoA layout (needs hdim 128)");
+    fused_weights_t fw;
+    memset(&fw, 0, sizeof fw);
+    fw.q_bytes = si_colsoa_bytes(s, 0);
+    fw.kv_bytes = si_colsoa_bytes(s, 1);
+    fw.o_bytes = si_colsoa_bytes(s, 2);
+    fw.q = dev_alloc(fw.q_bytes, "hipMalloc(q tiles)");
+    fw.kv = dev_alloc(fw.kv_bytes, "hipMalloc(kv tiles)");
+    fw.o = dev_alloc(fw.o_bytes, "hipMalloc(o tiles)");
+    fw.normed = dev_alloc(sizeof(float) * (size_t)s->hidden, "hipMalloc");
+    fw.kvpair = dev_alloc(sizeof(float) * 256, "hipMalloc");
+    fw.qpair = dev_alloc(sizeof(float) * 256, "hipMalloc");
+    fw.opair = dev_alloc(sizeof(float) * 256, "hipMalloc");
+    fw.inq8 = dev_alloc(sizeof(block_q8_0) * (size_t)(s->hidden / 32), "hipMalloc");
+    fw.oq = dev_alloc(sizeof(block_q8_0) * 8, "hipMalloc");
+    return fw;
+}
+
+fused_weights_t si_fused_weights_from_host(const si_model_t *l, const uint8_t *q,
+                                           const uint8_t *kv, const uint8_t *o) {
+    fused_weights_t fw = fused_alloc(l);
+    hip_check(hipMemcpy(fw.q, q, fw.q_bytes, hipMemcpyHostToDevice), "upload q tiles");
+    hip_check(hipMemcpy(fw.kv, kv, fw.kv_bytes, hipMemcpyHostToDevice), "upload kv tiles");
+    hip_check(hipMemcpy(fw.o, o, fw.o_bytes, hipMemcpyHostToDevice), "upload o tiles");
+    return fw;
+}
+
+fused_weights_t fused_weights_load(const si_model_t *l, const char *dir, int use_tcm, int block) {
+    (void)block;
+    if (use_tcm) die("FUSED_TCM requested, but the GPU has no scratchpad to stage tiles in");
+    const si_shape_t *s = &l->shape;
+    if (!colsoa_shape(s)) die("This shape has no column-SoA layout (needs hdim 128)");
+    uint8_t *q = read_weight_file(dir, "q.colsoa", si_colsoa_bytes(s, 0), 0);
+    uint8_t *kv = read_weight_file(dir, "kv.colsoa", si_colsoa_bytes(s, 1), 0);
+    uint8_t *o = read_weight_file(dir, "o.colsoa", si_colsoa_bytes(s, 2), 0);
+    fused_weights_t fw = si_fused_weights_from_host(l, q, kv, o);
+    free(q);
+    free(kv);
+    free(o);
+    return fw;
+}
+
+void fused_weights_free(fused_weights_t *fw) {
+    void *dev[] = {fw->q, fw->kv, fw->o, fw->normed, fw->kvpair, fw->qpair, fw->opair,
+                   fw->inq8, fw->oq};
+    for (size_t i = 0; i < sizeof dev / sizeof dev[0]; ++i)
+        if (dev[i]) (void)hipFree(dev[i]);
+    memset(fw, 0, sizeof *fw);
+}
+
+void fused_column_matvec(const uint8_t *tile, const block_q8_0 *x, int nblocks,
+                         const float *bias_lo, const float *bias_hi, float *output, int add) {
+    check(si_colsoa_matvec(tile, 1, x, nblocks, bias_lo, bias_hi, output, add, NULL),
+          "si_colsoa_matvec");
+}
+
+void fused_attention_pair(const si_model_t *l, const float *qpair, const uint16_t *kc,
+                          const uint16_t *vc, int context, int group, float *opair) {
+    if (context < 1 || context > l->max_pos) die("Context must be 1..max_pos");
+    check(si_attention_group(&l->shape, qpair, 2, group, kc, vc, context, opair, l->attn_ws,
+                             l->attn_ws_bytes, l->stream),
+          "si_attention_group");
+}
+
+/* Runs on the layer's stream; returns the stage's wall time after it ends. */
+static double finish(const si_model_t *l, double t0) {
+    hip_check(hipStreamSynchronize((hipStream_t)l->stream), "stage");
+    return wall_seconds() - t0;
+}
+
+void attention_wo_fused(const si_model_t *l, const fused_weights_t *fw, const float *qpair,
+                        const uint16_t *kc, const uint16_t *vc, int context, int group, int pair,
+                        float *output_y, fused_stats_t *stats, float *attention_capture,
+                        block_q8_0 *quantized_capture) {
+    const int H = l->shape.hidden;
+    double t = wall_seconds();
+    fused_attention_pair(l, qpair, kc, vc, context, group, fw->opair);
+    stats->phase.attention += (float)finish(l, t);
+    if (attention_capture)
+        hip_check(hipMemcpy(attention_capture + (size_t)pair * 256, fw->opair,
+                            256 * sizeof(float), hipMemcpyDeviceToHost), "attention capture");
+    t = wall_seconds();
+    check(si_quantize_q8(fw->opair, fw->oq, 256, l->stream), "si_quantize_q8");
+    stats->phase.q8_output += (float)finish(l, t);
+    if (quantized_capture)
+        hip_check(hipMemcpy(quantized_capture + (size_t)pair * 8, fw->oq, 8 * sizeof(block_q8_0),
+                            hipMemcpyDeviceToHost), "Q8 capture");
+    /* the pair's 256 input columns of W_O: H/256 output tiles of 8 blocks */
+    t = wall_seconds();
+    check(si_colsoa_matvec(fw->o + (size_t)pair * (H / 256) * 8 * COL_GROUP, H / 256, fw->oq, 8,
+                           NULL, NULL, output_y, 1, l->stream),
+          "si_colsoa_matvec");
+    stats->phase.out_proj += (float)finish(l, t);
+}
+
+fused_stats_t run_layer_legacy_fused(const si_model_t *l, const fused_weights_t *fw,
+                                     const float *x, uint16_t *kc, uint16_t *vc, int context,
+                                     float *output, float *attn_capture,
+                                     block_q8_0 *q8_capture) {
+    const si_shape_t *s = &l->shape;
+    if (!colsoa_shape(s)) die("This shape has no column-SoA layout (needs hdim 128)");
+    if (context < 1 || context > l->max_pos) die("Context must be 1..max_pos");
+    const int H = s->hidden, D = s->hdim, KVD = s->kvheads * D, nb = H / 32;
+    const int pairs_per_group = s->qheads / s->kvheads / 2;
+    const size_t tile = (size_t)nb * COL_GROUP;
+    hipStream_t st = (hipStream_t)l->stream;
+    fused_stats_t stats;
+    memset(&stats, 0, sizeof stats);
+
+    double t = wall_seconds();
+    check(si_rmsnorm(x, l->norm, 1, H, s->rms_eps, fw->normed, st), "si_rmsnorm");
+    stats.phase.rms = (float)finish(l, t);
+    t = wall_seconds();
+    check(si_quantize_q8(fw->normed, fw->inq8, H, st), "si_quantize_q8");
+    stats.phase.q8_input = (float)finish(l, t);
+    hip_check(hipMemsetAsync(output, 0, sizeof(float) * H, st), "zero output");
+
+    for (int g = 0; g < s->kvheads; ++g) {
+        t = wall_seconds();
+        check(si_colsoa_matvec(fw->kv + g * tile, 1, fw->inq8, nb, l->bk ? l->bk + g * D : NULL,
+                               l->bv ? l->bv + g * D : NULL, fw->kvpair, 0, st),
+              "si_colsoa_matvec");
+        const double kv_time = finish(l, t);
+        stats.phase.k_proj += (float)(kv_time * 0.5);
+        stats.phase.v_proj += (float)(kv_time * 0.5);
+        /* RoPE of the K half, fp16 K and V rows at context-1 */
+        t = wall_seconds();
+        check(si_rope(s, fw->kvpair, 1, context - 1, l->rope_cos, l->rope_sin, l->max_pos, st),
+              "si_rope");
+        const size_t row = (size_t)(context - 1) * KVD + (size_t)g * D;
+        check(si_f32_to_f16(fw->kvpair, kc + row, D, st), "si_f32_to_f16");
+        check(si_f32_to_f16(fw->kvpair + D, vc + row, D, st), "si_f32_to_f16");
+        stats.phase.rope_cache += (float)finish(l, t);
+        for (int p = 0; p < pairs_per_group; ++p) {
+            const int pair = g * pairs_per_group + p;
+            const float *bq = l->bq ? l->bq + (size_t)pair * 256 : NULL;
+            t = wall_seconds();
+            check(si_colsoa_matvec(fw->q + pair * tile, 1, fw->inq8, nb, bq, bq ? bq + 128 : NULL,
+                                   fw->qpair, 0, st),
+                  "si_colsoa_matvec");
+            stats.phase.q_proj += (float)finish(l, t);
+            t = wall_seconds();
+            check(si_rope(s, fw->qpair, 2, context - 1, l->rope_cos, l->rope_sin, l->max_pos, st),
+                  "si_rope");
+            stats.phase.rope_cache += (float)finish(l, t);
+            attention_wo_fused(l, fw, fw->qpair, kc, vc, context, g, pair, output, &stats,
+                               attn_capture, q8_capture);
+        }
+    }
+    return stats;
 }
 
 void si_quantize_q4_0_host(const float *src, uint8_t *dst, int count) {

@@ -24,6 +24,7 @@
  */
 #define _GNU_SOURCE
 #include <math.h>
+#include <stddef.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -127,38 +128,44 @@ static si_model_t *synthetic_layer(const si_shape_t *s, int max_pos) {
     return m;
 }
 
-/* Binary KiB/MiB footprints (qwen_one_layer.c:288-302). */
-static void fmt_bytes(size_t bytes, char *out, size_t n) {
-    if (bytes >= 1024u * 1024u)
-        snprintf(out, n, "%.2f MiB", (double)bytes / (1024.0 * 1024.0));
-    else if (bytes >= 1024u)
-        snprintf(out, n, "%.2f KiB", (double)bytes / 1024.0);
+/* "<what> <size>" with the size in the largest binary unit up to MiB that
+ * keeps it at 1 or more, two decimals past bytes (the tables' footprint
+ * column). */
+static void footprint(char *out, size_t n, const char *what, size_t bytes) {
+    static const char *const unit[] = {"B", "KiB", "MiB"};
+    double v = (double)bytes;
+    int u = 0;
+    while (u < 2 && v >= 1024.0) {
+        v /= 1024.0;
+        ++u;
+    }
+    if (u == 0)
+        snprintf(out, n, "%s %zu B", what, bytes);
     else
-        snprintf(out, n, "%zu B", bytes);
+        snprintf(out, n, "%s %.2f %s", what, v, unit[u]);
 }
 
-static void label(char *out, size_t n, const char *what, size_t bytes) {
-    char b[32];
-    fmt_bytes(bytes, b, sizeof b);
-    snprintf(out, n, "%s %s", what, b);
+/* phase_t's nine fields in report order, so the tables and sums loop over
+ * them instead of naming each one. */
+static const size_t PHASE_FIELD[9] = {
+    offsetof(phase_t, rms),        offsetof(phase_t, q8_input),  offsetof(phase_t, q_proj),
+    offsetof(phase_t, k_proj),     offsetof(phase_t, v_proj),    offsetof(phase_t, rope_cache),
+    offsetof(phase_t, attention),  offsetof(phase_t, q8_output), offsetof(phase_t, out_proj),
+};
+
+static double phase_value(const phase_t *p, int i) {
+    float v;
+    memcpy(&v, (const char *)p + PHASE_FIELD[i], sizeof v);
+    return v;
 }
 
-static void add_phase(phase_t *sum, phase_t p) {
-    sum->rms += p.rms;
-    sum->q8_input += p.q8_input;
-    sum->q_proj += p.q_proj;
-    sum->k_proj += p.k_proj;
-    sum->v_proj += p.v_proj;
-    sum->rope_cache += p.rope_cache;
-    sum->attention += p.attention;
-    sum->q8_output += p.q8_output;
-    sum->out_proj += p.out_proj;
-}
-
-static void as_array(const phase_t *p, double t[9]) {
-    t[0] = p->rms; t[1] = p->q8_input; t[2] = p->q_proj;
-    t[3] = p->k_proj; t[4] = p->v_proj; t[5] = p->rope_cache;
-    t[6] = p->attention; t[7] = p->q8_output; t[8] = p->out_proj;
+static void phase_accumulate(phase_t *into, const phase_t *from) {
+    for (int i = 0; i < 9; ++i) {
+        float v;
+        memcpy(&v, (const char *)into + PHASE_FIELD[i], sizeof v);
+        v += (float)phase_value(from, i);
+        memcpy((char *)into + PHASE_FIELD[i], &v, sizeof v);
+    }
 }
 
 /* The nine rows' output shapes and data footprints for a runtime shape. */
@@ -180,15 +187,17 @@ static void row_labels(const si_model_t *l, int context, rows_t *r) {
     snprintf(r->result[6], 32, "FP32 [%d x %d]", s->qheads, s->hdim);
     snprintf(r->result[7], 32, "Q8_0 [%d blocks]", (int)(QD / 32));
     snprintf(r->result[8], 32, "FP32 [%d]", (int)H);
-    label(r->data[0], 36, "Norm", H * sizeof(float));
-    label(r->data[1], 36, "Q8 buffer", H / 32 * 34);
-    label(r->data[2], 36, "Wq Q4_0", QD * H / 32 * 18);
-    label(r->data[3], 36, "Wk Q4_0", KVD * H / 32 * 18);
-    label(r->data[4], 36, "Wv Q4_0", KVD * H / 32 * 18);
-    label(r->data[5], 36, "New K+V", KVD * 2 * 2);
-    label(r->data[6], 36, "KV cache", (size_t)context * KVD * 2 * 2);
-    label(r->data[7], 36, "Q8 buffer", QD / 32 * 34);
-    label(r->data[8], 36, "Wo Q4_0", H * QD / 32 * 18);
+    const struct {
+        const char *what;
+        size_t bytes;
+    } data[9] = {
+        {"Norm", H * sizeof(float)},          {"Q8 buffer", H / 32 * 34},
+        {"Wq Q4_0", QD * H / 32 * 18},        {"Wk Q4_0", KVD * H / 32 * 18},
+        {"Wv Q4_0", KVD * H / 32 * 18},       {"New K+V", KVD * 2 * 2},
+        {"KV cache", (size_t)context * KVD * 2 * 2}, {"Q8 buffer", QD / 32 * 34},
+        {"Wo Q4_0", H * QD / 32 * 18},
+    };
+    for (int i = 0; i < 9; ++i) footprint(r->data[i], sizeof r->data[i], data[i].what, data[i].bytes);
 }
 
 static const char *const OPS[9] = {"RMSNorm", "Quantize input", "Q projection",
@@ -213,8 +222,7 @@ static void report(const phase_t *p, const si_model_t *l, const char *shape, int
     rows_t r;
     row_labels(l, context, &r);
     double t[9], total = 0.0;
-    as_array(p, t);
-    for (int i = 0; i < 9; ++i) total += t[i];
+    for (int i = 0; i < 9; ++i) total += t[i] = phase_value(p, i);
     const int H = l->shape.hidden;
     const double sum = checksum(out, H, "Non-finite projection output");
     printf("\nQwen2 %s | one attention sublayer (decode) | MI355X\n", shape);
@@ -256,8 +264,10 @@ static void report_compare(const phase_t *st, const phase_t *fl, const si_model_
     rows_t r;
     row_labels(l, context, &r);
     double a[9], b[9], ta = 0.0, tb = 0.0;
-    as_array(st, a);
-    as_array(fl, b);
+    for (int i = 0; i < 9; ++i) {
+        a[i] = phase_value(st, i);
+        b[i] = phase_value(fl, i);
+    }
     printf("\nQwen2 %s | single attention sublayer | STANDARD vs FLASH | MI355X\n", shape);
     printf("Context: %d | Repeats: %d per mode\n", context, repeat);
     puts("Weights Q4_0 | Activations Q8_0 | KV FP16 | Same tensors and W_O kernel");
@@ -323,11 +333,9 @@ static void report_fusion(const phase_t *base, const fused_stats_t *fused, const
                                          "RoPE + KV append", "Online attention (GQA)",
                                          "Quantize O", "W_o"};
     double a[9], b[9], ta = 0.0, tb = 0.0;
-    as_array(base, a);
-    as_array(&fused->phase, b);
     for (int i = 0; i < 9; ++i) {
-        ta += a[i];
-        tb += b[i];
+        ta += a[i] = phase_value(base, i);
+        tb += b[i] = phase_value(&fused->phase, i);
     }
     printf("\nQwen2 %s | STAGED FLASH vs FUSED DECODE KERNELS | MI355X\n", shape);
     printf("One token | context=%d | repeats=%d/mode\n", context, repeat);
@@ -371,158 +379,210 @@ static void report_fusion(const phase_t *base, const fused_stats_t *fused, const
     puts("On the GPU the staged flash layer already runs the fused decode kernels.\n");
 }
 
-int main(int argc, char **argv) {
+/* ---- command line ---------------------------------------------------- */
+
+typedef enum { RUN_SINGLE, RUN_COMPARE, RUN_FUSED, RUN_FUSED_COMPARE } run_kind_t;
+
+/* The reference's modes (qwen_one_layer.c:610-629).  On the GPU the staged
+ * and register-fused variants run the same fused decode kernels. */
+static const struct {
+    const char *name;
+    run_kind_t kind;
+    attention_method_t method;
+    const char *banner;
+} MODES[] = {
+    {"standard", RUN_SINGLE, ATTENTION_STANDARD, NULL},
+    {"flash", RUN_SINGLE, ATTENTION_FLASH, NULL},
+    {"reference", RUN_SINGLE, ATTENTION_FLASH, NULL},
+    {"compare", RUN_COMPARE, ATTENTION_FLASH, NULL},
+    {"fused", RUN_FUSED, ATTENTION_FLASH, "REGISTER FUSED"},
+    {"soa-fused", RUN_FUSED, ATTENTION_FLASH, "REGISTER FUSED"},
+    {"soa-staged", RUN_FUSED, ATTENTION_FLASH, "SOA STAGED"},
+    {"fused-compare", RUN_FUSED_COMPARE, ATTENTION_FLASH, NULL},
+};
+#define NMODES ((int)(sizeof MODES / sizeof MODES[0]))
+
+typedef struct {
+    const char *source; /* weights directory or "synthetic" */
+    int context, repeat, mode;
+} cli_t;
+
+/* A decimal argument; `complaint` when characters follow the number. */
+static long decimal_arg(const char *text, const char *complaint) {
+    char *rest = NULL;
+    const long v = strtol(text, &rest, 10);
+    if (*rest) die(complaint);
+    return v;
+}
+
+static cli_t parse_cli(int argc, char **argv) {
     if (argc < 2 || argc > 5) {
         fprintf(stderr,
                 "Usage: %s <weights_directory|synthetic> [context=256] [repeat=1] "
                 "[standard|flash|compare|fused|fused-compare|reference|soa-staged|soa-fused]\n"
                 "       (shape from SI_SHAPE: 0.5b, 1.5b or 7b; default 1.5b)\n",
                 argv[0]);
-        return 2;
+        exit(2);
     }
-    char *end = NULL;
-    const long context = argc >= 3 ? strtol(argv[2], &end, 10) : 256;
-    if (argc >= 3 && *end) die("Invalid context argument");
-    const long repeat = argc >= 4 ? strtol(argv[3], &end, 10) : 1;
-    if (argc >= 4 && *end) die("Invalid repeat argument");
+    cli_t c = {argv[1], 256, 1, -1};
+    const long context = argc > 2 ? decimal_arg(argv[2], "Invalid context argument") : 256;
+    const long repeat = argc > 3 ? decimal_arg(argv[3], "Invalid repeat argument") : 1;
     if (context < 1 || context > 32768 || repeat < 1 || repeat > 100000)
         die("Context must be 1..32768 and repeat 1..100000");
-    const char *mode = argc >= 5 ? argv[4] : "compare";
-    const int compare = !strcmp(mode, "compare");
-    const int fused_compare = !strcmp(mode, "fused-compare");
-    const int fused_mode = !strcmp(mode, "fused") || fused_compare ||
-                           !strcmp(mode, "soa-fused") || !strcmp(mode, "soa-staged");
-    const int single = !strcmp(mode, "standard") || !strcmp(mode, "flash") ||
-                       !strcmp(mode, "reference");
-    if (!compare && !fused_mode && !single)
+    c.context = (int)context;
+    c.repeat = (int)repeat;
+    const char *mode = argc > 4 ? argv[4] : "compare";
+    for (int i = 0; i < NMODES && c.mode < 0; ++i)
+        if (!strcmp(MODES[i].name, mode)) c.mode = i;
+    if (c.mode < 0)
         die("Attention mode must be standard, flash, compare, fused, fused-compare, reference, "
             "soa-staged or soa-fused");
-    const attention_method_t selected =
-        !strcmp(mode, "standard") ? ATTENTION_STANDARD : ATTENTION_FLASH;
+    return c;
+}
 
+/* Everything one layer call needs; slot 0/1 name the two paths a
+ * comparison alternates (their own outputs and captures). */
+typedef struct {
+    const si_model_t *l;
+    float *x;
+    uint16_t *kc, *vc;
+    int context;
+    float *out[2];              /* device */
+    float *att[2];              /* host captures, or NULL */
+    block_q8_0 *q8[2];
+    attention_method_t method[2];
+    int fused[2];               /* slot runs run_layer_fused */
+} bench_t;
+
+static phase_t run_slot(const bench_t *b, int slot) {
+    if (b->fused[slot])
+        return run_layer_fused(b->l, NULL, b->x, b->kc, b->vc, b->context, b->out[slot],
+                               b->att[slot], b->q8[slot])
+            .phase;
+    return run_layer(b->l, b->x, b->kc, b->vc, b->context, b->out[slot], b->method[slot], NULL,
+                     b->att[slot], b->q8[slot]);
+}
+
+/* `rounds` rounds over the first `nslots` slots, the slot order reversed on
+ * every other round so neither path always runs first; phases are summed
+ * per slot into sums unless it is NULL (warm-up). */
+static void interleave(const bench_t *b, int nslots, int rounds, phase_t *sums) {
+    for (int r = 0; r < rounds; ++r)
+        for (int k = 0; k < nslots; ++k) {
+            const int slot = (r & 1) ? nslots - 1 - k : k;
+            const phase_t p = run_slot(b, slot);
+            if (sums) phase_accumulate(&sums[slot], &p);
+        }
+}
+
+static void to_host(float *dst, const float *src, int n) {
+    hip_check(hipMemcpy(dst, src, (size_t)n * sizeof(float), hipMemcpyDeviceToHost), "copy");
+}
+
+int main(int argc, char **argv) {
+    const cli_t cli = parse_cli(argc, argv);
     const char *shape_name = getenv("SI_SHAPE") ? getenv("SI_SHAPE") : "1.5b";
     si_shape_t shape;
     if (!shape_named(shape_name, &shape)) die("SI_SHAPE must be 0.5b, 1.5b or 7b");
-    const int ctx = (int)context, reps = (int)repeat;
-    si_model_t *l = !strcmp(argv[1], "synthetic") ? synthetic_layer(&shape, ctx)
-                                                  : load_layer(&shape, argv[1], 1, ctx);
+    const int ctx = cli.context, reps = cli.repeat;
+    si_model_t *l = !strcmp(cli.source, "synthetic") ? synthetic_layer(&shape, ctx)
+                                                     : load_layer(&shape, cli.source, 1, ctx);
     const int H = shape.hidden, QD = shape.qheads * shape.hdim, KVD = shape.kvheads * shape.hdim;
+    const size_t kv_elems = (size_t)ctx * KVD;
 
-    /* synthetic inputs in the reference's order (qwen_one_layer.c:641-642) */
-    float *input = malloc((size_t)H * sizeof(float));
-    uint16_t *kh = calloc((size_t)ctx * KVD, sizeof(uint16_t));
-    uint16_t *vh = calloc((size_t)ctx * KVD, sizeof(uint16_t));
-    if (!input || !kh || !vh) die("Out of memory creating synthetic inputs");
-    for (int i = 0; i < H; ++i) input[i] = next_uniform();
-    for (size_t i = 0, n = (size_t)(ctx - 1) * KVD; i < n; ++i) {
-        kh[i] = to_half(next_uniform() * 0.25f);
-        vh[i] = to_half(next_uniform() * 0.25f);
+    /* the synthetic token, then the cache history, from the reference's
+     * input stream in its order (qwen_one_layer.c:641-642) */
+    float *token = malloc((size_t)H * sizeof(float));
+    uint16_t *hist[2] = {calloc(kv_elems, 2), calloc(kv_elems, 2)};
+    if (!token || !hist[0] || !hist[1]) die("Out of memory creating synthetic inputs");
+    for (int i = 0; i < H; ++i) token[i] = next_uniform();
+    const size_t hist_elems = kv_elems - KVD; /* rows 0..context-2 */
+    for (size_t i = 0; i < hist_elems; ++i) {
+        hist[0][i] = to_half(next_uniform() * 0.25f);
+        hist[1][i] = to_half(next_uniform() * 0.25f);
     }
-    float *x, *out[2];
-    uint16_t *kc, *vc;
-    hip_check(hipMalloc((void **)&x, (size_t)H * sizeof(float)), "hipMalloc");
-    hip_check(hipMalloc((void **)&out[0], (size_t)H * sizeof(float)), "hipMalloc");
-    hip_check(hipMalloc((void **)&out[1], (size_t)H * sizeof(float)), "hipMalloc");
-    hip_check(hipMalloc((void **)&kc, (size_t)ctx * KVD * 2), "hipMalloc");
-    hip_check(hipMalloc((void **)&vc, (size_t)ctx * KVD * 2), "hipMalloc");
-    hip_check(hipMemcpy(x, input, (size_t)H * sizeof(float), hipMemcpyHostToDevice), "copy");
-    hip_check(hipMemcpy(kc, kh, (size_t)ctx * KVD * 2, hipMemcpyHostToDevice), "copy");
-    hip_check(hipMemcpy(vc, vh, (size_t)ctx * KVD * 2, hipMemcpyHostToDevice), "copy");
 
+    bench_t b;
+    memset(&b, 0, sizeof b);
+    b.l = l;
+    b.context = ctx;
+    hip_check(hipMalloc((void **)&b.x, (size_t)H * sizeof(float)), "hipMalloc");
+    hip_check(hipMalloc((void **)&b.kc, kv_elems * 2), "hipMalloc");
+    hip_check(hipMalloc((void **)&b.vc, kv_elems * 2), "hipMalloc");
+    hip_check(hipMemcpy(b.x, token, (size_t)H * sizeof(float), hipMemcpyHostToDevice), "copy");
+    hip_check(hipMemcpy(b.kc, hist[0], kv_elems * 2, hipMemcpyHostToDevice), "copy");
+    hip_check(hipMemcpy(b.vc, hist[1], kv_elems * 2, hipMemcpyHostToDevice), "copy");
     float *y[2], *att[2];
     block_q8_0 *q8[2];
-    for (int i = 0; i < 2; ++i) {
-        y[i] = malloc((size_t)H * sizeof(float));
-        att[i] = malloc((size_t)QD * sizeof(float));
-        q8[i] = malloc((size_t)(QD / 32) * sizeof(block_q8_0));
-        if (!y[i] || !att[i] || !q8[i]) die("Out of memory for comparison buffers");
+    for (int s = 0; s < 2; ++s) {
+        hip_check(hipMalloc((void **)&b.out[s], (size_t)H * sizeof(float)), "hipMalloc");
+        y[s] = malloc((size_t)H * sizeof(float));
+        att[s] = malloc((size_t)QD * sizeof(float));
+        q8[s] = malloc((size_t)(QD / 32) * sizeof(block_q8_0));
+        if (!y[s] || !att[s] || !q8[s]) die("Out of memory for comparison buffers");
     }
+
     phase_t sums[2];
     memset(sums, 0, sizeof sums);
-    if (fused_compare) {
-        /* staged flash and fused, alternating, captures in an untimed replay */
-        fused_stats_t fs;
-        memset(&fs, 0, sizeof fs);
-        for (int i = 0; i < 4; ++i) {
-            if (i == 0 || i == 3)
-                (void)run_layer(l, x, kc, vc, ctx, out[0], ATTENTION_FLASH, NULL, NULL, NULL);
-            else
-                (void)run_layer_fused(l, x, kc, vc, ctx, out[1], NULL, NULL);
+    const run_kind_t kind = MODES[cli.mode].kind;
+    if (kind == RUN_COMPARE || kind == RUN_FUSED_COMPARE) {
+        /* slot 0: the staged path (standard, or flash against the fused
+         * kernels); slot 1: flash or fused */
+        b.method[0] = kind == RUN_COMPARE ? ATTENTION_STANDARD : ATTENTION_FLASH;
+        b.method[1] = ATTENTION_FLASH;
+        b.fused[1] = kind == RUN_FUSED_COMPARE;
+        interleave(&b, 2, 2, NULL); /* warm-up, untimed */
+        if (kind == RUN_COMPARE) {
+            b.att[0] = att[0], b.att[1] = att[1], b.q8[0] = q8[0], b.q8[1] = q8[1];
+            interleave(&b, 2, reps, sums);
+        } else {
+            interleave(&b, 2, reps, sums); /* timed without captures */
+            b.att[0] = att[0], b.att[1] = att[1], b.q8[0] = q8[0], b.q8[1] = q8[1];
+            interleave(&b, 2, 1, NULL);    /* one captured replay of each */
         }
-        for (int r = 0; r < reps; ++r)
-            for (int j = 0; j < 2; ++j) {
-                const int which = (r & 1) ? 1 - j : j;
-                if (which == 0) {
-                    add_phase(&sums[0],
-                              run_layer(l, x, kc, vc, ctx, out[0], ATTENTION_FLASH, NULL, NULL,
-                                        NULL));
-                } else {
-                    const fused_stats_t f = run_layer_fused(l, x, kc, vc, ctx, out[1], NULL, NULL);
-                    add_phase(&fs.phase, f.phase);
-                    fs.tcm_stage += f.tcm_stage;
-                }
-            }
-        (void)run_layer(l, x, kc, vc, ctx, out[0], ATTENTION_FLASH, NULL, att[0], q8[0]);
-        (void)run_layer_fused(l, x, kc, vc, ctx, out[1], att[1], q8[1]);
-        for (int i = 0; i < 2; ++i)
-            hip_check(hipMemcpy(y[i], out[i], (size_t)H * sizeof(float), hipMemcpyDeviceToHost),
-                      "copy");
-        report_fusion(&sums[0], &fs, shape_name, ctx, reps, y[0], y[1], att[0], att[1], q8[0],
-                      q8[1], H, QD);
-    } else if (fused_mode) {
-        fused_stats_t fs;
-        memset(&fs, 0, sizeof fs);
-        for (int r = 0; r < reps; ++r) {
-            const fused_stats_t f = run_layer_fused(l, x, kc, vc, ctx, out[0], NULL, NULL);
-            add_phase(&fs.phase, f.phase);
+        to_host(y[0], b.out[0], H);
+        to_host(y[1], b.out[1], H);
+        if (kind == RUN_COMPARE) {
+            report_compare(&sums[0], &sums[1], l, shape_name, ctx, reps, y[0], y[1], att[0],
+                           att[1], q8[0], q8[1]);
+        } else {
+            fused_stats_t fs;
+            memset(&fs, 0, sizeof fs);
+            fs.phase = sums[1];
+            report_fusion(&sums[0], &fs, shape_name, ctx, reps, y[0], y[1], att[0], att[1],
+                          q8[0], q8[1], H, QD);
         }
-        hip_check(hipMemcpy(y[0], out[0], (size_t)H * sizeof(float), hipMemcpyDeviceToHost),
-                  "copy");
-        double t[9], total = 0.0;
-        as_array(&fs.phase, t);
-        for (int i = 0; i < 9; ++i) total += t[i];
-        printf("%s one-token | context=%d repeats=%d | MI355X fused decode kernels\n",
-               !strcmp(mode, "soa-staged") ? "SOA STAGED" : "REGISTER FUSED", ctx, reps);
-        printf("Compute %.3f ms/token, staging %.3f ms/token, all %.3f ms/token\n",
-               total * 1e3 / reps, 0.0, total * 1e3 / reps);
-        printf("Output checksum %.10g | first four %.6g %.6g %.6g %.6g\n",
-               checksum(y[0], H, "Non-finite fused output"), y[0][0], y[0][1], y[0][2], y[0][3]);
-    } else if (compare) {
-        /* alternating-order warmup, excluded from the measurements (:714-719) */
-        for (int i = 0; i < 4; ++i) {
-            const int m = (i == 0 || i == 3) ? ATTENTION_STANDARD : ATTENTION_FLASH;
-            (void)run_layer(l, x, kc, vc, ctx, out[m], (attention_method_t)m, NULL, NULL, NULL);
-        }
-        for (int r = 0; r < reps; ++r)
-            for (int j = 0; j < 2; ++j) {
-                const int m = (r & 1) == 0 ? j : 1 - j;
-                add_phase(&sums[m], run_layer(l, x, kc, vc, ctx, out[m], (attention_method_t)m,
-                                              NULL, att[m], q8[m]));
-            }
-        for (int i = 0; i < 2; ++i)
-            hip_check(hipMemcpy(y[i], out[i], (size_t)H * sizeof(float), hipMemcpyDeviceToHost),
-                      "copy");
-        report_compare(&sums[0], &sums[1], l, shape_name, ctx, reps, y[0], y[1], att[0], att[1],
-                       q8[0], q8[1]);
     } else {
-        for (int r = 0; r < reps; ++r)
-            add_phase(&sums[0], run_layer(l, x, kc, vc, ctx, out[0], selected, NULL, NULL, NULL));
-        hip_check(hipMemcpy(y[0], out[0], (size_t)H * sizeof(float), hipMemcpyDeviceToHost),
-                  "copy");
-        report(&sums[0], l, shape_name, ctx, reps, y[0], selected);
+        b.method[0] = MODES[cli.mode].method;
+        b.fused[0] = kind == RUN_FUSED;
+        interleave(&b, 1, reps, sums);
+        to_host(y[0], b.out[0], H);
+        if (kind == RUN_SINGLE) {
+            report(&sums[0], l, shape_name, ctx, reps, y[0], b.method[0]);
+        } else {
+            double total = 0.0;
+            for (int i = 0; i < 9; ++i) total += phase_value(&sums[0], i);
+            printf("%s one-token | context=%d repeats=%d | MI355X fused decode kernels\n",
+                   MODES[cli.mode].banner, ctx, reps);
+            printf("Compute %.3f ms/token, staging %.3f ms/token, all %.3f ms/token\n",
+                   total * 1e3 / reps, 0.0, total * 1e3 / reps);
+            printf("Output checksum %.10g | first four %.6g %.6g %.6g %.6g\n",
+                   checksum(y[0], H, "Non-finite fused output"), y[0][0], y[0][1], y[0][2],
+                   y[0][3]);
+        }
     }
-    for (int i = 0; i < 2; ++i) {
-        free(y[i]);
-        free(att[i]);
-        free(q8[i]);
-        (void)hipFree(out[i]);
+    for (int s = 0; s < 2; ++s) {
+        free(y[s]);
+        free(att[s]);
+        free(q8[s]);
+        (void)hipFree(b.out[s]);
     }
-    (void)hipFree(x);
-    (void)hipFree(kc);
-    (void)hipFree(vc);
-    free(input);
-    free(kh);
-    free(vh);
+    (void)hipFree(b.x);
+    (void)hipFree(b.kc);
+    (void)hipFree(b.vc);
+    free(token);
+    free(hist[0]);
+    free(hist[1]);
     free_layer(l);
     return 0;
 }

@@ -92,6 +92,14 @@ _SIGS = {
     "si_attention_static": (_I, [ctypes.POINTER(Shape), _P, _I, _P, _P, _Z, _P, _I, _I, _I, _P,
                                  _P, _P, _P, _P]),
     "si_attention_standard": (_I, [ctypes.POINTER(Shape), _P, _P, _P, _I, _P, _P, _P]),
+    "si_f32_to_f16": (_I, [_P, _P, _Z, _P]),
+    "si_f16_to_f32": (_I, [_P, _P, _Z, _P]),
+    "si_matvec_q4q8_rowmajor": (_I, [_P, _P, _I, _I, _P, _P, _P]),
+    "si_colsoa_matvec": (_I, [_P, _I, _P, _I, _P, _P, _P, _I, _P]),
+    "si_rmsnorm": (_I, [_P, _P, _I, _I, _F, _P, _P]),
+    "si_rope": (_I, [ctypes.POINTER(Shape), _P, _I, _I, _P, _P, _I, _P]),
+    "si_attention_group": (_I, [ctypes.POINTER(Shape), _P, _I, _I, _P, _P, _I, _P, _P, _Z, _P]),
+    "si_attention_group_workspace": (_Z, [ctypes.POINTER(Shape), _I, _I]),
     "si_swiglu_q8": (_I, [_P, _I, _I, _P, _P, _P, _P, _P]),
     "si_layer_create": (_I, [ctypes.POINTER(Shape), ctypes.POINTER(LayerHost), _I, _I,
                              ctypes.POINTER(_P)]),

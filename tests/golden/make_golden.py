@@ -18,7 +18,7 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 sys.path.insert(0, ROOT)
-from oracle.oracle_py import Oracle, Reference  # noqa: E402
+from oracle.oracle_py import Q8_DTYPE, Oracle, Reference  # noqa: E402
 
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "ref_golden.npz")
 
@@ -112,6 +112,32 @@ def main():
         g[f"layer_q8_{ctx}"] = q8.view(np.uint8)
         g[f"layer_newk_{ctx}"] = kc[(ctx - 1) * kvd:]
         g[f"layer_newv_{ctx}"] = vc[(ctx - 1) * kvd:]
+    # the column-SoA path: fused_column_matvec on an arbitrary 8-block tile
+    # (fresh, then accumulating), and run_layer_fused (portable build =
+    # run_layer_legacy_fused) on the tiles of the layer above; the tiles are
+    # rebuilt on the test host by the oracle's repacker, whose layout the
+    # reference build pins (test_oracle_vs_reference.py)
+    rng = np.random.default_rng(6)
+    tile = rng.integers(0, 256, (8, 5120), dtype=np.uint8)
+    tile[:, 4096:] = rng.normal(0, 0.01, (8, 256)).astype(np.float16).astype(
+        np.float32).view(np.uint8).reshape(8, 1024)
+    g["fcm_tile"] = tile.reshape(-1)
+    g["fcm_xq"] = ref.quantize_q8(rng.standard_normal(256).astype(np.float32)).view(np.uint8)
+    g["fcm_bias"] = rng.normal(0, 0.02, 256).astype(np.float32)
+    xq = g["fcm_xq"].view(Q8_DTYPE)
+    g["fcm_out"] = ref.fused_column_matvec(g["fcm_tile"], xq, 8, g["fcm_bias"][:128],
+                                           g["fcm_bias"][128:])
+    g["fcm_out_add"] = ref.fused_column_matvec(g["fcm_tile"], xq, 8, out=g["fcm_out"], add=True)
+    tiles = oracle.colsoa_repack(s, lay)
+    g["colsoa_sha256"] = np.frombuffer(
+        hashlib.sha256(b"".join(t.tobytes() for t in tiles)).hexdigest().encode(), np.uint8)
+    for ctx in (1, 17, 64):
+        kc, vc = g[f"layer_kc_{ctx}"].copy(), g[f"layer_vc_{ctx}"].copy()
+        out, attn, q8 = ref.run_layer_fused(lay, tiles, g["layer_x"], kc, vc, ctx)
+        g[f"fused_out_{ctx}"], g[f"fused_attn_{ctx}"] = out, attn
+        g[f"fused_q8_{ctx}"] = q8.view(np.uint8)
+        g[f"fused_newk_{ctx}"] = kc[(ctx - 1) * kvd:]
+        g[f"fused_newv_{ctx}"] = vc[(ctx - 1) * kvd:]
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT} ({os.path.getsize(OUT)} bytes)")
 

@@ -206,3 +206,25 @@ def test_layer_from_gguf_matches_direct(tmp_path):
         assert all(np.array_equal(a, b) for a, b in zip(*outs)), flags
     Lg.close()
     Ld.close()
+
+
+@pytest.mark.gpu
+def test_device_manifest_round_trip(oracle):
+    """The ingest manifest of a created layer: raw Q4_0 SHA-256 per matrix,
+    the device arrays' digests, and the lossless unpack round trip."""
+    import hashlib
+    from oracle.oracle_py import make_shape as or_shape
+    from si_amd import repack
+    from tests.gpu_helpers import make_layer
+    sd = si_amd.SHAPES["0.5b"]
+    lay = make_layer(oracle, or_shape(**sd), 6)
+    L = si_amd.Layer(si_amd.make_shape(**sd), lay, 1, 16)
+    m = repack.device_manifest(L, lay)
+    assert set(m["matrices"]) == {"qkv", "o", "gate_up", "down"}
+    for name, parts in (("qkv", ("wq", "wk", "wv")), ("o", ("wo",)),
+                        ("gate_up", ("wgate", "wup")), ("down", ("wdown",))):
+        e = m["matrices"][name]
+        assert e["round_trip"], name
+        raw = b"".join(np.ascontiguousarray(lay[p]).tobytes() for p in parts)
+        assert e["raw_q4_sha256"] == hashlib.sha256(raw).hexdigest()
+    L.close()

@@ -124,3 +124,32 @@ def test_command_line_argument_errors():
         assert r.returncode == 1 and msg in r.stderr, (args, r.stderr)
     r = run("synthetic", 16, 1, "flash", shape="13b")
     assert r.returncode == 1 and "SI_SHAPE" in r.stderr
+
+
+def test_colsoa_repack_files_and_manifest(oracle, tmp_path):
+    """si_amd.repack writes repack_weights.py's three column-SoA files (the
+    product's C repacker, byte-equal to the oracle's layout, which the
+    reference build pins) and a manifest whose SHA-256 values match the
+    files and the raw Q4_0 tensors."""
+    import hashlib
+    import json
+    from oracle.oracle_py import make_shape as or_shape
+    from si_amd import repack
+    from tests.gpu_helpers import make_layer
+    sd = si_amd.SHAPES["1.5b_ref"]
+    lay = make_layer(oracle, or_shape(**sd), 4, ffn=False)
+    for stem, key in (("q", "wq"), ("k", "wk"), ("v", "wv"), ("o", "wo")):
+        lay[key].tofile(tmp_path / f"{stem}.q4_0")
+    m = repack.repack(str(tmp_path))
+    want = oracle.colsoa_repack(or_shape(**sd), lay)
+    for (name, t), w in zip((("q", 0), ("kv", 1), ("o", 2)), want):
+        data = (tmp_path / f"{name}.colsoa").read_bytes()
+        assert data == w.tobytes(), name
+        assert m["files"][name]["sha256"] == hashlib.sha256(data).hexdigest()
+    for stem, key in (("q", "wq"), ("k", "wk"), ("v", "wv"), ("o", "wo")):
+        assert m["raw_q4_sha256"][stem] == hashlib.sha256(lay[key].tobytes()).hexdigest()
+    on_disk = json.loads((tmp_path / "manifest_colsoa.json").read_text())
+    assert on_disk == m
+    # shapes without the layout are refused (hdim 64)
+    with pytest.raises(ValueError):
+        repack.repack(str(tmp_path), "0.5b")

@@ -65,3 +65,31 @@ def test_run_layer(oracle, g):
         assert cap["attq"].view(np.uint8).tobytes() == g[f"layer_q8_{ctx}"].tobytes()
         assert np.array_equal(kc[(ctx - 1) * kvd:], g[f"layer_newk_{ctx}"])
         assert np.array_equal(vc[(ctx - 1) * kvd:], g[f"layer_newv_{ctx}"])
+
+
+def test_fused_column_matvec(oracle, g):
+    xq = g["fcm_xq"].view(Q8_DTYPE)
+    y = oracle.fused_column_matvec(g["fcm_tile"], xq, 8, g["fcm_bias"][:128], g["fcm_bias"][128:])
+    assert np.array_equal(y.view(np.uint32), g["fcm_out"].view(np.uint32))
+    y2 = oracle.fused_column_matvec(g["fcm_tile"], xq, 8, out=y, add=True)
+    assert np.array_equal(y2.view(np.uint32), g["fcm_out_add"].view(np.uint32))
+
+
+def test_run_layer_fused(oracle, g):
+    """The reference's run_layer_fused (portable build) on column-SoA tiles
+    rebuilt here by the oracle's repacker (digest of the tiles recorded)."""
+    from tests.golden.make_golden import layer_weights
+    s = make_shape(**REF_SHAPE)
+    lay = layer_weights(oracle, int(g["layer_seed"][0]), s)
+    tiles = oracle.colsoa_repack(s, lay)
+    digest = hashlib.sha256(b"".join(t.tobytes() for t in tiles)).hexdigest()
+    assert digest == bytes(g["colsoa_sha256"]).decode()
+    kvd = s.kvheads * s.hdim
+    for ctx in (1, 17, 64):
+        kc, vc = g[f"layer_kc_{ctx}"].copy(), g[f"layer_vc_{ctx}"].copy()
+        out, attn, q8 = oracle.run_layer_legacy_fused(s, lay, tiles, g["layer_x"], kc, vc, ctx)
+        assert np.array_equal(out.view(np.uint32), g[f"fused_out_{ctx}"].view(np.uint32))
+        assert np.array_equal(attn.view(np.uint32), g[f"fused_attn_{ctx}"].view(np.uint32))
+        assert q8.view(np.uint8).tobytes() == g[f"fused_q8_{ctx}"].tobytes()
+        assert np.array_equal(kc[(ctx - 1) * kvd:], g[f"fused_newk_{ctx}"])
+        assert np.array_equal(vc[(ctx - 1) * kvd:], g[f"fused_newv_{ctx}"])

@@ -211,3 +211,94 @@ def test_full_prefill_equals_sequential_decode(oracle):
         assert np.array_equal(y[t], yt)
     assert np.array_equal(kc, kr) and np.array_equal(vc, vr)
     assert np.array_equal(ysub, y[[4, 1]])
+
+
+# Column-SoA tiles (repack_weights.py) and the legacy fused path: the
+# reference's portable build computes the same numbers in head-pair order as
+# run_layer does in its staged order (same per-row block order, same softmax
+# recurrence), so each fused piece must equal the staged function bit for bit
+# on the matching rows.  A wrong index in the repacker or the fused path
+# (a swapped nibble, pair or output tile) breaks these equalities.
+_FUSED_SHAPES = {
+    "1.5b": dict(hidden=1536, qheads=12, kvheads=2, hdim=128),
+    "2k_g8": dict(hidden=2048, qheads=16, kvheads=2, hdim=128),   # 4 pairs per group
+    "1k_g2": dict(hidden=1024, qheads=8, kvheads=4, hdim=128),    # 1 pair per group
+}
+
+
+def _fused_layer(oracle, s, seed):
+    rng = np.random.default_rng(seed)
+    H, QD, KVD = s.hidden, s.qheads * s.hdim, s.kvheads * s.hdim
+    q4 = lambda n, k: oracle.quantize_q4_0(rng.normal(0, 0.02, (n, k)).astype(np.float32))
+    return dict(wq=q4(QD, H), wk=q4(KVD, H), wv=q4(KVD, H), wo=q4(H, QD),
+                norm=rng.normal(1, 0.1, H).astype(np.float32),
+                bq=rng.normal(0, 0.02, QD).astype(np.float32),
+                bk=rng.normal(0, 0.02, KVD).astype(np.float32),
+                bv=rng.normal(0, 0.02, KVD).astype(np.float32))
+
+
+@pytest.mark.parametrize("name", list(_FUSED_SHAPES))
+def test_colsoa_tiles_equal_row_major_matvec(oracle, name):
+    from oracle.oracle_py import make_shape
+    s = make_shape(**_FUSED_SHAPES[name])
+    lay = _fused_layer(oracle, s, 5)
+    qt, kvt, ot = oracle.colsoa_repack(s, lay)
+    H, D, QD = s.hidden, s.hdim, s.qheads * s.hdim
+    nb, tile = H // 32, (H // 32) * 5120
+    rng = np.random.default_rng(6)
+    xq = oracle.quantize_q8(rng.standard_normal(H).astype(np.float32))
+    q = oracle.matvec(lay["wq"], xq, H, QD, lay["bq"])
+    for p in range(s.qheads // 2):
+        bq = lay["bq"][p * 256:(p + 1) * 256]
+        y = oracle.fused_column_matvec(qt[p * tile:(p + 1) * tile], xq, nb, bq[:128], bq[128:])
+        assert np.array_equal(y.view(np.uint32), q[p * 256:(p + 1) * 256].view(np.uint32)), p
+    k = oracle.matvec(lay["wk"], xq, H, s.kvheads * D, lay["bk"])
+    v = oracle.matvec(lay["wv"], xq, H, s.kvheads * D, lay["bv"])
+    for g in range(s.kvheads):
+        y = oracle.fused_column_matvec(kvt[g * tile:(g + 1) * tile], xq, nb,
+                                       lay["bk"][g * D:(g + 1) * D], lay["bv"][g * D:(g + 1) * D])
+        want = np.concatenate([k[g * D:(g + 1) * D], v[g * D:(g + 1) * D]])
+        assert np.array_equal(y.view(np.uint32), want.view(np.uint32)), g
+    # W_O: every pair's 8 input blocks added in pair order equals the staged
+    # mat-vec, whose block order is the same
+    aq = oracle.quantize_q8(rng.standard_normal(QD).astype(np.float32))
+    want = oracle.matvec(lay["wo"], aq, QD, H)
+    got = np.zeros(H, np.float32)
+    sub, yt = 8 * 5120, H // 256
+    for p in range(s.qheads // 2):
+        for t in range(yt):
+            base = (p * yt + t) * sub
+            got[t * 256:(t + 1) * 256] = oracle.fused_column_matvec(
+                ot[base:base + sub], aq[p * 8:(p + 1) * 8], 8, out=got[t * 256:(t + 1) * 256],
+                add=True)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", list(_FUSED_SHAPES))
+@pytest.mark.parametrize("context", [1, 33])
+def test_legacy_fused_layer_equals_run_layer(oracle, name, context):
+    from oracle.oracle_py import make_shape
+    s = make_shape(**_FUSED_SHAPES[name])
+    lay = _fused_layer(oracle, s, 8)
+    tiles = oracle.colsoa_repack(s, lay)
+    rng = np.random.default_rng(context)
+    kvd = s.kvheads * s.hdim
+    x = rng.standard_normal(s.hidden).astype(np.float32)
+    kc0 = oracle.f32_to_f16(rng.standard_normal(context * kvd).astype(np.float32))
+    vc0 = oracle.f32_to_f16(rng.standard_normal(context * kvd).astype(np.float32))
+    ka, va, kb, vb = kc0.copy(), vc0.copy(), kc0.copy(), vc0.copy()
+    fo, fa, fq = oracle.run_layer_legacy_fused(s, lay, tiles, x, ka, va, context)
+    so, sb = oracle.run_layer(s, lay, x, kb, vb, context, capture=True)
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    assert np.array_equal(fa.view(np.uint32), sb["attn"].view(np.uint32))
+    assert fq.tobytes() == sb["attq"].tobytes()
+    assert np.array_equal(fo.view(np.uint32), so.view(np.uint32))
+    # the pair attention is attention_flash's recurrence on the pair's heads
+    per = s.qheads // s.kvheads
+    for g in range(s.kvheads):
+        for p in range(per // 2):
+            h0 = g * per + 2 * p
+            qpair = sb["q"][h0 * s.hdim:(h0 + 2) * s.hdim]
+            got = oracle.attention_pair(s, qpair, kb, vb, context, g)
+            assert np.array_equal(got.view(np.uint32),
+                                  sb["attn"][h0 * s.hdim:(h0 + 2) * s.hdim].view(np.uint32))

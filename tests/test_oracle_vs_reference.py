@@ -182,3 +182,64 @@ def test_prefill_equals_sequential_reference_decode(oracle, ref):
 def test_reference_rng_matches(oracle, ref):
     for seed in (0x5217ac8b, 0x8f53491a, 0x91be2145):
         assert np.array_equal(oracle.rng_floats(seed, 1000), ref.rng_floats(seed, 1000))
+
+
+def _random_tile(rng, nblocks):
+    """Arbitrary column-SoA groups: random nibble bytes, fp32 scales that are
+    exact fp16 values (as repack_weights.py writes them)."""
+    t = rng.integers(0, 256, (nblocks, 5120), dtype=np.uint8)
+    sc = rng.normal(0, 0.01, (nblocks, 256)).astype(np.float16).astype(np.float32)
+    t[:, 4096:] = sc.view(np.uint8).reshape(nblocks, 1024)
+    return t.reshape(-1)
+
+
+@pytest.mark.parametrize("add,bias", [(False, False), (False, True), (True, False)])
+def test_fused_column_matvec_bit_exact(oracle, ref, add, bias):
+    rng = np.random.default_rng(31)
+    nb = 48
+    tile = _random_tile(rng, nb)
+    xq = ref.quantize_q8(rng.standard_normal(nb * QK).astype(np.float32))
+    bl = rng.normal(0, 0.02, 128).astype(np.float32) if bias else None
+    bh = rng.normal(0, 0.02, 128).astype(np.float32) if bias else None
+    start = rng.standard_normal(256).astype(np.float32) if add else None
+    a = oracle.fused_column_matvec(tile, xq, nb, bl, bh, start, add)
+    b = ref.fused_column_matvec(tile, xq, nb, bl, bh, start, add)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("context,kmul", [(1, 1.0), (2, 0.0125), (17, 1.0), (64, 0.0),
+                                          (300, 0.5)])
+def test_attention_pair_bit_exact(oracle, ref, context, kmul):
+    rng = np.random.default_rng(context)
+    s = ref.shape()
+    kvd = s.kvheads * s.hdim
+    kc = oracle.f32_to_f16((rng.uniform(-1, 1, context * kvd) * kmul).astype(np.float32))
+    vc = oracle.f32_to_f16((rng.uniform(-1, 1, context * kvd) * 0.25).astype(np.float32))
+    for group in range(s.kvheads):
+        qpair = rng.standard_normal(2 * s.hdim).astype(np.float32)
+        a = oracle.attention_pair(s, qpair, kc, vc, context, group)
+        b = ref.attention_pair(qpair, kc, vc, context, group)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("context", [1, 17, 64, 200])
+def test_run_layer_fused_bit_exact(oracle, ref, context):
+    """run_layer_fused of the portable build (= run_layer_legacy_fused over
+    column-SoA tiles) against the oracle's restatement, on tiles built by the
+    oracle's repacker: output, attention and Q8 captures, new K/V rows."""
+    from tests.golden.make_golden import layer_weights
+    s = ref.shape()
+    lay = layer_weights(oracle, 77, s)
+    tiles = oracle.colsoa_repack(s, lay)
+    rng = np.random.default_rng(context)
+    kvd = s.kvheads * s.hdim
+    x = rng.standard_normal(s.hidden).astype(np.float32)
+    kc0 = oracle.f32_to_f16(rng.uniform(-1, 1, context * kvd).astype(np.float32) * 0.25)
+    vc0 = oracle.f32_to_f16(rng.uniform(-1, 1, context * kvd).astype(np.float32) * 0.25)
+    ka, va, kb, vb = kc0.copy(), vc0.copy(), kc0.copy(), vc0.copy()
+    oa, aa, qa = oracle.run_layer_legacy_fused(s, lay, tiles, x, ka, va, context)
+    ob, ab, qb = ref.run_layer_fused(lay, tiles, x, kb, vb, context)
+    assert np.array_equal(oa.view(np.uint32), ob.view(np.uint32))
+    assert np.array_equal(aa.view(np.uint32), ab.view(np.uint32))
+    assert qa.tobytes() == qb.tobytes()
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
