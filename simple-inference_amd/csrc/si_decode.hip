@@ -75,13 +75,17 @@ __device__ __forceinline__ void quant_block_serial(const float (&v)[32], uint32_
 // per lane, then a fixed tree); the Q8 blocks are bit-exact given the
 // normalised values.  Two steps so a kernel can order its memory requests
 // as it consumes them (loads retire in issue order): load() requests the
-// thread's first x and gain values, the kernel then requests its weights,
-// and run() waits only for x and gain.  Workgroup 0 stores the captures.
+// thread's x and gain values (its first NI groups of 4: the whole row up
+// to 4*NI*T values), the kernel then requests its weights, and run() waits
+// only for x and gain.  Values past 4*NI*T are loaded by run() itself, and
+// those wait behind the weights.  Workgroup 0 stores the captures.
 template <int T>
 struct NormQ8Prologue {
+    // groups of 4 held per thread: rows of up to 4096 values at T >= 256
+    static constexpr int NI = T >= 256 ? (1024 + T - 1) / T : 4;
     const float *x, *gain;
     int n;
-    float4 v, g;
+    float4 v[NI], g[NI];
 
     __device__ __forceinline__ NormQ8Prologue(const float *__restrict__ x_,
                                               const float *__restrict__ gain_, int n_)
@@ -92,7 +96,8 @@ struct NormQ8Prologue {
         gv = gain ? *(const float4 *)(gain + 4 * e4) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     }
     __device__ __forceinline__ void load() {  // branch-free (clamped index)
-        load4(min((int)threadIdx.x, n / 4 - 1), v, g);
+#pragma unroll
+        for (int u = 0; u < NI; ++u) load4(min((int)threadIdx.x + u * T, n / 4 - 1), v[u], g[u]);
     }
 
     __device__ void run(float eps, Q8Lds xq, double *dscr, float *__restrict__ cap_normed,
@@ -100,12 +105,17 @@ struct NormQ8Prologue {
                         int16_t *__restrict__ cap_s) {
         const int t = threadIdx.x;
         const int n4 = n / 4;
+        auto sq = [](float4 a) {
+            return (double)a.x * a.x + (double)a.y * a.y + (double)a.z * a.z + (double)a.w * a.w;
+        };
         double ss = 0.0;
-        for (int e4 = t; e4 < n4; e4 += T) {
-            float4 xv = v, gv;
-            if (e4 != t) load4(e4, xv, gv);  // more values than 4 per thread
-            ss += (double)xv.x * xv.x + (double)xv.y * xv.y + (double)xv.z * xv.z +
-                  (double)xv.w * xv.w;
+#pragma unroll
+        for (int u = 0; u < NI; ++u)
+            if (t + u * T < n4) ss += sq(v[u]);
+        for (int e4 = t + NI * T; e4 < n4; e4 += T) {  // rows past 4*NI*T values
+            float4 xv, gv;
+            load4(e4, xv, gv);
+            ss += sq(xv);
         }
         ss = wave_sum_d(ss);
         if ((t & 63) == 0) dscr[t >> 6] = ss;
@@ -115,9 +125,7 @@ struct NormQ8Prologue {
         for (int w = 0; w < T / 64; ++w) tot += dscr[w];
         const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn((float)(tot / (double)n), eps)));
         const bool cap = blockIdx.x == 0;
-        for (int e4 = t; e4 < n4; e4 += T) {  // whole 8-lane groups (n4 % 8 == 0)
-            float4 xv = v, gv = g;
-            if (e4 != t) load4(e4, xv, gv);
+        auto emit = [&](int e4, float4 xv, float4 gv) {
             const float y[4] = {__fmul_rn(__fmul_rn(xv.x, inv), gv.x),
                                 __fmul_rn(__fmul_rn(xv.y, inv), gv.y),
                                 __fmul_rn(__fmul_rn(xv.z, inv), gv.z),
@@ -139,6 +147,15 @@ struct NormQ8Prologue {
                     if (cap_s) cap_s[blk] = (int16_t)bsum;
                 }
             }
+        };
+        // whole 8-lane groups in or out (n4 % 8 == 0)
+#pragma unroll
+        for (int u = 0; u < NI; ++u)
+            if (t + u * T < n4) emit(t + u * T, v[u], g[u]);
+        for (int e4 = t + NI * T; e4 < n4; e4 += T) {
+            float4 xv, gv;
+            load4(e4, xv, gv);
+            emit(e4, xv, gv);
         }
         __syncthreads();
     }
@@ -155,21 +172,27 @@ struct DecLds {
         return 16 * 8 + (size_t)red_floats<R, T>() * 4 + R * 4 + (with_xf ? (size_t)k * 4 : 0) +
                (size_t)extra_floats * 4 + (size_t)(k / 32) * 4 + 16 + k;
     }
+    // Offsets are counted from the (16-byte aligned) base, never through an
+    // integer round trip of the pointer: the compiler then keeps the LDS
+    // address space and emits ds_* accesses (a generic pointer gives flat
+    // accesses, which count as memory loads in the wait counters, so waits
+    // for LDS would also wait for every global load in flight).
     __device__ DecLds(char *p, int k, bool with_xf, int extra_floats) {
-        dscr = (double *)p;
-        p += 16 * 8;
-        red = (float *)p;
-        p += red_floats<R, T>() * 4;
-        y = (float *)p;
-        p += R * 4;
-        xf = (float *)p;
-        p += (with_xf ? (size_t)k * 4 : 0) + (size_t)extra_floats * 4;
-        xq.d = (uint16_t *)p;
-        p += (k / 32) * 2;
-        xq.s = (int16_t *)p;
-        p += (k / 32) * 2;
-        p = (char *)(((uintptr_t)p + 15) & ~(uintptr_t)15);
-        xq.qs = (int8_t *)p;
+        size_t o = 0;
+        dscr = (double *)(p + o);
+        o += 16 * 8;
+        red = (float *)(p + o);
+        o += red_floats<R, T>() * 4;
+        y = (float *)(p + o);
+        o += R * 4;
+        xf = (float *)(p + o);
+        o += (with_xf ? (size_t)k * 4 : 0) + (size_t)extra_floats * 4;
+        xq.d = (uint16_t *)(p + o);
+        o += (k / 32) * 2;
+        xq.s = (int16_t *)(p + o);
+        o += (k / 32) * 2;
+        o = (o + 15) & ~(size_t)15;
+        xq.qs = (int8_t *)(p + o);
     }
 };
 
@@ -225,13 +248,15 @@ __global__ void __launch_bounds__(T) k_dec_wo(
     // l e^(m-M') + l_s e^(m_s-M'), o e^(m-M') + o_s e^(m_s-M')), then
     // quantizes: 8 consecutive lanes hold one Q8_0 block of the output
     // (qwen_one_layer.c:272).  The first group of partials is requested
-    // before the weights, which then load while the merge runs.
+    // before the weights, which then load while the merge runs.  A
+    // wavefront with no elements in this round loads and merges nothing.
     constexpr int SC = 8;
     bool started = false;
     const int qd4 = qd / 4;
     for (int e40 = 0; e40 < qd4; e40 += T) {
         const int e4 = e40 + t;
         const bool eok = e4 < qd4;
+        const bool wact = e40 + (t & ~63) < qd4;  // wavefront-uniform
         const int ec = 4 * min(e4, qd4 - 1);
         const int h = ec / hdim, d = ec - h * hdim;
         float M = -INFINITY, Ls = 0.0f;
@@ -239,23 +264,27 @@ __global__ void __launch_bounds__(T) k_dec_wo(
         for (int s0 = 0; s0 < ns; s0 += SC) {
             float om[SC], ol[SC];
             float4 oo[SC];
+            if (wact) {
 #pragma unroll
-            for (int u = 0; u < SC; ++u) {  // branch-free loads, clamped index
-                const size_t pi = (size_t)h * ns + min(s0 + u, ns - 1);
-                om[u] = pm[pi];
-                ol[u] = pl[pi];
-                oo[u] = *(const float4 *)(po + pi * hdim + d);
+                for (int u = 0; u < SC; ++u) {  // clamped index
+                    const size_t pi = (size_t)h * ns + min(s0 + u, ns - 1);
+                    om[u] = pm[pi];
+                    ol[u] = pl[pi];
+                    oo[u] = *(const float4 *)(po + pi * hdim + d);
+                }
             }
             if (!started) {
                 g.start();
                 started = true;
             }
+            if (!wact) continue;
 #pragma unroll
             for (int u = 0; u < SC; ++u) {
                 if (s0 + u >= ns || om[u] == -INFINITY) continue;  // empty chunk
                 const float mn = fmaxf(M, om[u]);
-                const float a = M == -INFINITY ? 0.0f : expf(M - mn);
-                const float bw = expf(om[u] - mn);
+                // hardware exp2, as in the attention's own online softmax
+                const float a = M == -INFINITY ? 0.0f : __expf(M - mn);
+                const float bw = __expf(om[u] - mn);
                 A[0] = fmaf(oo[u].x, bw, A[0] * a);
                 A[1] = fmaf(oo[u].y, bw, A[1] * a);
                 A[2] = fmaf(oo[u].z, bw, A[2] * a);
@@ -369,7 +398,6 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int DA_TILE = 16;
-constexpr int DA_DEPTH = 2;  // K/V tiles in flight per wavefront (3 measured no faster)
 constexpr int DA_VPAD = 8;  // halves of padding per LDS V row
 
 __device__ __forceinline__ void hi_lo(float x, _Float16 &hi, _Float16 &lo) {
@@ -392,7 +420,10 @@ struct AttnLds {
     }
 };
 
-template <int D, int NW, bool FINAL, bool PAGED>
+// DEPTH: K/V tiles in flight per wavefront; 1 when every wavefront has at
+// most one tile (single queries: more chunks, a shorter chain), else 2 (3
+// measured no faster).
+template <int D, int NW, bool FINAL, bool PAGED, int DEPTH>
 __global__ void __launch_bounds__(NW * 64) k_dec_attn(
     const float *__restrict__ qkv, int ldqkv, int qheads, int kvheads,
     const float *__restrict__ rc, const float *__restrict__ rs, uint16_t *__restrict__ kc,
@@ -492,13 +523,13 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
             rv[u] = *src;
         }
     }
-    // 2. the wavefront's first DA_DEPTH K and V tiles (that many in flight
+    // 2. the wavefront's first DEPTH K and V tiles (that many in flight
     //    throughout)
     constexpr int STEP = DA_TILE * NW;
     int t0 = p0 + DA_TILE * wave;
-    uint4 kr[DA_DEPTH][KS], vr[DA_DEPTH][VL];
+    uint4 kr[DEPTH][KS], vr[DEPTH][VL];
 #pragma unroll
-    for (int b = 0; b < DA_DEPTH; ++b) {
+    for (int b = 0; b < DEPTH; ++b) {
         load_k(t0 + b * STEP, kr[b]);
         load_v(t0 + b * STEP, vr[b]);
     }
@@ -650,19 +681,23 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
-    // tiles t0, t0 + STEP, ... rotate through the DA_DEPTH register sets;
-    // each set is refilled DA_DEPTH tiles ahead once consumed (past the
-    // chunk: clamped, unused).  Every set of a round is consumed, also when
-    // its tile lies past the chunk (all scores masked: the state is
+    // tiles t0, t0 + STEP, ... rotate through the DEPTH register sets; each
+    // set is refilled DEPTH tiles ahead once consumed (past the chunk:
+    // clamped, unused).  With DEPTH 2 every set of a round is consumed, also
+    // when its tile lies past the chunk (all scores masked: the state is
     // unchanged): a conditional exit between the sets makes the compiler
-    // wait for every load in flight at the loop head.
-    for (; t0 < p1; t0 += DA_DEPTH * STEP) {
+    // wait for every load in flight at the loop head.  With DEPTH 1 nothing
+    // else is in flight, so the refill is skipped past the chunk (a
+    // wavefront-uniform test).
+    for (; t0 < p1; t0 += DEPTH * STEP) {
 #pragma unroll
-        for (int b = 0; b < DA_DEPTH; ++b) {
+        for (int b = 0; b < DEPTH; ++b) {
             const int tb = t0 + b * STEP;
             tile(tb, kr[b], vr[b]);
-            load_k(tb + DA_DEPTH * STEP, kr[b]);
-            load_v(tb + DA_DEPTH * STEP, vr[b]);
+            if (DEPTH > 1 || tb + STEP < p1) {
+                load_k(tb + DEPTH * STEP, kr[b]);
+                load_v(tb + DEPTH * STEP, vr[b]);
+            }
         }
     }
 
@@ -677,45 +712,30 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
             ml[wave * per + col] = lsum;
         }
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                mo[((size_t)wave * per + col) * D + 16 * dt + 4 * grp + r] = o[dt][r];
-    }
-    __syncthreads();
-    // per head: M = max over wavefronts, their scale factors e^(m_w - M) and
-    // the total l, once per head
-    float *sc = mo + (size_t)NW * per * D;  // [per][NW]
-    float *ltot = sc + per * NW;            // [per]
-    float *mtot = ltot + per;               // [per]
-    if (tid < per) {
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) M = fmaxf(M, mm[w * per + tid]);
-        float l = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            const float f = M == -INFINITY ? 0.0f : expf(mm[w * per + tid] - M);
-            sc[tid * NW + w] = f;
-            l = fmaf(ml[w * per + tid], f, l);
-        }
-        ltot[tid] = l;
-        mtot[tid] = M;
+        for (int dt = 0; dt < DT; ++dt)  // rows 4*grp .. 4*grp + 3: one 16-byte write
+            *(f4 *)(mo + ((size_t)wave * per + col) * D + 16 * dt + 4 * grp) = o[dt];
     }
     __syncthreads();
     // 4 consecutive elements per thread; 8 lanes = 32 elements = one Q8_0
-    // block of one head (D is a multiple of 32)
+    // block of one head (D is a multiple of 32).  Each thread forms its
+    // head's M = max over wavefronts, the factors e^(m_w - M) and the total
+    // l itself (broadcast LDS reads; no further barrier).
     const int nel4 = per * D / 4;
     for (int e40 = 0; e40 < nel4; e40 += NW * 64) {
         const int e4 = e40 + tid;
         const bool ok = e4 < nel4;
         const int ec = 4 * min(e4, nel4 - 1);
         const int hc = ec / D, dd = ec - hc * D;
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, mm[w * per + hc]);
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ltot = 0.0f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
             const float4 ov = *(const float4 *)(mo + ((size_t)w * per + hc) * D + dd);
-            const float f = sc[hc * NW + w];
+            // hardware exp2, as in the tile loop; an empty wavefront gives 0
+            const float f = M == -INFINITY ? 0.0f : __expf(mm[w * per + hc] - M);
+            ltot = fmaf(ml[w * per + hc], f, ltot);
             acc[0] = fmaf(ov.x, f, acc[0]);
             acc[1] = fmaf(ov.y, f, acc[1]);
             acc[2] = fmaf(ov.z, f, acc[2]);
@@ -726,15 +746,15 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
             if (ok) {
                 const size_t pi = ((size_t)qi * qheads + h) * ns + sp;
                 if (dd == 0) {
-                    ws_m[pi] = mtot[hc];
-                    ws_l[pi] = ltot[hc];
+                    ws_m[pi] = M;
+                    ws_l[pi] = ltot;
                 }
                 *(float4 *)(ws_o + pi * D + dd) = make_float4(acc[0], acc[1], acc[2], acc[3]);
             }
         } else if (e40 + (tid & ~7) < nel4) {
             // normalise (attention_kernels.h:163; no context: 0, :95-98) and
             // quantize_q8
-            const float r = mtot[hc] == -INFINITY ? 0.0f : 1.0f / ltot[hc];
+            const float r = M == -INFINITY ? 0.0f : 1.0f / ltot;
             const float y[4] = {acc[0] * r, acc[1] * r, acc[2] * r, acc[3] * r};
             uint16_t dbits;
             int bsum;
@@ -1245,6 +1265,12 @@ int dec_attn_chunks(int qheads, int kvheads, int hdim, int nq, int max_ctx) {
         return ns < 1 ? 1 : ns;
     }
     const int tiles = (max_ctx + DA_TILE - 1) / DA_TILE;
+    if (nq == 1) {
+        // one query is latency bound: one tile per wavefront (the shortest
+        // chain), up to 32 chunks
+        const int ns = (tiles + DA_NW - 1) / DA_NW;
+        return ns < 1 ? 1 : (ns > 32 ? 32 : ns);
+    }
     int ns = (tiles + 2 * DA_NW - 1) / (2 * DA_NW);
     // enough workgroups to cover the CUs once; a context split beyond that
     // only adds pipeline ramps and partial sums (7B, 64 x 4096: 131 -> 118 us)
@@ -1298,23 +1324,31 @@ static void dec_attn_impl(const float *qkv, int ldqkv, int nq, int qheads, int k
         return;
     }
     const dim3 grid(ns, kvheads, nq);
-#define CALL(DIM, NW, FIN)                                                                     \
-    hipLaunchKernelGGL((k_dec_attn<DIM, NW, FIN, PAGED>), grid, dim3(NW * 64),                        \
+#define CALL(DIM, NW, FIN, DEP)                                                                \
+    hipLaunchKernelGGL((k_dec_attn<DIM, NW, FIN, PAGED, DEP>), grid, dim3(NW * 64),            \
                        (AttnLds<DIM, NW>::bytes(per)), st, qkv, ldqkv, qheads, kvheads, rc, rs,  \
                        kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx, chunk, scale, q_cap,     \
                        ws_m, ws_l, ws_o, attn, aqs, ad, as, pg)
-    // 8 wavefronts unless the merge buffers of a wide GQA group exceed 64 KiB
+#define CALLN(DIM, NW, FIN)                                             \
+    if (chunk <= DA_TILE * NW) {                                        \
+        CALL(DIM, NW, FIN, 1);                                          \
+    } else {                                                            \
+        CALL(DIM, NW, FIN, 2);                                          \
+    }
+    // 8 wavefronts unless the merge buffers of a wide GQA group exceed 64
+    // KiB; one K/V tile in flight per wavefront when each has at most one
+    // (chunk <= 16 * NW positions)
 #define CALLD(DIM)                                           \
     if (AttnLds<DIM, DA_NW>::bytes(per) <= 65536) {          \
         if (fin) {                                           \
-            CALL(DIM, DA_NW, true);                          \
+            CALLN(DIM, DA_NW, true);                         \
         } else {                                             \
-            CALL(DIM, DA_NW, false);                         \
+            CALLN(DIM, DA_NW, false);                        \
         }                                                    \
     } else if (fin) {                                        \
-        CALL(DIM, 4, true);                                  \
+        CALLN(DIM, 4, true);                                 \
     } else {                                                 \
-        CALL(DIM, 4, false);                                 \
+        CALLN(DIM, 4, false);                                \
     }
     switch (hdim) {
         case 32: CALLD(32); break;
@@ -1323,6 +1357,7 @@ static void dec_attn_impl(const float *qkv, int ldqkv, int nq, int qheads, int k
         default: CALLD(128); break;
     }
 #undef CALLD
+#undef CALLN
 #undef CALL
 }
 
