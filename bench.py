@@ -8,12 +8,16 @@ the timed region.  The step cycles through enough distinct copies of the
 layer (weights + KV cache) to exceed the 256 MB Infinity Cache, so the
 reported GB/s is HBM traffic, not cache hits.
 
-The JSON line also carries the other BASELINE configurations (QKV GEMV,
-0.5B and 7B prefill, 7B batched decode), the roofline of the dominant kernel
-(timed with HIP events on its own stream) and the CPU baseline (the oracle's
-C restatement of the reference's portable path, one host core).
+The JSON line's "roofline" is the time-dominant kernel of that step (and
+"roofline_second" the kernel moving the most bytes), each timed by HIP
+events attached to its own dispatches; "configs" carries every BASELINE
+configuration (1 QKV mat-vec, 2 the decode layer, 3 and 4 the 0.5B and 7B
+prefills, 5 the 7B batched decode) with its dominant kernel's roofline and
+a CPU baseline: the oracle's C restatement of the reference's portable path
+on one pinned host core, each a bounded sample stated in the line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+    python bench.py --profile N     # configuration N's GPU legs only (rocprofv3)
 """
 import argparse
 import ctypes
@@ -32,11 +36,21 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, GB/s
 INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA, TOP/s
 MALL_BYTES = 256 << 20      # Infinity Cache
 METRIC = "decode layer µs + HBM GB/s; prefill tokens/s + int8 MFMA % (one GPU)"
-# HBM bytes per launch of the dominant kernel (k_dec_gateup, 0.5B), from two
-# rocprofv3 --pmc runs of `bench.py --dominant-only` (FETCH_SIZE 2521.4 KiB,
-# WRITE_SIZE 9.8 KiB per dispatch, medians) scaled by what the counters read
-# for a 256 MiB copy (FETCH_SIZE x2.000, WRITE_SIZE x1.000).
-DOMINANT_TRAFFIC_BYTES = (2521.4 * 2.000 + 9.8 * 1.000) * 1024
+# HBM bytes per launch of a configuration's kernels, from two rocprofv3
+# --pmc runs of `bench.py --profile N` (FETCH_SIZE, then WRITE_SIZE, KiB per
+# dispatch, medians over the run's dispatches of that kernel), scaled by what
+# the counters read for a 256 MiB copy (FETCH_SIZE x2.000, WRITE_SIZE
+# x1.000): {(config, kernel prefix): (FETCH_SIZE KiB, WRITE_SIZE KiB)}.
+# Kernels not listed report traffic null.
+PMC_KIB = {}
+FETCH_SCALE, WRITE_SCALE = 2.000, 1.000
+
+
+def pmc_traffic(cfg, kernel):
+    for (c, prefix), (f, w) in PMC_KIB.items():
+        if c == cfg and kernel.startswith(prefix):
+            return round((f * FETCH_SCALE + w * WRITE_SCALE) * 1024)
+    return None
 
 
 def log(*a):
@@ -98,6 +112,59 @@ def graph_time_ms(torch, stream, fn, count, replays=3):
     torch.cuda.synchronize()
     del g
     return ms
+
+
+def kernel_sequence(si_amd, fn, kernel_filter, capacity=16384):
+    """[(kernel, us)] in launch order: per-dispatch durations of the kernels
+    fn() launches whose names match kernel_filter (HIP events attached to
+    each dispatch by si_kernel_timing_*, on the stream it is launched on)."""
+    return [(n, ms * 1e3) for n, ms in si_amd.kernel_times_ms(kernel_filter, fn, capacity)]
+
+
+def kernel_durations(si_amd, fn, kernel_filter, capacity=16384):
+    """{kernel: [us, ...]} of kernel_sequence."""
+    out = {}
+    for name, us in kernel_sequence(si_amd, fn, kernel_filter, capacity):
+        out.setdefault(name, []).append(us)
+    return out
+
+
+def roofline_entry(kernel, us, work, bound, cfg, launches):
+    """One roofline block: work per launch (bytes for "hbm", int ops for
+    "mfma") over the kernel's mean per-dispatch duration."""
+    if bound == "hbm":
+        achieved, peak, unit = work / (us * 1e-6) / 1e9, HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved, peak, unit = work / (us * 1e-6) / 1e12, INT8_PEAK_TOPS, "TOP/s"
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": pmc_traffic(cfg, kernel),
+            "kernel": kernel, "kernel_us": round(us, 3), "launches": launches,
+            ("alg_bytes_per_launch" if bound == "hbm" else "int_ops_per_launch"): int(work),
+            "timing": "mean of per-dispatch HIP events (si_kernel_timing_*)"}
+
+
+DECODE_PHASES = ["qkv", "attention", "out_proj", "gate_up", "down"]
+
+
+def decode_kernel_work(s, ctx, nseq=1):
+    """Algorithmic bytes per launch of the decode layer's kernels by phase
+    (k_dec_qkv; k_dec_attn / k_dec_attn_rows; W_O: k_dec_wo or k_matvec;
+    k_dec_gateup; k_matvec for down): weights, the cache rows attention must
+    read, the new K/V rows, activation rows in and out, norm gains and
+    biases.  Partial states of a split context are implementation traffic,
+    not counted."""
+    H, QD, KVD, F = s.hidden, s.qheads * s.hdim, s.kvheads * s.hdim, s.ffn
+    NQKV = QD + 2 * KVD
+    q4 = lambda n, k: n * k // 32 * 18  # noqa: E731
+    q8 = lambda k: k + (k // 32) * 4  # noqa: E731  values, fp16 scale, int16 sum
+    return {
+        "qkv": q4(NQKV, H) + nseq * (H * 4) + H * 4 + NQKV * 4 + nseq * NQKV * 4,
+        "attention": nseq * ((ctx - 1) * KVD * 2 * 2 + KVD * 2 * 2 + NQKV * 4 + QD * 4)
+                     + s.hdim * 4,
+        "out_proj": q4(H, QD) + nseq * (QD * 4 + H * 4 + H * 4),
+        "gate_up": q4(2 * F, H) + nseq * (H * 4 + q8(F)) + H * 4,
+        "down": q4(H, F) + nseq * (q8(F) + H * 4 + H * 4),
+    }
 
 
 class _DevArray:
@@ -182,59 +249,36 @@ def bench_decode_layer(torch, si_amd, stream, steps, warmup, ctx=1024, shape_nam
                 acc[k] = acc.get(k, 0.0) + v / 20
         layers[0].set_timing(False)
         torch.cuda.synchronize()
+        # per-dispatch durations of the five kernels over min(steps, 200)
+        # eager steps (the same rotation of copies), by position in the step
+        nk = min(steps, 200)
+        seq = kernel_sequence(si_amd, lambda: [step(i) for i in range(nk)],
+                              "k_dec_|k_matvec<")
+        torch.cuda.synchronize()
+    per = len(DECODE_PHASES)
+    assert len(seq) == per * nk, f"{len(seq)} timed launches for {nk} steps"
+    kern = {ph: (seq[j][0], [us for _, us in seq[j::per]]) for j, ph in enumerate(DECODE_PHASES)}
     # timed region: exactly `steps` decode steps, captured as one HIP graph
     ms = graph_time_ms(torch, stream, step, steps, replays=3)
     alg = per_copy
     res = dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, alg_bytes=alg, copies=copies,
                eager_us=eager_ms * 1e3,
-               phases_us_eager={k: round(v * 1e3, 2) for k, v in acc.items()})
+               phases_us_eager={k: round(v * 1e3, 2) for k, v in acc.items()},
+               kernels={ph: {"kernel": n, "us": round(float(np.mean(v)), 3), "launches": len(v)}
+                        for ph, (n, v) in kern.items()})
     return res, (layers, caches, s, x, ws)
 
 
-def bench_dominant_kernel(torch, si_amd, stream, launches=400):
-    """Roofline of the decode step's dominant kernel: k_dec_gateup, the fused
-    post-norm -> Q8 -> gate|up mat-vec -> SwiGLU -> Q8 stage that moves 4.9 MB
-    of the 0.5B layer's 8.9 MB, launched alone (si_ffn_gateup_q8) on the bench
-    stream, cycling through enough copies of its weights to exceed the
-    Infinity Cache (cold weights, as in the layer)."""
-    L = si_amd.lib()
-    s = si_amd.make_shape(**si_amd.SHAPES["0.5b"])
-    F, H = s.ffn, s.hidden
-    n, k = 2 * F, H
-    per = n * k // 32 * 18
-    ncopy = int(np.ceil(1.25 * MALL_BYTES / per))
-    gen = torch.Generator(device="cuda").manual_seed(21)
-    nd = L.si_q4_scale_count(n, k, 32)
-    mats = []
-    for _ in range(ncopy):
-        qs = torch.randint(0, 256, (n * k // 2,), generator=gen, device="cuda", dtype=torch.uint8)
-        d = torch.full((nd,), 0x2000, dtype=torch.int16, device="cuda")  # fp16 2^-7
-        mats.append((qs, d))
-    h = torch.randn(H, generator=gen, device="cuda")
-    gain = torch.ones(H, device="cuda")
-    aq = torch.empty(F, dtype=torch.int8, device="cuda")
-    ad = torch.empty(F // 32, dtype=torch.int16, device="cuda")
-    asum = torch.empty(F // 32, dtype=torch.int16, device="cuda")
-
-    def launch(i):
-        qs, d = mats[i % ncopy]
-        rc = L.si_ffn_gateup_q8(si_amd.ptr(h), si_amd.ptr(gain), H, ctypes.c_float(1e-6),
-                                si_amd.ptr(qs), si_amd.ptr(d), 32, F, None, si_amd.ptr(aq),
-                                si_amd.ptr(ad), si_amd.ptr(asum), 0,
-                                si_amd.stream_handle(torch.cuda.current_stream()))
-        if rc:
-            raise si_amd.SiError(rc, L.si_last_error().decode())
-
-    with torch.cuda.stream(stream):
-        for i in range(ncopy + 5):
-            launch(i)
-    torch.cuda.synchronize()
-    ms = graph_time_ms(torch, stream, launch, launches, replays=3)
-    # weights + h + gain in, Q8 activation (values, scales, sums) out
-    alg = per + 2 * H * 4 + F + (F // 32) * 4
-    achieved = alg / (ms * 1e-3) / 1e9
-    return dict(kernel="k_dec_gateup<64, 512> (0.5B gate|up + SwiGLU, N=9728 K=896)",
-                us=ms * 1e3, alg_bytes=alg, achieved_gbs=achieved, copies=ncopy)
+def decode_rooflines(res, s, ctx, cfg, nseq=1):
+    """Roofline blocks of a decode run's kernels by phase, the time-dominant
+    one first."""
+    work = decode_kernel_work(s, ctx, nseq)
+    out = []
+    for ph, k in sorted(res["kernels"].items(), key=lambda kv: -kv[1]["us"]):
+        e = roofline_entry(k["kernel"], k["us"], work[ph], "hbm", cfg, k["launches"])
+        e["phase"] = ph
+        out.append(e)
+    return out
 
 
 def bench_qkv_gemv(torch, si_amd, stream, launches=1000):
@@ -276,10 +320,16 @@ def bench_qkv_gemv(torch, si_amd, stream, launches=1000):
     with torch.cuda.stream(stream):
         for i in range(50):
             launch(i)
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        kern = kernel_durations(si_amd, lambda: [launch(i) for i in range(launches)],
+                                "k_matvec<")
+        torch.cuda.synchronize()
     ms = graph_time_ms(torch, stream, launch, launches, replays=3)
     alg = 586168  # W 580,608 + x 952 + y 4,608 bytes (config 1)
-    return dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, copies=copies)
+    name, durs = next(iter(kern.items()))
+    return dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, copies=copies,
+                timing="HIP graph of the launches (us includes the launch-to-launch gap)",
+                roofline=roofline_entry(name, float(np.mean(durs)), alg, "hbm", "1", len(durs)))
 
 
 def bench_gemv_7b(torch, si_amd, stream, launches=200):
@@ -430,7 +480,7 @@ def bench_prefill(torch, si_amd, stream, shape_name, ntok, steps):
     vc = torch.zeros_like(kc)
     out = torch.empty(ntok * s.hidden, device="cuda")
     def call(i):
-        lay.prefill(x, ntok, 0, kc, vc, out, stream=torch.cuda.current_stream())
+        lay.prefill(x, ntok, 0, kc, vc, out, stream=torch.cuda.current_stream(), capture=False)
 
     with torch.cuda.stream(stream):
         for i in range(2):
@@ -439,17 +489,27 @@ def bench_prefill(torch, si_amd, stream, shape_name, ntok, steps):
         call(0)
         ph = lay.phase_ms()
         lay.set_timing(False)
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        # every kernel of `reps` prefill calls, per dispatch
+        reps = max(2, min(steps, 5))
+        kern = kernel_durations(si_amd, lambda: [call(i) for i in range(reps)], "k_")
+        torch.cuda.synchronize()
     ms = graph_time_ms(torch, stream, call, steps, replays=2)
-    gemm_ms = gemm_graph_ms(torch, si_amd, stream, lay, s, ntok, steps)
+    gemm_ms, gu = gemm_graph_ms(torch, si_amd, stream, lay, s, ntok, steps)
     ops = gemm_int_ops(s, ntok)
     lay.close()
+    cfg = "3" if shape_name == "0.5b" else "4"
+    per_call = {k: round(float(np.sum(v)) / reps, 3) for k, v in kern.items()}
+    gname, gdur = max(gu.items(), key=lambda kv: len(kv[1]))
     return dict(ms=ms, tokens_per_s=ntok / (ms * 1e-3),
                 gemm_ms=gemm_ms, gemm_tops=ops / (gemm_ms * 1e-3) / 1e12,
                 mfma_pct_gemm=100.0 * ops / (gemm_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
                 mfma_pct_layer=100.0 * ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
                 gemm_timing="the four projections alone, one HIP graph (gemm_graph_ms)",
-                phases_ms={k: round(v, 4) for k, v in ph.items()})
+                phases_ms={k: round(v, 4) for k, v in ph.items()},
+                kernels_us_per_call=dict(sorted(per_call.items(), key=lambda kv: -kv[1])),
+                roofline=roofline_entry(gname, float(np.mean(gdur)),
+                                        2 * ntok * 2 * s.ffn * s.hidden, "mfma", cfg, len(gdur)))
 
 
 def gemm_graph_ms(torch, si_amd, stream, lay, s, m, steps):
@@ -471,17 +531,26 @@ def gemm_graph_ms(torch, si_amd, stream, lay, s, m, steps):
                     b(xq), b(xd), m, None, res, dst, ldo, 0, wsp, ws_bytes,
                     si_amd.stream_handle(torch.cuda.current_stream()))
 
+    def gateup():
+        qs, d, tile, n, k = W[2]
+        # no gu / act outputs: the layer writes neither without SI_LAYER_CAPTURE
+        si_amd.call("si_gemm_gateup_q8", ctypes.c_void_p(qs), ctypes.c_void_p(d), tile, F, k,
+                    b("XQ2_QS"), b("XQ2_D"), m, None, None, b("ACTQ_QS"), b("ACTQ_D"),
+                    b("ACTQ_S"), 0, wsp, ws_bytes,
+                    si_amd.stream_handle(torch.cuda.current_stream()))
+
     def step(i):
         gemm(W[0], "XQ_QS", "XQ_D", b("QKV"), W[0][3])
         gemm(W[1], "ATTQ_QS", "ATTQ_D", b("ATTN_OUT"), H)
-        qs, d, tile, n, k = W[2]
-        si_amd.call("si_gemm_gateup_q8", ctypes.c_void_p(qs), ctypes.c_void_p(d), tile, F, k,
-                    b("XQ2_QS"), b("XQ2_D"), m, b("GU"), b("ACT"), b("ACTQ_QS"), b("ACTQ_D"),
-                    b("ACTQ_S"), 0, wsp, ws_bytes,
-                    si_amd.stream_handle(torch.cuda.current_stream()))
+        gateup()
         gemm(W[3], "ACTQ_QS", "ACTQ_D", si_amd.ptr(out), H, b("H"))
 
-    return graph_time_ms(torch, stream, step, steps, replays=2)
+    # the gate|up GEMM (the prefill's time-dominant kernel) alone, per dispatch
+    with torch.cuda.stream(stream):
+        gu = kernel_durations(si_amd, lambda: [gateup() for _ in range(max(3, steps))],
+                              "k_gemm")
+        torch.cuda.synchronize()
+    return graph_time_ms(torch, stream, step, steps, replays=2), gu
 
 
 def bench_batched_decode(torch, si_amd, stream, steps, nseq=64, ctx=4096):
@@ -498,7 +567,7 @@ def bench_batched_decode(torch, si_amd, stream, steps, nseq=64, ctx=4096):
     out = torch.empty(nseq * s.hidden, device="cuda")
     def call(i):
         lay.decode_batch(x, nseq, kc, vc, stride, ctx, ctx, out,
-                         stream=torch.cuda.current_stream())
+                         stream=torch.cuda.current_stream(), capture=False)
 
     with torch.cuda.stream(stream):
         for i in range(2):
@@ -507,12 +576,24 @@ def bench_batched_decode(torch, si_amd, stream, steps, nseq=64, ctx=4096):
         call(0)
         ph = lay.phase_ms()
         lay.set_timing(False)
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        reps = max(2, min(steps, 5))
+        kern = kernel_durations(si_amd, lambda: [call(i) for i in range(reps)], "k_")
+        torch.cuda.synchronize()
     ms = graph_time_ms(torch, stream, call, steps, replays=2)
     alg = weight_bytes(s) + nseq * 2 * ctx * kvd * 2 + small_bytes(s)
     lay.close()
-    return dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, alg_bytes=alg,
-                phases_us={k: round(v * 1e3, 2) for k, v in ph.items()})
+    per_call = {k: round(float(np.sum(v)) / reps, 3) for k, v in kern.items()}
+    res = dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, alg_bytes=alg,
+               phases_us={k: round(v * 1e3, 2) for k, v in ph.items()},
+               kernels_us_per_call=dict(sorted(per_call.items(), key=lambda kv: -kv[1])))
+    att = [k for k in kern if k.startswith("k_dec_attn")]
+    if att:
+        a = att[0]
+        res["roofline"] = roofline_entry(a, float(np.mean(kern[a])),
+                                         decode_kernel_work(s, ctx, nseq)["attention"],
+                                         "hbm", "5", len(kern[a]))
+    return res
 
 
 def bench_paged_decode(torch, si_amd, stream, steps, nseq=64, ctx=4096, page_size=64,
@@ -540,7 +621,7 @@ def bench_paged_decode(torch, si_amd, stream, steps, nseq=64, ctx=4096, page_siz
 
     def call(i):
         lay.decode_paged(x, nseq, kp, vp, npages, page_size, table, max_pages, ctx_dev, ctx, out,
-                         stream=torch.cuda.current_stream())
+                         stream=torch.cuda.current_stream(), capture=False)
 
     with torch.cuda.stream(stream):
         for i in range(2):
@@ -588,65 +669,188 @@ def bench_paged_decode(torch, si_amd, stream, steps, nseq=64, ctx=4096, page_siz
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the oracle (C restatement of the reference's portable path)
+# CPU baselines: the oracle (C restatement of the reference's portable path,
+# oracle/libsi_oracle.so built -O2 -ffp-contract=off as the reference's
+# Makefile:7), one pinned host core, medians after a warm-up call
+# (audit_fusion_timing.c:65-74, :272-317)
 # ---------------------------------------------------------------------------
-def cpu_baseline(budget_s=12.0, ctx=1024):
+def _cpu_name():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+class _Pinned:
+    """Runs the block on the first core this process may use."""
+
+    def __enter__(self):
+        self.old = os.sched_getaffinity(0)
+        self.core = sorted(self.old)[0]
+        os.sched_setaffinity(0, {self.core})
+        return self
+
+    def __exit__(self, *a):
+        os.sched_setaffinity(0, self.old)
+
+
+def _median_time(fn, budget_s, max_n=2000, min_n=1, warm=True):
+    if warm:
+        fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_n or (time.perf_counter() < t_end and len(times) < max_n):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def _oracle_inputs(si_amd, name, ctx, seed):
     from oracle.oracle_py import Oracle, make_shape as or_shape
-    import si_amd
     o = Oracle()
-    sd = si_amd.SHAPES["0.5b"]
+    sd = si_amd.SHAPES[name]
     s = or_shape(**sd)
-    tens = make_layer_tensors(si_amd, si_amd.make_shape(**sd), 1)
+    tens = make_layer_tensors(si_amd, si_amd.make_shape(**sd), seed)
     rng = np.random.default_rng(3)
     kvd = s.kvheads * s.hdim
     kc = o.f32_to_f16(rng.standard_normal(ctx * kvd).astype(np.float32))
     vc = o.f32_to_f16(rng.standard_normal(ctx * kvd).astype(np.float32))
-    x = rng.standard_normal(s.hidden).astype(np.float32)
-    old = os.sched_getaffinity(0)
-    core = sorted(old)[0]
-    os.sched_setaffinity(0, {core})
-    try:
-        o.layer_decode(s, tens, x, kc, vc, ctx)  # warm-up
-        times = []
-        t_end = time.perf_counter() + budget_s
-        while time.perf_counter() < t_end and len(times) < 2000:
-            t0 = time.perf_counter()
-            o.layer_decode(s, tens, x, kc, vc, ctx)
-            times.append(time.perf_counter() - t0)
-    finally:
-        os.sched_setaffinity(0, old)
-    med = float(np.median(times))
-    alg = weight_bytes(si_amd.make_shape(**sd)) + 2 * ctx * kvd * 2 + small_bytes(s)
-    cpu = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return dict(value=alg / med / 1e9, unit="GB/s", cores=1, kind="port",
-                sample=f"{len(times)} full 0.5B layer decodes at context 1024 "
-                       f"(median {med * 1e3:.2f} ms/token) on core {core} of '{cpu}', "
-                       f"oracle/libsi_oracle.so built -O2 -ffp-contract=off")
+    return o, s, tens, kc, vc, rng
+
+
+def cpu_baselines(si_amd, budget_s=10.0):
+    """Per-configuration CPU legs, each a bounded sample (stated in "sample")
+    in the unit of that configuration's GPU figure."""
+    cpu = _cpu_name()
+    common = f"oracle/libsi_oracle.so (-O2 -ffp-contract=off), 1 pinned core of '{cpu}'"
+    out = {}
+    with _Pinned() as pin:
+        where = f"core {pin.core}; {common}"
+        # config 2: full 0.5B layer decode at context 1024
+        o, s, tens, kc, vc, rng = _oracle_inputs(si_amd, "0.5b", 1024, 1)
+        x = rng.standard_normal(s.hidden).astype(np.float32)
+        med, n = _median_time(lambda: o.layer_decode(s, tens, x, kc, vc, 1024), budget_s)
+        sh = si_amd.make_shape(**si_amd.SHAPES["0.5b"])
+        alg = weight_bytes(sh) + 2 * 1024 * s.kvheads * s.hdim * 2 + small_bytes(sh)
+        out["2"] = dict(value=alg / med / 1e9, unit="GB/s", cores=1, kind="port",
+                        us_per_token=med * 1e6,
+                        sample=f"{n} layer decodes at context 1024, median {med * 1e3:.2f} "
+                               f"ms/token; {where}")
+        # config 1: the QKV mat-vec (K 896, N 1152) alone
+        wqkv = np.concatenate([tens["wq"].reshape(-1), tens["wk"].reshape(-1),
+                               tens["wv"].reshape(-1)])
+        bias = np.concatenate([tens["bq"], tens["bk"], tens["bv"]])
+        xq = o.quantize_q8(x)
+        med, n = _median_time(lambda: o.matvec(wqkv, xq, 896, 1152, bias), budget_s / 4)
+        out["1"] = dict(value=586168 / med / 1e9, unit="GB/s", cores=1, kind="port",
+                        us=med * 1e6,
+                        sample=f"{n} matvec_q4q8 calls (K 896, N 1152), median "
+                               f"{med * 1e6:.1f} us; {where}")
+        # config 3: 0.5B prefill of 512 tokens, in full
+        x3 = rng.standard_normal(512 * s.hidden).astype(np.float32)
+        kc3 = np.zeros(512 * s.kvheads * s.hdim, np.uint16)
+        vc3 = np.zeros_like(kc3)
+        med, n = _median_time(lambda: o.layer_prefill(s, tens, x3, 512, 0, kc3, vc3), 0.0,
+                              warm=False)
+        out["3"] = dict(value=512 / med, unit="tokens/s", cores=1, kind="port",
+                        s_per_prefill=med,
+                        sample=f"{n} full 512-token prefills, median {med:.2f} s; {where}")
+        del o, tens, kc, vc, kc3, vc3
+        # configs 4 and 5: the 7B layer
+        o, s, tens, kc, vc, rng = _oracle_inputs(si_amd, "7b", 4096, 5)
+        H, KVD = s.hidden, s.kvheads * s.hdim
+        # config 4 (2048-token prefill): K/V of 256 tokens, one token's full
+        # row, attention at context 2048, extrapolated linearly
+        x4 = rng.standard_normal(256 * H).astype(np.float32)
+        empty = np.zeros(0, np.int32)
+        t_kv, _ = _median_time(lambda: o.layer_prefill(s, tens, x4, 256, 0, kc, vc, rows=empty),
+                               0.0, warm=False)
+        t_row, _ = _median_time(lambda: o.layer_prefill(s, tens, x4[:H], 1, 0, kc, vc,
+                                                        rows=np.zeros(1, np.int32)), 0.0,
+                                min_n=3)
+        q = rng.standard_normal(s.qheads * s.hdim).astype(np.float32)
+        t_att, _ = _median_time(lambda: o.attention_flash(s, q, kc, vc, 2048), 0.0, min_n=5)
+        t_row_proj = t_row - t_kv / 256  # the single token's own K/V is in t_kv
+        total = 8 * t_kv + 2048 * t_row_proj + t_att * 2049 / 2
+        out["4"] = dict(value=2048 / total, unit="tokens/s", cores=1, kind="port",
+                        s_per_prefill_extrapolated=total,
+                        sample=f"measured: K/V of 256 tokens {t_kv:.2f} s, one token's full "
+                               f"row {t_row * 1e3:.0f} ms, attention at context 2048 "
+                               f"{t_att * 1e3:.1f} ms; extrapolated to 2048 tokens as 8 x "
+                               f"K/V(256) + 2048 x row + attention(2048) x 2049/2 (projections "
+                               f"exactly linear in tokens, attention linear in context); "
+                               f"{where}")
+        # config 5 (64 sequences x context 4096): 16 of the 64 single-token
+        # decodes (independent sequences: x4)
+        x5 = rng.standard_normal(H).astype(np.float32)
+        o.layer_decode(s, tens, x5, kc, vc, 4096)  # warm-up
+        t0 = time.perf_counter()
+        for _ in range(16):
+            o.layer_decode(s, tens, x5, kc, vc, 4096)
+        t16 = time.perf_counter() - t0
+        sh7 = si_amd.make_shape(**si_amd.SHAPES["7b"])
+        alg5 = weight_bytes(sh7) + 64 * 2 * 4096 * KVD * 2 + small_bytes(sh7)
+        out["5"] = dict(value=alg5 / (4 * t16) / 1e9, unit="GB/s", cores=1, kind="port",
+                        us_per_step_extrapolated=4 * t16 * 1e6,
+                        sample=f"16 of the 64 sequences' decodes at context 4096 in "
+                               f"{t16:.2f} s, x4 for the 64-sequence step (sequences are "
+                               f"independent); {where}")
+    return out
 
 
 # ---------------------------------------------------------------------------
+WORKLOADS = {
+    "1": "fused QKV Q4_0 x Q8_0 mat-vec, 1 token, 0.5B shape (K 896, N 1152)",
+    "2": "full Qwen2.5-0.5B-shaped layer, decode of 1 token at context 1024",
+    "3": "Qwen2.5-0.5B-shaped layer, prefill of 512 tokens",
+    "4": "Qwen2.5-7B-shaped layer, prefill of 2048 tokens",
+    "5": "Qwen2.5-7B-shaped layer, batched decode of 64 sequences x 1 token at context 4096",
+}
+
+
+def run_config(cfg, torch, si_amd, stream, steps, warmup):
+    """One BASELINE configuration's GPU figures and roofline block."""
+    if cfg == "1":
+        r = bench_qkv_gemv(torch, si_amd, stream)
+        r["hbm_frac"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
+        return r
+    if cfg == "2":
+        r, held = bench_decode_layer(torch, si_amd, stream, steps, warmup)
+        s = si_amd.make_shape(**si_amd.SHAPES["0.5b"])
+        roofs = decode_rooflines(r, s, 1024, "2")
+        r["roofline"] = roofs[0]
+        r["kernel_rooflines"] = roofs
+        r["hbm_frac"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
+        for lay in held[0]:
+            lay.close()
+        held[4].close()
+        return r
+    if cfg in ("3", "4"):
+        name, ntok = ("0.5b", 512) if cfg == "3" else ("7b", 2048)
+        return bench_prefill(torch, si_amd, stream, name, ntok, 10 if cfg == "3" else 3)
+    r = bench_batched_decode(torch, si_amd, stream, 5)
+    r["hbm_frac"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
+    return r
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--quick", action="store_true", help="skip the other configurations")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--dominant-only", action="store_true",
-                    help="run only the dominant-kernel leg (for rocprofv3)")
-    ap.add_argument("--only", choices=["prefill-0.5b", "prefill-7b", "batched-7b", "decode-7b",
-                                       "gguf-7b", "attention-7b", "paged-7b"],
-                    help="run only this configuration and print its result (for rocprofv3)")
+    ap.add_argument("--quick", action="store_true", help="configuration 2 and the 7B decode only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--profile", choices=sorted(WORKLOADS),
+                    help="run one configuration's GPU legs only (for rocprofv3)")
+    ap.add_argument("--only", choices=["gguf-7b", "attention-7b", "paged-7b", "decode-7b"],
+                    help="run one of the other measurements only")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); "
+        print(f"bench.py --gpus {args.gpus}: this build runs on one GPU only; "
               "the path is measured on one GPU's share and no multi-GPU run exists.",
               file=sys.stderr)
         sys.exit(2)
@@ -663,27 +867,22 @@ def main():
             r = bench_attention_modes(torch, si_amd)
         elif args.only == "paged-7b":
             r = bench_paged_decode(torch, si_amd, stream, 5)
-        elif args.only == "decode-7b":
-            r, _ = bench_decode_layer(torch, si_amd, stream, 100, 10, ctx=4096, shape_name="7b")
-        elif args.only == "batched-7b":
-            r = bench_batched_decode(torch, si_amd, stream, 5)
         else:
-            name, ntok = ("0.5b", 512) if args.only == "prefill-0.5b" else ("7b", 2048)
-            r = bench_prefill(torch, si_amd, stream, name, ntok, 3)
+            r, _ = bench_decode_layer(torch, si_amd, stream, 100, 10, ctx=4096, shape_name="7b")
         print(json.dumps({"only": args.only, **r}), flush=True)
         return
-    if args.dominant_only:
-        dom = bench_dominant_kernel(torch, si_amd, stream)
-        print(json.dumps({"dominant_kernel": dom["kernel"], "us": round(dom["us"], 3),
-                          "achieved_gbs": round(dom["achieved_gbs"], 2)}), flush=True)
+    if args.profile:
+        steps = min(args.steps, 100)
+        r = run_config(args.profile, torch, si_amd, stream, steps, min(args.warmup, 10))
+        print(json.dumps({"profile": args.profile, **r}), flush=True)
         return
     t0 = time.time()
+    configs = {}
     log("config 2: 0.5B decode layer, ctx 1024 ...")
-    dec, ctxobj = bench_decode_layer(torch, si_amd, stream, args.steps, args.warmup)
-    log(f"  {dec['us']:.2f} us/token, {dec['gbs']:.1f} GB/s ({time.time() - t0:.0f} s)")
-    log("roofline: dominant kernel ...")
-    dom = bench_dominant_kernel(torch, si_amd, stream)
-    log(f"  {dom['us']:.2f} us/launch, {dom['achieved_gbs']:.1f} GB/s")
+    dec = run_config("2", torch, si_amd, stream, args.steps, args.warmup)
+    configs["2"] = dec
+    log(f"  {dec['us']:.2f} us/token, {dec['gbs']:.1f} GB/s; kernels {dec['kernels']} "
+        f"({time.time() - t0:.0f} s)")
     extra = {}
     log("7B decode projections (k_matvec) ...")
     extra["gemv_7b_cold"] = bench_gemv_7b(torch, si_amd, stream)
@@ -694,39 +893,43 @@ def main():
         lay.close()
     held[4].close()
     del held
-    extra["decode_7b_ctx4096"] = {k: (round(v, 2) if isinstance(v, float) else v)
-                                  for k, v in d7.items()}
-    extra["decode_7b_ctx4096"]["hbm_frac"] = round(d7["gbs"] / HBM_PEAK_GBS, 4)
-    log(f"  {extra['decode_7b_ctx4096']}")
-    del d7
+    s7 = si_amd.make_shape(**si_amd.SHAPES["7b"])
+    d7["kernel_rooflines"] = decode_rooflines(d7, s7, 4096, "7b-decode")
+    d7["hbm_frac"] = round(d7["gbs"] / HBM_PEAK_GBS, 4)
+    extra["decode_7b_ctx4096"] = d7
+    log(f"  {d7['us']:.2f} us/token; kernels {d7['kernels']}")
     torch.cuda.empty_cache()
     if not args.quick:
-        log("config 1: QKV GEMV ...")
-        extra["cfg1_qkv_gemv_0.5b"] = bench_qkv_gemv(torch, si_amd, stream)
-        log(f"  {extra['cfg1_qkv_gemv_0.5b']}")
-        log("config 3: 0.5B prefill 512 ...")
-        extra["cfg3_prefill_0.5b_512"] = bench_prefill(torch, si_amd, stream, "0.5b", 512, 10)
-        log(f"  {extra['cfg3_prefill_0.5b_512']}")
-        log("config 4: 7B prefill 2048 ...")
-        extra["cfg4_prefill_7b_2048"] = bench_prefill(torch, si_amd, stream, "7b", 2048, 3)
-        log(f"  {extra['cfg4_prefill_7b_2048']}")
+        for cfg in ("1", "3", "4", "5"):
+            log(f"config {cfg}: {WORKLOADS[cfg]} ...")
+            configs[cfg] = run_config(cfg, torch, si_amd, stream, args.steps, args.warmup)
+            log(f"  {configs[cfg]}")
+            torch.cuda.empty_cache()
         log("attention methods, 7B-shaped, ctx 4096 ...")
         extra["attention_standard_vs_flash_7b_ctx4096"] = bench_attention_modes(torch, si_amd)
         log(f"  {extra['attention_standard_vs_flash_7b_ctx4096']}")
         log("GGUF ingest, 7B-shaped layer ...")
         extra["gguf_ingest_7b_layer"] = bench_gguf_ingest(torch, si_amd)
         log(f"  {extra['gguf_ingest_7b_layer']}")
-        log("config 5: 7B batched decode 64 x 4096 ...")
-        extra["cfg5_batched_decode_7b_64x4096"] = bench_batched_decode(torch, si_amd, stream, 5)
-        log(f"  {extra['cfg5_batched_decode_7b_64x4096']}")
         log("config 5 shape over a paged KV pool, and a 2-layer stack ...")
         extra["paged_batched_decode_7b_64x4096"] = bench_paged_decode(torch, si_amd, stream, 5)
         log(f"  {extra['paged_batched_decode_7b_64x4096']}")
-    cpu = None
+    cpu = {}
     if not args.no_cpu:
-        log("CPU baseline (oracle, 1 core) ...")
-        cpu = cpu_baseline()
-        log(f"  {cpu}")
+        log("CPU baselines (oracle, 1 pinned core) ...")
+        t1 = time.time()
+        cpu = cpu_baselines(si_amd)
+        log(f"  {cpu} ({time.time() - t1:.0f} s)")
+    gpu_value = {"1": ("gbs", "GB/s"), "2": ("gbs", "GB/s"), "3": ("tokens_per_s", "tokens/s"),
+                 "4": ("tokens_per_s", "tokens/s"), "5": ("gbs", "GB/s")}
+    for cfg, r in configs.items():
+        r["workload"] = WORKLOADS[cfg]
+        if cfg in cpu:
+            r["cpu_baseline"] = cpu[cfg]
+            key, unit = gpu_value[cfg]
+            assert cpu[cfg]["unit"] == unit
+            r["gpu_over_cpu"] = round(r[key] / cpu[cfg]["value"], 1)
+    second = [e for e in dec["kernel_rooflines"] if e["phase"] == "gate_up"]
     line = {
         "metric": METRIC,
         "value": round(dec["gbs"], 2),
@@ -740,23 +943,18 @@ def main():
         "vs_baseline": None,
         "dtype": "int8xint4 (fp32 accumulate)",
         "data": "synthetic (seeded N(0,0.02) weights -> Q4_0, N(0,1) activations and fp16 KV)",
-        "config": {"workload": "full Qwen2.5-0.5B-shaped layer, decode of 1 token at context "
-                               "1024 (BASELINE configs[1])",
+        "config": {"workload": WORKLOADS["2"] + " (BASELINE configs[1])",
                    "hidden": 896, "qheads": 14, "kvheads": 2, "head_dim": 64, "ffn": 4864,
                    "context": 1024, "layer_copies_rotated": dec["copies"],
                    "alg_bytes_per_step": dec["alg_bytes"]},
         "decode_layer_us": round(dec["us"], 3),
         "decode_layer_us_eager": round(dec["eager_us"], 3),
-        "phases_us_eager": dec["phases_us_eager"],
         "timing": "HIP graph replay of the K steps (one graph), HIP events on the bench stream",
-        "roofline": {"bound": "hbm", "achieved": round(dom["achieved_gbs"], 2),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom["achieved_gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": round(DOMINANT_TRAFFIC_BYTES),
-                     "kernel": dom["kernel"], "kernel_us": round(dom["us"], 3),
-                     "alg_bytes_per_launch": dom["alg_bytes"]},
-        "cpu_baseline": cpu,
-        "other_configs": extra,
+        "roofline": dec["roofline"],
+        "roofline_second": second[0] if second else None,
+        "cpu_baseline": cpu.get("2"),
+        "configs": configs,
+        "other": extra,
     }
     print(json.dumps(line), flush=True)
 

@@ -54,6 +54,22 @@ enum {
 /* Message of the last failing call on this host thread. */
 const char *si_last_error(void);
 
+/* Per-dispatch kernel timing, for benchmarks and profiles.  Between start
+ * and stop, each kernel launch of this library whose kernel name contains
+ * one of the '|'-separated alternatives of `filter` (e.g. "k_dec_attn<" or
+ * "k_dec_|k_matvec<") gets HIP events attached to the dispatch itself
+ * (hipExtLaunchKernelGGL), for up to `capacity` launches; launches under
+ * stream capture are not timed.  stop waits for the recorded launches and
+ * writes their durations in milliseconds, in launch order, to ms[0 ..
+ * *count - 1]; timing_name(i) is then the i-th timed launch's kernel (its
+ * demangled name without namespace and parameters, e.g.
+ * "k_dec_attn<64, 8, false, false, 1>"), valid until the next start.  Process-wide; not for concurrent use.  The
+ * reference times whole phases on the host instead (phase_t,
+ * qwen_one_layer.c:245-276). */
+int si_kernel_timing_start(const char *filter, int capacity);
+int si_kernel_timing_stop(float *ms, int capacity, int *count);
+const char *si_kernel_timing_name(int i);
+
 /* defines.h:16-25 (HIDDEN, QHEADS, KVHEADS, HDIM, ROPE_BASE, RMS_EPS) as
  * runtime values; ffn is the build-defined SwiGLU width (0 = none). */
 typedef struct si_shape {
@@ -140,9 +156,10 @@ size_t si_gemm_workspace(int m, int n, int k);
  * gu = [gate | up] = matvec_q4q8 of each row (qwen_one_layer.c:148-162)
  * against the 2f x k matrix [gate rows; up rows], act = silu(gate)*up,
  * quantize_q8(act) (:98-116) into planar qs/d/bsum ([m][f], [m][f/32]).
- * gu ([m][2f] fp32) is written too and serves as the intermediate when the
- * plan splits K (workspace from si_gemm_workspace(m, 2f, k)); act and bsum
- * may be NULL.  flags: SI_GEMM_EXACT as for si_gemm_q4q8. */
+ * gu ([m][2f] fp32) is written when given; it is required only where it is
+ * the intermediate: SI_GEMM_EXACT, or a plan that splits K (si_gemm_workspace
+ * (m, 2f, k) > 0) given less workspace than that.  act and bsum may be NULL.
+ * flags: SI_GEMM_EXACT as for si_gemm_q4q8. */
 int si_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, int k,
                       const int8_t *xqs, const uint16_t *xd, int m, float *gu, float *act,
                       int8_t *qs, uint16_t *d, int16_t *bsum, int flags, void *workspace,
@@ -324,10 +341,15 @@ enum {
     SI_LAYER_EXACT = 2,     /* reference rounding in every projection (bit-exact Q/K/V,
                                O, gate/up, down given identical inputs): mat-vecs
                                without K splits, GEMMs with the exact epilogue */
-    SI_LAYER_ATTN_STANDARD = 4 /* si_layer_decode only: the reference's staged order
+    SI_LAYER_ATTN_STANDARD = 4, /* si_layer_decode only: the reference's staged order
                                with ATTENTION_STANDARD (qwen_one_layer.c:260-275):
                                RoPE + K/V append, si_attention_standard into the
                                layer's [qheads][max_pos] score buffer, Q8, W_O */
+    SI_LAYER_CAPTURE = 8    /* also store the intermediates no later stage reads
+                               (si_layer_buffer: NORMED, NORMED2, GU, ACT, the
+                               decode's XQ, XQ2, Q, ATTN, ATTQ, ATTN_OUT); without it
+                               those buffers are not written, as the reference's
+                               NULL captures (qwen_one_layer.c:278-279) */
 };
 
 /* run_layer (qwen_one_layer.c:237-281) for one token at position context-1:

@@ -10,6 +10,9 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <cxxabi.h>
+
+#include <map>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -78,9 +81,112 @@ static int check_shape(const si_shape_t *s) {
     return SI_OK;
 }
 
+// Per-dispatch kernel timing: filter alternatives and a pool of event
+// pairs, handed out in launch order while timing is on (launches under
+// stream capture and past the pool's capacity are not timed), with the name
+// of each timed launch's kernel (demangled, without the "si::" namespace or
+// the parameter list, e.g. "k_dec_attn<64, 8, false, false, 1>").
+namespace si {
+bool g_kernel_timing_on = false;
+}
+static std::mutex g_kt_mu;
+static std::vector<std::string> g_kt_filter;
+static std::vector<hipEvent_t> g_kt_events;  // 2 per launch
+static std::vector<const char *> g_kt_names;
+static std::map<const void *, std::string> g_kt_name_of;  // kernel -> name
+static int g_kt_used = 0;
+
+static const char *kernel_name(const void *kernel, hipStream_t st) {
+    auto it = g_kt_name_of.find(kernel);
+    if (it != g_kt_name_of.end()) return it->second.c_str();
+    const char *raw = hipKernelNameRefByPtr(kernel, st);
+    std::string name = raw ? raw : "?";
+    if (name.compare(0, 2, "_Z") == 0) {
+        int status = 0;
+        char *dm = abi::__cxa_demangle(name.c_str(), nullptr, nullptr, &status);
+        if (dm && status == 0) name = dm;
+        free(dm);
+    }
+    // "void si::k_x<...>(args)" -> "k_x<...>"
+    size_t b = name.find("si::");
+    if (b != std::string::npos) name = name.substr(b + 4);
+    int depth = 0;
+    for (size_t i = 0; i < name.size(); ++i) {
+        if (name[i] == '<') ++depth;
+        if (name[i] == '>') --depth;
+        if (name[i] == '(' && depth == 0) {
+            name.resize(i);
+            break;
+        }
+    }
+    return g_kt_name_of.emplace(kernel, name).first->second.c_str();
+}
+
+bool si::kernel_timing_events(const void *kernel, hipStream_t st, hipEvent_t *start,
+                              hipEvent_t *stop) {
+    std::lock_guard<std::mutex> lock(g_kt_mu);
+    if (!g_kernel_timing_on || 2 * (g_kt_used + 1) > (int)g_kt_events.size()) return false;
+    const char *kernel_text = kernel_name(kernel, st);
+    bool match = false;
+    for (const std::string &f : g_kt_filter) match = match || strstr(kernel_text, f.c_str());
+    if (!match) return false;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+        return false;
+    *start = g_kt_events[2 * g_kt_used];
+    *stop = g_kt_events[2 * g_kt_used + 1];
+    g_kt_names[g_kt_used] = kernel_text;
+    ++g_kt_used;
+    return true;
+}
+
 extern "C" {
 
 const char *si_last_error(void) { return g_err.c_str(); }
+
+int si_kernel_timing_start(const char *filter, int capacity) {
+    SI_REQUIRE(filter && capacity > 0 && capacity <= (1 << 16),
+               "kernel_timing_start: filter and 1..65536 launches required");
+    std::lock_guard<std::mutex> lock(g_kt_mu);
+    SI_REQUIRE(!g_kernel_timing_on, "kernel timing is already on");
+    for (hipEvent_t e : g_kt_events) (void)hipEventDestroy(e);
+    g_kt_events.clear();
+    for (int i = 0; i < 2 * capacity; ++i) {
+        hipEvent_t e;
+        HIP_TRY(hipEventCreate(&e));
+        g_kt_events.push_back(e);
+    }
+    g_kt_names.assign(capacity, nullptr);
+    g_kt_filter.clear();
+    for (const char *p = filter;; ++p) {  // '|'-separated alternatives
+        const char *e = strchr(p, '|');
+        g_kt_filter.emplace_back(p, e ? (size_t)(e - p) : strlen(p));
+        if (!e) break;
+        p = e;
+    }
+    g_kt_used = 0;
+    g_kernel_timing_on = true;
+    return SI_OK;
+}
+
+int si_kernel_timing_stop(float *ms, int capacity, int *count) {
+    std::lock_guard<std::mutex> lock(g_kt_mu);
+    SI_REQUIRE(g_kernel_timing_on, "kernel timing is not on");
+    g_kernel_timing_on = false;
+    const int n = g_kt_used < capacity ? g_kt_used : capacity;
+    if (count) *count = n;
+    for (int i = 0; i < n; ++i) {
+        HIP_TRY(hipEventSynchronize(g_kt_events[2 * i + 1]));
+        HIP_TRY(hipEventElapsedTime(&ms[i], g_kt_events[2 * i], g_kt_events[2 * i + 1]));
+    }
+    return SI_OK;
+}
+
+const char *si_kernel_timing_name(int i) {
+    std::lock_guard<std::mutex> lock(g_kt_mu);
+    if (g_kernel_timing_on || i < 0 || i >= g_kt_used) return nullptr;
+    return g_kt_names[i];
+}
 
 static bool tile_ok(int tile) { return tile == 8 || tile == 16 || tile == 32 || tile == 64; }
 
@@ -219,7 +325,14 @@ int si_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, i
     SI_REQUIRE((size_t)m * k < ((size_t)1 << 31) && (size_t)f * k < ((size_t)1 << 31) &&
                    q4_scale_count(2 * f, k / 32, tile) * 2 < ((size_t)1 << 31),
                "gemm_gateup: operands beyond 2 GiB (m=%d f=%d k=%d)", m, f, k);
-    SI_REQUIRE(m == 0 || (wqs && wd && xqs && xd && gu && qs && d), "gemm_gateup: NULL pointer");
+    SI_REQUIRE(m == 0 || (wqs && wd && xqs && xd && qs && d), "gemm_gateup: NULL pointer");
+    {
+        const size_t need = gemm_workspace_bytes(m, 2 * f, k);
+        const bool gu_needed = (flags & SI_GEMM_EXACT) || (need > 0 && (!workspace || ws_bytes < need));
+        SI_REQUIRE(m == 0 || gu || !gu_needed,
+                   "gemm_gateup: gu is the intermediate here (exact mode, or a K split "
+                   "without its workspace)");
+    }
     SI_REQUIRE(((uintptr_t)wqs & 15) == 0 && ((uintptr_t)xqs & 15) == 0,
                "gemm_gateup: wqs and xqs must be 16-byte aligned");
     SI_REQUIRE((flags & ~SI_GEMM_EXACT) == 0, "gemm_gateup: unknown flags %d", flags);
@@ -879,7 +992,13 @@ static void project(si_layer *L, const Q4Dev &w, int rows, const Q8Buf &x, const
                          (flags & SI_LAYER_EXACT) != 0, L->gemm_ws, L->gemm_ws_bytes, st);
 }
 
-static int run_decode_ffn(si_layer *L, float *out, bool exact, hipStream_t st);
+static int run_decode_ffn(si_layer *L, float *out, bool exact, bool cap, hipStream_t st);
+
+// A capture buffer when SI_LAYER_CAPTURE is set, else NULL (not written).
+template <typename T>
+static inline T *capt(bool cap, T *p) {
+    return cap ? p : nullptr;
+}
 
 // Single-token decode: five fused kernels (si_decode.hip).
 static int run_decode(si_layer *L, const float *x, uint16_t *kc, uint16_t *vc, int ctx,
@@ -888,13 +1007,14 @@ static int run_decode(si_layer *L, const float *x, uint16_t *kc, uint16_t *vc, i
     const int H = s.hidden, QD = s.qheads * s.hdim, NQKV = QD + 2 * s.kvheads * s.hdim;
     const bool full = !(flags & SI_LAYER_ATTN_ONLY);
     const bool exact = (flags & SI_LAYER_EXACT) != 0;
+    const bool cap = (flags & SI_LAYER_CAPTURE) != 0;
     SI_REQUIRE(!full || L->ffn, "layer has no FFN weights: use SI_LAYER_ATTN_ONLY");
     for (bool &h : L->phase_hit) h = false;
     // qwen_one_layer.c:247-258: RMSNorm -> Q8 -> Q, K, V (+bias)
     mark(L, SI_PHASE_QKV, st);
     launch_dec_qkv(x, L->norm, H, s.rms_eps, L->wqkv.qs, L->wqkv.d, L->wqkv.tile, NQKV, L->bqkv,
-                   L->normed,
-                   L->xq.qs, L->xq.d, L->xq.s, L->qkv, exact, st);
+                   capt(cap, L->normed), capt(cap, L->xq.qs), capt(cap, L->xq.d),
+                   capt(cap, L->xq.s), L->qkv, exact, st);
     if (flags & SI_LAYER_ATTN_STANDARD) {
         // the reference's staged order with attention_standard
         // (qwen_one_layer.c:260-275, attention_kernels.h:33-78)
@@ -908,19 +1028,19 @@ static int run_decode(si_layer *L, const float *x, uint16_t *kc, uint16_t *vc, i
         mark(L, SI_PHASE_OUT_PROJ, st);
         launch_matvec(L->attq.qs, L->attq.d, L->attq.s, QD, L->wo.qs, L->wo.d, L->wo.tile, H,
                       nullptr, full ? x : nullptr, full ? L->h : out, exact, st,
-                      full ? L->attn_out : nullptr);
+                      full ? capt(cap, L->attn_out) : nullptr);
         if (!full) {
             mark(L, SI_PHASE_COUNT, st);
             return check_launch("layer decode (standard attention sublayer)");
         }
-        return run_decode_ffn(L, out, exact, st);
+        return run_decode_ffn(L, out, exact, cap, st);
     }
     // :260-270: RoPE, fp16 K/V append at context-1, attention over the cache
     mark(L, SI_PHASE_ATTENTION_Q8, st);
     const int ns = dec_attn_chunks(s.qheads, s.kvheads, s.hdim, 1, ctx);
     launch_dec_attn(L->qkv, NQKV, 1, s.qheads, s.kvheads, s.hdim, L->rope_cos, L->rope_sin, kc,
-                    vc, 0, nullptr, ctx, ctx, L->q, ns, L->attn_ws, nullptr, nullptr, nullptr,
-                    nullptr, st);
+                    vc, 0, nullptr, ctx, ctx, capt(cap, L->q), ns, L->attn_ws, nullptr, nullptr,
+                    nullptr, nullptr, st);
     // :272-275: Q8 of the attention output, W_O (no bias); + x in the full layer
     mark(L, SI_PHASE_OUT_PROJ, st);
     const float *pm = (const float *)L->attn_ws;
@@ -933,29 +1053,30 @@ static int run_decode(si_layer *L, const float *x, uint16_t *kc, uint16_t *vc, i
                             L->attq.s, st);
         launch_matvec(L->attq.qs, L->attq.d, L->attq.s, QD, L->wo.qs, L->wo.d, L->wo.tile, H,
                       nullptr, full ? x : nullptr, full ? L->h : out, exact, st,
-                      full ? L->attn_out : nullptr);
+                      full ? capt(cap, L->attn_out) : nullptr);
     } else {
         launch_dec_wo(pm, pl, po, ns, s.qheads, s.hdim, L->wo.qs, L->wo.d, L->wo.tile, H,
-                      full ? x : nullptr, L->attn, L->attq.qs, L->attq.d, L->attq.s,
-                      full ? L->attn_out : nullptr, full ? L->h : out, exact, st);
+                      full ? x : nullptr, capt(cap, L->attn), capt(cap, L->attq.qs),
+                      capt(cap, L->attq.d), capt(cap, L->attq.s),
+                      full ? capt(cap, L->attn_out) : nullptr, full ? L->h : out, exact, st);
     }
     if (!full) {
         mark(L, SI_PHASE_COUNT, st);
         return check_launch("layer decode (attention sublayer)");
     }
-    return run_decode_ffn(L, out, exact, st);
+    return run_decode_ffn(L, out, exact, cap, st);
 }
 
 // FFN half of the decode layer: RMSNorm(h) -> Q8 -> gate|up -> SwiGLU -> Q8
 // -> down + h
-static int run_decode_ffn(si_layer *L, float *out, bool exact, hipStream_t st) {
+static int run_decode_ffn(si_layer *L, float *out, bool exact, bool cap, hipStream_t st) {
     const si_shape_t &s = L->s;
     const int H = s.hidden;
     mark(L, SI_PHASE_GATE_UP, st);
     launch_dec_gateup(L->h, L->post_norm, H, s.rms_eps, L->wgu.qs, L->wgu.d, L->wgu.tile, s.ffn,
-                      L->normed2,
-                      L->xq2.qs, L->xq2.d, L->xq2.s, L->gu, L->act, L->actq.qs, L->actq.d,
-                      L->actq.s, exact, st);
+                      capt(cap, L->normed2), capt(cap, L->xq2.qs), capt(cap, L->xq2.d),
+                      capt(cap, L->xq2.s), capt(cap, L->gu), capt(cap, L->act), L->actq.qs,
+                      L->actq.d, L->actq.s, exact, st);
     mark(L, SI_PHASE_DOWN, st);
     launch_matvec(L->actq.qs, L->actq.d, L->actq.s, s.ffn, L->wdown.qs, L->wdown.d,
                   L->wdown.tile, H, nullptr,
@@ -976,12 +1097,13 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
     const si_shape_t &s = L->s;
     const int H = s.hidden, QD = s.qheads * s.hdim, NQKV = QD + 2 * s.kvheads * s.hdim;
     const bool full = !(flags & SI_LAYER_ATTN_ONLY);
+    const bool cap = (flags & SI_LAYER_CAPTURE) != 0;
     SI_REQUIRE(!full || L->ffn, "layer has no FFN weights: use SI_LAYER_ATTN_ONLY");
     for (bool &h : L->phase_hit) h = false;
     // qwen_one_layer.c:247-250: RMSNorm -> Q8
     mark(L, SI_PHASE_RMS_Q8, st);
-    launch_rmsnorm_q8(x, nullptr, L->norm, rows, H, s.rms_eps, nullptr, L->normed, L->xq.qs,
-                      L->xq.d, L->xq.s, st);
+    launch_rmsnorm_q8(x, nullptr, L->norm, rows, H, s.rms_eps, nullptr, capt(cap, L->normed),
+                      L->xq.qs, L->xq.d, L->xq.s, st);
     // :253-258: Q, K, V projections (+bias), fused into one N = qd + 2 kvd matrix
     mark(L, SI_PHASE_QKV, st);
     project(L, L->wqkv, rows, L->xq, L->bqkv, nullptr, L->qkv, flags, st);
@@ -992,12 +1114,14 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
         const int ns = dec_attn_chunks(s.qheads, s.kvheads, s.hdim, rows, max_ctx);
         if (ns == 1) {
             launch_dec_attn(L->qkv, NQKV, rows, s.qheads, s.kvheads, s.hdim, L->rope_cos,
-                            L->rope_sin, kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx, L->q, 1,
-                            L->attn_ws, L->attn, L->attq.qs, L->attq.d, L->attq.s, st, pg);
+                            L->rope_sin, kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx,
+                            capt(cap, L->q), 1, L->attn_ws, L->attn, L->attq.qs, L->attq.d,
+                            L->attq.s, st, pg);
         } else {
             launch_dec_attn(L->qkv, NQKV, rows, s.qheads, s.kvheads, s.hdim, L->rope_cos,
-                            L->rope_sin, kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx, L->q, ns,
-                            L->attn_ws, nullptr, nullptr, nullptr, nullptr, st, pg);
+                            L->rope_sin, kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx,
+                            capt(cap, L->q), ns, L->attn_ws, nullptr, nullptr, nullptr, nullptr,
+                            st, pg);
             launch_attn_combine(rows, s.qheads, s.hdim, ns, L->attn_ws, L->attn, L->attq.qs,
                                 L->attq.d, L->attq.s, st);
         }
@@ -1034,22 +1158,25 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
     // build-defined FFN half: h = x + o; RMSNorm -> Q8; gate|up; SwiGLU -> Q8; down + h
     if (osplits > 1)
         launch_rmsnorm_q8_parts(x, (const float *)L->gemm_ws, osplits, L->post_norm, rows, H,
-                                s.rms_eps, L->attn_out, L->h, L->normed2, L->xq2.qs, L->xq2.d,
-                                L->xq2.s, st);
+                                s.rms_eps, L->attn_out, L->h, capt(cap, L->normed2), L->xq2.qs,
+                                L->xq2.d, L->xq2.s, st);
     else
-        launch_rmsnorm_q8(x, L->attn_out, L->post_norm, rows, H, s.rms_eps, L->h, L->normed2,
-                          L->xq2.qs, L->xq2.d, L->xq2.s, st);
+        launch_rmsnorm_q8(x, L->attn_out, L->post_norm, rows, H, s.rms_eps, L->h,
+                          capt(cap, L->normed2), L->xq2.qs, L->xq2.d, L->xq2.s, st);
     mark(L, SI_PHASE_GATE_UP, st);
     if (rows == 1) {
         project(L, L->wgu, rows, L->xq2, nullptr, nullptr, L->gu, flags, st);
         mark(L, SI_PHASE_SWIGLU_Q8, st);
-        launch_swiglu_q8(L->gu, rows, s.ffn, L->act, L->actq.qs, L->actq.d, L->actq.s, st);
+        launch_swiglu_q8(L->gu, rows, s.ffn, capt(cap, L->act), L->actq.qs, L->actq.d, L->actq.s,
+                         st);
     } else {
         // SwiGLU -> Q8 in the gate|up GEMM's epilogue (the swiglu_q8 phase
-        // is then empty)
+        // is then empty); gu is written only as a capture or where it is the
+        // intermediate (exact mode)
+        const bool ex = (flags & SI_LAYER_EXACT) != 0;
         launch_gemm_gateup_q8(L->wgu.qs, L->wgu.d, L->wgu.tile, s.ffn, H, L->xq2.qs, L->xq2.d,
-                              rows, L->gu, L->act, L->actq.qs, L->actq.d, L->actq.s,
-                              (flags & SI_LAYER_EXACT) != 0, L->gemm_ws, L->gemm_ws_bytes, st);
+                              rows, capt(cap || ex, L->gu), capt(cap, L->act), L->actq.qs,
+                              L->actq.d, L->actq.s, ex, L->gemm_ws, L->gemm_ws_bytes, st);
         mark(L, SI_PHASE_SWIGLU_Q8, st);
     }
     mark(L, SI_PHASE_DOWN, st);
@@ -1063,7 +1190,8 @@ extern "C" {
 int si_layer_decode(si_layer_t *L, const float *x, uint16_t *kc, uint16_t *vc, int context,
                     float *out, int flags, void *stream) {
     SI_REQUIRE(L && x && kc && vc && out, "layer_decode: NULL pointer");
-    SI_REQUIRE((flags & ~(SI_LAYER_ATTN_ONLY | SI_LAYER_EXACT | SI_LAYER_ATTN_STANDARD)) == 0,
+    SI_REQUIRE((flags & ~(SI_LAYER_ATTN_ONLY | SI_LAYER_EXACT | SI_LAYER_ATTN_STANDARD |
+                          SI_LAYER_CAPTURE)) == 0,
                "layer_decode: unknown flags %d", flags);
     SI_REQUIRE(!(flags & SI_LAYER_ATTN_STANDARD) ||
                    ((uintptr_t)kc % 16 == 0 && (uintptr_t)vc % 16 == 0),
@@ -1078,7 +1206,7 @@ int si_layer_decode_batch(si_layer_t *L, const float *x, int nseq, uint16_t *kc,
                           size_t kv_seq_stride, const int *ctx_dev, int context, int max_ctx,
                           float *out, int flags, void *stream) {
     SI_REQUIRE(L && x && kc && vc && out, "layer_decode_batch: NULL pointer");
-    SI_REQUIRE((flags & ~(SI_LAYER_ATTN_ONLY | SI_LAYER_EXACT)) == 0,
+    SI_REQUIRE((flags & ~(SI_LAYER_ATTN_ONLY | SI_LAYER_EXACT | SI_LAYER_CAPTURE)) == 0,
                "layer_decode_batch: unsupported flags %d (standard attention is "
                "single-token decode only)", flags);
     SI_REQUIRE(nseq >= 1 && nseq <= L->max_tokens, "nseq %d outside 1..%d", nseq, L->max_tokens);
@@ -1098,7 +1226,7 @@ int si_layer_decode_paged(si_layer_t *L, const float *x, int nseq, uint16_t *k_p
                           int max_pages, const int *ctx_dev, int context, int max_ctx, float *out,
                           int flags, void *stream) {
     SI_REQUIRE(L && x && k_pool && v_pool && pages && out, "layer_decode_paged: NULL pointer");
-    SI_REQUIRE((flags & ~(SI_LAYER_ATTN_ONLY | SI_LAYER_EXACT)) == 0,
+    SI_REQUIRE((flags & ~(SI_LAYER_ATTN_ONLY | SI_LAYER_EXACT | SI_LAYER_CAPTURE)) == 0,
                "layer_decode_paged: unsupported flags %d (standard attention is "
                "single-token decode only)", flags);
     SI_REQUIRE(nseq >= 1 && nseq <= L->max_tokens, "nseq %d outside 1..%d", nseq, L->max_tokens);
@@ -1151,7 +1279,7 @@ int si_attention_paged(const si_shape_t *s, const float *q, int nq, const uint16
 int si_layer_prefill(si_layer_t *L, const float *x, int ntok, int prefix, uint16_t *kc,
                      uint16_t *vc, float *out, int flags, void *stream) {
     SI_REQUIRE(L && x && kc && vc && out, "layer_prefill: NULL pointer");
-    SI_REQUIRE((flags & ~(SI_LAYER_ATTN_ONLY | SI_LAYER_EXACT)) == 0,
+    SI_REQUIRE((flags & ~(SI_LAYER_ATTN_ONLY | SI_LAYER_EXACT | SI_LAYER_CAPTURE)) == 0,
                "layer_prefill: unsupported flags %d (standard attention is "
                "single-token decode only)", flags);
     // prefill_weight_stationary.h:187: 1 <= ntok, 0 <= prefix, prefix+ntok within range

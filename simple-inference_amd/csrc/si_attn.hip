@@ -58,7 +58,7 @@ void launch_rope_kv(const float *qkv, int ldqkv, int ntok, int qheads, int kvhea
                     const float *rs, float *q_out, uint16_t *kc, uint16_t *vc,
                     size_t kv_seq_stride, hipStream_t st, KvPages pg) {
     if (ntok <= 0) return;
-    hipLaunchKernelGGL(k_rope_kv, dim3(ntok, qheads + kvheads), dim3(hdim / 2), 0, st, qkv,
+    SI_LAUNCH(k_rope_kv, dim3(ntok, qheads + kvheads), dim3(hdim / 2), 0, st, qkv,
                        ldqkv, qheads, kvheads, hdim, pos0, pos_step, max_pos, ctx_dev, rc, rs,
                        q_out, kc, vc, kv_seq_stride, pg);
 }
@@ -173,10 +173,10 @@ static void combine(int qheads, int hdim, int nq, int nsplit, const float *ws_m,
                     const float *ws_l, const float *ws_o, float *attn, int8_t *qs, uint16_t *d,
                     int16_t *bsum, hipStream_t st) {
     if (nsplit >= 32)
-        hipLaunchKernelGGL(k_attn_combine_wide, dim3(qheads, nq), dim3(1024 / hdim * hdim), 0, st,
+        SI_LAUNCH(k_attn_combine_wide, dim3(qheads, nq), dim3(1024 / hdim * hdim), 0, st,
                            qheads, hdim, nsplit, ws_m, ws_l, ws_o, attn, qs, d, bsum);
     else
-        hipLaunchKernelGGL(k_attn_combine, dim3(qheads, nq), dim3(hdim), 0, st, qheads, hdim,
+        SI_LAUNCH(k_attn_combine, dim3(qheads, nq), dim3(hdim), 0, st, qheads, hdim,
                            nsplit, ws_m, ws_l, ws_o, attn, qs, d, bsum);
 }
 
@@ -702,7 +702,7 @@ void launch_attn_prefill(const float *q, int ntok, int qheads, int kvheads, int 
     const dim3 grid(2 * sp.nsplit + sp.qsplit, kvheads);
     const float scale = 1.0f / sqrtf((float)hdim);  // attention_kernels.h:86
 #define PF_CALL(DIM, NW)                                                                      \
-    hipLaunchKernelGGL((k_attn_prefill<DIM, NW>), grid, dim3(NW * 64),                        \
+    SI_LAUNCH((k_attn_prefill<DIM, NW>), grid, dim3(NW * 64),                        \
                        (PrefillLds<DIM, NW>::bytes()), st, q, ntok, qheads, kvheads, pos0, kc, \
                        vc, scale, attn, qs, qd, bsum, sp)
 #define PF_DIM(DIM)                     \
@@ -720,7 +720,7 @@ void launch_attn_prefill(const float *q, int ntok, int qheads, int kvheads, int 
 #undef PF_CALL
     if (sp.nsplit > 0) {
         const size_t t0 = (size_t)sp.qsplit * PF_T, qd_ = (size_t)qheads * hdim;
-        hipLaunchKernelGGL(k_attn_combine, dim3(qheads, rows_split), dim3(hdim), 0, st, qheads,
+        SI_LAUNCH(k_attn_combine, dim3(qheads, rows_split), dim3(hdim), 0, st, qheads,
                            hdim, 2, sp.ws_m, sp.ws_l, sp.ws_o, attn + t0 * qd_,
                            qs ? qs + t0 * qd_ : nullptr, qs ? qd + t0 * qd_ / SI_QK : nullptr,
                            bsum ? bsum + t0 * qd_ / SI_QK : nullptr);
@@ -767,7 +767,7 @@ void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
     const float scale = 1.0f / sqrtf((float)hdim);  // attention_kernels.h:86
     const dim3 grid(ns, kvheads, nq);
 #define SI_ATTN_LAUNCH(DIM)                                                                  \
-    hipLaunchKernelGGL(k_attn_decode_mfma<DIM>, grid, dim3(256), 0, st, q, qheads, kvheads, kc, \
+    SI_LAUNCH(k_attn_decode_mfma<DIM>, grid, dim3(256), 0, st, q, qheads, kvheads, kc, \
                        vc, kv_seq_stride, ctx_dev, ctx0, ctx_step, max_ctx, chunk, scale, ws_m, \
                        ws_l, ws_o, pg, kv_row)
     switch (hdim) {
@@ -923,16 +923,16 @@ void launch_attn_standard(const float *q, int qheads, int kvheads, int hdim, con
     if (ctx > 0) {
         const dim3 grid((ctx + 63) / 64, kvheads);
         switch (hdim) {  // the head dimensions check_shape admits
-        case 32: hipLaunchKernelGGL(k_std_scores<32>, grid, dim3(256), 0, st, q, kc, qheads, kvheads, ctx, inv, scores); break;
-        case 64: hipLaunchKernelGGL(k_std_scores<64>, grid, dim3(256), 0, st, q, kc, qheads, kvheads, ctx, inv, scores); break;
-        case 96: hipLaunchKernelGGL(k_std_scores<96>, grid, dim3(256), 0, st, q, kc, qheads, kvheads, ctx, inv, scores); break;
-        default: hipLaunchKernelGGL(k_std_scores<128>, grid, dim3(256), 0, st, q, kc, qheads, kvheads, ctx, inv, scores); break;
+        case 32: SI_LAUNCH(k_std_scores<32>, grid, dim3(256), 0, st, q, kc, qheads, kvheads, ctx, inv, scores); break;
+        case 64: SI_LAUNCH(k_std_scores<64>, grid, dim3(256), 0, st, q, kc, qheads, kvheads, ctx, inv, scores); break;
+        case 96: SI_LAUNCH(k_std_scores<96>, grid, dim3(256), 0, st, q, kc, qheads, kvheads, ctx, inv, scores); break;
+        default: SI_LAUNCH(k_std_scores<128>, grid, dim3(256), 0, st, q, kc, qheads, kvheads, ctx, inv, scores); break;
         }
-        hipLaunchKernelGGL(k_std_softmax, dim3(qheads), dim3(1024), 0, st, scores, ctx);
+        SI_LAUNCH(k_std_softmax, dim3(qheads), dim3(1024), 0, st, scores, ctx);
     }
     // context 0 leaves the output zero (attention_kernels.h:70)
     const int npair = qheads * (hdim / 8);
-    hipLaunchKernelGGL(k_std_pv, dim3(8 * ((npair + 7) / 8)), dim3(1024), 0, st, scores, vc,
+    SI_LAUNCH(k_std_pv, dim3(8 * ((npair + 7) / 8)), dim3(1024), 0, st, scores, vc,
                        qheads, kvheads, hdim, ctx, out);
 }
 

@@ -1172,7 +1172,7 @@ void launch_dec_qkv(const float *x, const float *gain, int hidden, float eps, co
                     int8_t *cap_qs, uint16_t *cap_d, int16_t *cap_s, float *qkv, bool exact,
                     hipStream_t st) {
 #define CALL(R, T, E)                                                                            \
-    hipLaunchKernelGGL((k_dec_qkv<R, T, E>), dim3((n + R - 1) / R), dim3(T),                      \
+    SI_LAUNCH((k_dec_qkv<R, T, E>), dim3((n + R - 1) / R), dim3(T),                      \
                        (DecLds<R, T>::bytes(hidden, false, 0)), st, x, gain, hidden, eps, wqs,    \
                        wd, tile, n, bias, cap_normed, cap_qs, cap_d, cap_s, qkv)
     if (exact) {
@@ -1190,7 +1190,7 @@ void launch_dec_wo(const float *pm, const float *pl, const float *po, int ns, in
                    int16_t *cap_s, float *cap_y, float *out, bool exact, hipStream_t st) {
     const int qd = qheads * hdim;
 #define CALL(R, T, E)                                                                            \
-    hipLaunchKernelGGL((k_dec_wo<R, T, E>), dim3((n + R - 1) / R), dim3(T),                       \
+    SI_LAUNCH((k_dec_wo<R, T, E>), dim3((n + R - 1) / R), dim3(T),                       \
                        (DecLds<R, T>::bytes(qd, false, 0)), st, pm, pl, po, ns,                    \
                        qheads, hdim, wqs, wd, tile, n, residual, cap_attn, cap_qs, cap_d, cap_s,  \
                        cap_y, out)
@@ -1212,7 +1212,7 @@ void launch_dec_gateup(const float *h, const float *gain, int hidden, float eps,
                        hipStream_t st) {
     const int n = 2 * f;
 #define CALL(R, T, E)                                                                            \
-    hipLaunchKernelGGL((k_dec_gateup<R, T, E>), dim3((n + R - 1) / R), dim3(T),                   \
+    SI_LAUNCH((k_dec_gateup<R, T, E>), dim3((n + R - 1) / R), dim3(T),                   \
                        (DecLds<R, T>::bytes(hidden, false, 0)), st, h, gain, hidden, eps, wqs,    \
                        wd, tile, f, cap_normed, cap_qs, cap_d, cap_s, gu, act, aqs, ad, as)
     if (exact) {
@@ -1301,7 +1301,7 @@ static void dec_attn_impl(const float *qkv, int ldqkv, int nq, int qheads, int k
     const bool fin = attn != nullptr;
     if (dec_rows_ok(qheads, kvheads, hdim, nq)) {
 #define RCALL(DIM, GG, FIN)                                                                       \
-    hipLaunchKernelGGL((k_dec_attn_rows<DIM, GG, FIN, PAGED>), dim3(ns, nq), dim3(256),                \
+    SI_LAUNCH((k_dec_attn_rows<DIM, GG, FIN, PAGED>), dim3(ns, nq), dim3(256),                \
                        (RowsLds<DIM, GG>::bytes(per)), st, qkv, ldqkv, qheads, rc, rs, kc, vc,   \
                        kv_seq_stride, ctx_dev, ctx0, max_ctx, chunk, scale, q_cap, ws_m, ws_l,    \
                        ws_o, attn, aqs, ad, as, pg)
@@ -1325,7 +1325,7 @@ static void dec_attn_impl(const float *qkv, int ldqkv, int nq, int qheads, int k
     }
     const dim3 grid(ns, kvheads, nq);
 #define CALL(DIM, NW, FIN, DEP)                                                                \
-    hipLaunchKernelGGL((k_dec_attn<DIM, NW, FIN, PAGED, DEP>), grid, dim3(NW * 64),            \
+    SI_LAUNCH((k_dec_attn<DIM, NW, FIN, PAGED, DEP>), grid, dim3(NW * 64),            \
                        (AttnLds<DIM, NW>::bytes(per)), st, qkv, ldqkv, qheads, kvheads, rc, rs,  \
                        kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx, chunk, scale, q_cap,     \
                        ws_m, ws_l, ws_o, attn, aqs, ad, as, pg)

@@ -50,15 +50,17 @@ __global__ void __launch_bounds__(T) k_matvec(
     }
     GemvRows<R, T, EXACT, RowIdentity> g(wqs, wd, tile, n, n, nb, tile0, RowIdentity{});
     g.start();
+    // Stored at the same clamped index, unconditionally (threads past the
+    // row rewrite its last piece with the value it already holds): a store
+    // under a branch lets the compiler sink the load into the branch, behind
+    // the weight loads, and wait for all of them.
 #pragma unroll
-    for (int u = 0; u < XQ; ++u)
-        if (t + u * T < k / 16) ((int4 *)lq)[t + u * T] = xr[u];
+    for (int u = 0; u < XQ; ++u) ((int4 *)lq)[min(t + u * T, k / 16 - 1)] = xr[u];
 #pragma unroll
-    for (int u = 0; u < XD; ++u)
-        if (t + u * T < nb) {
-            ld[t + u * T] = dr[u];
-            ls[t + u * T] = sr[u];
-        }
+    for (int u = 0; u < XD; ++u) {
+        ld[min(t + u * T, nb - 1)] = dr[u];
+        ls[min(t + u * T, nb - 1)] = sr[u];
+    }
     for (int i = t + XQ * T; i < k / 16; i += T) ((int4 *)lq)[i] = ((const int4 *)xqs)[i];
     for (int i = t + XD * T; i < nb; i += T) {
         ld[i] = xd[i];
@@ -80,7 +82,7 @@ void launch_matvec(const int8_t *xqs, const uint16_t *xd, const int16_t *xs, int
                    const float *residual, float *out, bool exact, hipStream_t st, float *pre) {
     if (n <= 0) return;
 #define CALL(R, T, E)                                                                        \
-    hipLaunchKernelGGL((k_matvec<R, T, E>), dim3((n + R - 1) / R), dim3(T),                  \
+    SI_LAUNCH((k_matvec<R, T, E>), dim3((n + R - 1) / R), dim3(T),                  \
                        (matvec_lds_bytes<R, T>(k)), st, xqs, xd, xs, k, wqs, wd, tile, n, bias,  \
                        residual, out, pre)
     if (exact) {
@@ -108,7 +110,7 @@ __global__ void __launch_bounds__(64) k_block_dots(const uint8_t *__restrict__ w
 void launch_block_dots(const uint8_t *wqs, int n, int k, const int8_t *xqs, const int16_t *xs,
                        int32_t *dots, hipStream_t st) {
     const int nb = k / SI_QK;
-    hipLaunchKernelGGL(k_block_dots, dim3((n + 63) / 64, nb), dim3(64), 0, st, wqs, n, nb, xqs,
+    SI_LAUNCH(k_block_dots, dim3((n + 63) / 64, nb), dim3(64), 0, st, wqs, n, nb, xqs,
                        xs, dots);
 }
 

@@ -1,8 +1,30 @@
 // si_kernels.hpp -- launcher prototypes shared by the HIP translation units.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
+namespace si {
+// Per-dispatch kernel timing (si_kernel_timing_start / _stop): when it is on
+// and the kernel's name contains the filter, hands out a pair of events for
+// hipExtLaunchKernelGGL to attach to the dispatch itself.
+bool kernel_timing_events(const void *kernel, hipStream_t st, hipEvent_t *start,
+                          hipEvent_t *stop);
+extern bool g_kernel_timing_on;
+}  // namespace si
+
+// Every kernel launch of the library goes through SI_LAUNCH (same arguments
+// as hipLaunchKernelGGL; K parenthesised when it holds commas).
+#define SI_LAUNCH(K, G, B, S, ST, ...)                                                 \
+    do {                                                                             \
+        hipEvent_t si_ev0_, si_ev1_;                                                 \
+        if (::si::g_kernel_timing_on &&                                              \
+            ::si::kernel_timing_events((const void *)(K), ST, &si_ev0_, &si_ev1_))   \
+            hipExtLaunchKernelGGL(K, G, B, S, ST, si_ev0_, si_ev1_, 0, __VA_ARGS__);  \
+        else                                                                         \
+            hipLaunchKernelGGL(K, G, B, S, ST, __VA_ARGS__);                         \
+    } while (0)
+
 namespace si {
 void launch_quantize_q8_aos(const float *src, void *dst, int count, hipStream_t st);
 void launch_quantize_q8_rows(const float *src, int rows, int k, int8_t *qs, uint16_t *d,

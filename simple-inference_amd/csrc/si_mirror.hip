@@ -69,7 +69,7 @@ __global__ void __launch_bounds__(64)
 void launch_matvec_rowmajor(const uint8_t *w, const void *x, int inputs, int outputs,
                             const float *bias, float *out, hipStream_t st) {
     if (outputs <= 0) return;
-    hipLaunchKernelGGL(k_matvec_rowmajor, dim3(outputs), dim3(64), 0, st, (const uint16_t *)w,
+    SI_LAUNCH(k_matvec_rowmajor, dim3(outputs), dim3(64), 0, st, (const uint16_t *)w,
                        (const uint16_t *)x, inputs / SI_QK, bias, out);
 }
 
@@ -126,7 +126,7 @@ void launch_colsoa_matvec(const uint8_t *tiles, int ntiles, const void *x, int n
                           const float *bias_lo, const float *bias_hi, float *out, int add,
                           hipStream_t st) {
     if (ntiles <= 0) return;
-    hipLaunchKernelGGL(k_colsoa_matvec, dim3(ntiles), dim3(256), 0, st, tiles,
+    SI_LAUNCH(k_colsoa_matvec, dim3(ntiles), dim3(256), 0, st, tiles,
                        (const uint16_t *)x, nblocks, bias_lo, bias_hi, out, add);
 }
 
@@ -160,7 +160,7 @@ __global__ void __launch_bounds__(256)
 void launch_rmsnorm(const float *x, const float *gain, int rows, int n, float eps, float *out,
                     hipStream_t st) {
     if (rows <= 0) return;
-    hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(256), 0, st, x, gain, n, eps, out);
+    SI_LAUNCH(k_rmsnorm, dim3(rows), dim3(256), 0, st, x, gain, n, eps, out);
 }
 
 // ---------------------------------------------------------------------------
@@ -185,7 +185,7 @@ void launch_rope_inplace(float *heads, int nheads, int hdim, int position, const
                          const float *rs, hipStream_t st) {
     const int n = nheads * (hdim / 2);
     if (n <= 0) return;
-    hipLaunchKernelGGL(k_rope_inplace, dim3((n + 255) / 256), dim3(256), 0, st, heads, nheads,
+    SI_LAUNCH(k_rope_inplace, dim3((n + 255) / 256), dim3(256), 0, st, heads, nheads,
                        hdim, position, rc, rs);
 }
 
@@ -205,10 +205,10 @@ void launch_f16_convert(const void *src, void *dst, size_t n, bool to_half, hipS
     if (n == 0) return;
     const dim3 grid((unsigned)((n + 255) / 256));
     if (to_half)
-        hipLaunchKernelGGL(k_f32_to_f16, grid, dim3(256), 0, st, (const float *)src,
+        SI_LAUNCH(k_f32_to_f16, grid, dim3(256), 0, st, (const float *)src,
                            (uint16_t *)dst, n);
     else
-        hipLaunchKernelGGL(k_f16_to_f32, grid, dim3(256), 0, st, (const uint16_t *)src,
+        SI_LAUNCH(k_f16_to_f32, grid, dim3(256), 0, st, (const uint16_t *)src,
                            (float *)dst, n);
 }
 

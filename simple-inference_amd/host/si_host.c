@@ -206,6 +206,8 @@ static phase_t decode(const si_model_t *l, const float *x, uint16_t *kc, uint16_
                       int context, float *output, int flags, float *attn_copy,
                       block_q8_0 *q8_copy) {
     if (context < 1 || context > l->max_pos) die("Context must be 1..max_pos");
+    /* the attention row and its Q8 stay in the layer's buffers only when asked for */
+    if (attn_copy || q8_copy) flags |= SI_LAYER_CAPTURE;
     check(si_layer_decode(l->layer, x, kc, vc, context, output, flags, l->stream),
           "si_layer_decode");
     float ms[SI_PHASE_COUNT];

@@ -23,6 +23,7 @@ Q8_DTYPE = np.dtype([("d", "<u2"), ("qs", "i1", (QK,))])  # defines.h:27-28
 
 SI_OK, SI_ERR_ARG, SI_ERR_HIP, SI_ERR_STATE, SI_ERR_NOMEM = range(5)
 SI_LAYER_FULL, SI_LAYER_ATTN_ONLY, SI_LAYER_EXACT, SI_LAYER_ATTN_STANDARD = 0, 1, 2, 4
+SI_LAYER_CAPTURE = 8
 SI_GEMM_EXACT = 1
 BUFFERS = ["NORMED", "XQ_QS", "XQ_D", "XQ_S", "QKV", "Q", "ATTN", "ATTQ_QS", "ATTQ_D",
            "ATTQ_S", "ATTN_OUT", "H", "NORMED2", "XQ2_QS", "XQ2_D", "XQ2_S", "GU", "ACT",
@@ -68,6 +69,9 @@ class LayerHost(ctypes.Structure):
 
 _SIGS = {
     "si_last_error": (ctypes.c_char_p, []),
+    "si_kernel_timing_start": (_I, [ctypes.c_char_p, _I]),
+    "si_kernel_timing_stop": (_I, [_P, _I, ctypes.POINTER(_I)]),
+    "si_kernel_timing_name": (ctypes.c_char_p, [_I]),
     "si_q4_repack": (_I, [_P, _I, _I, _I, _P, _P, _P]),
     "si_q4_unpack": (_I, [_P, _P, _I, _I, _I, _P, _P]),
     "si_q4_tile": (_I, [_I, _I]),
@@ -186,6 +190,24 @@ def call(name, *args):
     return rc
 
 
+def kernel_times_ms(kernel_filter, fn, capacity=4096):
+    """Runs fn() with per-dispatch timing on (si_kernel_timing_start) and
+    returns [(kernel, ms)] for the launches whose kernel name contains one of
+    the '|'-separated alternatives of kernel_filter, in launch order (none
+    under stream capture); kernel is the demangled name without namespace
+    and parameters, e.g. "k_dec_attn<64, 8, false, false, 1>"."""
+    call("si_kernel_timing_start", kernel_filter.encode(), capacity)
+    try:
+        fn()
+    finally:
+        ms = np.zeros(capacity, np.float32)
+        n = ctypes.c_int(0)
+        call("si_kernel_timing_stop", ms.ctypes.data_as(ctypes.c_void_p), capacity,
+             ctypes.byref(n))
+    names = [lib().si_kernel_timing_name(i).decode() for i in range(n.value)]
+    return list(zip(names, ms[:n.value].tolist()))
+
+
 def ptr(t):
     """Device (torch) or host (numpy) buffer address; None stays NULL."""
     if t is None:
@@ -285,24 +307,28 @@ class Layer:
              ctypes.byref(tile), ctypes.byref(n), ctypes.byref(k))
         return qs.value, d.value, tile.value, n.value, k.value
 
-    def decode(self, x, kc, vc, context, out, flags=SI_LAYER_FULL, stream=None):
-        call("si_layer_decode", self.h, ptr(x), ptr(kc), ptr(vc), context, ptr(out), flags,
-             stream_handle(stream))
+    # The layer calls below keep the intermediates in the layer's buffers
+    # (SI_LAYER_CAPTURE) unless capture=False, for the stagewise checks.
+    def decode(self, x, kc, vc, context, out, flags=SI_LAYER_FULL, stream=None, capture=True):
+        call("si_layer_decode", self.h, ptr(x), ptr(kc), ptr(vc), context, ptr(out),
+             flags | (SI_LAYER_CAPTURE if capture else 0), stream_handle(stream))
 
     def decode_batch(self, x, nseq, kc, vc, kv_seq_stride, context, max_ctx, out,
-                     ctx_dev=None, flags=SI_LAYER_FULL, stream=None):
+                     ctx_dev=None, flags=SI_LAYER_FULL, stream=None, capture=True):
         call("si_layer_decode_batch", self.h, ptr(x), nseq, ptr(kc), ptr(vc), kv_seq_stride,
-             ptr(ctx_dev), context, max_ctx, ptr(out), flags, stream_handle(stream))
+             ptr(ctx_dev), context, max_ctx, ptr(out),
+             flags | (SI_LAYER_CAPTURE if capture else 0), stream_handle(stream))
 
     def decode_paged(self, x, nseq, k_pool, v_pool, npages, page_size, pages, max_pages,
-                     ctx_dev, max_ctx, out, flags=SI_LAYER_FULL, stream=None):
+                     ctx_dev, max_ctx, out, flags=SI_LAYER_FULL, stream=None, capture=True):
         call("si_layer_decode_paged", self.h, ptr(x), nseq, ptr(k_pool), ptr(v_pool), npages,
-             page_size, ptr(pages), max_pages, ptr(ctx_dev), max_ctx, max_ctx, ptr(out), flags,
-             stream_handle(stream))
+             page_size, ptr(pages), max_pages, ptr(ctx_dev), max_ctx, max_ctx, ptr(out),
+             flags | (SI_LAYER_CAPTURE if capture else 0), stream_handle(stream))
 
-    def prefill(self, x, ntok, prefix, kc, vc, out, flags=SI_LAYER_FULL, stream=None):
+    def prefill(self, x, ntok, prefix, kc, vc, out, flags=SI_LAYER_FULL, stream=None,
+                capture=True):
         call("si_layer_prefill", self.h, ptr(x), ntok, prefix, ptr(kc), ptr(vc), ptr(out),
-             flags, stream_handle(stream))
+             flags | (SI_LAYER_CAPTURE if capture else 0), stream_handle(stream))
 
     def set_timing(self, on=True):
         call("si_layer_set_timing", self.h, int(on))

@@ -362,3 +362,48 @@ def test_host_mirror_run_layer(oracle):
         torch.cuda.synchronize()
         close(host(o), want, 2e-3, f"attention_compute({method})")
     H.free_layer(m)
+
+
+@pytest.mark.parametrize("mode", ["decode", "decode_7b", "batch", "prefill"])
+def test_capture_flag_leaves_outputs_unchanged(oracle, mode):
+    """SI_LAYER_CAPTURE only adds the intermediate buffers: the layer output
+    and the appended K/V rows are the same bits with and without it, and a
+    call without it leaves the capture buffers untouched."""
+    torch = _torch()
+    name = "7b" if mode == "decode_7b" else "0.5b"
+    s, os_ = _shapes(name)
+    lay = make_layer(oracle, os_, 91)
+    rng = np.random.default_rng(92)
+    kvd = s.kvheads * s.hdim
+    rows, ctx = {"decode": (1, 300), "decode_7b": (1, 700), "batch": (6, 150),
+                 "prefill": (40, 40)}[mode]
+    L = si_amd.Layer(s, lay, rows, ctx)
+    x = dev(rng.standard_normal(rows * s.hidden).astype(np.float32))
+    hist = kv_history(oracle, rng, rows * ctx, kvd)
+    outs = []
+    for capture in (True, False):
+        kc = dev(hist.view(np.int16).copy())
+        vc = dev(hist.view(np.int16)[::-1].copy())
+        out = empty(rows * s.hidden, torch.float32)
+        gu = si_amd_buffer(L, "GU", rows * 2 * s.ffn)
+        gu.fill_(7.0)
+        if mode.startswith("decode"):
+            L.decode(x, kc, vc, ctx, out, capture=capture)
+        elif mode == "batch":
+            L.decode_batch(x, rows, kc, vc, ctx * kvd, ctx, ctx, out, capture=capture)
+        else:
+            L.prefill(x, rows, 0, kc, vc, out, capture=capture)
+        torch.cuda.synchronize()
+        if capture:
+            assert not torch.all(gu == 7.0), "GU capture not written"
+        else:
+            assert torch.all(gu == 7.0), "GU written without SI_LAYER_CAPTURE"
+        outs.append((host(out).view(np.uint32), host(kc), host(vc)))
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
+    L.close()
+
+
+def si_amd_buffer(L, name, count):
+    from tests.gpu_helpers import device_view
+    return device_view(L.buffer(name), count, _torch().float32)
