@@ -41,16 +41,24 @@ METRIC = "decode layer µs + HBM GB/s; prefill tokens/s + int8 MFMA % (one GPU)"
 # dispatch, medians over the run's dispatches of that kernel), scaled by what
 # the counters read for a 256 MiB copy (FETCH_SIZE x2.000, WRITE_SIZE
 # x1.000): {(config, kernel prefix): (FETCH_SIZE KiB, WRITE_SIZE KiB)}.
-# Kernels not listed report traffic null.
-PMC_KIB = {}
+# Kernels not listed report traffic null.  Summaries: profiles/cfgN_*.md.
+PMC_KIB = {
+    ("1", "k_matvec<8, 128, false>"): (328.9, 4.5),
+    ("2", "k_dec_attn<64, 8, false, false, 1>"): (330.5, 35.5),
+    ("2", "k_dec_wo<8, 512, false>"): (579.0, 3.5),
+    ("2", "k_dec_gateup<64, 512, false>"): (2530.9, 9.8),
+    ("2", "k_matvec<8, 512, false>"): (1256.0, 3.5),
+    ("2", "k_dec_qkv<8, 512, false>"): (596.5, 4.5),
+    ("3", "k_gemm_fast<2, 2, 1, 2, true>"): (6863.0, 4800.0),
+    ("4", "k_gemm_fast<2, 2, 2, 2, true>"): (628021.2, 75914.8),
+    ("5", "k_dec_attn_rows<128, 4, false, false>"): (266834.6, 8192.1),
+}
 FETCH_SCALE, WRITE_SCALE = 2.000, 1.000
 
 
 def pmc_traffic(cfg, kernel):
-    for (c, prefix), (f, w) in PMC_KIB.items():
-        if c == cfg and kernel.startswith(prefix):
-            return round((f * FETCH_SCALE + w * WRITE_SCALE) * 1024)
-    return None
+    f, w = PMC_KIB.get((cfg, kernel), (None, None))
+    return None if f is None else round((f * FETCH_SCALE + w * WRITE_SCALE) * 1024)
 
 
 def log(*a):
