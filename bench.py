@@ -766,7 +766,8 @@ def cpu_baselines(si_amd, budget_s=10.0):
                               warm=False)
         out["3"] = dict(value=512 / med, unit="tokens/s", cores=1, kind="port",
                         s_per_prefill=med,
-                        sample=f"{n} full 512-token prefills, median {med:.2f} s; {where}")
+                        sample=f"{n} full 512-token prefill{'s' if n > 1 else ''}, "
+                               f"{'median ' if n > 1 else ''}{med:.2f} s; {where}")
         del o, tens, kc, vc, kc3, vc3
         # configs 4 and 5: the 7B layer
         o, s, tens, kc, vc, rng = _oracle_inputs(si_amd, "7b", 4096, 5)
