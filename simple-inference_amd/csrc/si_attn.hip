@@ -59,8 +59,8 @@ void launch_rope_kv(const float *qkv, int ldqkv, int ntok, int qheads, int kvhea
                     size_t kv_seq_stride, hipStream_t st, KvPages pg) {
     if (ntok <= 0) return;
     SI_LAUNCH(k_rope_kv, dim3(ntok, qheads + kvheads), dim3(hdim / 2), 0, st, qkv,
-                       ldqkv, qheads, kvheads, hdim, pos0, pos_step, max_pos, ctx_dev, rc, rs,
-                       q_out, kc, vc, kv_seq_stride, pg);
+              ldqkv, qheads, kvheads, hdim, pos0, pos_step, max_pos, ctx_dev, rc, rs,
+              q_out, kc, vc, kv_seq_stride, pg);
 }
 
 constexpr int ATT_MAXPER = 16;  // query heads per KV group (the 16 MFMA columns)
@@ -174,10 +174,10 @@ static void combine(int qheads, int hdim, int nq, int nsplit, const float *ws_m,
                     int16_t *bsum, hipStream_t st) {
     if (nsplit >= 32)
         SI_LAUNCH(k_attn_combine_wide, dim3(qheads, nq), dim3(1024 / hdim * hdim), 0, st,
-                           qheads, hdim, nsplit, ws_m, ws_l, ws_o, attn, qs, d, bsum);
+                  qheads, hdim, nsplit, ws_m, ws_l, ws_o, attn, qs, d, bsum);
     else
         SI_LAUNCH(k_attn_combine, dim3(qheads, nq), dim3(hdim), 0, st, qheads, hdim,
-                           nsplit, ws_m, ws_l, ws_o, attn, qs, d, bsum);
+                  nsplit, ws_m, ws_l, ws_o, attn, qs, d, bsum);
 }
 
 // ===========================================================================
@@ -702,9 +702,9 @@ void launch_attn_prefill(const float *q, int ntok, int qheads, int kvheads, int 
     const dim3 grid(2 * sp.nsplit + sp.qsplit, kvheads);
     const float scale = 1.0f / sqrtf((float)hdim);  // attention_kernels.h:86
 #define PF_CALL(DIM, NW)                                                                      \
-    SI_LAUNCH((k_attn_prefill<DIM, NW>), grid, dim3(NW * 64),                        \
-                       (PrefillLds<DIM, NW>::bytes()), st, q, ntok, qheads, kvheads, pos0, kc, \
-                       vc, scale, attn, qs, qd, bsum, sp)
+    SI_LAUNCH((k_attn_prefill<DIM, NW>), grid, dim3(NW * 64),                                 \
+              (PrefillLds<DIM, NW>::bytes()), st, q, ntok, qheads, kvheads, pos0, kc,         \
+              vc, scale, attn, qs, qd, bsum, sp)
 #define PF_DIM(DIM)                     \
     if (per <= 8)                       \
         PF_CALL(DIM, 8);                \
@@ -721,9 +721,9 @@ void launch_attn_prefill(const float *q, int ntok, int qheads, int kvheads, int 
     if (sp.nsplit > 0) {
         const size_t t0 = (size_t)sp.qsplit * PF_T, qd_ = (size_t)qheads * hdim;
         SI_LAUNCH(k_attn_combine, dim3(qheads, rows_split), dim3(hdim), 0, st, qheads,
-                           hdim, 2, sp.ws_m, sp.ws_l, sp.ws_o, attn + t0 * qd_,
-                           qs ? qs + t0 * qd_ : nullptr, qs ? qd + t0 * qd_ / SI_QK : nullptr,
-                           bsum ? bsum + t0 * qd_ / SI_QK : nullptr);
+                  hdim, 2, sp.ws_m, sp.ws_l, sp.ws_o, attn + t0 * qd_,
+                  qs ? qs + t0 * qd_ : nullptr, qs ? qd + t0 * qd_ / SI_QK : nullptr,
+                  bsum ? bsum + t0 * qd_ / SI_QK : nullptr);
     }
 }
 
@@ -767,9 +767,9 @@ void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
     const float scale = 1.0f / sqrtf((float)hdim);  // attention_kernels.h:86
     const dim3 grid(ns, kvheads, nq);
 #define SI_ATTN_LAUNCH(DIM)                                                                  \
-    SI_LAUNCH(k_attn_decode_mfma<DIM>, grid, dim3(256), 0, st, q, qheads, kvheads, kc, \
-                       vc, kv_seq_stride, ctx_dev, ctx0, ctx_step, max_ctx, chunk, scale, ws_m, \
-                       ws_l, ws_o, pg, kv_row)
+    SI_LAUNCH(k_attn_decode_mfma<DIM>, grid, dim3(256), 0, st, q, qheads, kvheads, kc,       \
+              vc, kv_seq_stride, ctx_dev, ctx0, ctx_step, max_ctx, chunk, scale, ws_m,       \
+              ws_l, ws_o, pg, kv_row)
     switch (hdim) {
         case 32: SI_ATTN_LAUNCH(32); break;
         case 64: SI_ATTN_LAUNCH(64); break;
@@ -933,7 +933,7 @@ void launch_attn_standard(const float *q, int qheads, int kvheads, int hdim, con
     // context 0 leaves the output zero (attention_kernels.h:70)
     const int npair = qheads * (hdim / 8);
     SI_LAUNCH(k_std_pv, dim3(8 * ((npair + 7) / 8)), dim3(1024), 0, st, scores, vc,
-                       qheads, kvheads, hdim, ctx, out);
+              qheads, kvheads, hdim, ctx, out);
 }
 
 }  // namespace si

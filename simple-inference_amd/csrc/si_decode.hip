@@ -1172,9 +1172,9 @@ void launch_dec_qkv(const float *x, const float *gain, int hidden, float eps, co
                     int8_t *cap_qs, uint16_t *cap_d, int16_t *cap_s, float *qkv, bool exact,
                     hipStream_t st) {
 #define CALL(R, T, E)                                                                            \
-    SI_LAUNCH((k_dec_qkv<R, T, E>), dim3((n + R - 1) / R), dim3(T),                      \
-                       (DecLds<R, T>::bytes(hidden, false, 0)), st, x, gain, hidden, eps, wqs,    \
-                       wd, tile, n, bias, cap_normed, cap_qs, cap_d, cap_s, qkv)
+    SI_LAUNCH((k_dec_qkv<R, T, E>), dim3((n + R - 1) / R), dim3(T),                              \
+              (DecLds<R, T>::bytes(hidden, false, 0)), st, x, gain, hidden, eps, wqs,            \
+              wd, tile, n, bias, cap_normed, cap_qs, cap_d, cap_s, qkv)
     if (exact) {
         CALL(64, 64, true);
     } else {
@@ -1190,10 +1190,10 @@ void launch_dec_wo(const float *pm, const float *pl, const float *po, int ns, in
                    int16_t *cap_s, float *cap_y, float *out, bool exact, hipStream_t st) {
     const int qd = qheads * hdim;
 #define CALL(R, T, E)                                                                            \
-    SI_LAUNCH((k_dec_wo<R, T, E>), dim3((n + R - 1) / R), dim3(T),                       \
-                       (DecLds<R, T>::bytes(qd, false, 0)), st, pm, pl, po, ns,                    \
-                       qheads, hdim, wqs, wd, tile, n, residual, cap_attn, cap_qs, cap_d, cap_s,  \
-                       cap_y, out)
+    SI_LAUNCH((k_dec_wo<R, T, E>), dim3((n + R - 1) / R), dim3(T),                               \
+              (DecLds<R, T>::bytes(qd, false, 0)), st, pm, pl, po, ns,                           \
+              qheads, hdim, wqs, wd, tile, n, residual, cap_attn, cap_qs, cap_d, cap_s,          \
+              cap_y, out)
     if (exact) {
         CALL(64, 64, true);
     } else {
@@ -1212,9 +1212,9 @@ void launch_dec_gateup(const float *h, const float *gain, int hidden, float eps,
                        hipStream_t st) {
     const int n = 2 * f;
 #define CALL(R, T, E)                                                                            \
-    SI_LAUNCH((k_dec_gateup<R, T, E>), dim3((n + R - 1) / R), dim3(T),                   \
-                       (DecLds<R, T>::bytes(hidden, false, 0)), st, h, gain, hidden, eps, wqs,    \
-                       wd, tile, f, cap_normed, cap_qs, cap_d, cap_s, gu, act, aqs, ad, as)
+    SI_LAUNCH((k_dec_gateup<R, T, E>), dim3((n + R - 1) / R), dim3(T),                           \
+              (DecLds<R, T>::bytes(hidden, false, 0)), st, h, gain, hidden, eps, wqs,            \
+              wd, tile, f, cap_normed, cap_qs, cap_d, cap_s, gu, act, aqs, ad, as)
     if (exact) {
         CALL(64, 64, true);
     } else if (hidden / SI_QK >= 8) {
@@ -1301,10 +1301,10 @@ static void dec_attn_impl(const float *qkv, int ldqkv, int nq, int qheads, int k
     const bool fin = attn != nullptr;
     if (dec_rows_ok(qheads, kvheads, hdim, nq)) {
 #define RCALL(DIM, GG, FIN)                                                                       \
-    SI_LAUNCH((k_dec_attn_rows<DIM, GG, FIN, PAGED>), dim3(ns, nq), dim3(256),                \
-                       (RowsLds<DIM, GG>::bytes(per)), st, qkv, ldqkv, qheads, rc, rs, kc, vc,   \
-                       kv_seq_stride, ctx_dev, ctx0, max_ctx, chunk, scale, q_cap, ws_m, ws_l,    \
-                       ws_o, attn, aqs, ad, as, pg)
+    SI_LAUNCH((k_dec_attn_rows<DIM, GG, FIN, PAGED>), dim3(ns, nq), dim3(256),                    \
+              (RowsLds<DIM, GG>::bytes(per)), st, qkv, ldqkv, qheads, rc, rs, kc, vc,             \
+              kv_seq_stride, ctx_dev, ctx0, max_ctx, chunk, scale, q_cap, ws_m, ws_l,             \
+              ws_o, attn, aqs, ad, as, pg)
 #define RCALLG(DIM)                                                \
     if (kvheads == 1) {                                            \
         if (fin) RCALL(DIM, 1, true); else RCALL(DIM, 1, false);   \
@@ -1325,10 +1325,10 @@ static void dec_attn_impl(const float *qkv, int ldqkv, int nq, int qheads, int k
     }
     const dim3 grid(ns, kvheads, nq);
 #define CALL(DIM, NW, FIN, DEP)                                                                \
-    SI_LAUNCH((k_dec_attn<DIM, NW, FIN, PAGED, DEP>), grid, dim3(NW * 64),            \
-                       (AttnLds<DIM, NW>::bytes(per)), st, qkv, ldqkv, qheads, kvheads, rc, rs,  \
-                       kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx, chunk, scale, q_cap,     \
-                       ws_m, ws_l, ws_o, attn, aqs, ad, as, pg)
+    SI_LAUNCH((k_dec_attn<DIM, NW, FIN, PAGED, DEP>), grid, dim3(NW * 64),                     \
+              (AttnLds<DIM, NW>::bytes(per)), st, qkv, ldqkv, qheads, kvheads, rc, rs,         \
+              kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx, chunk, scale, q_cap,              \
+              ws_m, ws_l, ws_o, attn, aqs, ad, as, pg)
 #define CALLN(DIM, NW, FIN)                                             \
     if (chunk <= DA_TILE * NW) {                                        \
         CALL(DIM, NW, FIN, 1);                                          \

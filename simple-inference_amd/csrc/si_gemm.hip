@@ -610,7 +610,7 @@ void launch_gemm_reduce(const float *part, int splits, int m, int n, float *out,
     const size_t tot = (size_t)m * n;
     if (!tot) return;
     SI_LAUNCH(k_gemm_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st,
-                       part, splits, m, n, nullptr, nullptr, out, n);
+              part, splits, m, n, nullptr, nullptr, out, n);
 }
 
 void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
@@ -630,7 +630,7 @@ static int gemm_core(const uint8_t *wqs, const uint16_t *wd, int tile, int n, in
     if (exact) {
         const dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM);
         SI_LAUNCH(k_gemm_q4q8<true>, grid, dim3(256), 0, st, wqs, wd, tile, n, nb, xqs,
-                           xd, m, bias, residual, out, ldo);
+                  xd, m, bias, residual, out, ldo);
         return 0;
     }
     GemmPlan p = gemm_plan(m, n, nb);
@@ -641,9 +641,9 @@ static int gemm_core(const uint8_t *wqs, const uint16_t *wd, int tile, int n, in
     float *part = p.splits > 1 ? (float *)workspace : nullptr;
     const dim3 grid((n + p.bn - 1) / p.bn, (m + p.bm - 1) / p.bm, p.splits);
 #define CALL(WM, WN, TM, TN)                                                                   \
-    SI_LAUNCH((k_gemm_fast<WM, WN, TM, TN, false>), grid, dim3(256),                  \
-                       (GemmCfg<WM, WN, TM, TN>::lds_bytes()), st, wqs, wd, tile, n, nb, xqs,   \
-                       xd, m, bias, residual, out, ldo, part, p.bps, GateUpOut{})
+    SI_LAUNCH((k_gemm_fast<WM, WN, TM, TN, false>), grid, dim3(256),                           \
+              (GemmCfg<WM, WN, TM, TN>::lds_bytes()), st, wqs, wd, tile, n, nb, xqs,           \
+              xd, m, bias, residual, out, ldo, part, p.bps, GateUpOut{})
     if (p.bm == 64)
         CALL(1, 4, 2, 1);
     else
@@ -655,10 +655,10 @@ static int gemm_core(const uint8_t *wqs, const uint16_t *wd, int tile, int n, in
         const auto al = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
         if (n % 4 == 0 && ldo % 4 == 0 && al(out) && al(bias) && al(residual))
             SI_LAUNCH(k_gemm_reduce4, dim3((unsigned)((tot / 4 + 255) / 256)), dim3(256),
-                               0, st, part, p.splits, m, n, bias, residual, out, ldo);
+                      0, st, part, p.splits, m, n, bias, residual, out, ldo);
         else
             SI_LAUNCH(k_gemm_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0,
-                               st, part, p.splits, m, n, bias, residual, out, ldo);
+                      st, part, p.splits, m, n, bias, residual, out, ldo);
     }
     return 0;
 }
@@ -681,7 +681,7 @@ void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int
         if (splits > 1) {
             const int tot = m * (f / SI_QK);
             SI_LAUNCH(k_gemm_reduce_swiglu_q8, dim3((tot + 7) / 8), dim3(256), 0, st,
-                               (const float *)workspace, splits, m, f, gu, act, qs, d, s);
+                      (const float *)workspace, splits, m, f, gu, act, qs, d, s);
         } else {
             launch_swiglu_q8(gu, m, f, act, qs, d, s, st);
         }
@@ -690,9 +690,9 @@ void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int
     const GateUpOut go{f, act, qs, d, s};
     const dim3 grid((n + p.bn - 1) / p.bn, (m + p.bm - 1) / p.bm, 1);
 #define CALL(WM, WN, TM, TN)                                                                   \
-    SI_LAUNCH((k_gemm_fast<WM, WN, TM, TN, true>), grid, dim3(256),                   \
-                       (GemmCfg<WM, WN, TM, TN>::lds_bytes()), st, wqs, wd, tile, n, nb, xqs,   \
-                       xd, m, nullptr, nullptr, gu, n, nullptr, nb, go)
+    SI_LAUNCH((k_gemm_fast<WM, WN, TM, TN, true>), grid, dim3(256),                            \
+              (GemmCfg<WM, WN, TM, TN>::lds_bytes()), st, wqs, wd, tile, n, nb, xqs,           \
+              xd, m, nullptr, nullptr, gu, n, nullptr, nb, go)
     if (p.bm == 64)
         CALL(2, 2, 1, 2);
     else

@@ -82,9 +82,9 @@ void launch_matvec(const int8_t *xqs, const uint16_t *xd, const int16_t *xs, int
                    const float *residual, float *out, bool exact, hipStream_t st, float *pre) {
     if (n <= 0) return;
 #define CALL(R, T, E)                                                                        \
-    SI_LAUNCH((k_matvec<R, T, E>), dim3((n + R - 1) / R), dim3(T),                  \
-                       (matvec_lds_bytes<R, T>(k)), st, xqs, xd, xs, k, wqs, wd, tile, n, bias,  \
-                       residual, out, pre)
+    SI_LAUNCH((k_matvec<R, T, E>), dim3((n + R - 1) / R), dim3(T),                           \
+              (matvec_lds_bytes<R, T>(k)), st, xqs, xd, xs, k, wqs, wd, tile, n, bias,       \
+              residual, out, pre)
     if (exact) {
         CALL(64, 64, true);
     } else {
@@ -111,7 +111,7 @@ void launch_block_dots(const uint8_t *wqs, int n, int k, const int8_t *xqs, cons
                        int32_t *dots, hipStream_t st) {
     const int nb = k / SI_QK;
     SI_LAUNCH(k_block_dots, dim3((n + 63) / 64, nb), dim3(64), 0, st, wqs, n, nb, xqs,
-                       xs, dots);
+              xs, dots);
 }
 
 }  // namespace si

@@ -70,7 +70,7 @@ void launch_matvec_rowmajor(const uint8_t *w, const void *x, int inputs, int out
                             const float *bias, float *out, hipStream_t st) {
     if (outputs <= 0) return;
     SI_LAUNCH(k_matvec_rowmajor, dim3(outputs), dim3(64), 0, st, (const uint16_t *)w,
-                       (const uint16_t *)x, inputs / SI_QK, bias, out);
+              (const uint16_t *)x, inputs / SI_QK, bias, out);
 }
 
 // ---------------------------------------------------------------------------
@@ -127,7 +127,7 @@ void launch_colsoa_matvec(const uint8_t *tiles, int ntiles, const void *x, int n
                           hipStream_t st) {
     if (ntiles <= 0) return;
     SI_LAUNCH(k_colsoa_matvec, dim3(ntiles), dim3(256), 0, st, tiles,
-                       (const uint16_t *)x, nblocks, bias_lo, bias_hi, out, add);
+              (const uint16_t *)x, nblocks, bias_lo, bias_hi, out, add);
 }
 
 // ---------------------------------------------------------------------------
@@ -186,7 +186,7 @@ void launch_rope_inplace(float *heads, int nheads, int hdim, int position, const
     const int n = nheads * (hdim / 2);
     if (n <= 0) return;
     SI_LAUNCH(k_rope_inplace, dim3((n + 255) / 256), dim3(256), 0, st, heads, nheads,
-                       hdim, position, rc, rs);
+              hdim, position, rc, rs);
 }
 
 // f32_to_f16 / f16_to_f32 (qwen_one_layer.c:42-86) elementwise.
@@ -206,10 +206,10 @@ void launch_f16_convert(const void *src, void *dst, size_t n, bool to_half, hipS
     const dim3 grid((unsigned)((n + 255) / 256));
     if (to_half)
         SI_LAUNCH(k_f32_to_f16, grid, dim3(256), 0, st, (const float *)src,
-                           (uint16_t *)dst, n);
+                  (uint16_t *)dst, n);
     else
         SI_LAUNCH(k_f16_to_f32, grid, dim3(256), 0, st, (const uint16_t *)src,
-                           (float *)dst, n);
+                  (float *)dst, n);
 }
 
 }  // namespace si

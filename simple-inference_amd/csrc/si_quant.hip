@@ -267,7 +267,7 @@ void launch_quantize_q8_aos(const float *src, void *dst, int count, hipStream_t 
     const int nb = count / SI_QK;
     if (nb == 0) return;
     SI_LAUNCH(k_quantize_q8_aos, dim3((nb + 7) / 8), dim3(256), 0, st, src,
-                       (uint8_t *)dst, nb);
+              (uint8_t *)dst, nb);
 }
 
 void launch_quantize_q8_rows(const float *src, int rows, int k, int8_t *qs, uint16_t *d,
@@ -275,7 +275,7 @@ void launch_quantize_q8_rows(const float *src, int rows, int k, int8_t *qs, uint
     const int nbr = k / SI_QK, tot = nbr * rows;
     if (tot == 0) return;
     SI_LAUNCH(k_quantize_q8_rows, dim3((tot + 7) / 8), dim3(256), 0, st, src, k, nbr,
-                       tot, qs, d, s);
+              tot, qs, d, s);
 }
 
 void launch_rmsnorm_q8_parts(const float *x, const float *part, int splits, const float *gain,
@@ -291,8 +291,8 @@ void launch_rmsnorm_q8_parts(const float *x, const float *part, int splits, cons
         return;
     }
 #define RMS_P(NPT)                                                                              \
-    SI_LAUNCH((k_rmsnorm_q8_v4<true, NPT, true>), dim3(rows), dim3(256), 0, st, x, part, \
-                       gain, n, eps, h, normed, qs, d, s, splits, y_out)
+    SI_LAUNCH((k_rmsnorm_q8_v4<true, NPT, true>), dim3(rows), dim3(256), 0, st, x, part,        \
+              gain, n, eps, h, normed, qs, d, s, splits, y_out)
     if (n4 <= 256) RMS_P(1);
     else if (n4 <= 512) RMS_P(2);
     else if (n4 <= 1024) RMS_P(4);
@@ -309,7 +309,7 @@ void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int ro
     if (n4 <= 2048 && al(x) && al(y) && al(h) && al(normed) && al(gain) && al(qs)) {
         const int npt = n4 <= 256 ? 1 : n4 <= 512 ? 2 : n4 <= 1024 ? 4 : 8;
 #define RMS_V4(RES, NPT)                                                                          \
-    SI_LAUNCH((k_rmsnorm_q8_v4<RES, NPT>), dim3(rows), dim3(256), 0, st, x, y, gain, n,    \
+    SI_LAUNCH((k_rmsnorm_q8_v4<RES, NPT>), dim3(rows), dim3(256), 0, st, x, y, gain, n,           \
               eps, h, normed, qs, d, s, 1, (float *)nullptr)
 #define RMS_V4N(RES)                     \
     switch (npt) {                       \
@@ -330,10 +330,10 @@ void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int ro
     const size_t lds = (size_t)n * sizeof(float);
     if (y)
         SI_LAUNCH(k_rmsnorm_q8<true>, dim3(rows), dim3(256), lds, st, x, y, gain, n,
-                           eps, h, normed, qs, d, s);
+                  eps, h, normed, qs, d, s);
     else
         SI_LAUNCH(k_rmsnorm_q8<false>, dim3(rows), dim3(256), lds, st, x, y, gain, n,
-                           eps, h, normed, qs, d, s);
+                  eps, h, normed, qs, d, s);
 }
 
 void launch_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs, uint16_t *d,
@@ -341,7 +341,7 @@ void launch_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs, 
     const int nbr = f / SI_QK, tot = nbr * rows;
     if (tot == 0) return;
     SI_LAUNCH(k_swiglu_q8, dim3((tot + 7) / 8), dim3(256), 0, st, gu, f, nbr, tot, act,
-                       qs, d, s);
+              qs, d, s);
 }
 
 void launch_q4_repack(const uint8_t *src, int n, int k, int tile, uint8_t *qs, uint16_t *d,
@@ -349,7 +349,7 @@ void launch_q4_repack(const uint8_t *src, int n, int k, int tile, uint8_t *qs, u
     const size_t tot = (size_t)n * (k / SI_QK);
     if (!tot) return;
     SI_LAUNCH(k_q4_repack, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, src,
-                       n, k / SI_QK, tile, qs, d);
+              n, k / SI_QK, tile, qs, d);
 }
 
 void launch_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k, int tile,
@@ -357,7 +357,7 @@ void launch_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k, int ti
     const size_t tot = (size_t)n * (k / SI_QK);
     if (!tot) return;
     SI_LAUNCH(k_q4_unpack, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, qs,
-                       d, n, k / SI_QK, tile, dst);
+              d, n, k / SI_QK, tile, dst);
 }
 
 }  // namespace si
