@@ -327,7 +327,7 @@ int si_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, i
                "gemm_gateup: operands beyond 2 GiB (m=%d f=%d k=%d)", m, f, k);
     SI_REQUIRE(m == 0 || (wqs && wd && xqs && xd && qs && d), "gemm_gateup: NULL pointer");
     {
-        const size_t need = gemm_workspace_bytes(m, 2 * f, k);
+        const size_t need = gemm_gateup_workspace_bytes(m, f, k);
         const bool gu_needed = (flags & SI_GEMM_EXACT) || (need > 0 && (!workspace || ws_bytes < need));
         SI_REQUIRE(m == 0 || gu || !gu_needed,
                    "gemm_gateup: gu is the intermediate here (exact mode, or a K split "

@@ -20,6 +20,8 @@
 #include "si_device.hpp"
 #include "si_kernels.hpp"
 
+#include <algorithm>
+
 namespace si {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -475,6 +477,375 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
         }
 }
 
+// ---------------------------------------------------------------------
+// Batched-decode GEMM (m <= 64 activation rows).
+//
+// At this size each output costs two VALU operations per K block (the
+// exact int32 dot converted, then one fused multiply-add by the fp32 scale
+// product) against a fraction of one matrix-core instruction, so the
+// kernel is built to keep the vector ALUs issuing:
+//   * a workgroup holds 32 activation rows of one K range (at most
+//     BD_MAX_CB blocks) in LDS for its whole life, filled once with
+//     coalesced loads, in MFMA operand order;
+//   * its 8 wavefronts share that range block by block (wavefront w takes
+//     blocks w, w + 8, ...) and stream their weights straight into
+//     registers P blocks ahead, with no barrier in the K loop, over a
+//     persistent walk of the workgroup's column tiles: the prefetch runs
+//     on across tiles;
+//   * at the end of a tile the 8 partial sums meet in LDS and are added in
+//     wavefront order (deterministic); wavefront w finishes output
+//     registers 2w and 2w + 1 of the 16 of every lane.
+// The two 32-row halves of a set of tiles run on the same XCD (blockIdx %
+// 8), so the second half's weight reads hit that XCD's L2.  Longer K is
+// split into ranges whose partials [c][m][n] are summed afterwards, as
+// k_gemm_fast's are.
+//
+// Operands: lane (j, g) of the 32x32x32 i8 MFMA supplies half g of a block
+// as elements 8g..8g+7 and 16+8g..16+8g+7 (A and B agree, so the MFMA gives
+// the block's exact integer dot): for Q4_0 these are both nibbles of bytes
+// 8g..8g+7, one 8-byte load.  Nibble n becomes the int8 16*(n - 8): n ^ 8
+// is the 4-bit two's complement of n - 8, so in a byte's top nibble it
+// reads as 16*(n - 8).  The dots come out 16x, exactly (|16 dot| < 2^20),
+// and fma(16 dot, s, 16 acc) is 16 times fma(dot, s, acc) bit for bit (a
+// power-of-two scale commutes with rounding), so the sums are scaled by
+// 1/16, exactly, once at the end.
+//
+// LDS: block b of the activations is 1 KB, [half g][slot][16 B], row i in
+// slot i ^ 2(b & 3): a fill instruction's 8 rows x 4 blocks then spread
+// over the banks, and the 32 lanes of a half read one 512-byte run.
+//
+// MODE 0 (TN = 1): out = residual + (acc + bias) (both optional), or the
+// partials.  MODE 1 (TN = 2, gate|up, one K range): tile u pairs the gate
+// rows 32u..32u+31 with the up rows f+32u..; SwiGLU + Q8_0 epilogue as
+// k_gemm_fast's.
+constexpr int BD_W = 8;                                    // wavefronts per workgroup
+constexpr int BD_RED = BD_W * 16 * 64 * 4;                 // a 32x32 fp32 tile per wavefront
+constexpr int BD_LDS_MAX = 160 * 1024;                     // LDS of a gfx950 CU
+constexpr int BD_XST = 130;  // x.d row stride in halves: 65 dwords, odd, >= 128 blocks
+constexpr int BD_XBYTES = 32 * BD_XST * 2;
+// LDS of a K range of cb blocks: Q8 rows (a multiple of 4 blocks), x.d
+// rows, partial tiles
+__host__ __device__ constexpr size_t bd_lds(int cb) {
+    return (size_t)((cb + 3) & ~3) * 1024 + BD_XBYTES + BD_RED;
+}
+constexpr int BD_MAX_CB = (BD_LDS_MAX - BD_XBYTES - BD_RED) / 1024 & ~3;  // 116 blocks
+constexpr int BD_FILL = (BD_MAX_CB * 64 + 511) / 512;      // 16-byte fill pieces per thread
+constexpr int BD_XFILL = 32 * 128 / 512;                   // x.d fill values per thread
+
+typedef unsigned gv2u __attribute__((vector_size(8)));  // an 8-byte buffer load's value
+typedef int v2i __attribute__((ext_vector_type(2)));
+
+template <int TN>
+struct BdStage {
+    gv2u w[TN];       // nibble bytes 8g..8g+7 of weight row j of tile u
+    uint16_t ws[TN];  // w.d fp16 bits (lanes 32..63: 0); widened where used, so
+                      // that nothing waits for the load before then
+};
+
+// A workgroup barrier ordering LDS only: __syncthreads() also orders global
+// memory, which waits for every global load in flight (here the weight
+// prefetch); the partial sums and the fill need the LDS half alone.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Workgroup id -> (row half h, K range c, slot s) with the halves of one
+// (c, s) on one XCD; q >= C * S: no work.
+__device__ __forceinline__ void bd_place(int id, int H, int S, int &h, int &q, int &c, int &s) {
+    const int x = id & 7, r = id >> 3;
+    h = r % H;
+    q = (r / H) * 8 + x;
+    c = q / S;
+    s = q - c * S;
+}
+
+template <int TN, int P, int MODE>
+__global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
+    const uint8_t *__restrict__ wqs, const uint16_t *__restrict__ wd, int tile, int n, int nb,
+    const int8_t *__restrict__ xqs, const uint16_t *__restrict__ xd, int m,
+    const float *__restrict__ bias, const float *__restrict__ residual, float *__restrict__ out,
+    int ldo, float *__restrict__ part, int H, int C, int S, int cb, int units, GateUpOut go) {
+    static_assert(MODE == 0 ? TN == 1 : TN == 2, "MODE 0 takes one tile, gate|up two");
+    extern __shared__ __attribute__((aligned(16))) uint8_t bd_sm[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    // the wavefront index as a scalar: block numbers derived from it are
+    // the buffer loads' scalar offsets
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 31, g = lane >> 5;
+    int h, q, c, s;
+    bd_place(blockIdx.x, H, S, h, q, c, s);
+    if (q >= C * S) return;  // the whole workgroup
+    const int m0 = 32 * h, b0 = c * cb, len = min(nb, b0 + cb) - b0;
+    const int k = nb * SI_QK;
+    const int cb4 = (cb + 3) & ~3;
+    uint8_t *a_l = bd_sm;  // [cb4][2][32][16 B]
+    // x.d rows of BD_XST halves, an odd number of dwords: the 32 rows'
+    // values of one block sit in 32 different banks
+    uint16_t *x_l = (uint16_t *)(bd_sm + (size_t)cb4 * 1024);               // [32][BD_XST]
+    float4 *red = (float4 *)(bd_sm + (size_t)cb4 * 1024 + BD_XBYTES);        // [8][4][64]
+
+    // ---- the tiles of this workgroup: units s, s + S, ...
+    const int per = (len + BD_W - 1) / BD_W;  // blocks per wavefront per tile (some may be past len)
+    const int nu = s < units ? (units - 1 - s) / S + 1 : 0;
+    const int total = nu * per;
+    const int ltile = __builtin_ctz((unsigned)tile);
+    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(wqs, (uint32_t)nb * n * 16);
+    const __amdgpu_buffer_rsrc_t rw =
+        buf_rsrc(wd, __builtin_amdgcn_readfirstlane((int)q4_scale_count(n, nb, tile) * 2));
+    // first column of tile u of unit iu (scalar)
+    auto col0 = [&](int iu, int u) {
+        const int unit = s + S * iu;
+        return MODE == 1 ? (u ? go.f : 0) + 32 * unit : 32 * unit;
+    };
+    // the load pointer: (unit lu, step lk), its lanes' byte offsets
+    int lu = 0, lk = 0, lu_set = -1;
+    uint32_t vob[TN], vow[TN];
+    auto set_unit = [&](int iu) {
+#pragma unroll
+        for (int u = 0; u < TN; ++u) {
+            const int cc = min(col0(iu, u) + j, n - 1);  // past n: any valid row
+            vob[u] = (uint32_t)cc * 16 + 8 * g;
+            vow[u] = g ? 0x80000000u
+                       : (uint32_t)(((cc >> ltile) * nb << ltile) + (cc & (tile - 1))) * 2;
+        }
+    };
+    auto load = [&](BdStage<TN> &st) {
+        const int iu = min(lu, nu - 1);  // past the end: a valid block again
+        if (iu != lu_set) {
+            set_unit(iu);
+            lu_set = iu;
+        }
+        const int b = b0 + min(BD_W * lk + wave, len - 1);
+#pragma unroll
+        for (int u = 0; u < TN; ++u) {
+            st.w[u] = __builtin_amdgcn_raw_buffer_load_b64(rb, vob[u], b * n * 16, 0);
+            st.ws[u] = __builtin_amdgcn_raw_buffer_load_b16(rw, vow[u], (b << ltile) * 2, 0);
+        }
+        if (++lk == per) {
+            lk = 0;
+            ++lu;
+        }
+    };
+
+    // P blocks of weights in flight, requested before the fill so that
+    // their latency and the fill's overlap.  Loads retire in issue order,
+    // so each stage's loads stay together and in stage order (scheduling
+    // barriers), and every load is issued (a valid block past the end):
+    // the wait before a block then counts the same later loads on every
+    // path into it.
+    BdStage<TN> st[P];
+    if (total > 0) {
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            load(st[i]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // bias and residual of up to two tiles are read before the K loop: a
+    // load in the epilogue would wait for every weight load in flight
+    float pb[2] = {0.0f, 0.0f}, pr[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+    const bool pre = MODE == 0 && nu <= 2 && (bias || residual);
+    if (pre) {
+#pragma unroll
+        for (int iu = 0; iu < 2; ++iu) {
+            if (iu >= nu) break;
+            const int col = min(col0(iu, 0) + j, n - 1);
+            if (bias) pb[iu] = bias[col];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int row = min(m0 + 8 * (wave >> 1) + 4 * g + 2 * (wave & 1) + i, m - 1);
+                if (residual) pr[iu][i] = residual[(size_t)row * ldo + col];
+            }
+        }
+    }
+
+    // ---- fill: the K range's 32 rows (clamped to m - 1) and their x.d
+    {
+        const __amdgpu_buffer_rsrc_t ra = buf_rsrc(xqs, (uint32_t)m * k);
+        const __amdgpu_buffer_rsrc_t rx = buf_rsrc(xd, (uint32_t)m * nb * 2);
+        v4i fv[BD_FILL];
+        uint32_t xv[BD_XFILL];
+        // Q8: 8 threads read a row's 128 bytes (4 blocks), 8 rows per 64
+        // threads; a wavefront's pieces are 4 whole blocks, so whether they
+        // are stored is decided per wavefront (pieces past len read zero)
+#pragma unroll
+        for (int i = 0; i < BD_FILL; ++i) {
+            const int p = tid + 512 * i, t8 = p & 7, ri = (p >> 3) & 31;
+            const int b = 4 * (p >> 8) + (t8 >> 1);
+            const int row = min(m0 + ri, m - 1);
+            const uint32_t off = b < len ? (uint32_t)row * k + (uint32_t)(b0 + b) * SI_QK + (t8 & 1) * 16
+                                         : 0x80000000u;  // past the end: zero, no access
+            fv[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
+        }
+        // x.d: 128 threads per row, consecutive blocks
+#pragma unroll
+        for (int i = 0; i < BD_XFILL; ++i) {
+            const int e = tid + 512 * i, ri = e >> 7, b = e & 127;
+            const int row = min(m0 + ri, m - 1);
+            const uint32_t off = b < len ? ((uint32_t)row * nb + b0 + b) * 2 : 0x80000000u;
+            xv[i] = __builtin_amdgcn_raw_buffer_load_b16(rx, off, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < BD_FILL; ++i) {
+            const int p4 = (tid >> 8) + 2 * i;  // the wavefront's group of 4 blocks
+            if (4 * p4 < len) {
+                const int p = tid + 512 * i, t8 = p & 7, ri = (p >> 3) & 31;
+                const int b = 4 * p4 + (t8 >> 1);
+                // 16 bytes = elements 16*part .. +15: bytes 0..7 go to half 0,
+                // bytes 8..15 to half 1, at offset 8*part of the row's slot
+                uint8_t *d = a_l + ((size_t)b * 64 + (ri ^ ((b & 3) << 1))) * 16 + (t8 & 1) * 8;
+                *(v2i *)d = (v2i){fv[i][0], fv[i][1]};
+                *(v2i *)(d + 512) = (v2i){fv[i][2], fv[i][3]};
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < BD_XFILL; ++i) {
+            const int e = tid + 512 * i;
+            x_l[(e >> 7) * BD_XST + (e & 127)] = (uint16_t)xv[i];  // row padding takes b >= 128
+        }
+        // every load so far complete (the fill's skipped pieces included, so
+        // no register is left waiting on a load of this phase), the first
+        // weight stages with them: they are needed first anyway
+        __builtin_amdgcn_s_waitcnt(0);
+    }
+    lds_barrier();
+
+    float acc[TN][16];
+#pragma unroll
+    for (int u = 0; u < TN; ++u)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[u][v] = 0.0f;
+    const uint32_t la = (uint32_t)(g * 32 + (j ^ ((wave & 3) << 1))) * 16;  // this wave's slots
+    // the activation operands of a step, read one step ahead of their use
+    v4i a_nx;
+    uint16_t x_nx;
+    auto fetch = [&](int ck) {
+        const int rel = min(BD_W * ck + wave, len - 1);
+        a_nx = *(const v4i *)(a_l + (size_t)rel * 1024 + la);
+        x_nx = x_l[j * BD_XST + rel];
+    };
+    auto compute = [&](const BdStage<TN> &st, const v4i &aop, uint16_t xs) {
+        // scale product x.d * w.d in the output layout: A carries x.d at
+        // k = 0 and k = 4, B carries w.d at k = 0 only
+        const gh4 asc = __builtin_bit_cast(gh4, (v2u){(uint32_t)xs, 0u});
+#pragma unroll
+        for (int u = 0; u < TN; ++u) {
+            // ((n ^ 8) << 4) per nibble: one shift and one three-input
+            // bitwise op for the low nibbles, one op for the high ones
+            const uint32_t w0 = st.w[u][0], w1 = st.w[u][1];
+            const v4i bop = (v4i){(int)(((w0 << 4) ^ 0x80808080u) & 0xf0f0f0f0u),
+                                  (int)(((w1 << 4) ^ 0x80808080u) & 0xf0f0f0f0u),
+                                  (int)((w0 ^ 0x80808080u) & 0xf0f0f0f0u),
+                                  (int)((w1 ^ 0x80808080u) & 0xf0f0f0f0u)};
+            const gh4 bsc = __builtin_bit_cast(gh4, (v2u){(uint32_t)st.ws[u], 0u});
+            v16i z = {};
+            const v16i dot = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, z, 0, 0, 0);
+            v16f zf = {};
+            const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(asc, bsc, zf, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[u][v] = fmaf((float)dot[v], sc[v], acc[u][v]);
+        }
+    };
+    // a tile's 8 partials summed in wavefront order; wavefront w gets
+    // registers 2w and 2w + 1 (rows 8(w/2) + 4g + 2(w%2) + {0, 1})
+    auto reduce = [&](const float (&a)[16], float (&r)[2]) {
+#pragma unroll
+        for (int v4 = 0; v4 < 4; ++v4)
+            red[(wave * 4 + v4) * 64 + lane] =
+                make_float4(a[4 * v4], a[4 * v4 + 1], a[4 * v4 + 2], a[4 * v4 + 3]);
+        lds_barrier();
+        const float *rf = (const float *)red;
+        const int o = ((wave >> 1) * 64 + lane) * 4 + 2 * (wave & 1);
+        float2 t = *(const float2 *)(rf + o);
+#pragma unroll
+        for (int w = 1; w < BD_W; ++w) {
+            const float2 p = *(const float2 *)(rf + w * 1024 + o);
+            t = make_float2(__fadd_rn(t.x, p.x), __fadd_rn(t.y, p.y));
+        }
+        r[0] = t.x * 0.0625f;  // the 16x of the operands, exactly
+        r[1] = t.y * 0.0625f;
+        lds_barrier();  // the area is written again next
+    };
+    auto finish = [&](int iu) {
+        float r[TN][2];
+#pragma unroll
+        for (int u = 0; u < TN; ++u) reduce(acc[u], r[u]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int row = m0 + 8 * (wave >> 1) + 4 * g + 2 * (wave & 1) + i;
+            if (MODE == 1) {
+                const int f = go.f, feat = col0(iu, 0) + j;
+                const float gv = r[0][i], uv = r[TN - 1][i];
+                const float silu = __fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)));
+                const float av = __fmul_rn(silu, uv);
+                uint16_t dbits;
+                int bsum;
+                const int qv = quant_block_lane(av, dbits, bsum);  // all 32 lanes of the half
+                if (row < m && feat < f) {
+                    const size_t o = (size_t)row * f + feat;
+                    if (out) {
+                        out[(size_t)row * ldo + feat] = gv;
+                        out[(size_t)row * ldo + f + feat] = uv;
+                    }
+                    if (go.act) go.act[o] = av;
+                    go.qs[o] = (int8_t)qv;
+                    if (j == 0) {
+                        go.d[o / SI_QK] = dbits;
+                        if (go.s) go.s[o / SI_QK] = (int16_t)bsum;
+                    }
+                }
+            } else {
+                const int col = col0(iu, 0) + j;
+                if (row < m && col < n) {
+                    if (part) {
+                        part[((size_t)c * m + row) * n + col] = r[0][i];
+                    } else if (pre) {
+                        float y = r[0][i] + (iu ? pb[1] : pb[0]);
+                        if (residual) y = __fadd_rn(iu ? pr[1][i] : pr[0][i], y);
+                        out[(size_t)row * ldo + col] = y;
+                    } else {
+                        float y = r[0][i] + (bias ? bias[col] : 0.0f);
+                        if (residual) y = __fadd_rn(residual[(size_t)row * ldo + col], y);
+                        out[(size_t)row * ldo + col] = y;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < TN; ++u)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[u][v] = 0.0f;
+    };
+
+    if (total > 0) {
+        fetch(0);
+        int cu = 0, ck = 0;  // the compute pointer
+        for (int it0 = 0; it0 < total; it0 += P) {
+#pragma unroll
+            for (int i = 0; i < P; ++i) {
+                if (it0 + i < total) {
+                    const v4i aop = a_nx;
+                    const uint16_t xs = x_nx;
+                    const bool valid = BD_W * ck + wave < len;
+                    const int ckn = ck + 1 == per ? 0 : ck + 1;
+                    fetch(ckn);
+                    if (valid) compute(st[i], aop, xs);
+                    ck = ckn;
+                    if (ck == 0) {
+                        finish(cu);
+                        ++cu;
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                load(st[i]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+}
+
 // The gate|up split partials [splits][m][2f] summed in split order (as
 // k_gemm_reduce4), gate|up written to gu (optional), then SwiGLU and Q8_0
 // exactly as k_swiglu_q8: half a wavefront per 32-feature block of a row.
@@ -588,9 +959,60 @@ static GemmPlan gemm_plan(int m, int n, int nb) {
     return p;
 }
 
+// k_gemm_bd's layout for m <= BD_MAX_M rows: H 32-row halves, C K ranges
+// of cb blocks, S workgroups (slots) per (half, range) sharing its tiles
+// round robin; H * C * S <= 256, one workgroup per CU (its LDS is most of
+// the CU's).
+constexpr int BD_MAX_M = 64;
+struct BdPlan {
+    int H, C, S, cb, units, grid;
+    size_t lds;
+};
+static BdPlan bd_plan(int m, int n, int nb, int mode) {
+    BdPlan p;
+    p.H = (m + 31) / 32;
+    p.C = (nb + BD_MAX_CB - 1) / BD_MAX_CB;
+    p.cb = (nb + p.C - 1) / p.C;
+    p.units = mode == 1 ? n / 64 : (n + 31) / 32;
+    p.S = std::max(1, std::min(256 / (p.H * p.C), p.units));
+    p.grid = 8 * p.H * ((p.C * p.S + 7) / 8);
+    p.lds = bd_lds(p.cb);
+    return p;
+}
+
 size_t gemm_workspace_bytes(int m, int n, int k) {
-    const GemmPlan p = gemm_plan(m, n, k / SI_QK);
-    return p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0;
+    const int nb = k / SI_QK;
+    const int splits = m <= BD_MAX_M ? bd_plan(m, n, nb, 0).C : gemm_plan(m, n, nb).splits;
+    return splits > 1 ? (size_t)splits * m * n * sizeof(float) : 0;
+}
+
+size_t gemm_gateup_workspace_bytes(int m, int f, int k) {
+    if (m <= BD_MAX_M && k / SI_QK <= BD_MAX_CB) return 0;  // one fused pass
+    return gemm_workspace_bytes(m, 2 * f, k);
+}
+
+// k_gemm_bd launch (mode 1: gate|up, f = n / 2 features, one K range).
+static void launch_bd(const BdPlan &p, int mode, const uint8_t *wqs, const uint16_t *wd,
+                      int tile, int n, int nb, const int8_t *xqs, const uint16_t *xd, int m,
+                      const float *bias, const float *residual, float *out, int ldo, float *part,
+                      const GateUpOut &go, hipStream_t st) {
+#define BD(TN, P, MODE)                                                                        \
+    do {                                                                                       \
+        static bool big_lds = false;                                                           \
+        if (!big_lds) {                                                                        \
+            hipFuncSetAttribute((const void *)k_gemm_bd<TN, P, MODE>,                          \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, BD_LDS_MAX);       \
+            big_lds = true;                                                                    \
+        }                                                                                      \
+        SI_LAUNCH((k_gemm_bd<TN, P, MODE>), dim3(p.grid), dim3(64 * BD_W), p.lds, st, wqs, wd, \
+                  tile, n, nb, xqs, xd, m, bias, residual, out, ldo, part, p.H, p.C, p.S,      \
+                  p.cb, p.units, go);                                                          \
+    } while (0)
+    if (mode == 1)
+        BD(2, 8, 1);
+    else
+        BD(1, 16, 0);
+#undef BD
 }
 
 static int gemm_core(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
@@ -633,32 +1055,56 @@ static int gemm_core(const uint8_t *wqs, const uint16_t *wd, int tile, int n, in
                   xd, m, bias, residual, out, ldo);
         return 0;
     }
-    GemmPlan p = gemm_plan(m, n, nb);
-    if (p.splits > 1 && (!workspace || ws_bytes < (size_t)p.splits * m * n * sizeof(float))) {
-        p.splits = 1;  // no workspace: one pass over K
-        p.bps = nb;
-    }
-    float *part = p.splits > 1 ? (float *)workspace : nullptr;
-    const dim3 grid((n + p.bn - 1) / p.bn, (m + p.bm - 1) / p.bm, p.splits);
+    const auto fits = [&](int splits) {
+        return workspace && ws_bytes >= (size_t)splits * m * n * sizeof(float);
+    };
+    float *part = nullptr;
+    int splits;
+    if (m <= BD_MAX_M) {
+        const BdPlan p = bd_plan(m, n, nb, 0);
+        if (p.C == 1 || fits(p.C)) {
+            part = p.C > 1 ? (float *)workspace : nullptr;
+            launch_bd(p, 0, wqs, wd, tile, n, nb, xqs, xd, m, bias, residual, out, ldo, part,
+                      GateUpOut{}, st);
+            splits = p.C;
+        } else {
+            // K longer than one LDS range and no workspace: the LDS-staged
+            // kernel in one pass
+            const dim3 grid((n + 127) / 128, (m + 63) / 64, 1);
+            SI_LAUNCH((k_gemm_fast<1, 4, 2, 1, false>), grid, dim3(256),
+                      (GemmCfg<1, 4, 2, 1>::lds_bytes()), st, wqs, wd, tile, n, nb, xqs, xd, m,
+                      bias, residual, out, ldo, nullptr, nb, GateUpOut{});
+            splits = 1;
+        }
+    } else {
+        GemmPlan p = gemm_plan(m, n, nb);
+        if (p.splits > 1 && !fits(p.splits)) {
+            p.splits = 1;
+            p.bps = nb;
+        }
+        part = p.splits > 1 ? (float *)workspace : nullptr;
+        const dim3 grid((n + p.bn - 1) / p.bn, (m + p.bm - 1) / p.bm, p.splits);
 #define CALL(WM, WN, TM, TN)                                                                   \
     SI_LAUNCH((k_gemm_fast<WM, WN, TM, TN, false>), grid, dim3(256),                           \
               (GemmCfg<WM, WN, TM, TN>::lds_bytes()), st, wqs, wd, tile, n, nb, xqs,           \
               xd, m, bias, residual, out, ldo, part, p.bps, GateUpOut{})
-    if (p.bm == 64)
-        CALL(1, 4, 2, 1);
-    else
-        CALL(2, 2, 2, 2);
+        if (p.bm == 64)
+            CALL(1, 4, 2, 1);
+        else
+            CALL(2, 2, 2, 2);
 #undef CALL
-    if (part && want_part) return p.splits;
+        splits = p.splits;
+    }
+    if (part && want_part) return splits;
     if (part) {
         const size_t tot = (size_t)m * n;
         const auto al = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
         if (n % 4 == 0 && ldo % 4 == 0 && al(out) && al(bias) && al(residual))
             SI_LAUNCH(k_gemm_reduce4, dim3((unsigned)((tot / 4 + 255) / 256)), dim3(256),
-                      0, st, part, p.splits, m, n, bias, residual, out, ldo);
+                      0, st, part, splits, m, n, bias, residual, out, ldo);
         else
             SI_LAUNCH(k_gemm_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0,
-                      st, part, p.splits, m, n, bias, residual, out, ldo);
+                      st, part, splits, m, n, bias, residual, out, ldo);
     }
     return 0;
 }
@@ -674,8 +1120,15 @@ void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int
                            size_t ws_bytes, hipStream_t st) {
     if (m <= 0) return;
     const int n = 2 * f, nb = k / SI_QK;
-    const GemmPlan p = gemm_plan(m, n, nb);
-    if (exact || p.splits > 1) {
+    if (!exact && m <= BD_MAX_M && nb <= BD_MAX_CB) {
+        launch_bd(bd_plan(m, n, nb, 1), 1, wqs, wd, tile, n, nb, xqs, xd, m, nullptr, nullptr, gu,
+                  n, nullptr, GateUpOut{f, act, qs, d, s}, st);
+        return;
+    }
+    // m <= BD_MAX_M with a longer K: k_gemm_bd's K-range partials (or, with
+    // too little workspace, one pass into gu), then the split reduce
+    const bool split = exact || m <= BD_MAX_M || gemm_plan(m, n, nb).splits > 1;
+    if (split) {
         const int splits = gemm_core(wqs, wd, tile, n, k, xqs, xd, m, nullptr, nullptr, gu, n,
                                      exact, workspace, ws_bytes, true, st);
         if (splits > 1) {
@@ -687,6 +1140,7 @@ void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int
         }
         return;
     }
+    const GemmPlan p = gemm_plan(m, n, nb);
     const GateUpOut go{f, act, qs, d, s};
     const dim3 grid((n + p.bn - 1) / p.bn, (m + p.bm - 1) / p.bm, 1);
 #define CALL(WM, WN, TM, TN)                                                                   \

@@ -68,6 +68,8 @@ void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int
                            int8_t *qs, uint16_t *d, int16_t *s, bool exact, void *workspace,
                            size_t ws_bytes, hipStream_t st);
 size_t gemm_workspace_bytes(int m, int n, int k);
+// workspace launch_gemm_gateup_q8 uses for f features (0: never splits K)
+size_t gemm_gateup_workspace_bytes(int m, int f, int k);
 }  // namespace si
 namespace si {
 // A paged KV cache: sequence i's position p lives in pool row

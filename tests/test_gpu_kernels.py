@@ -340,6 +340,40 @@ def test_gemm_residual(oracle):
         close(got[r], res[r] + oracle.matvec(w, xq[r * nb:(r + 1) * nb], k, n), 1e-5, "res")
 
 
+@pytest.mark.parametrize("m,n,k,ldo", [
+    (64, 256, 512, 256),     # batched-decode GEMM, one column tile per workgroup
+    (33, 9000, 256, 9008),   # three or more tiles per workgroup, a ragged last tile, ldo > n
+    (5, 200, 3840, 200),     # K longer than one LDS range: range partials, then their sum
+])
+def test_gemm_bias_residual_batched(oracle, m, n, k, ldo):
+    """out = residual + (GEMM + bias) at m <= 64 rows (k_gemm_bd), every row
+    against the float64 product of the dequantized operands, with and
+    without workspace."""
+    torch = _torch()
+    rng = np.random.default_rng(m + n + k)
+    w = q4(oracle, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.normal(0, 0.02, n).astype(np.float32)
+    res = rng.standard_normal((m, ldo)).astype(np.float32)
+    xq = oracle.quantize_q8(x)
+    qs, d, _ = aos_to_planar(xq)
+    wqs, wd, tile = _upload_q4(w, n, k)
+    want = res[:, :n] + (dequant_q8(xq, m, k) @ dequant_q4(w, n, k).T + b)
+    rms = np.sqrt(np.mean(want ** 2))
+    wsb = si_amd.lib().si_gemm_workspace(m, n, k)
+    for ws_bytes in sorted({0, wsb}):
+        ws = empty(max(ws_bytes, 4), torch.uint8)
+        out = dev(np.full((m, ldo), 7.0, np.float32))
+        si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), tile, n, k,
+                    si_amd.ptr(dev(qs)), si_amd.ptr(dev(d.view(np.int16))), m, si_amd.ptr(dev(b)),
+                    si_amd.ptr(dev(res)), si_amd.ptr(out), ldo, 0,
+                    si_amd.ptr(ws) if ws_bytes else None, ws_bytes, None)
+        got = host(out).reshape(m, ldo)
+        err = np.abs(got[:, :n] - want).max() / rms
+        assert err <= 1e-5, f"workspace {ws_bytes}: worst {err:.3g}"
+        assert np.all(got[:, n:] == 7.0), "columns past n written"
+
+
 @pytest.mark.parametrize("shape,ntok,pos0", [("0.5b", 1, 1023), ("7b", 5, 0), ("7b", 3, 4093)])
 def test_rope_kv_append_bit_exact(oracle, shape, ntok, pos0):
     torch = _torch()
@@ -546,6 +580,8 @@ def test_ffn_gateup_q8(oracle, shape, flags):
     (300, 4864, 896, 32, si_amd.SI_GEMM_EXACT, True),
     (600, 4864, 896, 32, 0, True),       # past 512 rows: 128-row tiles
     (2048, 18944, 3584, 32, 0, True),    # 7B 2048-token prefill, the instance config 4 times
+    (33, 96, 3712, 8, 0, True),          # batched decode, the longest K of one LDS range
+    (64, 256, 4096, 32, 0, True),        # batched decode, longer K: range partials + reduce
 ])
 def test_gemm_gateup_q8(oracle, m, f, k, tile, flags, act_out):
     """gate|up GEMM with the SwiGLU + Q8_0 epilogue: every row's gate|up
