@@ -487,13 +487,13 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
 //   * a workgroup holds 32 activation rows of one K range (at most
 //     BD_MAX_CB blocks) in LDS for its whole life, filled once with
 //     coalesced loads, in MFMA operand order;
-//   * its 8 wavefronts share that range block by block (wavefront w takes
-//     blocks w, w + 8, ...) and stream their weights straight into
-//     registers P blocks ahead, with no barrier in the K loop, over a
-//     persistent walk of the workgroup's column tiles: the prefetch runs
-//     on across tiles;
-//   * at the end of a tile the 8 partial sums meet in LDS and are added in
-//     wavefront order (deterministic); wavefront w finishes output
+//   * its W wavefronts (8, or 12 = 3 per SIMD) share that range block by
+//     block (wavefront w takes blocks w, w + W, ...) and stream their
+//     weights straight into registers P blocks ahead, with no barrier in
+//     the K loop, over a persistent walk of the workgroup's column tiles:
+//     the prefetch runs on across tiles;
+//   * at the end of a tile the partial sums meet in LDS and are added in a
+//     fixed order (deterministic); wavefront w < 8 finishes output
 //     registers 2w and 2w + 1 of the 16 of every lane.
 // The two 32-row halves of a set of tiles run on the same XCD (blockIdx %
 // 8), so the second half's weight reads hit that XCD's L2.  Longer K is
@@ -518,8 +518,7 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
 // partials.  MODE 1 (TN = 2, gate|up, one K range): tile u pairs the gate
 // rows 32u..32u+31 with the up rows f+32u..; SwiGLU + Q8_0 epilogue as
 // k_gemm_fast's.
-constexpr int BD_W = 8;                                    // wavefronts per workgroup
-constexpr int BD_RED = BD_W * 16 * 64 * 4;                 // a 32x32 fp32 tile per wavefront
+constexpr int BD_RED = 8 * 16 * 64 * 4;                    // 8 partial 32x32 fp32 tiles
 constexpr int BD_LDS_MAX = 160 * 1024;                     // LDS of a gfx950 CU
 constexpr int BD_XST = 130;  // x.d row stride in halves: 65 dwords, odd, >= 128 blocks
 constexpr int BD_XBYTES = 32 * BD_XST * 2;
@@ -529,8 +528,6 @@ __host__ __device__ constexpr size_t bd_lds(int cb) {
     return (size_t)((cb + 3) & ~3) * 1024 + BD_XBYTES + BD_RED;
 }
 constexpr int BD_MAX_CB = (BD_LDS_MAX - BD_XBYTES - BD_RED) / 1024 & ~3;  // 116 blocks
-constexpr int BD_FILL = (BD_MAX_CB * 64 + 511) / 512;      // 16-byte fill pieces per thread
-constexpr int BD_XFILL = 32 * 128 / 512;                   // x.d fill values per thread
 
 typedef unsigned gv2u __attribute__((vector_size(8)));  // an 8-byte buffer load's value
 typedef int v2i __attribute__((ext_vector_type(2)));
@@ -561,13 +558,17 @@ __device__ __forceinline__ void bd_place(int id, int H, int S, int &h, int &q, i
     s = q - c * S;
 }
 
-template <int TN, int P, int MODE>
+template <int TN, int P, int MODE, int BD_W>
 __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
     const uint8_t *__restrict__ wqs, const uint16_t *__restrict__ wd, int tile, int n, int nb,
     const int8_t *__restrict__ xqs, const uint16_t *__restrict__ xd, int m,
     const float *__restrict__ bias, const float *__restrict__ residual, float *__restrict__ out,
     int ldo, float *__restrict__ part, int H, int C, int S, int cb, int units, GateUpOut go) {
     static_assert(MODE == 0 ? TN == 1 : TN == 2, "MODE 0 takes one tile, gate|up two");
+    static_assert(BD_W >= 8 && BD_W <= 12 && BD_W % 4 == 0, "8 or 12 wavefronts");
+    constexpr int BD_T = 64 * BD_W;                              // threads
+    constexpr int BD_FILL = (BD_MAX_CB * 64 + BD_T - 1) / BD_T;  // 16-byte fill pieces per thread
+    constexpr int BD_XFILL = (32 * 128 + BD_T - 1) / BD_T;       // x.d fill values per thread
     extern __shared__ __attribute__((aligned(16))) uint8_t bd_sm[];
     const int tid = threadIdx.x, lane = tid & 63;
     // the wavefront index as a scalar: block numbers derived from it are
@@ -590,6 +591,7 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
     const int per = (len + BD_W - 1) / BD_W;  // blocks per wavefront per tile (some may be past len)
     const int nu = s < units ? (units - 1 - s) / S + 1 : 0;
     const int total = nu * per;
+    if (total <= 0) return;  // no tile here: the whole workgroup
     const int ltile = __builtin_ctz((unsigned)tile);
     const __amdgpu_buffer_rsrc_t rb = buf_rsrc(wqs, (uint32_t)nb * n * 16);
     const __amdgpu_buffer_rsrc_t rw =
@@ -629,24 +631,10 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
         }
     };
 
-    // P blocks of weights in flight, requested before the fill so that
-    // their latency and the fill's overlap.  Loads retire in issue order,
-    // so each stage's loads stay together and in stage order (scheduling
-    // barriers), and every load is issued (a valid block past the end):
-    // the wait before a block then counts the same later loads on every
-    // path into it.
-    BdStage<TN> st[P];
-    if (total > 0) {
-#pragma unroll
-        for (int i = 0; i < P; ++i) {
-            load(st[i]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
     // bias and residual of up to two tiles are read before the K loop: a
     // load in the epilogue would wait for every weight load in flight
     float pb[2] = {0.0f, 0.0f}, pr[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
-    const bool pre = MODE == 0 && nu <= 2 && (bias || residual);
+    const bool pre = MODE == 0 && nu <= 2 && (bias || residual) && wave < 8;
     if (pre) {
 #pragma unroll
         for (int iu = 0; iu < 2; ++iu) {
@@ -661,54 +649,69 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
         }
     }
 
-    // ---- fill: the K range's 32 rows (clamped to m - 1) and their x.d
+    // ---- fill: the K range's 32 rows (clamped to m - 1) and their x.d.
+    // Loads retire in issue order: the fill's loads go first, then the
+    // first P blocks of weights, and the fill waits for its own loads only,
+    // while the weights stream in behind them.
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(xqs, (uint32_t)m * k);
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(xd, (uint32_t)m * nb * 2);
+    v4i fv[BD_FILL];
+    uint32_t xv[BD_XFILL];
+    // Q8: 8 threads read a row's 128 bytes (4 blocks), 8 rows per 64
+    // threads; a wavefront's pieces are 4 whole blocks, so whether they are
+    // stored is decided per wavefront (pieces past len read zero)
+#pragma unroll
+    for (int i = 0; i < BD_FILL; ++i) {
+        const int p = tid + BD_T * i, t8 = p & 7, ri = (p >> 3) & 31;
+        const int b = 4 * (p >> 8) + (t8 >> 1);
+        const int row = min(m0 + ri, m - 1);
+        const uint32_t off = b < len ? (uint32_t)row * k + (uint32_t)(b0 + b) * SI_QK + (t8 & 1) * 16
+                                     : 0x80000000u;  // past the end: zero, no access
+        fv[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
+    }
+    // x.d: 128 threads per row, consecutive blocks
+#pragma unroll
+    for (int i = 0; i < BD_XFILL; ++i) {
+        const int e = tid + BD_T * i, ri = e >> 7, b = e & 127;
+        const int row = min(m0 + ri, m - 1);
+        const uint32_t off = b < len && ri < 32 ? ((uint32_t)row * nb + b0 + b) * 2 : 0x80000000u;
+        xv[i] = __builtin_amdgcn_raw_buffer_load_b16(rx, off, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // P blocks of weights in flight; each stage's loads stay together and
+    // in stage order (scheduling barriers), and every load is issued (a
+    // valid block past the end): the wait before a block then counts the
+    // same later loads on every path into it
+    BdStage<TN> st[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        load(st[i]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // everything but the weight stages complete (lgkmcnt and expcnt free)
     {
-        const __amdgpu_buffer_rsrc_t ra = buf_rsrc(xqs, (uint32_t)m * k);
-        const __amdgpu_buffer_rsrc_t rx = buf_rsrc(xd, (uint32_t)m * nb * 2);
-        v4i fv[BD_FILL];
-        uint32_t xv[BD_XFILL];
-        // Q8: 8 threads read a row's 128 bytes (4 blocks), 8 rows per 64
-        // threads; a wavefront's pieces are 4 whole blocks, so whether they
-        // are stored is decided per wavefront (pieces past len read zero)
+        constexpr int VM = P * 2 * TN;  // weight loads issued after the fill
+        static_assert(VM <= 63, "vmcnt holds 6 bits");
+        __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
+    }
 #pragma unroll
-        for (int i = 0; i < BD_FILL; ++i) {
-            const int p = tid + 512 * i, t8 = p & 7, ri = (p >> 3) & 31;
-            const int b = 4 * (p >> 8) + (t8 >> 1);
-            const int row = min(m0 + ri, m - 1);
-            const uint32_t off = b < len ? (uint32_t)row * k + (uint32_t)(b0 + b) * SI_QK + (t8 & 1) * 16
-                                         : 0x80000000u;  // past the end: zero, no access
-            fv[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
+    for (int i = 0; i < BD_FILL; ++i) {
+        const int p4 = (tid >> 8) + (BD_T >> 8) * i;  // the wavefront's group of 4 blocks
+        if (4 * p4 < len) {
+            const int p = tid + BD_T * i, t8 = p & 7, ri = (p >> 3) & 31;
+            const int b = 4 * p4 + (t8 >> 1);
+            // 16 bytes = elements 16*part .. +15: bytes 0..7 go to half 0,
+            // bytes 8..15 to half 1, at offset 8*part of the row's slot
+            uint8_t *d = a_l + ((size_t)b * 64 + (ri ^ ((b & 3) << 1))) * 16 + (t8 & 1) * 8;
+            *(v2i *)d = (v2i){fv[i][0], fv[i][1]};
+            *(v2i *)(d + 512) = (v2i){fv[i][2], fv[i][3]};
         }
-        // x.d: 128 threads per row, consecutive blocks
+    }
 #pragma unroll
-        for (int i = 0; i < BD_XFILL; ++i) {
-            const int e = tid + 512 * i, ri = e >> 7, b = e & 127;
-            const int row = min(m0 + ri, m - 1);
-            const uint32_t off = b < len ? ((uint32_t)row * nb + b0 + b) * 2 : 0x80000000u;
-            xv[i] = __builtin_amdgcn_raw_buffer_load_b16(rx, off, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < BD_FILL; ++i) {
-            const int p4 = (tid >> 8) + 2 * i;  // the wavefront's group of 4 blocks
-            if (4 * p4 < len) {
-                const int p = tid + 512 * i, t8 = p & 7, ri = (p >> 3) & 31;
-                const int b = 4 * p4 + (t8 >> 1);
-                // 16 bytes = elements 16*part .. +15: bytes 0..7 go to half 0,
-                // bytes 8..15 to half 1, at offset 8*part of the row's slot
-                uint8_t *d = a_l + ((size_t)b * 64 + (ri ^ ((b & 3) << 1))) * 16 + (t8 & 1) * 8;
-                *(v2i *)d = (v2i){fv[i][0], fv[i][1]};
-                *(v2i *)(d + 512) = (v2i){fv[i][2], fv[i][3]};
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < BD_XFILL; ++i) {
-            const int e = tid + 512 * i;
+    for (int i = 0; i < BD_XFILL; ++i) {
+        const int e = tid + BD_T * i;
+        if (32 * 128 % BD_T == 0 || e < 32 * 128)  // whole wavefronts
             x_l[(e >> 7) * BD_XST + (e & 127)] = (uint16_t)xv[i];  // row padding takes b >= 128
-        }
-        // every load so far complete (the fill's skipped pieces included, so
-        // no register is left waiting on a load of this phase), the first
-        // weight stages with them: they are needed first anyway
-        __builtin_amdgcn_s_waitcnt(0);
     }
     lds_barrier();
 
@@ -748,24 +751,37 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
             for (int v = 0; v < 16; ++v) acc[u][v] = fmaf((float)dot[v], sc[v], acc[u][v]);
         }
     };
-    // a tile's 8 partials summed in wavefront order; wavefront w gets
-    // registers 2w and 2w + 1 (rows 8(w/2) + 4g + 2(w%2) + {0, 1})
-    auto reduce = [&](const float (&a)[16], float (&r)[2]) {
+    // a tile's partial sums added in a fixed order: wavefronts 8..11 hand
+    // theirs to 0..3, then the 8 sums meet in LDS ([w][register][lane]
+    // floats, so no register is repacked); wavefront w < 8 gets registers
+    // 2w and 2w + 1 (rows 8(w/2) + 4g + 2(w%2) + {0, 1})
+    float *redf = (float *)red;
+    auto reduce = [&](float (&t)[16], float (&r)[2]) {  // t: this wavefront's sums (consumed)
+        if (BD_W > 8) {
+            if (wave >= 8)
 #pragma unroll
-        for (int v4 = 0; v4 < 4; ++v4)
-            red[(wave * 4 + v4) * 64 + lane] =
-                make_float4(a[4 * v4], a[4 * v4 + 1], a[4 * v4 + 2], a[4 * v4 + 3]);
-        lds_barrier();
-        const float *rf = (const float *)red;
-        const int o = ((wave >> 1) * 64 + lane) * 4 + 2 * (wave & 1);
-        float2 t = *(const float2 *)(rf + o);
+                for (int v = 0; v < 16; ++v) redf[((wave - 8) * 16 + v) * 64 + lane] = t[v];
+            lds_barrier();
+            if (wave < BD_W - 8)
 #pragma unroll
-        for (int w = 1; w < BD_W; ++w) {
-            const float2 p = *(const float2 *)(rf + w * 1024 + o);
-            t = make_float2(__fadd_rn(t.x, p.x), __fadd_rn(t.y, p.y));
+                for (int v = 0; v < 16; ++v)
+                    t[v] = __fadd_rn(t[v], redf[(wave * 16 + v) * 64 + lane]);
+            lds_barrier();
         }
-        r[0] = t.x * 0.0625f;  // the 16x of the operands, exactly
-        r[1] = t.y * 0.0625f;
+        if (wave < 8)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) redf[(wave * 16 + v) * 64 + lane] = t[v];
+        lds_barrier();
+        if (wave < 8) {
+            float s0 = redf[(2 * wave) * 64 + lane], s1 = redf[(2 * wave + 1) * 64 + lane];
+#pragma unroll
+            for (int w = 1; w < 8; ++w) {
+                s0 = __fadd_rn(s0, redf[(w * 16 + 2 * wave) * 64 + lane]);
+                s1 = __fadd_rn(s1, redf[(w * 16 + 2 * wave + 1) * 64 + lane]);
+            }
+            r[0] = s0 * 0.0625f;  // the 16x of the operands, exactly
+            r[1] = s1 * 0.0625f;
+        }
         lds_barrier();  // the area is written again next
     };
     auto finish = [&](int iu) {
@@ -774,6 +790,7 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
         for (int u = 0; u < TN; ++u) reduce(acc[u], r[u]);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
+            if (wave >= 8) break;  // the partial sums only
             const int row = m0 + 8 * (wave >> 1) + 4 * g + 2 * (wave & 1) + i;
             if (MODE == 1) {
                 const int f = go.f, feat = col0(iu, 0) + j;
@@ -819,7 +836,7 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
             for (int v = 0; v < 16; ++v) acc[u][v] = 0.0f;
     };
 
-    if (total > 0) {
+    {
         fetch(0);
         int cu = 0, ck = 0;  // the compute pointer
         for (int it0 = 0; it0 < total; it0 += P) {
@@ -996,22 +1013,25 @@ static void launch_bd(const BdPlan &p, int mode, const uint8_t *wqs, const uint1
                       int tile, int n, int nb, const int8_t *xqs, const uint16_t *xd, int m,
                       const float *bias, const float *residual, float *out, int ldo, float *part,
                       const GateUpOut &go, hipStream_t st) {
-#define BD(TN, P, MODE)                                                                        \
+#define BD(TN, P, MODE, W)                                                                     \
     do {                                                                                       \
         static bool big_lds = false;                                                           \
         if (!big_lds) {                                                                        \
-            hipFuncSetAttribute((const void *)k_gemm_bd<TN, P, MODE>,                          \
+            hipFuncSetAttribute((const void *)k_gemm_bd<TN, P, MODE, W>,                       \
                                 hipFuncAttributeMaxDynamicSharedMemorySize, BD_LDS_MAX);       \
             big_lds = true;                                                                    \
         }                                                                                      \
-        SI_LAUNCH((k_gemm_bd<TN, P, MODE>), dim3(p.grid), dim3(64 * BD_W), p.lds, st, wqs, wd, \
+        SI_LAUNCH((k_gemm_bd<TN, P, MODE, W>), dim3(p.grid), dim3(64 * W), p.lds, st, wqs, wd, \
                   tile, n, nb, xqs, xd, m, bias, residual, out, ldo, part, p.H, p.C, p.S,      \
                   p.cb, p.units, go);                                                          \
     } while (0)
+    // gate|up: 12 wavefronts (3 per SIMD; 4 weight blocks in flight fit
+    // their registers); one tile: 8, whose even share of 112 blocks wastes
+    // no step, 16 blocks in flight
     if (mode == 1)
-        BD(2, 8, 1);
+        BD(2, 4, 1, 12);
     else
-        BD(1, 16, 0);
+        BD(1, 16, 0, 8);
 #undef BD
 }
 
