@@ -520,14 +520,16 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
 // k_gemm_fast's.
 constexpr int BD_RED = 8 * 16 * 64 * 4;                    // 8 partial 32x32 fp32 tiles
 constexpr int BD_LDS_MAX = 160 * 1024;                     // LDS of a gfx950 CU
-constexpr int BD_XST = 130;  // x.d row stride in halves: 65 dwords, odd, >= 128 blocks
-constexpr int BD_XBYTES = 32 * BD_XST * 2;
+// x.d row stride in halves for a K range of cb blocks: an odd number of
+// dwords, so the 32 rows' values of one block sit in 32 different banks
+__host__ __device__ constexpr int bd_xst(int cb) { return 2 * (((cb + 1) >> 1) | 1); }
 // LDS of a K range of cb blocks: Q8 rows (a multiple of 4 blocks), x.d
 // rows, partial tiles
 __host__ __device__ constexpr size_t bd_lds(int cb) {
-    return (size_t)((cb + 3) & ~3) * 1024 + BD_XBYTES + BD_RED;
+    return (size_t)((cb + 3) & ~3) * 1024 + 64 * (size_t)bd_xst(cb) + BD_RED;
 }
-constexpr int BD_MAX_CB = (BD_LDS_MAX - BD_XBYTES - BD_RED) / 1024 & ~3;  // 116 blocks
+constexpr int BD_MAX_CB = 120;
+static_assert(bd_lds(BD_MAX_CB) <= BD_LDS_MAX, "a K range fits a CU's LDS");
 
 typedef unsigned gv2u __attribute__((vector_size(8)));  // an 8-byte buffer load's value
 typedef int v2i __attribute__((ext_vector_type(2)));
@@ -582,10 +584,9 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
     const int k = nb * SI_QK;
     const int cb4 = (cb + 3) & ~3;
     uint8_t *a_l = bd_sm;  // [cb4][2][32][16 B]
-    // x.d rows of BD_XST halves, an odd number of dwords: the 32 rows'
-    // values of one block sit in 32 different banks
-    uint16_t *x_l = (uint16_t *)(bd_sm + (size_t)cb4 * 1024);               // [32][BD_XST]
-    float4 *red = (float4 *)(bd_sm + (size_t)cb4 * 1024 + BD_XBYTES);        // [8][4][64]
+    const int xst = bd_xst(cb);  // x.d row stride (halves)
+    uint16_t *x_l = (uint16_t *)(bd_sm + (size_t)cb4 * 1024);  // [32][xst]
+    float4 *red = (float4 *)(bd_sm + bd_lds(cb) - BD_RED);    // [8][16][64] floats
 
     // ---- the tiles of this workgroup: units s, s + S, ...
     const int per = (len + BD_W - 1) / BD_W;  // blocks per wavefront per tile (some may be past len)
@@ -710,8 +711,7 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
 #pragma unroll
     for (int i = 0; i < BD_XFILL; ++i) {
         const int e = tid + BD_T * i;
-        if (32 * 128 % BD_T == 0 || e < 32 * 128)  // whole wavefronts
-            x_l[(e >> 7) * BD_XST + (e & 127)] = (uint16_t)xv[i];  // row padding takes b >= 128
+        if ((e & 127) < len && e < 32 * 128) x_l[(e >> 7) * xst + (e & 127)] = (uint16_t)xv[i];
     }
     lds_barrier();
 
@@ -727,7 +727,7 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
     auto fetch = [&](int ck) {
         const int rel = min(BD_W * ck + wave, len - 1);
         a_nx = *(const v4i *)(a_l + (size_t)rel * 1024 + la);
-        x_nx = x_l[j * BD_XST + rel];
+        x_nx = x_l[j * xst + rel];
     };
     auto compute = [&](const BdStage<TN> &st, const v4i &aop, uint16_t xs) {
         // scale product x.d * w.d in the output layout: A carries x.d at

@@ -141,6 +141,12 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8_v4(const float *__restrict__
     const int r = blockIdx.x, tid = threadIdx.x, n4 = n / 4;
     const size_t base = (size_t)r * n;
     float v[NPT][4];
+    // the gain is read with the row, not after the reduction
+    float4 gv[NPT];
+#pragma unroll
+    for (int i = 0; i < NPT; ++i)
+        gv[i] = gain ? *(const float4 *)(gain + 4 * min(tid + 256 * i, n4 - 1))
+                     : make_float4(1.f, 1.f, 1.f, 1.f);
     double ss = 0.0;
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
@@ -185,8 +191,7 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8_v4(const float *__restrict__
     for (int i = 0; i < NPT; ++i) {
         const int c = tid + 256 * i;
         if (c < n4) {  // whole 8-thread groups (n is a multiple of 32)
-            const float4 gv = gain ? *(const float4 *)(gain + 4 * c) : make_float4(1.f, 1.f, 1.f, 1.f);
-            const float g4[4] = {gv.x, gv.y, gv.z, gv.w};
+            const float g4[4] = {gv[i].x, gv[i].y, gv[i].z, gv[i].w};
             float o[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) o[k] = __fmul_rn(__fmul_rn(v[i][k], inv), g4[k]);

@@ -343,7 +343,7 @@ def test_gemm_residual(oracle):
 @pytest.mark.parametrize("m,n,k,ldo", [
     (64, 256, 512, 256),     # batched-decode GEMM, one column tile per workgroup
     (33, 9000, 256, 9008),   # three or more tiles per workgroup, a ragged last tile, ldo > n
-    (5, 200, 3840, 200),     # K longer than one LDS range: range partials, then their sum
+    (5, 200, 3872, 200),     # K longer than one LDS range: range partials, then their sum
 ])
 def test_gemm_bias_residual_batched(oracle, m, n, k, ldo):
     """out = residual + (GEMM + bias) at m <= 64 rows (k_gemm_bd), every row
@@ -580,7 +580,7 @@ def test_ffn_gateup_q8(oracle, shape, flags):
     (300, 4864, 896, 32, si_amd.SI_GEMM_EXACT, True),
     (600, 4864, 896, 32, 0, True),       # past 512 rows: 128-row tiles
     (2048, 18944, 3584, 32, 0, True),    # 7B 2048-token prefill, the instance config 4 times
-    (33, 96, 3712, 8, 0, True),          # batched decode, the longest K of one LDS range
+    (33, 96, 3840, 8, 0, True),          # batched decode, the longest K of one LDS range
     (64, 256, 4096, 32, 0, True),        # batched decode, longer K: range partials + reduce
 ])
 def test_gemm_gateup_q8(oracle, m, f, k, tile, flags, act_out):
