@@ -8,8 +8,9 @@
 // the int8 matrix core produces the per-block int32 dots exactly, then the
 // fp32 epilogue applies both fp16 block scales:
 //     acc[m][n] += (float)dot * (x.d[m] * w.d[n])
-// The weights are staged once per tile as signed int8 (nibble - 8) so the
-// matrix core needs no offset correction.
+// The weights are staged once per tile as signed int8 (nibble - 8, or
+// 16*(nibble - 8) on the fast paths) so the matrix core needs no offset
+// correction.
 //
 // MFMA operand layout (32x32x32 i8): lane l supplies 16 int8 of row l%32 for
 // k-half l/32 of both A and B; output element (i, j) of a 32x32 tile lives in
@@ -162,7 +163,10 @@ __global__ void __launch_bounds__(256) k_gemm_q4q8(
 //     two blocks per stage keep the kernel under 168 VGPRs (3 waves per
 //     SIMD), which hides more latency than deeper stages do;
 //   * MFMA results are written to VGPRs (-amdgpu-mfma-vgpr-form), so the
-//     epilogue reads them without a v_accvgpr_read per element.
+//     epilogue reads them without a v_accvgpr_read per element;
+//   * the weights are staged as 16*(nibble - 8), three ALU ops per nibble
+//     word (see k_gemm_bd): the sums come out 16x, exactly, and are scaled
+//     by 1/16 in the epilogue.
 // Counters on the 7B gate|up GEMM (2048 x 37888 x 3584): the VALU is ~90%
 // busy, 73% of its instructions are the cvt + fma epilogue, the matrix
 // pipe ~33% (i8 and f16 MFMA 32 cycles each per 32x32 tile and block).
@@ -297,11 +301,13 @@ struct GemmStage {
                 const int row = p / G_KB, blk = p % G_KB;
                 const uint32_t w[4] = {(uint32_t)rb[i][0], (uint32_t)rb[i][1], (uint32_t)rb[i][2],
                                        (uint32_t)rb[i][3]};
+                // 16*(nibble - 8) as int8: (n ^ 8) in the byte's top nibble
+                // (the dots come out 16x, exactly; k_gemm_fast rescales)
                 uint32_t lo[4], hi[4];
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    lo[t] = nib_to_s8(w[t] & 0x0f0f0f0fu);
-                    hi[t] = nib_to_s8((w[t] >> 4) & 0x0f0f0f0fu);
+                    lo[t] = ((w[t] << 4) ^ 0x80808080u) & 0xf0f0f0f0u;
+                    hi[t] = (w[t] ^ 0x80808080u) & 0xf0f0f0f0u;
                 }
                 uint8_t *dst = b_l + (((size_t)buf * G_KB + blk) * BN + row) * G_ST;
                 *(uint4 *)dst = make_uint4(lo[0], lo[1], lo[2], lo[3]);
@@ -431,7 +437,7 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int row = m0 + (wm * TM + a) * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
-                const float gv = acc[a][0][v], uv = acc[a][TN - 1][v];
+                const float gv = acc[a][0][v] * 0.0625f, uv = acc[a][TN - 1][v] * 0.0625f;
                 // SwiGLU exactly as k_swiglu_q8, then the block's Q8_0 over
                 // the 32 lanes of this half (every lane takes part)
                 const float silu = __fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)));
@@ -467,9 +473,9 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
                 const int row = m0 + (wm * TM + a) * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
                 if (row >= m) continue;
                 if (part) {
-                    part[((size_t)blockIdx.z * m + row) * n + col] = acc[a][b][v];
+                    part[((size_t)blockIdx.z * m + row) * n + col] = acc[a][b][v] * 0.0625f;
                 } else {
-                    float y = acc[a][b][v] + bv;
+                    float y = acc[a][b][v] * 0.0625f + bv;
                     if (residual) y = __fadd_rn(residual[(size_t)row * ldo + col], y);
                     out[(size_t)row * ldo + col] = y;
                 }
