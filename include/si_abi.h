@@ -159,6 +159,7 @@ size_t si_gemm_workspace(int m, int n, int k);
  * gu ([m][2f] fp32) is written when given; it is required only where it is
  * the intermediate: SI_GEMM_EXACT, or a plan that splits K (si_gemm_workspace
  * (m, 2f, k) > 0) given less workspace than that.  act and bsum may be NULL.
+ * wqs, xqs, qs and act are 16-byte aligned.
  * flags: SI_GEMM_EXACT as for si_gemm_q4q8. */
 int si_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, int k,
                       const int8_t *xqs, const uint16_t *xd, int m, float *gu, float *act,

@@ -14,7 +14,7 @@
 #include <stdlib.h>
 #include <string.h>
 
-static void or_die(const char *what) {
+static __attribute__((noreturn)) void or_die(const char *what) {
     /* qwen_one_layer.c:26-28: errors are fail-stop. */
     fprintf(stderr, "oracle error: %s\n", what);
     exit(1);

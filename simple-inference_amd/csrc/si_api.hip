@@ -333,8 +333,9 @@ int si_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, i
                    "gemm_gateup: gu is the intermediate here (exact mode, or a K split "
                    "without its workspace)");
     }
-    SI_REQUIRE(((uintptr_t)wqs & 15) == 0 && ((uintptr_t)xqs & 15) == 0,
-               "gemm_gateup: wqs and xqs must be 16-byte aligned");
+    SI_REQUIRE(((uintptr_t)wqs & 15) == 0 && ((uintptr_t)xqs & 15) == 0 &&
+                   ((uintptr_t)qs & 15) == 0 && ((uintptr_t)act & 15) == 0,
+               "gemm_gateup: wqs, xqs, qs and act must be 16-byte aligned");
     SI_REQUIRE((flags & ~SI_GEMM_EXACT) == 0, "gemm_gateup: unknown flags %d", flags);
     launch_gemm_gateup_q8(wqs, wd, tile, f, k, xqs, xd, m, gu, act, qs, d, bsum,
                           (flags & SI_GEMM_EXACT) != 0, workspace, workspace ? ws_bytes : 0,

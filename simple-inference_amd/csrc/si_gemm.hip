@@ -430,35 +430,68 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
     // output (i, j) of a 32x32 tile: lane j + 32*((i/4)%2), register (i%4) + 4*(i/8)
     if (FUSE) {
         const int f = go.f;
-        const int feat = (n0 + wn * 64) / 2 + j;  // this lane's feature
-        const bool fok = feat < f;                // a 32-feature block is all in or all out
+        const int fb = (n0 + wn * 64) / 2;  // the wavefront's 32 features: one Q8 block
+        const bool fok = fb < f;            // the block is all in or all out
+        // SwiGLU exactly as k_swiglu_q8 per output; then each row's block is
+        // read back row-wise from this wavefront's LDS area, lanes l and
+        // l ^ 32 holding features 0..15 and 16..31 of row l & 31, and
+        // quantized with the same rules (quant_block_pair16): one scale
+        // division per block instead of one per output, no half-wave
+        // reductions per register, 16-byte stores
+        constexpr int FT = 36;  // floats per LDS row (16-byte aligned rows)
+        static_assert(4 * 32 * FT * 4 <= C::lds_bytes(), "the transposition fits the stage LDS");
+        float *tl = (float *)gsm + wave * (32 * FT);
+        const int rr = lane & 31, hh = lane >> 5;
 #pragma unroll
-        for (int a = 0; a < TM; ++a)
+        for (int a = 0; a < TM; ++a) {
+            const int r0 = m0 + (wm * TM + a) * 32;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const int row = m0 + (wm * TM + a) * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
+                const int i = 8 * (v >> 2) + 4 * g + (v & 3);
                 const float gv = acc[a][0][v] * 0.0625f, uv = acc[a][TN - 1][v] * 0.0625f;
-                // SwiGLU exactly as k_swiglu_q8, then the block's Q8_0 over
-                // the 32 lanes of this half (every lane takes part)
                 const float silu = __fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)));
-                const float av = __fmul_rn(silu, uv);
-                uint16_t dbits;
-                int bsum;
-                const int q = quant_block_lane(av, dbits, bsum);
-                if (row < m && fok) {
-                    const size_t o = (size_t)row * f + feat;
-                    if (out) {
-                        out[(size_t)row * ldo + feat] = gv;
-                        out[(size_t)row * ldo + f + feat] = uv;
-                    }
-                    if (go.act) go.act[o] = av;
-                    go.qs[o] = (int8_t)q;
-                    if (j == 0) {
-                        go.d[o / SI_QK] = dbits;
-                        if (go.s) go.s[o / SI_QK] = (int16_t)bsum;
-                    }
+                tl[i * FT + j] = __fmul_rn(silu, uv);
+                if (out && r0 + i < m && fok) {
+                    out[(size_t)(r0 + i) * ldo + fb + j] = gv;
+                    out[(size_t)(r0 + i) * ldo + f + fb + j] = uv;
                 }
             }
+            // the wavefront's own area: its LDS accesses complete in order
+            __builtin_amdgcn_wave_barrier();
+            float x[16];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float4 p = *(const float4 *)(tl + rr * FT + 16 * hh + 4 * t);
+                x[4 * t] = p.x;
+                x[4 * t + 1] = p.y;
+                x[4 * t + 2] = p.z;
+                x[4 * t + 3] = p.w;
+            }
+            __builtin_amdgcn_wave_barrier();  // the next tile rewrites the area
+            int q[16];
+            uint16_t dbits;
+            int bsum;
+            quant_block_pair16(x, q, dbits, bsum);
+            const int row = r0 + rr;
+            if (row < m && fok) {
+                const size_t o = (size_t)row * f + fb + 16 * hh;
+                if (go.act)
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        *(float4 *)(go.act + o + 4 * t) =
+                            make_float4(x[4 * t], x[4 * t + 1], x[4 * t + 2], x[4 * t + 3]);
+                uint32_t pk[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    pk[t] = (uint32_t)(q[4 * t] & 0xff) | (uint32_t)(q[4 * t + 1] & 0xff) << 8 |
+                            (uint32_t)(q[4 * t + 2] & 0xff) << 16 | (uint32_t)q[4 * t + 3] << 24;
+                *(uint4 *)(go.qs + o) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+                if (hh == 0) {
+                    go.d[o / SI_QK] = dbits;
+                    if (go.s) go.s[o / SI_QK] = (int16_t)bsum;
+                }
+            }
+        }
         return;
     }
 #pragma unroll
@@ -1023,8 +1056,9 @@ static void launch_bd(const BdPlan &p, int mode, const uint8_t *wqs, const uint1
     do {                                                                                       \
         static bool big_lds = false;                                                           \
         if (!big_lds) {                                                                        \
-            hipFuncSetAttribute((const void *)k_gemm_bd<TN, P, MODE, W>,                       \
-                                hipFuncAttributeMaxDynamicSharedMemorySize, BD_LDS_MAX);       \
+            /* a failure here surfaces as the launch's error */                                \
+            (void)hipFuncSetAttribute((const void *)k_gemm_bd<TN, P, MODE, W>,                 \
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, BD_LDS_MAX); \
             big_lds = true;                                                                    \
         }                                                                                      \
         SI_LAUNCH((k_gemm_bd<TN, P, MODE, W>), dim3(p.grid), dim3(64 * W), p.lds, st, wqs, wd, \
