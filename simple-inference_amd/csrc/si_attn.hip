@@ -370,9 +370,11 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(
 // ===========================================================================
 // Causal prefill attention (flash attention over 32 x 32 tiles).
 //
-// One workgroup owns one KV group and 32 consecutive query tokens; wavefront
-// w < per computes query head g*per + w for those tokens, so each K/V tile
-// staged in LDS serves the whole GQA group.  Per 32-position K/V tile a
+// One workgroup owns one KV group, 32 consecutive query tokens and NW of
+// the group's query heads (blockIdx.z picks which NW); wavefront w computes
+// one head for those tokens, so each K/V tile staged in LDS serves NW heads.
+// Fewer heads per workgroup give more, shorter workgroups where the tokens
+// alone would not fill the CUs.  Per 32-position K/V tile a
 // wavefront computes
 //     S^T[pos][tok] = K[pos][:] . Q[tok][:]          (v_mfma_f32_32x32x16_f16)
 // (Q split into fp16 hi + lo halves, each product done twice, for fp32-level
@@ -393,6 +395,7 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(
 // reduction indices to (slice, element) is exact.
 // ===========================================================================
 typedef float f16v __attribute__((ext_vector_type(16)));
+typedef int pf_v4i __attribute__((ext_vector_type(4)));
 
 constexpr int PF_T = 32;      // query tokens per workgroup, positions per K/V tile
 constexpr int PF_KPAD = 8;    // halves of padding per K row
@@ -414,7 +417,7 @@ struct PrefillLds {
 };
 
 template <int D, int NW>
-__global__ void __launch_bounds__(NW * 64) k_attn_prefill(
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) k_attn_prefill(
     const float *__restrict__ q, int ntok, int qheads, int kvheads, int pos0,
     const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, float scale,
     float *__restrict__ attn, int8_t *__restrict__ qs, uint16_t *__restrict__ qd,
@@ -454,8 +457,9 @@ __global__ void __launch_bounds__(NW * 64) k_attn_prefill(
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int t = lane & 31, hh = lane >> 5;
     const int per = qheads / kvheads;
-    const bool active = w < per;
-    const int h = g * per + (active ? w : 0);
+    const int hw = blockIdx.z * NW + w;  // head within the group
+    const bool active = hw < per;
+    const int h = g * per + (active ? hw : 0);
     const int tq = qt * PF_T + t;  // this lane's query token
     const int ptq = pos0 + tq;     // its position: it sees cache rows 0..ptq
     const int kvd = kvheads * D;
@@ -485,22 +489,23 @@ __global__ void __launch_bounds__(NW * 64) k_attn_prefill(
 
     // register staging of one K/V tile (rows clamped to `last`; the clamped
     // duplicates lie past every token's causal limit and are masked)
-    uint4 rk[KPT], rv[VPT][2];
+    // clang vectors, not uint4 structs: arrays of those stay in registers
+    pf_v4i rk[KPT], rv[VPT][2];
     auto load_tile = [&](int kv0) {
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int c = min(tid + NT * i, KPIECES - 1);
             const int r = c / (D / 8), e8 = c % (D / 8);
             const int pos = min(kv0 + r, last);
-            rk[i] = *(const uint4 *)(kc + (size_t)pos * kvd + (size_t)g * D + 8 * e8);
+            rk[i] = *(const pf_v4i *)(kc + (size_t)pos * kvd + (size_t)g * D + 8 * e8);
         }
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const int c = min(tid + NT * i, VITEMS - 1);
             const int pr = c % (PF_T / 2), e8 = c / (PF_T / 2);
             const int p0 = min(kv0 + 2 * pr, last), p1 = min(kv0 + 2 * pr + 1, last);
-            rv[i][0] = *(const uint4 *)(vc + (size_t)p0 * kvd + (size_t)g * D + 8 * e8);
-            rv[i][1] = *(const uint4 *)(vc + (size_t)p1 * kvd + (size_t)g * D + 8 * e8);
+            rv[i][0] = *(const pf_v4i *)(vc + (size_t)p0 * kvd + (size_t)g * D + 8 * e8);
+            rv[i][1] = *(const pf_v4i *)(vc + (size_t)p1 * kvd + (size_t)g * D + 8 * e8);
         }
     };
     auto store_tile = [&]() {
@@ -509,7 +514,7 @@ __global__ void __launch_bounds__(NW * 64) k_attn_prefill(
             const int c = tid + NT * i;
             if (KPIECES % NT == 0 || c < KPIECES) {
                 const int r = c / (D / 8), e8 = c % (D / 8);
-                *(uint4 *)(k_l + r * Lds::KROW + 8 * e8) = rk[i];
+                *(pf_v4i *)(k_l + r * Lds::KROW + 8 * e8) = rk[i];
             }
         }
 #pragma unroll
@@ -519,8 +524,10 @@ __global__ void __launch_bounds__(NW * 64) k_attn_prefill(
                 // position pairs fastest: with 18-dword V^T rows the 64
                 // lanes' 4-byte writes hit 64 distinct banks
                 const int pr = c % (PF_T / 2), e8 = c / (PF_T / 2);
-                const uint32_t a[4] = {rv[i][0].x, rv[i][0].y, rv[i][0].z, rv[i][0].w};
-                const uint32_t b[4] = {rv[i][1].x, rv[i][1].y, rv[i][1].z, rv[i][1].w};
+                const uint32_t a[4] = {(uint32_t)rv[i][0][0], (uint32_t)rv[i][0][1],
+                                       (uint32_t)rv[i][0][2], (uint32_t)rv[i][0][3]};
+                const uint32_t b[4] = {(uint32_t)rv[i][1][0], (uint32_t)rv[i][1][1],
+                                       (uint32_t)rv[i][1][2], (uint32_t)rv[i][1][3]};
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     // dims 8*e8 + 2j (low halves) and + 2j + 1 (high halves)
@@ -543,7 +550,10 @@ __global__ void __launch_bounds__(NW * 64) k_attn_prefill(
         const int kv0 = it * PF_T;
         store_tile();
         __syncthreads();
-        if (it + 1 < it1) load_tile(kv0 + PF_T);  // next tile in flight
+        // next tile in flight, unconditionally (the last iteration re-reads
+        // its own rows): a conditional load keeps the staging registers in
+        // scratch memory and waits for every load
+        load_tile(min(kv0 + PF_T, (it1 - 1) * PF_T));
         if (active) {
             // scores S^T[pos = kv0 + i][tok = t]
             f16v sh = (f16v){}, sl = (f16v){};  // two independent MFMA chains
@@ -699,17 +709,27 @@ void launch_attn_prefill(const float *q, int ntok, int qheads, int kvheads, int 
         sp.ws_l = sp.ws_m + np;
         sp.ws_o = sp.ws_l + np;
     }
-    const dim3 grid(2 * sp.nsplit + sp.qsplit, kvheads);
+    // heads per workgroup: the group's (up to 16), halved while the grid has
+    // fewer than ~2 workgroups per CU (down to 2 heads for hdim >= 96, whose
+    // one-wavefront workgroups would spill registers)
+    const int units = 2 * sp.nsplit + sp.qsplit;
+    const int nw_min = hdim >= 96 ? 2 : 1;
+    int nw = per <= 8 ? 8 : 16;
+    while (nw > nw_min && (size_t)units * kvheads * ((per + nw - 1) / nw) < 512) nw /= 2;
+    const dim3 grid(units, kvheads, (per + nw - 1) / nw);
     const float scale = 1.0f / sqrtf((float)hdim);  // attention_kernels.h:86
 #define PF_CALL(DIM, NW)                                                                      \
     SI_LAUNCH((k_attn_prefill<DIM, NW>), grid, dim3(NW * 64),                                 \
               (PrefillLds<DIM, NW>::bytes()), st, q, ntok, qheads, kvheads, pos0, kc,         \
               vc, scale, attn, qs, qd, bsum, sp)
 #define PF_DIM(DIM)                     \
-    if (per <= 8)                       \
-        PF_CALL(DIM, 8);                \
-    else                                \
-        PF_CALL(DIM, 16);
+    switch (nw) {                       \
+        case 1: PF_CALL(DIM, 1); break; \
+        case 2: PF_CALL(DIM, 2); break; \
+        case 4: PF_CALL(DIM, 4); break; \
+        case 8: PF_CALL(DIM, 8); break; \
+        default: PF_CALL(DIM, 16);      \
+    }
     switch (hdim) {
         case 32: PF_DIM(32); break;
         case 64: PF_DIM(64); break;
