@@ -709,12 +709,13 @@ void launch_attn_prefill(const float *q, int ntok, int qheads, int kvheads, int 
         sp.ws_l = sp.ws_m + np;
         sp.ws_o = sp.ws_l + np;
     }
-    // heads per workgroup: the group's (up to 16), halved while the grid has
-    // fewer than ~2 workgroups per CU (down to 2 heads for hdim >= 96, whose
-    // one-wavefront workgroups would spill registers)
+    // heads per workgroup: up to 8 (a wider group takes several
+    // workgroups), halved while the grid has fewer than ~2 workgroups per CU
+    // (down to 2 heads for hdim >= 96, whose one-wavefront workgroups would
+    // spill registers)
     const int units = 2 * sp.nsplit + sp.qsplit;
     const int nw_min = hdim >= 96 ? 2 : 1;
-    int nw = per <= 8 ? 8 : 16;
+    int nw = 8;
     while (nw > nw_min && (size_t)units * kvheads * ((per + nw - 1) / nw) < 512) nw /= 2;
     const dim3 grid(units, kvheads, (per + nw - 1) / nw);
     const float scale = 1.0f / sqrtf((float)hdim);  // attention_kernels.h:86
@@ -727,8 +728,7 @@ void launch_attn_prefill(const float *q, int ntok, int qheads, int kvheads, int 
         case 1: PF_CALL(DIM, 1); break; \
         case 2: PF_CALL(DIM, 2); break; \
         case 4: PF_CALL(DIM, 4); break; \
-        case 8: PF_CALL(DIM, 8); break; \
-        default: PF_CALL(DIM, 16);      \
+        default: PF_CALL(DIM, 8);       \
     }
     switch (hdim) {
         case 32: PF_DIM(32); break;

@@ -464,12 +464,19 @@ def test_attention_batched_sequences(oracle):
         close(got[i], want, 2e-3, f"seq {i}")
 
 
-@pytest.mark.parametrize("shape,ntok,prefix", [("0.5b", 40, 300), ("7b", 45, 17)])
+# query heads per KV group beyond one workgroup's 8 (two head subsets) and
+# an odd group width, besides the BASELINE shapes
+_WIDE_GROUPS = {"wide16": dict(hidden=2048, qheads=32, kvheads=2, hdim=64),
+                "odd3": dict(hidden=1152, qheads=9, kvheads=3, hdim=128)}
+
+
+@pytest.mark.parametrize("shape,ntok,prefix", [("0.5b", 40, 300), ("7b", 45, 17),
+                                               ("wide16", 70, 33), ("odd3", 33, 64)])
 def test_attention_causal_prefill(oracle, shape, ntok, prefix):
     """nq query rows over one cache (the flash prefill kernel): row t attends
     to prefix+t+1 positions; every row and its Q8_0."""
     torch = _torch()
-    sd = si_amd.SHAPES[shape]
+    sd = si_amd.SHAPES.get(shape) or _WIDE_GROUPS[shape]
     s, os_ = si_amd.make_shape(**sd), or_shape(**sd)
     KVD, QD = s.kvheads * s.hdim, s.qheads * s.hdim
     rng = np.random.default_rng(7)
