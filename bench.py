@@ -49,8 +49,8 @@ PMC_KIB = {
     ("2", "k_dec_gateup<64, 512, false>"): (2530.9, 9.8),
     ("2", "k_matvec<8, 512, false>"): (1256.0, 3.5),
     ("2", "k_dec_qkv<8, 512, false>"): (596.5, 4.5),
-    ("3", "k_gemm_fast<2, 2, 1, 2, true>"): (6867.5, 4800.1),
-    ("4", "k_gemm_fast<2, 2, 2, 2, true>"): (626132.8, 75966.6),
+    ("3", "k_gemm_fast<2, 2, 1, 2, true>"): (6800.5, 4800.0),
+    ("4", "k_gemm_fast<2, 2, 2, 2, true>"): (626739.1, 75937.2),
     ("5", "k_dec_attn_rows<128, 4, false, false>"): (266834.6, 8192.0),
 }
 FETCH_SCALE, WRITE_SCALE = 2.000, 1.000
