@@ -526,7 +526,7 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
 //   * a workgroup holds 32 activation rows of one K range (at most
 //     BD_MAX_CB blocks) in LDS for its whole life, filled once with
 //     coalesced loads, in MFMA operand order;
-//   * its W wavefronts (8, or 12 = 3 per SIMD) share that range block by
+//   * its W wavefronts (8, 12 or 16: 2-4 per SIMD) share that range block by
 //     block (wavefront w takes blocks w, w + W, ...) and stream their
 //     weights straight into registers P blocks ahead, with no barrier in
 //     the K loop, over a persistent walk of the workgroup's column tiles:
@@ -606,7 +606,7 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
     const float *__restrict__ bias, const float *__restrict__ residual, float *__restrict__ out,
     int ldo, float *__restrict__ part, int H, int C, int S, int cb, int units, GateUpOut go) {
     static_assert(MODE == 0 ? TN == 1 : TN == 2, "MODE 0 takes one tile, gate|up two");
-    static_assert(BD_W >= 8 && BD_W <= 12 && BD_W % 4 == 0, "8 or 12 wavefronts");
+    static_assert(BD_W >= 8 && BD_W <= 16 && BD_W % 4 == 0, "8, 12 or 16 wavefronts");
     constexpr int BD_T = 64 * BD_W;                              // threads
     constexpr int BD_FILL = (BD_MAX_CB * 64 + BD_T - 1) / BD_T;  // 16-byte fill pieces per thread
     constexpr int BD_XFILL = (32 * 128 + BD_T - 1) / BD_T;       // x.d fill values per thread
@@ -790,8 +790,8 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
             for (int v = 0; v < 16; ++v) acc[u][v] = fmaf((float)dot[v], sc[v], acc[u][v]);
         }
     };
-    // a tile's partial sums added in a fixed order: wavefronts 8..11 hand
-    // theirs to 0..3, then the 8 sums meet in LDS ([w][register][lane]
+    // a tile's partial sums added in a fixed order: wavefronts 8..W-1 hand
+    // theirs to 0..W-9, then the 8 sums meet in LDS ([w][register][lane]
     // floats, so no register is repacked); wavefront w < 8 gets registers
     // 2w and 2w + 1 (rows 8(w/2) + 4g + 2(w%2) + {0, 1})
     float *redf = (float *)red;
@@ -1066,12 +1066,13 @@ static void launch_bd(const BdPlan &p, int mode, const uint8_t *wqs, const uint1
                   p.cb, p.units, go);                                                          \
     } while (0)
     // gate|up: 12 wavefronts (3 per SIMD; 4 weight blocks in flight fit
-    // their registers); one tile: 8, whose even share of 112 blocks wastes
-    // no step, 16 blocks in flight
+    // their registers); one tile: 16 (4 per SIMD, 7 of 112 blocks each, 4
+    // in flight; 8 wavefronts with 16 in flight took 56 us for QKV + O +
+    // down at 7B x 64 rows, 16 with 2, 4, 6 or 8 in flight 50-54 us)
     if (mode == 1)
         BD(2, 4, 1, 12);
     else
-        BD(1, 16, 0, 8);
+        BD(1, 4, 0, 16);
 #undef BD
 }
 
