@@ -49,6 +49,12 @@ def test_argument_errors_do_not_launch():
     assert L.si_gemm_gateup_q8(None, None, 8, 64, 64, None, None, 4, None, None, None, None,
                                None, 0, None, 0, None) == si_amd.SI_ERR_ARG  # NULL
     assert b"NULL" in L.si_last_error()
+    # a q output off 16-byte alignment (the epilogue stores 16 bytes); the
+    # pointers are never dereferenced: the call is refused first
+    a16, odd = 1 << 12, (1 << 12) + 4
+    assert L.si_gemm_gateup_q8(a16, a16, 8, 64, 64, a16, a16, 4, a16, None, odd, a16, None, 0,
+                               None, 0, None) == si_amd.SI_ERR_ARG
+    assert b"16-byte aligned" in L.si_last_error()
     assert L.si_gemm_q4q8(None, None, 8, 1 << 20, 8192, None, None, 4, None, None, None,
                           1 << 20, 0, None, 0, None) == si_amd.SI_ERR_ARG
     assert b"2 GiB" in L.si_last_error()
