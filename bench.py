@@ -152,6 +152,8 @@ def roofline_entry(kernel, us, work, bound, cfg, launches):
 
 
 DECODE_PHASES = ["qkv", "attention", "out_proj", "gate_up", "down"]
+# a small layer projects Q|K|V inside its attention kernel (k_dec_attn<..., true>)
+DECODE_PHASES_FUSED = ["qkv_attention", "out_proj", "gate_up", "down"]
 
 
 def decode_kernel_work(s, ctx, nseq=1):
@@ -165,7 +167,7 @@ def decode_kernel_work(s, ctx, nseq=1):
     NQKV = QD + 2 * KVD
     q4 = lambda n, k: n * k // 32 * 18  # noqa: E731
     q8 = lambda k: k + (k // 32) * 4  # noqa: E731  values, fp16 scale, int16 sum
-    return {
+    work = {
         "qkv": q4(NQKV, H) + nseq * (H * 4) + H * 4 + NQKV * 4 + nseq * NQKV * 4,
         "attention": nseq * ((ctx - 1) * KVD * 2 * 2 + KVD * 2 * 2 + NQKV * 4 + QD * 4)
                      + s.hdim * 4,
@@ -173,6 +175,9 @@ def decode_kernel_work(s, ctx, nseq=1):
         "gate_up": q4(2 * F, H) + nseq * (H * 4 + q8(F)) + H * 4,
         "down": q4(H, F) + nseq * (q8(F) + H * 4 + H * 4),
     }
+    # the fused kernel: both, without the q|k|v row written and read back
+    work["qkv_attention"] = work["qkv"] + work["attention"] - 2 * nseq * NQKV * 4
+    return work
 
 
 class _DevArray:
@@ -257,15 +262,16 @@ def bench_decode_layer(torch, si_amd, stream, steps, warmup, ctx=1024, shape_nam
                 acc[k] = acc.get(k, 0.0) + v / 20
         layers[0].set_timing(False)
         torch.cuda.synchronize()
-        # per-dispatch durations of the five kernels over min(steps, 200)
+        # per-dispatch durations of the step's kernels over min(steps, 200)
         # eager steps (the same rotation of copies), by position in the step
         nk = min(steps, 200)
         seq = kernel_sequence(si_amd, lambda: [step(i) for i in range(nk)],
                               "k_dec_|k_matvec<")
         torch.cuda.synchronize()
-    per = len(DECODE_PHASES)
+    phases = DECODE_PHASES_FUSED if len(seq) == len(DECODE_PHASES_FUSED) * nk else DECODE_PHASES
+    per = len(phases)
     assert len(seq) == per * nk, f"{len(seq)} timed launches for {nk} steps"
-    kern = {ph: (seq[j][0], [us for _, us in seq[j::per]]) for j, ph in enumerate(DECODE_PHASES)}
+    kern = {ph: (seq[j][0], [us for _, us in seq[j::per]]) for j, ph in enumerate(phases)}
     # timed region: exactly `steps` decode steps, captured as one HIP graph
     ms = graph_time_ms(torch, stream, step, steps, replays=3)
     alg = per_copy

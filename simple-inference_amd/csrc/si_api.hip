@@ -1011,12 +1011,19 @@ static int run_decode(si_layer *L, const float *x, uint16_t *kc, uint16_t *vc, i
     const bool cap = (flags & SI_LAYER_CAPTURE) != 0;
     SI_REQUIRE(!full || L->ffn, "layer has no FFN weights: use SI_LAYER_ATTN_ONLY");
     for (bool &h : L->phase_hit) h = false;
-    // qwen_one_layer.c:247-258: RMSNorm -> Q8 -> Q, K, V (+bias)
-    mark(L, SI_PHASE_QKV, st);
-    launch_dec_qkv(x, L->norm, H, s.rms_eps, L->wqkv.qs, L->wqkv.d, L->wqkv.tile, NQKV, L->bqkv,
-                   capt(cap, L->normed), capt(cap, L->xq.qs), capt(cap, L->xq.d),
-                   capt(cap, L->xq.s), L->qkv, exact, st);
-    if (flags & SI_LAYER_ATTN_STANDARD) {
+    const bool standard = (flags & SI_LAYER_ATTN_STANDARD) != 0;
+    // a small layer projects Q|K|V inside the attention kernel (no q|k|v
+    // round trip); the exact projections and standard attention take the
+    // staged kernels
+    const bool fused_qkv = !exact && !standard && dec_qkv_attn_ok(H, s.qheads, s.kvheads, s.hdim);
+    if (!fused_qkv) {
+        // qwen_one_layer.c:247-258: RMSNorm -> Q8 -> Q, K, V (+bias)
+        mark(L, SI_PHASE_QKV, st);
+        launch_dec_qkv(x, L->norm, H, s.rms_eps, L->wqkv.qs, L->wqkv.d, L->wqkv.tile, NQKV,
+                       L->bqkv, capt(cap, L->normed), capt(cap, L->xq.qs), capt(cap, L->xq.d),
+                       capt(cap, L->xq.s), L->qkv, exact, st);
+    }
+    if (standard) {
         // the reference's staged order with attention_standard
         // (qwen_one_layer.c:260-275, attention_kernels.h:33-78)
         mark(L, SI_PHASE_ROPE_KV, st);
@@ -1039,9 +1046,29 @@ static int run_decode(si_layer *L, const float *x, uint16_t *kc, uint16_t *vc, i
     // :260-270: RoPE, fp16 K/V append at context-1, attention over the cache
     mark(L, SI_PHASE_ATTENTION_Q8, st);
     const int ns = dec_attn_chunks(s.qheads, s.kvheads, s.hdim, 1, ctx);
-    launch_dec_attn(L->qkv, NQKV, 1, s.qheads, s.kvheads, s.hdim, L->rope_cos, L->rope_sin, kc,
-                    vc, 0, nullptr, ctx, ctx, capt(cap, L->q), ns, L->attn_ws, nullptr, nullptr,
-                    nullptr, nullptr, st);
+    if (fused_qkv) {
+        DecQkvIn fq;
+        fq.x = x;
+        fq.gain = L->norm;
+        fq.hidden = H;
+        fq.eps = s.rms_eps;
+        fq.wqs = L->wqkv.qs;
+        fq.wd = L->wqkv.d;
+        fq.tile = L->wqkv.tile;
+        fq.n = NQKV;
+        fq.bias = L->bqkv;
+        fq.cap_normed = capt(cap, L->normed);
+        fq.cap_qs = capt(cap, L->xq.qs);
+        fq.cap_d = capt(cap, L->xq.d);
+        fq.cap_s = capt(cap, L->xq.s);
+        fq.cap_qkv = capt(cap, L->qkv);
+        launch_dec_qkv_attn(fq, s.qheads, s.kvheads, s.hdim, L->rope_cos, L->rope_sin, kc, vc,
+                            ctx, ns, capt(cap, L->q), L->attn_ws, st);
+    } else {
+        launch_dec_attn(L->qkv, NQKV, 1, s.qheads, s.kvheads, s.hdim, L->rope_cos, L->rope_sin,
+                        kc, vc, 0, nullptr, ctx, ctx, capt(cap, L->q), ns, L->attn_ws, nullptr,
+                        nullptr, nullptr, nullptr, st);
+    }
     // :272-275: Q8 of the attention output, W_O (no bias); + x in the full layer
     mark(L, SI_PHASE_OUT_PROJ, st);
     const float *pm = (const float *)L->attn_ws;

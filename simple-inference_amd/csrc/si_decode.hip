@@ -420,17 +420,33 @@ struct AttnLds {
     }
 };
 
+// LDS of the fused QKV prologue (FQ), after the attention's own: the
+// norm's scratch, the three mat-vecs' partial sums, the normalised Q8 row.
+template <int D, int NW>
+struct FqLds {
+    static constexpr int RED = red_floats<D, NW * 64>();
+    static constexpr size_t bytes(int hidden) {
+        return 16 * 8 + (size_t)3 * RED * 4 + (size_t)(hidden / 32) * 4 + 16 + hidden;
+    }
+};
+
 // DEPTH: K/V tiles in flight per wavefront; 1 when every wavefront has at
 // most one tile (single queries: more chunks, a shorter chain), else 2 (3
-// measured no faster).
-template <int D, int NW, bool FINAL, bool PAGED, int DEPTH>
+// measured no faster).  FQ: single-token decode with the Q|K|V projection
+// inside (a workgroup per (chunk, query head): RMSNorm -> Q8 of the layer
+// input, then the head's q rows and its group's k and v rows of the fused
+// matrix, + bias), for a small model whose 3*hdim rows a workgroup streams
+// quickly; the k_dec_qkv launch and the q|k|v round trip through memory
+// disappear, at the price of every chunk recomputing its head's rows.
+template <int D, int NW, bool FINAL, bool PAGED, int DEPTH, bool FQ = false>
 __global__ void __launch_bounds__(NW * 64) k_dec_attn(
     const float *__restrict__ qkv, int ldqkv, int qheads, int kvheads,
     const float *__restrict__ rc, const float *__restrict__ rs, uint16_t *__restrict__ kc,
     uint16_t *__restrict__ vc, size_t kv_seq_stride, const int *__restrict__ ctx_dev, int ctx0,
     int max_ctx, int chunk, float scale, float *__restrict__ q_cap, float *__restrict__ ws_m,
     float *__restrict__ ws_l, float *__restrict__ ws_o, float *__restrict__ attn,
-    int8_t *__restrict__ aqs, uint16_t *__restrict__ ad, int16_t *__restrict__ as, KvPages pg) {
+    int8_t *__restrict__ aqs, uint16_t *__restrict__ ad, int16_t *__restrict__ as, KvPages pg,
+    DecQkvIn fq) {
     constexpr int KS = D / 32, DT = D / 16, HALF = D / 2;
     constexpr int VROW = AttnLds<D, NW>::VROW;
     constexpr int VL = DA_TILE * D / (64 * 8);  // 16-byte V pieces per lane per tile
@@ -440,10 +456,14 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
     char *big = smem + 2 * D * 2;
     _Float16 *vbuf = (_Float16 *)big;
 
-    const int sp = blockIdx.x, g = blockIdx.y, qi = blockIdx.z, ns = gridDim.x;
+    const int sp = blockIdx.x, qi = FQ ? 0 : blockIdx.z, ns = gridDim.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int per = qheads / kvheads;
+    // this workgroup's query heads: hbase .. hbase + nh - 1, of group g
+    const int g = FQ ? (int)blockIdx.y / per : (int)blockIdx.y;
+    const int nh = FQ ? 1 : per;
+    const int hbase = FQ ? (int)blockIdx.y : g * per;
     const int qd = qheads * D, kvd = kvheads * D;
     int ctx = ctx_dev ? ctx_dev[qi] : ctx0;
     ctx = min(ctx, max_ctx);
@@ -498,45 +518,105 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
     // Requests in the order they are consumed (loads retire in issue order):
     // 1. the group's raw q rows, the raw K and V rows of the new token and
     //    the RoPE row at its position, one or a few floats per thread;
-    float *qraw = (float *)big;   // [per][D]; these LDS rows are reused for
-    float *kraw = qraw + per * D; // the V tiles once Q is in registers
+    float *qraw = (float *)big;   // [nh][D]; these LDS rows are reused for
+    float *kraw = qraw + nh * D;  // the V tiles once Q is in registers
     float *vraw = kraw + D;
     float *csr = vraw + D;        // [HALF] cos, then [HALF] sin
-    const int nraw = per * D + 3 * D;
-    constexpr int RAWPT = (16 * D + 3 * D + NW * 64 - 1) / (NW * 64);
-    float rv[RAWPT];
-#pragma unroll
-    for (int u = 0; u < RAWPT; ++u) {  // branch-free: clamped index
-        const int i = min(tid + u * NW * 64, nraw - 1);
-        {
-            const float *src;
-            if (i < per * D)
-                src = row + (size_t)g * per * D + i;
-            else if (i < per * D + D)
-                src = row + qd + g * D + (i - per * D);
-            else if (i < per * D + 2 * D)
-                src = row + qd + kvd + g * D + (i - per * D - D);
-            else {
-                const int j = i - per * D - 2 * D;
-                src = j < HALF ? cr + j : sr + (j - HALF);
-            }
-            rv[u] = *src;
-        }
-    }
-    // 2. the wavefront's first DEPTH K and V tiles (that many in flight
-    //    throughout)
     constexpr int STEP = DA_TILE * NW;
     int t0 = p0 + DA_TILE * wave;
     uint4 kr[DEPTH][KS], vr[DEPTH][VL];
+    if constexpr (FQ) {
+        // 1. the layer input and gain, the rows' weights, bias and RoPE
+        //    row, 2. the first K and V tiles; then the Q8 row in LDS and
+        //    the three mat-vecs (their sums meet in separate LDS areas)
+        constexpr int NT = NW * 64;
+        using F = FqLds<D, NW>;
+        char *fx = smem + ((AttnLds<D, NW>::bytes(1) + 15) & ~(size_t)15);
+        double *dscr = (double *)fx;
+        float *red = (float *)(fx + 16 * 8);
+        const int nb = fq.hidden / SI_QK;
+        Q8Lds xq;
+        xq.d = (uint16_t *)(red + 3 * F::RED);
+        xq.s = (int16_t *)(xq.d + nb);
+        xq.qs = (int8_t *)(xq.s + nb + (8 - (2 * nb) % 8) % 8);  // 16-byte aligned
+        NormQ8Prologue<NT> pro(fq.x, fq.gain, fq.hidden);
+        pro.load();
+        GemvRows<D, NT, false, RowIdentity, DEC_U> wq(fq.wqs, fq.wd, fq.tile, fq.n, fq.n, nb,
+                                                     hbase * D, RowIdentity{});
+        GemvRows<D, NT, false, RowIdentity, DEC_U> wk(fq.wqs, fq.wd, fq.tile, fq.n, fq.n, nb,
+                                                     qd + g * D, RowIdentity{});
+        GemvRows<D, NT, false, RowIdentity, DEC_U> wv(fq.wqs, fq.wd, fq.tile, fq.n, fq.n, nb,
+                                                     qd + kvd + g * D, RowIdentity{});
+        wq.start();
+        wk.start();
+        wv.start();
+        const int e = min(tid, D - 1);
+        const float cs = e < HALF ? cr[e] : sr[e - HALF];
+        float bq = 0.0f, bk = 0.0f, bv = 0.0f;
+        if (fq.bias) {
+            bq = fq.bias[hbase * D + e];
+            bk = fq.bias[qd + g * D + e];
+            bv = fq.bias[qd + kvd + g * D + e];
+        }
 #pragma unroll
-    for (int b = 0; b < DEPTH; ++b) {
-        load_k(t0 + b * STEP, kr[b]);
-        load_v(t0 + b * STEP, vr[b]);
-    }
+        for (int b = 0; b < DEPTH; ++b) {
+            load_k(t0 + b * STEP, kr[b]);
+            load_v(t0 + b * STEP, vr[b]);
+        }
+        const bool c0 = blockIdx.y == 0;  // (workgroup (0, 0) writes the row captures)
+        pro.run(fq.eps, xq, dscr, c0 ? fq.cap_normed : nullptr, c0 ? fq.cap_qs : nullptr,
+                c0 ? fq.cap_d : nullptr, c0 ? fq.cap_s : nullptr);
+        const Q8Row xr{xq.qs, xq.d, xq.s};
+        const float yq = wq.finish(xr, 0.0f, red) + bq;
+        const float yk = wk.finish(xr, 0.0f, red + F::RED) + bk;
+        const float yv = wv.finish(xr, 0.0f, red + 2 * F::RED) + bv;
+        if (tid < D) {
+            qraw[tid] = yq;
+            kraw[tid] = yk;
+            vraw[tid] = yv;
+            csr[tid] = cs;
+            if (fq.cap_qkv && sp == 0) {
+                fq.cap_qkv[hbase * D + tid] = yq;
+                if (hbase == g * per) {
+                    fq.cap_qkv[qd + g * D + tid] = yk;
+                    fq.cap_qkv[qd + kvd + g * D + tid] = yv;
+                }
+            }
+        }
+    } else {
+        const int nraw = per * D + 3 * D;
+        constexpr int RAWPT = (16 * D + 3 * D + NW * 64 - 1) / (NW * 64);
+        float rv[RAWPT];
 #pragma unroll
-    for (int u = 0; u < RAWPT; ++u) {
-        const int i = tid + u * NW * 64;
-        if (i < nraw) qraw[i] = rv[u];
+        for (int u = 0; u < RAWPT; ++u) {  // branch-free: clamped index
+            const int i = min(tid + u * NW * 64, nraw - 1);
+            {
+                const float *src;
+                if (i < per * D)
+                    src = row + (size_t)g * per * D + i;
+                else if (i < per * D + D)
+                    src = row + qd + g * D + (i - per * D);
+                else if (i < per * D + 2 * D)
+                    src = row + qd + kvd + g * D + (i - per * D - D);
+                else {
+                    const int j = i - per * D - 2 * D;
+                    src = j < HALF ? cr + j : sr + (j - HALF);
+                }
+                rv[u] = *src;
+            }
+        }
+        // 2. the wavefront's first DEPTH K and V tiles (that many in flight
+        //    throughout)
+#pragma unroll
+        for (int b = 0; b < DEPTH; ++b) {
+            load_k(t0 + b * STEP, kr[b]);
+            load_v(t0 + b * STEP, vr[b]);
+        }
+#pragma unroll
+        for (int u = 0; u < RAWPT; ++u) {
+            const int i = tid + u * NW * 64;
+            if (i < nraw) qraw[i] = rv[u];
+        }
     }
     __syncthreads();
     // rotate-half RoPE (qwen_one_layer.c:172-183) of element dd of a head row
@@ -560,8 +640,8 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
     // rotated from 8 consecutive pairs read as 16-byte LDS vectors
     h8 qh[KS], ql[KS];
     {
-        const bool hv = col < per && pnew >= 0;
-        const int hc = col < per ? col : 0;
+        const bool hv = col < nh && pnew >= 0;
+        const int hc = col < nh ? col : 0;
         const bool capq = q_cap && sp == 0 && wave == 0 && hv;
         const float *qh_row = qraw + hc * D;
         auto ld8 = [](const float *p, float (&v)[8]) {
@@ -589,7 +669,7 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
                 ql[ks][e] = lo;
             }
             if (capq) {
-                float *qc = q_cap + (size_t)qi * qd + (size_t)(g * per + hc) * D + d0;
+                float *qc = q_cap + (size_t)qi * qd + (size_t)(hbase + hc) * D + d0;
                 *(float4 *)qc = make_float4(v[0], v[1], v[2], v[3]);
                 *(float4 *)(qc + 4) = make_float4(v[4], v[5], v[6], v[7]);
             }
@@ -703,24 +783,24 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
 
     // merge the NW wavefront states in LDS (reusing the V rows)
     __syncthreads();
-    float *mm = (float *)big;   // [NW][per]
-    float *ml = mm + NW * per;  // [NW][per]
-    float *mo = ml + NW * per;  // [NW][per][D]
-    if (col < per) {
+    float *mm = (float *)big;  // [NW][nh]
+    float *ml = mm + NW * nh;  // [NW][nh]
+    float *mo = ml + NW * nh;  // [NW][nh][D]
+    if (col < nh) {
         if (grp == 0) {
-            mm[wave * per + col] = m;
-            ml[wave * per + col] = lsum;
+            mm[wave * nh + col] = m;
+            ml[wave * nh + col] = lsum;
         }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)  // rows 4*grp .. 4*grp + 3: one 16-byte write
-            *(f4 *)(mo + ((size_t)wave * per + col) * D + 16 * dt + 4 * grp) = o[dt];
+            *(f4 *)(mo + ((size_t)wave * nh + col) * D + 16 * dt + 4 * grp) = o[dt];
     }
     __syncthreads();
     // 4 consecutive elements per thread; 8 lanes = 32 elements = one Q8_0
     // block of one head (D is a multiple of 32).  Each thread forms its
     // head's M = max over wavefronts, the factors e^(m_w - M) and the total
     // l itself (broadcast LDS reads; no further barrier).
-    const int nel4 = per * D / 4;
+    const int nel4 = nh * D / 4;
     for (int e40 = 0; e40 < nel4; e40 += NW * 64) {
         const int e4 = e40 + tid;
         const bool ok = e4 < nel4;
@@ -728,20 +808,20 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
         const int hc = ec / D, dd = ec - hc * D;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) M = fmaxf(M, mm[w * per + hc]);
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, mm[w * nh + hc]);
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ltot = 0.0f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-            const float4 ov = *(const float4 *)(mo + ((size_t)w * per + hc) * D + dd);
+            const float4 ov = *(const float4 *)(mo + ((size_t)w * nh + hc) * D + dd);
             // hardware exp2, as in the tile loop; an empty wavefront gives 0
-            const float f = M == -INFINITY ? 0.0f : __expf(mm[w * per + hc] - M);
-            ltot = fmaf(ml[w * per + hc], f, ltot);
+            const float f = M == -INFINITY ? 0.0f : __expf(mm[w * nh + hc] - M);
+            ltot = fmaf(ml[w * nh + hc], f, ltot);
             acc[0] = fmaf(ov.x, f, acc[0]);
             acc[1] = fmaf(ov.y, f, acc[1]);
             acc[2] = fmaf(ov.z, f, acc[2]);
             acc[3] = fmaf(ov.w, f, acc[3]);
         }
-        const int h = g * per + hc;
+        const int h = hbase + hc;
         if (!FINAL) {
             if (ok) {
                 const size_t pi = ((size_t)qi * qheads + h) * ns + sp;
@@ -1328,7 +1408,7 @@ static void dec_attn_impl(const float *qkv, int ldqkv, int nq, int qheads, int k
     SI_LAUNCH((k_dec_attn<DIM, NW, FIN, PAGED, DEP>), grid, dim3(NW * 64),                     \
               (AttnLds<DIM, NW>::bytes(per)), st, qkv, ldqkv, qheads, kvheads, rc, rs,         \
               kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx, chunk, scale, q_cap,              \
-              ws_m, ws_l, ws_o, attn, aqs, ad, as, pg)
+              ws_m, ws_l, ws_o, attn, aqs, ad, as, pg, DecQkvIn{})
 #define CALLN(DIM, NW, FIN)                                             \
     if (chunk <= DA_TILE * NW) {                                        \
         CALL(DIM, NW, FIN, 1);                                          \
@@ -1359,6 +1439,43 @@ static void dec_attn_impl(const float *qkv, int ldqkv, int nq, int qheads, int k
 #undef CALLD
 #undef CALLN
 #undef CALL
+}
+
+// Single-token decode with the Q|K|V projection inside the attention
+// (k_dec_attn<..., FQ>): worth it while a workgroup's 3*hdim weight rows
+// stream in well under a kernel boundary (0.5B: 97 KB); 7B's 384 rows of
+// 3584 values (774 KB) would take one CU several microseconds.
+bool dec_qkv_attn_ok(int hidden, int qheads, int kvheads, int hdim) {
+    if (kvheads <= 0 || qheads % kvheads || qheads / kvheads > 16) return false;
+    if (hdim != 64 && hdim != 128) return false;
+    if (hidden % SI_QK) return false;
+    return (size_t)3 * hdim * (hidden / SI_QK) * 18 <= 128 * 1024;
+}
+
+void launch_dec_qkv_attn(const DecQkvIn &fq, int qheads, int kvheads, int hdim, const float *rc,
+                         const float *rs, uint16_t *kc, uint16_t *vc, int ctx, int ns,
+                         float *q_cap, void *workspace, hipStream_t st) {
+    int chunk = (ctx + ns - 1) / ns;
+    chunk = (chunk + DA_TILE - 1) / DA_TILE * DA_TILE;
+    float *ws_m = (float *)workspace;
+    float *ws_l = ws_m + (size_t)qheads * ns;
+    float *ws_o = ws_l + (size_t)qheads * ns;
+    const float scale = 1.0f / sqrtf((float)hdim);  // attention_kernels.h:86
+    const dim3 grid(ns, qheads, 1);
+#define FQCALL(DIM, DEP)                                                                       \
+    SI_LAUNCH((k_dec_attn<DIM, DA_NW, false, false, DEP, true>), grid, dim3(DA_NW * 64),       \
+              ((AttnLds<DIM, DA_NW>::bytes(1) + 15) / 16 * 16 +                                \
+               FqLds<DIM, DA_NW>::bytes(fq.hidden)),                                           \
+              st, nullptr, 0, qheads, kvheads, rc, rs, kc, vc, (size_t)0, nullptr, ctx, ctx,   \
+              chunk, scale, q_cap, ws_m, ws_l, ws_o, nullptr, nullptr, nullptr, nullptr,       \
+              KvPages(), fq)
+    const bool one = chunk <= DA_TILE * DA_NW;
+    if (hdim == 64) {
+        if (one) FQCALL(64, 1); else FQCALL(64, 2);
+    } else {
+        if (one) FQCALL(128, 1); else FQCALL(128, 2);
+    }
+#undef FQCALL
 }
 
 void launch_dec_attn(const float *qkv, int ldqkv, int nq, int qheads, int kvheads, int hdim,

@@ -137,6 +137,27 @@ void launch_dec_gateup(const float *h, const float *gain, int hidden, float eps,
                        int8_t *cap_qs, uint16_t *cap_d, int16_t *cap_s, float *gu, float *act,
                        int8_t *aqs, uint16_t *ad, int16_t *as, bool exact, hipStream_t st);
 int dec_attn_chunks(int qheads, int kvheads, int hdim, int nq, int max_ctx);
+// The layer input, RMSNorm gain and fused Q|K|V matrix (+bias) of the
+// single-token decode kernel that projects and attends in one launch.
+struct DecQkvIn {
+    const float *x = nullptr, *gain = nullptr;
+    int hidden = 0;
+    float eps = 0.0f;
+    const uint8_t *wqs = nullptr;
+    const uint16_t *wd = nullptr;
+    int tile = 0, n = 0;
+    const float *bias = nullptr;
+    // optional captures: the normalised row and its Q8, the q|k|v row
+    float *cap_normed = nullptr;
+    int8_t *cap_qs = nullptr;
+    uint16_t *cap_d = nullptr;
+    int16_t *cap_s = nullptr;
+    float *cap_qkv = nullptr;
+};
+bool dec_qkv_attn_ok(int hidden, int qheads, int kvheads, int hdim);
+void launch_dec_qkv_attn(const DecQkvIn &fq, int qheads, int kvheads, int hdim, const float *rc,
+                         const float *rs, uint16_t *kc, uint16_t *vc, int ctx, int ns,
+                         float *q_cap, void *workspace, hipStream_t st);
 size_t dec_attn_workspace_bytes(int qheads, int hdim, int kvheads, int nq, int max_ctx);
 void launch_dec_attn(const float *qkv, int ldqkv, int nq, int qheads, int kvheads, int hdim,
                      const float *rc, const float *rs, uint16_t *kc, uint16_t *vc,
