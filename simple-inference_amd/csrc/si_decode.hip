@@ -1332,6 +1332,15 @@ static bool dec_rows_ok(int qheads, int kvheads, int hdim, int nq) {
     return b <= 65536;
 }
 
+// A single query over more than 128 tiles (2048 positions) takes 4
+// wavefronts per workgroup and up to 64 chunks of one tile per wavefront:
+// twice the workgroups of 8-wavefront chunks, whose 32-chunk cap left half
+// the CUs idle (7B, context 4096: attention 8.5-8.9 -> 7.2-7.4 us, the
+// layer 52.1 -> 51.3 us with the larger merge).
+static bool dec_long_single(int nq, int max_ctx) {
+    return nq == 1 && (max_ctx + DA_TILE - 1) / DA_TILE > 128;
+}
+
 int dec_attn_chunks(int qheads, int kvheads, int hdim, int nq, int max_ctx) {
     if (dec_rows_ok(qheads, kvheads, hdim, nq)) {
         // >= 4 steps of 16*(4/kvheads) positions per chunk (fewer partials
@@ -1345,6 +1354,10 @@ int dec_attn_chunks(int qheads, int kvheads, int hdim, int nq, int max_ctx) {
         return ns < 1 ? 1 : ns;
     }
     const int tiles = (max_ctx + DA_TILE - 1) / DA_TILE;
+    if (dec_long_single(nq, max_ctx)) {
+        const int ns = (tiles + 3) / 4;
+        return ns > 64 ? 64 : ns;
+    }
     if (nq == 1) {
         // one query is latency bound: one tile per wavefront (the shortest
         // chain), up to 32 chunks
@@ -1416,10 +1429,12 @@ static void dec_attn_impl(const float *qkv, int ldqkv, int nq, int qheads, int k
         CALL(DIM, NW, FIN, 2);                                          \
     }
     // 8 wavefronts unless the merge buffers of a wide GQA group exceed 64
-    // KiB; one K/V tile in flight per wavefront when each has at most one
-    // (chunk <= 16 * NW positions)
+    // KiB or a single query spans many chunks (dec_long_single); one K/V
+    // tile in flight per wavefront when each has at most one (chunk <= 16 *
+    // NW positions)
+    const bool long1 = dec_long_single(nq, max_ctx);
 #define CALLD(DIM)                                           \
-    if (AttnLds<DIM, DA_NW>::bytes(per) <= 65536) {          \
+    if (AttnLds<DIM, DA_NW>::bytes(per) <= 65536 && !long1) { \
         if (fin) {                                           \
             CALLN(DIM, DA_NW, true);                         \
         } else {                                             \
