@@ -18,6 +18,10 @@
 //   5 k_matvec     down mat-vec + residual h                     -> out
 //                  (si_gemv.hip)
 //
+// A small layer (dec_qkv_attn_ok) runs 1 and 2 as one kernel,
+// k_dec_attn<..., FQ = true>: each (chunk, query head) workgroup projects
+// its head's q and its group's k and v itself.
+//
 // The mat-vec core is GemvRows (si_gemv.hpp); with SI_LAYER_EXACT every
 // projection runs its bit-exact instantiation.
 #include "si_device.hpp"
