@@ -245,6 +245,9 @@ __global__ void __launch_bounds__(T) k_dec_wo(
     const int tile0 = blockIdx.x * R;
     const int t = threadIdx.x;
     const bool cap = blockIdx.x == 0;
+    // the residual is requested first: read after the sums it would add a
+    // memory round trip to the end of the kernel
+    const float r0 = residual ? residual[min(tile0 + (t % R), n - 1)] : 0.0f;
     GemvRows<R, T, EXACT, RowIdentity, DEC_U> g(wqs, wd, tile, n, n, qd / SI_QK, tile0,
                                          RowIdentity{});
     // Thread t merges the 4 consecutive elements 4*e4.. (e4 = t + T*i), 8
@@ -326,7 +329,7 @@ __global__ void __launch_bounds__(T) k_dec_wo(
     const int row = tile0 + t;
     if (t < R && row < n) {
         if (cap_y) cap_y[row] = y;
-        out[row] = residual ? __fadd_rn(residual[row], y) : y;
+        out[row] = residual ? __fadd_rn(r0, y) : y;
     }
 }
 

@@ -66,14 +66,17 @@ __global__ void __launch_bounds__(T) k_matvec(
         ld[i] = xd[i];
         ls[i] = xs[i];
     }
+    // bias and residual requested before the weights are consumed: a load
+    // after the sums would wait a whole memory round trip at the end
     const int row = tile0 + (t % R);
     const float b0 = bias ? bias[min(row, n - 1)] : 0.0f;
+    const float r0 = residual ? residual[min(row, n - 1)] : 0.0f;
     __syncthreads();
     const float y = g.finish(Q8Row{lq, ld, ls}, EXACT ? b0 : 0.0f, red);
     if (t < R && row < n) {
         const float v = EXACT ? y : y + b0;
         if (pre) pre[row] = v;
-        out[row] = residual ? __fadd_rn(residual[row], v) : v;
+        out[row] = residual ? __fadd_rn(r0, v) : v;
     }
 }
 
