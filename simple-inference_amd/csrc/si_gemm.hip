@@ -1015,11 +1015,13 @@ static GemmPlan gemm_plan(int m, int n, int nb) {
     return p;
 }
 
-// k_gemm_bd's layout for m <= BD_MAX_M rows: H 32-row halves, C K ranges
-// of cb blocks, S workgroups (slots) per (half, range) sharing its tiles
-// round robin; H * C * S <= 256, one workgroup per CU (its LDS is most of
-// the CU's).
-constexpr int BD_MAX_M = 64;
+// k_gemm_bd's layout: H 32-row halves, C K ranges of cb blocks, S
+// workgroups (slots) per (half, range) sharing its tiles round robin, one
+// workgroup per CU (its LDS is most of the CU's).  Workgroup i runs on XCD
+// i % 8 and the H halves of a slot share one, so S is sized for at most 32
+// (one XCD's CUs) per XCD: C * S <= 8 * floor(32 / H).
+constexpr int BD_SMALL_M = 64;  // every projection and the gate|up pair
+constexpr int BD_MAX_M = 512;   // one-tile projections, when bd_takes() says so
 struct BdPlan {
     int H, C, S, cb, units, grid;
     size_t lds;
@@ -1030,20 +1032,42 @@ static BdPlan bd_plan(int m, int n, int nb, int mode) {
     p.C = (nb + BD_MAX_CB - 1) / BD_MAX_CB;
     p.cb = (nb + p.C - 1) / p.C;
     p.units = mode == 1 ? n / 64 : (n + 31) / 32;
-    p.S = std::max(1, std::min(256 / (p.H * p.C), p.units));
+    const int per_xcd = std::max(1, 32 / p.H);
+    p.S = std::max(1, std::min(8 * per_xcd / p.C, p.units));
     p.grid = 8 * p.H * ((p.C * p.S + 7) / 8);
     p.lds = bd_lds(p.cb);
     return p;
 }
 
+// Whether gemm_core takes k_gemm_bd for a one-tile projection: always up to
+// BD_SMALL_M rows; up to BD_MAX_M while K fits two LDS ranges and a slot's
+// serial work (tiles per slot x blocks per range) stays near 1000 blocks.
+// Measured per GEMM against the tile kernel and its K-split reduce: 0.5B
+// QKV, O and down at 96-512 rows 6-19 us against 10-22; 7B QKV and O 12-38
+// against 19-41; 7B down (five ranges, 833-4522 blocks per slot) 48-159
+// against 40-119, so it keeps the tile kernel.  The gate|up pair stays on
+// the tile kernel past BD_SMALL_M (0.5B, 512 rows: each slot's ten units
+// took 45 us against 28).
+static bool bd_takes(int m, int n, int nb) {
+    if (m <= BD_SMALL_M) return true;
+    if (m > BD_MAX_M) return false;
+    const BdPlan p = bd_plan(m, n, nb, 0);
+    return p.C <= 2 && (p.units + p.S - 1) / p.S * p.cb <= 1024;
+}
+
+// K splits gemm_core plans for an m x n x nb problem (1: one pass, no
+// partials); the workspace size and the gate|up launcher decide with it
+static int gemm_splits(int m, int n, int nb) {
+    return bd_takes(m, n, nb) ? bd_plan(m, n, nb, 0).C : gemm_plan(m, n, nb).splits;
+}
+
 size_t gemm_workspace_bytes(int m, int n, int k) {
-    const int nb = k / SI_QK;
-    const int splits = m <= BD_MAX_M ? bd_plan(m, n, nb, 0).C : gemm_plan(m, n, nb).splits;
+    const int splits = gemm_splits(m, n, k / SI_QK);
     return splits > 1 ? (size_t)splits * m * n * sizeof(float) : 0;
 }
 
 size_t gemm_gateup_workspace_bytes(int m, int f, int k) {
-    if (m <= BD_MAX_M && k / SI_QK <= BD_MAX_CB) return 0;  // one fused pass
+    if (m <= BD_SMALL_M && k / SI_QK <= BD_MAX_CB) return 0;  // one fused pass
     return gemm_workspace_bytes(m, 2 * f, k);
 }
 
@@ -1121,7 +1145,7 @@ static int gemm_core(const uint8_t *wqs, const uint16_t *wd, int tile, int n, in
     };
     float *part = nullptr;
     int splits;
-    if (m <= BD_MAX_M) {
+    if (bd_takes(m, n, nb)) {
         const BdPlan p = bd_plan(m, n, nb, 0);
         if (p.C == 1 || fits(p.C)) {
             part = p.C > 1 ? (float *)workspace : nullptr;
@@ -1181,14 +1205,16 @@ void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int
                            size_t ws_bytes, hipStream_t st) {
     if (m <= 0) return;
     const int n = 2 * f, nb = k / SI_QK;
-    if (!exact && m <= BD_MAX_M && nb <= BD_MAX_CB) {
+    if (!exact && m <= BD_SMALL_M && nb <= BD_MAX_CB) {
         launch_bd(bd_plan(m, n, nb, 1), 1, wqs, wd, tile, n, nb, xqs, xd, m, nullptr, nullptr, gu,
                   n, nullptr, GateUpOut{f, act, qs, d, s}, st);
         return;
     }
-    // m <= BD_MAX_M with a longer K: k_gemm_bd's K-range partials (or, with
-    // too little workspace, one pass into gu), then the split reduce
-    const bool split = exact || m <= BD_MAX_M || gemm_plan(m, n, nb).splits > 1;
+    // a K split (gemm_core's own plan: k_gemm_bd's K-range partials or the
+    // tile kernel's), or, with too little workspace, one pass into gu; then
+    // the split reduce.  Without a split gemm_core would write gu, which is
+    // optional here: the fused pass below.
+    const bool split = exact || gemm_splits(m, n, nb) > 1;
     if (split) {
         const int splits = gemm_core(wqs, wd, tile, n, k, xqs, xd, m, nullptr, nullptr, gu, n,
                                      exact, workspace, ws_bytes, true, st);

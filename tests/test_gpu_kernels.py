@@ -583,6 +583,7 @@ def test_ffn_gateup_q8(oracle, shape, flags):
     (130, 96, 256, 8, 0, True),          # ragged rows, f an odd number of 32-blocks
     (64, 4864, 896, 32, 0, True),        # 0.5B batched-decode shape (64-row tiles)
     (512, 4864, 896, 32, 0, False),      # 0.5B prefill shape; also without act and sums
+    (128, 4864, 896, 32, 0, True),       # one-pass plan where the tile kernel would split K
     (2, 160, 96, 16, 0, True),           # tiny: the plan splits K (GEMM + SwiGLU kernel)
     (300, 4864, 896, 32, si_amd.SI_GEMM_EXACT, True),
     (600, 4864, 896, 32, 0, True),       # past 512 rows: 128-row tiles
@@ -607,8 +608,8 @@ def test_gemm_gateup_q8(oracle, m, f, k, tile, flags, act_out):
     ws = empty(max(wsb, 4), torch.uint8)
     xqs_d, xd_d = dev(qs), dev(d.view(np.int16))
 
-    def run(with_act):
-        gu = empty(m * 2 * f, torch.float32)
+    def run(with_act, with_gu=True):
+        gu = empty(m * 2 * f, torch.float32) if with_gu else None
         act = empty(m * f, torch.float32) if with_act else None
         aq, ad = empty(m * f, torch.int8), empty(m * f // 32, torch.int16)
         asum = empty(m * f // 32, torch.int16) if with_act else None
@@ -619,6 +620,9 @@ def test_gemm_gateup_q8(oracle, m, f, k, tile, flags, act_out):
         return gu, act, aq, ad, asum
 
     gu, act, aq, ad, asum = run(True)
+    if not flags:  # gu is optional given the workspace: the same Q8_0 without it
+        _, _, aq3, ad3, _ = run(True, with_gu=False)
+        assert np.array_equal(host(aq3), host(aq)) and np.array_equal(host(ad3), host(ad))
     if not act_out:  # NULL act and block sums: the same gate|up and Q8_0
         gu2, _, aq2, ad2, _ = run(False)
         assert np.array_equal(host(gu2).view(np.uint32), host(gu).view(np.uint32))

@@ -171,6 +171,7 @@ def _prefill_case(oracle, shape, ntok, prefix, seed, flags, rows):
 @pytest.mark.parametrize("shape,ntok,prefix,rows,flags", [
     ("0.5b", 512, 0, [0, 1, 17, 63, 255, 511], EXACT),
     ("0.5b", 512, 0, [0, 63, 255, 511], si_amd.SI_LAYER_FULL),
+    ("0.5b", 128, 0, [0, 127], si_amd.SI_LAYER_FULL),        # streaming one-tile GEMMs
     ("0.5b", 37, 100, [0, 36], EXACT),                      # ragged, cached prefix
 ])
 def test_prefill_vs_oracle(oracle, shape, ntok, prefix, rows, flags):
