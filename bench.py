@@ -43,13 +43,13 @@ METRIC = "decode layer µs + HBM GB/s; prefill tokens/s + int8 MFMA % (one GPU)"
 # x1.000): {(config, kernel prefix): (FETCH_SIZE KiB, WRITE_SIZE KiB)}.
 # Kernels not listed report traffic null.  Summaries: profiles/cfgN_*.md.
 PMC_KIB = {
-    ("1", "k_matvec<8, 128, false>"): (328.9, 4.5),
+    ("1", "k_matvec<8, 128, false>"): (330.9, 4.5),
     ("2", "k_dec_attn<64, 8, false, false, 1, true>"): (2697.2, 35.5),
     ("2", "k_dec_gateup<64, 512, false>"): (2530.9, 9.8),
     ("2", "k_matvec<8, 512, false>"): (1256.0, 3.5),
     ("2", "k_dec_wo<8, 512, false>"): (579.0, 3.5),
     ("3", "k_gemm_fast<2, 2, 1, 2, true>"): (6798.0, 4800.0),
-    ("4", "k_gemm_fast<2, 2, 2, 2, true>"): (627281.6, 75938.8),
+    ("4", "k_gemm_fast<2, 2, 2, 2, true>"): (627399.1, 75937.1),
     ("5", "k_dec_attn_rows<128, 4, false, false>"): (266834.6, 8192.0),
 }
 FETCH_SCALE, WRITE_SCALE = 2.000, 1.000
