@@ -286,7 +286,8 @@ def test_gemm_matches_oracle_rows(oracle, m, n, k):
 
 @pytest.mark.parametrize("m,n,k", [(512, 1152, 896), (64, 4608, 3584), (130, 896, 4864),
                                    (100, 9728, 896), (64, 3584, 18944), (2048, 384, 896),
-                                   (130, 200, 96), (1, 4608, 3584)])
+                                   (130, 200, 96), (1, 4608, 3584), (200, 1152, 896),
+                                   (384, 3584, 3584)])
 @pytest.mark.parametrize("split", [False, True])
 def test_gemm_every_row_vs_float64(oracle, m, n, k, split):
     """Every output row of the layer-shaped GEMMs against the float64 product
@@ -344,11 +345,14 @@ def test_gemm_residual(oracle):
     (64, 256, 512, 256),     # batched-decode GEMM, one column tile per workgroup
     (33, 9000, 256, 9008),   # three or more tiles per workgroup, a ragged last tile, ldo > n
     (5, 200, 3872, 200),     # K longer than one LDS range: range partials, then their sum
+    (300, 896, 896, 904),    # past 64 rows: ten 32-row halves, two tiles per slot
+    (200, 896, 4864, 896),   # past 64 rows with two K ranges (no workspace: the tile kernel)
 ])
 def test_gemm_bias_residual_batched(oracle, m, n, k, ldo):
-    """out = residual + (GEMM + bias) at m <= 64 rows (k_gemm_bd), every row
-    against the float64 product of the dequantized operands, with and
-    without workspace."""
+    """out = residual + (GEMM + bias) on k_gemm_bd (every projection of up to
+    64 rows, one-tile projections of up to 512), every row against the
+    float64 product of the dequantized operands, with and without
+    workspace."""
     torch = _torch()
     rng = np.random.default_rng(m + n + k)
     w = q4(oracle, rng, n, k)
