@@ -517,7 +517,8 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
 }
 
 // ---------------------------------------------------------------------
-// Batched-decode GEMM (m <= 64 activation rows).
+// Batched-decode GEMM (m <= 64 activation rows; also the short-K one-tile
+// projections of prefill up to 512 rows, bd_takes).
 //
 // At this size each output costs two VALU operations per K block (the
 // exact int32 dot converted, then one fused multiply-add by the fp32 scale
@@ -534,8 +535,8 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
 //   * at the end of a tile the partial sums meet in LDS and are added in a
 //     fixed order (deterministic); wavefront w < 8 finishes output
 //     registers 2w and 2w + 1 of the 16 of every lane.
-// The two 32-row halves of a set of tiles run on the same XCD (blockIdx %
-// 8), so the second half's weight reads hit that XCD's L2.  Longer K is
+// The 32-row halves of a set of tiles run on the same XCD (blockIdx % 8),
+// so the later halves' weight reads hit that XCD's L2.  Longer K is
 // split into ranges whose partials [c][m][n] are summed afterwards, as
 // k_gemm_fast's are.
 //
