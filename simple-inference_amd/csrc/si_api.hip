@@ -87,7 +87,7 @@ static int check_shape(const si_shape_t *s) {
 // of each timed launch's kernel (demangled, without the "si::" namespace or
 // the parameter list, e.g. "k_dec_attn<64, 8, false, false, 1>").
 namespace si {
-bool g_kernel_timing_on = false;
+std::atomic<bool> g_kernel_timing_on{false};
 }
 static std::mutex g_kt_mu;
 static std::vector<std::string> g_kt_filter;
@@ -165,14 +165,14 @@ int si_kernel_timing_start(const char *filter, int capacity) {
         p = e;
     }
     g_kt_used = 0;
-    g_kernel_timing_on = true;
+    g_kernel_timing_on.store(true);
     return SI_OK;
 }
 
 int si_kernel_timing_stop(float *ms, int capacity, int *count) {
     std::lock_guard<std::mutex> lock(g_kt_mu);
     SI_REQUIRE(g_kernel_timing_on, "kernel timing is not on");
-    g_kernel_timing_on = false;
+    g_kernel_timing_on.store(false);
     const int n = g_kt_used < capacity ? g_kt_used : capacity;
     if (count) *count = n;
     for (int i = 0; i < n; ++i) {
@@ -1015,7 +1015,8 @@ static int run_decode(si_layer *L, const float *x, uint16_t *kc, uint16_t *vc, i
     // a small layer projects Q|K|V inside the attention kernel (no q|k|v
     // round trip); the exact projections and standard attention take the
     // staged kernels
-    const bool fused_qkv = !exact && !standard && dec_qkv_attn_ok(H, s.qheads, s.kvheads, s.hdim);
+    const bool fused_qkv =
+        !exact && !standard && dec_qkv_attn_ok(H, s.qheads, s.kvheads, s.hdim, ctx);
     if (!fused_qkv) {
         // qwen_one_layer.c:247-258: RMSNorm -> Q8 -> Q, K, V (+bias)
         mark(L, SI_PHASE_QKV, st);

@@ -127,7 +127,7 @@ struct NormQ8Prologue {
         double tot = 0.0;
 #pragma unroll
         for (int w = 0; w < T / 64; ++w) tot += dscr[w];
-        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn((float)(tot / (double)n), eps)));
+        const float inv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn((float)(tot / (double)n), eps)));
         const bool cap = blockIdx.x == 0;
         auto emit = [&](int e4, float4 xv, float4 gv) {
             const float y[4] = {__fmul_rn(__fmul_rn(xv.x, inv), gv.x),
@@ -1466,8 +1466,12 @@ static void dec_attn_impl(const float *qkv, int ldqkv, int nq, int qheads, int k
 // Single-token decode with the Q|K|V projection inside the attention
 // (k_dec_attn<..., FQ>): worth it while a workgroup's 3*hdim weight rows
 // stream in well under a kernel boundary (0.5B: 97 KB); 7B's 384 rows of
-// 3584 values (774 KB) would take one CU several microseconds.
-bool dec_qkv_attn_ok(int hidden, int qheads, int kvheads, int hdim) {
+// 3584 values (774 KB) would take one CU several microseconds.  Past 2048
+// positions the context splits into up to 64 chunks sized for 4-wavefront
+// workgroups; every chunk would re-project its head's rows, so such
+// contexts take the staged pair (k_dec_qkv, then k_dec_attn).
+bool dec_qkv_attn_ok(int hidden, int qheads, int kvheads, int hdim, int ctx) {
+    if (dec_long_single(1, ctx)) return false;
     if (kvheads <= 0 || qheads % kvheads || qheads / kvheads > 16) return false;
     if (hdim != 64 && hdim != 128) return false;
     if (hidden % SI_QK) return false;

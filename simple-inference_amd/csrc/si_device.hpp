@@ -11,6 +11,12 @@
 
 namespace si {
 
+// Correctly rounded binary32 square root (glibc sqrtf, as rmsnorm uses it,
+// qwen_one_layer.c:167).  HIP's __fsqrt_rn is the hardware v_sqrt_f32 (about
+// 1 ulp) unless OCML_BASIC_ROUNDED_OPERATIONS is defined; the builtin
+// compiles to v_sqrt_f32 plus a two-neighbour correction by fma.
+__device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
+
 __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 __device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
 

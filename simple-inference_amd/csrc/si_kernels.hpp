@@ -3,6 +3,7 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
+#include <atomic>
 #include <stdint.h>
 namespace si {
 // Per-dispatch kernel timing (si_kernel_timing_start / _stop): when it is on
@@ -10,7 +11,9 @@ namespace si {
 // hipExtLaunchKernelGGL to attach to the dispatch itself.
 bool kernel_timing_events(const void *kernel, hipStream_t st, hipEvent_t *start,
                           hipEvent_t *stop);
-extern bool g_kernel_timing_on;
+// Read on every launch from any host thread (relaxed: the events it guards
+// are handed out under the timing mutex); written under that mutex.
+extern std::atomic<bool> g_kernel_timing_on;
 }  // namespace si
 
 // Every kernel launch of the library goes through SI_LAUNCH (same arguments
@@ -18,7 +21,7 @@ extern bool g_kernel_timing_on;
 #define SI_LAUNCH(K, G, B, S, ST, ...)                                                 \
     do {                                                                             \
         hipEvent_t si_ev0_, si_ev1_;                                                 \
-        if (::si::g_kernel_timing_on &&                                              \
+        if (::si::g_kernel_timing_on.load(std::memory_order_relaxed) &&             \
             ::si::kernel_timing_events((const void *)(K), ST, &si_ev0_, &si_ev1_))   \
             hipExtLaunchKernelGGL(K, G, B, S, ST, si_ev0_, si_ev1_, 0, __VA_ARGS__);  \
         else                                                                         \
@@ -154,7 +157,7 @@ struct DecQkvIn {
     int16_t *cap_s = nullptr;
     float *cap_qkv = nullptr;
 };
-bool dec_qkv_attn_ok(int hidden, int qheads, int kvheads, int hdim);
+bool dec_qkv_attn_ok(int hidden, int qheads, int kvheads, int hdim, int ctx);
 void launch_dec_qkv_attn(const DecQkvIn &fq, int qheads, int kvheads, int hdim, const float *rc,
                          const float *rs, uint16_t *kc, uint16_t *vc, int ctx, int ns,
                          float *q_cap, void *workspace, hipStream_t st);

@@ -152,7 +152,7 @@ __global__ void __launch_bounds__(256)
     if (lane == 0) red[wave] = ss;
     __syncthreads();
     const double tot = (red[0] + red[1]) + (red[2] + red[3]);
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn((float)(tot / (double)n), eps)));
+    const float inv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn((float)(tot / (double)n), eps)));
     for (int i = threadIdx.x; i < n; i += 256)
         out[base + i] = __fmul_rn(__fmul_rn(x[base + i], inv), gain ? gain[i] : 1.0f);
 }
@@ -190,20 +190,27 @@ void launch_rope_inplace(float *heads, int nheads, int hdim, int position, const
 }
 
 // f32_to_f16 / f16_to_f32 (qwen_one_layer.c:42-86) elementwise.
+// Grid-stride loops over a capped grid: any n the 64-bit size allows maps
+// onto at most F16_MAX_BLOCKS workgroups (a 1-D grid is limited to 2^32
+// threads).
+constexpr unsigned F16_MAX_BLOCKS = 8192;
 __global__ void k_f32_to_f16(const float *__restrict__ src, uint16_t *__restrict__ dst,
                              size_t n) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) dst[i] = f2h(src[i]);
+    const size_t step = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step)
+        dst[i] = f2h(src[i]);
 }
 __global__ void k_f16_to_f32(const uint16_t *__restrict__ src, float *__restrict__ dst,
                              size_t n) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) dst[i] = h2f(src[i]);
+    const size_t step = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step)
+        dst[i] = h2f(src[i]);
 }
 
 void launch_f16_convert(const void *src, void *dst, size_t n, bool to_half, hipStream_t st) {
     if (n == 0) return;
-    const dim3 grid((unsigned)((n + 255) / 256));
+    const size_t blocks = (n + 255) / 256;
+    const dim3 grid((unsigned)(blocks < F16_MAX_BLOCKS ? blocks : F16_MAX_BLOCKS));
     if (to_half)
         SI_LAUNCH(k_f32_to_f16, grid, dim3(256), 0, st, (const float *)src,
                   (uint16_t *)dst, n);

@@ -110,7 +110,7 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8(const float *__restrict__ x,
     }
     const double tot = block_sum_d(ss, red);
     const float ms = (float)(tot / (double)n);
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(ms, eps)));
+    const float inv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(ms, eps)));
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
         float v = __fmul_rn(lds[i], inv);
         v = __fmul_rn(v, gain ? gain[i] : 1.0f);
@@ -186,7 +186,7 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8_v4(const float *__restrict__
     }
     const double tot = block_sum_d(ss, red);
     const float ms = (float)(tot / (double)n);
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(ms, eps)));
+    const float inv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(ms, eps)));
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
         const int c = tid + 256 * i;

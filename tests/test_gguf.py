@@ -175,27 +175,41 @@ def test_malformed_files(tmp_path):
 
 
 @pytest.mark.gpu
-def test_layer_from_gguf_matches_direct(tmp_path):
-    """A 0.5B-shaped layer written to GGUF and loaded back decodes to the
-    same bits as the layer built from the arrays (both exact and fast)."""
+@pytest.mark.parametrize("name,ctx", [("0.5b", 300), ("7b", 1024)])
+def test_layer_from_gguf_matches_direct(tmp_path, name, ctx):
+    """A layer written to GGUF and loaded back (extract_weights.py:144-199
+    feeding load_layer, qwen_one_layer.c:210-221): the tensors read equal
+    the source arrays byte for byte, the decode passes the chained oracle
+    check (tests/chain.py) on the source arrays, FULL and EXACT, and gives
+    the same bits as the layer built from the arrays directly."""
     from oracle.oracle_py import Oracle
+    from tests.chain import LayerBuffers, check_row
     from tests.gpu_helpers import make_layer, torch_cuda
     torch = torch_cuda()  # torch's device first, then the native layers
     from oracle.oracle_py import make_shape as or_shape
     oracle = Oracle()
-    sd = dict(si_amd.SHAPES["0.5b"])
-    s = si_amd.make_shape(**sd)
-    lay = make_layer(oracle, or_shape(**sd), 17)
+    sd = dict(si_amd.SHAPES[name])
+    s, os_ = si_amd.make_shape(**sd), or_shape(**sd)
+    lay = make_layer(oracle, os_, 17)
     path = str(tmp_path / "l.gguf")
     gguf.write_gguf(path, gguf.layer_meta(sd), gguf.layer_tensors_gguf(sd, lay, layer=5))
     with gguf.GGUFFile(path) as gf:
         gsd, gt = gguf.load_layer(gf, 5)
-        Lg = si_amd.Layer(si_amd.make_shape(**gsd), gt, 1, 300)
-    Ld = si_amd.Layer(s, lay, 1, 300)
-    ctx, kvd = 300, s.kvheads * s.hdim
+        for key, shape_val in sd.items():
+            assert gsd[key] == shape_val, key
+        for key, arr in lay.items():
+            if arr is None:
+                assert gt[key] is None, key
+            else:
+                assert np.array_equal(np.asarray(gt[key]).view(np.uint8).reshape(-1),
+                                      np.asarray(arr).view(np.uint8).reshape(-1)), key
+        Lg = si_amd.Layer(si_amd.make_shape(**gsd), gt, 1, ctx)
+    Ld = si_amd.Layer(s, lay, 1, ctx)
+    kvd = s.kvheads * s.hdim
     rng = np.random.default_rng(18)
     kc0, vc0 = kv_history(oracle, rng, ctx, kvd), kv_history(oracle, rng, ctx, kvd)
-    x = dev(rng.standard_normal(s.hidden).astype(np.float32))
+    xh = rng.standard_normal(s.hidden).astype(np.float32)
+    x = dev(xh)
     for flags in (si_amd.SI_LAYER_FULL, si_amd.SI_LAYER_EXACT):
         outs = []
         for L in (Lg, Ld):
@@ -203,6 +217,11 @@ def test_layer_from_gguf_matches_direct(tmp_path):
             out = empty(s.hidden, torch.float32)
             L.decode(x, kc, vc, ctx, out, flags)
             outs.append((host(out), host(kc), host(vc)))
+            if L is Lg:
+                B = LayerBuffers(Lg, os_, 1)
+                hk, hv = outs[-1][1].view(np.uint16), outs[-1][2].view(np.uint16)
+                check_row(oracle, os_, lay, xh, 0, B, hk, hv, 0, ctx - 1, ctx, outs[-1][0],
+                          flags == si_amd.SI_LAYER_EXACT)
         assert all(np.array_equal(a, b) for a, b in zip(*outs)), flags
     Lg.close()
     Ld.close()

@@ -70,3 +70,34 @@ def test_f2h_edge_neighbourhoods(oracle, center, sign):
     n = 1 << 17
     start = (center - n // 2) & 0x7fffffff if center >= n // 2 else 0
     _sweep(oracle, (start | sign) & 0xffffffff, 1, n)
+
+
+def test_abi_f16_conversions(oracle):
+    """si_f16_to_f32 / si_f32_to_f16 through the C ABI (the mirror's
+    f16_to_f32 / f32_to_f16, qwen_one_layer.c:42-86): every half widened bit
+    for bit, and a strided sweep of fp32 patterns plus the rounding edges
+    narrowed bit for bit.  One call spans several grid-stride rounds (the
+    grid is capped at 8192 workgroups of 256 threads)."""
+    torch = _torch()
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    wide = empty(65536, torch.float32)
+    si_amd.call("si_f16_to_f32", si_amd.ptr(dev(h.view(np.int16))), si_amd.ptr(wide), 65536,
+                None)
+    assert np.array_equal(host(wide).view(np.uint32), oracle.f16_to_f32(h).view(np.uint32))
+    stride = 1021
+    bits = np.arange(0, 1 << 32, stride, dtype=np.uint64).astype(np.uint32)
+    edges = [0x00000000, 0x33000000, 0x33800000, 0x387fc000, 0x38800000, 0x477fe000,
+             0x477ff000, 0x7f800000]
+    near = np.concatenate([(np.uint32(c) + np.arange(-2048, 2048, dtype=np.int64)
+                            .astype(np.uint32)) for c in edges])
+    bits = np.concatenate([bits, near, near | np.uint32(0x80000000)])
+    n = bits.size
+    assert n > 8192 * 256  # more than one grid-stride round
+    narrow = empty(n, torch.int16)
+    si_amd.call("si_f32_to_f16", si_amd.ptr(dev(bits.view(np.float32))), si_amd.ptr(narrow), n,
+                None)
+    got = host(narrow).view(np.uint16)
+    want = oracle.f32_to_f16(bits.view(np.float32))
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, (f"{bad.size} patterns differ, first 0x{int(bits[bad[0]]):08x}: "
+                           f"got 0x{int(got[bad[0]]):04x} want 0x{int(want[bad[0]]):04x}")

@@ -23,8 +23,17 @@ def _torch():
     return torch
 
 
+# Test-only shapes beside si_amd.SHAPES.  d128_small: hdim 128 with a
+# hidden small enough (3 * 128 rows x 512 values = 110,592 B of Q4_0 per
+# head) that single-token decode projects Q|K|V inside the attention kernel
+# (the hdim-128 instances of the fused path), one KV group of 4 heads.
+_TEST_SHAPES = {
+    "d128_small": dict(hidden=512, qheads=4, kvheads=1, hdim=128, ffn=1024),
+}
+
+
 def _shapes(name):
-    sd = si_amd.SHAPES[name]
+    sd = _TEST_SHAPES.get(name) or si_amd.SHAPES[name]
     return si_amd.make_shape(**sd), or_shape(**sd)
 
 
@@ -86,12 +95,16 @@ def test_decode_full_layer_0_5b_ctx1024(oracle, flags):
 
 @pytest.mark.parametrize("shape,ctx", [("0.5b", 1), ("0.5b", 2), ("0.5b", 16), ("0.5b", 17),
                                        ("0.5b", 129), ("0.5b", 500), ("0.5b", 5000), ("7b", 33),
-                                       ("7b", 4096)])
+                                       ("7b", 4096), ("d128_small", 1), ("d128_small", 17),
+                                       ("d128_small", 300), ("d128_small", 2048),
+                                       ("d128_small", 2100)])
 def test_decode_contexts(oracle, shape, ctx):
     """Single-token decode over contexts that put the new token at every kind
     of place in the attention chunks (first tile, tile edge, last chunk); at
     0.5B 5000 and 7B 4096 the chunk partials exceed 32 KB and are merged once
-    before W_O instead of inside it."""
+    before W_O instead of inside it.  d128_small runs the hdim-128 fused
+    Q|K|V + attention kernel up to 2048 positions (one and two tiles in
+    flight) and the staged pair past them."""
     torch = _torch()
     s, os_ = _shapes(shape)
     lay = make_layer(oracle, os_, 40 + ctx)
@@ -104,7 +117,12 @@ def test_decode_contexts(oracle, shape, ctx):
     for flags in (si_amd.SI_LAYER_FULL, EXACT):
         kc, vc = dev(kc0.view(np.int16)), dev(vc0.view(np.int16))
         out = empty(s.hidden, torch.float32)
-        L.decode(dev(x), kc, vc, ctx, out, flags)
+        ran = si_amd.kernel_times_ms("k_dec_attn", lambda: L.decode(dev(x), kc, vc, ctx, out,
+                                                                    flags))
+        if shape == "d128_small" and flags == si_amd.SI_LAYER_FULL:
+            fused = [n for n, _ in ran if n.startswith("k_dec_attn<128,") and
+                     n.endswith(", true>")]
+            assert bool(fused) == (ctx <= 2048), f"ctx {ctx}: kernels {ran}"
         B = LayerBuffers(L, os_, 1)
         hk, hv = host(kc).view(np.uint16), host(vc).view(np.uint16)
         check_row(oracle, os_, lay, x, 0, B, hk, hv, 0, ctx - 1, ctx, host(out), flags == EXACT)
@@ -188,10 +206,23 @@ def test_prefill_vs_oracle(oracle, shape, ntok, prefix, rows, flags):
     L.close()
 
 
-def test_prefill_7b_2048_sampled_rows(oracle):
-    """7B layer, 2048-token causal prefill."""
-    L, *_ = _prefill_case(oracle, "7b", 2048, 0, 5, EXACT, [0, 1, 63, 1023, 2047])
+@pytest.mark.parametrize("flags", [EXACT, si_amd.SI_LAYER_FULL])
+def test_prefill_7b_2048_sampled_rows(oracle, flags):
+    """7B layer, 2048-token causal prefill, in the
+    reference's block order (EXACT) and with the fast kernels bench.py times
+    (default flags: single-pass tile GEMMs for Q|K|V and O, a 5-way K split
+    and reduce for down, the fused SwiGLU + Q8 gate|up instance)."""
+    rows = [0, 1, 63, 1023, 2047]
+    L, s, os_, lay, x, kc0, vc0, hk, hv, got = _prefill_case(oracle, "7b", 2048, 0, 5, flags,
+                                                             rows)
     L.close()
+    kr, vr = kc0.copy(), vc0.copy()
+    want = oracle.layer_prefill(os_, lay, x, 2048, 0, kr, vr, rows=rows)
+    if flags == EXACT:
+        assert np.array_equal(hk, kr) and np.array_equal(hv, vr)
+    e2e = [end_to_end_report(got[t], want[i]) for i, t in enumerate(rows)]
+    print("end-to-end vs oracle:", e2e)
+    assert max(e["max_over_rms"] for e in e2e) <= E2E_BOUND["7b"], e2e
 
 
 @pytest.mark.parametrize("shape,ntok,prefix", [

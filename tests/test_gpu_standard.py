@@ -21,6 +21,7 @@ from tests.gpu_helpers import close, dev, empty, host, kv_history, make_layer
 pytestmark = pytest.mark.gpu
 STD = si_amd.SI_LAYER_ATTN_STANDARD
 CLI = os.path.join(os.path.dirname(si_amd.AMD_SO), "si_qwen_layer")
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ref_golden.npz")
 _SHAPES = {
     "g1_d32": dict(hidden=256, qheads=8, kvheads=1, hdim=32, ffn=0),
     "0.5b": si_amd.SHAPES["0.5b"],
@@ -112,6 +113,20 @@ def test_standard_vs_reference_function(oracle, ref, ctx):
     want, pw = ref.attention_standard(q, kc, vc, ctx, with_scores=True)
     np.testing.assert_allclose(p, pw, rtol=2e-5, atol=1e-9)
     close(got, want, 2e-3, "vs reference attention_standard")
+
+
+def test_standard_vs_reference_fixture():
+    """Against the reference's own attention_standard output recorded in the
+    golden fixture (1.5B shape, context 64; tests/golden/make_golden.py), so
+    the comparison also runs where the reference build is absent."""
+    g = np.load(GOLDEN, allow_pickle=False)
+    s = si_amd.make_shape(**si_amd.SHAPES["1.5b_ref"])
+    ctx = 64
+    got, p = _run_standard(s, dev(g["att_q"]), dev(g["att_kc"].view(np.int16)),
+                           dev(g["att_vc"].view(np.int16)), ctx)
+    close(got, g["att_standard"], 2e-3, "vs the reference's attention_standard (fixture)")
+    # each head's normalised scores sum to one
+    np.testing.assert_allclose(p.astype(np.float64).sum(1), 1.0, rtol=1e-5)
 
 
 @pytest.mark.parametrize("name,ctx,flags", [
