@@ -6,7 +6,10 @@ one layer decode of one token.  Inputs are synthetic (seeded N(0,0.02)
 weights -> Q4_0, N(0,1) activations and fp16 KV) and resident in HBM before
 the timed region.  The step cycles through enough distinct copies of the
 layer (weights + KV cache) to exceed the 256 MB Infinity Cache, so the
-reported GB/s is HBM traffic, not cache hits.
+reported GB/s is HBM traffic, not cache hits: with fewer steps than copies,
+the timed HIP graphs start at staggered copies and are replayed in turn, so
+every copy is visited before any is reused.  Each figure is the median over
+at least five timed replays, with their min and max.
 
 The JSON line's "roofline" is the time-dominant kernel of that step (and
 "roofline_second" the kernel moving the most bytes), each timed by HIP
@@ -21,6 +24,7 @@ on one pinned host core, each a bounded sample stated in the line.
 """
 import argparse
 import ctypes
+import hashlib
 import json
 import os
 import sys
@@ -40,24 +44,44 @@ METRIC = "decode layer µs + HBM GB/s; prefill tokens/s + int8 MFMA % (one GPU)"
 # --pmc runs of `bench.py --profile N` (FETCH_SIZE, then WRITE_SIZE, KiB per
 # dispatch, medians over the run's dispatches of that kernel), scaled by what
 # the counters read for a 256 MiB copy (FETCH_SIZE x2.000, WRITE_SIZE
-# x1.000): {(config, kernel prefix): (FETCH_SIZE KiB, WRITE_SIZE KiB)}.
-# Kernels not listed report traffic null.  Summaries: profiles/cfgN_*.md.
+# x1.000): {(config, kernel): (FETCH_SIZE KiB, WRITE_SIZE KiB, csrc digest)}.
+# The digest (csrc_digest()) names the kernel sources the counters were read
+# from; a roofline block whose kernel sources have changed since reports its
+# traffic with "traffic_current": false.  Kernels not listed report traffic
+# null.  Summaries: profiles/cfgN_*.md.
 PMC_KIB = {
-    ("1", "k_matvec<8, 128, false>"): (330.9, 4.5),
-    ("2", "k_dec_attn<64, 8, false, false, 1, true>"): (2697.2, 35.5),
-    ("2", "k_dec_gateup<64, 512, false>"): (2530.9, 9.8),
-    ("2", "k_matvec<8, 512, false>"): (1256.0, 3.5),
-    ("2", "k_dec_wo<8, 512, false>"): (579.0, 3.5),
-    ("3", "k_gemm_fast<2, 2, 1, 2, true>"): (6798.0, 4800.0),
-    ("4", "k_gemm_fast<2, 2, 2, 2, true>"): (627399.1, 75937.1),
-    ("5", "k_dec_attn_rows<128, 4, false, false>"): (266834.6, 8192.0),
+    ("1", "k_matvec<8, 128, false>"): (330.9, 4.5, "r2"),
+    ("2", "k_dec_attn<64, 8, false, false, 1, true>"): (2697.2, 35.5, "r2"),
+    ("2", "k_dec_gateup<64, 512, false>"): (2530.9, 9.8, "r2"),
+    ("2", "k_matvec<8, 512, false>"): (1256.0, 3.5, "r2"),
+    ("2", "k_dec_wo<8, 512, false>"): (579.0, 3.5, "r2"),
+    ("3", "k_gemm_fast<2, 2, 1, 2, true>"): (6798.0, 4800.0, "r2"),
+    ("4", "k_gemm_fast<2, 2, 2, 2, true>"): (627399.1, 75937.1, "r2"),
+    ("5", "k_dec_attn_rows<128, 4, false, false>"): (266834.6, 8192.0, "r2"),
 }
 FETCH_SCALE, WRITE_SCALE = 2.000, 1.000
+_DIGEST = None
+
+
+def csrc_digest():
+    """sha256 (first 12 hex digits) of the HIP sources (csrc/*.hip, *.hpp)."""
+    global _DIGEST
+    if _DIGEST is None:
+        h = hashlib.sha256()
+        d = os.path.join(ROOT, "simple-inference_amd", "csrc")
+        for f in sorted(os.listdir(d)):
+            if f.endswith((".hip", ".hpp")):
+                h.update(f.encode())
+                with open(os.path.join(d, f), "rb") as fh:
+                    h.update(fh.read())
+        _DIGEST = h.hexdigest()[:12]
+    return _DIGEST
 
 
 def pmc_traffic(cfg, kernel):
-    f, w = PMC_KIB.get((cfg, kernel), (None, None))
-    return None if f is None else round((f * FETCH_SCALE + w * WRITE_SCALE) * 1024)
+    """(bytes per launch or None, digest the counters were read at or None)."""
+    f, w, src = PMC_KIB.get((cfg, kernel), (None, None, None))
+    return (None, None) if f is None else (round((f * FETCH_SCALE + w * WRITE_SCALE) * 1024), src)
 
 
 def log(*a):
@@ -98,27 +122,41 @@ def gemm_int_ops(shape, m):
     return 2 * m * ((QD + 2 * KVD) * H + H * QD + 2 * F * H + H * F)
 
 
-def graph_time_ms(torch, stream, fn, count, replays=3):
-    """Capture fn(0..count-1) into one HIP graph on `stream`, replay it on the
-    same stream and return the mean milliseconds per fn call, timed with HIP
-    events recorded on that stream around the replays.  The launches are
-    enqueued by C code through ctypes; replaying the graph removes the
-    host-side issue cost, so the events time the GPU work."""
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=stream):
-        for i in range(count):
-            fn(i)
+def graph_time(torch, stream, fn, count, replays=5, offsets=(0,)):
+    """Capture fn(o), fn(o + 1), ..., fn(o + count - 1) into one HIP graph per
+    offset o on `stream`; replay each graph once to warm up, then `replays`
+    times in turn (graph r % len(offsets)), each replay timed alone with HIP
+    events recorded on that stream.  Returns ms per fn call: the median over
+    the replays ("ms"), their min and max.  The launches are enqueued by C
+    code through ctypes; replaying a graph removes the host-side issue cost,
+    so the events time the GPU work."""
+    graphs = []
+    for o in offsets:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for i in range(count):
+                fn(o + i)
+        graphs.append(g)
+    per = []
     with torch.cuda.stream(stream):
-        g.replay()  # warm
+        for g in graphs:
+            g.replay()
         stream.synchronize()
         t = Timer(torch, stream)
-        t.start()
-        for _ in range(replays):
-            g.replay()
-        ms = t.stop_ms() / (replays * count)
+        for r in range(replays):
+            t.start()
+            graphs[r % len(graphs)].replay()
+            per.append(t.stop_ms() / count)
     torch.cuda.synchronize()
-    del g
-    return ms
+    del graphs
+    return dict(ms=float(np.median(per)), min=float(np.min(per)), max=float(np.max(per)),
+                replays=replays, graphs=len(offsets), steps_per_replay=count)
+
+
+def spread_us(gt):
+    """The replay statistics of graph_time in microseconds per step."""
+    return {"median": round(gt["ms"] * 1e3, 3), "min": round(gt["min"] * 1e3, 3),
+            "max": round(gt["max"] * 1e3, 3), "replays": gt["replays"]}
 
 
 def kernel_sequence(si_amd, fn, kernel_filter, capacity=16384):
@@ -143,8 +181,10 @@ def roofline_entry(kernel, us, work, bound, cfg, launches):
         achieved, peak, unit = work / (us * 1e-6) / 1e9, HBM_PEAK_GBS, "GB/s"
     else:
         achieved, peak, unit = work / (us * 1e-6) / 1e12, INT8_PEAK_TOPS, "TOP/s"
+    traffic, src = pmc_traffic(cfg, kernel)
     return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
-            "frac": round(achieved / peak, 4), "traffic": pmc_traffic(cfg, kernel),
+            "frac": round(achieved / peak, 4), "traffic": traffic,
+            "traffic_src": src, "traffic_current": None if src is None else src == csrc_digest(),
             "kernel": kernel, "kernel_us": round(us, 3), "launches": launches,
             ("alg_bytes_per_launch" if bound == "hbm" else "int_ops_per_launch"): int(work),
             "timing": "mean of per-dispatch HIP events (si_kernel_timing_*)"}
@@ -261,9 +301,10 @@ def bench_decode_layer(torch, si_amd, stream, steps, warmup, ctx=1024, shape_nam
                 acc[k] = acc.get(k, 0.0) + v / 20
         layers[0].set_timing(False)
         torch.cuda.synchronize()
-        # per-dispatch durations of the step's kernels over min(steps, 200)
-        # eager steps (the same rotation of copies), by position in the step
-        nk = min(steps, 200)
+        # per-dispatch durations of the step's kernels over whole rotations
+        # of the copies (every copy visited, about 200 steps), by position in
+        # the step
+        nk = copies * max(1, 200 // copies)
         seq = kernel_sequence(si_amd, lambda: [step(i) for i in range(nk)],
                               "k_dec_|k_matvec<")
         torch.cuda.synchronize()
@@ -271,14 +312,30 @@ def bench_decode_layer(torch, si_amd, stream, steps, warmup, ctx=1024, shape_nam
     per = len(phases)
     assert len(seq) == per * nk, f"{len(seq)} timed launches for {nk} steps"
     kern = {ph: (seq[j][0], [us for _, us in seq[j::per]]) for j, ph in enumerate(phases)}
-    # timed region: exactly `steps` decode steps, captured as one HIP graph
-    ms = graph_time_ms(torch, stream, step, steps, replays=3)
+    # timed region: exactly `steps` decode steps per replay, one HIP graph per
+    # starting copy; with fewer steps than copies the graphs start `steps`
+    # copies apart and are replayed in turn, so consecutive replays walk the
+    # whole rotation and a copy is reused only after every other copy
+    # (copies x per_copy bytes, 1.25 x the Infinity Cache) has been touched
+    ngraphs = 1 if steps >= copies else -(-copies // steps)
+    offsets = [(j * steps) % copies for j in range(ngraphs)]
+    gt = graph_time(torch, stream, step, steps, replays=max(5, 2 * ngraphs), offsets=offsets)
+    ms = gt["ms"]
     alg = per_copy
+    kus = {ph: float(np.mean(v)) for ph, (n, v) in kern.items()}
     res = dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, alg_bytes=alg, copies=copies,
+               spread_us=spread_us(gt),
+               rotation={"copies": copies, "bytes_per_copy": per_copy,
+                         "graphs": ngraphs, "steps_per_replay": steps,
+                         "copies_per_replay": min(steps, copies),
+                         "bytes_between_reuse_of_a_copy": copies * per_copy,
+                         "infinity_cache_bytes": MALL_BYTES},
                eager_us=eager_ms * 1e3,
                phases_us_eager={k: round(v * 1e3, 2) for k, v in acc.items()},
-               kernels={ph: {"kernel": n, "us": round(float(np.mean(v)), 3), "launches": len(v)}
-                        for ph, (n, v) in kern.items()})
+               kernels={ph: {"kernel": n, "us": round(kus[ph], 3), "launches": len(v)}
+                        for ph, (n, v) in kern.items()},
+               kernels_sum_us=round(sum(kus.values()), 3),
+               step_minus_kernels_us=round(ms * 1e3 - sum(kus.values()), 3))
     return res, (layers, caches, s, x, ws)
 
 
@@ -337,10 +394,12 @@ def bench_qkv_gemv(torch, si_amd, stream, launches=1000):
         kern = kernel_durations(si_amd, lambda: [launch(i) for i in range(launches)],
                                 "k_matvec<")
         torch.cuda.synchronize()
-    ms = graph_time_ms(torch, stream, launch, launches, replays=3)
+    gt = graph_time(torch, stream, launch, launches, replays=5)
+    ms = gt["ms"]
     alg = 586168  # W 580,608 + x 952 + y 4,608 bytes (config 1)
     name, durs = next(iter(kern.items()))
     return dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, copies=copies,
+                spread_us=spread_us(gt),
                 timing="HIP graph of the launches (us includes the launch-to-launch gap)",
                 roofline=roofline_entry(name, float(np.mean(durs)), alg, "hbm", "1", len(durs)))
 
@@ -382,12 +441,63 @@ def bench_gemv_7b(torch, si_amd, stream, launches=200):
             for i in range(copies + 5):
                 launch(i)
         torch.cuda.synchronize()
-        ms = graph_time_ms(torch, stream, launch, launches, replays=2)
+        ms = graph_time(torch, stream, launch, launches, replays=5)["ms"]
         alg = per + k + (k // 32) * 4 + n * 4
         gbs = alg / (ms * 1e-3) / 1e9
         res[name] = dict(n=n, k=k, tile=tile, us=round(ms * 1e3, 3), gbs=round(gbs, 1),
                          hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
         del mats
+        torch.cuda.empty_cache()
+    return res
+
+
+def bench_stream_read(torch, si_amd, stream, sizes_mb=(9, 76, 537), launches=40):
+    """The plain streaming-read ceiling (si_stream_read: one pass, 16-byte
+    loads, nothing else) at the traffic sizes of the path's kernels: ~9 MB
+    (the 0.5B decode layer, a 7B QKV mat-vec), 76 MB (the 7B gate|up
+    matrix), 537 MB (config 5's K/V cache).  Buffers are rotated over enough
+    copies to exceed the Infinity Cache; each size is swept over grids of
+    256 to 8192 workgroups and 4, 8 or 16 loads in flight per thread and
+    the best is reported, per launch in a HIP graph (back-to-back) and per
+    dispatch (HIP events on the dispatch)."""
+    L = si_amd.lib()
+    res = {}
+    for mb in sizes_mb:
+        nbytes = (mb * 1000 * 1000) // 4096 * 4096
+        copies = max(1, int(np.ceil(1.25 * MALL_BYTES / nbytes)))
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+        for b in bufs:
+            b.fill_(1)
+        sink = torch.empty(8192, dtype=torch.int32, device="cuda")
+        best = None
+        for wgs, depth in [(w, dp) for w in (256, 512, 1024, 2048, 4096, 8192)
+                           for dp in (4, 8, 16)]:
+            def launch(i, wgs=wgs, depth=depth):
+                si_amd.call("si_stream_read", si_amd.ptr(bufs[i % copies]), nbytes,
+                            si_amd.ptr(sink), wgs, depth,
+                            si_amd.stream_handle(torch.cuda.current_stream()))
+            n = max(launches // 2, copies)
+            with torch.cuda.stream(stream):
+                for i in range(copies):
+                    launch(i)
+            torch.cuda.synchronize()
+            ms = graph_time(torch, stream, launch, n, replays=5)["ms"]
+            with torch.cuda.stream(stream):
+                d = kernel_durations(si_amd, lambda: [launch(i) for i in range(n)],
+                                     "k_stream_read")
+            torch.cuda.synchronize()
+            us_d = float(np.mean(next(iter(d.values()))))
+            if best is None or ms < best[1]:
+                best = (wgs, depth, ms, us_d)
+        wgs, depth, ms, us_d = best
+        res[f"{mb}MB"] = dict(bytes=nbytes, copies=copies, workgroups=wgs, depth=depth,
+                              us_graph=round(ms * 1e3, 3),
+                              gbs_graph=round(nbytes / (ms * 1e-3) / 1e9, 1),
+                              us_dispatch=round(us_d, 3),
+                              gbs_dispatch=round(nbytes / (us_d * 1e-6) / 1e9, 1),
+                              hbm_frac_dispatch=round(nbytes / (us_d * 1e-6) / 1e9 /
+                                                      HBM_PEAK_GBS, 4))
+        del bufs
         torch.cuda.empty_cache()
     return res
 
@@ -438,7 +548,7 @@ def bench_attention_modes(torch, si_amd, shape_name="7b", ctx=4096, count=100):
             for i in range(4):
                 fn(i)
         torch.cuda.synchronize()
-        ms = graph_time_ms(torch, stream, fn, count)
+        ms = graph_time(torch, stream, fn, count, replays=5)["ms"]
         res[name + "_us"] = round(ms * 1e3, 3)
         res[name + "_gbs"] = round(alg / (ms * 1e-3) / 1e9, 1)
     res["speedup_flash"] = round(res["standard_us"] / res["flash_us"], 3)
@@ -507,22 +617,34 @@ def bench_prefill(torch, si_amd, stream, shape_name, ntok, steps):
         reps = max(2, min(steps, 5))
         kern = kernel_durations(si_amd, lambda: [call(i) for i in range(reps)], "k_")
         torch.cuda.synchronize()
-    ms = graph_time_ms(torch, stream, call, steps, replays=2)
+    gt = graph_time(torch, stream, call, steps, replays=5)
+    ms = gt["ms"]
     gemm_ms, gu = gemm_graph_ms(torch, si_amd, stream, lay, s, ntok, steps)
     ops = gemm_int_ops(s, ntok)
     lay.close()
     cfg = "3" if shape_name == "0.5b" else "4"
     per_call = {k: round(float(np.sum(v)) / reps, 3) for k, v in kern.items()}
     gname, gdur = max(gu.items(), key=lambda kv: len(kv[1]))
-    return dict(ms=ms, tokens_per_s=ntok / (ms * 1e-3),
+    gu_ops = 2 * ntok * 2 * s.ffn * s.hidden
+    # the dominant kernel (the gate|up GEMM) timed per dispatch inside the
+    # layer calls (the roofline), and the same instance launched alone on the
+    # layer's buffers (roofline_alone)
+    in_layer = kern.get(gname, gdur)
+    return dict(ms=ms, tokens_per_s=ntok / (ms * 1e-3), spread_us=spread_us(gt),
                 gemm_ms=gemm_ms, gemm_tops=ops / (gemm_ms * 1e-3) / 1e12,
                 mfma_pct_gemm=100.0 * ops / (gemm_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
                 mfma_pct_layer=100.0 * ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
                 gemm_timing="the four projections alone, one HIP graph (gemm_graph_ms)",
                 phases_ms={k: round(v, 4) for k, v in ph.items()},
                 kernels_us_per_call=dict(sorted(per_call.items(), key=lambda kv: -kv[1])),
-                roofline=roofline_entry(gname, float(np.mean(gdur)),
-                                        2 * ntok * 2 * s.ffn * s.hidden, "mfma", cfg, len(gdur)))
+                kernels_sum_us=round(sum(per_call.values()), 3),
+                step_minus_kernels_us=round(ms * 1e3 - sum(per_call.values()), 3),
+                roofline=dict(roofline_entry(gname, float(np.mean(in_layer)), gu_ops, "mfma",
+                                             cfg, len(in_layer)),
+                              where="inside the layer calls"),
+                roofline_alone=dict(roofline_entry(gname, float(np.mean(gdur)), gu_ops, "mfma",
+                                                   cfg, len(gdur)),
+                                    where="launched alone on the layer's buffers"))
 
 
 def gemm_graph_ms(torch, si_amd, stream, lay, s, m, steps):
@@ -563,7 +685,7 @@ def gemm_graph_ms(torch, si_amd, stream, lay, s, m, steps):
         gu = kernel_durations(si_amd, lambda: [gateup() for _ in range(max(3, steps))],
                               "k_gemm")
         torch.cuda.synchronize()
-    return graph_time_ms(torch, stream, step, steps, replays=2), gu
+    return graph_time(torch, stream, step, steps, replays=5)["ms"], gu
 
 
 def bench_batched_decode(torch, si_amd, stream, steps, nseq=64, ctx=4096):
@@ -593,13 +715,17 @@ def bench_batched_decode(torch, si_amd, stream, steps, nseq=64, ctx=4096):
         reps = max(2, min(steps, 5))
         kern = kernel_durations(si_amd, lambda: [call(i) for i in range(reps)], "k_")
         torch.cuda.synchronize()
-    ms = graph_time_ms(torch, stream, call, steps, replays=2)
+    gt = graph_time(torch, stream, call, steps, replays=5)
+    ms = gt["ms"]
     alg = weight_bytes(s) + nseq * 2 * ctx * kvd * 2 + small_bytes(s)
     lay.close()
     per_call = {k: round(float(np.sum(v)) / reps, 3) for k, v in kern.items()}
     res = dict(us=ms * 1e3, gbs=alg / (ms * 1e-3) / 1e9, alg_bytes=alg,
+               spread_us=spread_us(gt),
                phases_us={k: round(v * 1e3, 2) for k, v in ph.items()},
-               kernels_us_per_call=dict(sorted(per_call.items(), key=lambda kv: -kv[1])))
+               kernels_us_per_call=dict(sorted(per_call.items(), key=lambda kv: -kv[1])),
+               kernels_sum_us=round(sum(per_call.values()), 3),
+               step_minus_kernels_us=round(ms * 1e3 - sum(per_call.values()), 3))
     att = [k for k in kern if k.startswith("k_dec_attn")]
     if att:
         a = att[0]
@@ -644,7 +770,7 @@ def bench_paged_decode(torch, si_amd, stream, steps, nseq=64, ctx=4096, page_siz
         ph = lay.phase_ms()
         lay.set_timing(False)
     torch.cuda.synchronize()
-    ms = graph_time_ms(torch, stream, call, steps, replays=2)
+    ms = graph_time(torch, stream, call, steps, replays=5)["ms"]
     alg = weight_bytes(s) + nseq * 2 * ctx * kvd * 2 + small_bytes(s)
     lay.close()
     del kp, vp
@@ -674,7 +800,7 @@ def bench_paged_decode(torch, si_amd, stream, steps, nseq=64, ctx=4096, page_siz
     with torch.cuda.stream(stream):
         step(0)
     torch.cuda.synchronize()
-    ms_s = graph_time_ms(torch, stream, step, max(1, steps // 2), replays=2)
+    ms_s = graph_time(torch, stream, step, max(1, steps // 2), replays=5)["ms"]
     H.si_stack_destroy(st)
     res.update(stack_layers=nlayers, stack_step_us=round(ms_s * 1e3, 2),
                stack_us_per_layer=round(ms_s * 1e3 / nlayers, 2))
@@ -860,7 +986,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--profile", choices=sorted(WORKLOADS),
                     help="run one configuration's GPU legs only (for rocprofv3)")
-    ap.add_argument("--only", choices=["gguf-7b", "attention-7b", "paged-7b", "decode-7b"],
+    ap.add_argument("--only", choices=["gguf-7b", "attention-7b", "paged-7b", "decode-7b",
+                                       "stream-read"],
                     help="run one of the other measurements only")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -881,6 +1008,8 @@ def main():
             r = bench_attention_modes(torch, si_amd)
         elif args.only == "paged-7b":
             r = bench_paged_decode(torch, si_amd, stream, 5)
+        elif args.only == "stream-read":
+            r = bench_stream_read(torch, si_amd, stream)
         else:
             r, _ = bench_decode_layer(torch, si_amd, stream, 100, 10, ctx=4096, shape_name="7b")
         print(json.dumps({"only": args.only, **r}), flush=True)
@@ -898,6 +1027,9 @@ def main():
     log(f"  {dec['us']:.2f} us/token, {dec['gbs']:.1f} GB/s; kernels {dec['kernels']} "
         f"({time.time() - t0:.0f} s)")
     extra = {}
+    log("streaming-read ceiling (si_stream_read) at 9, 76 and 537 MB ...")
+    extra["stream_read_ceiling"] = bench_stream_read(torch, si_amd, stream)
+    log(f"  {extra['stream_read_ceiling']}")
     log("7B decode projections (k_matvec) ...")
     extra["gemv_7b_cold"] = bench_gemv_7b(torch, si_amd, stream)
     log(f"  {extra['gemv_7b_cold']}")
@@ -960,10 +1092,14 @@ def main():
         "config": {"workload": WORKLOADS["2"] + " (BASELINE configs[1])",
                    "hidden": 896, "qheads": 14, "kvheads": 2, "head_dim": 64, "ffn": 4864,
                    "context": 1024, "layer_copies_rotated": dec["copies"],
-                   "alg_bytes_per_step": dec["alg_bytes"]},
+                   "rotation": dec["rotation"], "alg_bytes_per_step": dec["alg_bytes"]},
         "decode_layer_us": round(dec["us"], 3),
+        "decode_layer_spread_us": dec["spread_us"],
+        "decode_kernels_sum_us": dec["kernels_sum_us"],
+        "decode_step_minus_kernels_us": dec["step_minus_kernels_us"],
         "decode_layer_us_eager": round(dec["eager_us"], 3),
-        "timing": "HIP graph replay of the K steps (one graph), HIP events on the bench stream",
+        "timing": "median over >= 5 replays of a HIP graph of the K steps (graphs starting at "
+                  "staggered layer copies, replayed in turn), HIP events on the bench stream",
         "roofline": dec["roofline"],
         "roofline_second": second[0] if second else None,
         "cpu_baseline": cpu.get("2"),

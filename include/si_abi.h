@@ -70,6 +70,18 @@ int si_kernel_timing_start(const char *filter, int capacity);
 int si_kernel_timing_stop(float *ms, int capacity, int *count);
 const char *si_kernel_timing_name(int i);
 
+/* Measurement only, no counterpart in the reference: one streaming pass
+ * over `bytes` (a multiple of 16, buf 16-byte aligned) of device memory
+ * with 16-byte loads, `depth` (4, 8 or 16) per thread in flight, the buffer
+ * cut into at most `workgroups` (1..65536) contiguous slices of 256-thread
+ * workgroups; workgroup i writes one word of a checksum to sink[i] (the
+ * XOR of all sink words equals the XOR of the buffer's 32-bit words; at
+ * most `workgroups` words are written).  Its rate at a kernel's traffic
+ * size is the plain-read ceiling that kernel's HBM fraction is compared
+ * against. */
+int si_stream_read(const void *buf, size_t bytes, uint32_t *sink, int workgroups, int depth,
+                   void *stream);
+
 /* defines.h:16-25 (HIDDEN, QHEADS, KVHEADS, HDIM, ROPE_BASE, RMS_EPS) as
  * runtime values; ffn is the build-defined SwiGLU width (0 = none). */
 typedef struct si_shape {

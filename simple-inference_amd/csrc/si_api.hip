@@ -484,6 +484,19 @@ int si_attention_static(const si_shape_t *s, const float *q, int nq, const uint1
                           (size_t)SI_ATTENTION_STATIC_MAX, stream);
 }
 
+int si_stream_read(const void *buf, size_t bytes, uint32_t *sink, int workgroups, int depth,
+                   void *stream) {
+    SI_REQUIRE(buf && sink, "stream_read: NULL pointer");
+    SI_REQUIRE(bytes > 0 && bytes % 16 == 0 && (uintptr_t)buf % 16 == 0,
+               "stream_read: %zu bytes: a positive multiple of 16 at a 16-byte aligned address",
+               bytes);
+    SI_REQUIRE(workgroups >= 1 && workgroups <= 65536, "stream_read: %d workgroups",
+               workgroups);
+    SI_REQUIRE(depth == 4 || depth == 8 || depth == 16, "stream_read: depth %d", depth);
+    launch_stream_read(buf, bytes, sink, workgroups, depth, S(stream));
+    return check_launch("si_stream_read");
+}
+
 int si_f32_to_f16(const float *src, uint16_t *dst, size_t n, void *stream) {
     SI_REQUIRE(n == 0 || (src && dst), "f32_to_f16: NULL pointer");
     SI_REQUIRE(n < ((size_t)1 << 40), "f32_to_f16: %zu values", n);

@@ -181,4 +181,7 @@ void launch_rmsnorm(const float *x, const float *gain, int rows, int n, float ep
 void launch_rope_inplace(float *heads, int nheads, int hdim, int position, const float *rc,
                          const float *rs, hipStream_t st);
 void launch_f16_convert(const void *src, void *dst, size_t n, bool to_half, hipStream_t st);
+// one streaming pass over bytes (a multiple of 16) of buf (si_stream.hip)
+void launch_stream_read(const void *buf, size_t bytes, uint32_t *sink, int workgroups,
+                        int depth, hipStream_t st);
 }  // namespace si

@@ -72,6 +72,7 @@ _SIGS = {
     "si_kernel_timing_start": (_I, [ctypes.c_char_p, _I]),
     "si_kernel_timing_stop": (_I, [_P, _I, ctypes.POINTER(_I)]),
     "si_kernel_timing_name": (ctypes.c_char_p, [_I]),
+    "si_stream_read": (_I, [_P, ctypes.c_size_t, _P, _I, _I, _P]),
     "si_q4_repack": (_I, [_P, _I, _I, _I, _P, _P, _P]),
     "si_q4_unpack": (_I, [_P, _P, _I, _I, _I, _P, _P]),
     "si_q4_tile": (_I, [_I, _I]),

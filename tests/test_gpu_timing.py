@@ -77,3 +77,22 @@ def test_kernel_timing_skips_captured_launches():
     got = si_amd.kernel_times_ms("k_quantize_q8_rows", capture_and_replay)
     assert got == []
     assert np.array_equal(qs.cpu().numpy(), np.full(rows * k, 127, np.int8))
+
+
+@pytest.mark.parametrize("nbytes,wgs,depth", [(16, 1, 4), (4096 * 16 + 48, 7, 8),
+                                              (9 << 20, 2048, 16), (9 << 20, 100, 8)])
+def test_stream_read_checksum(nbytes, wgs, depth):
+    """The streaming-read measurement kernel reads every byte once: the XOR
+    of its per-workgroup words equals the XOR of the buffer's 32-bit words
+    (any grid, depth and tail), and it refuses unaligned sizes."""
+    import torch
+    rng = np.random.default_rng(nbytes)
+    words = rng.integers(0, 1 << 32, nbytes // 4, dtype=np.uint64).astype(np.uint32)
+    buf = dev(words.view(np.int32))
+    sink = dev(np.zeros(wgs, np.int32))  # slices past the buffer write nothing
+    si_amd.call("si_stream_read", si_amd.ptr(buf), nbytes, si_amd.ptr(sink), wgs, depth, None)
+    got = np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32))
+    assert got == np.bitwise_xor.reduce(words)
+    with pytest.raises(si_amd.SiError):
+        si_amd.call("si_stream_read", si_amd.ptr(buf), nbytes - 4 if nbytes > 16 else 8,
+                    si_amd.ptr(sink), wgs, depth, None)
