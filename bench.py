@@ -619,7 +619,7 @@ def bench_prefill(torch, si_amd, stream, shape_name, ntok, steps):
         torch.cuda.synchronize()
     gt = graph_time(torch, stream, call, steps, replays=5)
     ms = gt["ms"]
-    gemm_ms, gu = gemm_graph_ms(torch, si_amd, stream, lay, s, ntok, steps)
+    gemm_ms, gu, gu16 = gemm_graph_ms(torch, si_amd, stream, lay, s, ntok, steps)
     ops = gemm_int_ops(s, ntok)
     lay.close()
     cfg = "3" if shape_name == "0.5b" else "4"
@@ -644,7 +644,14 @@ def bench_prefill(torch, si_amd, stream, shape_name, ntok, steps):
                               where="inside the layer calls"),
                 roofline_alone=dict(roofline_entry(gname, float(np.mean(gdur)), gu_ops, "mfma",
                                                    cfg, len(gdur)),
-                                    where="launched alone on the layer's buffers"))
+                                    where="launched alone on the layer's buffers"),
+                gateup_f16_formulation={
+                    k16: {"us": round(float(np.mean(v16)), 3),
+                          "mfma_frac": round(gu_ops / (float(np.mean(v16)) * 1e-6) / 1e12 /
+                                             INT8_PEAK_TOPS, 4),
+                          "launches": len(v16),
+                          "note": "SI_GEMM_F16, bit-identical results; launched alone"}
+                    for k16, v16 in gu16.items()})
 
 
 def gemm_graph_ms(torch, si_amd, stream, lay, s, m, steps):
@@ -666,12 +673,12 @@ def gemm_graph_ms(torch, si_amd, stream, lay, s, m, steps):
                     b(xq), b(xd), m, None, res, dst, ldo, 0, wsp, ws_bytes,
                     si_amd.stream_handle(torch.cuda.current_stream()))
 
-    def gateup():
+    def gateup(flags=0):
         qs, d, tile, n, k = W[2]
         # no gu / act outputs: the layer writes neither without SI_LAYER_CAPTURE
         si_amd.call("si_gemm_gateup_q8", ctypes.c_void_p(qs), ctypes.c_void_p(d), tile, F, k,
                     b("XQ2_QS"), b("XQ2_D"), m, None, None, b("ACTQ_QS"), b("ACTQ_D"),
-                    b("ACTQ_S"), 0, wsp, ws_bytes,
+                    b("ACTQ_S"), flags, wsp, ws_bytes,
                     si_amd.stream_handle(torch.cuda.current_stream()))
 
     def step(i):
@@ -680,12 +687,15 @@ def gemm_graph_ms(torch, si_amd, stream, lay, s, m, steps):
         gateup()
         gemm(W[3], "ACTQ_QS", "ACTQ_D", si_amd.ptr(out), H, b("H"))
 
-    # the gate|up GEMM (the prefill's time-dominant kernel) alone, per dispatch
+    # the gate|up GEMM (the prefill's time-dominant kernel) alone, per
+    # dispatch; and its f16 formulation (SI_GEMM_F16, bit-identical results)
     with torch.cuda.stream(stream):
         gu = kernel_durations(si_amd, lambda: [gateup() for _ in range(max(3, steps))],
                               "k_gemm")
+        gu16 = kernel_durations(si_amd, lambda: [gateup(si_amd.SI_GEMM_F16)
+                                                 for _ in range(max(3, steps))], "k_gemm")
         torch.cuda.synchronize()
-    return graph_time(torch, stream, step, steps, replays=5)["ms"], gu
+    return graph_time(torch, stream, step, steps, replays=5)["ms"], gu, gu16
 
 
 def bench_batched_decode(torch, si_amd, stream, steps, nseq=64, ctx=4096):

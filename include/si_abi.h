@@ -133,7 +133,13 @@ int si_q4q8_block_dots(const uint8_t *wqs, const uint16_t *wd, int n, int k,
                        const int8_t *xqs, const int16_t *xs, int32_t *dots,
                        void *stream);
 
-enum { SI_GEMM_EXACT = 1 }; /* flags of si_matvec_q4q8 / si_gemm_q4q8 */
+/* flags of si_matvec_q4q8 / si_gemm_q4q8 / si_gemm_gateup_q8.
+ * SI_GEMM_F16 (si_gemm_gateup_q8 only, not with SI_GEMM_EXACT, no K split):
+ * the same results bit for bit from f16 matrix-core products of the
+ * integer-valued operands (one fused multiply-add per output and block in
+ * place of a conversion and one); slower than the default int8 formulation
+ * at the layer shapes measured on MI355X, kept as the measured alternative. */
+enum { SI_GEMM_EXACT = 1, SI_GEMM_F16 = 2 };
 
 /* matvec_q4q8 (qwen_one_layer.c:148-162), one activation row:
  *   out[r] = residual[r] + (bias[r] + sum_b ((float)dot_b * w.d) * x.d)
@@ -172,7 +178,7 @@ size_t si_gemm_workspace(int m, int n, int k);
  * the intermediate: SI_GEMM_EXACT, or a plan that splits K (si_gemm_workspace
  * (m, 2f, k) > 0) given less workspace than that.  act and bsum may be NULL.
  * wqs, xqs, qs and act are 16-byte aligned.
- * flags: SI_GEMM_EXACT as for si_gemm_q4q8. */
+ * flags: SI_GEMM_EXACT as for si_gemm_q4q8, or SI_GEMM_F16. */
 int si_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, int k,
                       const int8_t *xqs, const uint16_t *xd, int m, float *gu, float *act,
                       int8_t *qs, uint16_t *d, int16_t *bsum, int flags, void *workspace,

@@ -516,6 +516,391 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
         }
 }
 
+// ===========================================================================
+// Fast path, f16 formulation (k_gemm_h16): the same products as k_gemm_fast
+// with one VALU operation per (row, column, block) instead of two.
+//
+// A Q8_0 value (-127..127) and a Q4_0 value (nibble - 8, -8..7) are exact
+// fp16 numbers, their products (|p| <= 1016) exact in fp32 and every partial
+// sum of a 32-wide block (|s| <= 32512 < 2^24) too, so two
+// v_mfma_f32_32x32x16_f16 over the block's 32 values give the block's
+// int32 dot exactly, already in fp32: the epilogue is the one fma by the
+// scale product (itself one f16 MFMA, as in k_gemm_fast), no conversion.
+// The results equal k_gemm_fast's bit for bit (same blocks in the same
+// order through the same fma; k_gemm_fast's 16x operands scale every term
+// by a power of two, which commutes with rounding).
+//
+// The operands are converted once per LDS stage, by all threads of the
+// workgroup while the stage is written to LDS, so each converted value
+// serves a whole tile of outputs:
+//   int8 b -> fp16: the byte b ^ 0x80 = b + 128 as the low byte of the half
+//     0x64xx is 1024 + b + 128 (one v_perm_b32 per pair), minus 1152 (one
+//     v_pk_add_f16 per pair), exact;
+//   nibble n -> fp16 n - 8: 0x6400 | n is 1024 + n, minus 1032, likewise.
+// LDS rows hold a block's 32 halves in element order, 80 bytes apart; two
+// stage buffers, the next stage converted and written while this one is
+// consumed, one barrier per stage.
+// Measured on the 7B gate|up GEMM (2048 x 37888 x 3584), bit-identical to
+// k_gemm_fast: 951-965 us for 128 x 256 workgroup tiles (8 wavefronts of
+// 2 x 2 MFMA tiles; 1121-1410 us for the other tilings tried) against
+// 745-822 us for k_gemm_fast.  Counters: the conversions are gone but the
+// operand conversion adds about as many VALU instructions back (42 per
+// thread per stage at 128 x 128), the matrix pipe works 1.5x the cycles
+// (two f16 MFMAs per block instead of one i8), LDS traffic doubles, and
+// neither pipe passes ~60 % busy (waits on LDS and barriers), so the
+// default path keeps the int8 formulation; SI_GEMM_F16 selects this one.
+// ===========================================================================
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+
+constexpr int H_KB = 2;   // K blocks per LDS stage
+constexpr int H_ST = 80;  // LDS bytes per (row, block): 32 halves + 16 bytes of padding
+
+// four int8 (one dword) -> four fp16, element order (two dwords)
+__device__ __forceinline__ void s8x4_to_h(uint32_t x, uint32_t &p0, uint32_t &p1) {
+    const uint32_t u = x ^ 0x80808080u;
+    const h2v bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    p0 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v, __builtin_amdgcn_perm(
+                                                                0x64646464u, u, 0x04010400u)) +
+                                          bias);
+    p1 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v, __builtin_amdgcn_perm(
+                                                                0x64646464u, u, 0x04030402u)) +
+                                          bias);
+}
+// four nibbles, one per byte (bits 0..3) -> four fp16 (nibble - 8)
+__device__ __forceinline__ void n4x4_to_h(uint32_t x, uint32_t &p0, uint32_t &p1) {
+    const h2v bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    p0 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v, __builtin_amdgcn_perm(
+                                                                0x64646464u, x, 0x04010400u)) +
+                                          bias);
+    p1 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v, __builtin_amdgcn_perm(
+                                                                0x64646464u, x, 0x04030402u)) +
+                                          bias);
+}
+
+template <int WM, int WN, int TM, int TN>
+struct H16Cfg {
+    static constexpr int NT = 64 * WM * WN;  // threads
+    static constexpr int BM = 32 * WM * TM, BN = 32 * WN * TN;
+    static constexpr int A_PIECES = BM * H_KB * 2;  // 16 int8 per piece
+    static constexpr int B_PIECES = BN * H_KB;      // 32 nibbles per piece
+    static constexpr int A_PT = (A_PIECES + NT - 1) / NT, B_PT = (B_PIECES + NT - 1) / NT;
+    static constexpr int SX_PT = (BM * H_KB + NT - 1) / NT, SW_PT = (BN * H_KB + NT - 1) / NT;
+    static constexpr int SW_TWIN = H_KB * BN + 8;  // as GemmCfg: w.d, padding, a zero copy
+    // one stage buffer: operands, then scales
+    static constexpr size_t buf_bytes() {
+        return (size_t)H_KB * (BM + BN) * H_ST + (size_t)(H_KB * BM + SW_TWIN + H_KB * BN) * 8;
+    }
+    // two stage buffers: the next stage is written while this one is used
+    static constexpr size_t lds_bytes() { return 2 * buf_bytes(); }
+};
+
+// Register staging of one stage (GemmStage's scheme for NT threads), the
+// operands converted to fp16 on their way into LDS.
+template <typename C>
+struct H16Stage {
+    v4i ra[C::A_PT], rb[C::B_PT];
+    uint16_t rsx[C::SX_PT], rsw[C::SW_PT];
+    uint32_t oa[C::A_PT], ob[C::B_PT], osx[C::SX_PT], osw[C::SW_PT];
+
+    __device__ __forceinline__ void init(int tile, int n, int nb, int m, int m0, int n0,
+                                         int gu_f) {
+        const int tid = threadIdx.x, k = nb * SI_QK;
+#pragma unroll
+        for (int i = 0; i < C::A_PT; ++i) {
+            const int p = min(tid + C::NT * i, C::A_PIECES - 1);
+            const int row = p / (H_KB * 2), blk = (p >> 1) % H_KB, half = p & 1;
+            oa[i] = (uint32_t)(min(m0 + row, m - 1) * k + blk * SI_QK + half * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < C::B_PT; ++i) {
+            const int p = min(tid + C::NT * i, C::B_PIECES - 1);
+            const int row = p / H_KB, blk = p % H_KB;
+            const int lr = min(n0 + row, n - 1);
+            ob[i] = (uint32_t)((blk * n + (gu_f ? gate_up_row(lr, gu_f) : lr)) * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < C::SX_PT; ++i) {
+            const int p = min(tid + C::NT * i, C::BM * H_KB - 1);
+            const int row = p / H_KB, blk = p % H_KB;
+            osx[i] = (uint32_t)((min(m0 + row, m - 1) * nb + blk) * 2);
+        }
+#pragma unroll
+        for (int i = 0; i < C::SW_PT; ++i) {
+            const int p = min(tid + C::NT * i, C::BN * H_KB - 1);
+            const int row = p / H_KB, blk = p % H_KB;
+            const int lr = min(n0 + row, n - 1);
+            osw[i] = (uint32_t)(q4_scale_index(gu_f ? gate_up_row(lr, gu_f) : lr, blk, nb, tile) *
+                                2);
+        }
+    }
+
+    __device__ __forceinline__ void load(const uint8_t *__restrict__ wqs,
+                                         const uint16_t *__restrict__ wd, int tile, int n, int nb,
+                                         const int8_t *__restrict__ xqs,
+                                         const uint16_t *__restrict__ xd, int m, int bs) {
+        const uint32_t k = (uint32_t)nb * SI_QK;
+        const __amdgpu_buffer_rsrc_t ra_s = buf_rsrc(xqs + (size_t)bs * SI_QK,
+                                                     (uint32_t)m * k - (uint32_t)bs * SI_QK);
+        const __amdgpu_buffer_rsrc_t rb_s = buf_rsrc(wqs + (size_t)bs * n * 16,
+                                                     (uint32_t)(nb - bs) * (uint32_t)n * 16);
+        const __amdgpu_buffer_rsrc_t rx_s = buf_rsrc(xd + bs, ((uint32_t)m * nb - bs) * 2);
+        const uint32_t wcount = (uint32_t)q4_scale_count(n, nb, tile);
+        const __amdgpu_buffer_rsrc_t rw_s = buf_rsrc(wd + (size_t)bs * tile,
+                                                     (wcount - (uint32_t)bs * tile) * 2);
+#pragma unroll
+        for (int i = 0; i < C::A_PT; ++i)
+            ra[i] = __builtin_amdgcn_raw_buffer_load_b128(ra_s, oa[i], 0, 0);
+#pragma unroll
+        for (int i = 0; i < C::B_PT; ++i)
+            rb[i] = __builtin_amdgcn_raw_buffer_load_b128(rb_s, ob[i], 0, 0);
+#pragma unroll
+        for (int i = 0; i < C::SX_PT; ++i)
+            rsx[i] = __builtin_amdgcn_raw_buffer_load_b16(rx_s, osx[i], 0, 0);
+#pragma unroll
+        for (int i = 0; i < C::SW_PT; ++i)
+            rsw[i] = __builtin_amdgcn_raw_buffer_load_b16(rw_s, osw[i], 0, 0);
+    }
+
+    __device__ __forceinline__ void store(uint8_t *a_l, uint8_t *b_l, v2u *sx_l,
+                                          v2u *sw_l) const {
+        const int tid = threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < C::A_PT; ++i) {
+            const int p = tid + C::NT * i;
+            if (C::A_PIECES % C::NT == 0 || p < C::A_PIECES) {
+                const int row = p / (H_KB * 2), blk = (p >> 1) % H_KB, half = p & 1;
+                uint32_t h[8];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) s8x4_to_h((uint32_t)ra[i][t], h[2 * t], h[2 * t + 1]);
+                uint8_t *dst = a_l + ((size_t)blk * C::BM + row) * H_ST + half * 32;
+                *(uint4 *)dst = make_uint4(h[0], h[1], h[2], h[3]);
+                *(uint4 *)(dst + 16) = make_uint4(h[4], h[5], h[6], h[7]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < C::B_PT; ++i) {
+            const int p = tid + C::NT * i;
+            if (C::B_PIECES % C::NT == 0 || p < C::B_PIECES) {
+                const int row = p / H_KB, blk = p % H_KB;
+                // byte t holds element t (low nibble) and t + 16 (high)
+                uint32_t lo[8], hi[8];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint32_t w = (uint32_t)rb[i][t];
+                    n4x4_to_h(w & 0x0f0f0f0fu, lo[2 * t], lo[2 * t + 1]);
+                    n4x4_to_h((w >> 4) & 0x0f0f0f0fu, hi[2 * t], hi[2 * t + 1]);
+                }
+                uint8_t *dst = b_l + ((size_t)blk * C::BN + row) * H_ST;
+                *(uint4 *)dst = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+                *(uint4 *)(dst + 16) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+                *(uint4 *)(dst + 32) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+                *(uint4 *)(dst + 48) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < C::SX_PT; ++i) {
+            const int p = tid + C::NT * i;
+            if ((C::BM * H_KB) % C::NT == 0 || p < C::BM * H_KB) {
+                const int row = p / H_KB, blk = p % H_KB;
+                sx_l[(size_t)blk * C::BM + row] = (v2u){(unsigned)rsx[i], 0u};
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < C::SW_PT; ++i) {
+            const int p = tid + C::NT * i;
+            if ((C::BN * H_KB) % C::NT == 0 || p < C::BN * H_KB) {
+                const int row = p / H_KB, blk = p % H_KB;
+                sw_l[(size_t)blk * C::BN + row] = (v2u){(unsigned)rsw[i], 0u};
+            }
+        }
+    }
+};
+
+// Same interface and epilogues as k_gemm_fast (FUSE: gate|up SwiGLU + Q8).
+template <int WM, int WN, int TM, int TN, bool FUSE>
+__global__ void __launch_bounds__(64 * WM * WN) k_gemm_h16(
+    const uint8_t *__restrict__ wqs, const uint16_t *__restrict__ wd, int tile, int n, int nb,
+    const int8_t *__restrict__ xqs, const uint16_t *__restrict__ xd, int m,
+    const float *__restrict__ bias, const float *__restrict__ residual, float *__restrict__ out,
+    int ldo, float *__restrict__ part, int bps, GateUpOut go) {
+    static_assert(!FUSE || TN == 2, "gate|up fusion pairs two column tiles per wavefront");
+    using C = H16Cfg<WM, WN, TM, TN>;
+    constexpr int BM = C::BM, BN = C::BN, NT = C::NT;
+    extern __shared__ __attribute__((aligned(16))) uint8_t hsm[];
+    // stage buffer q (0, 1): operands [H_KB][BM][H_ST], [H_KB][BN][H_ST],
+    // scales [H_KB][BM], [H_KB][BN], pad, zero copy
+    auto a_of = [&](int q) { return hsm + (size_t)q * C::buf_bytes(); };
+    auto b_of = [&](int q) { return a_of(q) + H_KB * BM * H_ST; };
+    auto sx_of = [&](int q) { return (v2u *)(b_of(q) + H_KB * BN * H_ST); };
+    auto sw_of = [&](int q) { return sx_of(q) + H_KB * BM; };
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int j = lane & 31, g = lane >> 5;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int b_begin = blockIdx.z * bps, b_end = min(nb, b_begin + bps);
+
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int i = 0; i < (H_KB * BN + NT - 1) / NT; ++i)  // the zero copies
+            if ((H_KB * BN) % NT == 0 || tid + NT * i < H_KB * BN)
+                sw_of(q)[C::SW_TWIN + tid + NT * i] = (v2u){0u, 0u};
+    H16Stage<C> stg;
+    float acc[TM][TN][16];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+
+    const int nstage = (b_end - b_begin + H_KB - 1) / H_KB;
+    const int last = b_begin + (nstage - 1) * H_KB;  // first block of the last stage
+    stg.init(tile, n, nb, m, m0, n0, FUSE ? go.f : 0);
+    stg.load(wqs, wd, tile, n, nb, xqs, xd, m, b_begin);
+    stg.store(a_of(0), b_of(0), sx_of(0), sw_of(0));
+    __syncthreads();
+    // stage st+1 in registers, then written to the other buffer while stage
+    // st is consumed; one barrier per stage (branch-free loads: past the
+    // last stage the last one is re-read and never stored)
+    stg.load(wqs, wd, tile, n, nb, xqs, xd, m, min(b_begin + H_KB, last));
+    for (int st = 0; st < nstage; ++st) {
+        const int cur = st & 1;
+        if (st + 1 < nstage) {
+            stg.store(a_of(cur ^ 1), b_of(cur ^ 1), sx_of(cur ^ 1), sw_of(cur ^ 1));
+            stg.load(wqs, wd, tile, n, nb, xqs, xd, m, min(b_begin + (st + 2) * H_KB, last));
+        }
+        const int bs = b_begin + st * H_KB;
+#pragma unroll
+        for (int blk = 0; blk < H_KB; ++blk) {
+            if (bs + blk >= b_end) break;
+            const uint8_t *ab = a_of(cur) + (size_t)blk * BM * H_ST;
+            const uint8_t *bb = b_of(cur) + (size_t)blk * BN * H_ST;
+            const v2u *sxb = sx_of(cur) + (size_t)blk * BM;
+            const v2u *swl = sw_of(cur) + (size_t)blk * BN + g * C::SW_TWIN;
+            h8v aop[TM][2], bop[TN][2];
+            gh4 asc[TM], bsc[TN];
+            // lane (j, g) of MFMA step s supplies elements 16 s + 8 g .. +7
+            // of row (A) / column (B) j, in both operands
+#pragma unroll
+            for (int a = 0; a < TM; ++a) {
+                const int r = (wm * TM + a) * 32 + j;
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+                    aop[a][s] = *(const h8v *)(ab + r * H_ST + 32 * s + 16 * g);
+                asc[a] = __builtin_bit_cast(gh4, sxb[r]);
+            }
+#pragma unroll
+            for (int b = 0; b < TN; ++b) {
+                const int c = (wn * TN + b) * 32 + j;
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+                    bop[b][s] = *(const h8v *)(bb + c * H_ST + 32 * s + 16 * g);
+                bsc[b] = __builtin_bit_cast(gh4, swl[c]);
+            }
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+#pragma unroll
+                for (int b = 0; b < TN; ++b) {
+                    v16f dot = {};
+                    dot = __builtin_amdgcn_mfma_f32_32x32x16_f16(aop[a][0], bop[b][0], dot, 0, 0, 0);
+                    dot = __builtin_amdgcn_mfma_f32_32x32x16_f16(aop[a][1], bop[b][1], dot, 0, 0, 0);
+                    v16f zf = {};
+                    const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(asc[a], bsc[b], zf, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[a][b][v] = fmaf(dot[v], sc[v], acc[a][b][v]);
+                }
+        }
+        // the stage written above is complete, and this one's reads are
+        // done before it is rewritten two stages on
+        __syncthreads();
+    }
+
+    // output (i, j) of a 32x32 tile: lane j + 32*((i/4)%2), register (i%4) + 4*(i/8)
+    if (FUSE) {
+        const int f = go.f;
+        const int fb = (n0 + wn * 64) / 2;  // the wavefront's 32 features: one Q8 block
+        const bool fok = fb < f;
+        constexpr int FT = 36;  // floats per LDS row (16-byte aligned rows)
+        static_assert((size_t)(NT / 64) * 32 * FT * 4 <= C::lds_bytes(),
+                      "the transposition fits the stage LDS");
+        float *tl = (float *)hsm + wave * (32 * FT);  // after the last barrier: free
+        const int rr = lane & 31, hh = lane >> 5;
+#pragma unroll
+        for (int a = 0; a < TM; ++a) {
+            const int r0 = m0 + (wm * TM + a) * 32;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int i = 8 * (v >> 2) + 4 * g + (v & 3);
+                const float gv = acc[a][0][v], uv = acc[a][TN - 1][v];
+                const float silu = __fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)));
+                tl[i * FT + j] = __fmul_rn(silu, uv);
+                if (out && r0 + i < m && fok) {
+                    out[(size_t)(r0 + i) * ldo + fb + j] = gv;
+                    out[(size_t)(r0 + i) * ldo + f + fb + j] = uv;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            float x[16];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float4 p = *(const float4 *)(tl + rr * FT + 16 * hh + 4 * t);
+                x[4 * t] = p.x;
+                x[4 * t + 1] = p.y;
+                x[4 * t + 2] = p.z;
+                x[4 * t + 3] = p.w;
+            }
+            __builtin_amdgcn_wave_barrier();
+            int q[16];
+            uint16_t dbits;
+            int bsum;
+            quant_block_pair16(x, q, dbits, bsum);
+            const int row = r0 + rr;
+            if (row < m && fok) {
+                const size_t o = (size_t)row * f + fb + 16 * hh;
+                if (go.act)
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        *(float4 *)(go.act + o + 4 * t) =
+                            make_float4(x[4 * t], x[4 * t + 1], x[4 * t + 2], x[4 * t + 3]);
+                uint32_t pk[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    pk[t] = (uint32_t)(q[4 * t] & 0xff) | (uint32_t)(q[4 * t + 1] & 0xff) << 8 |
+                            (uint32_t)(q[4 * t + 2] & 0xff) << 16 | (uint32_t)q[4 * t + 3] << 24;
+                *(uint4 *)(go.qs + o) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+                if (hh == 0) {
+                    go.d[o / SI_QK] = dbits;
+                    if (go.s) go.s[o / SI_QK] = (int16_t)bsum;
+                }
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const int col = n0 + (wn * TN + b) * 32 + j;
+            if (col >= n) continue;
+            const float bv = (part == nullptr && bias) ? bias[col] : 0.0f;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int row = m0 + (wm * TM + a) * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
+                if (row >= m) continue;
+                if (part) {
+                    part[((size_t)blockIdx.z * m + row) * n + col] = acc[a][b][v];
+                } else {
+                    float y = acc[a][b][v] + bv;
+                    if (residual) y = __fadd_rn(residual[(size_t)row * ldo + col], y);
+                    out[(size_t)row * ldo + col] = y;
+                }
+            }
+        }
+}
+
 // ---------------------------------------------------------------------
 // Batched-decode GEMM (m <= 64 activation rows; also the short-K one-tile
 // projections of prefill up to 512 rows, bd_takes).
@@ -985,6 +1370,25 @@ __global__ void __launch_bounds__(256) k_gemm_reduce4(const float *__restrict__ 
     *(float4 *)o = y;
 }
 
+// k_gemm_h16 launch: its stage LDS exceeds the default 64 KB limit.
+template <int WM, int WN, int TM, int TN, bool FUSE>
+static void launch_h16(dim3 grid, const uint8_t *wqs, const uint16_t *wd, int tile, int n, int nb,
+                       const int8_t *xqs, const uint16_t *xd, int m, const float *bias,
+                       const float *residual, float *out, int ldo, float *part, int bps,
+                       const GateUpOut &go, hipStream_t st) {
+    using C = H16Cfg<WM, WN, TM, TN>;
+    static bool big_lds = false;
+    if (!big_lds) {
+        // a failure here surfaces as the launch's error
+        (void)hipFuncSetAttribute((const void *)k_gemm_h16<WM, WN, TM, TN, FUSE>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)C::lds_bytes());
+        big_lds = true;
+    }
+    SI_LAUNCH((k_gemm_h16<WM, WN, TM, TN, FUSE>), grid, dim3(C::NT), C::lds_bytes(), st, wqs, wd,
+              tile, n, nb, xqs, xd, m, bias, residual, out, ldo, part, bps, go);
+}
+
 // Tile choice and K splits of the fast path for an m x n x nb problem.
 struct GemmPlan {
     int bm, bn, splits, bps;
@@ -1203,9 +1607,17 @@ static int gemm_core(const uint8_t *wqs, const uint16_t *wd, int tile, int n, in
 void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, int k,
                            const int8_t *xqs, const uint16_t *xd, int m, float *gu, float *act,
                            int8_t *qs, uint16_t *d, int16_t *s, bool exact, void *workspace,
-                           size_t ws_bytes, hipStream_t st) {
+                           size_t ws_bytes, hipStream_t st, bool f16) {
     if (m <= 0) return;
     const int n = 2 * f, nb = k / SI_QK;
+    if (f16 && !exact) {
+        // the f16 formulation: 128 x 256 tiles (the fastest of the tilings
+        // measured), one pass over K
+        launch_h16<2, 4, 2, 2, true>(dim3((n + 255) / 256, (m + 127) / 128, 1), wqs, wd, tile, n,
+                                     nb, xqs, xd, m, nullptr, nullptr, gu, n, nullptr, nb,
+                                     GateUpOut{f, act, qs, d, s}, st);
+        return;
+    }
     if (!exact && m <= BD_SMALL_M && nb <= BD_MAX_CB) {
         launch_bd(bd_plan(m, n, nb, 1), 1, wqs, wd, tile, n, nb, xqs, xd, m, nullptr, nullptr, gu,
                   n, nullptr, GateUpOut{f, act, qs, d, s}, st);

@@ -66,10 +66,11 @@ void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, i
                       const int8_t *xqs, const uint16_t *xd, int m, const float *bias,
                       const float *residual, float *out, int ldo, bool exact, void *workspace,
                       size_t ws_bytes, hipStream_t st);
+// f16: k_gemm_h16 (the f16 formulation) where the plan runs one fused pass
 void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, int k,
                            const int8_t *xqs, const uint16_t *xd, int m, float *gu, float *act,
                            int8_t *qs, uint16_t *d, int16_t *s, bool exact, void *workspace,
-                           size_t ws_bytes, hipStream_t st);
+                           size_t ws_bytes, hipStream_t st, bool f16 = false);
 size_t gemm_workspace_bytes(int m, int n, int k);
 // workspace launch_gemm_gateup_q8 uses for f features (0: never splits K)
 size_t gemm_gateup_workspace_bytes(int m, int f, int k);

@@ -25,6 +25,7 @@ SI_OK, SI_ERR_ARG, SI_ERR_HIP, SI_ERR_STATE, SI_ERR_NOMEM = range(5)
 SI_LAYER_FULL, SI_LAYER_ATTN_ONLY, SI_LAYER_EXACT, SI_LAYER_ATTN_STANDARD = 0, 1, 2, 4
 SI_LAYER_CAPTURE = 8
 SI_GEMM_EXACT = 1
+SI_GEMM_F16 = 2
 BUFFERS = ["NORMED", "XQ_QS", "XQ_D", "XQ_S", "QKV", "Q", "ATTN", "ATTQ_QS", "ATTQ_D",
            "ATTQ_S", "ATTN_OUT", "H", "NORMED2", "XQ2_QS", "XQ2_D", "XQ2_S", "GU", "ACT",
            "ACTQ_QS", "ACTQ_D", "ACTQ_S"]

@@ -656,3 +656,39 @@ def test_gemm_gateup_q8(oracle, m, f, k, tile, flags, act_out):
     assert np.array_equal(host(aq), want_q)
     assert np.array_equal(host(ad).view(np.uint16), want_d)
     assert np.array_equal(host(asum), want_s)
+
+
+@pytest.mark.parametrize("m,f,k", [(130, 96, 256), (600, 4864, 896), (2048, 18944, 3584),
+                                   (77, 160, 3840)])
+def test_gemm_gateup_f16_formulation_bit_identical(oracle, m, f, k):
+    """SI_GEMM_F16 (f16 matrix-core products of the integer-valued operands,
+    converted once per LDS stage) gives the default int8 formulation's
+    gate|up, SwiGLU and Q8_0 bit for bit: both form each block's exact dot
+    and apply the same fused multiply-adds in the same order.  Ragged rows
+    and columns included; SI_GEMM_EXACT with it is refused."""
+    torch = _torch()
+    rng = np.random.default_rng(m + 3 * f)
+    w = np.concatenate([q4(oracle, rng, f, k), q4(oracle, rng, f, k)])
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    qs, d, _ = aos_to_planar(oracle.quantize_q8(x))
+    wqs, wd, _ = _upload_q4(w, 2 * f, k, 32)
+    xqs_d, xd_d = dev(qs), dev(d.view(np.int16))
+    outs = []
+    for flags in (0, si_amd.SI_GEMM_F16):
+        gu = empty(m * 2 * f, torch.float32)
+        act = empty(m * f, torch.float32)
+        aq, ad = empty(m * f, torch.int8), empty(m * f // 32, torch.int16)
+        asum = empty(m * f // 32, torch.int16)
+        # no workspace: the default formulation also runs one pass over K
+        # (a K split would add its partial sums in another order)
+        si_amd.call("si_gemm_gateup_q8", si_amd.ptr(wqs), si_amd.ptr(wd), 32, f, k,
+                    si_amd.ptr(xqs_d), si_amd.ptr(xd_d), m, si_amd.ptr(gu), si_amd.ptr(act),
+                    si_amd.ptr(aq), si_amd.ptr(ad), si_amd.ptr(asum), flags, None, 0, None)
+        outs.append([host(t) for t in (gu, act, aq, ad, asum)])
+    for name, a, b in zip(("gate|up", "act", "q", "d", "sums"), *outs):
+        assert np.array_equal(np.asarray(a).view(np.uint8), np.asarray(b).view(np.uint8)), name
+    with pytest.raises(si_amd.SiError):
+        si_amd.call("si_gemm_gateup_q8", si_amd.ptr(wqs), si_amd.ptr(wd), 32, f, k,
+                    si_amd.ptr(xqs_d), si_amd.ptr(xd_d), m, si_amd.ptr(gu), None, si_amd.ptr(aq),
+                    si_amd.ptr(ad), None, si_amd.SI_GEMM_EXACT | si_amd.SI_GEMM_F16, None, 0,
+                    None)
