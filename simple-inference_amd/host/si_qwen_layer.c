@@ -12,10 +12,16 @@
  *   - compare: both methods on the same tensors, alternating order, the
  *     table with both columns plus attention / Q8 / output agreement
  *     (report_compare, :421-511);
- *   - fused / soa-staged / soa-fused: the fused decode kernels, summary
- *     line (:687-701); there is no scratchpad staging on the GPU, so the
- *     staged variants run the same kernels;
- *   - fused-compare: staged flash vs fused (report_fusion, :526-594).
+ *   - fused / soa-staged / soa-fused: run_layer_legacy_fused on the
+ *     reference's column-SoA tiles (q.colsoa, kv.colsoa, o.colsoa, as
+ *     repack_weights.py writes them; fused_weights_load, :650) when the
+ *     weights directory holds them, or on tiles built from the synthetic
+ *     weights; for a shape with no column-SoA layout (hdim 64, odd heads per
+ *     group) or a directory without the files, the fused decode kernels.
+ *     Summary line (:687-701); there is no scratchpad staging on the GPU, so
+ *     the staged variant runs the same path;
+ *   - fused-compare: staged flash vs that fused path, alternating order
+ *     (report_fusion, :526-594).
  * The shape comes from SI_SHAPE (0.5b, 1.5b, 7b; default 1.5b, the
  * reference's compile-time shape, defines.h:16-25).  weights_dir holds the
  * files load_layer reads; "synthetic" generates seeded Q4_0 weights instead.
@@ -29,6 +35,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
 #include <hip/hip_runtime_api.h>
 
@@ -94,7 +101,10 @@ static int shape_named(const char *name, si_shape_t *s) {
 /* Seeded synthetic attention weights (no files): Q4_0 of uniform values in
  * +-0.05, norm gains 1 +- 0.1, biases +-0.02, from a stream separate from
  * the inputs'. */
-static si_model_t *synthetic_layer(const si_shape_t *s, int max_pos) {
+/* The synthetic layer; when fw is not NULL and the shape has a column-SoA
+ * layout, also its column-SoA tiles (*have_fw = 1). */
+static si_model_t *synthetic_layer(const si_shape_t *s, int max_pos, fused_weights_t *fw,
+                                   int *have_fw) {
     const size_t H = (size_t)s->hidden, QD = (size_t)s->qheads * s->hdim;
     const size_t KVD = (size_t)s->kvheads * s->hdim;
     const uint32_t saved = g_rng;
@@ -122,6 +132,16 @@ static si_model_t *synthetic_layer(const si_shape_t *s, int max_pos) {
     h.wq = w[0]; h.wk = w[1]; h.wv = w[2]; h.wo = w[3];
     h.norm = norm; h.bq = bq; h.bk = bk; h.bv = bv;
     si_model_t *m = si_model_from_host(s, &h, 1, max_pos);
+    if (fw && have_fw && si_colsoa_bytes(s, 0) > 0) {
+        uint8_t *t[3];
+        for (int i = 0; i < 3; ++i)
+            if (!(t[i] = malloc(si_colsoa_bytes(s, i))))
+                die("Out of memory building column-SoA tiles");
+        si_colsoa_repack_host(s, &h, t[0], t[1], t[2]);
+        *fw = si_fused_weights_from_host(m, t[0], t[1], t[2]);
+        *have_fw = 1;
+        for (int i = 0; i < 3; ++i) free(t[i]);
+    }
     for (int i = 0; i < 4; ++i) free(w[i]);
     free(norm); free(bq); free(bk); free(bv);
     g_rng = saved;
@@ -328,7 +348,8 @@ static void report_compare(const phase_t *st, const phase_t *fl, const si_model_
 static void report_fusion(const phase_t *base, const fused_stats_t *fused, const char *shape,
                           int context, int repeat, const float *y_ref, const float *y_fused,
                           const float *att_ref, const float *att_fused,
-                          const block_q8_0 *q8_ref, const block_q8_0 *q8_fused, int H, int QD) {
+                          const block_q8_0 *q8_ref, const block_q8_0 *q8_fused, int H, int QD,
+                          int legacy) {
     static const char *const names[9] = {"RMSNorm", "Quantize X", "Wq", "Wk", "Wv",
                                          "RoPE + KV append", "Online attention (GQA)",
                                          "Quantize O", "W_o"};
@@ -337,7 +358,8 @@ static void report_fusion(const phase_t *base, const fused_stats_t *fused, const
         ta += a[i] = phase_value(base, i);
         tb += b[i] = phase_value(&fused->phase, i);
     }
-    printf("\nQwen2 %s | STAGED FLASH vs FUSED DECODE KERNELS | MI355X\n", shape);
+    printf("\nQwen2 %s | STAGED FLASH vs %s | MI355X\n", shape,
+           legacy ? "COLUMN-SoA FUSED (run_layer_legacy_fused)" : "FUSED DECODE KERNELS");
     printf("One token | context=%d | repeats=%d/mode\n", context, repeat);
     puts("All weights remain 4-bit Q4_0; activations Q8_0; KV FP16.");
     puts("--------------------------------------------------------------------------");
@@ -376,7 +398,20 @@ static void report_fusion(const phase_t *base, const fused_stats_t *fused, const
     printf("             checksum baseline=%.10g fused=%.10g\n",
            checksum(y_ref, H, "Non-finite fused output"),
            checksum(y_fused, H, "Non-finite fused output"));
-    puts("On the GPU the staged flash layer already runs the fused decode kernels.\n");
+    puts(legacy ? "Fused path: the column-SoA tiles, per head pair, W_O accumulated per pair.\n"
+                : "On the GPU the staged flash layer already runs the fused decode kernels.\n");
+}
+
+/* Whether dir holds the three column-SoA tile files fused_weights_load
+ * reads. */
+static int has_colsoa_files(const char *dir) {
+    static const char *const names[3] = {"q.colsoa", "kv.colsoa", "o.colsoa"};
+    char path[4096];
+    for (int i = 0; i < 3; ++i) {
+        if (snprintf(path, sizeof path, "%s/%s", dir, names[i]) >= (int)sizeof path) return 0;
+        if (access(path, R_OK) != 0) return 0;
+    }
+    return 1;
 }
 
 /* ---- command line ---------------------------------------------------- */
@@ -384,7 +419,7 @@ static void report_fusion(const phase_t *base, const fused_stats_t *fused, const
 typedef enum { RUN_SINGLE, RUN_COMPARE, RUN_FUSED, RUN_FUSED_COMPARE } run_kind_t;
 
 /* The reference's modes (qwen_one_layer.c:610-629).  On the GPU the staged
- * and register-fused variants run the same fused decode kernels. */
+ * and register-fused variants run the same fused path (no scratchpad). */
 static const struct {
     const char *name;
     run_kind_t kind;
@@ -451,10 +486,15 @@ typedef struct {
     float *att[2];              /* host captures, or NULL */
     block_q8_0 *q8[2];
     attention_method_t method[2];
-    int fused[2];               /* slot runs run_layer_fused */
+    int fused[2];               /* slot runs the fused path */
+    const fused_weights_t *fw;  /* column-SoA tiles: run_layer_legacy_fused; NULL: run_layer_fused */
 } bench_t;
 
 static phase_t run_slot(const bench_t *b, int slot) {
+    if (b->fused[slot] && b->fw)
+        return run_layer_legacy_fused(b->l, b->fw, b->x, b->kc, b->vc, b->context,
+                                      b->out[slot], b->att[slot], b->q8[slot])
+            .phase;
     if (b->fused[slot])
         return run_layer_fused(b->l, NULL, b->x, b->kc, b->vc, b->context, b->out[slot],
                                b->att[slot], b->q8[slot])
@@ -485,8 +525,22 @@ int main(int argc, char **argv) {
     si_shape_t shape;
     if (!shape_named(shape_name, &shape)) die("SI_SHAPE must be 0.5b, 1.5b or 7b");
     const int ctx = cli.context, reps = cli.repeat;
-    si_model_t *l = !strcmp(cli.source, "synthetic") ? synthetic_layer(&shape, ctx)
-                                                     : load_layer(&shape, cli.source, 1, ctx);
+    const run_kind_t kind = MODES[cli.mode].kind;
+    const int fused_kind = kind == RUN_FUSED || kind == RUN_FUSED_COMPARE;
+    const int synthetic = !strcmp(cli.source, "synthetic");
+    fused_weights_t fw;
+    int have_fw = 0;
+    memset(&fw, 0, sizeof fw);
+    si_model_t *l = synthetic ? synthetic_layer(&shape, ctx, fused_kind ? &fw : NULL, &have_fw)
+                              : load_layer(&shape, cli.source, 1, ctx);
+    if (fused_kind && !synthetic && si_colsoa_bytes(&shape, 0) > 0 &&
+        has_colsoa_files(cli.source)) {
+        /* qwen_one_layer.c:647-650: FUSED_TCM / TCM_BLOCK as the reference
+         * reads them (a TCM request is refused: the GPU has no scratchpad) */
+        const char *tcm = getenv("FUSED_TCM"), *blk = getenv("TCM_BLOCK");
+        fw = fused_weights_load(l, cli.source, tcm && atoi(tcm) != 0, blk ? atoi(blk) : 0);
+        have_fw = 1;
+    }
     const int H = shape.hidden, QD = shape.qheads * shape.hdim, KVD = shape.kvheads * shape.hdim;
     const size_t kv_elems = (size_t)ctx * KVD;
 
@@ -506,6 +560,7 @@ int main(int argc, char **argv) {
     memset(&b, 0, sizeof b);
     b.l = l;
     b.context = ctx;
+    b.fw = have_fw ? &fw : NULL;
     hip_check(hipMalloc((void **)&b.x, (size_t)H * sizeof(float)), "hipMalloc");
     hip_check(hipMalloc((void **)&b.kc, kv_elems * 2), "hipMalloc");
     hip_check(hipMalloc((void **)&b.vc, kv_elems * 2), "hipMalloc");
@@ -524,7 +579,6 @@ int main(int argc, char **argv) {
 
     phase_t sums[2];
     memset(sums, 0, sizeof sums);
-    const run_kind_t kind = MODES[cli.mode].kind;
     if (kind == RUN_COMPARE || kind == RUN_FUSED_COMPARE) {
         /* slot 0: the staged path (standard, or flash against the fused
          * kernels); slot 1: flash or fused */
@@ -550,7 +604,7 @@ int main(int argc, char **argv) {
             memset(&fs, 0, sizeof fs);
             fs.phase = sums[1];
             report_fusion(&sums[0], &fs, shape_name, ctx, reps, y[0], y[1], att[0], att[1],
-                          q8[0], q8[1], H, QD);
+                          q8[0], q8[1], H, QD, have_fw);
         }
     } else {
         b.method[0] = MODES[cli.mode].method;
@@ -562,8 +616,10 @@ int main(int argc, char **argv) {
         } else {
             double total = 0.0;
             for (int i = 0; i < 9; ++i) total += phase_value(&sums[0], i);
-            printf("%s one-token | context=%d repeats=%d | MI355X fused decode kernels\n",
-                   MODES[cli.mode].banner, ctx, reps);
+            printf("%s one-token | context=%d repeats=%d | MI355X %s\n",
+                   MODES[cli.mode].banner, ctx, reps,
+                   have_fw ? "column-SoA tiles (run_layer_legacy_fused)"
+                           : "fused decode kernels");
             printf("Compute %.3f ms/token, staging %.3f ms/token, all %.3f ms/token\n",
                    total * 1e3 / reps, 0.0, total * 1e3 / reps);
             printf("Output checksum %.10g | first four %.6g %.6g %.6g %.6g\n",
@@ -577,6 +633,7 @@ int main(int argc, char **argv) {
         free(q8[s]);
         (void)hipFree(b.out[s]);
     }
+    if (have_fw) fused_weights_free(&fw);
     (void)hipFree(b.x);
     (void)hipFree(b.kc);
     (void)hipFree(b.vc);

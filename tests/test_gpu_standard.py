@@ -291,3 +291,59 @@ def test_cli_synthetic_7b_and_errors(tmp_path):
     assert _cli(["synthetic"], "13b").returncode == 1
     assert _cli([tmp_path, 16], "0.5b").returncode == 1  # no weight files
     assert _cli([], "0.5b").returncode == 2
+
+
+@pytest.fixture(scope="module")
+def weights_colsoa(tmp_path_factory, oracle):
+    """The reference's own 1.5B shape with its weight files and the
+    column-SoA tiles repack_weights.py would write next to them
+    (si_amd.repack, through the product's C repacker)."""
+    from si_amd import repack
+    sd = dict(si_amd.SHAPES["1.5b_ref"])
+    os_ = or_shape(**sd)
+    lay = make_layer(oracle, os_, 78, ffn=False)
+    d = tmp_path_factory.mktemp("w15")
+    _write_weights(d, lay)
+    repack.repack(str(d), "1.5b_ref")
+    return d, os_, lay
+
+
+@pytest.mark.parametrize("ctx", [1, 300])
+def test_cli_fused_compare_on_colsoa_files(oracle, weights_colsoa, ctx):
+    """fused-compare with the column-SoA files present compares two different
+    paths, as qwen_one_layer.c:650-686 does: the staged flash layer against
+    run_layer_legacy_fused on the tiles.  Both outputs agree with the
+    oracle's run_layer on the reference's input stream, the attention
+    outputs within 2e-3 and the Q8 blocks with at most a rounding flip."""
+    d, os_, lay = weights_colsoa
+    r = _cli([d, ctx, 2, "fused-compare"], "1.5b")
+    assert r.returncode == 0
+    assert "COLUMN-SoA FUSED (run_layer_legacy_fused)" in r.stdout
+    m = re.search(r"attention max_abs=(\S+), Q8 blocks different=(\d+)/(\d+)", r.stdout)
+    assert float(m.group(1).rstrip(",")) < 2e-3 and int(m.group(3)) == 48
+    assert int(m.group(2)) <= 2, r.stdout
+    cs = re.search(r"checksum baseline=(\S+) fused=(\S+)", r.stdout)
+    x, kc, vc = _ref_inputs(oracle, os_.hidden, os_.kvheads * os_.hdim, ctx)
+    want = oracle.run_layer(os_, lay, x, kc, vc, ctx).astype(np.float64)
+    tol = 2e-3 * float(np.abs(want).sum())
+    for v in cs.groups():
+        assert abs(float(v) - want.sum()) <= tol, (v, want.sum())
+    # the single fused mode runs the same tiles
+    r = _cli([d, ctx, 1, "soa-fused"], "1.5b")
+    assert r.returncode == 0 and "column-SoA tiles (run_layer_legacy_fused)" in r.stdout
+    c = float(re.search(r"Output checksum (\S+)", r.stdout).group(1))
+    assert abs(c - want.sum()) <= tol
+
+
+def test_cli_fused_synthetic_tiles_and_refusals(weights_colsoa):
+    """Synthetic weights at a column-SoA shape build their tiles; a TCM
+    request is refused (the GPU has no scratchpad to stage tiles in)."""
+    r = _cli(["synthetic", 64, 1, "fused-compare"], "1.5b")
+    assert r.returncode == 0 and "COLUMN-SoA FUSED" in r.stdout
+    m = re.search(r"Q8 blocks different=(\d+)/48", r.stdout)
+    assert int(m.group(1)) <= 2
+    d, _, _ = weights_colsoa
+    env_tcm = dict(os.environ, SI_SHAPE="1.5b", FUSED_TCM="1")
+    rr = subprocess.run([CLI, str(d), "16", "1", "fused"], env=env_tcm, capture_output=True,
+                        text=True, timeout=100)
+    assert rr.returncode == 1 and "scratchpad" in rr.stderr
