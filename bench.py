@@ -50,14 +50,14 @@ METRIC = "decode layer µs + HBM GB/s; prefill tokens/s + int8 MFMA % (one GPU)"
 # traffic with "traffic_current": false.  Kernels not listed report traffic
 # null.  Summaries: profiles/cfgN_*.md.
 PMC_KIB = {
-    ("1", "k_matvec<8, 128, false>"): (330.9, 4.5, "r2"),
-    ("2", "k_dec_attn<64, 8, false, false, 1, true>"): (2697.2, 35.5, "r2"),
-    ("2", "k_dec_gateup<64, 512, false>"): (2530.9, 9.8, "r2"),
-    ("2", "k_matvec<8, 512, false>"): (1256.0, 3.5, "r2"),
-    ("2", "k_dec_wo<8, 512, false>"): (579.0, 3.5, "r2"),
-    ("3", "k_gemm_fast<2, 2, 1, 2, true>"): (6798.0, 4800.0, "r2"),
-    ("4", "k_gemm_fast<2, 2, 2, 2, true>"): (627399.1, 75937.1, "r2"),
-    ("5", "k_dec_attn_rows<128, 4, false, false>"): (266834.6, 8192.0, "r2"),
+    ("1", "k_matvec<8, 128, false>"): (330.9, 4.5, "26b31f30a4a1"),
+    ("2", "k_dec_attn<64, 8, false, false, 1, true>"): (2709.0, 35.5, "26b31f30a4a1"),
+    ("2", "k_dec_gateup<64, 512, false>"): (2534.9, 9.8, "26b31f30a4a1"),
+    ("2", "k_matvec<8, 512, false>"): (1256.0, 3.5, "26b31f30a4a1"),
+    ("2", "k_dec_wo<8, 512, false>"): (571.6, 3.5, "26b31f30a4a1"),
+    ("3", "k_gemm_fast<2, 2, 1, 2, true>"): (6802.0, 4800.0, "26b31f30a4a1"),
+    ("4", "k_gemm_fast<2, 2, 2, 2, true>"): (626832.8, 75937.6, "26b31f30a4a1"),
+    ("5", "k_dec_attn_rows<128, 4, false, false>"): (266838.0, 8192.0, "26b31f30a4a1"),
 }
 FETCH_SCALE, WRITE_SCALE = 2.000, 1.000
 _DIGEST = None
