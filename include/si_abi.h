@@ -138,8 +138,23 @@ int si_q4q8_block_dots(const uint8_t *wqs, const uint16_t *wd, int n, int k,
  * the same results bit for bit from f16 matrix-core products of the
  * integer-valued operands (one fused multiply-add per output and block in
  * place of a conversion and one); slower than the default int8 formulation
- * at the layer shapes measured on MI355X, kept as the measured alternative. */
-enum { SI_GEMM_EXACT = 1, SI_GEMM_F16 = 2 };
+ * at the layer shapes measured on MI355X, kept as the measured alternative.
+ * SI_GEMM_TILED_A (si_gemm_q4q8 only, m <= 64, not with SI_GEMM_EXACT): xqs
+ * and xd hold the activations operand-tiled (si_q8_tile); the product runs
+ * in one pass over any K (no workspace) with each block's activations
+ * streamed next to its weights.  Per output the same sum as the default,
+ * in the same order where the default runs one pass. */
+enum { SI_GEMM_EXACT = 1, SI_GEMM_F16 = 2, SI_GEMM_TILED_A = 4 };
+
+/* Operand-tiled Q8_0 (the activation operand of SI_GEMM_TILED_A): rows in
+ * panels of 32 (the last padded: ceil(m/32) panels); block b of panel p is
+ * 1 KB at tq + (p * k/32 + b) * 1024, laid out [half g][row j][16 bytes],
+ * half g of row j holding the block's bytes 8g..8g+7 then 16+8g..16+8g+7;
+ * scales td[(p * k/32 + b) * 32 + j].  si_q8_tile writes it from planar
+ * qs [m][k] / d [m][k/32] (padding rows: zero).  No reference counterpart:
+ * a device layout of block_q8_0 (defines.h:27-28) for the matrix cores. */
+int si_q8_tile(const int8_t *qs, const uint16_t *d, int m, int k, int8_t *tq, uint16_t *td,
+               void *stream);
 
 /* matvec_q4q8 (qwen_one_layer.c:148-162), one activation row:
  *   out[r] = residual[r] + (bias[r] + sum_b ((float)dot_b * w.d) * x.d)
@@ -435,6 +450,8 @@ enum {
     SI_BUF_GU,          /* fp32 [rows][2 ffn] gate | up         */
     SI_BUF_ACT,         /* fp32 [rows][ffn]                     */
     SI_BUF_ACTQ_QS, SI_BUF_ACTQ_D, SI_BUF_ACTQ_S,
+    SI_BUF_ACTQ_TQ,     /* act Q8_0 operand-tiled, batched calls of 2..64 rows */
+    SI_BUF_ACTQ_TD,     /* (what the down projection read; else not written)  */
     SI_BUF_COUNT
 };
 void *si_layer_buffer(si_layer_t *l, int which);

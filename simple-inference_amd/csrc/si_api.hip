@@ -308,11 +308,30 @@ int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
     SI_REQUIRE(m == 0 || (wqs && wd && xqs && xd && out), "gemm: NULL pointer");
     SI_REQUIRE(((uintptr_t)wqs & 15) == 0 && ((uintptr_t)xqs & 15) == 0,
                "gemm: wqs and xqs must be 16-byte aligned");
-    SI_REQUIRE((flags & ~SI_GEMM_EXACT) == 0, "gemm: unknown flags %d", flags);
+    SI_REQUIRE((flags & ~(SI_GEMM_EXACT | SI_GEMM_TILED_A)) == 0, "gemm: unknown flags %d", flags);
+    if (flags & SI_GEMM_TILED_A) {
+        SI_REQUIRE(!(flags & SI_GEMM_EXACT), "gemm: SI_GEMM_TILED_A has no exact mode");
+        SI_REQUIRE(m <= 64, "gemm: SI_GEMM_TILED_A takes at most 64 rows (m=%d)", m);
+        launch_gemm_q4q8_tiled(wqs, wd, tile, n, k, xqs, xd, m, bias, residual, out, ldo,
+                               S(stream));
+        return check_launch("si_gemm_q4q8");
+    }
     launch_gemm_q4q8(wqs, wd, tile, n, k, xqs, xd, m, bias, residual, out, ldo,
                      (flags & SI_GEMM_EXACT) != 0, workspace, workspace ? ws_bytes : 0,
                      S(stream));
     return check_launch("si_gemm_q4q8");
+}
+
+int si_q8_tile(const int8_t *qs, const uint16_t *d, int m, int k, int8_t *tq, uint16_t *td,
+               void *stream) {
+    SI_REQUIRE(m >= 0 && k > 0 && k % 32 == 0, "q8_tile: bad size m=%d k=%d", m, k);
+    SI_REQUIRE((size_t)(m + 31) / 32 * 32 * k < ((size_t)1 << 31),
+               "q8_tile: operands beyond 2 GiB (m=%d k=%d)", m, k);
+    SI_REQUIRE(m == 0 || (qs && d && tq && td), "q8_tile: NULL pointer");
+    SI_REQUIRE(((uintptr_t)qs & 15) == 0 && ((uintptr_t)tq & 15) == 0,
+               "q8_tile: qs and tq must be 16-byte aligned");
+    launch_q8_tile(qs, d, m, k, tq, td, S(stream));
+    return check_launch("si_q8_tile");
 }
 
 int si_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, int k,
@@ -628,6 +647,8 @@ struct Q8Buf {
     int8_t *qs = nullptr;
     uint16_t *d = nullptr;
     int16_t *s = nullptr;
+    int8_t *tq = nullptr;    // optional operand-tiled copy (q8_tiled_byte), up to 64 rows
+    uint16_t *td = nullptr;
 };
 
 // Device allocations owned by one object, released with it.
@@ -731,6 +752,24 @@ static int make_workspace(const si_shape_t *s, int max_tokens, int max_pos,
         TRY(m.alloc(&W->actq.qs, M * F));
         TRY(m.alloc(&W->actq.d, M * F / 32));
         TRY(m.alloc(&W->actq.s, M * F / 32));
+    }
+    if (max_tokens >= 2) {
+        // operand-tiled copies of the four GEMM inputs for calls of 2..64
+        // rows (the projections then stream them); padding rows stay zero
+        const size_t tr = (size_t)(std::min(max_tokens, 64) + 31) / 32 * 32;
+        auto tiled = [&](Q8Buf &b, size_t k) -> int {
+            TRY(m.alloc(&b.tq, tr * k));
+            TRY(m.alloc(&b.td, tr * k / 32));
+            HIP_TRY(hipMemset(b.tq, 0, tr * k));
+            HIP_TRY(hipMemset(b.td, 0, tr * k / 32 * sizeof(uint16_t)));
+            return SI_OK;
+        };
+        TRY(tiled(W->xq, H));
+        TRY(tiled(W->attq, QD));
+        if (W->ffn) {
+            TRY(tiled(W->xq2, H));
+            TRY(tiled(W->actq, F));
+        }
     }
     // attention partials: the split count depends on the row count, so the
     // size is the worst case over 1..max_tokens rows of either schedule
@@ -955,6 +994,8 @@ void *si_layer_buffer(si_layer_t *L, int which) {
         case SI_BUF_ACTQ_QS: return L->actq.qs;
         case SI_BUF_ACTQ_D: return L->actq.d;
         case SI_BUF_ACTQ_S: return L->actq.s;
+        case SI_BUF_ACTQ_TQ: return L->actq.tq;
+        case SI_BUF_ACTQ_TD: return L->actq.td;
         default: return nullptr;
     }
 }
@@ -1145,13 +1186,23 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
     const bool cap = (flags & SI_LAYER_CAPTURE) != 0;
     SI_REQUIRE(!full || L->ffn, "layer has no FFN weights: use SI_LAYER_ATTN_ONLY");
     for (bool &h : L->phase_hit) h = false;
+    // 2..64 rows, not exact: every Q8 activation is also written operand-
+    // tiled and the projections stream it (k_gemm_bd's streamed mode)
+    const bool ex = (flags & SI_LAYER_EXACT) != 0;
+    const bool tl = rows >= 2 && rows <= 64 && !ex && L->xq.tq;
     // qwen_one_layer.c:247-250: RMSNorm -> Q8
     mark(L, SI_PHASE_RMS_Q8, st);
     launch_rmsnorm_q8(x, nullptr, L->norm, rows, H, s.rms_eps, nullptr, capt(cap, L->normed),
-                      L->xq.qs, L->xq.d, L->xq.s, st);
+                      L->xq.qs, L->xq.d, L->xq.s, st, tl ? L->xq.tq : nullptr,
+                      tl ? L->xq.td : nullptr);
     // :253-258: Q, K, V projections (+bias), fused into one N = qd + 2 kvd matrix
     mark(L, SI_PHASE_QKV, st);
-    project(L, L->wqkv, rows, L->xq, L->bqkv, nullptr, L->qkv, flags, st);
+    if (tl)
+        launch_gemm_q4q8_tiled(L->wqkv.qs, L->wqkv.d, L->wqkv.tile, NQKV, H, L->xq.tq, L->xq.td,
+                               rows, L->bqkv, nullptr, L->qkv, NQKV, st);
+    else
+        project(L, L->wqkv, rows, L->xq, L->bqkv, nullptr, L->qkv, flags, st);
+    bool tl_att = false;  // the attention's Q8 written operand-tiled too
     if (ctx_step == 0) {
         // batched decode: RoPE + K/V append inside the attention kernel,
         // contiguous caches or a paged pool (pg)
@@ -1167,8 +1218,10 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
                             L->rope_sin, kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx,
                             capt(cap, L->q), ns, L->attn_ws, nullptr, nullptr, nullptr, nullptr,
                             st, pg);
+            tl_att = tl;
             launch_attn_combine(rows, s.qheads, s.hdim, ns, L->attn_ws, L->attn, L->attq.qs,
-                                L->attq.d, L->attq.s, st);
+                                L->attq.d, L->attq.s, st, tl ? L->attq.tq : nullptr,
+                                tl ? L->attq.td : nullptr);
         }
     } else {
         mark(L, SI_PHASE_ROPE_KV, st);
@@ -1195,20 +1248,30 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
     }
     // W_O; a K-split leaves its partials to the post-norm kernel, which sums
     // them (o, kept in attn_out) on the way
-    const int osplits = launch_gemm_q4q8_parts(L->wo.qs, L->wo.d, L->wo.tile, L->wo.n, L->wo.k,
-                                               L->attq.qs, L->attq.d, rows, L->attn_out,
-                                               (flags & SI_LAYER_EXACT) != 0, L->gemm_ws,
-                                               L->gemm_ws_bytes, st);
+    int osplits = 0;
+    if (tl_att)
+        launch_gemm_q4q8_tiled(L->wo.qs, L->wo.d, L->wo.tile, L->wo.n, L->wo.k, L->attq.tq,
+                               L->attq.td, rows, nullptr, nullptr, L->attn_out, L->wo.n, st);
+    else
+        osplits = launch_gemm_q4q8_parts(L->wo.qs, L->wo.d, L->wo.tile, L->wo.n, L->wo.k,
+                                         L->attq.qs, L->attq.d, rows, L->attn_out, ex,
+                                         L->gemm_ws, L->gemm_ws_bytes, st);
     mark(L, SI_PHASE_POST_NORM_Q8, st);
     // build-defined FFN half: h = x + o; RMSNorm -> Q8; gate|up; SwiGLU -> Q8; down + h
     if (osplits > 1)
         launch_rmsnorm_q8_parts(x, (const float *)L->gemm_ws, osplits, L->post_norm, rows, H,
                                 s.rms_eps, L->attn_out, L->h, capt(cap, L->normed2), L->xq2.qs,
-                                L->xq2.d, L->xq2.s, st);
+                                L->xq2.d, L->xq2.s, st, tl ? L->xq2.tq : nullptr,
+                                tl ? L->xq2.td : nullptr);
     else
         launch_rmsnorm_q8(x, L->attn_out, L->post_norm, rows, H, s.rms_eps, L->h,
-                          capt(cap, L->normed2), L->xq2.qs, L->xq2.d, L->xq2.s, st);
+                          capt(cap, L->normed2), L->xq2.qs, L->xq2.d, L->xq2.s, st,
+                          tl ? L->xq2.tq : nullptr, tl ? L->xq2.td : nullptr);
     mark(L, SI_PHASE_GATE_UP, st);
+    // the SwiGLU Q8 also operand-tiled where the fused gate|up pass runs;
+    // the down projection then streams it in one pass (no K split, no
+    // reduce)
+    const bool tiled = tl && gemm_gateup_tiles_out(rows, H, ex, false);
     if (rows == 1) {
         project(L, L->wgu, rows, L->xq2, nullptr, nullptr, L->gu, flags, st);
         mark(L, SI_PHASE_SWIGLU_Q8, st);
@@ -1218,14 +1281,19 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
         // SwiGLU -> Q8 in the gate|up GEMM's epilogue (the swiglu_q8 phase
         // is then empty); gu is written only as a capture or where it is the
         // intermediate (exact mode)
-        const bool ex = (flags & SI_LAYER_EXACT) != 0;
         launch_gemm_gateup_q8(L->wgu.qs, L->wgu.d, L->wgu.tile, s.ffn, H, L->xq2.qs, L->xq2.d,
                               rows, capt(cap || ex, L->gu), capt(cap, L->act), L->actq.qs,
-                              L->actq.d, L->actq.s, ex, L->gemm_ws, L->gemm_ws_bytes, st);
+                              L->actq.d, L->actq.s, ex, L->gemm_ws, L->gemm_ws_bytes, st, false,
+                              tiled ? L->actq.tq : nullptr, tiled ? L->actq.td : nullptr,
+                              tl ? L->xq2.tq : nullptr, tl ? L->xq2.td : nullptr);
         mark(L, SI_PHASE_SWIGLU_Q8, st);
     }
     mark(L, SI_PHASE_DOWN, st);
-    project(L, L->wdown, rows, L->actq, nullptr, L->h, out, flags, st);
+    if (tiled)
+        launch_gemm_q4q8_tiled(L->wdown.qs, L->wdown.d, L->wdown.tile, H, s.ffn, L->actq.tq,
+                               L->actq.td, rows, nullptr, L->h, out, H, st);
+    else
+        project(L, L->wdown, rows, L->actq, nullptr, L->h, out, flags, st);
     mark(L, SI_PHASE_COUNT, st);
     return check_launch("layer");
 }

@@ -65,11 +65,13 @@ void launch_rope_kv(const float *qkv, int ldqkv, int ntok, int qheads, int kvhea
 
 constexpr int ATT_MAXPER = 16;  // query heads per KV group (the 16 MFMA columns)
 
-// grid (qheads, nq), block hdim: merge chunks, normalise, quantize to Q8_0.
+// grid (qheads, nq), block hdim: merge chunks, normalise, quantize to Q8_0
+// (tq/td, optional: the Q8_0 also operand-tiled, q8_tiled_byte).
 __global__ void k_attn_combine(int qheads, int hdim, int nsplit, const float *__restrict__ ws_m,
                                const float *__restrict__ ws_l, const float *__restrict__ ws_o,
                                float *__restrict__ attn, int8_t *__restrict__ qs,
-                               uint16_t *__restrict__ d, int16_t *__restrict__ bsum) {
+                               uint16_t *__restrict__ d, int16_t *__restrict__ bsum,
+                               int8_t *__restrict__ tq, uint16_t *__restrict__ td) {
     const int h = blockIdx.x, qi = blockIdx.y, jj = threadIdx.x;
     const size_t base = ((size_t)qi * qheads + h) * nsplit;
     // unrolled: the loads of 8 splits are in flight together
@@ -97,6 +99,12 @@ __global__ void k_attn_combine(int qheads, int hdim, int nsplit, const float *__
             const size_t bi = off / SI_QK;
             d[bi] = dbits;
             if (bsum) bsum[bi] = (int16_t)sum;
+        }
+        if (tq) {
+            const int qd = qheads * hdim;
+            const size_t pb = (size_t)(qi >> 5) * (qd / SI_QK) + (h * hdim + jj) / SI_QK;
+            tq[q8_tiled_byte(pb, qi & 31, jj & 31)] = (int8_t)q;
+            if ((jj & 31) == 0) td[pb * 32 + (qi & 31)] = dbits;
         }
     }
 }
@@ -126,7 +134,8 @@ __device__ __forceinline__ float block_reduce_1024(float v, float *red, bool is_
 __global__ __launch_bounds__(1024) void k_attn_combine_wide(
     int qheads, int hdim, int nsplit, const float *__restrict__ ws_m,
     const float *__restrict__ ws_l, const float *__restrict__ ws_o, float *__restrict__ attn,
-    int8_t *__restrict__ qs, uint16_t *__restrict__ d, int16_t *__restrict__ bsum) {
+    int8_t *__restrict__ qs, uint16_t *__restrict__ d, int16_t *__restrict__ bsum,
+    int8_t *__restrict__ tq, uint16_t *__restrict__ td) {
     __shared__ float red_o[1024];
     __shared__ float red_l[32];
     __shared__ float red_m[16];
@@ -165,19 +174,25 @@ __global__ __launch_bounds__(1024) void k_attn_combine_wide(
             d[bi] = dbits;
             if (bsum) bsum[bi] = (int16_t)sum;
         }
+        if (tq) {
+            const int qd = qheads * hdim;
+            const size_t pb = (size_t)(qi >> 5) * (qd / SI_QK) + (h * hdim + jj) / SI_QK;
+            tq[q8_tiled_byte(pb, qi & 31, jj & 31)] = (int8_t)q;
+            if ((jj & 31) == 0) td[pb * 32 + (qi & 31)] = dbits;
+        }
     }
 }
 
 // Either combine kernel by partial count.
 static void combine(int qheads, int hdim, int nq, int nsplit, const float *ws_m,
                     const float *ws_l, const float *ws_o, float *attn, int8_t *qs, uint16_t *d,
-                    int16_t *bsum, hipStream_t st) {
+                    int16_t *bsum, hipStream_t st, int8_t *tq = nullptr, uint16_t *td = nullptr) {
     if (nsplit >= 32)
         SI_LAUNCH(k_attn_combine_wide, dim3(qheads, nq), dim3(1024 / hdim * hdim), 0, st,
-                  qheads, hdim, nsplit, ws_m, ws_l, ws_o, attn, qs, d, bsum);
+                  qheads, hdim, nsplit, ws_m, ws_l, ws_o, attn, qs, d, bsum, tq, td);
     else
         SI_LAUNCH(k_attn_combine, dim3(qheads, nq), dim3(hdim), 0, st, qheads, hdim,
-                  nsplit, ws_m, ws_l, ws_o, attn, qs, d, bsum);
+                  nsplit, ws_m, ws_l, ws_o, attn, qs, d, bsum, tq, td);
 }
 
 // ===========================================================================
@@ -747,7 +762,8 @@ void launch_attn_prefill(const float *q, int ntok, int qheads, int kvheads, int 
         SI_LAUNCH(k_attn_combine, dim3(qheads, rows_split), dim3(hdim), 0, st, qheads,
                   hdim, 2, sp.ws_m, sp.ws_l, sp.ws_o, attn + t0 * qd_,
                   qs ? qs + t0 * qd_ : nullptr, qs ? qd + t0 * qd_ / SI_QK : nullptr,
-                  bsum ? bsum + t0 * qd_ / SI_QK : nullptr);
+                  bsum ? bsum + t0 * qd_ / SI_QK : nullptr, (int8_t *)nullptr,
+                  (uint16_t *)nullptr);
     }
 }
 
@@ -807,11 +823,12 @@ void launch_attention(const float *q, int nq, int qheads, int kvheads, int hdim,
 // Merge of nsplit partials laid out as [nq][qheads][nsplit] (m, l) and
 // [nq][qheads][nsplit][hdim] (o) in one workspace.
 void launch_attn_combine(int nq, int qheads, int hdim, int nsplit, const void *workspace,
-                         float *attn, int8_t *qs, uint16_t *d, int16_t *bsum, hipStream_t st) {
+                         float *attn, int8_t *qs, uint16_t *d, int16_t *bsum, hipStream_t st,
+                         int8_t *tq, uint16_t *td) {
     const float *ws_m = (const float *)workspace;
     const float *ws_l = ws_m + (size_t)nq * qheads * nsplit;
     const float *ws_o = ws_l + (size_t)nq * qheads * nsplit;
-    combine(qheads, hdim, nq, nsplit, ws_m, ws_l, ws_o, attn, qs, d, bsum, st);
+    combine(qheads, hdim, nq, nsplit, ws_m, ws_l, ws_o, attn, qs, d, bsum, st, tq, td);
 }
 
 // ---------------------------------------------------------------------------

@@ -17,6 +17,18 @@ namespace si {
 // compiles to v_sqrt_f32 plus a two-neighbour correction by fma.
 __device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
 
+// Operand-tiled Q8_0: the activation operand of the batched-decode GEMM
+// (k_gemm_bd's streamed mode) in the order its matrix-core lanes take it.
+// Rows are grouped in panels of 32; block b of panel p (pb = p * nb + b) is
+// one 1 KB run [half g][row j][16 bytes], half g of row j holding the
+// block's bytes 8g..8g+7 then 16+8g..16+8g+7 (the elements lane (j, g) of a
+// 32x32x32 i8 MFMA supplies).  Scales are [panel][block][row] fp16 bits
+// (q8_tiled_d index pb * 32 + j).  Byte i (0..31) of row j of block pb:
+__host__ __device__ constexpr size_t q8_tiled_byte(size_t pb, int j, int i) {
+    return pb * 1024 + (size_t)((i >> 3) & 1) * 512 + (size_t)j * 16 +
+           (size_t)((i & 7) | ((i >> 4) << 3));
+}
+
 __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 __device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
 

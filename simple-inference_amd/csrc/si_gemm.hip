@@ -213,6 +213,8 @@ struct GateUpOut {
     int8_t *qs;     // Q8_0 of the SwiGLU output, planar [m][f]
     uint16_t *d;    // [m][f/32] fp16 scale bits
     int16_t *s;     // optional [m][f/32] block sums
+    int8_t *tq;     // optional: the same Q8_0 operand-tiled (q8_tiled_qs)
+    uint16_t *td;   // with tq: its scales (q8_tiled_d)
 };
 
 // Register staging of one LDS stage of k_gemm_fast.  Each thread's byte
@@ -942,7 +944,22 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm_h16(
 // MODE 0 (TN = 1): out = residual + (acc + bias) (both optional), or the
 // partials.  MODE 1 (TN = 2, gate|up, one K range): tile u pairs the gate
 // rows 32u..32u+31 with the up rows f+32u..; SwiGLU + Q8_0 epilogue as
-// k_gemm_fast's.
+// k_gemm_fast's, optionally also written operand-tiled.
+//
+// DA (one K range of any length): the activations arrive
+// operand-tiled (q8_tiled_qs / q8_tiled_d): a block of a 32-row panel is one
+// contiguous 1 KB run in exactly the order the MFMA lanes take it, so each
+// stage loads its block's activations with one 16-byte load per lane next to
+// its weights, and there is no fill, no LDS copy of the rows and no K-range
+// limit (one pass, no partials).  Read from the planar layout the same loads
+// would touch 32 cache lines each (one per row); through the LDS fill they
+// cost a serial phase per workgroup and, for long K, the K split.
+//
+// PIPE (one tile): block i's two matrix-core products are issued before
+// block i-1's epilogue runs, which consumes the products issued one step
+// earlier (two register sets by the parity of the unrolled step), so each
+// wavefront has its products in flight while it converts and accumulates;
+// the blocks are still accumulated in the same order (same bits).
 constexpr int BD_RED = 8 * 16 * 64 * 4;                    // 8 partial 32x32 fp32 tiles
 constexpr int BD_LDS_MAX = 160 * 1024;                     // LDS of a gfx950 CU
 // x.d row stride in halves for a K range of cb blocks: an odd number of
@@ -964,6 +981,8 @@ struct BdStage {
     gv2u w[TN];       // nibble bytes 8g..8g+7 of weight row j of tile u
     uint16_t ws[TN];  // w.d fp16 bits (lanes 32..63: 0); widened where used, so
                       // that nothing waits for the load before then
+    v4i a;            // streamed activations: this lane's 16 operand bytes
+    uint16_t xs;      // streamed activations: x.d of row j
 };
 
 // A workgroup barrier ordering LDS only: __syncthreads() also orders global
@@ -985,7 +1004,7 @@ __device__ __forceinline__ void bd_place(int id, int H, int S, int &h, int &q, i
     s = q - c * S;
 }
 
-template <int TN, int P, int MODE, int BD_W>
+template <int TN, int P, int MODE, int BD_W, bool DA, bool PIPE = false>
 __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
     const uint8_t *__restrict__ wqs, const uint16_t *__restrict__ wd, int tile, int n, int nb,
     const int8_t *__restrict__ xqs, const uint16_t *__restrict__ xd, int m,
@@ -993,6 +1012,7 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
     int ldo, float *__restrict__ part, int H, int C, int S, int cb, int units, GateUpOut go) {
     static_assert(MODE == 0 ? TN == 1 : TN == 2, "MODE 0 takes one tile, gate|up two");
     static_assert(BD_W >= 8 && BD_W <= 16 && BD_W % 4 == 0, "8, 12 or 16 wavefronts");
+    static_assert(!PIPE || (TN == 1 && P % 2 == 0), "pipelined: one tile, an even unroll");
     constexpr int BD_T = 64 * BD_W;                              // threads
     constexpr int BD_FILL = (BD_MAX_CB * 64 + BD_T - 1) / BD_T;  // 16-byte fill pieces per thread
     constexpr int BD_XFILL = (32 * 128 + BD_T - 1) / BD_T;       // x.d fill values per thread
@@ -1007,11 +1027,12 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
     if (q >= C * S) return;  // the whole workgroup
     const int m0 = 32 * h, b0 = c * cb, len = min(nb, b0 + cb) - b0;
     const int k = nb * SI_QK;
-    const int cb4 = (cb + 3) & ~3;
+    const int cb4 = DA ? 0 : (cb + 3) & ~3;
     uint8_t *a_l = bd_sm;  // [cb4][2][32][16 B]
     const int xst = bd_xst(cb);  // x.d row stride (halves)
     uint16_t *x_l = (uint16_t *)(bd_sm + (size_t)cb4 * 1024);  // [32][xst]
-    float4 *red = (float4 *)(bd_sm + bd_lds(cb) - BD_RED);    // [8][16][64] floats
+    // [8][16][64] floats (streamed activations: the only LDS)
+    float4 *red = (float4 *)(DA ? bd_sm : bd_sm + bd_lds(cb) - BD_RED);
 
     // ---- the tiles of this workgroup: units s, s + S, ...
     const int per = (len + BD_W - 1) / BD_W;  // blocks per wavefront per tile (some may be past len)
@@ -1020,6 +1041,12 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
     if (total <= 0) return;  // no tile here: the whole workgroup
     const int ltile = __builtin_ctz((unsigned)tile);
     const __amdgpu_buffer_rsrc_t rb = buf_rsrc(wqs, (uint32_t)nb * n * 16);
+    // streamed activations: panel h's block b at (h nb + b) KB; lane (j, g)
+    // reads 16 bytes at g * 512 + j * 16 of it, its x.d at (h nb + b) * 64 + 2 j
+    const __amdgpu_buffer_rsrc_t rta = buf_rsrc(xqs, DA ? (uint32_t)H * nb * 1024 : 0u);
+    const __amdgpu_buffer_rsrc_t rtx = buf_rsrc(xd, DA ? (uint32_t)H * nb * 64 : 0u);
+    const uint32_t vta = (uint32_t)h * nb * 1024 + g * 512 + j * 16;
+    const uint32_t vtx = ((uint32_t)h * nb * 32 + j) * 2;
     const __amdgpu_buffer_rsrc_t rw =
         buf_rsrc(wd, __builtin_amdgcn_readfirstlane((int)q4_scale_count(n, nb, tile) * 2));
     // first column of tile u of unit iu (scalar)
@@ -1046,6 +1073,10 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
             lu_set = iu;
         }
         const int b = b0 + min(BD_W * lk + wave, len - 1);
+        if (DA) {
+            st.a = __builtin_amdgcn_raw_buffer_load_b128(rta, vta, b * 1024, 0);
+            st.xs = __builtin_amdgcn_raw_buffer_load_b16(rtx, vtx, b * 64, 0);
+        }
 #pragma unroll
         for (int u = 0; u < TN; ++u) {
             st.w[u] = __builtin_amdgcn_raw_buffer_load_b64(rb, vob[u], b * n * 16, 0);
@@ -1078,11 +1109,13 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
     // ---- fill: the K range's 32 rows (clamped to m - 1) and their x.d.
     // Loads retire in issue order: the fill's loads go first, then the
     // first P blocks of weights, and the fill waits for its own loads only,
-    // while the weights stream in behind them.
+    // while the weights stream in behind them.  (Streamed activations: no
+    // fill.)
+    v4i fv[DA ? 1 : BD_FILL];
+    uint32_t xv[DA ? 1 : BD_XFILL];
+    if constexpr (!DA) {
     const __amdgpu_buffer_rsrc_t ra = buf_rsrc(xqs, (uint32_t)m * k);
     const __amdgpu_buffer_rsrc_t rx = buf_rsrc(xd, (uint32_t)m * nb * 2);
-    v4i fv[BD_FILL];
-    uint32_t xv[BD_XFILL];
     // Q8: 8 threads read a row's 128 bytes (4 blocks), 8 rows per 64
     // threads; a wavefront's pieces are 4 whole blocks, so whether they are
     // stored is decided per wavefront (pieces past len read zero)
@@ -1103,6 +1136,7 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
         const uint32_t off = b < len && ri < 32 ? ((uint32_t)row * nb + b0 + b) * 2 : 0x80000000u;
         xv[i] = __builtin_amdgcn_raw_buffer_load_b16(rx, off, 0, 0);
     }
+    }
     __builtin_amdgcn_sched_barrier(0);
     // P blocks of weights in flight; each stage's loads stay together and
     // in stage order (scheduling barriers), and every load is issued (a
@@ -1115,6 +1149,7 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
         __builtin_amdgcn_sched_barrier(0);
     }
     // everything but the weight stages complete (lgkmcnt and expcnt free)
+    if constexpr (!DA) {
     {
         constexpr int VM = P * 2 * TN;  // weight loads issued after the fill
         static_assert(VM <= 63, "vmcnt holds 6 bits");
@@ -1139,6 +1174,7 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
         if ((e & 127) < len && e < 32 * 128) x_l[(e >> 7) * xst + (e & 127)] = (uint16_t)xv[i];
     }
     lds_barrier();
+    }
 
     float acc[TN][16];
 #pragma unroll
@@ -1150,9 +1186,11 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
     v4i a_nx;
     uint16_t x_nx;
     auto fetch = [&](int ck) {
-        const int rel = min(BD_W * ck + wave, len - 1);
-        a_nx = *(const v4i *)(a_l + (size_t)rel * 1024 + la);
-        x_nx = x_l[j * xst + rel];
+        if constexpr (!DA) {
+            const int rel = min(BD_W * ck + wave, len - 1);
+            a_nx = *(const v4i *)(a_l + (size_t)rel * 1024 + la);
+            x_nx = x_l[j * xst + rel];
+        }
     };
     auto compute = [&](const BdStage<TN> &st, const v4i &aop, uint16_t xs) {
         // scale product x.d * w.d in the output layout: A carries x.d at
@@ -1176,6 +1214,27 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
             for (int v = 0; v < 16; ++v) acc[u][v] = fmaf((float)dot[v], sc[v], acc[u][v]);
         }
     };
+    // PIPE: the products of a block (issue), consumed one step later (epi)
+    auto issue = [&](const BdStage<TN> &st, const v4i &aop, uint16_t xs, v16i &dot, v16f &sc) {
+        const gh4 asc = __builtin_bit_cast(gh4, (v2u){(uint32_t)xs, 0u});
+        const uint32_t w0 = st.w[0][0], w1 = st.w[0][1];
+        const v4i bop = (v4i){(int)(((w0 << 4) ^ 0x80808080u) & 0xf0f0f0f0u),
+                              (int)(((w1 << 4) ^ 0x80808080u) & 0xf0f0f0f0u),
+                              (int)((w0 ^ 0x80808080u) & 0xf0f0f0f0u),
+                              (int)((w1 ^ 0x80808080u) & 0xf0f0f0f0u)};
+        const gh4 bsc = __builtin_bit_cast(gh4, (v2u){(uint32_t)st.ws[0], 0u});
+        v16i z = {};
+        dot = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, z, 0, 0, 0);
+        v16f zf = {};
+        sc = __builtin_amdgcn_mfma_f32_32x32x8f16(asc, bsc, zf, 0, 0, 0);
+    };
+    auto epi = [&](const v16i &dot, const v16f &sc) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[0][v] = fmaf((float)dot[v], sc[v], acc[0][v]);
+    };
+    v16i pdot[PIPE ? 2 : 1] = {};
+    v16f psc[PIPE ? 2 : 1] = {};
+    bool pend = false;  // a block issued, its epilogue not yet run
     // a tile's partial sums added in a fixed order: wavefronts 8..W-1 hand
     // theirs to 0..W-9, then the 8 sums meet in LDS ([w][register][lane]
     // floats, so no register is repacked); wavefront w < 8 gets registers
@@ -1237,6 +1296,11 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
                         go.d[o / SI_QK] = dbits;
                         if (go.s) go.s[o / SI_QK] = (int16_t)bsum;
                     }
+                    if (go.tq) {
+                        const size_t pb = (size_t)(row >> 5) * (f / SI_QK) + feat / SI_QK;
+                        go.tq[q8_tiled_byte(pb, row & 31, j)] = (int8_t)qv;
+                        if (j == 0) go.td[pb * 32 + (row & 31)] = dbits;
+                    }
                 }
             } else {
                 const int col = col0(iu, 0) + j;
@@ -1268,14 +1332,35 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
 #pragma unroll
             for (int i = 0; i < P; ++i) {
                 if (it0 + i < total) {
-                    const v4i aop = a_nx;
-                    const uint16_t xs = x_nx;
+                    const v4i aop = DA ? st[i].a : a_nx;
+                    const uint16_t xs = DA ? st[i].xs : x_nx;
                     const bool valid = BD_W * ck + wave < len;
                     const int ckn = ck + 1 == per ? 0 : ck + 1;
                     fetch(ckn);
-                    if (valid) compute(st[i], aop, xs);
+                    if constexpr (PIPE) {
+                        // a pending block was issued at the previous step
+                        // (set (i + 1) & 1): a valid step consumes it after
+                        // issuing its own, an invalid one (a block past the
+                        // range) just consumes it, so at a tile's end the
+                        // pending block, if any, is this step's (set i & 1)
+                        if (valid) {
+                            issue(st[i], aop, xs, pdot[i & 1], psc[i & 1]);
+                            __builtin_amdgcn_sched_barrier(0);
+                            if (pend) epi(pdot[(i + 1) & 1], psc[(i + 1) & 1]);
+                            pend = true;
+                        } else if (pend) {
+                            epi(pdot[(i + 1) & 1], psc[(i + 1) & 1]);
+                            pend = false;
+                        }
+                    } else {
+                        if (valid) compute(st[i], aop, xs);
+                    }
                     ck = ckn;
                     if (ck == 0) {
+                        if constexpr (PIPE) {
+                            if (pend) epi(pdot[i & 1], psc[i & 1]);
+                            pend = false;
+                        }
                         finish(cu);
                         ++cu;
                     }
@@ -1429,18 +1514,21 @@ constexpr int BD_SMALL_M = 64;  // every projection and the gate|up pair
 constexpr int BD_MAX_M = 512;   // one-tile projections, when bd_takes() says so
 struct BdPlan {
     int H, C, S, cb, units, grid;
+    bool da;  // streamed (operand-tiled) activations: one K range, no fill
     size_t lds;
 };
-static BdPlan bd_plan(int m, int n, int nb, int mode) {
+static BdPlan bd_plan(int m, int n, int nb, int mode, bool da = false) {
+    // (da: m <= 64; for mode 1 the caller keeps nb <= BD_MAX_CB as without)
     BdPlan p;
     p.H = (m + 31) / 32;
-    p.C = (nb + BD_MAX_CB - 1) / BD_MAX_CB;
+    p.da = da;
+    p.C = da ? 1 : (nb + BD_MAX_CB - 1) / BD_MAX_CB;
     p.cb = (nb + p.C - 1) / p.C;
     p.units = mode == 1 ? n / 64 : (n + 31) / 32;
     const int per_xcd = std::max(1, 32 / p.H);
     p.S = std::max(1, std::min(8 * per_xcd / p.C, p.units));
     p.grid = 8 * p.H * ((p.C * p.S + 7) / 8);
-    p.lds = bd_lds(p.cb);
+    p.lds = da ? (size_t)BD_RED : bd_lds(p.cb);
     return p;
 }
 
@@ -1481,27 +1569,37 @@ static void launch_bd(const BdPlan &p, int mode, const uint8_t *wqs, const uint1
                       int tile, int n, int nb, const int8_t *xqs, const uint16_t *xd, int m,
                       const float *bias, const float *residual, float *out, int ldo, float *part,
                       const GateUpOut &go, hipStream_t st) {
-#define BD(TN, P, MODE, W)                                                                     \
+#define BD(TN, P, MODE, W, DA, PIPE)                                                           \
     do {                                                                                       \
         static bool big_lds = false;                                                           \
         if (!big_lds) {                                                                        \
             /* a failure here surfaces as the launch's error */                                \
-            (void)hipFuncSetAttribute((const void *)k_gemm_bd<TN, P, MODE, W>,                 \
+            (void)hipFuncSetAttribute((const void *)k_gemm_bd<TN, P, MODE, W, DA, PIPE>,       \
                                       hipFuncAttributeMaxDynamicSharedMemorySize, BD_LDS_MAX); \
             big_lds = true;                                                                    \
         }                                                                                      \
-        SI_LAUNCH((k_gemm_bd<TN, P, MODE, W>), dim3(p.grid), dim3(64 * W), p.lds, st, wqs, wd, \
-                  tile, n, nb, xqs, xd, m, bias, residual, out, ldo, part, p.H, p.C, p.S,      \
-                  p.cb, p.units, go);                                                          \
+        SI_LAUNCH((k_gemm_bd<TN, P, MODE, W, DA, PIPE>), dim3(p.grid), dim3(64 * W), p.lds,   \
+                  st, wqs, wd, tile, n, nb, xqs, xd, m, bias, residual, out, ldo, part, p.H,   \
+                  p.C, p.S, p.cb, p.units, go);                                                \
     } while (0)
     // gate|up: 12 wavefronts (3 per SIMD; 4 weight blocks in flight fit
     // their registers); one tile: 16 (4 per SIMD, 7 of 112 blocks each, 4
     // in flight; 8 wavefronts with 16 in flight took 56 us for QKV + O +
     // down at 7B x 64 rows, 16 with 2, 4, 6 or 8 in flight 50-54 us)
-    if (mode == 1)
-        BD(2, 4, 1, 12);
-    else
-        BD(1, 4, 0, 16);
+    // streamed one-tile projections: 12 wavefronts, 2 stages, pipelined (7B
+    // x 64 rows, cold weights: down 24.4 -> 23.3 us, QKV 13.0 -> 12.0, O
+    // 8.7 -> 7.8 against 16 wavefronts x 4 stages unpipelined; 8 or 16
+    // wavefronts and 3-12 stages took as long or longer)
+    if (mode == 1) {
+        if (p.da)
+            BD(2, 3, 1, 12, true, false);
+        else
+            BD(2, 4, 1, 12, false, false);
+    } else if (p.da) {
+        BD(1, 2, 0, 12, true, true);
+    } else {
+        BD(1, 4, 0, 16, false, false);
+    }
 #undef BD
 }
 
@@ -1531,6 +1629,19 @@ void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, i
                       size_t ws_bytes, hipStream_t st) {
     gemm_core(wqs, wd, tile, n, k, xqs, xd, m, bias, residual, out, ldo, exact, workspace,
               ws_bytes, false, st);
+}
+
+void launch_gemm_q4q8_tiled(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
+                            const int8_t *tq, const uint16_t *td, int m, const float *bias,
+                            const float *residual, float *out, int ldo, hipStream_t st) {
+    if (m <= 0 || n <= 0) return;
+    const int nb = k / SI_QK;
+    launch_bd(bd_plan(m, n, nb, 0, true), 0, wqs, wd, tile, n, nb, tq, td, m, bias, residual,
+              out, ldo, nullptr, GateUpOut{}, st);
+}
+
+bool gemm_gateup_tiles_out(int m, int k, bool exact, bool f16) {
+    return !exact && !f16 && m <= BD_SMALL_M && k / SI_QK <= BD_MAX_CB;
 }
 
 static int gemm_core(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
@@ -1607,7 +1718,8 @@ static int gemm_core(const uint8_t *wqs, const uint16_t *wd, int tile, int n, in
 void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, int k,
                            const int8_t *xqs, const uint16_t *xd, int m, float *gu, float *act,
                            int8_t *qs, uint16_t *d, int16_t *s, bool exact, void *workspace,
-                           size_t ws_bytes, hipStream_t st, bool f16) {
+                           size_t ws_bytes, hipStream_t st, bool f16, int8_t *tq, uint16_t *td,
+                           const int8_t *txq, const uint16_t *txd) {
     if (m <= 0) return;
     const int n = 2 * f, nb = k / SI_QK;
     if (f16 && !exact) {
@@ -1618,9 +1730,12 @@ void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int
                                      GateUpOut{f, act, qs, d, s}, st);
         return;
     }
-    if (!exact && m <= BD_SMALL_M && nb <= BD_MAX_CB) {
-        launch_bd(bd_plan(m, n, nb, 1), 1, wqs, wd, tile, n, nb, xqs, xd, m, nullptr, nullptr, gu,
-                  n, nullptr, GateUpOut{f, act, qs, d, s}, st);
+    if (gemm_gateup_tiles_out(m, k, exact, f16)) {
+        // the activations streamed when given operand-tiled (txq / txd)
+        const bool da = txq && txd;
+        launch_bd(bd_plan(m, n, nb, 1, da), 1, wqs, wd, tile, n, nb, da ? txq : xqs,
+                  da ? txd : xd, m, nullptr, nullptr, gu, n, nullptr,
+                  GateUpOut{f, act, qs, d, s, tq, td}, st);
         return;
     }
     // a K split (gemm_core's own plan: k_gemm_bd's K-range partials or the

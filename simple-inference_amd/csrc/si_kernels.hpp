@@ -32,9 +32,10 @@ namespace si {
 void launch_quantize_q8_aos(const float *src, void *dst, int count, hipStream_t st);
 void launch_quantize_q8_rows(const float *src, int rows, int k, int8_t *qs, uint16_t *d,
                              int16_t *s, hipStream_t st);
+// tq/td (optional): the Q8_0 output operand-tiled as well (q8_tiled_byte)
 void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int rows, int n,
                        float eps, float *h, float *normed, int8_t *qs, uint16_t *d, int16_t *s,
-                       hipStream_t st);
+                       hipStream_t st, int8_t *tq = nullptr, uint16_t *td = nullptr);
 void launch_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs, uint16_t *d,
                       int16_t *s, hipStream_t st);
 void launch_q4_repack(const uint8_t *src, int n, int k, int tile, uint8_t *qs, uint16_t *d,
@@ -61,16 +62,33 @@ void launch_gemm_reduce(const float *part, int splits, int m, int n, float *out,
 // written to y_out as well.
 void launch_rmsnorm_q8_parts(const float *x, const float *part, int splits, const float *gain,
                              int rows, int n, float eps, float *y_out, float *h, float *normed,
-                             int8_t *qs, uint16_t *d, int16_t *s, hipStream_t st);
+                             int8_t *qs, uint16_t *d, int16_t *s, hipStream_t st,
+                             int8_t *tq = nullptr, uint16_t *td = nullptr);
 void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
                       const int8_t *xqs, const uint16_t *xd, int m, const float *bias,
                       const float *residual, float *out, int ldo, bool exact, void *workspace,
                       size_t ws_bytes, hipStream_t st);
-// f16: k_gemm_h16 (the f16 formulation) where the plan runs one fused pass
+// planar Q8_0 (qs [m][k], d [m][k/32]) -> operand-tiled (q8_tiled_byte)
+void launch_q8_tile(const int8_t *qs, const uint16_t *d, int m, int k, int8_t *tq, uint16_t *td,
+                    hipStream_t st);
+// launch_gemm_q4q8 (no K split, not exact) with the activations operand-
+// tiled (q8_tiled_byte: tq [ceil(m/32)][k/32] KB, td [ceil(m/32)][k/32][32]);
+// m <= 64.
+void launch_gemm_q4q8_tiled(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
+                            const int8_t *tq, const uint16_t *td, int m, const float *bias,
+                            const float *residual, float *out, int ldo, hipStream_t st);
+// f16: k_gemm_h16 (the f16 formulation) where the plan runs one fused pass.
+// Where gemm_gateup_tiles_out() holds for the call: tq/td (optional) get
+// the Q8_0 output operand-tiled as well, and txq/txd (optional), the same
+// activations as xqs/xd operand-tiled, are streamed instead of staged.
 void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, int k,
                            const int8_t *xqs, const uint16_t *xd, int m, float *gu, float *act,
                            int8_t *qs, uint16_t *d, int16_t *s, bool exact, void *workspace,
-                           size_t ws_bytes, hipStream_t st, bool f16 = false);
+                           size_t ws_bytes, hipStream_t st, bool f16 = false,
+                           int8_t *tq = nullptr, uint16_t *td = nullptr,
+                           const int8_t *txq = nullptr, const uint16_t *txd = nullptr);
+// Whether launch_gemm_gateup_q8 writes tq/td for m rows over K = k.
+bool gemm_gateup_tiles_out(int m, int k, bool exact, bool f16);
 size_t gemm_workspace_bytes(int m, int n, int k);
 // workspace launch_gemm_gateup_q8 uses for f features (0: never splits K)
 size_t gemm_gateup_workspace_bytes(int m, int f, int k);
@@ -168,8 +186,10 @@ void launch_dec_attn(const float *qkv, int ldqkv, int nq, int qheads, int kvhead
                      size_t kv_seq_stride, const int *ctx_dev, int ctx0, int max_ctx,
                      float *q_cap, int ns, void *workspace, float *attn, int8_t *aqs,
                      uint16_t *ad, int16_t *as, hipStream_t st, KvPages pg = KvPages());
+// tq/td (optional): the Q8_0 also operand-tiled (q8_tiled_byte; qs required)
 void launch_attn_combine(int nq, int qheads, int hdim, int nsplit, const void *workspace,
-                         float *attn, int8_t *qs, uint16_t *d, int16_t *bsum, hipStream_t st);
+                         float *attn, int8_t *qs, uint16_t *d, int16_t *bsum, hipStream_t st,
+                         int8_t *tq = nullptr, uint16_t *td = nullptr);
 // Kernels over the reference's own formats (si_mirror.hip): row-major Q4_0
 // with block_q8_0 records, column-SoA tiles, stand-alone rmsnorm and rope.
 void launch_matvec_rowmajor(const uint8_t *w, const void *x, int inputs, int outputs,

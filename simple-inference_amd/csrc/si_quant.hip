@@ -127,6 +127,8 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8(const float *__restrict__ x,
 // pass over global memory, no LDS staging; needs 16-byte aligned rows.
 // PARTS (with RESIDUAL): y is the split-order sum of y[sp * rows * n + ...]
 // for sp < splits (a K-split GEMM's partials), also written to y_out.
+// tq/td (optional): the Q8_0 row written operand-tiled as well
+// (q8_tiled_byte; a thread's 4 values are 4 consecutive bytes there too).
 template <bool RESIDUAL, int NPT, bool PARTS = false>
 __global__ void __launch_bounds__(256) k_rmsnorm_q8_v4(const float *__restrict__ x,
                                                        const float *__restrict__ y,
@@ -136,7 +138,9 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8_v4(const float *__restrict__
                                                        int8_t *__restrict__ qs,
                                                        uint16_t *__restrict__ d,
                                                        int16_t *__restrict__ s, int splits = 1,
-                                                       float *__restrict__ y_out = nullptr) {
+                                                       float *__restrict__ y_out = nullptr,
+                                                       int8_t *__restrict__ tq = nullptr,
+                                                       uint16_t *__restrict__ td = nullptr) {
     __shared__ double red[4];
     const int r = blockIdx.x, tid = threadIdx.x, n4 = n / 4;
     const size_t base = (size_t)r * n;
@@ -204,6 +208,11 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8_v4(const float *__restrict__
                 const size_t bi = (base + 4 * c) / SI_QK;
                 d[bi] = dbits;
                 if (s) s[bi] = (int16_t)bsum;
+            }
+            if (tq) {
+                const size_t pb = (size_t)(r >> 5) * (n / SI_QK) + (4 * c) / SI_QK;
+                *(uint32_t *)(tq + q8_tiled_byte(pb, r & 31, (4 * c) % SI_QK)) = packed;
+                if ((tid & 7) == 0) td[pb * 32 + (r & 31)] = dbits;
             }
         }
     }
@@ -285,19 +294,20 @@ void launch_quantize_q8_rows(const float *src, int rows, int k, int8_t *qs, uint
 
 void launch_rmsnorm_q8_parts(const float *x, const float *part, int splits, const float *gain,
                              int rows, int n, float eps, float *y_out, float *h, float *normed,
-                             int8_t *qs, uint16_t *d, int16_t *s, hipStream_t st) {
+                             int8_t *qs, uint16_t *d, int16_t *s, hipStream_t st, int8_t *tq,
+                             uint16_t *td) {
     if (rows == 0) return;
     const auto al = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
     const int n4 = n / 4;
     if (!(n4 <= 2048 && al(x) && al(part) && al(y_out) && al(h) && al(normed) && al(gain) &&
           al(qs))) {
         launch_gemm_reduce(part, splits, rows, n, y_out, st);
-        launch_rmsnorm_q8(x, y_out, gain, rows, n, eps, h, normed, qs, d, s, st);
+        launch_rmsnorm_q8(x, y_out, gain, rows, n, eps, h, normed, qs, d, s, st, tq, td);
         return;
     }
 #define RMS_P(NPT)                                                                              \
     SI_LAUNCH((k_rmsnorm_q8_v4<true, NPT, true>), dim3(rows), dim3(256), 0, st, x, part,        \
-              gain, n, eps, h, normed, qs, d, s, splits, y_out)
+              gain, n, eps, h, normed, qs, d, s, splits, y_out, tq, td)
     if (n4 <= 256) RMS_P(1);
     else if (n4 <= 512) RMS_P(2);
     else if (n4 <= 1024) RMS_P(4);
@@ -307,7 +317,7 @@ void launch_rmsnorm_q8_parts(const float *x, const float *part, int splits, cons
 
 void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int rows, int n,
                        float eps, float *h, float *normed, int8_t *qs, uint16_t *d, int16_t *s,
-                       hipStream_t st) {
+                       hipStream_t st, int8_t *tq, uint16_t *td) {
     if (rows == 0) return;
     const auto al = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
     const int n4 = n / 4;
@@ -315,7 +325,7 @@ void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int ro
         const int npt = n4 <= 256 ? 1 : n4 <= 512 ? 2 : n4 <= 1024 ? 4 : 8;
 #define RMS_V4(RES, NPT)                                                                          \
     SI_LAUNCH((k_rmsnorm_q8_v4<RES, NPT>), dim3(rows), dim3(256), 0, st, x, y, gain, n,           \
-              eps, h, normed, qs, d, s, 1, (float *)nullptr)
+              eps, h, normed, qs, d, s, 1, (float *)nullptr, tq, td)
 #define RMS_V4N(RES)                     \
     switch (npt) {                       \
         case 1: RMS_V4(RES, 1); break;   \
@@ -339,6 +349,7 @@ void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int ro
     else
         SI_LAUNCH(k_rmsnorm_q8<false>, dim3(rows), dim3(256), lds, st, x, y, gain, n,
                   eps, h, normed, qs, d, s);
+    if (tq) launch_q8_tile(qs, d, rows, n, tq, td, st);  // this path writes planar only
 }
 
 void launch_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs, uint16_t *d,
@@ -363,6 +374,38 @@ void launch_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k, int ti
     if (!tot) return;
     SI_LAUNCH(k_q4_unpack, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, qs,
               d, n, k / SI_QK, tile, dst);
+}
+
+// Planar Q8_0 -> operand-tiled (q8_tiled_byte): one thread per (row of
+// the padded panels, block); padding rows get zeros.
+__global__ void __launch_bounds__(256) k_q8_tile(const int8_t *__restrict__ qs,
+                                                 const uint16_t *__restrict__ d, int m, int nb,
+                                                 int8_t *__restrict__ tq, uint16_t *__restrict__ td,
+                                                 int total) {
+    const int t = blockIdx.x * 256 + threadIdx.x;  // row-major over (row, block)
+    if (t >= total) return;
+    const int r = t / nb, b = t - r * nb;
+    int4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};  // bytes 0..15 and 16..31 of the block
+    uint16_t sc = 0;
+    if (r < m) {
+        const int4 *src = (const int4 *)(qs + ((size_t)r * nb + b) * SI_QK);
+        lo = src[0];
+        hi = src[1];
+        sc = d[(size_t)r * nb + b];
+    }
+    const size_t pb = (size_t)(r >> 5) * nb + b;
+    int8_t *dst = tq + q8_tiled_byte(pb, r & 31, 0);
+    *(int4 *)dst = (int4){lo.x, lo.y, hi.x, hi.y};          // half 0: bytes 0..7, 16..23
+    *(int4 *)(dst + 512) = (int4){lo.z, lo.w, hi.z, hi.w};  // half 1: bytes 8..15, 24..31
+    td[pb * 32 + (r & 31)] = sc;
+}
+
+void launch_q8_tile(const int8_t *qs, const uint16_t *d, int m, int k, int8_t *tq, uint16_t *td,
+                    hipStream_t st) {
+    const int nb = k / SI_QK, total = (m + 31) / 32 * 32 * nb;
+    if (total == 0) return;
+    SI_LAUNCH(k_q8_tile, dim3((total + 255) / 256), dim3(256), 0, st, qs, d, m, nb, tq, td,
+              total);
 }
 
 }  // namespace si

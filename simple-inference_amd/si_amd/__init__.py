@@ -26,9 +26,10 @@ SI_LAYER_FULL, SI_LAYER_ATTN_ONLY, SI_LAYER_EXACT, SI_LAYER_ATTN_STANDARD = 0, 1
 SI_LAYER_CAPTURE = 8
 SI_GEMM_EXACT = 1
 SI_GEMM_F16 = 2
+SI_GEMM_TILED_A = 4
 BUFFERS = ["NORMED", "XQ_QS", "XQ_D", "XQ_S", "QKV", "Q", "ATTN", "ATTQ_QS", "ATTQ_D",
            "ATTQ_S", "ATTN_OUT", "H", "NORMED2", "XQ2_QS", "XQ2_D", "XQ2_S", "GU", "ACT",
-           "ACTQ_QS", "ACTQ_D", "ACTQ_S"]
+           "ACTQ_QS", "ACTQ_D", "ACTQ_S", "ACTQ_TQ", "ACTQ_TD"]
 BUF = {n: i for i, n in enumerate(BUFFERS)}
 PHASES = ["rms_q8", "qkv_proj", "rope_kv", "attention_q8", "out_proj", "post_norm_q8",
           "gate_up", "swiglu_q8", "down_proj"]
@@ -74,6 +75,7 @@ _SIGS = {
     "si_kernel_timing_stop": (_I, [_P, _I, ctypes.POINTER(_I)]),
     "si_kernel_timing_name": (ctypes.c_char_p, [_I]),
     "si_stream_read": (_I, [_P, ctypes.c_size_t, _P, _I, _I, _P]),
+    "si_q8_tile": (_I, [_P, _P, _I, _I, _P, _P, _P]),
     "si_q4_repack": (_I, [_P, _I, _I, _I, _P, _P, _P]),
     "si_q4_unpack": (_I, [_P, _P, _I, _I, _I, _P, _P]),
     "si_q4_tile": (_I, [_I, _I]),

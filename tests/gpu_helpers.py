@@ -110,6 +110,23 @@ def aos_to_planar(blocks):
         blocks["qs"].astype(np.int32).sum(1).astype(np.int16)
 
 
+def q8_tiled(qs, d, m, k):
+    """Planar Q8 (int8 [m*k], uint16 [m*k/32]) -> operand-tiled (int8 and
+    uint16 flat arrays): rows in ceil(m/32) panels of 32 (padding rows zero);
+    block b of panel p is [half g][row j][16 bytes], half g of row j holding
+    the block's bytes 8g..8g+7 then 16+8g..16+8g+7; scales [p][b][j]."""
+    nb, P = k // QK, (m + 31) // 32
+    a = np.zeros((P * 32, nb, QK), np.int8)
+    a[:m] = np.asarray(qs, np.int8).reshape(m, nb, QK)
+    sc = np.zeros((P * 32, nb), np.uint16)
+    sc[:m] = np.asarray(d, np.uint16).reshape(m, nb)
+    a = a.reshape(P, 32, nb, QK).transpose(0, 2, 1, 3)  # [p][b][j][32 bytes]
+    halves = np.stack([np.concatenate([a[..., 0:8], a[..., 16:24]], -1),
+                       np.concatenate([a[..., 8:16], a[..., 24:32]], -1)], 2)  # [p][b][g][j][16]
+    td = sc.reshape(P, 32, nb).transpose(0, 2, 1)  # [p][b][j]
+    return np.ascontiguousarray(halves).reshape(-1), np.ascontiguousarray(td).reshape(-1)
+
+
 def q4(oracle, rng, n, k, sigma=0.02):
     return oracle.quantize_q4_0(rng.normal(0, sigma, (n, k)).astype(np.float32))
 

@@ -12,7 +12,7 @@ import pytest
 import si_amd
 from oracle.oracle_py import Q8_DTYPE, make_shape as or_shape
 from tests.gpu_helpers import (aos_to_planar, close, dequant_q4, dequant_q8, dev, empty, host,
-                               kv_history, q4, zeros)
+                               kv_history, q4, q8_tiled, zeros)
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ref_golden.npz")
@@ -378,6 +378,85 @@ def test_gemm_bias_residual_batched(oracle, m, n, k, ldo):
         err = np.abs(got[:, :n] - want).max() / rms
         assert err <= 1e-5, f"workspace {ws_bytes}: worst {err:.3g}"
         assert np.all(got[:, n:] == 7.0), "columns past n written"
+
+
+@pytest.mark.parametrize("m", [1, 5, 32, 33, 64, 100])
+def test_q8_tile_layout(m):
+    """si_q8_tile against the layout restated on the host (q8_tiled), padding
+    rows included (zero)."""
+    torch = _torch()
+    k = 384
+    rng = np.random.default_rng(m)
+    qs = rng.integers(-127, 128, m * k).astype(np.int8)
+    d = rng.integers(0, 1 << 16, m * k // 32).astype(np.uint16)
+    P = (m + 31) // 32
+    tq = dev(np.full(P * 32 * k, 99, np.int8))
+    td = dev(np.full(P * 32 * k // 32, 7, np.uint16).view(np.int16))
+    si_amd.call("si_q8_tile", si_amd.ptr(dev(qs)), si_amd.ptr(dev(d.view(np.int16))), m, k,
+                si_amd.ptr(tq), si_amd.ptr(td), None)
+    wq, wd = q8_tiled(qs, d, m, k)
+    assert np.array_equal(host(tq), wq)
+    assert np.array_equal(host(td).view(np.uint16), wd)
+
+
+@pytest.mark.parametrize("m,n,k,bias,res", [
+    (64, 3584, 18944, False, True),   # config 5's down projection (+ residual)
+    (64, 4608, 3584, True, False),    # config 5's Q|K|V (+ bias)
+    (64, 3584, 3584, False, False),   # config 5's W_O
+    (33, 200, 3872, True, True),      # ragged panel and columns, K past one LDS range
+    (5, 256, 512, True, False),
+    (1, 1152, 896, False, True),
+])
+def test_gemm_tiled_a(oracle, m, n, k, bias, res):
+    """SI_GEMM_TILED_A (operand-tiled activations streamed with the weights,
+    one pass over K) against the float64 product of the dequantized operands
+    on every row, and against the default path (planar activations) within
+    fp32 summation-order differences: the streamed kernel spreads K over 12
+    wavefronts, the default over 16 and, for long K, over workgroups."""
+    torch = _torch()
+    rng = np.random.default_rng(m * 7 + n + k)
+    w = q4(oracle, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.normal(0, 0.02, n).astype(np.float32) if bias else None
+    r = rng.standard_normal((m, n)).astype(np.float32) if res else None
+    xq = oracle.quantize_q8(x)
+    qs, d, _ = aos_to_planar(xq)
+    wqs, wd, tile = _upload_q4(w, n, k)
+    P = (m + 31) // 32
+    tq = empty(P * 32 * k, torch.int8)
+    td = empty(P * k, torch.int16)
+    si_amd.call("si_q8_tile", si_amd.ptr(dev(qs)), si_amd.ptr(dev(d.view(np.int16))), m, k,
+                si_amd.ptr(tq), si_amd.ptr(td), None)
+    b_d = dev(b) if bias else None
+    r_d = dev(r) if res else None
+
+    def gemm(xa, xs, flags, ws=None, wsb=0):
+        out = empty(m * n, torch.float32)
+        si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), tile, n, k, si_amd.ptr(xa),
+                    si_amd.ptr(xs), m, si_amd.ptr(b_d), si_amd.ptr(r_d), si_amd.ptr(out), n, flags,
+                    si_amd.ptr(ws), wsb, None)
+        return out
+
+    outs = []
+    ran = [kn for kn, _ in si_amd.kernel_times_ms(
+        "k_gemm", lambda: outs.append(gemm(tq, td, si_amd.SI_GEMM_TILED_A)))]
+    assert ran == ["k_gemm_bd<1, 2, 0, 12, true, true>"], ran
+    got = host(outs[0]).reshape(m, n)
+    want = dequant_q8(xq, m, k) @ dequant_q4(w, n, k).T
+    if bias:
+        want = want + b[None, :].astype(np.float64)
+    if res:
+        want = want + r.astype(np.float64)
+    rms = np.sqrt(np.mean(want ** 2))
+    err = np.abs(got - want).max(axis=1) / rms
+    bad = np.nonzero(err > 1e-5)[0]
+    assert bad.size == 0, f"rows off, first {bad[:8].tolist()}, worst {err.max():.3g}"
+    wsb = si_amd.lib().si_gemm_workspace(m, n, k)
+    ws = empty(max(wsb, 4), torch.uint8)
+    ref = host(gemm(dev(qs), dev(d.view(np.int16)), 0, ws, wsb)).reshape(m, n)
+    assert np.abs(got - ref).max() / rms <= 2e-6
+    again = host(gemm(tq, td, si_amd.SI_GEMM_TILED_A)).reshape(m, n)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "not deterministic"
 
 
 @pytest.mark.parametrize("shape,ntok,pos0", [("0.5b", 1, 1023), ("7b", 5, 0), ("7b", 3, 4093)])

@@ -11,7 +11,8 @@ import pytest
 import si_amd
 from oracle.oracle_py import Q8_DTYPE, make_shape as or_shape
 from tests.chain import E2E_BOUND, LayerBuffers, check_row, end_to_end_report
-from tests.gpu_helpers import close, dev, empty, host, kv_history, make_layer
+from tests.gpu_helpers import (close, dev, device_view, empty, host, kv_history, make_layer,
+                               q8_tiled)
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ref_golden.npz")
@@ -316,6 +317,16 @@ def test_batched_decode_7b(oracle, nseq, ctx, check, flags):
     out = empty(nseq * s.hidden, torch.float32)
     L.decode_batch(dev(x), nseq, kc, vc, stride, ctx, ctx, out, flags=flags)
     B = LayerBuffers(L, os_, nseq)
+    if flags != EXACT:
+        # the down projection read the SwiGLU Q8 operand-tiled: that copy
+        # holds the planar one's bytes (every row, padding zero)
+        F, P = s.ffn, (nseq + 31) // 32
+        qs = host(device_view(L.buffer("ACTQ_QS"), nseq * F, torch.int8).clone())
+        d = host(device_view(L.buffer("ACTQ_D"), nseq * F // 32, torch.int16).clone())
+        tq = host(device_view(L.buffer("ACTQ_TQ"), P * 32 * F, torch.int8).clone())
+        td = host(device_view(L.buffer("ACTQ_TD"), P * F, torch.int16).clone())
+        wq, wd = q8_tiled(qs, d.view(np.uint16), nseq, F)
+        assert np.array_equal(tq, wq) and np.array_equal(td.view(np.uint16), wd)
     hk, hv = host(kc).view(np.uint16), host(vc).view(np.uint16)
     got = host(out).reshape(nseq, s.hidden)
     for i in check:

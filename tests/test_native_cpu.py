@@ -59,6 +59,16 @@ def test_argument_errors_do_not_launch():
                           1 << 20, 0, None, 0, None) == si_amd.SI_ERR_ARG
     assert b"2 GiB" in L.si_last_error()
     assert L.si_gemm_workspace(64, 3584, 18944) > 0  # small grid: K is split
+    # operand-tiled activations: at most 64 rows, no exact mode
+    assert L.si_gemm_q4q8(a16, a16, 8, 64, 64, a16, a16, 65, None, None, a16, 64,
+                          si_amd.SI_GEMM_TILED_A, None, 0, None) == si_amd.SI_ERR_ARG
+    assert b"at most 64 rows" in L.si_last_error()
+    assert L.si_gemm_q4q8(a16, a16, 8, 64, 64, a16, a16, 4, None, None, a16, 64,
+                          si_amd.SI_GEMM_TILED_A | si_amd.SI_GEMM_EXACT, None, 0,
+                          None) == si_amd.SI_ERR_ARG
+    assert L.si_q8_tile(a16, a16, 4, 48, a16, a16, None) == si_amd.SI_ERR_ARG  # k % 32
+    assert L.si_q8_tile(odd, a16, 4, 64, a16, a16, None) == si_amd.SI_ERR_ARG
+    assert b"16-byte aligned" in L.si_last_error()
     assert L.si_gemm_workspace(2048, 3584, 3584) == 0
     assert L.si_matvec_q4q8(None, None, 8, 64, 64, None, None, None, None, None, None, 0,
                             None) == si_amd.SI_ERR_ARG
