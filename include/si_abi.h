@@ -139,11 +139,12 @@ int si_q4q8_block_dots(const uint8_t *wqs, const uint16_t *wd, int n, int k,
  * integer-valued operands (one fused multiply-add per output and block in
  * place of a conversion and one); slower than the default int8 formulation
  * at the layer shapes measured on MI355X, kept as the measured alternative.
- * SI_GEMM_TILED_A (si_gemm_q4q8 only, m <= 64, not with SI_GEMM_EXACT): xqs
- * and xd hold the activations operand-tiled (si_q8_tile); the product runs
- * in one pass over any K (no workspace) with each block's activations
- * streamed next to its weights.  Per output the same sum as the default,
- * in the same order where the default runs one pass. */
+ * SI_GEMM_TILED_A (m <= 64, alone): xqs and xd hold the activations
+ * operand-tiled (si_q8_tile), streamed next to the weights block by block.
+ * si_gemm_q4q8: one pass over any K (no workspace); the same sums as the
+ * default within fp32 summation order (K is spread over 12 wavefronts
+ * instead of 16).  si_gemm_gateup_q8 (k <= 3840): the same results as the
+ * default bit for bit. */
 enum { SI_GEMM_EXACT = 1, SI_GEMM_F16 = 2, SI_GEMM_TILED_A = 4 };
 
 /* Operand-tiled Q8_0 (the activation operand of SI_GEMM_TILED_A): rows in

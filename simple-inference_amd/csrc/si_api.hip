@@ -355,10 +355,19 @@ int si_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, i
     SI_REQUIRE(((uintptr_t)wqs & 15) == 0 && ((uintptr_t)xqs & 15) == 0 &&
                    ((uintptr_t)qs & 15) == 0 && ((uintptr_t)act & 15) == 0,
                "gemm_gateup: wqs, xqs, qs and act must be 16-byte aligned");
-    SI_REQUIRE((flags & ~(SI_GEMM_EXACT | SI_GEMM_F16)) == 0, "gemm_gateup: unknown flags %d",
-               flags);
+    SI_REQUIRE((flags & ~(SI_GEMM_EXACT | SI_GEMM_F16 | SI_GEMM_TILED_A)) == 0,
+               "gemm_gateup: unknown flags %d", flags);
     SI_REQUIRE(!(flags & SI_GEMM_F16) || !(flags & SI_GEMM_EXACT),
                "gemm_gateup: SI_GEMM_F16 is a fast-path formulation (not with SI_GEMM_EXACT)");
+    if (flags & SI_GEMM_TILED_A) {
+        SI_REQUIRE(flags == SI_GEMM_TILED_A, "gemm_gateup: SI_GEMM_TILED_A takes no other flag");
+        SI_REQUIRE(m == 0 || gemm_gateup_streams(m, f, k),
+                   "gemm_gateup: SI_GEMM_TILED_A needs m <= 64 and k <= 3840 (m=%d f=%d k=%d)",
+                   m, f, k);
+        launch_gemm_gateup_q8(wqs, wd, tile, f, k, xqs, xd, m, gu, act, qs, d, bsum, false,
+                              nullptr, 0, S(stream), false, nullptr, nullptr, xqs, xd);
+        return check_launch("si_gemm_gateup_q8");
+    }
     launch_gemm_gateup_q8(wqs, wd, tile, f, k, xqs, xd, m, gu, act, qs, d, bsum,
                           (flags & SI_GEMM_EXACT) != 0, workspace, workspace ? ws_bytes : 0,
                           S(stream), (flags & SI_GEMM_F16) != 0);

@@ -1268,7 +1268,73 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
         }
         lds_barrier();  // the area is written again next
     };
+    // MODE 1: SwiGLU + Q8_0 of the gate|up pair (row, feat); every lane of
+    // the half-wavefront calls it (quant_block_lane reduces over the 32
+    // features of the row's block)
+    auto gateup_out = [&](int row, int feat, float gv, float uv) {
+        const int f = go.f;
+        const float silu = __fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)));
+        const float av = __fmul_rn(silu, uv);
+        uint16_t dbits;
+        int bsum;
+        const int qv = quant_block_lane(av, dbits, bsum);  // all 32 lanes of the half
+        if (row < m && feat < f) {
+            const size_t o = (size_t)row * f + feat;
+            if (out) {
+                out[(size_t)row * ldo + feat] = gv;
+                out[(size_t)row * ldo + f + feat] = uv;
+            }
+            if (go.act) go.act[o] = av;
+            go.qs[o] = (int8_t)qv;
+            if (j == 0) {
+                go.d[o / SI_QK] = dbits;
+                if (go.s) go.s[o / SI_QK] = (int16_t)bsum;
+            }
+            if (go.tq) {
+                const size_t pb = (size_t)(row >> 5) * (f / SI_QK) + feat / SI_QK;
+                go.tq[q8_tiled_byte(pb, row & 31, j)] = (int8_t)qv;
+                if (j == 0) go.td[pb * 32 + (row & 31)] = dbits;
+            }
+        }
+    };
+    // DEFER (gate|up with streamed activations, whose LDS is free): at a
+    // tile's end every wavefront's partial sums go to LDS ([W][TN][16][64]
+    // floats), one barrier, and all wavefronts sum the (tile, register)
+    // pairs into the slot's sums ([units][TN][16][64]) in reduce()'s order
+    // (w + 8 added to w < W - 8, then w = 0..7 in turn: the same bits);
+    // SwiGLU + Q8_0 of all the slot's units run once after the last (every
+    // wavefront takes (unit, register) items).  Two barriers per unit
+    // instead of eight, and no epilogue between units.
+    constexpr bool DEFER = MODE == 1 && DA;
+    float *dpart = (float *)bd_sm;
+    float *dsum = dpart + BD_W * TN * 16 * 64;
+    auto finish_defer = [&](int iu) {
+#pragma unroll
+        for (int u = 0; u < TN; ++u)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) dpart[((wave * TN + u) * 16 + v) * 64 + lane] = acc[u][v];
+        lds_barrier();
+        for (int q = wave; q < TN * 16; q += BD_W) {  // q = 16 u + v, wavefront-uniform
+            auto part = [&](int w) {  // wavefront w's sum, with w + 8's added as reduce() does
+                const float t = dpart[(w * TN * 16 + q) * 64 + lane];
+                return w < BD_W - 8 ? __fadd_rn(t, dpart[((w + 8) * TN * 16 + q) * 64 + lane]) : t;
+            };
+            float sum = part(0);
+#pragma unroll
+            for (int w = 1; w < 8; ++w) sum = __fadd_rn(sum, part(w));
+            dsum[(iu * TN * 16 + q) * 64 + lane] = sum * 0.0625f;  // the operands' 16x, exactly
+        }
+        lds_barrier();  // the partial area is written again next
+#pragma unroll
+        for (int u = 0; u < TN; ++u)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[u][v] = 0.0f;
+    };
     auto finish = [&](int iu) {
+        if constexpr (DEFER) {
+            finish_defer(iu);
+            return;
+        }
         float r[TN][2];
 #pragma unroll
         for (int u = 0; u < TN; ++u) reduce(acc[u], r[u]);
@@ -1277,31 +1343,7 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
             if (wave >= 8) break;  // the partial sums only
             const int row = m0 + 8 * (wave >> 1) + 4 * g + 2 * (wave & 1) + i;
             if (MODE == 1) {
-                const int f = go.f, feat = col0(iu, 0) + j;
-                const float gv = r[0][i], uv = r[TN - 1][i];
-                const float silu = __fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)));
-                const float av = __fmul_rn(silu, uv);
-                uint16_t dbits;
-                int bsum;
-                const int qv = quant_block_lane(av, dbits, bsum);  // all 32 lanes of the half
-                if (row < m && feat < f) {
-                    const size_t o = (size_t)row * f + feat;
-                    if (out) {
-                        out[(size_t)row * ldo + feat] = gv;
-                        out[(size_t)row * ldo + f + feat] = uv;
-                    }
-                    if (go.act) go.act[o] = av;
-                    go.qs[o] = (int8_t)qv;
-                    if (j == 0) {
-                        go.d[o / SI_QK] = dbits;
-                        if (go.s) go.s[o / SI_QK] = (int16_t)bsum;
-                    }
-                    if (go.tq) {
-                        const size_t pb = (size_t)(row >> 5) * (f / SI_QK) + feat / SI_QK;
-                        go.tq[q8_tiled_byte(pb, row & 31, j)] = (int8_t)qv;
-                        if (j == 0) go.td[pb * 32 + (row & 31)] = dbits;
-                    }
-                }
+                gateup_out(row, col0(iu, 0) + j, r[0][i], r[TN - 1][i]);
             } else {
                 const int col = col0(iu, 0) + j;
                 if (row < m && col < n) {
@@ -1369,6 +1411,17 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
                 load(st[i]);
                 __builtin_amdgcn_sched_barrier(0);
             }
+        }
+    }
+    if constexpr (DEFER) {
+        // the slot's sums are complete (the last tile ended on a barrier):
+        // SwiGLU + Q8_0 of (unit, register) items; register v holds rows
+        // 8 (v / 4) + 4 g + v % 4 of the tile, lane j feature j
+        for (int it = wave; it < nu * 16; it += BD_W) {
+            const int iu = it >> 4, v = it & 15;
+            const float gv = dsum[((iu * TN) * 16 + v) * 64 + lane];
+            const float uv = dsum[((iu * TN + TN - 1) * 16 + v) * 64 + lane];
+            gateup_out(m0 + 8 * (v >> 2) + 4 * g + (v & 3), col0(iu, 0) + j, gv, uv);
         }
     }
 }
@@ -1511,6 +1564,7 @@ static GemmPlan gemm_plan(int m, int n, int nb) {
 // i % 8 and the H halves of a slot share one, so S is sized for at most 32
 // (one XCD's CUs) per XCD: C * S <= 8 * floor(32 / H).
 constexpr int BD_SMALL_M = 64;  // every projection and the gate|up pair
+constexpr int BD_GU_W = 12;     // wavefronts of the gate|up instances
 constexpr int BD_MAX_M = 512;   // one-tile projections, when bd_takes() says so
 struct BdPlan {
     int H, C, S, cb, units, grid;
@@ -1529,6 +1583,14 @@ static BdPlan bd_plan(int m, int n, int nb, int mode, bool da = false) {
     p.S = std::max(1, std::min(8 * per_xcd / p.C, p.units));
     p.grid = 8 * p.H * ((p.C * p.S + 7) / 8);
     p.lds = da ? (size_t)BD_RED : bd_lds(p.cb);
+    if (da && mode == 1) {
+        // k_gemm_bd's deferred gate|up epilogue: the wavefronts' partial
+        // sums and the slot's unit sums, 8 KB each; too many units per slot
+        // for the LDS: staged activations and the per-unit epilogue instead
+        const size_t units_per_slot = (size_t)(p.units + p.S - 1) / p.S;
+        p.lds = (BD_GU_W + units_per_slot) * 8192;
+        if (p.lds > (size_t)BD_LDS_MAX) return bd_plan(m, n, nb, mode, false);
+    }
     return p;
 }
 
@@ -1589,12 +1651,14 @@ static void launch_bd(const BdPlan &p, int mode, const uint8_t *wqs, const uint1
     // streamed one-tile projections: 12 wavefronts, 2 stages, pipelined (7B
     // x 64 rows, cold weights: down 24.4 -> 23.3 us, QKV 13.0 -> 12.0, O
     // 8.7 -> 7.8 against 16 wavefronts x 4 stages unpipelined; 8 or 16
-    // wavefronts and 3-12 stages took as long or longer)
+    // wavefronts and 3-12 stages took as long or longer).  Streamed gate|up:
+    // 12 wavefronts, 2 stages (7B x 64 rows, cold weights: 41.3 us; 3-6
+    // stages 41.6-44.9, 16 wavefronts 42.9; staged 43.7)
     if (mode == 1) {
         if (p.da)
-            BD(2, 3, 1, 12, true, false);
+            BD(2, 2, 1, BD_GU_W, true, false);
         else
-            BD(2, 4, 1, 12, false, false);
+            BD(2, 4, 1, BD_GU_W, false, false);
     } else if (p.da) {
         BD(1, 2, 0, 12, true, true);
     } else {
@@ -1642,6 +1706,10 @@ void launch_gemm_q4q8_tiled(const uint8_t *wqs, const uint16_t *wd, int tile, in
 
 bool gemm_gateup_tiles_out(int m, int k, bool exact, bool f16) {
     return !exact && !f16 && m <= BD_SMALL_M && k / SI_QK <= BD_MAX_CB;
+}
+
+bool gemm_gateup_streams(int m, int f, int k) {
+    return gemm_gateup_tiles_out(m, k, false, false) && bd_plan(m, 2 * f, k / SI_QK, 1, true).da;
 }
 
 static int gemm_core(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
@@ -1732,10 +1800,9 @@ void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int
     }
     if (gemm_gateup_tiles_out(m, k, exact, f16)) {
         // the activations streamed when given operand-tiled (txq / txd)
-        const bool da = txq && txd;
-        launch_bd(bd_plan(m, n, nb, 1, da), 1, wqs, wd, tile, n, nb, da ? txq : xqs,
-                  da ? txd : xd, m, nullptr, nullptr, gu, n, nullptr,
-                  GateUpOut{f, act, qs, d, s, tq, td}, st);
+        const BdPlan p = bd_plan(m, n, nb, 1, txq && txd);
+        launch_bd(p, 1, wqs, wd, tile, n, nb, p.da ? txq : xqs, p.da ? txd : xd, m, nullptr,
+                  nullptr, gu, n, nullptr, GateUpOut{f, act, qs, d, s, tq, td}, st);
         return;
     }
     // a K split (gemm_core's own plan: k_gemm_bd's K-range partials or the

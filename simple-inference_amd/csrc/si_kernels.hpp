@@ -89,6 +89,8 @@ void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int
                            const int8_t *txq = nullptr, const uint16_t *txd = nullptr);
 // Whether launch_gemm_gateup_q8 writes tq/td for m rows over K = k.
 bool gemm_gateup_tiles_out(int m, int k, bool exact, bool f16);
+// Whether it streams txq/txd (default flags) for m rows, f features, K = k.
+bool gemm_gateup_streams(int m, int f, int k);
 size_t gemm_workspace_bytes(int m, int n, int k);
 // workspace launch_gemm_gateup_q8 uses for f features (0: never splits K)
 size_t gemm_gateup_workspace_bytes(int m, int f, int k);

@@ -737,6 +737,52 @@ def test_gemm_gateup_q8(oracle, m, f, k, tile, flags, act_out):
     assert np.array_equal(host(asum), want_s)
 
 
+@pytest.mark.parametrize("m,f,k", [(64, 18944, 3584), (33, 4864, 896), (2, 256, 512),
+                                   (64, 160, 3840)])
+def test_gemm_gateup_tiled_a_bit_identical(oracle, m, f, k):
+    """SI_GEMM_TILED_A on the gate|up GEMM (operand-tiled activations
+    streamed with the weights; the wavefronts' partial sums reduced in LDS
+    per tile, SwiGLU + Q8_0 of all a workgroup's tiles at its end) gives the
+    default's gate|up, SwiGLU and Q8_0 bit for bit: the same blocks per
+    wavefront and the same order of sums.  Ragged row panels included;
+    shapes it does not take are refused."""
+    torch = _torch()
+    rng = np.random.default_rng(m + 5 * f)
+    w = np.concatenate([q4(oracle, rng, f, k), q4(oracle, rng, f, k)])
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    qs, d, _ = aos_to_planar(oracle.quantize_q8(x))
+    wqs, wd, _ = _upload_q4(w, 2 * f, k, 32)
+    P = (m + 31) // 32
+    tq = empty(P * 32 * k, torch.int8)
+    td = empty(P * k, torch.int16)
+    si_amd.call("si_q8_tile", si_amd.ptr(dev(qs)), si_amd.ptr(dev(d.view(np.int16))), m, k,
+                si_amd.ptr(tq), si_amd.ptr(td), None)
+    ins = {0: (dev(qs), dev(d.view(np.int16))), si_amd.SI_GEMM_TILED_A: (tq, td)}
+    outs = []
+    for flags, (xa, xs) in ins.items():
+        gu = empty(m * 2 * f, torch.float32)
+        act = empty(m * f, torch.float32)
+        aq, ad = empty(m * f, torch.int8), empty(m * f // 32, torch.int16)
+        asum = empty(m * f // 32, torch.int16)
+
+        def run():
+            si_amd.call("si_gemm_gateup_q8", si_amd.ptr(wqs), si_amd.ptr(wd), 32, f, k,
+                        si_amd.ptr(xa), si_amd.ptr(xs), m, si_amd.ptr(gu), si_amd.ptr(act),
+                        si_amd.ptr(aq), si_amd.ptr(ad), si_amd.ptr(asum), flags, None, 0, None)
+        ran = [kn for kn, _ in si_amd.kernel_times_ms("k_gemm", run)]
+        assert len(ran) == 1 and ran[0].startswith("k_gemm_bd<2,") and \
+            ran[0].endswith(", true, false>" if flags else ", false, false>"), ran
+        outs.append([host(t) for t in (gu, act, aq, ad, asum)])
+    for name, a, b in zip(("gate|up", "SwiGLU", "Q8", "scales", "block sums"), *outs):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), name
+    L = si_amd.lib()
+    a16 = 1 << 12
+    assert L.si_gemm_gateup_q8(a16, a16, 32, 64, 64, a16, a16, 65, None, None, a16, a16, None,
+                               si_amd.SI_GEMM_TILED_A, None, 0, None) == si_amd.SI_ERR_ARG
+    assert L.si_gemm_gateup_q8(a16, a16, 32, 64, 3872, a16, a16, 8, None, None, a16, a16, None,
+                               si_amd.SI_GEMM_TILED_A, None, 0, None) == si_amd.SI_ERR_ARG
+
+
 @pytest.mark.parametrize("m,f,k", [(130, 96, 256), (600, 4864, 896), (2048, 18944, 3584),
                                    (77, 160, 3840)])
 def test_gemm_gateup_f16_formulation_bit_identical(oracle, m, f, k):
