@@ -139,7 +139,8 @@ int si_q4q8_block_dots(const uint8_t *wqs, const uint16_t *wd, int n, int k,
  * integer-valued operands (one fused multiply-add per output and block in
  * place of a conversion and one); slower than the default int8 formulation
  * at the layer shapes measured on MI355X, kept as the measured alternative.
- * SI_GEMM_TILED_A (m <= 64, alone): xqs and xd hold the activations
+ * SI_GEMM_TILED_A (si_gemm_q4q8: m <= 512; si_gemm_gateup_q8: m <= 64; alone):
+ * xqs and xd hold the activations
  * operand-tiled (si_q8_tile), streamed next to the weights block by block.
  * si_gemm_q4q8: one pass over any K (no workspace); the same sums as the
  * default within fp32 summation order (K is spread over 12 wavefronts
@@ -451,8 +452,8 @@ enum {
     SI_BUF_GU,          /* fp32 [rows][2 ffn] gate | up         */
     SI_BUF_ACT,         /* fp32 [rows][ffn]                     */
     SI_BUF_ACTQ_QS, SI_BUF_ACTQ_D, SI_BUF_ACTQ_S,
-    SI_BUF_ACTQ_TQ,     /* act Q8_0 operand-tiled, batched calls of 2..64 rows */
-    SI_BUF_ACTQ_TD,     /* (what the down projection read; else not written)  */
+    SI_BUF_ACTQ_TQ,     /* act Q8_0 operand-tiled: calls of 2..512 rows whose  */
+    SI_BUF_ACTQ_TD,     /* down projection streamed it (else not written)     */
     SI_BUF_COUNT
 };
 void *si_layer_buffer(si_layer_t *l, int which);

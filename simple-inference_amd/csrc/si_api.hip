@@ -311,7 +311,7 @@ int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
     SI_REQUIRE((flags & ~(SI_GEMM_EXACT | SI_GEMM_TILED_A)) == 0, "gemm: unknown flags %d", flags);
     if (flags & SI_GEMM_TILED_A) {
         SI_REQUIRE(!(flags & SI_GEMM_EXACT), "gemm: SI_GEMM_TILED_A has no exact mode");
-        SI_REQUIRE(m <= 64, "gemm: SI_GEMM_TILED_A takes at most 64 rows (m=%d)", m);
+        SI_REQUIRE(m <= 512, "gemm: SI_GEMM_TILED_A takes at most 512 rows (m=%d)", m);
         launch_gemm_q4q8_tiled(wqs, wd, tile, n, k, xqs, xd, m, bias, residual, out, ldo,
                                S(stream));
         return check_launch("si_gemm_q4q8");
@@ -763,9 +763,9 @@ static int make_workspace(const si_shape_t *s, int max_tokens, int max_pos,
         TRY(m.alloc(&W->actq.s, M * F / 32));
     }
     if (max_tokens >= 2) {
-        // operand-tiled copies of the four GEMM inputs for calls of 2..64
+        // operand-tiled copies of the four GEMM inputs for calls of 2..512
         // rows (the projections then stream them); padding rows stay zero
-        const size_t tr = (size_t)(std::min(max_tokens, 64) + 31) / 32 * 32;
+        const size_t tr = (size_t)(std::min(max_tokens, 512) + 31) / 32 * 32;
         auto tiled = [&](Q8Buf &b, size_t k) -> int {
             TRY(m.alloc(&b.tq, tr * k));
             TRY(m.alloc(&b.td, tr * k / 32));
@@ -1211,18 +1211,25 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
     const bool cap = (flags & SI_LAYER_CAPTURE) != 0;
     SI_REQUIRE(!full || L->ffn, "layer has no FFN weights: use SI_LAYER_ATTN_ONLY");
     for (bool &h : L->phase_hit) h = false;
-    // 2..64 rows, not exact: every Q8 activation is also written operand-
-    // tiled and the projections stream it (k_gemm_bd's streamed mode)
+    // 2..512 rows, not exact: the Q8 activations are also written operand-
+    // tiled, and the projections whose plan is the one-tile kernel stream
+    // them (k_gemm_bd's streamed mode, gemm_streams)
     const bool ex = (flags & SI_LAYER_EXACT) != 0;
-    const bool tl = rows >= 2 && rows <= 64 && !ex && L->xq.tq;
+    const bool tl = rows >= 2 && rows <= 512 && !ex && L->xq.tq;
     // qwen_one_layer.c:247-250: RMSNorm -> Q8
     mark(L, SI_PHASE_RMS_Q8, st);
+    // up to 64 rows every projection streams; past that only down (below)
+    const bool tl_x = tl && rows <= 64;
     launch_rmsnorm_q8(x, nullptr, L->norm, rows, H, s.rms_eps, nullptr, capt(cap, L->normed),
-                      L->xq.qs, L->xq.d, L->xq.s, st, tl ? L->xq.tq : nullptr,
-                      tl ? L->xq.td : nullptr);
+                      L->xq.qs, L->xq.d, L->xq.s, st, tl_x ? L->xq.tq : nullptr,
+                      tl_x ? L->xq.td : nullptr);
     // :253-258: Q, K, V projections (+bias), fused into one N = qd + 2 kvd matrix
     mark(L, SI_PHASE_QKV, st);
-    if (tl)
+    // past 64 rows only the down projection streams: there the K-split
+    // partials and their reduce disappear (0.5B, 512 rows: 21.0 -> 16.6 us),
+    // while Q|K|V gains little (10.1 -> 10.0 us) and its changed sum order
+    // would move the fp16 K/V rows the later rows attend to
+    if (tl_x && gemm_streams(rows, NQKV, H))
         launch_gemm_q4q8_tiled(L->wqkv.qs, L->wqkv.d, L->wqkv.tile, NQKV, H, L->xq.tq, L->xq.td,
                                rows, L->bqkv, nullptr, L->qkv, NQKV, st);
     else
@@ -1243,10 +1250,10 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
                             L->rope_sin, kc, vc, kv_seq_stride, ctx_dev, ctx0, max_ctx,
                             capt(cap, L->q), ns, L->attn_ws, nullptr, nullptr, nullptr, nullptr,
                             st, pg);
-            tl_att = tl;
+            tl_att = tl_x;
             launch_attn_combine(rows, s.qheads, s.hdim, ns, L->attn_ws, L->attn, L->attq.qs,
-                                L->attq.d, L->attq.s, st, tl ? L->attq.tq : nullptr,
-                                tl ? L->attq.td : nullptr);
+                                L->attq.d, L->attq.s, st, tl_x ? L->attq.tq : nullptr,
+                                tl_x ? L->attq.td : nullptr);
         }
     } else {
         mark(L, SI_PHASE_ROPE_KV, st);
@@ -1274,7 +1281,7 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
     // W_O; a K-split leaves its partials to the post-norm kernel, which sums
     // them (o, kept in attn_out) on the way
     int osplits = 0;
-    if (tl_att)
+    if (tl_att && gemm_streams(rows, L->wo.n, L->wo.k))
         launch_gemm_q4q8_tiled(L->wo.qs, L->wo.d, L->wo.tile, L->wo.n, L->wo.k, L->attq.tq,
                                L->attq.td, rows, nullptr, nullptr, L->attn_out, L->wo.n, st);
     else
@@ -1286,17 +1293,16 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
     if (osplits > 1)
         launch_rmsnorm_q8_parts(x, (const float *)L->gemm_ws, osplits, L->post_norm, rows, H,
                                 s.rms_eps, L->attn_out, L->h, capt(cap, L->normed2), L->xq2.qs,
-                                L->xq2.d, L->xq2.s, st, tl ? L->xq2.tq : nullptr,
-                                tl ? L->xq2.td : nullptr);
+                                L->xq2.d, L->xq2.s, st, tl_x ? L->xq2.tq : nullptr,
+                                tl_x ? L->xq2.td : nullptr);
     else
         launch_rmsnorm_q8(x, L->attn_out, L->post_norm, rows, H, s.rms_eps, L->h,
                           capt(cap, L->normed2), L->xq2.qs, L->xq2.d, L->xq2.s, st,
-                          tl ? L->xq2.tq : nullptr, tl ? L->xq2.td : nullptr);
+                          tl_x ? L->xq2.tq : nullptr, tl_x ? L->xq2.td : nullptr);
     mark(L, SI_PHASE_GATE_UP, st);
-    // the SwiGLU Q8 also operand-tiled where the fused gate|up pass runs;
-    // the down projection then streams it in one pass (no K split, no
-    // reduce)
-    const bool tiled = tl && gemm_gateup_tiles_out(rows, H, ex, false);
+    // the SwiGLU Q8 also operand-tiled; a streamed down projection runs in
+    // one pass (no K split, no reduce)
+    const bool tiled = tl && gemm_streams(rows, H, s.ffn);
     if (rows == 1) {
         project(L, L->wgu, rows, L->xq2, nullptr, nullptr, L->gu, flags, st);
         mark(L, SI_PHASE_SWIGLU_Q8, st);
@@ -1310,7 +1316,7 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
                               rows, capt(cap || ex, L->gu), capt(cap, L->act), L->actq.qs,
                               L->actq.d, L->actq.s, ex, L->gemm_ws, L->gemm_ws_bytes, st, false,
                               tiled ? L->actq.tq : nullptr, tiled ? L->actq.td : nullptr,
-                              tl ? L->xq2.tq : nullptr, tl ? L->xq2.td : nullptr);
+                              tl_x ? L->xq2.tq : nullptr, tl_x ? L->xq2.td : nullptr);
         mark(L, SI_PHASE_SWIGLU_Q8, st);
     }
     mark(L, SI_PHASE_DOWN, st);

@@ -492,6 +492,15 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
                     go.d[o / SI_QK] = dbits;
                     if (go.s) go.s[o / SI_QK] = (int16_t)bsum;
                 }
+                if (go.tq) {
+                    // bytes 16hh..16hh+7 and +8..+15 of the row's block: the
+                    // first 8 of halves 0 and 1 at position 8hh
+                    const size_t pb = (size_t)(row >> 5) * (f / SI_QK) + fb / SI_QK;
+                    int8_t *tb = go.tq + q8_tiled_byte(pb, row & 31, 16 * hh);
+                    *(uint2 *)tb = make_uint2(pk[0], pk[1]);
+                    *(uint2 *)(tb + 512) = make_uint2(pk[2], pk[3]);
+                    if (hh == 0) go.td[pb * 32 + (row & 31)] = dbits;
+                }
             }
         }
         return;
@@ -876,6 +885,15 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm_h16(
                 if (hh == 0) {
                     go.d[o / SI_QK] = dbits;
                     if (go.s) go.s[o / SI_QK] = (int16_t)bsum;
+                }
+                if (go.tq) {
+                    // bytes 16hh..16hh+7 and +8..+15 of the row's block: the
+                    // first 8 of halves 0 and 1 at position 8hh
+                    const size_t pb = (size_t)(row >> 5) * (f / SI_QK) + fb / SI_QK;
+                    int8_t *tb = go.tq + q8_tiled_byte(pb, row & 31, 16 * hh);
+                    *(uint2 *)tb = make_uint2(pk[0], pk[1]);
+                    *(uint2 *)(tb + 512) = make_uint2(pk[2], pk[3]);
+                    if (hh == 0) go.td[pb * 32 + (row & 31)] = dbits;
                 }
             }
         }
@@ -1432,7 +1450,7 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
 __global__ void __launch_bounds__(256) k_gemm_reduce_swiglu_q8(
     const float *__restrict__ part, int splits, int m, int f, float *__restrict__ gu,
     float *__restrict__ act, int8_t *__restrict__ qs, uint16_t *__restrict__ d,
-    int16_t *__restrict__ bs) {
+    int16_t *__restrict__ bs, int8_t *__restrict__ tq, uint16_t *__restrict__ td) {
     const int nbr = f / SI_QK;
     const int blk = blockIdx.x * 8 + (threadIdx.x >> 5);
     const int j = threadIdx.x & 31;
@@ -1461,6 +1479,11 @@ __global__ void __launch_bounds__(256) k_gemm_reduce_swiglu_q8(
     if (j == 0) {
         d[blk] = dbits;
         if (bs) bs[blk] = (int16_t)bsum;
+    }
+    if (tq) {
+        const size_t pb = (size_t)(r >> 5) * nbr + b;
+        tq[q8_tiled_byte(pb, r & 31, j)] = (int8_t)q;
+        if (j == 0) td[pb * 32 + (r & 31)] = dbits;
     }
 }
 
@@ -1704,12 +1727,20 @@ void launch_gemm_q4q8_tiled(const uint8_t *wqs, const uint16_t *wd, int tile, in
               out, ldo, nullptr, GateUpOut{}, st);
 }
 
-bool gemm_gateup_tiles_out(int m, int k, bool exact, bool f16) {
-    return !exact && !f16 && m <= BD_SMALL_M && k / SI_QK <= BD_MAX_CB;
-}
+// gate|up's fused k_gemm_bd pass (default flags, no f16)
+static bool gateup_bd(int m, int k) { return m <= BD_SMALL_M && k / SI_QK <= BD_MAX_CB; }
 
 bool gemm_gateup_streams(int m, int f, int k) {
-    return gemm_gateup_tiles_out(m, k, false, false) && bd_plan(m, 2 * f, k / SI_QK, 1, true).da;
+    return gateup_bd(m, k) && bd_plan(m, 2 * f, k / SI_QK, 1, true).da;
+}
+
+bool gemm_streams(int m, int n, int k) {
+    const int nb = k / SI_QK;
+    if (m <= BD_SMALL_M) return true;
+    if (m > BD_MAX_M || !bd_takes(m, n, nb)) return false;
+    // a slot's serial work with one K range, as bd_takes bounds it
+    const BdPlan p = bd_plan(m, n, nb, 0, true);
+    return (p.units + p.S - 1) / p.S * nb <= 1024;
 }
 
 static int gemm_core(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
@@ -1795,10 +1826,10 @@ void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int
         // measured), one pass over K
         launch_h16<2, 4, 2, 2, true>(dim3((n + 255) / 256, (m + 127) / 128, 1), wqs, wd, tile, n,
                                      nb, xqs, xd, m, nullptr, nullptr, gu, n, nullptr, nb,
-                                     GateUpOut{f, act, qs, d, s}, st);
+                                     GateUpOut{f, act, qs, d, s, tq, td}, st);
         return;
     }
-    if (gemm_gateup_tiles_out(m, k, exact, f16)) {
+    if (!exact && gateup_bd(m, k)) {
         // the activations streamed when given operand-tiled (txq / txd)
         const BdPlan p = bd_plan(m, n, nb, 1, txq && txd);
         launch_bd(p, 1, wqs, wd, tile, n, nb, p.da ? txq : xqs, p.da ? txd : xd, m, nullptr,
@@ -1816,14 +1847,14 @@ void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int
         if (splits > 1) {
             const int tot = m * (f / SI_QK);
             SI_LAUNCH(k_gemm_reduce_swiglu_q8, dim3((tot + 7) / 8), dim3(256), 0, st,
-                      (const float *)workspace, splits, m, f, gu, act, qs, d, s);
+                      (const float *)workspace, splits, m, f, gu, act, qs, d, s, tq, td);
         } else {
-            launch_swiglu_q8(gu, m, f, act, qs, d, s, st);
+            launch_swiglu_q8(gu, m, f, act, qs, d, s, st, tq, td);
         }
         return;
     }
     const GemmPlan p = gemm_plan(m, n, nb);
-    const GateUpOut go{f, act, qs, d, s};
+    const GateUpOut go{f, act, qs, d, s, tq, td};
     const dim3 grid((n + p.bn - 1) / p.bn, (m + p.bm - 1) / p.bm, 1);
 #define CALL(WM, WN, TM, TN)                                                                   \
     SI_LAUNCH((k_gemm_fast<WM, WN, TM, TN, true>), grid, dim3(256),                            \

@@ -37,7 +37,7 @@ void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int ro
                        float eps, float *h, float *normed, int8_t *qs, uint16_t *d, int16_t *s,
                        hipStream_t st, int8_t *tq = nullptr, uint16_t *td = nullptr);
 void launch_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs, uint16_t *d,
-                      int16_t *s, hipStream_t st);
+                      int16_t *s, hipStream_t st, int8_t *tq = nullptr, uint16_t *td = nullptr);
 void launch_q4_repack(const uint8_t *src, int n, int k, int tile, uint8_t *qs, uint16_t *d,
                       hipStream_t st);
 void launch_q4_unpack(const uint8_t *qs, const uint16_t *d, int n, int k, int tile,
@@ -78,19 +78,21 @@ void launch_gemm_q4q8_tiled(const uint8_t *wqs, const uint16_t *wd, int tile, in
                             const int8_t *tq, const uint16_t *td, int m, const float *bias,
                             const float *residual, float *out, int ldo, hipStream_t st);
 // f16: k_gemm_h16 (the f16 formulation) where the plan runs one fused pass.
-// Where gemm_gateup_tiles_out() holds for the call: tq/td (optional) get
-// the Q8_0 output operand-tiled as well, and txq/txd (optional), the same
-// activations as xqs/xd operand-tiled, are streamed instead of staged.
+// tq/td (optional): the Q8_0 output operand-tiled as well.  txq/txd
+// (optional): the same activations as xqs/xd operand-tiled, streamed instead
+// of staged where gemm_gateup_streams() holds for the call.
 void launch_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, int k,
                            const int8_t *xqs, const uint16_t *xd, int m, float *gu, float *act,
                            int8_t *qs, uint16_t *d, int16_t *s, bool exact, void *workspace,
                            size_t ws_bytes, hipStream_t st, bool f16 = false,
                            int8_t *tq = nullptr, uint16_t *td = nullptr,
                            const int8_t *txq = nullptr, const uint16_t *txd = nullptr);
-// Whether launch_gemm_gateup_q8 writes tq/td for m rows over K = k.
-bool gemm_gateup_tiles_out(int m, int k, bool exact, bool f16);
-// Whether it streams txq/txd (default flags) for m rows, f features, K = k.
+// Whether launch_gemm_gateup_q8 streams txq/txd (default flags) for m rows,
+// f features, K = k.
 bool gemm_gateup_streams(int m, int f, int k);
+// Whether launch_gemm_q4q8_tiled is the one-tile kernel's plan for m x n x k
+// (the default path would take k_gemm_bd too); it takes any m <= 512.
+bool gemm_streams(int m, int n, int k);
 size_t gemm_workspace_bytes(int m, int n, int k);
 // workspace launch_gemm_gateup_q8 uses for f features (0: never splits K)
 size_t gemm_gateup_workspace_bytes(int m, int f, int k);

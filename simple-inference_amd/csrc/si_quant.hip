@@ -218,13 +218,16 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8_v4(const float *__restrict__
     }
 }
 
-// Build-defined SwiGLU then quantize_q8: a = (g / (1 + expf(-g))) * u.
+// Build-defined SwiGLU then quantize_q8: a = (g / (1 + expf(-g))) * u
+// (tq/td, optional: the Q8_0 also operand-tiled, q8_tiled_byte).
 __global__ void __launch_bounds__(256) k_swiglu_q8(const float *__restrict__ gu, int f,
                                                    int nb_row, int total_blocks,
                                                    float *__restrict__ act,
                                                    int8_t *__restrict__ qs,
                                                    uint16_t *__restrict__ d,
-                                                   int16_t *__restrict__ s) {
+                                                   int16_t *__restrict__ s,
+                                                   int8_t *__restrict__ tq,
+                                                   uint16_t *__restrict__ td) {
     const int blk = blockIdx.x * 8 + (threadIdx.x >> 5);
     const int j = threadIdx.x & 31;
     if (blk >= total_blocks) return;
@@ -243,6 +246,11 @@ __global__ void __launch_bounds__(256) k_swiglu_q8(const float *__restrict__ gu,
     if (j == 0) {
         d[blk] = dbits;
         if (s) s[blk] = (int16_t)bsum;
+    }
+    if (tq) {
+        const size_t pb = (size_t)(r >> 5) * nb_row + b;
+        tq[q8_tiled_byte(pb, r & 31, j)] = (int8_t)q;
+        if (j == 0) td[pb * 32 + (r & 31)] = dbits;
     }
 }
 
@@ -353,11 +361,11 @@ void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int ro
 }
 
 void launch_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs, uint16_t *d,
-                      int16_t *s, hipStream_t st) {
+                      int16_t *s, hipStream_t st, int8_t *tq, uint16_t *td) {
     const int nbr = f / SI_QK, tot = nbr * rows;
     if (tot == 0) return;
     SI_LAUNCH(k_swiglu_q8, dim3((tot + 7) / 8), dim3(256), 0, st, gu, f, nbr, tot, act,
-              qs, d, s);
+              qs, d, s, tq, td);
 }
 
 void launch_q4_repack(const uint8_t *src, int n, int k, int tile, uint8_t *qs, uint16_t *d,

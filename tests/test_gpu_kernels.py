@@ -406,6 +406,8 @@ def test_q8_tile_layout(m):
     (33, 200, 3872, True, True),      # ragged panel and columns, K past one LDS range
     (5, 256, 512, True, False),
     (1, 1152, 896, False, True),
+    (512, 896, 4864, False, True),    # config 3's down projection (+ residual)
+    (200, 1152, 896, True, False),    # ragged panel past 64 rows
 ])
 def test_gemm_tiled_a(oracle, m, n, k, bias, res):
     """SI_GEMM_TILED_A (operand-tiled activations streamed with the weights,

@@ -204,6 +204,17 @@ def test_prefill_vs_oracle(oracle, shape, ntok, prefix, rows, flags):
     e2e = [end_to_end_report(got[t], want[i]) for i, t in enumerate(rows)]
     print("end-to-end vs oracle:", e2e)
     assert max(e["max_over_rms"] for e in e2e) <= E2E_BOUND[shape], e2e
+    if flags != EXACT and ntok >= 128:
+        # the down projection streamed the SwiGLU Q8 operand-tiled: that
+        # copy holds the planar one's bytes
+        torch = _torch()
+        F, P = s.ffn, (ntok + 31) // 32
+        qs = host(device_view(L.buffer("ACTQ_QS"), ntok * F, torch.int8).clone())
+        d = host(device_view(L.buffer("ACTQ_D"), ntok * F // 32, torch.int16).clone())
+        tq = host(device_view(L.buffer("ACTQ_TQ"), P * 32 * F, torch.int8).clone())
+        td = host(device_view(L.buffer("ACTQ_TD"), P * F, torch.int16).clone())
+        wq, wd = q8_tiled(qs, d.view(np.uint16), ntok, F)
+        assert np.array_equal(tq, wq) and np.array_equal(td.view(np.uint16), wd)
     L.close()
 
 

@@ -59,10 +59,10 @@ def test_argument_errors_do_not_launch():
                           1 << 20, 0, None, 0, None) == si_amd.SI_ERR_ARG
     assert b"2 GiB" in L.si_last_error()
     assert L.si_gemm_workspace(64, 3584, 18944) > 0  # small grid: K is split
-    # operand-tiled activations: at most 64 rows, no exact mode
-    assert L.si_gemm_q4q8(a16, a16, 8, 64, 64, a16, a16, 65, None, None, a16, 64,
+    # operand-tiled activations: at most 512 rows, no exact mode
+    assert L.si_gemm_q4q8(a16, a16, 8, 64, 64, a16, a16, 513, None, None, a16, 64,
                           si_amd.SI_GEMM_TILED_A, None, 0, None) == si_amd.SI_ERR_ARG
-    assert b"at most 64 rows" in L.si_last_error()
+    assert b"at most 512 rows" in L.si_last_error()
     assert L.si_gemm_q4q8(a16, a16, 8, 64, 64, a16, a16, 4, None, None, a16, 64,
                           si_amd.SI_GEMM_TILED_A | si_amd.SI_GEMM_EXACT, None, 0,
                           None) == si_amd.SI_ERR_ARG
