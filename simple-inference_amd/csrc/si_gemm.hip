@@ -1232,15 +1232,20 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
             for (int v = 0; v < 16; ++v) acc[u][v] = fmaf((float)dot[v], sc[v], acc[u][v]);
         }
     };
-    // PIPE: the products of a block (issue), consumed one step later (epi)
-    auto issue = [&](const BdStage<TN> &st, const v4i &aop, uint16_t xs, v16i &dot, v16f &sc) {
+    // PIPE: the products of a block (issue), consumed one step later (epi).
+    // A block past the range is issued with a zero weight scale: its
+    // products add +-0 to sums that are never -0 (they start at +0, and an
+    // exact zero sum rounds to +0), so they leave them unchanged, and every
+    // step runs the same straight-line code.
+    auto issue = [&](const BdStage<TN> &st, const v4i &aop, uint16_t xs, bool on, v16i &dot,
+                     v16f &sc) {
         const gh4 asc = __builtin_bit_cast(gh4, (v2u){(uint32_t)xs, 0u});
         const uint32_t w0 = st.w[0][0], w1 = st.w[0][1];
         const v4i bop = (v4i){(int)(((w0 << 4) ^ 0x80808080u) & 0xf0f0f0f0u),
                               (int)(((w1 << 4) ^ 0x80808080u) & 0xf0f0f0f0u),
                               (int)((w0 ^ 0x80808080u) & 0xf0f0f0f0u),
                               (int)((w1 ^ 0x80808080u) & 0xf0f0f0f0u)};
-        const gh4 bsc = __builtin_bit_cast(gh4, (v2u){(uint32_t)st.ws[0], 0u});
+        const gh4 bsc = __builtin_bit_cast(gh4, (v2u){on ? (uint32_t)st.ws[0] : 0u, 0u});
         v16i z = {};
         dot = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, z, 0, 0, 0);
         v16f zf = {};
@@ -1250,9 +1255,9 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[0][v] = fmaf((float)dot[v], sc[v], acc[0][v]);
     };
+    // (set 1 starts neutral: the first step's epilogue adds 0 * 0)
     v16i pdot[PIPE ? 2 : 1] = {};
     v16f psc[PIPE ? 2 : 1] = {};
-    bool pend = false;  // a block issued, its epilogue not yet run
     // a tile's partial sums added in a fixed order: wavefronts 8..W-1 hand
     // theirs to 0..W-9, then the 8 sums meet in LDS ([w][register][lane]
     // floats, so no register is repacked); wavefront w < 8 gets registers
@@ -1398,28 +1403,23 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
                     const int ckn = ck + 1 == per ? 0 : ck + 1;
                     fetch(ckn);
                     if constexpr (PIPE) {
-                        // a pending block was issued at the previous step
-                        // (set (i + 1) & 1): a valid step consumes it after
-                        // issuing its own, an invalid one (a block past the
-                        // range) just consumes it, so at a tile's end the
-                        // pending block, if any, is this step's (set i & 1)
-                        if (valid) {
-                            issue(st[i], aop, xs, pdot[i & 1], psc[i & 1]);
-                            __builtin_amdgcn_sched_barrier(0);
-                            if (pend) epi(pdot[(i + 1) & 1], psc[(i + 1) & 1]);
-                            pend = true;
-                        } else if (pend) {
-                            epi(pdot[(i + 1) & 1], psc[(i + 1) & 1]);
-                            pend = false;
-                        }
+                        // this step's block goes to set i & 1, then the
+                        // previous step's (set (i + 1) & 1, neutral at a
+                        // tile's first step) is accumulated
+                        issue(st[i], aop, xs, valid, pdot[i & 1], psc[i & 1]);
+                        __builtin_amdgcn_sched_barrier(0);
+                        epi(pdot[(i + 1) & 1], psc[(i + 1) & 1]);
                     } else {
                         if (valid) compute(st[i], aop, xs);
                     }
                     ck = ckn;
                     if (ck == 0) {
                         if constexpr (PIPE) {
-                            if (pend) epi(pdot[i & 1], psc[i & 1]);
-                            pend = false;
+                            // the tile's last block, then its set made
+                            // neutral for the next tile's first step
+                            epi(pdot[i & 1], psc[i & 1]);
+#pragma unroll
+                            for (int v = 0; v < 16; ++v) psc[i & 1][v] = 0.0f;
                         }
                         finish(cu);
                         ++cu;
