@@ -1212,8 +1212,12 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
     };
     auto compute = [&](const BdStage<TN> &st, const v4i &aop, uint16_t xs) {
         // scale product x.d * w.d in the output layout: A carries x.d at
-        // k = 0 and k = 4, B carries w.d at k = 0 only
+        // k = 0 and k = 4, B carries w.d at k = 0 only.  Every tile's
+        // products are issued before the first epilogue, so one tile's
+        // conversions run while the next tile's products are in flight.
         const gh4 asc = __builtin_bit_cast(gh4, (v2u){(uint32_t)xs, 0u});
+        v16i dot[TN];
+        v16f sc[TN];
 #pragma unroll
         for (int u = 0; u < TN; ++u) {
             // ((n ^ 8) << 4) per nibble: one shift and one three-input
@@ -1223,13 +1227,20 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
                                   (int)(((w1 << 4) ^ 0x80808080u) & 0xf0f0f0f0u),
                                   (int)((w0 ^ 0x80808080u) & 0xf0f0f0f0u),
                                   (int)((w1 ^ 0x80808080u) & 0xf0f0f0f0u)};
-            const gh4 bsc = __builtin_bit_cast(gh4, (v2u){(uint32_t)st.ws[u], 0u});
             v16i z = {};
-            const v16i dot = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, z, 0, 0, 0);
-            v16f zf = {};
-            const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(asc, bsc, zf, 0, 0, 0);
+            dot[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, z, 0, 0, 0);
+        }
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[u][v] = fmaf((float)dot[v], sc[v], acc[u][v]);
+        for (int u = 0; u < TN; ++u) {
+            const gh4 bsc = __builtin_bit_cast(gh4, (v2u){(uint32_t)st.ws[u], 0u});
+            v16f zf = {};
+            sc[u] = __builtin_amdgcn_mfma_f32_32x32x8f16(asc, bsc, zf, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < TN; ++u) {
+            __builtin_amdgcn_sched_barrier(0);  // the epilogues in issue order
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[u][v] = fmaf((float)dot[u][v], sc[u][v], acc[u][v]);
         }
     };
     // PIPE: the products of a block (issue), consumed one step later (epi).
