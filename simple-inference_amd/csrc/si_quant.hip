@@ -67,7 +67,8 @@ __device__ __forceinline__ void quantize_lds_row(const float *row_lds, int n, in
     }
 }
 
-// Block-wide double sum (256 threads = 4 wavefronts).
+// Block-wide double sum over blockDim.x / 64 wavefronts (scratch: one per
+// wavefront), added in wavefront order.
 __device__ __forceinline__ double block_sum_d(double v, double *scratch) {
     v = wave_sum_d(v);
     const int w = threadIdx.x >> 6;
@@ -122,15 +123,17 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8(const float *__restrict__ x,
 }
 
 // The same RMSNorm + Q8_0 with the row held in registers: thread t owns the
-// float4 chunks t + 256*i (i < NPT) of its workgroup's row, so 8 consecutive
+// float4 chunks t + T*i (i < NPT) of its workgroup's row, so 8 consecutive
 // threads hold one 32-value block and quantize it with quant_block_oct.  One
 // pass over global memory, no LDS staging; needs 16-byte aligned rows.
 // PARTS (with RESIDUAL): y is the split-order sum of y[sp * rows * n + ...]
 // for sp < splits (a K-split GEMM's partials), also written to y_out.
 // tq/td (optional): the Q8_0 row written operand-tiled as well
 // (q8_tiled_byte; a thread's 4 values are 4 consecutive bytes there too).
-template <bool RESIDUAL, int NPT, bool PARTS = false>
-__global__ void __launch_bounds__(256) k_rmsnorm_q8_v4(const float *__restrict__ x,
+// T threads per row: 1024 for a few long rows (each thread's serial share
+// of the quantization shrinks), 256 otherwise.
+template <bool RESIDUAL, int NPT, bool PARTS = false, int T = 256>
+__global__ void __launch_bounds__(T) k_rmsnorm_q8_v4(const float *__restrict__ x,
                                                        const float *__restrict__ y,
                                                        const float *__restrict__ gain, int n,
                                                        float eps, float *__restrict__ h_out,
@@ -141,7 +144,7 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8_v4(const float *__restrict__
                                                        float *__restrict__ y_out = nullptr,
                                                        int8_t *__restrict__ tq = nullptr,
                                                        uint16_t *__restrict__ td = nullptr) {
-    __shared__ double red[4];
+    __shared__ double red[T / 64];
     const int r = blockIdx.x, tid = threadIdx.x, n4 = n / 4;
     const size_t base = (size_t)r * n;
     float v[NPT][4];
@@ -149,12 +152,12 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8_v4(const float *__restrict__
     float4 gv[NPT];
 #pragma unroll
     for (int i = 0; i < NPT; ++i)
-        gv[i] = gain ? *(const float4 *)(gain + 4 * min(tid + 256 * i, n4 - 1))
+        gv[i] = gain ? *(const float4 *)(gain + 4 * min(tid + T * i, n4 - 1))
                      : make_float4(1.f, 1.f, 1.f, 1.f);
     double ss = 0.0;
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
-        const int c = min(tid + 256 * i, n4 - 1);  // clamped: branch-free loads
+        const int c = min(tid + T * i, n4 - 1);  // clamped: branch-free loads
         float4 a = *(const float4 *)(x + base + 4 * c);
         if (RESIDUAL) {
             float4 b = *(const float4 *)(y + base + 4 * c);
@@ -176,13 +179,13 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8_v4(const float *__restrict__
                         b.w = on ? b.w + p[k].w : b.w;
                     }
                 }
-                if (tid + 256 * i < n4) *(float4 *)(y_out + base + 4 * c) = b;
+                if (tid + T * i < n4) *(float4 *)(y_out + base + 4 * c) = b;
             }
             a = make_float4(__fadd_rn(a.x, b.x), __fadd_rn(a.y, b.y), __fadd_rn(a.z, b.z),
                             __fadd_rn(a.w, b.w));
         }
         v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
-        if (tid + 256 * i < n4) {
+        if (tid + T * i < n4) {
             if (RESIDUAL) *(float4 *)(h_out + base + 4 * c) = a;
 #pragma unroll
             for (int k = 0; k < 4; ++k) ss += (double)v[i][k] * (double)v[i][k];
@@ -193,7 +196,7 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8_v4(const float *__restrict__
     const float inv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(ms, eps)));
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
-        const int c = tid + 256 * i;
+        const int c = tid + T * i;
         if (c < n4) {  // whole 8-thread groups (n is a multiple of 32)
             const float g4[4] = {gv[i].x, gv[i].y, gv[i].z, gv[i].w};
             float o[4];
@@ -330,16 +333,24 @@ void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int ro
     const auto al = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
     const int n4 = n / 4;
     if (n4 <= 2048 && al(x) && al(y) && al(h) && al(normed) && al(gain) && al(qs)) {
-        const int npt = n4 <= 256 ? 1 : n4 <= 512 ? 2 : n4 <= 1024 ? 4 : 8;
-#define RMS_V4(RES, NPT)                                                                          \
-    SI_LAUNCH((k_rmsnorm_q8_v4<RES, NPT>), dim3(rows), dim3(256), 0, st, x, y, gain, n,           \
+        // a few long rows (batched decode): 1024 threads per row
+        const bool wide = rows <= 128 && n4 > 256;
+        const int npt = wide ? (n4 <= 1024 ? 1 : 2)
+                             : n4 <= 256 ? 1 : n4 <= 512 ? 2 : n4 <= 1024 ? 4 : 8;
+#define RMS_V4(RES, NPT, T)                                                                       \
+    SI_LAUNCH((k_rmsnorm_q8_v4<RES, NPT, false, T>), dim3(rows), dim3(T), 0, st, x, y, gain, n,   \
               eps, h, normed, qs, d, s, 1, (float *)nullptr, tq, td)
-#define RMS_V4N(RES)                     \
-    switch (npt) {                       \
-        case 1: RMS_V4(RES, 1); break;   \
-        case 2: RMS_V4(RES, 2); break;   \
-        case 4: RMS_V4(RES, 4); break;   \
-        default: RMS_V4(RES, 8); break;  \
+#define RMS_V4N(RES)                             \
+    if (wide) {                                  \
+        if (npt == 1) RMS_V4(RES, 1, 1024);      \
+        else RMS_V4(RES, 2, 1024);               \
+    } else {                                     \
+        switch (npt) {                           \
+            case 1: RMS_V4(RES, 1, 256); break;  \
+            case 2: RMS_V4(RES, 2, 256); break;  \
+            case 4: RMS_V4(RES, 4, 256); break;  \
+            default: RMS_V4(RES, 8, 256); break; \
+        }                                        \
     }
         if (y) {
             RMS_V4N(true);
