@@ -1084,25 +1084,50 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
                        : (uint32_t)(((cc >> ltile) * nb << ltile) + (cc & (tile - 1))) * 2;
         }
     };
+    // Streamed activations (one K range, b0 = 0, len = nb): the scalar
+    // offsets of block b = BD_W lk + wave advance by a constant per step.
+    // They are not clamped: a block past nb reads as zero (past the buffer)
+    // or as another panel's block, and only steps whose block is in range
+    // use their loads (the pipelined step gives the others zero scales).
+    uint32_t oa = 0, ox = 0, ow = 0, os = 0;
+    auto da_reset = [&]() {
+        const uint32_t b = (uint32_t)(b0 + wave);
+        oa = b * 1024;
+        ox = b * 64;
+        ow = b * (uint32_t)n * 16;
+        os = (b << ltile) * 2;
+    };
+    if (DA) da_reset();
     auto load = [&](BdStage<TN> &st) {
         const int iu = min(lu, nu - 1);  // past the end: a valid block again
         if (iu != lu_set) {
             set_unit(iu);
             lu_set = iu;
         }
-        const int b = b0 + min(BD_W * lk + wave, len - 1);
-        if (DA) {
-            st.a = __builtin_amdgcn_raw_buffer_load_b128(rta, vta, b * 1024, 0);
-            st.xs = __builtin_amdgcn_raw_buffer_load_b16(rtx, vtx, b * 64, 0);
-        }
+        if constexpr (DA) {
+            st.a = __builtin_amdgcn_raw_buffer_load_b128(rta, vta, oa, 0);
+            st.xs = __builtin_amdgcn_raw_buffer_load_b16(rtx, vtx, ox, 0);
 #pragma unroll
-        for (int u = 0; u < TN; ++u) {
-            st.w[u] = __builtin_amdgcn_raw_buffer_load_b64(rb, vob[u], b * n * 16, 0);
-            st.ws[u] = __builtin_amdgcn_raw_buffer_load_b16(rw, vow[u], (b << ltile) * 2, 0);
+            for (int u = 0; u < TN; ++u) {
+                st.w[u] = __builtin_amdgcn_raw_buffer_load_b64(rb, vob[u], ow, 0);
+                st.ws[u] = __builtin_amdgcn_raw_buffer_load_b16(rw, vow[u], os, 0);
+            }
+            oa += BD_W * 1024;
+            ox += BD_W * 64;
+            ow += (uint32_t)BD_W * n * 16;
+            os += (uint32_t)(BD_W << ltile) * 2;
+        } else {
+            const int b = b0 + min(BD_W * lk + wave, len - 1);
+#pragma unroll
+            for (int u = 0; u < TN; ++u) {
+                st.w[u] = __builtin_amdgcn_raw_buffer_load_b64(rb, vob[u], b * n * 16, 0);
+                st.ws[u] = __builtin_amdgcn_raw_buffer_load_b16(rw, vow[u], (b << ltile) * 2, 0);
+            }
         }
         if (++lk == per) {
             lk = 0;
             ++lu;
+            if (DA) da_reset();
         }
     };
 
@@ -1404,13 +1429,14 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
     {
         fetch(0);
         int cu = 0, ck = 0;  // the compute pointer
+        int vrem = len - wave;  // len - (BD_W ck + wave): the block is in range while > 0
         for (int it0 = 0; it0 < total; it0 += P) {
 #pragma unroll
             for (int i = 0; i < P; ++i) {
                 if (it0 + i < total) {
                     const v4i aop = DA ? st[i].a : a_nx;
                     const uint16_t xs = DA ? st[i].xs : x_nx;
-                    const bool valid = BD_W * ck + wave < len;
+                    const bool valid = vrem > 0;  // BD_W ck + wave < len
                     const int ckn = ck + 1 == per ? 0 : ck + 1;
                     fetch(ckn);
                     if constexpr (PIPE) {
@@ -1424,6 +1450,7 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
                         if (valid) compute(st[i], aop, xs);
                     }
                     ck = ckn;
+                    vrem = ck == 0 ? len - wave : vrem - BD_W;
                     if (ck == 0) {
                         if constexpr (PIPE) {
                             // the tile's last block, then its set made
