@@ -1237,45 +1237,64 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
     };
     auto compute = [&](const BdStage<TN> &st, const v4i &aop, uint16_t xs) {
         // scale product x.d * w.d in the output layout: A carries x.d at
-        // k = 0 and k = 4, B carries w.d at k = 0 only.  Every tile's
-        // products are issued before the first epilogue, so one tile's
-        // conversions run while the next tile's products are in flight.
+        // k = 0 and k = 4, B carries w.d at k = 0 only.  Streamed
+        // activations: every tile's products are issued before the first
+        // epilogue, so one tile's conversions run while the next tile's
+        // products are in flight (the staged kernel, with 4 stages of
+        // weights in registers, would spill the extra products).
         const gh4 asc = __builtin_bit_cast(gh4, (v2u){(uint32_t)xs, 0u});
-        v16i dot[TN];
-        v16f sc[TN];
-#pragma unroll
-        for (int u = 0; u < TN; ++u) {
-            // ((n ^ 8) << 4) per nibble: one shift and one three-input
-            // bitwise op for the low nibbles, one op for the high ones
+        // ((n ^ 8) << 4) per nibble: one shift and one three-input bitwise op
+        // for the low nibbles, one op for the high ones
+        auto bop_of = [&](int u) {
             const uint32_t w0 = st.w[u][0], w1 = st.w[u][1];
-            const v4i bop = (v4i){(int)(((w0 << 4) ^ 0x80808080u) & 0xf0f0f0f0u),
-                                  (int)(((w1 << 4) ^ 0x80808080u) & 0xf0f0f0f0u),
-                                  (int)((w0 ^ 0x80808080u) & 0xf0f0f0f0u),
-                                  (int)((w1 ^ 0x80808080u) & 0xf0f0f0f0u)};
-            v16i z = {};
-            dot[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, z, 0, 0, 0);
-        }
+            return (v4i){(int)(((w0 << 4) ^ 0x80808080u) & 0xf0f0f0f0u),
+                         (int)(((w1 << 4) ^ 0x80808080u) & 0xf0f0f0f0u),
+                         (int)((w0 ^ 0x80808080u) & 0xf0f0f0f0u),
+                         (int)((w1 ^ 0x80808080u) & 0xf0f0f0f0u)};
+        };
+        auto bsc_of = [&](int u) {
+            return __builtin_bit_cast(gh4, (v2u){(uint32_t)st.ws[u], 0u});
+        };
+        if constexpr (DA) {
+            v16i dot[TN];
+            v16f sc[TN];
 #pragma unroll
-        for (int u = 0; u < TN; ++u) {
-            const gh4 bsc = __builtin_bit_cast(gh4, (v2u){(uint32_t)st.ws[u], 0u});
-            v16f zf = {};
-            sc[u] = __builtin_amdgcn_mfma_f32_32x32x8f16(asc, bsc, zf, 0, 0, 0);
-        }
+            for (int u = 0; u < TN; ++u) {
+                v16i z = {};
+                dot[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop_of(u), z, 0, 0, 0);
+            }
 #pragma unroll
-        for (int u = 0; u < TN; ++u) {
-            __builtin_amdgcn_sched_barrier(0);  // the epilogues in issue order
+            for (int u = 0; u < TN; ++u) {
+                v16f zf = {};
+                sc[u] = __builtin_amdgcn_mfma_f32_32x32x8f16(asc, bsc_of(u), zf, 0, 0, 0);
+            }
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[u][v] = fmaf((float)dot[u][v], sc[u][v], acc[u][v]);
+            for (int u = 0; u < TN; ++u) {
+                __builtin_amdgcn_sched_barrier(0);  // the epilogues in issue order
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    acc[u][v] = fmaf((float)dot[u][v], sc[u][v], acc[u][v]);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < TN; ++u) {
+                v16i z = {};
+                const v16i dot = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop_of(u), z, 0, 0, 0);
+                v16f zf = {};
+                const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(asc, bsc_of(u), zf, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[u][v] = fmaf((float)dot[v], sc[v], acc[u][v]);
+            }
         }
     };
     // PIPE: the products of a block (issue), consumed one step later (epi).
-    // A block past the range is issued with a zero weight scale: its
-    // products add +-0 to sums that are never -0 (they start at +0, and an
-    // exact zero sum rounds to +0), so they leave them unchanged, and every
-    // step runs the same straight-line code.
+    // A block past the range is issued with zero scales (its loads may hold
+    // another panel's rows): its products add +0 to sums that are never -0
+    // (they start at +0, and an exact zero sum rounds to +0), so they leave
+    // them unchanged, and every step runs the same straight-line code.
     auto issue = [&](const BdStage<TN> &st, const v4i &aop, uint16_t xs, bool on, v16i &dot,
                      v16f &sc) {
-        const gh4 asc = __builtin_bit_cast(gh4, (v2u){(uint32_t)xs, 0u});
+        const gh4 asc = __builtin_bit_cast(gh4, (v2u){on ? (uint32_t)xs : 0u, 0u});
         const uint32_t w0 = st.w[0][0], w1 = st.w[0][1];
         const v4i bop = (v4i){(int)(((w0 << 4) ^ 0x80808080u) & 0xf0f0f0f0u),
                               (int)(((w1 << 4) ^ 0x80808080u) & 0xf0f0f0f0u),

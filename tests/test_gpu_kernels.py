@@ -461,6 +461,39 @@ def test_gemm_tiled_a(oracle, m, n, k, bias, res):
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "not deterministic"
 
 
+def test_gemm_tiled_a_other_panel_nonfinite(oracle):
+    """Streamed activations, 64 rows, K = 896 (28 blocks over 12 wavefronts,
+    so some steps fall past the range and read the next panel's blocks):
+    panel 1 given infinite / NaN scales must leave panel 0's rows exactly as
+    with finite ones (an out-of-range block's products carry zero scales)."""
+    torch = _torch()
+    m, n, k = 64, 128, 896
+    rng = np.random.default_rng(5)
+    w = q4(oracle, rng, n, k)
+    xq = oracle.quantize_q8(rng.standard_normal((m, k)).astype(np.float32))
+    qs, d, _ = aos_to_planar(xq)
+    wqs, wd, tile = _upload_q4(w, n, k)
+    tq = empty(2 * 32 * k, torch.int8)
+    td = empty(2 * k, torch.int16)
+    si_amd.call("si_q8_tile", si_amd.ptr(dev(qs)), si_amd.ptr(dev(d.view(np.int16))), m, k,
+                si_amd.ptr(tq), si_amd.ptr(td), None)
+
+    def gemm(tdv):
+        out = empty(m * n, torch.float32)
+        si_amd.call("si_gemm_q4q8", si_amd.ptr(wqs), si_amd.ptr(wd), tile, n, k,
+                    si_amd.ptr(tq), si_amd.ptr(tdv), m, None, None, si_amd.ptr(out), n,
+                    si_amd.SI_GEMM_TILED_A, None, 0, None)
+        return host(out).reshape(m, n)
+
+    base = gemm(td)
+    bad_td = host(td).copy()
+    half = k // 32 * 32  # panel 1's scales: [panel][block][row]
+    bad_td[half:] = np.where(np.arange(bad_td.size - half) % 2 == 0, 0x7C00, 0x7E00)  # inf, NaN
+    got = gemm(dev(bad_td))
+    assert np.isfinite(base).all()
+    assert np.array_equal(got[:32].view(np.uint32), base[:32].view(np.uint32))
+
+
 @pytest.mark.parametrize("shape,ntok,pos0", [("0.5b", 1, 1023), ("7b", 5, 0), ("7b", 3, 4093)])
 def test_rope_kv_append_bit_exact(oracle, shape, ntok, pos0):
     torch = _torch()
