@@ -19,17 +19,23 @@
 
 namespace si {
 
-// grid (ntok, qheads + kvheads), block hdim/2: one thread per rotation pair.
-// With a page table (pg.pages != nullptr) token t's K/V row goes to the
-// pool row of sequence t's position pos (kv_seq_stride unused).
-__global__ void k_rope_kv(const float *__restrict__ qkv, int ldqkv, int qheads, int kvheads,
-                          int hdim, int pos0, int pos_step, int max_pos,
-                          const int *__restrict__ ctx_dev,
-                          const float *__restrict__ rc, const float *__restrict__ rs,
-                          float *__restrict__ q_out, uint16_t *__restrict__ kc,
-                          uint16_t *__restrict__ vc, size_t kv_seq_stride, KvPages pg) {
-    const int t = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
+// grid (ntok, ceil((qheads + kvheads) * hdim/2 / 256)), block 256: one
+// thread per rotation pair (head h = j / (hdim/2), pair i = j % (hdim/2) of
+// token t), so a workgroup covers several heads of a token (half-wavefront
+// workgroups per head had left most lanes idle).  With a page table
+// (pg.pages != nullptr) token t's K/V row goes to the pool row of sequence
+// t's position pos (kv_seq_stride unused).
+constexpr int ROPE_T = 256;
+__global__ void __launch_bounds__(ROPE_T) k_rope_kv(
+    const float *__restrict__ qkv, int ldqkv, int qheads, int kvheads, int hdim, int pos0,
+    int pos_step, int max_pos, const int *__restrict__ ctx_dev, const float *__restrict__ rc,
+    const float *__restrict__ rs, float *__restrict__ q_out, uint16_t *__restrict__ kc,
+    uint16_t *__restrict__ vc, size_t kv_seq_stride, KvPages pg) {
+    const int t = blockIdx.x;
     const int half = hdim >> 1;
+    const int j = blockIdx.y * ROPE_T + threadIdx.x;
+    if (j >= (qheads + kvheads) * half) return;
+    const int h = j / half, i = j - h * half;
     const int pos = ctx_dev ? ctx_dev[t] - 1 : pos0 + t * pos_step;
     if (pos < 0 || pos >= max_pos) return;  // device-supplied contexts are not host-checked
     const float c = rc[(size_t)pos * half + i], s = rs[(size_t)pos * half + i];
@@ -58,7 +64,8 @@ void launch_rope_kv(const float *qkv, int ldqkv, int ntok, int qheads, int kvhea
                     const float *rs, float *q_out, uint16_t *kc, uint16_t *vc,
                     size_t kv_seq_stride, hipStream_t st, KvPages pg) {
     if (ntok <= 0) return;
-    SI_LAUNCH(k_rope_kv, dim3(ntok, qheads + kvheads), dim3(hdim / 2), 0, st, qkv,
+    const int pairs = (qheads + kvheads) * (hdim / 2);
+    SI_LAUNCH(k_rope_kv, dim3(ntok, (pairs + ROPE_T - 1) / ROPE_T), dim3(ROPE_T), 0, st, qkv,
               ldqkv, qheads, kvheads, hdim, pos0, pos_step, max_pos, ctx_dev, rc, rs,
               q_out, kc, vc, kv_seq_stride, pg);
 }
