@@ -50,22 +50,14 @@ METRIC = "decode layer µs + HBM GB/s; prefill tokens/s + int8 MFMA % (one GPU)"
 # traffic with "traffic_current": false.  Kernels not listed report traffic
 # null.  Summaries: profiles/cfgN_*.md.
 PMC_KIB = {
-    ("1", "k_matvec<8, 128, false>"): (330.9, 4.5, "d6d68a2a01ac"),
-    ("2", "k_dec_attn<64, 8, false, false, 1, true>"): (6540.0, 35.5, "d6d68a2a01ac"),
-    ("2", "k_dec_gateup<64, 512, false>"): (2534.9, 9.8, "d6d68a2a01ac"),
-    ("2", "k_matvec<8, 512, false>"): (1256.0, 3.5, "d6d68a2a01ac"),
-    ("2", "k_dec_wo<8, 512, false>"): (571.6, 3.5, "d6d68a2a01ac"),
-    ("3", "k_gemm_fast<2, 2, 1, 2, true>"): (6801.5, 4800.0, "d6d68a2a01ac"),
-    ("4", "k_gemm_fast<2, 2, 2, 2, true>"): (627205.6, 75905.8, "d6d68a2a01ac"),
-    ("5", "k_dec_attn_rows<128, 4, false, false>"): (266836.3, 8192.0, "d6d68a2a01ac"),
-}
-# What a traffic figure holds besides the kernel's own algorithmic bytes.
-PMC_NOTES = {
-    ("2", "k_dec_attn<64, 8, false, false, 1, true>"):
-        "FETCH_SIZE includes the W_O, gate|up and down weight lines (7.9 MB) that the kernel's "
-        "extra prefetch workgroups touch (one 4-byte load per 128-byte line) so the next "
-        "three kernels find them in the Infinity Cache; they are those kernels' bytes, "
-        "fetched early, not re-reads",
+    ("1", "k_matvec<8, 128, false>"): (330.9, 4.5, "3dbd822484b9"),
+    ("2", "k_dec_attn<64, 8, false, false, 1, true>"): (2709.0, 35.5, "3dbd822484b9"),
+    ("2", "k_dec_gateup<64, 512, false>"): (2534.9, 9.8, "3dbd822484b9"),
+    ("2", "k_dec_wo<8, 512, false>"): (571.6, 3.5, "3dbd822484b9"),
+    ("2", "k_matvec<8, 512, false>"): (1256.0, 3.5, "3dbd822484b9"),
+    ("3", "k_gemm_fast<2, 2, 1, 2, true>"): (6799.0, 4800.0, "3dbd822484b9"),
+    ("4", "k_gemm_fast<2, 2, 2, 2, true>"): (627540.9, 75935.2, "3dbd822484b9"),
+    ("5", "k_dec_attn_rows<128, 4, false, false>"): (266838.0, 8192.0, "3dbd822484b9"),
 }
 FETCH_SCALE, WRITE_SCALE = 2.000, 1.000
 _DIGEST = None
@@ -193,7 +185,6 @@ def roofline_entry(kernel, us, work, bound, cfg, launches):
     return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic,
             "traffic_src": src, "traffic_current": None if src is None else src == csrc_digest(),
-            **({"traffic_note": PMC_NOTES[(cfg, kernel)]} if (cfg, kernel) in PMC_NOTES else {}),
             "kernel": kernel, "kernel_us": round(us, 3), "launches": launches,
             ("alg_bytes_per_launch" if bound == "hbm" else "int_ops_per_launch"): int(work),
             "timing": "mean of per-dispatch HIP events (si_kernel_timing_*)"}

@@ -828,8 +828,6 @@ struct si_layer {
     void *gemm_ws = nullptr;
     size_t gemm_ws_bytes = 0;
     float *scores = nullptr;
-    // single-token decode: the fused first kernel prefetches the later weights
-    bool pf_decode = true;
     // phase timing: events[i] marks the start of phase i, events[COUNT] the end
     bool timing = false;
     hipEvent_t events[SI_PHASE_COUNT + 1] = {};
@@ -1131,20 +1129,6 @@ static int run_decode(si_layer *L, const float *x, uint16_t *kc, uint16_t *vc, i
         fq.cap_d = capt(cap, L->xq.d);
         fq.cap_s = capt(cap, L->xq.s);
         fq.cap_qkv = capt(cap, L->qkv);
-        if (full && L->pf_decode) {
-            // W_O, gate|up and down, touched by 32 extra workgroups (on the
-            // CUs the 16 x 14 grid of a 0.5B layer leaves free) while the
-            // attention runs: the next three kernels then read them from the
-            // memory-side cache instead of HBM
-            const Q4Dev *ws[3] = {&L->wo, &L->wgu, &L->wdown};
-            for (const Q4Dev *w : ws) {
-                fq.pf_ptr[fq.pf_n] = w->qs;
-                fq.pf_bytes[fq.pf_n++] = (size_t)w->n * w->k / 2;
-                fq.pf_ptr[fq.pf_n] = w->d;
-                fq.pf_bytes[fq.pf_n++] = q4_scale_count(w->n, w->k / SI_QK, w->tile) * 2;
-            }
-            fq.pf_wgs = 32;
-        }
         launch_dec_qkv_attn(fq, s.qheads, s.kvheads, s.hdim, L->rope_cos, L->rope_sin, kc, vc,
                             ctx, ns, capt(cap, L->q), L->attn_ws, st);
     } else {

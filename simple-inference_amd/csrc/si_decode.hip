@@ -445,27 +445,6 @@ struct FqLds {
 // matrix, + bias), for a small model whose 3*hdim rows a workgroup streams
 // quickly; the k_dec_qkv launch and the q|k|v round trip through memory
 // disappear, at the price of every chunk recomputing its head's rows.
-// Prefetch workgroup w of nw: one 4-byte load per 128-byte line of slice w
-// of every range (DecQkvIn::pf_*), all in flight together, so the lines pass
-// through L2 into the memory-side cache for the step's later kernels.
-__device__ void dec_prefetch(const DecQkvIn &fq, int w, int nw) {
-    uint32_t acc = 0;
-    for (int r = 0; r < fq.pf_n; ++r) {
-        const uint32_t *base = (const uint32_t *)fq.pf_ptr[r];
-        const size_t lines = fq.pf_bytes[r] / 128;
-        const size_t per = (lines + nw - 1) / nw;
-        const size_t l0 = (size_t)w * per, l1 = min(lines, l0 + per);
-        for (size_t l = l0 + threadIdx.x; l < l1; l += 8 * blockDim.x) {
-            uint32_t v[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = base[32 * min(l + (size_t)k * blockDim.x, l1 - 1)];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) acc ^= v[k];
-        }
-    }
-    if (fq.pf_sink) fq.pf_sink[(size_t)w * blockDim.x + threadIdx.x] = acc;
-}
-
 template <int D, int NW, bool FINAL, bool PAGED, int DEPTH, bool FQ = false>
 __global__ void __launch_bounds__(NW * 64) k_dec_attn(
     const float *__restrict__ qkv, int ldqkv, int qheads, int kvheads,
@@ -478,11 +457,6 @@ __global__ void __launch_bounds__(NW * 64) k_dec_attn(
     constexpr int KS = D / 32, DT = D / 16, HALF = D / 2;
     constexpr int VROW = AttnLds<D, NW>::VROW;
     constexpr int VL = DA_TILE * D / (64 * 8);  // 16-byte V pieces per lane per tile
-    if (FQ && (int)blockIdx.y >= qheads) {  // a prefetch workgroup (whole workgroup)
-        dec_prefetch(fq, (int)((blockIdx.y - qheads) * gridDim.x + blockIdx.x),
-                     (int)((gridDim.y - qheads) * gridDim.x));
-        return;
-    }
     extern __shared__ __attribute__((aligned(16))) char smem[];
     uint16_t *newk = (uint16_t *)smem;  // fp16 K and V rows of the new token
     uint16_t *newv = newk + D;
@@ -1513,9 +1487,7 @@ void launch_dec_qkv_attn(const DecQkvIn &fq, int qheads, int kvheads, int hdim, 
     float *ws_l = ws_m + (size_t)qheads * ns;
     float *ws_o = ws_l + (size_t)qheads * ns;
     const float scale = 1.0f / sqrtf((float)hdim);  // attention_kernels.h:86
-    // prefetch workgroups in whole extra rows of the grid
-    const int pf_rows = fq.pf_n ? (fq.pf_wgs + ns - 1) / ns : 0;
-    const dim3 grid(ns, qheads + pf_rows, 1);
+    const dim3 grid(ns, qheads, 1);
 #define FQCALL(DIM, DEP)                                                                       \
     SI_LAUNCH((k_dec_attn<DIM, DA_NW, false, false, DEP, true>), grid, dim3(DA_NW * 64),       \
               ((AttnLds<DIM, DA_NW>::bytes(1) + 15) / 16 * 16 +                                \

@@ -179,15 +179,6 @@ struct DecQkvIn {
     uint16_t *cap_d = nullptr;
     int16_t *cap_s = nullptr;
     float *cap_qkv = nullptr;
-    // optional: the step's later weights, touched by pf_wgs extra workgroups
-    // of the launch (one load per 128-byte line) so that the following
-    // kernels find them in the memory-side cache; the loaded words are
-    // folded and stored only through pf_sink (NULL in the layer)
-    static constexpr int PF_MAX = 6;
-    const void *pf_ptr[PF_MAX] = {};
-    size_t pf_bytes[PF_MAX] = {};
-    int pf_n = 0, pf_wgs = 0;
-    uint32_t *pf_sink = nullptr;
 };
 bool dec_qkv_attn_ok(int hidden, int qheads, int kvheads, int hdim, int ctx);
 void launch_dec_qkv_attn(const DecQkvIn &fq, int qheads, int kvheads, int hdim, const float *rc,
