@@ -877,7 +877,8 @@ struct RowsLds {
     static constexpr int NWG = 4 / G;            // wavefronts per group
     static constexpr int ROWS = DA_TILE * NWG;  // positions per step
     static constexpr int RW = G * D + 8;        // halves per LDS row (padded)
-    static constexpr size_t tile_bytes = (size_t)2 * ROWS * RW * 2;  // K and V
+    // K and V rows of a step, twice: steps alternate between the two copies
+    static constexpr size_t tile_bytes = (size_t)2 * 2 * ROWS * RW * 2;
     static constexpr size_t raw_bytes(int per) {
         return (size_t)(G * per * D + 2 * G * D + D) * 4;
     }
@@ -910,8 +911,13 @@ __global__ void __launch_bounds__(256) k_dec_attn_rows(
     uint16_t *newk = (uint16_t *)smem;  // [G*D] fp16 K row of the new token (RoPE'd)
     uint16_t *newv = newk + KVD;        // [G*D] its V row
     char *big = smem + 2 * KVD * 2;
-    _Float16 *kt = (_Float16 *)big;     // [ROWS][RW]
-    _Float16 *vt = kt + ROWS * RW;      // [ROWS][RW]
+    // [2][K, V][ROWS][RW]: even steps stage their rows in copy 0, odd steps
+    // in copy 1, so a step's staging never overwrites rows another
+    // wavefront may still be reading (one barrier per step)
+    _Float16 *kt0 = (_Float16 *)big;
+    _Float16 *vt0 = kt0 + ROWS * RW;
+    _Float16 *kt1 = vt0 + ROWS * RW;
+    _Float16 *vt1 = kt1 + ROWS * RW;
 
     const int sp = blockIdx.x, qi = blockIdx.y, ns = gridDim.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1047,7 +1053,7 @@ __global__ void __launch_bounds__(256) k_dec_attn_rows(
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[dt] = (f4){0.f, 0.f, 0.f, 0.f};
     const int nsteps = (p1 - p0 + ROWS - 1) / ROWS;  // 0 for an empty chunk
-    auto step = [&](uint4 (&rk)[PT], uint4 (&rvv)[PT], int st) {
+    auto step = [&](uint4 (&rk)[PT], uint4 (&rvv)[PT], int st, _Float16 *kt, _Float16 *vt) {
         const int ps = p0 + st * ROWS;
         const bool tail = ps + ROWS > p1;  // workgroup-uniform
         // stage the step's rows; V rows past the context as zeros (their
@@ -1141,15 +1147,18 @@ __global__ void __launch_bounds__(256) k_dec_attn_rows(
             acc = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pl, acc, 0, 0, 0);
             o[dt] = acc;
         }
-        __syncthreads();  // the step's rows are rewritten next
+        // no barrier: the next step stages the other copy, and the step
+        // after it rewrites this one only once every wavefront has passed
+        // the next step's barrier, i.e. finished reading this step's rows
     };
     // steps in pairs (workgroup-uniform); the second step of the last pair
     // of an odd count lies past the chunk, is masked out entirely and
     // leaves the softmax state as it is
     for (int st = 0; st < nsteps; st += 2) {
-        step(ak, av, st);
-        step(bk, bv, st + 1);
+        step(ak, av, st, kt0, vt0);
+        step(bk, bv, st + 1, kt1, vt1);
     }
+    __syncthreads();  // the rows' LDS is reused below
 
     if constexpr (NWG == 1 && !FINAL) {
         // one wavefront per group: its state is the chunk's partial, written
@@ -1317,6 +1326,10 @@ void launch_dec_gateup(const float *h, const float *gain, int hidden, float eps,
 // than ~1024 workgroups in total.
 constexpr int DA_NW = 8;
 
+// LDS of a whole-row workgroup (two copies of a step's K and V rows):
+// two workgroups still fit a CU's 160 KB
+constexpr size_t ROWS_LDS_MAX = 80 * 1024;
+
 // The whole-row kernel serves batches (>= 8 queries: one query is latency
 // bound and k_dec_attn's shorter chain wins) of 1, 2 or 4 KV groups of up to
 // 16 query heads.
@@ -1336,7 +1349,7 @@ static bool dec_rows_ok(int qheads, int kvheads, int hdim, int nq) {
         default: return false;
     }
 #undef RB
-    return b <= 65536;
+    return b <= ROWS_LDS_MAX;
 }
 
 // A single query over more than 128 tiles (2048 positions) takes 4
@@ -1401,10 +1414,20 @@ static void dec_attn_impl(const float *qkv, int ldqkv, int nq, int qheads, int k
     const bool fin = attn != nullptr;
     if (dec_rows_ok(qheads, kvheads, hdim, nq)) {
 #define RCALL(DIM, GG, FIN)                                                                       \
-    SI_LAUNCH((k_dec_attn_rows<DIM, GG, FIN, PAGED>), dim3(ns, nq), dim3(256),                    \
-              (RowsLds<DIM, GG>::bytes(per)), st, qkv, ldqkv, qheads, rc, rs, kc, vc,             \
-              kv_seq_stride, ctx_dev, ctx0, max_ctx, chunk, scale, q_cap, ws_m, ws_l,             \
-              ws_o, attn, aqs, ad, as, pg)
+    do {                                                                                          \
+        static bool big_lds = false;                                                              \
+        if (!big_lds) {                                                                           \
+            /* past 64 KB of dynamic LDS; a failure surfaces as the launch's error */            \
+            (void)hipFuncSetAttribute((const void *)k_dec_attn_rows<DIM, GG, FIN, PAGED>,         \
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,                 \
+                                      (int)ROWS_LDS_MAX);                                         \
+            big_lds = true;                                                                       \
+        }                                                                                         \
+        SI_LAUNCH((k_dec_attn_rows<DIM, GG, FIN, PAGED>), dim3(ns, nq), dim3(256),                \
+                  (RowsLds<DIM, GG>::bytes(per)), st, qkv, ldqkv, qheads, rc, rs, kc, vc,         \
+                  kv_seq_stride, ctx_dev, ctx0, max_ctx, chunk, scale, q_cap, ws_m, ws_l,         \
+                  ws_o, attn, aqs, ad, as, pg);                                                   \
+    } while (0)
 #define RCALLG(DIM)                                                \
     if (kvheads == 1) {                                            \
         if (fin) RCALL(DIM, 1, true); else RCALL(DIM, 1, false);   \
