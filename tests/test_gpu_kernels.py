@@ -414,7 +414,7 @@ def test_gemm_tiled_a(oracle, m, n, k, bias, res):
     one pass over K) against the float64 product of the dequantized operands
     on every row, and against the default path (planar activations) within
     fp32 summation-order differences: the streamed kernel spreads K over 12
-    wavefronts, the default over 16 and, for long K, over workgroups."""
+    (or 8) wavefronts, the default over 16 and, for long K, over workgroups."""
     torch = _torch()
     rng = np.random.default_rng(m * 7 + n + k)
     w = q4(oracle, rng, n, k)
@@ -442,7 +442,11 @@ def test_gemm_tiled_a(oracle, m, n, k, bias, res):
     outs = []
     ran = [kn for kn, _ in si_amd.kernel_times_ms(
         "k_gemm", lambda: outs.append(gemm(tq, td, si_amd.SI_GEMM_TILED_A)))]
-    assert ran == ["k_gemm_bd<1, 2, 0, 12, true, true>"], ran
+    # up to 64 rows whose 32-row halves outnumber the 256 CUs: one unit per
+    # 8-wavefront workgroup (one round); otherwise the pipelined 12
+    wide = m <= 64 and -(-n // 32) * -(-m // 32) > 256
+    assert ran == ["k_gemm_bd<1, 2, 0, 8, true, false>" if wide
+                   else "k_gemm_bd<1, 2, 0, 12, true, true>"], ran
     got = host(outs[0]).reshape(m, n)
     want = dequant_q8(xq, m, k) @ dequant_q4(w, n, k).T
     if bias:
