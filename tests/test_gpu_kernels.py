@@ -442,9 +442,9 @@ def test_gemm_tiled_a(oracle, m, n, k, bias, res):
     outs = []
     ran = [kn for kn, _ in si_amd.kernel_times_ms(
         "k_gemm", lambda: outs.append(gemm(tq, td, si_amd.SI_GEMM_TILED_A)))]
-    # up to 64 rows whose 32-row halves outnumber the 256 CUs: one unit per
-    # 8-wavefront workgroup (one round); otherwise the pipelined 12
-    wide = m <= 64 and -(-n // 32) * -(-m // 32) > 256
+    # more 32-row halves than the 256 CUs: one unit per 8-wavefront
+    # workgroup, two per CU; otherwise the pipelined 12
+    wide = -(-n // 32) * -(-m // 32) > 256
     assert ran == ["k_gemm_bd<1, 2, 0, 8, true, false>" if wide
                    else "k_gemm_bd<1, 2, 0, 12, true, true>"], ran
     got = host(outs[0]).reshape(m, n)
