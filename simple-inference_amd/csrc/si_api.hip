@@ -816,6 +816,12 @@ struct si_layer {
     bool ffn = false;
     DevArena mem;  // weights
     Q4Dev wqkv, wo, wgu, wdown;
+    // prefill of more than 64 rows: Q|K|V with its output rows in
+    // rope_perm_row order (and its bias), for the projection that applies
+    // RoPE and appends K/V in its epilogue
+    Q4Dev wqkv_rope;
+    float *bqkv_rope = nullptr;
+    bool has_rope = false;
     float *norm = nullptr, *bqkv = nullptr, *post_norm = nullptr;
     std::shared_ptr<Workspace> ws;
     // views of the workspace buffers
@@ -915,6 +921,25 @@ static int build_layer(const si_layer_host_t *w, std::shared_ptr<Workspace> W,
         if (w->bk) memcpy(b.data() + QD, w->bk, KVD * sizeof(float));
         if (w->bv) memcpy(b.data() + QD + KVD, w->bv, KVD * sizeof(float));
         TRY(upload_f32(L->mem, &L->bqkv, b.data(), NQKV));
+        if (L->max_tokens > 64 && s->hdim % 2 == 0) {
+            std::vector<float> bp(NQKV);
+            for (int pr = 0; pr < NQKV; ++pr) bp[pr] = b[rope_perm_row(pr, s->hdim)];
+            TRY(upload_f32(L->mem, &L->bqkv_rope, bp.data(), NQKV));
+        }
+    }
+    if (L->max_tokens > 64 && s->hdim % 2 == 0) {
+        // the Q|K|V rows regathered in rope_perm_row order (row-major Q4_0)
+        const size_t rb = (size_t)(H / SI_QK) * 18;
+        std::vector<uint8_t> perm((size_t)NQKV * rb);
+        for (int pr = 0; pr < NQKV; ++pr) {
+            const int o = rope_perm_row(pr, s->hdim);
+            const uint8_t *src = o < QD         ? w->wq + (size_t)o * rb
+                                 : o < QD + KVD ? w->wk + (size_t)(o - QD) * rb
+                                                : w->wv + (size_t)(o - QD - KVD) * rb;
+            memcpy(perm.data() + (size_t)pr * rb, src, rb);
+        }
+        TRY(upload_q4(L->mem, &L->wqkv_rope, {perm.data()}, {NQKV}, H, gemv_tile_for(NQKV)));
+        L->has_rope = true;
     }
     L->rope_cos = W->rope_cos;
     L->rope_sin = W->rope_sin;
@@ -1213,7 +1238,19 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
     // partials and their reduce disappear (0.5B, 512 rows: 21.0 -> 16.6 us),
     // while Q|K|V gains little (10.1 -> 10.0 us) and its changed sum order
     // would move the fp16 K/V rows the later rows attend to
-    if (tl_x && gemm_streams(rows, NQKV, H))
+    // a prefill of 65-512 rows: RoPE and the K/V append in the projection's
+    // epilogue (the rope_kv phase is then empty)
+    bool roped = false;
+    if (ctx_step == 1 && !ctx_dev && !pg.pages && !ex && L->has_rope) {
+        const RopeOut ro{L->rope_cos, L->rope_sin, L->q, kc, vc, kv_seq_stride,
+                         pos0, max_ctx, s.hdim, QD, s.kvheads * s.hdim};
+        roped = launch_gemm_qkv_rope(L->wqkv_rope.qs, L->wqkv_rope.d, L->wqkv_rope.tile, NQKV,
+                                     H, L->xq.qs, L->xq.d, rows, L->bqkv_rope, capt(cap, L->qkv),
+                                     ro, st);
+    }
+    if (roped)
+        ;
+    else if (tl_x && gemm_streams(rows, NQKV, H))
         launch_gemm_q4q8_tiled(L->wqkv.qs, L->wqkv.d, L->wqkv.tile, NQKV, H, L->xq.tq, L->xq.td,
                                rows, L->bqkv, nullptr, L->qkv, NQKV, st);
     else
@@ -1242,8 +1279,10 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
     } else {
         mark(L, SI_PHASE_ROPE_KV, st);
         // :260-266: RoPE at the token's position, fp16 K/V append
-        launch_rope_kv(L->qkv, NQKV, rows, s.qheads, s.kvheads, s.hdim, pos0, pos_step, max_ctx,
-                       ctx_dev, L->rope_cos, L->rope_sin, L->q, kc, vc, kv_seq_stride, st);
+        if (!roped)
+            launch_rope_kv(L->qkv, NQKV, rows, s.qheads, s.kvheads, s.hdim, pos0, pos_step,
+                           max_ctx, ctx_dev, L->rope_cos, L->rope_sin, L->q, kc, vc,
+                           kv_seq_stride, st);
         // :268-272: attention over the fp16 cache -> Q8
         mark(L, SI_PHASE_ATTENTION_Q8, st);
         if (ctx_dev == nullptr && attn_prefill_supported(s.qheads, s.kvheads, s.hdim))

@@ -217,6 +217,7 @@ struct GateUpOut {
     uint16_t *td;   // with tq: its scales (q8_tiled_d)
 };
 
+
 // Register staging of one LDS stage of k_gemm_fast.  Each thread's byte
 // offsets inside a stage are fixed (rows clamped once); a stage moves the
 // buffer bases, scalar work, so a stage costs no per-load VALU address math.
@@ -1027,8 +1028,9 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
     const uint8_t *__restrict__ wqs, const uint16_t *__restrict__ wd, int tile, int n, int nb,
     const int8_t *__restrict__ xqs, const uint16_t *__restrict__ xd, int m,
     const float *__restrict__ bias, const float *__restrict__ residual, float *__restrict__ out,
-    int ldo, float *__restrict__ part, int H, int C, int S, int cb, int units, GateUpOut go) {
-    static_assert(MODE == 0 ? TN == 1 : TN == 2, "MODE 0 takes one tile, gate|up two");
+    int ldo, float *__restrict__ part, int H, int C, int S, int cb, int units, GateUpOut go,
+    RopeOut ro) {
+    static_assert(MODE == 1 ? TN == 2 : TN == 1, "MODE 0 and 2 take one tile, gate|up two");
     static_assert(BD_W >= 8 && BD_W <= 16 && BD_W % 4 == 0, "8, 12 or 16 wavefronts");
     static_assert(!PIPE || (TN == 1 && P % 2 == 0), "pipelined: one tile, an even unroll");
     constexpr int BD_T = 64 * BD_W;                              // threads
@@ -1422,6 +1424,35 @@ __global__ void __launch_bounds__(64 * BD_W) k_gemm_bd(
             const int row = m0 + 8 * (wave >> 1) + 4 * g + 2 * (wave & 1) + i;
             if (MODE == 1) {
                 gateup_out(row, col0(iu, 0) + j, r[0][i], r[TN - 1][i]);
+            } else if (MODE == 2) {
+                // permuted column pc: head pc / hdim, element e = (pc % hdim)
+                // / 2 of its first (even pc) or second half; the pair's other
+                // value is the neighbouring lane's (j ^ 1, same rows)
+                const int pc = col0(iu, 0) + j;
+                const float y = r[0][i] + (bias ? bias[pc] : 0.0f);
+                const float yo = dpp_f<DPP_XOR1>(y);
+                const int half = ro.hdim >> 1, within = pc % ro.hdim, side = within & 1;
+                const int e = within >> 1, col = pc - within + e + side * half;
+                if (row < m) {
+                    if (out) out[(size_t)row * ldo + col] = y;
+                    const int pos = ro.pos0 + row;
+                    if (pos < ro.max_pos) {
+                        // qwen_one_layer.c:172-183 as k_rope_kv: (a, b) ->
+                        // (a c - b s, b c + a s)
+                        const float a = side ? yo : y, b = side ? y : yo;
+                        const float cs = ro.rc[(size_t)pos * half + e];
+                        const float sn = ro.rs[(size_t)pos * half + e];
+                        const float x = side ? __fadd_rn(__fmul_rn(b, cs), __fmul_rn(a, sn))
+                                             : __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn));
+                        const size_t kvrow = (size_t)row * ro.kv_seq_stride + (size_t)pos * ro.kvd;
+                        if (col < ro.qd)
+                            ro.q_out[(size_t)row * ro.qd + col] = x;
+                        else if (col < ro.qd + ro.kvd)
+                            ro.kc[kvrow + (col - ro.qd)] = f2h(x);
+                        else
+                            ro.vc[kvrow + (col - ro.qd - ro.kvd)] = f2h(y);
+                    }
+                }
             } else {
                 const int col = col0(iu, 0) + j;
                 if (row < m && col < n) {
@@ -1718,7 +1749,7 @@ size_t gemm_gateup_workspace_bytes(int m, int f, int k) {
 static void launch_bd(const BdPlan &p, int mode, const uint8_t *wqs, const uint16_t *wd,
                       int tile, int n, int nb, const int8_t *xqs, const uint16_t *xd, int m,
                       const float *bias, const float *residual, float *out, int ldo, float *part,
-                      const GateUpOut &go, hipStream_t st) {
+                      const GateUpOut &go, hipStream_t st, const RopeOut &ro = RopeOut{}) {
 #define BD(TN, P, MODE, W, DA, PIPE)                                                           \
     do {                                                                                       \
         static bool big_lds = false;                                                           \
@@ -1730,7 +1761,7 @@ static void launch_bd(const BdPlan &p, int mode, const uint8_t *wqs, const uint1
         }                                                                                      \
         SI_LAUNCH((k_gemm_bd<TN, P, MODE, W, DA, PIPE>), dim3(p.grid), dim3(64 * W), p.lds,   \
                   st, wqs, wd, tile, n, nb, xqs, xd, m, bias, residual, out, ldo, part, p.H,   \
-                  p.C, p.S, p.cb, p.units, go);                                                \
+                  p.C, p.S, p.cb, p.units, go, ro);                                            \
     } while (0)
     // gate|up: 12 wavefronts (3 per SIMD; 4 weight blocks in flight fit
     // their registers); one tile: 16 (4 per SIMD, 7 of 112 blocks each, 4
@@ -1742,7 +1773,10 @@ static void launch_bd(const BdPlan &p, int mode, const uint8_t *wqs, const uint1
     // wavefronts and 3-12 stages took as long or longer).  Streamed gate|up:
     // 12 wavefronts, 2 stages (7B x 64 rows, cold weights: 41.3 us; 3-6
     // stages 41.6-44.9, 16 wavefronts 42.9; staged 43.7)
-    if (mode == 1) {
+    if (mode == 2) {
+        // Q|K|V + RoPE: the staged one-tile kernel (same sums as mode 0)
+        BD(1, 4, 2, 16, false, false);
+    } else if (mode == 1) {
         if (p.da)
             BD(2, 2, 1, BD_GU_W, true, false);
         else
@@ -1812,6 +1846,19 @@ bool gemm_streams(int m, int n, int k) {
     // a slot's serial work with one K range, as bd_takes bounds it
     const BdPlan p = bd_plan(m, n, nb, 0, true);
     return (p.units + p.S - 1) / p.S * nb <= 1024;
+}
+
+bool launch_gemm_qkv_rope(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
+                          const int8_t *xqs, const uint16_t *xd, int m, const float *bias_perm,
+                          float *out, const RopeOut &ro, hipStream_t st) {
+    const int nb = k / SI_QK;
+    if (m <= BD_SMALL_M || m > BD_MAX_M || n % 32 || ro.hdim % 2 || !bd_takes(m, n, nb))
+        return false;
+    const BdPlan p = bd_plan(m, n, nb, 2);
+    if (p.C != 1) return false;  // no K-split partials in this epilogue
+    launch_bd(p, 2, wqs, wd, tile, n, nb, xqs, xd, m, bias_perm, nullptr, out, n, nullptr,
+              GateUpOut{}, st, ro);
+    return true;
 }
 
 static int gemm_core(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,

@@ -124,6 +124,35 @@ struct KvPages {
                      : at<false>(seq, pos, kv_seq_stride, kvd);
     }
 };
+// k_gemm_bd MODE 2 (the fused Q|K|V projection of a prefill) over weights
+// whose output rows are permuted per head as [e, hdim/2 + e] for e = 0 ..
+// hdim/2 - 1 (rope_perm_row), so a rotation pair sits in two neighbouring
+// lanes of one tile: RoPE of q and k at token t's position pos0 + t, q to
+// q_out, k and v as fp16 into the caches at row t * kv_seq_stride + pos *
+// kvd (contiguous layout); out (optional) gets the unrotated q|k|v in the
+// original column order
+struct RopeOut {
+    const float *rc, *rs;  // [pos][hdim / 2] cos, sin
+    float *q_out;          // [m][qd]
+    uint16_t *kc, *vc;
+    size_t kv_seq_stride;
+    int pos0, max_pos, hdim, qd, kvd;
+};
+// The prefill Q|K|V projection + bias with the RoPE and the K/V append in
+// its epilogue (k_gemm_bd MODE 2, LDS-staged activations), over weights and
+// bias whose output rows are in rope_perm_row order: false (nothing
+// launched) unless the staged one-tile kernel runs the shape in one K range
+// (more than 64 and up to 512 rows); the caller then projects and runs
+// k_rope_kv.
+bool launch_gemm_qkv_rope(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
+                          const int8_t *xqs, const uint16_t *xd, int m, const float *bias_perm,
+                          float *out, const RopeOut &ro, hipStream_t st);
+// Original output row of row pr of the RoPE-permuted Q|K|V weights: per head
+// of hdim rows, [e, hdim/2 + e] for e = 0 .. hdim/2 - 1.
+inline int rope_perm_row(int pr, int hdim) {
+    const int head = pr / hdim, within = pr % hdim;
+    return head * hdim + (within >> 1) + (within & 1) * (hdim >> 1);
+}
 void launch_rope_kv(const float *qkv, int ldqkv, int ntok, int qheads, int kvheads, int hdim,
                     int pos0, int pos_step, int max_pos, const int *ctx_dev, const float *rc,
                     const float *rs, float *q_out, uint16_t *kc, uint16_t *vc,

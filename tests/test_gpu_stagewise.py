@@ -132,7 +132,8 @@ def _stagewise(oracle, L, lay, s, os_, x, rows, kc_host, vc_host, positions, ctx
 
 
 @pytest.mark.parametrize("shape,ntok,prefix", [
-    ("0.5b", 200, 30),    # ragged last tile, cached prefix
+    ("0.5b", 200, 30),    # ragged last tile, cached prefix; RoPE in the Q|K|V epilogue
+    ("7b", 100, 7),       # the same fused epilogue at hdim 128
     ("7b", 2048, 0),      # BASELINE config 4 as the bench times it (default flags)
 ])
 def test_prefill_stagewise(shape, ntok, prefix):
