@@ -652,6 +652,14 @@ struct Q4Dev {
     int n = 0, k = 0, tile = 8;
 };
 
+// A Q4 matrix for the fp6 GEMM formulation (prefill of more than 512 rows):
+// w [nb][n][24] fp6 codes of (nibble - 8) / 2, d [nb][n] fp16 scales, logical
+// row order (gate|up interleaved as the fused pass reads it)
+struct Q6Dev {
+    uint8_t *w = nullptr;
+    uint16_t *d = nullptr;
+};
+
 struct Q8Buf {
     int8_t *qs = nullptr;
     uint16_t *d = nullptr;
@@ -705,6 +713,7 @@ struct Workspace {
     void *gemm_ws = nullptr;  // split-K partial sums of the matrix-core GEMMs
     size_t gemm_ws_bytes = 0;
     float *scores = nullptr;  // [qheads][max_pos]: the standard attention mode
+    uint8_t *x6 = nullptr;    // past 512 rows: a GEMM input as fp6 hi/lo codes
 };
 
 struct si_workspace {
@@ -792,6 +801,8 @@ static int make_workspace(const si_shape_t *s, int max_tokens, int max_pos,
     TRY(m.alloc(&ws, W->attn_ws_bytes));
     W->attn_ws = ws;
     TRY(m.alloc(&W->scores, (size_t)s->qheads * max_pos));
+    if (max_tokens > 512)
+        TRY(m.alloc(&W->x6, M * (size_t)(std::max(std::max(H, QD), F) / 32) * 48));
     // GEMM split-K partials: the largest need over the layer's projections
     // and every row count up to max_tokens (the split depends on both)
     {
@@ -822,6 +833,10 @@ struct si_layer {
     Q4Dev wqkv_rope;
     float *bqkv_rope = nullptr;
     bool has_rope = false;
+    // prefill of more than 512 rows: the four matrices for the fp6 GEMMs
+    Q6Dev wqkv6, wo6, wgu6, wdown6;
+    bool has_f6 = false;
+    uint8_t *x6 = nullptr;
     float *norm = nullptr, *bqkv = nullptr, *post_norm = nullptr;
     std::shared_ptr<Workspace> ws;
     // views of the workspace buffers
@@ -878,6 +893,17 @@ static int upload_q4(DevArena &mem, Q4Dev *w, const std::vector<const uint8_t *>
     hipError_t e = hipDeviceSynchronize();
     (void)hipFree(tmp);
     if (e != hipSuccess) return fail(SI_ERR_HIP, "repack: %s", hipGetErrorString(e));
+    return SI_OK;
+}
+
+// The fp6 copy of a repacked Q4 matrix (gu_f > 0: the gate|up pair of gu_f
+// features, stored in the fused pass's row order).
+static int make_q6(DevArena &mem, const Q4Dev &q, int gu_f, Q6Dev *o) {
+    const size_t cnt = (size_t)q.n * (q.k / 32);
+    TRY(mem.alloc(&o->w, cnt * 24));
+    TRY(mem.alloc(&o->d, cnt));
+    launch_q4_to_w6(q.qs, q.d, q.n, q.k / 32, q.tile, gu_f, o->w, o->d, 0);
+    HIP_TRY(hipDeviceSynchronize());
     return SI_OK;
 }
 
@@ -940,6 +966,16 @@ static int build_layer(const si_layer_host_t *w, std::shared_ptr<Workspace> W,
         }
         TRY(upload_q4(L->mem, &L->wqkv_rope, {perm.data()}, {NQKV}, H, gemv_tile_for(NQKV)));
         L->has_rope = true;
+    }
+    if (L->max_tokens > 512 && W->x6) {
+        TRY(make_q6(L->mem, L->wqkv, 0, &L->wqkv6));
+        TRY(make_q6(L->mem, L->wo, 0, &L->wo6));
+        if (ffn) {
+            TRY(make_q6(L->mem, L->wgu, F, &L->wgu6));
+            TRY(make_q6(L->mem, L->wdown, 0, &L->wdown6));
+        }
+        L->x6 = W->x6;
+        L->has_f6 = true;
     }
     L->rope_cos = W->rope_cos;
     L->rope_sin = W->rope_sin;
@@ -1248,9 +1284,17 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
                                      H, L->xq.qs, L->xq.d, rows, L->bqkv_rope, capt(cap, L->qkv),
                                      ro, st);
     }
+    // past 512 rows the four GEMMs run in the fp6 formulation, each input
+    // first converted to fp6 hi/lo codes
+    const bool f6 = L->has_f6 && rows > 512 && !ex;
     if (roped)
         ;
-    else if (tl_x && gemm_streams(rows, NQKV, H))
+    else if (f6) {
+        launch_q8_to_x6(L->xq.qs, rows, H / SI_QK, L->x6, st);
+        launch_gemm_f6(L->wqkv6.w, L->wqkv6.d, NQKV, H, L->x6, L->xq.d, rows, L->bqkv, nullptr,
+                       L->qkv, NQKV, L->gemm_ws, L->gemm_ws_bytes, false, 0, nullptr, nullptr,
+                       nullptr, nullptr, st);
+    } else if (tl_x && gemm_streams(rows, NQKV, H))
         launch_gemm_q4q8_tiled(L->wqkv.qs, L->wqkv.d, L->wqkv.tile, NQKV, H, L->xq.tq, L->xq.td,
                                rows, L->bqkv, nullptr, L->qkv, NQKV, st);
     else
@@ -1307,7 +1351,13 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
     if (tl_att && gemm_streams(rows, L->wo.n, L->wo.k))
         launch_gemm_q4q8_tiled(L->wo.qs, L->wo.d, L->wo.tile, L->wo.n, L->wo.k, L->attq.tq,
                                L->attq.td, rows, nullptr, nullptr, L->attn_out, L->wo.n, st);
-    else
+    else if (f6) {
+        launch_q8_to_x6(L->attq.qs, rows, QD / SI_QK, L->x6, st);
+        osplits = launch_gemm_f6(L->wo6.w, L->wo6.d, L->wo.n, L->wo.k, L->x6, L->attq.d, rows,
+                                 nullptr, nullptr, L->attn_out, L->wo.n, L->gemm_ws,
+                                 L->gemm_ws_bytes, true, 0, nullptr, nullptr, nullptr, nullptr,
+                                 st);
+    } else
         osplits = launch_gemm_q4q8_parts(L->wo.qs, L->wo.d, L->wo.tile, L->wo.n, L->wo.k,
                                          L->attq.qs, L->attq.d, rows, L->attn_out, ex,
                                          L->gemm_ws, L->gemm_ws_bytes, st);
@@ -1335,18 +1385,33 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
         // SwiGLU -> Q8 in the gate|up GEMM's epilogue (the swiglu_q8 phase
         // is then empty); gu is written only as a capture or where it is the
         // intermediate (exact mode)
-        launch_gemm_gateup_q8(L->wgu.qs, L->wgu.d, L->wgu.tile, s.ffn, H, L->xq2.qs, L->xq2.d,
-                              rows, capt(cap || ex, L->gu), capt(cap, L->act), L->actq.qs,
-                              L->actq.d, L->actq.s, ex, L->gemm_ws, L->gemm_ws_bytes, st, false,
-                              tiled ? L->actq.tq : nullptr, tiled ? L->actq.td : nullptr,
-                              tl_x ? L->xq2.tq : nullptr, tl_x ? L->xq2.td : nullptr);
+        bool fused6 = false;
+        if (f6) {
+            launch_q8_to_x6(L->xq2.qs, rows, H / SI_QK, L->x6, st);
+            fused6 = launch_gemm_f6(L->wgu6.w, L->wgu6.d, 2 * s.ffn, H, L->x6, L->xq2.d, rows,
+                                    nullptr, nullptr, capt(cap, L->gu), 2 * s.ffn, nullptr, 0,
+                                    false, s.ffn, capt(cap, L->act), L->actq.qs, L->actq.d,
+                                    L->actq.s, st) >= 0;
+        }
+        if (!fused6)
+            launch_gemm_gateup_q8(L->wgu.qs, L->wgu.d, L->wgu.tile, s.ffn, H, L->xq2.qs,
+                                  L->xq2.d, rows, capt(cap || ex, L->gu), capt(cap, L->act),
+                                  L->actq.qs, L->actq.d, L->actq.s, ex, L->gemm_ws,
+                                  L->gemm_ws_bytes, st, false, tiled ? L->actq.tq : nullptr,
+                                  tiled ? L->actq.td : nullptr, tl_x ? L->xq2.tq : nullptr,
+                                  tl_x ? L->xq2.td : nullptr);
         mark(L, SI_PHASE_SWIGLU_Q8, st);
     }
     mark(L, SI_PHASE_DOWN, st);
     if (tiled)
         launch_gemm_q4q8_tiled(L->wdown.qs, L->wdown.d, L->wdown.tile, H, s.ffn, L->actq.tq,
                                L->actq.td, rows, nullptr, L->h, out, H, st);
-    else
+    else if (f6) {
+        launch_q8_to_x6(L->actq.qs, rows, s.ffn / SI_QK, L->x6, st);
+        launch_gemm_f6(L->wdown6.w, L->wdown6.d, H, s.ffn, L->x6, L->actq.d, rows, nullptr, L->h,
+                       out, H, L->gemm_ws, L->gemm_ws_bytes, false, 0, nullptr, nullptr, nullptr,
+                       nullptr, st);
+    } else
         project(L, L->wdown, rows, L->actq, nullptr, L->h, out, flags, st);
     mark(L, SI_PHASE_COUNT, st);
     return check_launch("layer");

@@ -181,6 +181,8 @@ typedef unsigned v2u __attribute__((ext_vector_type(2)));
 
 constexpr int G_KB = 2;   // K blocks per LDS stage (deeper stages cost occupancy)
 constexpr int G_ST = 48;  // LDS bytes per (row, block): 32 data + 16 padding
+constexpr int F6_BYTES = 24;  // 32 six-bit codes
+typedef int v8i __attribute__((ext_vector_type(8)));
 
 template <int WM, int WN, int TM, int TN>
 struct GemmCfg {
@@ -340,6 +342,117 @@ struct GemmStage {
 // up), read in gate_up_row order; the epilogue writes the gate|up outputs in
 // physical order to out (optional) and SwiGLU + Q8_0 (k_swiglu_q8's rules)
 // to go.  Needs TN == 2 and one K split.
+// Epilogue of the fast-path tile kernels for a wavefront's TM x TN tiles of
+// 32 x 32 sums acc, each scaled by os on the way out (exact: a power of two).
+// FUSE: gate|up SwiGLU + Q8_0 through the wavefront's 32 x GEMM_EPI_FT floats
+// at tl_base (free LDS, after the last barrier); otherwise bias + residual into
+// out, or the K split's partials into part.
+constexpr int GEMM_EPI_FT = 36;  // floats per LDS row of the transposition (16-byte aligned)
+template <int WM, int WN, int TM, int TN, bool FUSE>
+__device__ __forceinline__ void gemm_tile_epilogue(
+    const float (&acc)[TM][TN][16], float os, float *tl_base, int m, int n, int m0, int n0,
+    const float *__restrict__ bias, const float *__restrict__ residual, float *__restrict__ out,
+    int ldo, float *__restrict__ part, const GateUpOut &go) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int j = lane & 31, g = lane >> 5;
+    // output (i, j) of a 32x32 tile: lane j + 32*((i/4)%2), register (i%4) + 4*(i/8)
+    if (FUSE) {
+        const int f = go.f;
+        const int fb = (n0 + wn * 64) / 2;  // the wavefront's 32 features: one Q8 block
+        const bool fok = fb < f;            // the block is all in or all out
+        // SwiGLU exactly as k_swiglu_q8 per output; then each row's block is
+        // read back row-wise from this wavefront's LDS area, lanes l and
+        // l ^ 32 holding features 0..15 and 16..31 of row l & 31, and
+        // quantized with the same rules (quant_block_pair16): one scale
+        // division per block instead of one per output, no half-wave
+        // reductions per register, 16-byte stores
+        constexpr int FT = GEMM_EPI_FT;
+        float *tl = tl_base + wave * (32 * FT);
+        const int rr = lane & 31, hh = lane >> 5;
+#pragma unroll
+        for (int a = 0; a < TM; ++a) {
+            const int r0 = m0 + (wm * TM + a) * 32;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int i = 8 * (v >> 2) + 4 * g + (v & 3);
+                const float gv = acc[a][0][v] * os, uv = acc[a][TN - 1][v] * os;
+                const float silu = __fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)));
+                tl[i * FT + j] = __fmul_rn(silu, uv);
+                if (out && r0 + i < m && fok) {
+                    out[(size_t)(r0 + i) * ldo + fb + j] = gv;
+                    out[(size_t)(r0 + i) * ldo + f + fb + j] = uv;
+                }
+            }
+            // the wavefront's own area: its LDS accesses complete in order
+            __builtin_amdgcn_wave_barrier();
+            float x[16];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float4 p = *(const float4 *)(tl + rr * FT + 16 * hh + 4 * t);
+                x[4 * t] = p.x;
+                x[4 * t + 1] = p.y;
+                x[4 * t + 2] = p.z;
+                x[4 * t + 3] = p.w;
+            }
+            __builtin_amdgcn_wave_barrier();  // the next tile rewrites the area
+            int q[16];
+            uint16_t dbits;
+            int bsum;
+            quant_block_pair16(x, q, dbits, bsum);
+            const int row = r0 + rr;
+            if (row < m && fok) {
+                const size_t o = (size_t)row * f + fb + 16 * hh;
+                if (go.act)
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        *(float4 *)(go.act + o + 4 * t) =
+                            make_float4(x[4 * t], x[4 * t + 1], x[4 * t + 2], x[4 * t + 3]);
+                uint32_t pk[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    pk[t] = (uint32_t)(q[4 * t] & 0xff) | (uint32_t)(q[4 * t + 1] & 0xff) << 8 |
+                            (uint32_t)(q[4 * t + 2] & 0xff) << 16 | (uint32_t)q[4 * t + 3] << 24;
+                *(uint4 *)(go.qs + o) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+                if (hh == 0) {
+                    go.d[o / SI_QK] = dbits;
+                    if (go.s) go.s[o / SI_QK] = (int16_t)bsum;
+                }
+                if (go.tq) {
+                    // bytes 16hh..16hh+7 and +8..+15 of the row's block: the
+                    // first 8 of halves 0 and 1 at position 8hh
+                    const size_t pb = (size_t)(row >> 5) * (f / SI_QK) + fb / SI_QK;
+                    int8_t *tb = go.tq + q8_tiled_byte(pb, row & 31, 16 * hh);
+                    *(uint2 *)tb = make_uint2(pk[0], pk[1]);
+                    *(uint2 *)(tb + 512) = make_uint2(pk[2], pk[3]);
+                    if (hh == 0) go.td[pb * 32 + (row & 31)] = dbits;
+                }
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const int col = n0 + (wn * TN + b) * 32 + j;
+            if (col >= n) continue;
+            const float bv = (part == nullptr && bias) ? bias[col] : 0.0f;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int row = m0 + (wm * TM + a) * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
+                if (row >= m) continue;
+                if (part) {
+                    part[((size_t)blockIdx.z * m + row) * n + col] = acc[a][b][v] * os;
+                } else {
+                    float y = acc[a][b][v] * os + bv;
+                    if (residual) y = __fadd_rn(residual[(size_t)row * ldo + col], y);
+                    out[(size_t)row * ldo + col] = y;
+                }
+            }
+        }
+}
+
 template <int WM, int WN, int TM, int TN, bool FUSE>
 __global__ void __launch_bounds__(256) k_gemm_fast(
     const uint8_t *__restrict__ wqs, const uint16_t *__restrict__ wd, int tile, int n, int nb,
@@ -430,102 +543,226 @@ __global__ void __launch_bounds__(256) k_gemm_fast(
         __syncthreads();  // the stage's LDS is rewritten next
     }
 
-    // output (i, j) of a 32x32 tile: lane j + 32*((i/4)%2), register (i%4) + 4*(i/8)
-    if (FUSE) {
-        const int f = go.f;
-        const int fb = (n0 + wn * 64) / 2;  // the wavefront's 32 features: one Q8 block
-        const bool fok = fb < f;            // the block is all in or all out
-        // SwiGLU exactly as k_swiglu_q8 per output; then each row's block is
-        // read back row-wise from this wavefront's LDS area, lanes l and
-        // l ^ 32 holding features 0..15 and 16..31 of row l & 31, and
-        // quantized with the same rules (quant_block_pair16): one scale
-        // division per block instead of one per output, no half-wave
-        // reductions per register, 16-byte stores
-        constexpr int FT = 36;  // floats per LDS row (16-byte aligned rows)
-        static_assert(4 * 32 * FT * 4 <= C::lds_bytes(), "the transposition fits the stage LDS");
-        float *tl = (float *)gsm + wave * (32 * FT);
-        const int rr = lane & 31, hh = lane >> 5;
+    static_assert(4 * 32 * GEMM_EPI_FT * 4 <= C::lds_bytes(), "the transposition fits the stage LDS");
+    gemm_tile_epilogue<WM, WN, TM, TN, FUSE>(acc, 0.0625f, (float *)gsm, m, n, m0, n0, bias,
+                                             residual, out, ldo, part, go);
+}
+
+// ===========================================================================
+// Fast path, fp6 formulation (k_gemm_f6): the same sums as k_gemm_fast bit for
+// bit, with one VALU operation per output and block instead of two.
+//
+// The weights are w6 + d6 [nb][n] (launch_q4_to_w6: fp6 e2m3 codes of
+// (nibble - 8) / 2, logical row order, gate|up included) and each Q8
+// activation x6 (launch_q8_to_x6: q = 16 hi + lo, hi = q >> 4 in -8..7,
+// lo = q & 15, codes of hi / 2 and lo / 2).  A row's 32 codes are 24 bytes,
+// kept as a 16-byte and an 8-byte part: a region of R rows (w6: one block,
+// n rows; x6: one block's hi or lo codes, m rows) is [R][16] then [R][8],
+// w6 [nb] regions, x6 [nb][2].  One
+// v_mfma_scale_f32_32x32x64_f8f6f4 takes a block's 32 hi codes in k 0..31
+// (lanes 0..31, block scale 2^5) and its 32 lo codes in k 32..63 (lanes
+// 32..63, scale 2^1) against the weight codes twice (scale 2^1): every
+// product is an integer of magnitude <= 1016 and every partial sum (<= 32512)
+// is exact in fp32, so the block dot arrives exactly, as a float, and the
+// epilogue is k_gemm_fast's fma without the conversion; the nibble unpack is
+// gone too.  The matrix instruction issues at the i8 one's rate (~36 cycles
+// per 32 x 32 x 64, measured on MI355X).
+//
+// Staging: a stage (G_KB blocks) is copied global -> LDS by buffer loads
+// that write LDS directly (no staging registers), into two static buffers
+// used in turn; the copy of stage s + 1 is issued right after the barrier
+// that opens stage s and waited for (vmcnt(0)) before the next barrier, so it
+// overlaps a whole stage of matrix work, with one barrier per stage.  The
+// grid runs M tiles fastest (workgroups sharing a weight tile run together).
+// One lane's operand: 32 six-bit codes, bytes 0..15 at p16 (16-byte aligned)
+// and 16..23 at p8; the instruction reads six registers.
+__device__ __forceinline__ v8i f6_operand(const uint8_t *p16, const uint8_t *p8) {
+    const uint4 a = *(const uint4 *)p16;
+    const uint2 b = *(const uint2 *)p8;
+    return (v8i){(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, 0, 0};
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One wavefront copy global -> LDS: lane l's 16 bytes at voff of r land at
+// lds + 16 l; a 2-byte copy lands zero-extended in the dword at lds + 4 l
+// (measured on MI355X); lds wavefront-uniform.
+__device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 16, voff, 0, 0, 0);
+}
+__device__ __forceinline__ void lds_copy2(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 2, voff, 0, 0, 0);
+}
+
+// this wavefront's copies into LDS complete, its LDS writes too, then the
+// workgroup barrier (no memory fence: the fence of __syncthreads would also
+// wait for the next stage's copies already in flight)
+__device__ __forceinline__ void f6_stage_sync() {
+    __builtin_amdgcn_s_waitcnt(0x3070);  // vmcnt(0) lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int WM, int WN, int TM, int TN, bool FUSE>
+__global__ void __launch_bounds__(256, 3) k_gemm_f6(
+    const uint8_t *__restrict__ w6, const uint16_t *__restrict__ d6, int n, int nb,
+    const uint8_t *__restrict__ x6, const uint16_t *__restrict__ xd, int m,
+    const float *__restrict__ bias, const float *__restrict__ residual, float *__restrict__ out,
+    int ldo, float *__restrict__ part, int bps, GateUpOut go) {
+    static_assert(!FUSE || TN == 2, "gate|up fusion pairs two column tiles per wavefront");
+    static_assert(WM * WN == 4, "four wavefronts");
+    using C = GemmCfg<WM, WN, TM, TN>;
+    constexpr int BM = C::BM, BN = C::BN;
+    // a stage buffer: activations [G_KB][2] regions of BM rows, weights
+    // [G_KB] regions of BN rows (each [rows][16] then [rows][8]), scales x.d
+    // [G_KB][BM] and w.d [G_KB][BN] (fp16 bits zero-extended to a dword: the
+    // low register of the scale-product operand)
+    constexpr int A_BYTES = G_KB * 2 * BM * F6_BYTES, B_BYTES = G_KB * BN * F6_BYTES;
+    constexpr int SX_OFF = A_BYTES + B_BYTES, SW_OFF = SX_OFF + G_KB * BM * 4;
+    constexpr int STAGE = SW_OFF + G_KB * BN * 4;
+    // wavefront copy instructions per stage: 64 lanes x 16 bytes (operands),
+    // 64 lanes x 2 bytes into dwords (scales); instruction q goes to
+    // wavefront q % 4
+    constexpr int AR = BM * F6_BYTES / 16, BR = BN * F6_BYTES / 16;  // 16-byte pieces per region
+    constexpr int A_WI = G_KB * 2 * AR / 64, B_WI = G_KB * BR / 64;
+    constexpr int SX_WI = G_KB * BM / 64, SW_WI = G_KB * BN / 64;
+    static_assert(G_KB * 2 * AR % 64 == 0 && G_KB * BR % 64 == 0, "whole copy instructions");
+    constexpr int A_PW = (A_WI + 3) / 4, B_PW = (B_WI + 3) / 4;
+    constexpr int SX_PW = (SX_WI + 3) / 4, SW_PW = (SW_WI + 3) / 4;
+    // sb0 also holds the gate|up epilogue's transposition
+    constexpr int EPI = 4 * 32 * GEMM_EPI_FT * 4;
+    __shared__ __attribute__((aligned(16))) uint8_t sb0[STAGE > EPI ? STAGE : EPI];
+    __shared__ __attribute__((aligned(16))) uint8_t sb1[STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int j = lane & 31, g = lane >> 5;
+    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+    const int b_begin = blockIdx.z * bps, b_end = min(nb, b_begin + bps);
+    const int f6_sa = g ? 128 : 132;  // hi codes 2^5 (16 x the codes' 2^1), lo 2^1
+
+    // stage-relative source offsets of this lane's copies
+    uint32_t oa[A_PW], ob[B_PW], osx[SX_PW], osw[SW_PW];
+    // piece q of a region's stage slice: rows' 16-byte parts (q < rows),
+    // then their 8-byte parts, in LDS at 16 q either way
 #pragma unroll
-        for (int a = 0; a < TM; ++a) {
-            const int r0 = m0 + (wm * TM + a) * 32;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int i = 8 * (v >> 2) + 4 * g + (v & 3);
-                const float gv = acc[a][0][v] * 0.0625f, uv = acc[a][TN - 1][v] * 0.0625f;
-                const float silu = __fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)));
-                tl[i * FT + j] = __fmul_rn(silu, uv);
-                if (out && r0 + i < m && fok) {
-                    out[(size_t)(r0 + i) * ldo + fb + j] = gv;
-                    out[(size_t)(r0 + i) * ldo + f + fb + j] = uv;
-                }
-            }
-            // the wavefront's own area: its LDS accesses complete in order
-            __builtin_amdgcn_wave_barrier();
-            float x[16];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const float4 p = *(const float4 *)(tl + rr * FT + 16 * hh + 4 * t);
-                x[4 * t] = p.x;
-                x[4 * t + 1] = p.y;
-                x[4 * t + 2] = p.z;
-                x[4 * t + 3] = p.w;
-            }
-            __builtin_amdgcn_wave_barrier();  // the next tile rewrites the area
-            int q[16];
-            uint16_t dbits;
-            int bsum;
-            quant_block_pair16(x, q, dbits, bsum);
-            const int row = r0 + rr;
-            if (row < m && fok) {
-                const size_t o = (size_t)row * f + fb + 16 * hh;
-                if (go.act)
-#pragma unroll
-                    for (int t = 0; t < 4; ++t)
-                        *(float4 *)(go.act + o + 4 * t) =
-                            make_float4(x[4 * t], x[4 * t + 1], x[4 * t + 2], x[4 * t + 3]);
-                uint32_t pk[4];
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    pk[t] = (uint32_t)(q[4 * t] & 0xff) | (uint32_t)(q[4 * t + 1] & 0xff) << 8 |
-                            (uint32_t)(q[4 * t + 2] & 0xff) << 16 | (uint32_t)q[4 * t + 3] << 24;
-                *(uint4 *)(go.qs + o) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-                if (hh == 0) {
-                    go.d[o / SI_QK] = dbits;
-                    if (go.s) go.s[o / SI_QK] = (int16_t)bsum;
-                }
-                if (go.tq) {
-                    // bytes 16hh..16hh+7 and +8..+15 of the row's block: the
-                    // first 8 of halves 0 and 1 at position 8hh
-                    const size_t pb = (size_t)(row >> 5) * (f / SI_QK) + fb / SI_QK;
-                    int8_t *tb = go.tq + q8_tiled_byte(pb, row & 31, 16 * hh);
-                    *(uint2 *)tb = make_uint2(pk[0], pk[1]);
-                    *(uint2 *)(tb + 512) = make_uint2(pk[2], pk[3]);
-                    if (hh == 0) go.td[pb * 32 + (row & 31)] = dbits;
-                }
-            }
-        }
-        return;
+    for (int i = 0; i < A_PW; ++i) {
+        const int p = (4 * i + wave) * 64 + lane, reg = p / AR, q = p % AR;
+        oa[i] = (uint32_t)(reg * m * F6_BYTES +
+                           (q < BM ? m0 * 16 + q * 16 : m * 16 + m0 * 8 + (q - BM) * 16));
     }
+#pragma unroll
+    for (int i = 0; i < B_PW; ++i) {
+        const int p = (4 * i + wave) * 64 + lane, blk = p / BR, q = p % BR;
+        ob[i] = (uint32_t)(blk * n * F6_BYTES +
+                           (q < BN ? n0 * 16 + q * 16 : n * 16 + n0 * 8 + (q - BN) * 16));
+    }
+#pragma unroll
+    for (int i = 0; i < SX_PW; ++i) {
+        const int e = (4 * i + wave) * 64 + lane, blk = e / BM, row = e % BM;
+        osx[i] = (uint32_t)((min(m0 + row, m - 1) * nb + blk) * 2);
+    }
+#pragma unroll
+    for (int i = 0; i < SW_PW; ++i) {
+        const int e = (4 * i + wave) * 64 + lane, blk = e / BN, c = e % BN;
+        osw[i] = (uint32_t)((blk * n + min(n0 + c, n - 1)) * 2);
+    }
+    // copy the stage starting at block bs into buf: past row m or n a piece
+    // reads the next region or, past the array, zero (buffer bounds); such
+    // rows and columns reach only outputs that are never stored
+    const auto issue = [&](uint8_t *buf, int bs) {
+        const uint32_t left = (uint32_t)(nb - bs);
+        const __amdgpu_buffer_rsrc_t ra_s =
+            buf_rsrc(x6 + (size_t)bs * 2 * m * F6_BYTES, left * 2 * (uint32_t)m * F6_BYTES);
+        const __amdgpu_buffer_rsrc_t rb_s =
+            buf_rsrc(w6 + (size_t)bs * n * F6_BYTES, left * (uint32_t)n * F6_BYTES);
+        const __amdgpu_buffer_rsrc_t rx_s = buf_rsrc(xd + bs, ((uint32_t)m * nb - bs) * 2);
+        const __amdgpu_buffer_rsrc_t rw_s = buf_rsrc(d6 + (size_t)bs * n, left * (uint32_t)n * 2);
+#pragma unroll
+        for (int i = 0; i < A_PW; ++i)
+            if (A_WI % 4 == 0 || 4 * i + wave < A_WI)
+                lds_copy16(ra_s, buf + 1024 * (4 * i + wave), oa[i]);
+#pragma unroll
+        for (int i = 0; i < B_PW; ++i)
+            if (B_WI % 4 == 0 || 4 * i + wave < B_WI)
+                lds_copy16(rb_s, buf + A_BYTES + 1024 * (4 * i + wave), ob[i]);
+#pragma unroll
+        for (int i = 0; i < SX_PW; ++i)
+            if (SX_WI % 4 == 0 || 4 * i + wave < SX_WI)
+                lds_copy2(rx_s, buf + SX_OFF + 256 * (4 * i + wave), osx[i]);
+#pragma unroll
+        for (int i = 0; i < SW_PW; ++i)
+            if (SW_WI % 4 == 0 || 4 * i + wave < SW_WI)
+                lds_copy2(rw_s, buf + SW_OFF + 256 * (4 * i + wave), osw[i]);
+    };
+
+    float acc[TM][TN][16];
 #pragma unroll
     for (int a = 0; a < TM; ++a)
 #pragma unroll
-        for (int b = 0; b < TN; ++b) {
-            const int col = n0 + (wn * TN + b) * 32 + j;
-            if (col >= n) continue;
-            const float bv = (part == nullptr && bias) ? bias[col] : 0.0f;
+        for (int b = 0; b < TN; ++b)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int row = m0 + (wm * TM + a) * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
-                if (row >= m) continue;
-                if (part) {
-                    part[((size_t)blockIdx.z * m + row) * n + col] = acc[a][b][v] * 0.0625f;
-                } else {
-                    float y = acc[a][b][v] * 0.0625f + bv;
-                    if (residual) y = __fadd_rn(residual[(size_t)row * ldo + col], y);
-                    out[(size_t)row * ldo + col] = y;
-                }
+            for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+
+    // per-lane LDS offsets inside a stage buffer (each access is then the
+    // buffer's static address + a constant + one of these): the lane's hi
+    // (lanes 0..31) or lo (32..63) activation row, weight row, scales
+    const int ra = wm * TM * 32 + j, rb = wn * TN * 32 + j;
+    const int a16 = g * BM * F6_BYTES + ra * 16, a8 = g * BM * F6_BYTES + BM * 16 + ra * 8;
+    const int b16 = A_BYTES + rb * 16, b8 = A_BYTES + BN * 16 + rb * 8;
+    const int sx_off = SX_OFF + ra * 4, sw_off = SW_OFF + rb * 4;
+    const auto compute = [&](const uint8_t *buf, int bs) {
+#pragma unroll
+        for (int blk = 0; blk < G_KB; ++blk) {
+            if (bs + blk >= b_end) break;
+            // scale-product operands {x.d, 0, 0, 0} and {w.d, 0, 0, 0}: x.d at
+            // k = 0 and 4, w.d at k = 0 only (lanes 32..63 take zero)
+            v8i aop[TM], bop[TN];
+            gh4 asc[TM], bsc[TN];
+#pragma unroll
+            for (int a = 0; a < TM; ++a) {
+                aop[a] = f6_operand(buf + a16 + blk * 2 * BM * F6_BYTES + a * 32 * 16,
+                                    buf + a8 + blk * 2 * BM * F6_BYTES + a * 32 * 8);
+                const unsigned xs = *(const uint32_t *)(buf + sx_off + (blk * BM + a * 32) * 4);
+                asc[a] = __builtin_bit_cast(gh4, (v2u){xs, 0u});
             }
+#pragma unroll
+            for (int b = 0; b < TN; ++b) {
+                bop[b] = f6_operand(buf + b16 + blk * BN * F6_BYTES + b * 32 * 16,
+                                    buf + b8 + blk * BN * F6_BYTES + b * 32 * 8);
+                const unsigned ws = *(const uint32_t *)(buf + sw_off + (blk * BN + b * 32) * 4);
+                bsc[b] = __builtin_bit_cast(gh4, (v2u){g ? 0u : ws, 0u});
+            }
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+#pragma unroll
+                for (int b = 0; b < TN; ++b) {
+                    v16f zf = {};
+                    const v16f dot = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        aop[a], bop[b], zf, 2, 2, 0, f6_sa, 0, 128);
+                    const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(asc[a], bsc[b], zf, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[a][b][v] = fmaf(dot[v], sc[v], acc[a][b][v]);
+                }
         }
+    };
+
+    // the two buffers in turn, unrolled so each access names its buffer
+    const int nstage = (b_end - b_begin + G_KB - 1) / G_KB;
+    if (nstage > 0) issue(sb0, b_begin);
+    for (int st = 0; st < nstage; st += 2) {
+        f6_stage_sync();  // stage st in sb0; everyone is done with sb1
+        if (st + 1 < nstage) issue(sb1, b_begin + (st + 1) * G_KB);
+        compute(sb0, b_begin + st * G_KB);
+        if (st + 1 >= nstage) break;
+        f6_stage_sync();  // stage st + 1 in sb1; everyone is done with sb0
+        if (st + 2 < nstage) issue(sb0, b_begin + (st + 2) * G_KB);
+        compute(sb1, b_begin + (st + 1) * G_KB);
+    }
+    __syncthreads();  // no copy in flight; every wavefront is done reading
+    gemm_tile_epilogue<WM, WN, TM, TN, FUSE>(acc, 1.0f, (float *)sb0, m, n, m0, n0, bias,
+                                             residual, out, ldo, part, go);
 }
 
 // ===========================================================================
@@ -1924,6 +2161,142 @@ static int gemm_core(const uint8_t *wqs, const uint16_t *wd, int tile, int n, in
             SI_LAUNCH(k_gemm_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0,
                       st, part, splits, m, n, bias, residual, out, ldo);
     }
+    return 0;
+}
+
+// ===========================================================================
+// Operands of the fp6 formulation (k_gemm_fast with F6)
+
+// e2m3 codes of v / 2 for four 4-bit values n, one per byte (each value's
+// half is an e2m3 number: 0.5 subnormal, 1..7.5 normal): unsigned, v = n
+// (0..15), or two's complement, v = n - 16 for n >= 8 (-8..7), sign in bit 5.
+// Two byte lookups (v_perm) from 8-entry tables and a select on bit 3.
+__device__ __forceinline__ uint32_t f6_codes4(uint32_t n, bool sgn) {
+    const uint32_t t0 = 0x0c080400u, t1 = 0x16141210u;   // v = 0..3, 4..7
+    const uint32_t u0 = sgn ? 0x32343638u : 0x1b1a1918u;  // n = 8..11
+    const uint32_t u1 = sgn ? 0x24282c30u : 0x1f1e1d1cu;  // n = 12..15
+    const uint32_t idx = n & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(t1, t0, idx), hi = __builtin_amdgcn_perm(u1, u0, idx);
+    const uint32_t m = ((n >> 3) & 0x01010101u) * 0xffu;
+    return (hi & m) | (lo & ~m);
+}
+
+// four codes (bytes of c, each < 64) -> 24 bits, code k at bit 6 k
+__device__ __forceinline__ uint32_t f6_pack4(uint32_t c) {
+    return (c & 0x3fu) | ((c >> 2) & 0xfc0u) | ((c >> 4) & 0x3f000u) | ((c >> 6) & 0xfc0000u);
+}
+
+// 32 codes (8 dwords of 4) -> 24 bytes, code i at bit 6 i of six little-
+// endian dwords (the operand packing of the fp6 matrix instructions); bytes
+// 0..15 to p16, 16..23 to p8
+__device__ __forceinline__ void f6_store(uint8_t *p16, uint8_t *p8, const uint32_t (&c)[8]) {
+    uint32_t q[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) q[k] = f6_pack4(c[k]);
+    *(uint4 *)p16 = make_uint4(q[0] | q[1] << 24, q[1] >> 8 | q[2] << 16, q[2] >> 16 | q[3] << 8,
+                               q[4] | q[5] << 24);
+    *(uint2 *)p8 = make_uint2(q[5] >> 8 | q[6] << 16, q[6] >> 16 | q[7] << 8);
+}
+
+// Q8 values, planar [m][nb * 32] -> x6: per block the region of the codes of
+// hi = q >> 4 (-8..7), then that of lo = q & 15 (q = 16 hi + lo), each m rows
+// as [m][16] then [m][8].  Grid (ceil(m / 256), nb), a thread per (row,
+// block), consecutive threads consecutive rows.
+__global__ void __launch_bounds__(256) k_q8_to_x6(const int8_t *__restrict__ qs, int m, int nb,
+                                                  uint8_t *__restrict__ x6) {
+    const int row = blockIdx.x * 256 + threadIdx.x, blk = blockIdx.y;
+    if (row >= m) return;
+    const int8_t *src = qs + ((size_t)row * nb + blk) * SI_QK;
+    const uint4 q0 = *(const uint4 *)src, q1 = *(const uint4 *)(src + 16);
+    const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    uint32_t hi[8], lo[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        hi[k] = f6_codes4((w[k] >> 4) & 0x0f0f0f0fu, true);
+        lo[k] = f6_codes4(w[k] & 0x0f0f0f0fu, false);
+    }
+    uint8_t *rh = x6 + (size_t)(2 * blk) * m * F6_BYTES, *rl = rh + (size_t)m * F6_BYTES;
+    f6_store(rh + (size_t)row * 16, rh + (size_t)m * 16 + (size_t)row * 8, hi);
+    f6_store(rl + (size_t)row * 16, rl + (size_t)m * 16 + (size_t)row * 8, lo);
+}
+
+// Repacked Q4 [nb][n][16] (byte i: element i low nibble, i + 16 high) and its
+// tiled scales -> w6 (per block a region of n rows, [n][16] then [n][8], codes
+// of nibble - 8: the two's-complement table at nibble ^ 8) and d6 [nb][n];
+// logical row r is physical row gate_up_row(r, gu_f) when gu_f > 0.
+__global__ void __launch_bounds__(256) k_q4_to_w6(const uint8_t *__restrict__ qs,
+                                                  const uint16_t *__restrict__ d, int n, int nb,
+                                                  int tile, int gu_f, uint8_t *__restrict__ w6,
+                                                  uint16_t *__restrict__ d6) {
+    const int r = blockIdx.x * 256 + threadIdx.x, blk = blockIdx.y;
+    if (r >= n) return;
+    const int pr = gu_f ? gate_up_row(r, gu_f) : r;
+    const uint4 b = *(const uint4 *)(qs + ((size_t)blk * n + pr) * 16);
+    const uint32_t w[4] = {b.x, b.y, b.z, b.w};
+    uint32_t c[8];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        c[t] = f6_codes4((w[t] & 0x0f0f0f0fu) ^ 0x08080808u, true);             // elements 4t..
+        c[4 + t] = f6_codes4(((w[t] >> 4) & 0x0f0f0f0fu) ^ 0x08080808u, true);  // 16 + 4t..
+    }
+    uint8_t *rg = w6 + (size_t)blk * n * F6_BYTES;
+    f6_store(rg + (size_t)r * 16, rg + (size_t)n * 16 + (size_t)r * 8, c);
+    d6[(size_t)blk * n + r] = d[q4_scale_index(pr, blk, nb, tile)];
+}
+
+void launch_q8_to_x6(const int8_t *qs, int m, int nb, uint8_t *x6, hipStream_t st) {
+    if (m <= 0 || nb <= 0) return;
+    SI_LAUNCH(k_q8_to_x6, dim3((unsigned)((m + 255) / 256), (unsigned)nb), dim3(256), 0, st, qs,
+              m, nb, x6);
+}
+
+void launch_q4_to_w6(const uint8_t *qs, const uint16_t *d, int n, int nb, int tile, int gu_f,
+                     uint8_t *w6, uint16_t *d6, hipStream_t st) {
+    if (n <= 0 || nb <= 0) return;
+    SI_LAUNCH(k_q4_to_w6, dim3((unsigned)((n + 255) / 256), (unsigned)nb), dim3(256), 0, st, qs, d,
+              n, nb, tile, gu_f, w6, d6);
+}
+
+int launch_gemm_f6(const uint8_t *w6, const uint16_t *d6, int n, int k, const uint8_t *x6,
+                   const uint16_t *xd, int m, const float *bias, const float *residual,
+                   float *out, int ldo, void *workspace, size_t ws_bytes, bool want_part,
+                   int gu_f, float *act, int8_t *aqs, uint16_t *ad, int16_t *as, hipStream_t st) {
+    if (m <= 0 || n <= 0) return 0;
+    const int nb = k / SI_QK;
+    GemmPlan p = gemm_plan(m, n, nb);
+    if (gu_f && p.splits > 1) return -1;
+    if (p.splits > 1 && !(workspace && ws_bytes >= (size_t)p.splits * m * n * sizeof(float))) {
+        p.splits = 1;
+        p.bps = nb;
+    }
+    float *part = p.splits > 1 ? (float *)workspace : nullptr;
+    const dim3 grid((m + p.bm - 1) / p.bm, (n + p.bn - 1) / p.bn, p.splits);
+    const GateUpOut go{gu_f, act, aqs, ad, as, nullptr, nullptr};
+#define CALL(WM, WN, TM, TN, FUSE)                                                             \
+    SI_LAUNCH((k_gemm_f6<WM, WN, TM, TN, FUSE>), grid, dim3(256), 0, st, w6, d6, n, nb, x6, xd, \
+              m, bias, residual, out, ldo, part, p.bps, go)
+    if (gu_f) {
+        if (p.bm == 64)
+            CALL(2, 2, 1, 2, true);
+        else
+            CALL(2, 2, 2, 2, true);
+    } else {
+        if (p.bm == 64)
+            CALL(1, 4, 2, 1, false);
+        else
+            CALL(2, 2, 2, 2, false);
+    }
+#undef CALL
+    if (!part) return 0;
+    if (want_part) return p.splits;
+    const size_t tot = (size_t)m * n;
+    const auto al = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
+    if (n % 4 == 0 && ldo % 4 == 0 && al(out) && al(bias) && al(residual))
+        SI_LAUNCH(k_gemm_reduce4, dim3((unsigned)((tot / 4 + 255) / 256)), dim3(256), 0, st,
+                  part, p.splits, m, n, bias, residual, out, ldo);
+    else
+        SI_LAUNCH(k_gemm_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, part,
+                  p.splits, m, n, bias, residual, out, ldo);
     return 0;
 }
 
