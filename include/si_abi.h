@@ -145,8 +145,19 @@ int si_q4q8_block_dots(const uint8_t *wqs, const uint16_t *wd, int n, int k,
  * si_gemm_q4q8: one pass over any K (no workspace); the same sums as the
  * default within fp32 summation order (K is spread over 12 wavefronts
  * instead of 16).  si_gemm_gateup_q8 (k <= 3840): the same results as the
- * default bit for bit. */
-enum { SI_GEMM_EXACT = 1, SI_GEMM_F16 = 2, SI_GEMM_TILED_A = 4 };
+ * default bit for bit.
+ * SI_GEMM_F6 (alone; si_gemm_gateup_q8: shapes whose plan needs no K split):
+ * the exact fp6 formulation the layer's prefill GEMMs use past 512 rows.
+ * Each Q8 value q = 16 (q >> 4) + (q & 15) and each weight (nibble - 8) are
+ * fp6 e2m3 codes of half the value; one scaled fp6 matrix instruction per
+ * 32 x 32 tile and block gives the block's integer dot exactly, as a float
+ * (no conversion in the epilogue).  The call converts both operands into
+ * the workspace first, which must be si_gemm_f6_workspace(m, n, k) bytes
+ * (gate|up: n = 2f), 256-byte aligned.  The sums are those of the default
+ * tile kernel's plan (bit for bit where the default runs it: more than 512
+ * rows, or a shape the streaming kernel does not take).  No reference
+ * counterpart: a device formulation of matvec_q4q8 (qwen_one_layer.c:148-162). */
+enum { SI_GEMM_EXACT = 1, SI_GEMM_F16 = 2, SI_GEMM_TILED_A = 4, SI_GEMM_F6 = 8 };
 
 /* Operand-tiled Q8_0 (the activation operand of SI_GEMM_TILED_A): rows in
  * panels of 32 (the last padded: ceil(m/32) panels); block b of panel p is
@@ -186,6 +197,9 @@ int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
                  const float *bias, const float *residual, float *out, int ldo,
                  int flags, void *workspace, size_t ws_bytes, void *stream);
 size_t si_gemm_workspace(int m, int n, int k);
+/* Workspace bytes of si_gemm_q4q8 / si_gemm_gateup_q8 with SI_GEMM_F6 (the
+ * converted operands and the K-split partials).  No reference counterpart. */
+size_t si_gemm_f6_workspace(int m, int n, int k);
 
 /* The FFN gate|up projection of m activation rows with SwiGLU and Q8_0:
  * gu = [gate | up] = matvec_q4q8 of each row (qwen_one_layer.c:148-162)
@@ -195,7 +209,7 @@ size_t si_gemm_workspace(int m, int n, int k);
  * the intermediate: SI_GEMM_EXACT, or a plan that splits K (si_gemm_workspace
  * (m, 2f, k) > 0) given less workspace than that.  act and bsum may be NULL.
  * wqs, xqs, qs and act are 16-byte aligned.
- * flags: SI_GEMM_EXACT as for si_gemm_q4q8, or SI_GEMM_F16. */
+ * flags: SI_GEMM_EXACT as for si_gemm_q4q8, SI_GEMM_F16, or SI_GEMM_F6. */
 int si_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, int k,
                       const int8_t *xqs, const uint16_t *xd, int m, float *gu, float *act,
                       int8_t *qs, uint16_t *d, int16_t *bsum, int flags, void *workspace,

@@ -293,6 +293,23 @@ int si_ffn_gateup_q8(const float *h, const float *gain, int hidden, float eps,
     return check_launch("si_ffn_gateup_q8");
 }
 
+// SI_GEMM_F6 workspace: the fp6 weights w6 and scales d6, the activations
+// x6, then the K-split partials (none for the fused gate|up pass), each part
+// 256-byte aligned.
+struct F6Ws {
+    size_t w6 = 0, d6 = 0, x6 = 0, part = 0, total = 0;
+};
+static F6Ws f6_ws(int m, int n, int k, bool partials) {
+    const size_t nb = (size_t)k / 32;
+    const auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    F6Ws o;
+    o.d6 = up((size_t)n * nb * 24);
+    o.x6 = o.d6 + up((size_t)n * nb * 2);
+    o.part = o.x6 + up((size_t)m * nb * 48);
+    o.total = o.part + (partials ? up(gemm_f6_partial_bytes(m, n, k)) : 0);
+    return o;
+}
+
 int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
                  const int8_t *xqs, const uint16_t *xd, int m, const float *bias,
                  const float *residual, float *out, int ldo, int flags, void *workspace,
@@ -308,7 +325,27 @@ int si_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
     SI_REQUIRE(m == 0 || (wqs && wd && xqs && xd && out), "gemm: NULL pointer");
     SI_REQUIRE(((uintptr_t)wqs & 15) == 0 && ((uintptr_t)xqs & 15) == 0,
                "gemm: wqs and xqs must be 16-byte aligned");
-    SI_REQUIRE((flags & ~(SI_GEMM_EXACT | SI_GEMM_TILED_A)) == 0, "gemm: unknown flags %d", flags);
+    SI_REQUIRE((flags & ~(SI_GEMM_EXACT | SI_GEMM_TILED_A | SI_GEMM_F6)) == 0,
+               "gemm: unknown flags %d", flags);
+    if (flags & SI_GEMM_F6) {
+        SI_REQUIRE(flags == SI_GEMM_F6, "gemm: SI_GEMM_F6 takes no other flag");
+        SI_REQUIRE((size_t)m * k / 32 * 48 < ((size_t)1 << 31) &&
+                       (size_t)n * k / 32 * 24 < ((size_t)1 << 31),
+                   "gemm: SI_GEMM_F6 operands beyond 2 GiB (m=%d n=%d k=%d)", m, n, k);
+        if (m == 0) return SI_OK;
+        const F6Ws L = f6_ws(m, n, k, true);
+        SI_REQUIRE(workspace && ws_bytes >= L.total && ((uintptr_t)workspace & 255) == 0,
+                   "gemm: SI_GEMM_F6 needs si_gemm_f6_workspace(m, n, k) = %zu bytes of "
+                   "256-byte aligned workspace", L.total);
+        uint8_t *ws = (uint8_t *)workspace;
+        const hipStream_t st = S(stream);
+        launch_q4_to_w6(wqs, wd, n, k / 32, tile, 0, ws + L.w6, (uint16_t *)(ws + L.d6), st);
+        launch_q8_to_x6(xqs, m, k / 32, ws + L.x6, st);
+        launch_gemm_f6(ws + L.w6, (const uint16_t *)(ws + L.d6), n, k, ws + L.x6, xd, m, bias,
+                       residual, out, ldo, ws + L.part, L.total - L.part, false, 0, nullptr,
+                       nullptr, nullptr, nullptr, st);
+        return check_launch("si_gemm_q4q8");
+    }
     if (flags & SI_GEMM_TILED_A) {
         SI_REQUIRE(!(flags & SI_GEMM_EXACT), "gemm: SI_GEMM_TILED_A has no exact mode");
         SI_REQUIRE(m <= 512, "gemm: SI_GEMM_TILED_A takes at most 512 rows (m=%d)", m);
@@ -355,8 +392,29 @@ int si_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, i
     SI_REQUIRE(((uintptr_t)wqs & 15) == 0 && ((uintptr_t)xqs & 15) == 0 &&
                    ((uintptr_t)qs & 15) == 0 && ((uintptr_t)act & 15) == 0,
                "gemm_gateup: wqs, xqs, qs and act must be 16-byte aligned");
-    SI_REQUIRE((flags & ~(SI_GEMM_EXACT | SI_GEMM_F16 | SI_GEMM_TILED_A)) == 0,
+    SI_REQUIRE((flags & ~(SI_GEMM_EXACT | SI_GEMM_F16 | SI_GEMM_TILED_A | SI_GEMM_F6)) == 0,
                "gemm_gateup: unknown flags %d", flags);
+    if (flags & SI_GEMM_F6) {
+        SI_REQUIRE(flags == SI_GEMM_F6, "gemm_gateup: SI_GEMM_F6 takes no other flag");
+        SI_REQUIRE((size_t)m * k / 32 * 48 < ((size_t)1 << 31) &&
+                       (size_t)2 * f * k / 32 * 24 < ((size_t)1 << 31),
+                   "gemm_gateup: SI_GEMM_F6 operands beyond 2 GiB (m=%d f=%d k=%d)", m, f, k);
+        if (m == 0) return SI_OK;
+        SI_REQUIRE(gemm_f6_partial_bytes(m, 2 * f, k) == 0,
+                   "gemm_gateup: SI_GEMM_F6 runs the fused one-pass plan only; this shape "
+                   "splits K (m=%d f=%d k=%d)", m, f, k);
+        const F6Ws L = f6_ws(m, 2 * f, k, false);
+        SI_REQUIRE(workspace && ws_bytes >= L.total && ((uintptr_t)workspace & 255) == 0,
+                   "gemm_gateup: SI_GEMM_F6 needs si_gemm_f6_workspace(m, 2f, k) = %zu bytes "
+                   "of 256-byte aligned workspace", L.total);
+        uint8_t *ws = (uint8_t *)workspace;
+        const hipStream_t st = S(stream);
+        launch_q4_to_w6(wqs, wd, 2 * f, k / 32, tile, f, ws + L.w6, (uint16_t *)(ws + L.d6), st);
+        launch_q8_to_x6(xqs, m, k / 32, ws + L.x6, st);
+        launch_gemm_f6(ws + L.w6, (const uint16_t *)(ws + L.d6), 2 * f, k, ws + L.x6, xd, m,
+                       nullptr, nullptr, gu, 2 * f, nullptr, 0, false, f, act, qs, d, bsum, st);
+        return check_launch("si_gemm_gateup_q8");
+    }
     SI_REQUIRE(!(flags & SI_GEMM_F16) || !(flags & SI_GEMM_EXACT),
                "gemm_gateup: SI_GEMM_F16 is a fast-path formulation (not with SI_GEMM_EXACT)");
     if (flags & SI_GEMM_TILED_A) {
@@ -377,6 +435,11 @@ int si_gemm_gateup_q8(const uint8_t *wqs, const uint16_t *wd, int tile, int f, i
 size_t si_gemm_workspace(int m, int n, int k) {
     if (m <= 0 || n <= 0 || k <= 0 || k % 32) return 0;
     return gemm_workspace_bytes(m, n, k);
+}
+
+size_t si_gemm_f6_workspace(int m, int n, int k) {
+    if (m <= 0 || n <= 0 || k <= 0 || k % 32) return 0;
+    return f6_ws(m, n, k, true).total;
 }
 
 int si_rope_table(int npos, int hdim, float base, float *c, float *s) {

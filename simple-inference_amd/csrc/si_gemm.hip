@@ -2193,8 +2193,9 @@ __device__ __forceinline__ void f6_store(uint8_t *p16, uint8_t *p8, const uint32
     uint32_t q[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) q[k] = f6_pack4(c[k]);
-    *(uint4 *)p16 = make_uint4(q[0] | q[1] << 24, q[1] >> 8 | q[2] << 16, q[2] >> 16 | q[3] << 8,
-                               q[4] | q[5] << 24);
+    // 8-byte stores: a region of an odd row count starts only 8-byte aligned
+    *(uint2 *)p16 = make_uint2(q[0] | q[1] << 24, q[1] >> 8 | q[2] << 16);
+    *(uint2 *)(p16 + 8) = make_uint2(q[2] >> 16 | q[3] << 8, q[4] | q[5] << 24);
     *(uint2 *)p8 = make_uint2(q[5] >> 8 | q[6] << 16, q[6] >> 16 | q[7] << 8);
 }
 
@@ -2255,6 +2256,11 @@ void launch_q4_to_w6(const uint8_t *qs, const uint16_t *d, int n, int nb, int ti
     if (n <= 0 || nb <= 0) return;
     SI_LAUNCH(k_q4_to_w6, dim3((unsigned)((n + 255) / 256), (unsigned)nb), dim3(256), 0, st, qs, d,
               n, nb, tile, gu_f, w6, d6);
+}
+
+size_t gemm_f6_partial_bytes(int m, int n, int k) {
+    const GemmPlan p = gemm_plan(m, n, k / SI_QK);
+    return p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0;
 }
 
 int launch_gemm_f6(const uint8_t *w6, const uint16_t *d6, int n, int k, const uint8_t *x6,

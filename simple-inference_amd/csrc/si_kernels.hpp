@@ -155,6 +155,7 @@ bool launch_gemm_qkv_rope(const uint8_t *wqs, const uint16_t *wd, int tile, int 
 // it is the fused gate|up + SwiGLU + Q8 pass (out: the optional gate|up, ldo
 // 2 gu_f), and returns -1 (nothing launched) when that plan needs a K split.
 void launch_q8_to_x6(const int8_t *qs, int m, int nb, uint8_t *x6, hipStream_t st);
+size_t gemm_f6_partial_bytes(int m, int n, int k);  // launch_gemm_f6's K-split partials
 void launch_q4_to_w6(const uint8_t *qs, const uint16_t *d, int n, int nb, int tile, int gu_f,
                      uint8_t *w6, uint16_t *d6, hipStream_t st);
 int launch_gemm_f6(const uint8_t *w6, const uint16_t *d6, int n, int k, const uint8_t *x6,

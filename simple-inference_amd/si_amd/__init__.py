@@ -27,6 +27,7 @@ SI_LAYER_CAPTURE = 8
 SI_GEMM_EXACT = 1
 SI_GEMM_F16 = 2
 SI_GEMM_TILED_A = 4
+SI_GEMM_F6 = 8
 BUFFERS = ["NORMED", "XQ_QS", "XQ_D", "XQ_S", "QKV", "Q", "ATTN", "ATTQ_QS", "ATTQ_D",
            "ATTQ_S", "ATTN_OUT", "H", "NORMED2", "XQ2_QS", "XQ2_D", "XQ2_S", "GU", "ACT",
            "ACTQ_QS", "ACTQ_D", "ACTQ_S", "ACTQ_TQ", "ACTQ_TD"]
@@ -89,6 +90,7 @@ _SIGS = {
     "si_ffn_gateup_q8": (_I, [_P, _P, _I, _F, _P, _P, _I, _I, _P, _P, _P, _P, _I, _P]),
     "si_gemm_q4q8": (_I, [_P, _P, _I, _I, _I, _P, _P, _I, _P, _P, _P, _I, _I, _P, _Z, _P]),
     "si_gemm_workspace": (_Z, [_I, _I, _I]),
+    "si_gemm_f6_workspace": (_Z, [_I, _I, _I]),
     "si_gemm_gateup_q8": (_I, [_P, _P, _I, _I, _I, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _Z,
                                _P]),
     "si_rope_kv_append": (_I, [ctypes.POINTER(Shape), _P, _I, _I, _I, _I, _I, _P, _P, _P, _P,
