@@ -671,6 +671,7 @@ __global__ void __launch_bounds__(256, 3) k_gemm_f6(
     // copy the stage starting at block bs into buf: past row m or n a piece
     // reads the next region or, past the array, zero (buffer bounds); such
     // rows and columns reach only outputs that are never stored
+    const int wu = __builtin_amdgcn_readfirstlane(wave);  // scalar copy addresses
     const auto issue = [&](uint8_t *buf, int bs) {
         const uint32_t left = (uint32_t)(nb - bs);
         const __amdgpu_buffer_rsrc_t ra_s =
@@ -681,20 +682,20 @@ __global__ void __launch_bounds__(256, 3) k_gemm_f6(
         const __amdgpu_buffer_rsrc_t rw_s = buf_rsrc(d6 + (size_t)bs * n, left * (uint32_t)n * 2);
 #pragma unroll
         for (int i = 0; i < A_PW; ++i)
-            if (A_WI % 4 == 0 || 4 * i + wave < A_WI)
-                lds_copy16(ra_s, buf + 1024 * (4 * i + wave), oa[i]);
+            if (A_WI % 4 == 0 || 4 * i + wu < A_WI)
+                lds_copy16(ra_s, buf + 1024 * (4 * i + wu), oa[i]);
 #pragma unroll
         for (int i = 0; i < B_PW; ++i)
-            if (B_WI % 4 == 0 || 4 * i + wave < B_WI)
-                lds_copy16(rb_s, buf + A_BYTES + 1024 * (4 * i + wave), ob[i]);
+            if (B_WI % 4 == 0 || 4 * i + wu < B_WI)
+                lds_copy16(rb_s, buf + A_BYTES + 1024 * (4 * i + wu), ob[i]);
 #pragma unroll
         for (int i = 0; i < SX_PW; ++i)
-            if (SX_WI % 4 == 0 || 4 * i + wave < SX_WI)
-                lds_copy2(rx_s, buf + SX_OFF + 256 * (4 * i + wave), osx[i]);
+            if (SX_WI % 4 == 0 || 4 * i + wu < SX_WI)
+                lds_copy2(rx_s, buf + SX_OFF + 256 * (4 * i + wu), osx[i]);
 #pragma unroll
         for (int i = 0; i < SW_PW; ++i)
-            if (SW_WI % 4 == 0 || 4 * i + wave < SW_WI)
-                lds_copy2(rw_s, buf + SW_OFF + 256 * (4 * i + wave), osw[i]);
+            if (SW_WI % 4 == 0 || 4 * i + wu < SW_WI)
+                lds_copy2(rw_s, buf + SW_OFF + 256 * (4 * i + wu), osw[i]);
     };
 
     float acc[TM][TN][16];
@@ -724,6 +725,9 @@ __global__ void __launch_bounds__(256, 3) k_gemm_f6(
             for (int a = 0; a < TM; ++a) {
                 aop[a] = f6_operand(buf + a16 + blk * 2 * BM * F6_BYTES + a * 32 * 16,
                                     buf + a8 + blk * 2 * BM * F6_BYTES + a * 32 * 8);
+                // keeps each operand's two reads its own (merged reads of two
+                // tiles' 8-byte parts cost register copies)
+                __builtin_amdgcn_sched_barrier(0);
                 const unsigned xs = *(const uint32_t *)(buf + sx_off + (blk * BM + a * 32) * 4);
                 asc[a] = __builtin_bit_cast(gh4, (v2u){xs, 0u});
             }
@@ -731,6 +735,7 @@ __global__ void __launch_bounds__(256, 3) k_gemm_f6(
             for (int b = 0; b < TN; ++b) {
                 bop[b] = f6_operand(buf + b16 + blk * BN * F6_BYTES + b * 32 * 16,
                                     buf + b8 + blk * BN * F6_BYTES + b * 32 * 8);
+                __builtin_amdgcn_sched_barrier(0);
                 const unsigned ws = *(const uint32_t *)(buf + sw_off + (blk * BN + b * 32) * 4);
                 bsc[b] = __builtin_bit_cast(gh4, (v2u){g ? 0u : ws, 0u});
             }
