@@ -619,22 +619,37 @@ def bench_prefill(torch, si_amd, stream, shape_name, ntok, steps):
         torch.cuda.synchronize()
     gt = graph_time(torch, stream, call, steps, replays=5)
     ms = gt["ms"]
-    gemm_ms, gu, gu16 = gemm_graph_ms(torch, si_amd, stream, lay, s, ntok, steps)
+    # past 512 rows the layer runs its GEMMs in the fp6 formulation
+    f6 = ntok > 512
+    gemm_ms, gu, gu16 = gemm_graph_ms(torch, si_amd, stream, lay, s, ntok, steps, f6)
     ops = gemm_int_ops(s, ntok)
     lay.close()
     cfg = "3" if shape_name == "0.5b" else "4"
     per_call = {k: round(float(np.sum(v)) / reps, 3) for k, v in kern.items()}
-    gname, gdur = max(gu.items(), key=lambda kv: len(kv[1]))
+    if f6:
+        # the layer's own GEMM dispatches and the conversions of their inputs
+        # (the ABI's fp6 call would also convert the weights, which the layer
+        # does once when built)
+        gemm_ms = sum(v for k, v in per_call.items()
+                      if k.startswith(("k_gemm", "k_q8_to_x6"))) * 1e-3
+        gemm_timing = ("sum of the layer's GEMM and k_q8_to_x6 dispatches (per-dispatch "
+                       "HIP events)")
+    else:
+        gemm_timing = "the four projections alone, one HIP graph (gemm_graph_ms)"
+    # the dominant kernel: the fused gate|up instance the layer dispatched,
+    # timed per dispatch inside the layer calls (the roofline), and the same
+    # instance launched alone on the layer's buffers (roofline_alone)
+    gname = next((k for k in kern if k in gu), None)
+    if gname is None:  # not dispatched by the layer: the stand-alone instance
+        gname = max(gu, key=lambda k: len(gu[k]))
+    gdur = gu[gname]
     gu_ops = 2 * ntok * 2 * s.ffn * s.hidden
-    # the dominant kernel (the gate|up GEMM) timed per dispatch inside the
-    # layer calls (the roofline), and the same instance launched alone on the
-    # layer's buffers (roofline_alone)
     in_layer = kern.get(gname, gdur)
     return dict(ms=ms, tokens_per_s=ntok / (ms * 1e-3), spread_us=spread_us(gt),
                 gemm_ms=gemm_ms, gemm_tops=ops / (gemm_ms * 1e-3) / 1e12,
                 mfma_pct_gemm=100.0 * ops / (gemm_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
                 mfma_pct_layer=100.0 * ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
-                gemm_timing="the four projections alone, one HIP graph (gemm_graph_ms)",
+                gemm_timing=gemm_timing,
                 phases_ms={k: round(v, 4) for k, v in ph.items()},
                 kernels_us_per_call=dict(sorted(per_call.items(), key=lambda kv: -kv[1])),
                 kernels_sum_us=round(sum(per_call.values()), 3),
@@ -654,15 +669,19 @@ def bench_prefill(torch, si_amd, stream, shape_name, ntok, steps):
                     for k16, v16 in gu16.items()})
 
 
-def gemm_graph_ms(torch, si_amd, stream, lay, s, m, steps):
+def gemm_graph_ms(torch, si_amd, stream, lay, s, m, steps, f6=False):
     """The layer's four projections alone (the same kernels, weights and
     activation buffers a prefill call uses, left valid by it), captured as one
-    HIP graph: the GEMM time without per-phase event gaps."""
+    HIP graph: the GEMM time without per-phase event gaps; and the gate|up
+    instance alone, per dispatch (f6: in the fp6 formulation, as the layer
+    runs it past 512 rows)."""
     L = si_amd.lib()
     H, F = s.hidden, s.ffn
     W = [lay.weights(i) for i in range(4)]  # QKV, O, gate|up, down
     b = lambda n: ctypes.c_void_p(lay.buffer(n))
     ws_bytes = max(L.si_gemm_workspace(m, w[3], w[4]) for w in W)
+    if f6:
+        ws_bytes = max(ws_bytes, L.si_gemm_f6_workspace(m, 2 * F, W[2][4]))
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device="cuda")
     out = torch.empty(m * H, device="cuda")
     wsp = si_amd.ptr(ws)
@@ -690,7 +709,8 @@ def gemm_graph_ms(torch, si_amd, stream, lay, s, m, steps):
     # the gate|up GEMM (the prefill's time-dominant kernel) alone, per
     # dispatch; and its f16 formulation (SI_GEMM_F16, bit-identical results)
     with torch.cuda.stream(stream):
-        gu = kernel_durations(si_amd, lambda: [gateup() for _ in range(max(3, steps))],
+        gu_flags = si_amd.SI_GEMM_F6 if f6 else 0
+        gu = kernel_durations(si_amd, lambda: [gateup(gu_flags) for _ in range(max(3, steps))],
                               "k_gemm")
         gu16 = kernel_durations(si_amd, lambda: [gateup(si_amd.SI_GEMM_F16)
                                                  for _ in range(max(3, steps))], "k_gemm")
