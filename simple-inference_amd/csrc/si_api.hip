@@ -864,7 +864,8 @@ static int make_workspace(const si_shape_t *s, int max_tokens, int max_pos,
     TRY(m.alloc(&ws, W->attn_ws_bytes));
     W->attn_ws = ws;
     TRY(m.alloc(&W->scores, (size_t)s->qheads * max_pos));
-    if (max_tokens > 512)
+    // past 64 rows the gate|up GEMM (past 512 all four) runs in the fp6 formulation
+    if (max_tokens > 64)
         TRY(m.alloc(&W->x6, M * (size_t)(std::max(std::max(H, QD), F) / 32) * 48));
     // GEMM split-K partials: the largest need over the layer's projections
     // and every row count up to max_tokens (the split depends on both)
@@ -896,9 +897,9 @@ struct si_layer {
     Q4Dev wqkv_rope;
     float *bqkv_rope = nullptr;
     bool has_rope = false;
-    // prefill of more than 512 rows: the four matrices for the fp6 GEMMs
+    // the matrices for the fp6 GEMMs: gate|up past 64 rows, all four past 512
     Q6Dev wqkv6, wo6, wgu6, wdown6;
-    bool has_f6 = false;
+    bool has_f6 = false, has_f6_gu = false;
     uint8_t *x6 = nullptr;
     float *norm = nullptr, *bqkv = nullptr, *post_norm = nullptr;
     std::shared_ptr<Workspace> ws;
@@ -1030,13 +1031,15 @@ static int build_layer(const si_layer_host_t *w, std::shared_ptr<Workspace> W,
         TRY(upload_q4(L->mem, &L->wqkv_rope, {perm.data()}, {NQKV}, H, gemv_tile_for(NQKV)));
         L->has_rope = true;
     }
+    if (L->max_tokens > 64 && W->x6 && ffn) {
+        TRY(make_q6(L->mem, L->wgu, F, &L->wgu6));
+        L->x6 = W->x6;
+        L->has_f6_gu = true;
+    }
     if (L->max_tokens > 512 && W->x6) {
         TRY(make_q6(L->mem, L->wqkv, 0, &L->wqkv6));
         TRY(make_q6(L->mem, L->wo, 0, &L->wo6));
-        if (ffn) {
-            TRY(make_q6(L->mem, L->wgu, F, &L->wgu6));
-            TRY(make_q6(L->mem, L->wdown, 0, &L->wdown6));
-        }
+        if (ffn) TRY(make_q6(L->mem, L->wdown, 0, &L->wdown6));
         L->x6 = W->x6;
         L->has_f6 = true;
     }
@@ -1448,13 +1451,16 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
         // SwiGLU -> Q8 in the gate|up GEMM's epilogue (the swiglu_q8 phase
         // is then empty); gu is written only as a capture or where it is the
         // intermediate (exact mode)
+        // past 64 rows in the fp6 formulation (the fused pass also writes the
+        // operand-tiled Q8 a streamed down projection reads)
         bool fused6 = false;
-        if (f6) {
+        if (L->has_f6_gu && rows > 64 && !ex) {
             launch_q8_to_x6(L->xq2.qs, rows, H / SI_QK, L->x6, st);
             fused6 = launch_gemm_f6(L->wgu6.w, L->wgu6.d, 2 * s.ffn, H, L->x6, L->xq2.d, rows,
                                     nullptr, nullptr, capt(cap, L->gu), 2 * s.ffn, nullptr, 0,
                                     false, s.ffn, capt(cap, L->act), L->actq.qs, L->actq.d,
-                                    L->actq.s, st) >= 0;
+                                    L->actq.s, st, tiled ? L->actq.tq : nullptr,
+                                    tiled ? L->actq.td : nullptr) >= 0;
         }
         if (!fused6)
             launch_gemm_gateup_q8(L->wgu.qs, L->wgu.d, L->wgu.tile, s.ffn, H, L->xq2.qs,

@@ -2206,11 +2206,12 @@ __device__ __forceinline__ void f6_store(uint8_t *p16, uint8_t *p8, const uint32
 
 // Q8 values, planar [m][nb * 32] -> x6: per block the region of the codes of
 // hi = q >> 4 (-8..7), then that of lo = q & 15 (q = 16 hi + lo), each m rows
-// as [m][16] then [m][8].  Grid (ceil(m / 256), nb), a thread per (row,
-// block), consecutive threads consecutive rows.
-__global__ void __launch_bounds__(256) k_q8_to_x6(const int8_t *__restrict__ qs, int m, int nb,
-                                                  uint8_t *__restrict__ x6) {
-    const int row = blockIdx.x * 256 + threadIdx.x, blk = blockIdx.y;
+// as [m][16] then [m][8].  Grid (ceil(m / 64), nb), a thread per (row,
+// block), consecutive threads consecutive rows (one-wavefront workgroups: a
+// few hundred rows still spread over the CUs).
+__global__ void __launch_bounds__(64) k_q8_to_x6(const int8_t *__restrict__ qs, int m, int nb,
+                                                 uint8_t *__restrict__ x6) {
+    const int row = blockIdx.x * 64 + threadIdx.x, blk = blockIdx.y;
     if (row >= m) return;
     const int8_t *src = qs + ((size_t)row * nb + blk) * SI_QK;
     const uint4 q0 = *(const uint4 *)src, q1 = *(const uint4 *)(src + 16);
@@ -2252,8 +2253,8 @@ __global__ void __launch_bounds__(256) k_q4_to_w6(const uint8_t *__restrict__ qs
 
 void launch_q8_to_x6(const int8_t *qs, int m, int nb, uint8_t *x6, hipStream_t st) {
     if (m <= 0 || nb <= 0) return;
-    SI_LAUNCH(k_q8_to_x6, dim3((unsigned)((m + 255) / 256), (unsigned)nb), dim3(256), 0, st, qs,
-              m, nb, x6);
+    SI_LAUNCH(k_q8_to_x6, dim3((unsigned)((m + 63) / 64), (unsigned)nb), dim3(64), 0, st, qs, m,
+              nb, x6);
 }
 
 void launch_q4_to_w6(const uint8_t *qs, const uint16_t *d, int n, int nb, int tile, int gu_f,
@@ -2271,7 +2272,8 @@ size_t gemm_f6_partial_bytes(int m, int n, int k) {
 int launch_gemm_f6(const uint8_t *w6, const uint16_t *d6, int n, int k, const uint8_t *x6,
                    const uint16_t *xd, int m, const float *bias, const float *residual,
                    float *out, int ldo, void *workspace, size_t ws_bytes, bool want_part,
-                   int gu_f, float *act, int8_t *aqs, uint16_t *ad, int16_t *as, hipStream_t st) {
+                   int gu_f, float *act, int8_t *aqs, uint16_t *ad, int16_t *as, hipStream_t st,
+                   int8_t *atq, uint16_t *atd) {
     if (m <= 0 || n <= 0) return 0;
     const int nb = k / SI_QK;
     GemmPlan p = gemm_plan(m, n, nb);
@@ -2282,7 +2284,7 @@ int launch_gemm_f6(const uint8_t *w6, const uint16_t *d6, int n, int k, const ui
     }
     float *part = p.splits > 1 ? (float *)workspace : nullptr;
     const dim3 grid((m + p.bm - 1) / p.bm, (n + p.bn - 1) / p.bn, p.splits);
-    const GateUpOut go{gu_f, act, aqs, ad, as, nullptr, nullptr};
+    const GateUpOut go{gu_f, act, aqs, ad, as, atq, atd};
 #define CALL(WM, WN, TM, TN, FUSE)                                                             \
     SI_LAUNCH((k_gemm_f6<WM, WN, TM, TN, FUSE>), grid, dim3(256), 0, st, w6, d6, n, nb, x6, xd, \
               m, bias, residual, out, ldo, part, p.bps, go)

@@ -153,7 +153,8 @@ bool launch_gemm_qkv_rope(const uint8_t *wqs, const uint16_t *wd, int tile, int 
 // and lo codes).  launch_gemm_f6 has gemm_core's plan, splits and reduce
 // (want_part: the split count, partials left in the workspace); with gu_f > 0
 // it is the fused gate|up + SwiGLU + Q8 pass (out: the optional gate|up, ldo
-// 2 gu_f), and returns -1 (nothing launched) when that plan needs a K split.
+// 2 gu_f; atq/atd, optional: the Q8 also operand-tiled), and returns -1
+// (nothing launched) when that plan needs a K split.
 void launch_q8_to_x6(const int8_t *qs, int m, int nb, uint8_t *x6, hipStream_t st);
 size_t gemm_f6_partial_bytes(int m, int n, int k);  // launch_gemm_f6's K-split partials
 void launch_q4_to_w6(const uint8_t *qs, const uint16_t *d, int n, int nb, int tile, int gu_f,
@@ -161,7 +162,8 @@ void launch_q4_to_w6(const uint8_t *qs, const uint16_t *d, int n, int nb, int ti
 int launch_gemm_f6(const uint8_t *w6, const uint16_t *d6, int n, int k, const uint8_t *x6,
                    const uint16_t *xd, int m, const float *bias, const float *residual,
                    float *out, int ldo, void *workspace, size_t ws_bytes, bool want_part,
-                   int gu_f, float *act, int8_t *aqs, uint16_t *ad, int16_t *as, hipStream_t st);
+                   int gu_f, float *act, int8_t *aqs, uint16_t *ad, int16_t *as, hipStream_t st,
+                   int8_t *atq = nullptr, uint16_t *atd = nullptr);
 // Original output row of row pr of the RoPE-permuted Q|K|V weights: per head
 // of hdim rows, [e, hdim/2 + e] for e = 0 .. hdim/2 - 1.
 inline int rope_perm_row(int pr, int hdim) {
