@@ -1428,16 +1428,21 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
                                          L->attq.qs, L->attq.d, rows, L->attn_out, ex,
                                          L->gemm_ws, L->gemm_ws_bytes, st);
     mark(L, SI_PHASE_POST_NORM_Q8, st);
+    // past 64 rows the gate|up GEMM runs in the fp6 formulation; up to 512
+    // rows the norm writes its input codes itself (past that its scattered
+    // 4-byte code stores cost the norm more than a separate conversion)
+    const bool f6gu = L->has_f6_gu && rows > 64 && !ex;
+    uint8_t *norm_x6 = f6gu && rows <= 512 ? L->x6 : nullptr;
     // build-defined FFN half: h = x + o; RMSNorm -> Q8; gate|up; SwiGLU -> Q8; down + h
     if (osplits > 1)
         launch_rmsnorm_q8_parts(x, (const float *)L->gemm_ws, osplits, L->post_norm, rows, H,
                                 s.rms_eps, L->attn_out, L->h, capt(cap, L->normed2), L->xq2.qs,
                                 L->xq2.d, L->xq2.s, st, tl_x ? L->xq2.tq : nullptr,
-                                tl_x ? L->xq2.td : nullptr);
+                                tl_x ? L->xq2.td : nullptr, norm_x6);
     else
         launch_rmsnorm_q8(x, L->attn_out, L->post_norm, rows, H, s.rms_eps, L->h,
                           capt(cap, L->normed2), L->xq2.qs, L->xq2.d, L->xq2.s, st,
-                          tl_x ? L->xq2.tq : nullptr, tl_x ? L->xq2.td : nullptr);
+                          tl_x ? L->xq2.tq : nullptr, tl_x ? L->xq2.td : nullptr, norm_x6);
     mark(L, SI_PHASE_GATE_UP, st);
     // the SwiGLU Q8 also operand-tiled; a streamed down projection runs in
     // one pass (no K split, no reduce)
@@ -1454,8 +1459,8 @@ static int run_rows(si_layer *L, const float *x, int rows, uint16_t *kc, uint16_
         // past 64 rows in the fp6 formulation (the fused pass also writes the
         // operand-tiled Q8 a streamed down projection reads)
         bool fused6 = false;
-        if (L->has_f6_gu && rows > 64 && !ex) {
-            launch_q8_to_x6(L->xq2.qs, rows, H / SI_QK, L->x6, st);
+        if (f6gu) {
+            if (!norm_x6) launch_q8_to_x6(L->xq2.qs, rows, H / SI_QK, L->x6, st);
             fused6 = launch_gemm_f6(L->wgu6.w, L->wgu6.d, 2 * s.ffn, H, L->x6, L->xq2.d, rows,
                                     nullptr, nullptr, capt(cap, L->gu), 2 * s.ffn, nullptr, 0,
                                     false, s.ffn, capt(cap, L->act), L->actq.qs, L->actq.d,

@@ -91,6 +91,7 @@ enum : int {
     DPP_ROR4 = 0x124,     // row_ror:4  (lane i <- lane (i-4) % 16 of its row)
     DPP_ROR8 = 0x128,     // row_ror:8
     DPP_HMIRROR = 0x141,  // row_half_mirror (lane i <- 7-i within 8)
+    DPP_SHL1 = 0x101,     // row_shl:1 (lane i <- lane i+1 of its row; the row's last lane gets 0)
 };
 
 template <int CTRL>
@@ -311,6 +312,44 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32
 // Signed 8-bit 4-way dot product with int32 accumulate (v_dot4_i32_i8).
 __device__ __forceinline__ int sdot4(int a, int b, int c) {
     return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+// e2m3 codes of v / 2 for four 4-bit values n, one per byte (each value's
+// half is an e2m3 number: 0.5 subnormal, 1..7.5 normal): unsigned, v = n
+// (0..15), or two's complement, v = n - 16 for n >= 8 (-8..7), sign in bit 5.
+// Two byte lookups (v_perm) from 8-entry tables and a select on bit 3.
+__device__ __forceinline__ uint32_t f6_codes4(uint32_t n, bool sgn) {
+    const uint32_t t0 = 0x0c080400u, t1 = 0x16141210u;   // v = 0..3, 4..7
+    const uint32_t u0 = sgn ? 0x32343638u : 0x1b1a1918u;  // n = 8..11
+    const uint32_t u1 = sgn ? 0x24282c30u : 0x1f1e1d1cu;  // n = 12..15
+    const uint32_t idx = n & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(t1, t0, idx), hi = __builtin_amdgcn_perm(u1, u0, idx);
+    const uint32_t m = ((n >> 3) & 0x01010101u) * 0xffu;
+    return (hi & m) | (lo & ~m);
+}
+
+// four codes (bytes of c, each < 64) -> 24 bits, code k at bit 6 k
+__device__ __forceinline__ uint32_t f6_pack4(uint32_t c) {
+    return (c & 0x3fu) | ((c >> 2) & 0xfc0u) | ((c >> 4) & 0x3f000u) | ((c >> 6) & 0xfc0000u);
+}
+
+// The fp6 GEMM's activation codes (launch_q8_to_x6's layout: per block blk
+// the region of the hi codes then that of the lo codes, each of m rows as
+// [m][16 B] then [m][8 B]) written by an 8-lane group holding one Q8 block of
+// row row, lane t = lane & 7 with its values 4t..4t+3 as the bytes of q: the
+// lane's four hi (lo) codes are 24 bits, and lanes 0-2 and 4-6 each complete
+// one dword with the next lane's bits (every lane of the group active).
+__device__ __forceinline__ void f6_store_oct(uint32_t q, uint8_t *x6, int m, int row, int blk) {
+    const int t = threadIdx.x & 7, tq = t & 3;
+    const uint32_t ph = f6_pack4(f6_codes4((q >> 4) & 0x0f0f0f0fu, true));
+    const uint32_t pl = f6_pack4(f6_codes4(q & 0x0f0f0f0fu, false));
+    const uint32_t nh = (uint32_t)dpp_i<DPP_SHL1>((int)ph), nl = (uint32_t)dpp_i<DPP_SHL1>((int)pl);
+    if (tq == 3) return;  // lanes 3 and 7 start no dword
+    uint8_t *rh = x6 + (size_t)(2 * blk) * m * 24, *rl = rh + (size_t)m * 24;
+    const int k = t - (t >> 2);  // dword k of the row's 24 bytes
+    const size_t o = k < 4 ? (size_t)row * 16 + 4 * k : (size_t)m * 16 + (size_t)row * 8 + 4 * (k - 4);
+    *(uint32_t *)(rh + o) = (ph >> (8 * tq)) | (nh << (24 - 8 * tq));
+    *(uint32_t *)(rl + o) = (pl >> (8 * tq)) | (nl << (24 - 8 * tq));
 }
 
 }  // namespace si

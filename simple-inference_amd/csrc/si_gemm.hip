@@ -2172,25 +2172,6 @@ static int gemm_core(const uint8_t *wqs, const uint16_t *wd, int tile, int n, in
 // ===========================================================================
 // Operands of the fp6 formulation (k_gemm_fast with F6)
 
-// e2m3 codes of v / 2 for four 4-bit values n, one per byte (each value's
-// half is an e2m3 number: 0.5 subnormal, 1..7.5 normal): unsigned, v = n
-// (0..15), or two's complement, v = n - 16 for n >= 8 (-8..7), sign in bit 5.
-// Two byte lookups (v_perm) from 8-entry tables and a select on bit 3.
-__device__ __forceinline__ uint32_t f6_codes4(uint32_t n, bool sgn) {
-    const uint32_t t0 = 0x0c080400u, t1 = 0x16141210u;   // v = 0..3, 4..7
-    const uint32_t u0 = sgn ? 0x32343638u : 0x1b1a1918u;  // n = 8..11
-    const uint32_t u1 = sgn ? 0x24282c30u : 0x1f1e1d1cu;  // n = 12..15
-    const uint32_t idx = n & 0x07070707u;
-    const uint32_t lo = __builtin_amdgcn_perm(t1, t0, idx), hi = __builtin_amdgcn_perm(u1, u0, idx);
-    const uint32_t m = ((n >> 3) & 0x01010101u) * 0xffu;
-    return (hi & m) | (lo & ~m);
-}
-
-// four codes (bytes of c, each < 64) -> 24 bits, code k at bit 6 k
-__device__ __forceinline__ uint32_t f6_pack4(uint32_t c) {
-    return (c & 0x3fu) | ((c >> 2) & 0xfc0u) | ((c >> 4) & 0x3f000u) | ((c >> 6) & 0xfc0000u);
-}
-
 // 32 codes (8 dwords of 4) -> 24 bytes, code i at bit 6 i of six little-
 // endian dwords (the operand packing of the fp6 matrix instructions); bytes
 // 0..15 to p16, 16..23 to p8

@@ -32,10 +32,13 @@ namespace si {
 void launch_quantize_q8_aos(const float *src, void *dst, int count, hipStream_t st);
 void launch_quantize_q8_rows(const float *src, int rows, int k, int8_t *qs, uint16_t *d,
                              int16_t *s, hipStream_t st);
-// tq/td (optional): the Q8_0 output operand-tiled as well (q8_tiled_byte)
+// tq/td (optional): the Q8_0 output operand-tiled as well (q8_tiled_byte);
+// x6 (optional): as the fp6 GEMM's activation codes as well (launch_q8_to_x6's
+// layout, m = rows)
 void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int rows, int n,
                        float eps, float *h, float *normed, int8_t *qs, uint16_t *d, int16_t *s,
-                       hipStream_t st, int8_t *tq = nullptr, uint16_t *td = nullptr);
+                       hipStream_t st, int8_t *tq = nullptr, uint16_t *td = nullptr,
+                       uint8_t *x6 = nullptr);
 void launch_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs, uint16_t *d,
                       int16_t *s, hipStream_t st, int8_t *tq = nullptr, uint16_t *td = nullptr);
 void launch_q4_repack(const uint8_t *src, int n, int k, int tile, uint8_t *qs, uint16_t *d,
@@ -63,7 +66,7 @@ void launch_gemm_reduce(const float *part, int splits, int m, int n, float *out,
 void launch_rmsnorm_q8_parts(const float *x, const float *part, int splits, const float *gain,
                              int rows, int n, float eps, float *y_out, float *h, float *normed,
                              int8_t *qs, uint16_t *d, int16_t *s, hipStream_t st,
-                             int8_t *tq = nullptr, uint16_t *td = nullptr);
+                             int8_t *tq = nullptr, uint16_t *td = nullptr, uint8_t *x6 = nullptr);
 void launch_gemm_q4q8(const uint8_t *wqs, const uint16_t *wd, int tile, int n, int k,
                       const int8_t *xqs, const uint16_t *xd, int m, const float *bias,
                       const float *residual, float *out, int ldo, bool exact, void *workspace,

@@ -130,6 +130,8 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8(const float *__restrict__ x,
 // for sp < splits (a K-split GEMM's partials), also written to y_out.
 // tq/td (optional): the Q8_0 row written operand-tiled as well
 // (q8_tiled_byte; a thread's 4 values are 4 consecutive bytes there too).
+// x6 (optional): the row's fp6 GEMM codes as well (f6_store_oct, m =
+// gridDim.x rows).
 // T threads per row: 1024 for a few long rows (each thread's serial share
 // of the quantization shrinks), 256 otherwise.
 template <bool RESIDUAL, int NPT, bool PARTS = false, int T = 256>
@@ -143,7 +145,8 @@ __global__ void __launch_bounds__(T) k_rmsnorm_q8_v4(const float *__restrict__ x
                                                        int16_t *__restrict__ s, int splits = 1,
                                                        float *__restrict__ y_out = nullptr,
                                                        int8_t *__restrict__ tq = nullptr,
-                                                       uint16_t *__restrict__ td = nullptr) {
+                                                       uint16_t *__restrict__ td = nullptr,
+                                                       uint8_t *__restrict__ x6 = nullptr) {
     __shared__ double red[T / 64];
     const int r = blockIdx.x, tid = threadIdx.x, n4 = n / 4;
     const size_t base = (size_t)r * n;
@@ -217,6 +220,7 @@ __global__ void __launch_bounds__(T) k_rmsnorm_q8_v4(const float *__restrict__ x
                 *(uint32_t *)(tq + q8_tiled_byte(pb, r & 31, (4 * c) % SI_QK)) = packed;
                 if ((tid & 7) == 0) td[pb * 32 + (r & 31)] = dbits;
             }
+            if (x6) f6_store_oct(packed, x6, gridDim.x, r, (4 * c) / SI_QK);
         }
     }
 }
@@ -306,19 +310,19 @@ void launch_quantize_q8_rows(const float *src, int rows, int k, int8_t *qs, uint
 void launch_rmsnorm_q8_parts(const float *x, const float *part, int splits, const float *gain,
                              int rows, int n, float eps, float *y_out, float *h, float *normed,
                              int8_t *qs, uint16_t *d, int16_t *s, hipStream_t st, int8_t *tq,
-                             uint16_t *td) {
+                             uint16_t *td, uint8_t *x6) {
     if (rows == 0) return;
     const auto al = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
     const int n4 = n / 4;
     if (!(n4 <= 2048 && al(x) && al(part) && al(y_out) && al(h) && al(normed) && al(gain) &&
           al(qs))) {
         launch_gemm_reduce(part, splits, rows, n, y_out, st);
-        launch_rmsnorm_q8(x, y_out, gain, rows, n, eps, h, normed, qs, d, s, st, tq, td);
+        launch_rmsnorm_q8(x, y_out, gain, rows, n, eps, h, normed, qs, d, s, st, tq, td, x6);
         return;
     }
 #define RMS_P(NPT)                                                                              \
     SI_LAUNCH((k_rmsnorm_q8_v4<true, NPT, true>), dim3(rows), dim3(256), 0, st, x, part,        \
-              gain, n, eps, h, normed, qs, d, s, splits, y_out, tq, td)
+              gain, n, eps, h, normed, qs, d, s, splits, y_out, tq, td, x6)
     if (n4 <= 256) RMS_P(1);
     else if (n4 <= 512) RMS_P(2);
     else if (n4 <= 1024) RMS_P(4);
@@ -328,7 +332,7 @@ void launch_rmsnorm_q8_parts(const float *x, const float *part, int splits, cons
 
 void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int rows, int n,
                        float eps, float *h, float *normed, int8_t *qs, uint16_t *d, int16_t *s,
-                       hipStream_t st, int8_t *tq, uint16_t *td) {
+                       hipStream_t st, int8_t *tq, uint16_t *td, uint8_t *x6) {
     if (rows == 0) return;
     const auto al = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
     const int n4 = n / 4;
@@ -339,7 +343,7 @@ void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int ro
                              : n4 <= 256 ? 1 : n4 <= 512 ? 2 : n4 <= 1024 ? 4 : 8;
 #define RMS_V4(RES, NPT, T)                                                                       \
     SI_LAUNCH((k_rmsnorm_q8_v4<RES, NPT, false, T>), dim3(rows), dim3(T), 0, st, x, y, gain, n,   \
-              eps, h, normed, qs, d, s, 1, (float *)nullptr, tq, td)
+              eps, h, normed, qs, d, s, 1, (float *)nullptr, tq, td, x6)
 #define RMS_V4N(RES)                             \
     if (wide) {                                  \
         if (npt == 1) RMS_V4(RES, 1, 1024);      \
@@ -369,6 +373,7 @@ void launch_rmsnorm_q8(const float *x, const float *y, const float *gain, int ro
         SI_LAUNCH(k_rmsnorm_q8<false>, dim3(rows), dim3(256), lds, st, x, y, gain, n,
                   eps, h, normed, qs, d, s);
     if (tq) launch_q8_tile(qs, d, rows, n, tq, td, st);  // this path writes planar only
+    if (x6) launch_q8_to_x6(qs, rows, n / SI_QK, x6, st);
 }
 
 void launch_swiglu_q8(const float *gu, int rows, int f, float *act, int8_t *qs, uint16_t *d,

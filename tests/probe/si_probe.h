@@ -12,10 +12,10 @@
 extern "C" {
 #endif
 
-/* Cross-lane moves (DPP quad_perm / row_ror / row_half_mirror,
+/* Cross-lane moves (DPP quad_perm / row_ror / row_half_mirror / row_shl,
  * v_permlane16/32_swap) and the reductions built on them: each lane of one
- * wavefront feeds its index; out[k*64 + lane] (18 x 64 ints) is what lane
- * received from operation k. */
+ * wavefront feeds its index (row_shl: index + 1); out[k*64 + lane] (19 x 64
+ * ints) is what lane received from operation k. */
 int si_probe_lane_ops(int *out, void *stream);
 
 /* fp16 matrix-core lane layouts: a [16][32] and b [32][16] fp16 (row-major)

@@ -40,6 +40,7 @@ __global__ void __launch_bounds__(64) k_probe_lane_ops(int *__restrict__ out) {
     out[15 * 64 + l] = (int)fold_rows<16>(f);
     out[16 * 64 + l] = (int)fold_rows<32>(f);
     out[17 * 64 + l] = (int)wave_sum_d((double)l);
+    out[18 * 64 + l] = dpp_i<DPP_SHL1>(l + 1);
 }
 
 // One 16x16 tile with each of the two f16 matrix-core shapes the attention

@@ -644,10 +644,10 @@ def test_cross_lane_ops_layouts():
     """The DPP / permlane moves behind every in-kernel reduction, checked
     against their documented lane maps."""
     torch = _torch()
-    out = zeros(18 * 64, torch.int32)
+    out = zeros(19 * 64, torch.int32)
     from tests.probe import call as probe_call
     probe_call("si_probe_lane_ops", si_amd.ptr(out), None)
-    got = host(out).reshape(18, 64)
+    got = host(out).reshape(19, 64)
     lane = np.arange(64)
     row0 = lane & ~15
     expect = {
@@ -670,6 +670,8 @@ def test_cross_lane_ops_layouts():
         want = np.array([lane[lane % r == l % r].sum() for l in lane])
         assert np.array_equal(got[k], want), f"fold_rows<{r}>"
     assert np.array_equal(got[17], grp(64)), "wave_sum_d"
+    # row_shl:1 of lane + 1: lane i gets lane i + 1's value, a row's last lane 0
+    assert np.array_equal(got[18], np.where(lane % 16 != 15, lane + 2, 0)), "DPP_SHL1"
 
 
 @pytest.mark.parametrize("shape,flags", [("0.5b", 0), ("0.5b", si_amd.SI_GEMM_EXACT),
