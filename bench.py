@@ -50,14 +50,14 @@ METRIC = "decode layer µs + HBM GB/s; prefill tokens/s + int8 MFMA % (one GPU)"
 # traffic with "traffic_current": false.  Kernels not listed report traffic
 # null.  Summaries: profiles/cfgN_*.md.
 PMC_KIB = {
-    ("1", "k_matvec<8, 128, false>"): (330.9, 4.5, "e8bae9c013ab"),
-    ("2", "k_dec_attn<64, 8, false, false, 1, true>"): (2709.0, 35.5, "e8bae9c013ab"),
-    ("2", "k_dec_gateup<64, 512, false>"): (2534.9, 9.8, "e8bae9c013ab"),
-    ("2", "k_dec_wo<8, 512, false>"): (571.6, 3.5, "e8bae9c013ab"),
-    ("2", "k_matvec<8, 512, false>"): (1256.0, 3.5, "e8bae9c013ab"),
-    ("3", "k_gemm_f6<2, 2, 1, 2, true>"): (28135.2, 5320.0, "e8bae9c013ab"),
-    ("4", "k_gemm_f6<2, 2, 2, 2, true>"): (514518.5, 44768.2, "e8bae9c013ab"),
-    ("5", "k_dec_attn_rows<128, 4, false, false>"): (266837.5, 8192.0, "e8bae9c013ab"),
+    ("1", "k_matvec<8, 128, false>"): (330.9, 4.5, "4041115cd2c8"),
+    ("2", "k_dec_attn<64, 8, false, false, 1, true>"): (2709.0, 35.5, "4041115cd2c8"),
+    ("2", "k_dec_gateup<64, 512, false>"): (2534.9, 9.8, "4041115cd2c8"),
+    ("2", "k_dec_wo<8, 512, false>"): (571.6, 3.5, "4041115cd2c8"),
+    ("2", "k_matvec<8, 512, false>"): (1256.0, 3.5, "4041115cd2c8"),
+    ("3", "k_gemm_f6<2, 2, 1, 2, true>"): (28135.5, 5320.0, "4041115cd2c8"),
+    ("4", "k_gemm_f6<2, 2, 2, 2, true>"): (513303.4, 44773.9, "4041115cd2c8"),
+    ("5", "k_dec_attn_rows<128, 4, false, false>"): (266837.5, 8192.0, "4041115cd2c8"),
 }
 FETCH_SCALE, WRITE_SCALE = 2.000, 1.000
 _DIGEST = None
