@@ -150,13 +150,15 @@ def test_gemm_gateup_f6_bit_identical_to_default(oracle, m, f, k):
     assert err.max() <= 1e-5, f"gate|up rows off the float64 product: worst {err.max():.3g}"
 
 
-def test_gemm_f6_small_m(oracle):
+@pytest.mark.parametrize("m,n,k", [(100, 256, 512), (64, 3584, 18944)],
+                         ids=["100x256x512", "config5_down"])
+def test_gemm_f6_small_m(oracle, m, n, k):
     """Below 513 rows the default path streams with another summation order;
-    the fp6 tile pass (64-row tiles) is checked against float64 there."""
+    the fp6 tile pass (64-row tiles) is checked against float64 there, also
+    at config 5's down projection (a 21-way K split and its reduce)."""
     torch = _torch()
     L = si_amd.lib()
-    m, n, k = 100, 256, 512
-    rng = np.random.default_rng(5)
+    rng = np.random.default_rng(m + n + k)
     w = q4(oracle, rng, n, k)
     xq = oracle.quantize_q8(rng.standard_normal((m, k)).astype(np.float32))
     qs, d, _ = aos_to_planar(xq)
